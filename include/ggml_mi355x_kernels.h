@@ -1,0 +1,163 @@
+/*
+ * ggml_mi355x_kernels.h -- C ABI of the MI355X (gfx950) decode kernels.
+ *
+ * This layer replaces the reference's aclnn operator ABI (two-phase
+ * aclnnXxxGetWorkspaceSize + aclnnXxx(ws, n, exec, stream)) that the CANN
+ * backend calls on the decode hot path.  Every entry point takes plain device
+ * pointers, sizes and a hipStream_t passed as void*, returns 0 on success or a
+ * negative MI_ERR_* / positive hipError_t code, never aborts, and keeps no
+ * global state other than per-device lazily created function handles.
+ * The last error message of the calling thread is available from
+ * mi_last_error().
+ *
+ * Reference citations are relative to the reference repository
+ * (patch:N = line N of patches/ascend310b4-llama-cpp.patch).
+ */
+#ifndef GGML_MI355X_KERNELS_H
+#define GGML_MI355X_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI_OK            0
+#define MI_ERR_ARG      -1   /* bad size / shape / null pointer */
+#define MI_ERR_ALIGN    -2   /* pointer or stride alignment not supported */
+#define MI_ERR_WORKSPACE -3  /* workspace too small */
+#define MI_ERR_NODEVICE -4   /* no HIP device */
+#define MI_ERR_UNSUPPORTED -5
+
+/* activation quantizer rounding (ggml-CPU has two): */
+#define MI_Q8_ROUND_REF 0    /* ggml quantize_row_q8_0_ref: id = 1/d, round half away from zero */
+#define MI_Q8_ROUND_X86 1    /* ggml-cpu x86 SIMD quantize_row_q8_0: id = 127/amax, round half to even */
+
+const char *mi_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * Device plumbing used by hosts that have no other HIP runtime (tests,
+ * benchmarks, the ggml adapter).  Thin wrappers of hipMalloc & co.
+ * ---------------------------------------------------------------------- */
+int mi_device_count(int *count);
+int mi_set_device(int device);
+int mi_device_name(int device, char *buf, size_t len);
+int mi_malloc(void **ptr, size_t bytes);
+int mi_free(void *ptr);
+int mi_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream);
+int mi_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream);
+int mi_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream);
+int mi_memset(void *dst, int value, size_t bytes, void *stream);
+int mi_stream_create(void **stream);
+int mi_stream_destroy(void *stream);
+int mi_stream_sync(void *stream);
+int mi_device_sync(void);
+int mi_event_create(void **event);
+int mi_event_destroy(void *event);
+int mi_event_record(void *event, void *stream);
+int mi_event_elapsed_ms(float *ms, void *start, void *stop);
+
+/* ------------------------------------------------------------------------
+ * Weight prepack (replaces the set_tensor side layouts: FRACTAL_NZ via
+ * aclnnTransMatmulWeight patch:1700-1809, and the host A8W8 transform
+ * ggml_backend_cann_transform_f16_a8w8 patch:1674-1695; sizes replace
+ * ggml_cann_310b_nz_size / a8w8_size patch:1535-1562).
+ *
+ * Q8_0 packed layout for a weight of n rows x k columns (nb = k/32 blocks
+ * per row), three 256-byte-aligned planes:
+ *   qlo [n][nb][16] int8   -- qs[0..15]  of block (row, b)
+ *   qhi [n][nb][16] int8   -- qs[16..31] of block (row, b)
+ *   d   [n][nb]     fp16   -- block scale
+ * Q4_0 packed layout: qs [n][nb][16] (ggml nibble order kept), d [n][nb] fp16.
+ * src is ggml block_q8_0 / block_q4_0 rows (34 / 18 bytes per block).
+ * ---------------------------------------------------------------------- */
+size_t mi_q8_0_packed_size(int64_t n, int64_t k);
+size_t mi_q4_0_packed_size(int64_t n, int64_t k);
+int mi_prepack_q8_0(void *stream, const void *src_blocks, void *dst_packed, int64_t n, int64_t k);
+int mi_prepack_q4_0(void *stream, const void *src_blocks, void *dst_packed, int64_t n, int64_t k);
+/* host-side versions of the same layouts (byte-identical to the device ones) */
+int mi_prepack_q8_0_host(const void *src_blocks, void *dst_packed, int64_t n, int64_t k);
+int mi_prepack_q4_0_host(const void *src_blocks, void *dst_packed, int64_t n, int64_t k);
+int mi_unpack_q8_0_host(const void *packed, void *dst_blocks, int64_t n, int64_t k);
+int mi_unpack_q4_0_host(const void *packed, void *dst_blocks, int64_t n, int64_t k);
+
+/* ------------------------------------------------------------------------
+ * Activation quantization (replaces aclnnW8a8QuantizeCustom,
+ * experiments/a8w8/w8a8_quantize_custom_vector.cpp:97-106, plus the fp32->fp16
+ * cast before it, patch:1266-1267).  ggml Q8_0 per 32-block semantics.
+ * x     : fp32 [m][k]
+ * inv_s : fp32 [k] SmoothQuant reciprocal factors (x*inv_s is quantized), or NULL
+ * xq    : output, planar: qs int8 [m][k] at xq, d fp16 [m][k/32] at xq + mi_xq_d_offset(m,k)
+ * ---------------------------------------------------------------------- */
+size_t mi_xq_size(int64_t m, int64_t k);
+size_t mi_xq_d_offset(int64_t m, int64_t k);
+int mi_act_quant_q8_0(void *stream, const float *x, const float *inv_s, int64_t m, int64_t k, void *xq,
+                      int rounding);
+
+/* ------------------------------------------------------------------------
+ * A8W8 Q8_0 GEMV, m <= 8 activation rows (replaces aclnnMatmulW8a8I32Custom +
+ * W8a8DequantCustom + cast, patch:1268-1271; kernel
+ * experiments/a8w8/custom_ops_nz/op_kernel/matmul_w8a8_i32_custom.cpp:15-48).
+ * y[i][row] = sum_b float(sumi(row,b,i)) * (d_w(row,b) * d_x(i,b)), sumi exact int32.
+ * ---------------------------------------------------------------------- */
+int mi_gemv_q8_0(void *stream, const void *w_packed, const void *xq, float *y, int64_t n, int64_t k,
+                 int64_t m);
+/* fused chain: quantize x (with optional inv_s) in the kernel prologue, then GEMV;
+ * the whole A8W8 branch of ggml_cann_mat_mul_fp (patch:1223-1281) in one launch */
+int mi_mul_mat_q8_0_f32(void *stream, const void *w_packed, const float *x, const float *inv_s, float *y,
+                        int64_t n, int64_t k, int64_t m, int rounding);
+/* debug: exact per-block int32 dot products out[row][b] for activation row 0 */
+int mi_q8_0_block_dots(void *stream, const void *w_packed, const void *xq, int32_t *out, int64_t n, int64_t k);
+
+/* ------------------------------------------------------------------------
+ * W4A16 GEMV, int4 group-32 (ggml Q4_0) x fp16 activations, fp32 accumulation
+ * (replaces the add-on's standalone add_custom operator,
+ * experiments/w4a16-gemv/source/w4a16_gemv_qwen.cpp:24-180).
+ * x_f16 : fp16 [m][k];  y : fp32 [m][n]
+ * ---------------------------------------------------------------------- */
+int mi_gemv_q4_0_f16(void *stream, const void *w_packed, const uint16_t *x_f16, float *y, int64_t n, int64_t k,
+                     int64_t m);
+/* same with fp32 activations converted to fp16 (RNE) in the prologue */
+int mi_mul_mat_q4_0_f32(void *stream, const void *w_packed, const float *x, float *y, int64_t n, int64_t k,
+                        int64_t m);
+
+/* ------------------------------------------------------------------------
+ * F16 GEMV (replaces cast + aclnnMatmul(FRACTAL_NZ) + cast, patch:1286-1309,
+ * used for the tied output head).  w : fp16 rows, row stride ldw elements
+ * (>= k, multiple of 8); x : fp32 [m][k], rounded to fp16 like ggml's
+ * vec_dot_type conversion; y : fp32 [m][n]; fp32 accumulation.
+ * ---------------------------------------------------------------------- */
+int mi_gemv_f16(void *stream, const uint16_t *w, int64_t ldw, const float *x, float *y, int64_t n, int64_t k,
+                int64_t m);
+
+/* ------------------------------------------------------------------------
+ * Single-token GQA flash-decoding (replaces AttentionStepCustom,
+ * experiments/attention-step-custom/custom_ops/attention_step_custom.json:2-18,
+ * op_host/attention_step_custom.cpp:80-121, and the q/out casts patch:1403,1426).
+ * q    : fp32 [n_q_heads][d]
+ * k, v : fp16, element (pos, kv_head, i) at byte offset pos*nb1 + kv_head*nb2 + 2*i
+ *        (the ggml KV-cache view; strides multiples of 16 bytes)
+ * mask : fp16 [n_kv] added to the scaled scores (-inf excludes), or NULL
+ * kv_len: device int32[1], effective KV length (ggml src[5]); used when
+ *        0 < *kv_len < n_kv, else n_kv; may be NULL
+ * out  : fp32 [n_q_heads][d]
+ * ws   : workspace of mi_fa_decode_workspace_size() bytes (split partials)
+ * d must be 64 or 128; n_q_heads % n_kv_heads == 0; group size <= 8.
+ * ---------------------------------------------------------------------- */
+size_t mi_fa_decode_workspace_size(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d);
+int mi_fa_decode(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
+                 const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                 size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out,
+                 void *ws, size_t ws_bytes);
+
+/* ------------------------------------------------------------------------
+ * kv_lengths on the device (replaces the host scan set_input_kv_lengths,
+ * patch:2900-2929): out[r] = max(1, 1 + last index with a finite mask value).
+ * ---------------------------------------------------------------------- */
+int mi_kv_lengths(void *stream, const void *mask, int mask_is_f16, int64_t n_kv, int64_t n_rows, int32_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,353 @@
+// fattn.hip -- single-token GQA flash-decoding for gfx950.
+//
+// Replaces AttentionStepCustom
+// (experiments/attention-step-custom/custom_ops/op_kernel/attention_step_custom.cpp:60-597):
+// instead of one core per q head streaming the whole KV length, the KV length is
+// split across workgroups (one per (split, kv head)); every K/V row is read once
+// and shared by all q heads of its GQA group; each workgroup keeps an online
+// softmax state (m, l, o) per q head and a log-sum-exp combine kernel merges
+// the splits.  Score order follows the reference and ggml: q rounded to fp16,
+// s = (q.k) * scale, s += mask, online softmax, one final divide.
+#include "mi_common.h"
+
+#include <math.h>
+
+namespace {
+
+using namespace mi;
+
+constexpr int kNW = 4;  // waves per workgroup
+constexpr int kT = 4;   // positions per lane group per tile
+
+template <int D>
+constexpr int part_stride() { return D + 4; }  // o[D], m, l, pad -> 16-byte aligned records
+
+struct FaPlan {
+    int chunk;
+    int n_splits;
+};
+
+inline FaPlan fa_plan(int64_t n_kv, int64_t n_kv_heads) {
+    const int64_t target_wg = 512;
+    int64_t per = (n_kv * n_kv_heads + target_wg - 1) / target_wg;
+    if (per < 32) per = 32;
+    per = (per + 15) / 16 * 16;
+    FaPlan p;
+    p.chunk = (int)per;
+    p.n_splits = (int)((n_kv + per - 1) / per);
+    return p;
+}
+
+template <int LPR>
+__device__ __forceinline__ void merge_state(float &m, float &l, float *o, int xor_mask) {
+    const float mo = __shfl_xor(m, xor_mask, 64);
+    const float lo = __shfl_xor(l, xor_mask, 64);
+    float oo[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) oo[i] = __shfl_xor(o[i], xor_mask, 64);
+    const float mn = fmaxf(m, mo);
+    if (mn == -INFINITY) return;
+    const float a = expf(m - mn);
+    const float b = expf(mo - mn);
+    l = l * a + lo * b;
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = o[i] * a + oo[i] * b;
+    m = mn;
+}
+
+template <int D, int GQ>
+__global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, const uint8_t *__restrict__ kc,
+                                                  const uint8_t *__restrict__ vc, const uint16_t *__restrict__ mask,
+                                                  const int32_t *__restrict__ kv_len_p, int n_kv, size_t k_nb1,
+                                                  size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, int chunk,
+                                                  int n_splits, float *__restrict__ part, float *__restrict__ out) {
+    constexpr int LPR = D / 8;     // lanes per position row (16 B = 8 halves per lane)
+    constexpr int PPW = 64 / LPR;  // positions per wave step
+    constexpr int NG = kNW * PPW;  // lane groups per workgroup
+    constexpr int PS = part_stride<D>();
+    __shared__ float s_m[kNW][GQ];
+    __shared__ float s_l[kNW][GQ];
+    __shared__ __align__(16) float s_o[kNW][GQ][D];
+
+    const int split = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int lane = tid % 64;
+    const int wave = tid / 64;
+    const int c = lane % LPR;
+    const int g = wave * PPW + lane / LPR;
+
+    int eff = n_kv;
+    if (kv_len_p) {
+        const int kl = *kv_len_p;
+        if (kl > 0 && kl < n_kv) eff = kl;
+    }
+    const int start = split * chunk;
+    const int end = min(start + chunk, eff);
+
+    uint32_t qh[GQ][4];
+#pragma unroll
+    for (int h = 0; h < GQ; h++) {
+        const float4 *qp = (const float4 *)(q + (size_t)(kvh * GQ + h) * D + 8 * c);
+        const float4 a = qp[0], b = qp[1];
+        qh[h][0] = (uint32_t)f2h(a.x) | ((uint32_t)f2h(a.y) << 16);
+        qh[h][1] = (uint32_t)f2h(a.z) | ((uint32_t)f2h(a.w) << 16);
+        qh[h][2] = (uint32_t)f2h(b.x) | ((uint32_t)f2h(b.y) << 16);
+        qh[h][3] = (uint32_t)f2h(b.z) | ((uint32_t)f2h(b.w) << 16);
+    }
+
+    float m[GQ], l[GQ], o[GQ][8];
+#pragma unroll
+    for (int h = 0; h < GQ; h++) {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[h][i] = 0.0f;
+    }
+
+    const uint8_t *kb = kc + (size_t)kvh * k_nb2 + (size_t)c * 16;
+    const uint8_t *vb = vc + (size_t)kvh * v_nb2 + (size_t)c * 16;
+
+    for (int p0 = start + g; p0 < end; p0 += NG * kT) {
+        int4 kr[kT], vr[kT];
+        float mk[kT];
+        bool val[kT];
+#pragma unroll
+        for (int t = 0; t < kT; t++) {
+            const int p = p0 + t * NG;
+            val[t] = p < end;
+            if (val[t]) {
+                kr[t] = *(const int4 *)(kb + (size_t)p * k_nb1);
+                vr[t] = *(const int4 *)(vb + (size_t)p * v_nb1);
+                mk[t] = mask ? h2f(mask[p]) : 0.0f;
+            } else {
+                kr[t] = make_int4(0, 0, 0, 0);
+                vr[t] = make_int4(0, 0, 0, 0);
+                mk[t] = -INFINITY;
+            }
+        }
+        float s[GQ][kT];
+#pragma unroll
+        for (int t = 0; t < kT; t++) {
+#pragma unroll
+            for (int h = 0; h < GQ; h++) {
+                float dsum = 0.0f;
+                dsum = fdot2(qh[h][0], (uint32_t)kr[t].x, dsum);
+                dsum = fdot2(qh[h][1], (uint32_t)kr[t].y, dsum);
+                dsum = fdot2(qh[h][2], (uint32_t)kr[t].z, dsum);
+                dsum = fdot2(qh[h][3], (uint32_t)kr[t].w, dsum);
+                dsum = group_sum<LPR>(dsum);
+                const float sc = __fadd_rn(__fmul_rn(dsum, scale), mk[t]);
+                s[h][t] = val[t] ? sc : -INFINITY;
+            }
+        }
+        float vf[kT][8];
+#pragma unroll
+        for (int t = 0; t < kT; t++) {
+            const uint32_t w4[4] = {(uint32_t)vr[t].x, (uint32_t)vr[t].y, (uint32_t)vr[t].z, (uint32_t)vr[t].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                vf[t][2 * i] = h2f((uint16_t)(w4[i] & 0xffffu));
+                vf[t][2 * i + 1] = h2f((uint16_t)(w4[i] >> 16));
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < GQ; h++) {
+            float mt = s[h][0];
+#pragma unroll
+            for (int t = 1; t < kT; t++) mt = fmaxf(mt, s[h][t]);
+            const float mn = fmaxf(m[h], mt);
+            if (mn == -INFINITY) continue;  // nothing unmasked yet (uniform in the lane group)
+            const float alpha = expf(m[h] - mn);
+            l[h] *= alpha;
+#pragma unroll
+            for (int i = 0; i < 8; i++) o[h][i] *= alpha;
+#pragma unroll
+            for (int t = 0; t < kT; t++) {
+                const float p = expf(s[h][t] - mn);
+                l[h] += p;
+#pragma unroll
+                for (int i = 0; i < 8; i++) o[h][i] = fmaf(p, vf[t][i], o[h][i]);
+            }
+            m[h] = mn;
+        }
+    }
+
+    // merge the lane groups of this wave
+#pragma unroll
+    for (int x = LPR; x < 64; x *= 2) {
+#pragma unroll
+        for (int h = 0; h < GQ; h++) merge_state<LPR>(m[h], l[h], o[h], x);
+    }
+    // every lane group of the wave now holds the wave state; group 0 publishes it
+    if (lane < LPR) {
+#pragma unroll
+        for (int h = 0; h < GQ; h++) {
+            *(float4 *)&s_o[wave][h][8 * c] = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+            *(float4 *)&s_o[wave][h][8 * c + 4] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+            if (c == 0) {
+                s_m[wave][h] = m[h];
+                s_l[wave][h] = l[h];
+            }
+        }
+    }
+    __syncthreads();
+
+    // final merge across waves: thread (h, dim) for GQ*D threads, strided over the block
+    for (int idx = tid; idx < GQ * D; idx += 256) {
+        const int h = idx / D;
+        const int dd = idx % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kNW; w++) M = fmaxf(M, s_m[w][h]);
+        float L = 0.0f, acc = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < kNW; w++) {
+                const float e = expf(s_m[w][h] - M);
+                L += s_l[w][h] * e;
+                acc += s_o[w][h][dd] * e;
+            }
+        }
+        const int qh_idx = kvh * GQ + h;
+        if (n_splits == 1) {
+            out[(size_t)qh_idx * D + dd] = L == 0.0f ? 0.0f : acc / L;
+        } else {
+            float *rec = part + ((size_t)qh_idx * n_splits + split) * PS;
+            rec[dd] = acc;
+            if (dd == 0) {
+                rec[D] = M;
+                rec[D + 1] = L;
+            }
+        }
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(D) void k_fa_combine(const float *__restrict__ part, float *__restrict__ out,
+                                                  int n_splits) {
+    constexpr int PS = part_stride<D>();
+    const int h = blockIdx.x;
+    const int dd = threadIdx.x;
+    const float *ph = part + (size_t)h * n_splits * PS;
+    float M = -INFINITY;
+    for (int s = 0; s < n_splits; s++) M = fmaxf(M, ph[(size_t)s * PS + D]);
+    float L = 0.0f, acc = 0.0f;
+    if (M != -INFINITY) {
+        for (int s = 0; s < n_splits; s++) {
+            const float ms = ph[(size_t)s * PS + D];
+            if (ms == -INFINITY) continue;
+            const float e = expf(ms - M);
+            L += ph[(size_t)s * PS + D + 1] * e;
+            acc += ph[(size_t)s * PS + dd] * e;
+        }
+    }
+    out[(size_t)h * D + dd] = L == 0.0f ? 0.0f : acc / L;
+}
+
+template <int D, int GQ>
+int launch_split(hipStream_t st, const float *q, const void *k, const void *v, const uint16_t *mask,
+                 const int32_t *kv_len, int64_t n_kv, int64_t n_kv_heads, size_t k_nb1, size_t k_nb2, size_t v_nb1,
+                 size_t v_nb2, float scale, float *out, float *part, const FaPlan &p) {
+    hipLaunchKernelGGL((k_fa_split<D, GQ>), dim3((unsigned)p.n_splits, (unsigned)n_kv_heads), dim3(256), 0, st, q,
+                       (const uint8_t *)k, (const uint8_t *)v, mask, kv_len, (int)n_kv, k_nb1, k_nb2, v_nb1, v_nb2,
+                       scale, p.chunk, p.n_splits, part, out);
+    MI_CHECK_LAUNCH("k_fa_split");
+    if (p.n_splits > 1) {
+        hipLaunchKernelGGL((k_fa_combine<D>), dim3((unsigned)(n_kv_heads * GQ)), dim3(D), 0, st, part, out,
+                           p.n_splits);
+        MI_CHECK_LAUNCH("k_fa_combine");
+    }
+    return MI_OK;
+}
+
+template <int D>
+int launch_d(hipStream_t st, int gq, const float *q, const void *k, const void *v, const uint16_t *mask,
+             const int32_t *kv_len, int64_t n_kv, int64_t n_kv_heads, size_t k_nb1, size_t k_nb2, size_t v_nb1,
+             size_t v_nb2, float scale, float *out, float *part, const FaPlan &p) {
+#define MI_FA_CASE(G)                                                                                          \
+    case G:                                                                                                    \
+        return launch_split<D, G>(st, q, k, v, mask, kv_len, n_kv, n_kv_heads, k_nb1, k_nb2, v_nb1, v_nb2, scale, \
+                                  out, part, p);
+    switch (gq) {
+        MI_FA_CASE(1)
+        MI_FA_CASE(2)
+        MI_FA_CASE(3)
+        MI_FA_CASE(4)
+        MI_FA_CASE(5)
+        MI_FA_CASE(6)
+        MI_FA_CASE(7)
+        MI_FA_CASE(8)
+        default: set_error("fa_decode: GQA group size %d not in 1..8", gq); return MI_ERR_UNSUPPORTED;
+    }
+#undef MI_FA_CASE
+}
+
+// kv_lengths: one workgroup per mask row
+__global__ __launch_bounds__(256) void k_kv_lengths(const void *__restrict__ mask, int is_f16, int64_t n_kv,
+                                                    int32_t *__restrict__ out) {
+    const int64_t r = blockIdx.x;
+    int64_t last = -1;
+    for (int64_t i = threadIdx.x; i < n_kv; i += 256) {
+        const float v = is_f16 ? h2f(((const uint16_t *)mask)[r * n_kv + i]) : ((const float *)mask)[r * n_kv + i];
+        if (isfinite(v)) last = i;
+    }
+    __shared__ int64_t s_last[256];
+    s_last[threadIdx.x] = last;
+    __syncthreads();
+    for (int s = 128; s > 0; s /= 2) {
+        if ((int)threadIdx.x < s) s_last[threadIdx.x] = max(s_last[threadIdx.x], s_last[threadIdx.x + s]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const int64_t len = s_last[0] + 1;
+        out[r] = (int32_t)(len > 1 ? len : 1);
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mi_fa_decode_workspace_size(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d) {
+    if (n_kv <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || d <= 0) return 0;
+    const FaPlan p = fa_plan(n_kv, n_kv_heads);
+    return (size_t)n_q_heads * p.n_splits * (d + 4) * sizeof(float);
+}
+
+int mi_fa_decode(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
+                 const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                 size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out, void *ws,
+                 size_t ws_bytes) {
+    MI_CHECK_ARG(q && k && v && out, "fa_decode: null pointer");
+    MI_CHECK_ARG(n_kv > 0 && n_kv < (1ll << 31) && n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0,
+                 "fa_decode: bad heads/length n_kv=%lld nq=%lld nkv=%lld", (long long)n_kv, (long long)n_q_heads,
+                 (long long)n_kv_heads);
+    MI_CHECK_ARG(d == 64 || d == 128, "fa_decode: head dim %lld not supported (64, 128)", (long long)d);
+    MI_CHECK_ARG(mi::aligned(k, 16) && mi::aligned(v, 16) && k_nb1 % 16 == 0 && k_nb2 % 16 == 0 && v_nb1 % 16 == 0 &&
+                     v_nb2 % 16 == 0 && mi::aligned(q, 16) && mi::aligned(out, 16),
+                 "fa_decode: K/V base and strides must be 16-byte aligned");
+    const FaPlan p = fa_plan(n_kv, n_kv_heads);
+    const size_t need = mi_fa_decode_workspace_size(n_kv, n_q_heads, n_kv_heads, d);
+    if (p.n_splits > 1 && (!ws || ws_bytes < need)) {
+        mi::set_error("fa_decode: workspace %zu < %zu bytes", ws_bytes, need);
+        return MI_ERR_WORKSPACE;
+    }
+    const int gq = (int)(n_q_heads / n_kv_heads);
+    hipStream_t st = (hipStream_t)stream;
+    if (d == 128)
+        return launch_d<128>(st, gq, q, k, v, mask, kv_len, n_kv, n_kv_heads, k_nb1, k_nb2, v_nb1, v_nb2, scale, out,
+                             (float *)ws, p);
+    return launch_d<64>(st, gq, q, k, v, mask, kv_len, n_kv, n_kv_heads, k_nb1, k_nb2, v_nb1, v_nb2, scale, out,
+                        (float *)ws, p);
+}
+
+int mi_kv_lengths(void *stream, const void *mask, int mask_is_f16, int64_t n_kv, int64_t n_rows, int32_t *out) {
+    MI_CHECK_ARG(mask && out && n_kv > 0 && n_rows > 0, "kv_lengths: bad arguments");
+    hipLaunchKernelGGL(k_kv_lengths, dim3((unsigned)n_rows), dim3(256), 0, (hipStream_t)stream, mask, mask_is_f16,
+                       n_kv, out);
+    MI_CHECK_LAUNCH("k_kv_lengths");
+    return MI_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,102 @@
+// mi_common.h -- shared device/host helpers for the gfx950 decode kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "ggml_mi355x_kernels.h"
+
+namespace mi {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- errors
+void set_error(const char *fmt, ...);
+int hip_fail(hipError_t e, const char *what);
+
+#define MI_CHECK_ARG(cond, ...)                 \
+    do {                                        \
+        if (!(cond)) {                          \
+            ::mi::set_error(__VA_ARGS__);       \
+            return MI_ERR_ARG;                  \
+        }                                       \
+    } while (0)
+
+#define MI_CHECK_LAUNCH(what)                                   \
+    do {                                                        \
+        hipError_t e_ = hipGetLastError();                      \
+        if (e_ != hipSuccess) return ::mi::hip_fail(e_, what);  \
+    } while (0)
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// ---------------------------------------------------------------- device helpers
+typedef _Float16 half_t;
+typedef half_t half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    half_t v = __builtin_bit_cast(half_t, h);
+    return (float)v;
+}
+
+__device__ __forceinline__ uint16_t f2h(float f) {  // round to nearest even (hardware default mode)
+    half_t v = (half_t)f;
+    return __builtin_bit_cast(uint16_t, v);
+}
+
+__device__ __forceinline__ half2_t u2h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t h22u(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// fp32 += a.x*b.x + a.y*b.y with exact fp16 products (v_dot2_f32_f16)
+__device__ __forceinline__ float fdot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(u2h2(a), u2h2(b), c, false);
+}
+
+// DPP move helpers (row = 16 lanes)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
+}
+
+constexpr int DPP_QUAD_1032 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_2301 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_MIRROR = 0x140;
+
+// sum over aligned groups of G lanes (G in 1,2,4,8,16,32,64); every lane of the group gets the sum
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (G >= 2) v += dpp_f<DPP_QUAD_1032>(v);
+    if constexpr (G >= 4) v += dpp_f<DPP_QUAD_2301>(v);
+    if constexpr (G >= 8) v += dpp_f<DPP_ROW_HALF_MIRROR>(v);
+    if constexpr (G >= 16) v += dpp_f<DPP_ROW_MIRROR>(v);
+    if constexpr (G >= 32) v += __shfl_xor(v, 16, 64);
+    if constexpr (G >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (G >= 2) v = fmaxf(v, dpp_f<DPP_QUAD_1032>(v));
+    if constexpr (G >= 4) v = fmaxf(v, dpp_f<DPP_QUAD_2301>(v));
+    if constexpr (G >= 8) v = fmaxf(v, dpp_f<DPP_ROW_HALF_MIRROR>(v));
+    if constexpr (G >= 16) v = fmaxf(v, dpp_f<DPP_ROW_MIRROR>(v));
+    if constexpr (G >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
+    if constexpr (G >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
+// streaming (read-once) 16-byte load of weights
+typedef int int4v_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int4 ld_stream16(const void *p) {
+    const int4v_t v = __builtin_nontemporal_load((const int4v_t *)p);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+
+}  // namespace mi

@@ -1,0 +1,269 @@
+// q4_0.hip -- W4A16 decode GEMV for gfx950: ggml Q4_0 weights (int4, group 32,
+// offset 8, fp16 group scale) times an fp16 activation row, fp32 accumulation.
+//
+// Nibbles are turned into exact fp16 values (nib - 8) with a magic-exponent
+// OR (0x6400 | nib == 1024 + nib) and one packed fp16 subtract, then reduced
+// with v_dot2_f32_f16 (exact fp16 products, fp32 accumulation); the group
+// scale is applied once per 32-group, as the reference operator does
+// (experiments/w4a16-gemv/source/w4a16_gemv_qwen.cpp:127-148).
+// Replaces the add-on's add_custom W4A16 operator (same file, :24-180).
+#include "mi_common.h"
+
+#include <string.h>
+
+namespace {
+
+using namespace mi;
+
+constexpr int QK = 32;
+
+struct Q4Planes {
+    size_t plane;
+    size_t total;
+};
+
+inline Q4Planes q4_planes(int64_t n, int64_t k) {
+    const int64_t nb = k / QK;
+    Q4Planes p;
+    p.plane = align_up((size_t)n * nb * 16, 256);
+    p.total = p.plane + align_up((size_t)n * nb * 2, 256);
+    return p;
+}
+
+__global__ void k_prepack_q4_0(const uint8_t *__restrict__ src, uint8_t *__restrict__ qs, uint16_t *__restrict__ dpl,
+                               int64_t nblocks) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const uint16_t *s = (const uint16_t *)(src + i * 18);
+    uint16_t w[9];
+#pragma unroll
+    for (int t = 0; t < 9; t++) w[t] = s[t];
+    *(uint4 *)(qs + i * 16) = make_uint4((uint32_t)w[1] | ((uint32_t)w[2] << 16), (uint32_t)w[3] | ((uint32_t)w[4] << 16),
+                                         (uint32_t)w[5] | ((uint32_t)w[6] << 16), (uint32_t)w[7] | ((uint32_t)w[8] << 16));
+    dpl[i] = w[0];
+}
+
+// dword t of a Q4_0 block holds elements 4t..4t+3 (low nibbles) and 16+4t..16+4t+3 (high nibbles)
+__device__ __forceinline__ float q4_block_dot(const int4 q, const uint32_t *xs /* 16 half2 of the block */) {
+    const half2_t off = {(half_t)1032.0f, (half_t)1032.0f};
+    float s = 0.0f;
+    const uint32_t qq[4] = {(uint32_t)q.x, (uint32_t)q.y, (uint32_t)q.z, (uint32_t)q.w};
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const uint32_t v = qq[t];
+        const uint32_t lo01 = 0x64006400u | (v & 0xfu) | ((v & 0xf00u) << 8);
+        const uint32_t lo23 = 0x64006400u | ((v >> 16) & 0xfu) | ((v >> 8) & 0xf0000u);
+        const uint32_t hi01 = 0x64006400u | ((v >> 4) & 0xfu) | ((v << 4) & 0xf0000u);
+        const uint32_t hi23 = 0x64006400u | ((v >> 20) & 0xfu) | ((v >> 12) & 0xf0000u);
+        s = fdot2(h22u(u2h2(lo01) - off), xs[2 * t], s);
+        s = fdot2(h22u(u2h2(lo23) - off), xs[2 * t + 1], s);
+        s = fdot2(h22u(u2h2(hi01) - off), xs[8 + 2 * t], s);
+        s = fdot2(h22u(u2h2(hi23) - off), xs[8 + 2 * t + 1], s);
+    }
+    return s;
+}
+
+// G lanes per output row; lane j owns blocks j, j+G, ... (U per pass, loads
+// branch-free with clamped addresses); the fp16 activation rows are staged in LDS.
+template <int G, int U, int M, bool F32X>
+__global__ __launch_bounds__(256) void k_gemv_q4_0(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ wd,
+                                                   const uint16_t *__restrict__ x16, const float *__restrict__ x32,
+                                                   float *__restrict__ y, int n, int nb, int m) {
+    constexpr int RPB = 256 / G;
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint16_t *s_x = (uint16_t *)smem;  // [M][k]
+    const int tid = threadIdx.x;
+    const int j = tid % G;
+    const int row = blockIdx.x * RPB + tid / G;
+    const bool row_ok = row < n;
+    const int k = nb * QK;
+    const size_t rbase = (size_t)min(row, n - 1) * nb;
+
+    int4 wq[U];
+    uint32_t dw[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int b = min(j + u * G, nb - 1);
+        wq[u] = ld_stream16(qs + (rbase + b) * 16);
+        dw[u] = wd[rbase + b];
+    }
+
+    if constexpr (F32X) {
+        for (int i = tid * 4; i < m * k; i += 256 * 4) {
+            const float4 v = *(const float4 *)(x32 + i);
+            *(uint2 *)(s_x + i) = make_uint2((uint32_t)f2h(v.x) | ((uint32_t)f2h(v.y) << 16),
+                                             (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16));
+        }
+    } else {
+        for (int i = tid * 8; i < m * k; i += 256 * 8) *(int4 *)(s_x + i) = *(const int4 *)(x16 + i);
+    }
+    __syncthreads();
+
+    float acc[M];
+#pragma unroll
+    for (int i = 0; i < M; i++) acc[i] = 0.0f;
+
+    auto consume = [&](int b, const int4 &q4, uint32_t dbits) {
+        const float d = h2f((uint16_t)dbits);
+#pragma unroll
+        for (int i = 0; i < M; i++) {
+            if (i < m) {
+                const int4 *xp = (const int4 *)(s_x + (size_t)i * k + b * QK);
+                uint32_t xs[16];
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const int4 t = xp[c];
+                    xs[4 * c + 0] = (uint32_t)t.x; xs[4 * c + 1] = (uint32_t)t.y;
+                    xs[4 * c + 2] = (uint32_t)t.z; xs[4 * c + 3] = (uint32_t)t.w;
+                }
+                acc[i] = fmaf(d, q4_block_dot(q4, xs), acc[i]);
+            }
+        }
+    };
+
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int b = j + u * G;
+        if (b < nb) consume(b, wq[u], dw[u]);
+    }
+    for (int b0 = U * G; b0 < nb; b0 += U * G) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int b = min(b0 + j + u * G, nb - 1);
+            wq[u] = ld_stream16(qs + (rbase + b) * 16);
+            dw[u] = wd[rbase + b];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int b = b0 + j + u * G;
+            if (b < nb) consume(b, wq[u], dw[u]);
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < M; i++) {
+        const float s = group_sum<G>(acc[i]);
+        if (row_ok && j == 0 && i < m) y[(size_t)i * n + row] = s;
+    }
+}
+
+template <int G, int U, int M, bool F32X>
+int launch_gu(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16,
+              const float *x32, float *y) {
+    const Q4Planes p = q4_planes(n, k);
+    constexpr int RPB = 256 / G;
+    const size_t smem = (size_t)M * k * 2;
+    if (smem > 64 * 1024) {
+        set_error("gemv_q4_0: activation of %d x %lld does not fit in LDS", M, (long long)k);
+        return MI_ERR_UNSUPPORTED;
+    }
+    hipLaunchKernelGGL((k_gemv_q4_0<G, U, M, F32X>), dim3((unsigned)((n + RPB - 1) / RPB)), dim3(256), smem, st,
+                       base, (const uint16_t *)(base + p.plane), x16, x32, y, (int)n, (int)(k / QK), (int)m);
+    MI_CHECK_LAUNCH("k_gemv_q4_0");
+    return MI_OK;
+}
+
+template <int G, int M, bool F32X>
+int launch_g(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16,
+             const float *x32, float *y) {
+    const int64_t nb = k / QK;
+    int64_t u = (nb + G - 1) / G;
+    if (u > 8) u = (u + 1) / 2 > 8 ? 8 : (u + 1) / 2;
+#define MI_U_CASE(UU) case UU: return launch_gu<G, UU, M, F32X>(st, base, n, k, m, x16, x32, y);
+    switch (u) {
+        MI_U_CASE(1) MI_U_CASE(2) MI_U_CASE(3) MI_U_CASE(4) MI_U_CASE(5) MI_U_CASE(6) MI_U_CASE(7) MI_U_CASE(8)
+    }
+#undef MI_U_CASE
+    return MI_ERR_ARG;
+}
+
+template <int M, bool F32X>
+int launch_m(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16,
+             const float *x32, float *y) {
+    const int64_t nb = k / QK;
+    if (nb <= 128) return launch_g<16, M, F32X>(st, base, n, k, m, x16, x32, y);
+    if (nb <= 256) return launch_g<32, M, F32X>(st, base, n, k, m, x16, x32, y);
+    return launch_g<64, M, F32X>(st, base, n, k, m, x16, x32, y);
+}
+
+template <bool F32X>
+int launch(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16,
+           const float *x32, float *y) {
+    if (m == 1) return launch_m<1, F32X>(st, base, n, k, m, x16, x32, y);
+    if (m == 2) return launch_m<2, F32X>(st, base, n, k, m, x16, x32, y);
+    if (m >= 3 && m <= 4) return launch_m<4, F32X>(st, base, n, k, m, x16, x32, y);
+    if (m >= 5 && m <= 8) return launch_m<8, F32X>(st, base, n, k, m, x16, x32, y);
+    set_error("gemv_q4_0: m=%lld not in 1..8", (long long)m);
+    return MI_ERR_ARG;
+}
+
+int check_shape(const char *what, int64_t n, int64_t k) {
+    MI_CHECK_ARG(n > 0 && k > 0 && k % QK == 0, "%s: bad shape n=%lld k=%lld (k must be a multiple of 32)", what,
+                 (long long)n, (long long)k);
+    MI_CHECK_ARG(n < (1ll << 31) && k < (1ll << 24), "%s: shape too large", what);
+    return MI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mi_q4_0_packed_size(int64_t n, int64_t k) { return q4_planes(n, k).total; }
+
+int mi_prepack_q4_0(void *stream, const void *src_blocks, void *dst_packed, int64_t n, int64_t k) {
+    if (int r = check_shape("prepack_q4_0", n, k)) return r;
+    MI_CHECK_ARG(src_blocks && dst_packed, "prepack_q4_0: null pointer");
+    MI_CHECK_ARG(mi::aligned(src_blocks, 2) && mi::aligned(dst_packed, 256), "prepack_q4_0: src must be 2-byte, dst 256-byte aligned");
+    const Q4Planes p = q4_planes(n, k);
+    const int64_t nblocks = n * (k / QK);
+    uint8_t *base = (uint8_t *)dst_packed;
+    hipLaunchKernelGGL(k_prepack_q4_0, dim3((unsigned)((nblocks + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t *)src_blocks, base, (uint16_t *)(base + p.plane), nblocks);
+    MI_CHECK_LAUNCH("k_prepack_q4_0");
+    return MI_OK;
+}
+
+int mi_prepack_q4_0_host(const void *src_blocks, void *dst_packed, int64_t n, int64_t k) {
+    if (int r = check_shape("prepack_q4_0_host", n, k)) return r;
+    const Q4Planes p = q4_planes(n, k);
+    const int64_t nblocks = n * (k / QK);
+    const uint8_t *s = (const uint8_t *)src_blocks;
+    uint8_t *base = (uint8_t *)dst_packed;
+    memset(base, 0, p.total);
+    for (int64_t i = 0; i < nblocks; i++) {
+        memcpy(base + i * 16, s + i * 18 + 2, 16);
+        memcpy(base + p.plane + i * 2, s + i * 18, 2);
+    }
+    return MI_OK;
+}
+
+int mi_unpack_q4_0_host(const void *packed, void *dst_blocks, int64_t n, int64_t k) {
+    if (int r = check_shape("unpack_q4_0_host", n, k)) return r;
+    const Q4Planes p = q4_planes(n, k);
+    const int64_t nblocks = n * (k / QK);
+    const uint8_t *base = (const uint8_t *)packed;
+    uint8_t *d = (uint8_t *)dst_blocks;
+    for (int64_t i = 0; i < nblocks; i++) {
+        memcpy(d + i * 18, base + p.plane + i * 2, 2);
+        memcpy(d + i * 18 + 2, base + i * 16, 16);
+    }
+    return MI_OK;
+}
+
+int mi_gemv_q4_0_f16(void *stream, const void *w_packed, const uint16_t *x_f16, float *y, int64_t n, int64_t k,
+                     int64_t m) {
+    if (int r = check_shape("gemv_q4_0_f16", n, k)) return r;
+    MI_CHECK_ARG(w_packed && x_f16 && y, "gemv_q4_0_f16: null pointer");
+    MI_CHECK_ARG(mi::aligned(w_packed, 256) && mi::aligned(x_f16, 16), "gemv_q4_0_f16: w_packed must be 256-byte, x 16-byte aligned");
+    return launch<false>((hipStream_t)stream, (const uint8_t *)w_packed, n, k, m, x_f16, nullptr, y);
+}
+
+int mi_mul_mat_q4_0_f32(void *stream, const void *w_packed, const float *x, float *y, int64_t n, int64_t k,
+                        int64_t m) {
+    if (int r = check_shape("mul_mat_q4_0_f32", n, k)) return r;
+    MI_CHECK_ARG(w_packed && x && y, "mul_mat_q4_0_f32: null pointer");
+    MI_CHECK_ARG(mi::aligned(w_packed, 256) && mi::aligned(x, 16), "mul_mat_q4_0_f32: w_packed must be 256-byte, x 16-byte aligned");
+    return launch<true>((hipStream_t)stream, (const uint8_t *)w_packed, n, k, m, nullptr, x, y);
+}
+
+}  // extern "C"

@@ -1,0 +1,410 @@
+// q8_0.hip -- A8W8 (ggml Q8_0 x Q8_0) decode path for gfx950:
+//   * weight prepack into the planar layout (qlo / qhi / d planes),
+//   * per-token activation quantization (ggml Q8_0, SmoothQuant divisor folded in),
+//   * the GEMV: one lane owns whole 32-blocks, exact int32 block dots with
+//     v_dot4_i32_i8, fp32 scaling d_w*d_x fused in the epilogue, split-K over a
+//     power-of-two lane group per output row reduced with DPP row ops.
+//
+// Replaces, on the reference side: the A8W8 weight transform at set_tensor
+// (patch:1674-1695, 1700-1809), W8a8QuantizeCustom
+// (experiments/a8w8/w8a8_quantize_custom_vector.cpp:20-64), MatmulW8a8I32Custom
+// (experiments/a8w8/custom_ops_nz/op_kernel/matmul_w8a8_i32_custom.cpp:15-48)
+// and W8a8DequantCustom (called at patch:1269-1270) with its casts.
+#include "mi_common.h"
+
+#include <string.h>
+
+namespace {
+
+using namespace mi;
+
+constexpr int QK = 32;
+
+struct Q8Planes {
+    size_t plane;  // bytes of one qs half-plane (256-aligned)
+    size_t total;
+};
+
+inline Q8Planes q8_planes(int64_t n, int64_t k) {
+    const int64_t nb = k / QK;
+    Q8Planes p;
+    p.plane = align_up((size_t)n * nb * 16, 256);
+    p.total = 2 * p.plane + align_up((size_t)n * nb * 2, 256);
+    return p;
+}
+
+// ------------------------------------------------------------------ prepack
+
+__global__ void k_prepack_q8_0(const uint8_t *__restrict__ src, uint8_t *__restrict__ qlo,
+                               uint8_t *__restrict__ qhi, uint16_t *__restrict__ dpl, int64_t nblocks) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const uint16_t *s = (const uint16_t *)(src + i * 34);  // 2-byte aligned block
+    uint16_t w[17];
+#pragma unroll
+    for (int t = 0; t < 17; t++) w[t] = s[t];
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        lo[t] = (uint32_t)w[1 + 2 * t] | ((uint32_t)w[2 + 2 * t] << 16);
+        hi[t] = (uint32_t)w[9 + 2 * t] | ((uint32_t)w[10 + 2 * t] << 16);
+    }
+    *(uint4 *)(qlo + i * 16) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    *(uint4 *)(qhi + i * 16) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    dpl[i] = w[0];
+}
+
+// ------------------------------------------------------------------ activation quant
+
+// 8 lanes per 32-block, 4 consecutive values per lane.  Returns the 4 int8 values
+// packed in a uint32 and the block scale d (fp32, before fp16 rounding).
+__device__ __forceinline__ uint32_t quant4(float v0, float v1, float v2, float v3, int rounding, float &d) {
+    float a = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+    const float amax = group_max<8>(a);
+    d = amax / 127.0f;
+    int q0, q1, q2, q3;
+    if (rounding == MI_Q8_ROUND_X86) {
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        q0 = (int)rintf(v0 * id); q1 = (int)rintf(v1 * id);
+        q2 = (int)rintf(v2 * id); q3 = (int)rintf(v3 * id);
+    } else {
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        q0 = (int)roundf(v0 * id); q1 = (int)roundf(v1 * id);
+        q2 = (int)roundf(v2 * id); q3 = (int)roundf(v3 * id);
+    }
+    return (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+           ((uint32_t)(q3 & 0xff) << 24);
+}
+
+// grid: ceil(m*nb / 32) x 256 threads
+__global__ __launch_bounds__(256) void k_act_quant_q8_0(const float *__restrict__ x, const float *__restrict__ inv_s,
+                                                        int8_t *__restrict__ qs, uint16_t *__restrict__ dout,
+                                                        int64_t k, int64_t total_blocks, int rounding) {
+    const int64_t blk = (int64_t)blockIdx.x * 32 + threadIdx.x / 8;
+    const int sub = threadIdx.x % 8;
+    const bool valid = blk < total_blocks;
+    const int64_t nb = k / QK;
+    const int64_t row = valid ? blk / nb : 0;
+    const int64_t b = valid ? blk % nb : 0;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (valid) {
+        v = *(const float4 *)(x + row * k + b * QK + sub * 4);
+        if (inv_s) {
+            const float4 s = *(const float4 *)(inv_s + b * QK + sub * 4);
+            v.x *= s.x; v.y *= s.y; v.z *= s.z; v.w *= s.w;
+        }
+    }
+    float d;
+    const uint32_t q = quant4(v.x, v.y, v.z, v.w, rounding, d);
+    if (valid) {
+        *(uint32_t *)(qs + row * k + b * QK + sub * 4) = q;
+        if (sub == 0) dout[row * nb + b] = f2h(d);
+    }
+}
+
+// ------------------------------------------------------------------ GEMV
+
+// Lane layout: G lanes per output row (power of two), RPB = 256/G rows per
+// 256-thread workgroup.  Lane j of a row handles blocks b = j, j+G, ..., U of
+// them per pass.  The U weight loads of the first pass (2 x 16 B + fp16 scale
+// each) use clamped addresses and no branches, so they are all in flight
+// before the activation is staged in LDS and the HBM latency overlaps the
+// prologue.  The activation rows (m <= M) live in LDS as int8 qs + fp32 d.
+template <int G, int U, int M, bool FUSED>
+__global__ __launch_bounds__(256) void k_gemv_q8_0(const uint8_t *__restrict__ qlo, const uint8_t *__restrict__ qhi,
+                                                   const uint16_t *__restrict__ wd,
+                                                   const int8_t *__restrict__ xq_qs, const uint16_t *__restrict__ xq_d,
+                                                   const float *__restrict__ x, const float *__restrict__ inv_s,
+                                                   float *__restrict__ y, int n, int nb, int m, int rounding) {
+    constexpr int RPB = 256 / G;
+    extern __shared__ __align__(16) uint8_t smem[];
+    int8_t *s_qs = (int8_t *)smem;                                          // [M][nb*32]
+    float *s_d = (float *)(smem + (((size_t)M * nb * QK + 15) / 16) * 16);  // [M][nb]
+
+    const int tid = threadIdx.x;
+    const int j = tid % G;
+    const int row = blockIdx.x * RPB + tid / G;
+    const bool row_ok = row < n;
+    const int k = nb * QK;
+    const size_t rbase = (size_t)min(row, n - 1) * nb;
+
+    int4 lo[U], hi[U];
+    uint32_t dw[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int b = min(j + u * G, nb - 1);
+        lo[u] = ld_stream16(qlo + (rbase + b) * 16);
+        hi[u] = ld_stream16(qhi + (rbase + b) * 16);
+        dw[u] = wd[rbase + b];
+    }
+
+    // ---- stage the activation rows in LDS
+    if constexpr (FUSED) {
+        const int total = m * nb;
+        const int sub = tid % 8;
+        for (int base = 0; base < total; base += 32) {  // uniform trip count across the workgroup
+            const int blk = base + tid / 8;
+            const bool valid = blk < total;
+            const int i = valid ? blk / nb : 0;
+            const int b = valid ? blk % nb : 0;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (valid) {
+                v = *(const float4 *)(x + (size_t)i * k + b * QK + sub * 4);
+                if (inv_s) {
+                    const float4 s = *(const float4 *)(inv_s + b * QK + sub * 4);
+                    v.x *= s.x; v.y *= s.y; v.z *= s.z; v.w *= s.w;
+                }
+            }
+            float d;
+            const uint32_t q = quant4(v.x, v.y, v.z, v.w, rounding, d);
+            if (valid) {
+                *(uint32_t *)(s_qs + (size_t)i * k + b * QK + sub * 4) = q;
+                if (sub == 0) s_d[i * nb + b] = h2f(f2h(d));
+            }
+        }
+    } else {
+        const int qbytes = m * k;
+        for (int off = tid * 16; off < qbytes; off += 256 * 16)
+            *(int4 *)(s_qs + off) = *(const int4 *)(xq_qs + off);
+        for (int i = tid; i < m * nb; i += 256) s_d[i] = h2f(xq_d[i]);
+    }
+    __syncthreads();
+
+    float acc[M];
+#pragma unroll
+    for (int i = 0; i < M; i++) acc[i] = 0.0f;
+
+    auto consume = [&](int b, const int4 &l4, const int4 &h4, uint32_t dbits) {
+        const float dwf = h2f((uint16_t)dbits);
+#pragma unroll
+        for (int i = 0; i < M; i++) {
+            if (i < m) {
+                const int4 *xs = (const int4 *)(s_qs + (size_t)i * k + b * QK);
+                const int4 x0 = xs[0];
+                const int4 x1 = xs[1];
+                int s = 0;
+                s = __builtin_amdgcn_sdot4(l4.x, x0.x, s, false);
+                s = __builtin_amdgcn_sdot4(l4.y, x0.y, s, false);
+                s = __builtin_amdgcn_sdot4(l4.z, x0.z, s, false);
+                s = __builtin_amdgcn_sdot4(l4.w, x0.w, s, false);
+                s = __builtin_amdgcn_sdot4(h4.x, x1.x, s, false);
+                s = __builtin_amdgcn_sdot4(h4.y, x1.y, s, false);
+                s = __builtin_amdgcn_sdot4(h4.z, x1.z, s, false);
+                s = __builtin_amdgcn_sdot4(h4.w, x1.w, s, false);
+                acc[i] = fmaf((float)s, dwf * s_d[i * nb + b], acc[i]);
+            }
+        }
+    };
+
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int b = j + u * G;
+        if (b < nb) consume(b, lo[u], hi[u], dw[u]);
+    }
+    // rows longer than U*G blocks: further passes
+    for (int b0 = U * G; b0 < nb; b0 += U * G) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int b = min(b0 + j + u * G, nb - 1);
+            lo[u] = ld_stream16(qlo + (rbase + b) * 16);
+            hi[u] = ld_stream16(qhi + (rbase + b) * 16);
+            dw[u] = wd[rbase + b];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int b = b0 + j + u * G;
+            if (b < nb) consume(b, lo[u], hi[u], dw[u]);
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < M; i++) {
+        const float s = group_sum<G>(acc[i]);
+        if (row_ok && j == 0 && i < m) y[(size_t)i * n + row] = s;
+    }
+}
+
+// exact per-block int32 dots (debug / bit-exactness check), activation row 0
+__global__ void k_q8_0_block_dots(const uint8_t *__restrict__ qlo, const uint8_t *__restrict__ qhi,
+                                  const int8_t *__restrict__ xq_qs, int32_t *__restrict__ out, int64_t n, int nb) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n * nb) return;
+    const int b = (int)(i % nb);
+    const int4 lo = *(const int4 *)(qlo + i * 16);
+    const int4 hi = *(const int4 *)(qhi + i * 16);
+    const int4 x0 = *(const int4 *)(xq_qs + (size_t)b * QK);
+    const int4 x1 = *(const int4 *)(xq_qs + (size_t)b * QK + 16);
+    int s = 0;
+    s = __builtin_amdgcn_sdot4(lo.x, x0.x, s, false);
+    s = __builtin_amdgcn_sdot4(lo.y, x0.y, s, false);
+    s = __builtin_amdgcn_sdot4(lo.z, x0.z, s, false);
+    s = __builtin_amdgcn_sdot4(lo.w, x0.w, s, false);
+    s = __builtin_amdgcn_sdot4(hi.x, x1.x, s, false);
+    s = __builtin_amdgcn_sdot4(hi.y, x1.y, s, false);
+    s = __builtin_amdgcn_sdot4(hi.z, x1.z, s, false);
+    s = __builtin_amdgcn_sdot4(hi.w, x1.w, s, false);
+    out[i] = s;
+}
+
+// ------------------------------------------------------------------ launch helpers
+
+template <int G, int U, int M, bool FUSED>
+int launch_gemv_gu(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
+                   const uint16_t *xq_d, const float *x, const float *inv_s, float *y, int rounding) {
+    const Q8Planes p = q8_planes(n, k);
+    const int nb = (int)(k / QK);
+    constexpr int RPB = 256 / G;
+    const size_t smem = align_up((size_t)M * k, 16) + (size_t)M * nb * sizeof(float);
+    if (smem > 64 * 1024) {
+        set_error("gemv_q8_0: activation of %d x %lld does not fit in LDS", M, (long long)k);
+        return MI_ERR_UNSUPPORTED;
+    }
+    dim3 grid((unsigned)((n + RPB - 1) / RPB));
+    hipLaunchKernelGGL((k_gemv_q8_0<G, U, M, FUSED>), grid, dim3(256), smem, st, base, base + p.plane,
+                       (const uint16_t *)(base + 2 * p.plane), xq_qs, xq_d, x, inv_s, y, (int)n, nb, (int)m,
+                       rounding);
+    MI_CHECK_LAUNCH("k_gemv_q8_0");
+    return MI_OK;
+}
+
+template <int G, int M, bool FUSED>
+int launch_gemv_g(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
+                  const uint16_t *xq_d, const float *x, const float *inv_s, float *y, int rounding) {
+    const int64_t nb = k / QK;
+    int64_t u = (nb + G - 1) / G;
+    if (u > 8) u = (u + 1) / 2 > 8 ? 8 : (u + 1) / 2;  // several passes of U blocks
+#define MI_U_CASE(UU) \
+    case UU: return launch_gemv_gu<G, UU, M, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
+    switch (u) {
+        MI_U_CASE(1) MI_U_CASE(2) MI_U_CASE(3) MI_U_CASE(4) MI_U_CASE(5) MI_U_CASE(6) MI_U_CASE(7) MI_U_CASE(8)
+    }
+#undef MI_U_CASE
+    return MI_ERR_ARG;
+}
+
+template <int M, bool FUSED>
+int launch_gemv_m(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
+                  const uint16_t *xq_d, const float *x, const float *inv_s, float *y, int rounding) {
+    const int64_t nb = k / QK;
+    // lanes per row: at most 8 blocks per lane per pass, as few lanes per row as that allows
+    if (nb <= 128) return launch_gemv_g<16, M, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
+    if (nb <= 256) return launch_gemv_g<32, M, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
+    return launch_gemv_g<64, M, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
+}
+
+template <bool FUSED>
+int launch_gemv(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
+                const uint16_t *xq_d, const float *x, const float *inv_s, float *y, int rounding) {
+    if (m == 1) return launch_gemv_m<1, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
+    if (m == 2) return launch_gemv_m<2, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
+    if (m >= 3 && m <= 4) return launch_gemv_m<4, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
+    if (m >= 5 && m <= 8) return launch_gemv_m<8, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
+    set_error("gemv_q8_0: m=%lld not in 1..8", (long long)m);
+    return MI_ERR_ARG;
+}
+
+int check_shape(const char *what, int64_t n, int64_t k) {
+    MI_CHECK_ARG(n > 0 && k > 0 && k % QK == 0, "%s: bad shape n=%lld k=%lld (k must be a multiple of 32)", what,
+                 (long long)n, (long long)k);
+    MI_CHECK_ARG(n < (1ll << 31) && k < (1ll << 24), "%s: shape too large n=%lld k=%lld", what, (long long)n,
+                 (long long)k);
+    return MI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mi_q8_0_packed_size(int64_t n, int64_t k) { return q8_planes(n, k).total; }
+
+size_t mi_xq_d_offset(int64_t m, int64_t k) { return mi::align_up((size_t)m * k, 256); }
+size_t mi_xq_size(int64_t m, int64_t k) { return mi_xq_d_offset(m, k) + mi::align_up((size_t)m * (k / QK) * 2, 256); }
+
+int mi_prepack_q8_0(void *stream, const void *src_blocks, void *dst_packed, int64_t n, int64_t k) {
+    if (int r = check_shape("prepack_q8_0", n, k)) return r;
+    MI_CHECK_ARG(src_blocks && dst_packed, "prepack_q8_0: null pointer");
+    MI_CHECK_ARG(mi::aligned(src_blocks, 2) && mi::aligned(dst_packed, 256), "prepack_q8_0: src must be 2-byte, dst 256-byte aligned");
+    const Q8Planes p = q8_planes(n, k);
+    const int64_t nblocks = n * (k / QK);
+    uint8_t *base = (uint8_t *)dst_packed;
+    hipLaunchKernelGGL(k_prepack_q8_0, dim3((unsigned)((nblocks + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t *)src_blocks, base, base + p.plane, (uint16_t *)(base + 2 * p.plane), nblocks);
+    MI_CHECK_LAUNCH("k_prepack_q8_0");
+    return MI_OK;
+}
+
+int mi_prepack_q8_0_host(const void *src_blocks, void *dst_packed, int64_t n, int64_t k) {
+    if (int r = check_shape("prepack_q8_0_host", n, k)) return r;
+    const Q8Planes p = q8_planes(n, k);
+    const int64_t nblocks = n * (k / QK);
+    const uint8_t *s = (const uint8_t *)src_blocks;
+    uint8_t *base = (uint8_t *)dst_packed;
+    memset(base, 0, p.total);
+    for (int64_t i = 0; i < nblocks; i++) {
+        memcpy(base + i * 16, s + i * 34 + 2, 16);
+        memcpy(base + p.plane + i * 16, s + i * 34 + 18, 16);
+        memcpy(base + 2 * p.plane + i * 2, s + i * 34, 2);
+    }
+    return MI_OK;
+}
+
+int mi_unpack_q8_0_host(const void *packed, void *dst_blocks, int64_t n, int64_t k) {
+    if (int r = check_shape("unpack_q8_0_host", n, k)) return r;
+    const Q8Planes p = q8_planes(n, k);
+    const int64_t nblocks = n * (k / QK);
+    const uint8_t *base = (const uint8_t *)packed;
+    uint8_t *d = (uint8_t *)dst_blocks;
+    for (int64_t i = 0; i < nblocks; i++) {
+        memcpy(d + i * 34, base + 2 * p.plane + i * 2, 2);
+        memcpy(d + i * 34 + 2, base + i * 16, 16);
+        memcpy(d + i * 34 + 18, base + p.plane + i * 16, 16);
+    }
+    return MI_OK;
+}
+
+int mi_act_quant_q8_0(void *stream, const float *x, const float *inv_s, int64_t m, int64_t k, void *xq,
+                      int rounding) {
+    if (int r = check_shape("act_quant_q8_0", m, k)) return r;
+    MI_CHECK_ARG(x && xq, "act_quant_q8_0: null pointer");
+    MI_CHECK_ARG(mi::aligned(x, 16) && mi::aligned(xq, 16) && (!inv_s || mi::aligned(inv_s, 16)),
+                 "act_quant_q8_0: pointers must be 16-byte aligned");
+    const int64_t total = m * (k / QK);
+    uint8_t *base = (uint8_t *)xq;
+    hipLaunchKernelGGL(k_act_quant_q8_0, dim3((unsigned)((total + 31) / 32)), dim3(256), 0, (hipStream_t)stream, x,
+                       inv_s, (int8_t *)base, (uint16_t *)(base + mi_xq_d_offset(m, k)), k, total, rounding);
+    MI_CHECK_LAUNCH("k_act_quant_q8_0");
+    return MI_OK;
+}
+
+int mi_gemv_q8_0(void *stream, const void *w_packed, const void *xq, float *y, int64_t n, int64_t k, int64_t m) {
+    if (int r = check_shape("gemv_q8_0", n, k)) return r;
+    MI_CHECK_ARG(w_packed && xq && y, "gemv_q8_0: null pointer");
+    MI_CHECK_ARG(mi::aligned(w_packed, 256) && mi::aligned(xq, 16), "gemv_q8_0: w_packed must be 256-byte, xq 16-byte aligned");
+    const uint8_t *xb = (const uint8_t *)xq;
+    return launch_gemv<false>((hipStream_t)stream, (const uint8_t *)w_packed, n, k, m, (const int8_t *)xb,
+                              (const uint16_t *)(xb + mi_xq_d_offset(m, k)), nullptr, nullptr, y, 0);
+}
+
+int mi_mul_mat_q8_0_f32(void *stream, const void *w_packed, const float *x, const float *inv_s, float *y,
+                        int64_t n, int64_t k, int64_t m, int rounding) {
+    if (int r = check_shape("mul_mat_q8_0_f32", n, k)) return r;
+    MI_CHECK_ARG(w_packed && x && y, "mul_mat_q8_0_f32: null pointer");
+    MI_CHECK_ARG(mi::aligned(w_packed, 256) && mi::aligned(x, 16) && (!inv_s || mi::aligned(inv_s, 16)),
+                 "mul_mat_q8_0_f32: w_packed must be 256-byte, x/inv_s 16-byte aligned");
+    return launch_gemv<true>((hipStream_t)stream, (const uint8_t *)w_packed, n, k, m, nullptr, nullptr, x, inv_s, y,
+                             rounding);
+}
+
+int mi_q8_0_block_dots(void *stream, const void *w_packed, const void *xq, int32_t *out, int64_t n, int64_t k) {
+    if (int r = check_shape("q8_0_block_dots", n, k)) return r;
+    MI_CHECK_ARG(w_packed && xq && out, "q8_0_block_dots: null pointer");
+    const Q8Planes p = q8_planes(n, k);
+    const int64_t total = n * (k / QK);
+    const uint8_t *base = (const uint8_t *)w_packed;
+    hipLaunchKernelGGL(k_q8_0_block_dots, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       base, base + p.plane, (const int8_t *)xq, out, n, (int)(k / QK));
+    MI_CHECK_LAUNCH("k_q8_0_block_dots");
+    return MI_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,304 @@
+"""Python host binding of libggml_mi355x.so (ctypes + numpy, no torch).
+
+The library carries its own HIP runtime link (/opt/rocm), so the host side
+here uses the library's device-memory, stream and event wrappers instead of a
+second HIP runtime.  Every entry point raises MiError on a non-zero status;
+nothing falls back to a CPU path: a missing library is an ImportError-like
+failure at load time.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libggml_mi355x.so")
+
+MI_OK = 0
+MI_ERR_ARG = -1
+MI_ERR_ALIGN = -2
+MI_ERR_WORKSPACE = -3
+MI_ERR_NODEVICE = -4
+MI_ERR_UNSUPPORTED = -5
+
+Q8_ROUND_REF = 0
+Q8_ROUND_X86 = 1
+
+
+class MiError(RuntimeError):
+    def __init__(self, fn, code, msg):
+        super().__init__(f"{fn} failed with status {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_SZ = ctypes.c_size_t
+_F = ctypes.c_float
+_I = ctypes.c_int
+
+_SIGS = {
+    "mi_last_error": (ctypes.c_char_p, []),
+    "mi_device_count": (_I, [ctypes.POINTER(_I)]),
+    "mi_set_device": (_I, [_I]),
+    "mi_device_name": (_I, [_I, ctypes.c_char_p, _SZ]),
+    "mi_malloc": (_I, [ctypes.POINTER(_P), _SZ]),
+    "mi_free": (_I, [_P]),
+    "mi_memcpy_h2d": (_I, [_P, _P, _SZ, _P]),
+    "mi_memcpy_d2h": (_I, [_P, _P, _SZ, _P]),
+    "mi_memcpy_d2d": (_I, [_P, _P, _SZ, _P]),
+    "mi_memset": (_I, [_P, _I, _SZ, _P]),
+    "mi_stream_create": (_I, [ctypes.POINTER(_P)]),
+    "mi_stream_destroy": (_I, [_P]),
+    "mi_stream_sync": (_I, [_P]),
+    "mi_device_sync": (_I, []),
+    "mi_event_create": (_I, [ctypes.POINTER(_P)]),
+    "mi_event_destroy": (_I, [_P]),
+    "mi_event_record": (_I, [_P, _P]),
+    "mi_event_elapsed_ms": (_I, [ctypes.POINTER(_F), _P, _P]),
+    "mi_q8_0_packed_size": (_SZ, [_I64, _I64]),
+    "mi_q4_0_packed_size": (_SZ, [_I64, _I64]),
+    "mi_prepack_q8_0": (_I, [_P, _P, _P, _I64, _I64]),
+    "mi_prepack_q4_0": (_I, [_P, _P, _P, _I64, _I64]),
+    "mi_prepack_q8_0_host": (_I, [_P, _P, _I64, _I64]),
+    "mi_prepack_q4_0_host": (_I, [_P, _P, _I64, _I64]),
+    "mi_unpack_q8_0_host": (_I, [_P, _P, _I64, _I64]),
+    "mi_unpack_q4_0_host": (_I, [_P, _P, _I64, _I64]),
+    "mi_xq_size": (_SZ, [_I64, _I64]),
+    "mi_xq_d_offset": (_SZ, [_I64, _I64]),
+    "mi_act_quant_q8_0": (_I, [_P, _P, _P, _I64, _I64, _P, _I]),
+    "mi_gemv_q8_0": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
+    "mi_mul_mat_q8_0_f32": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I]),
+    "mi_q8_0_block_dots": (_I, [_P, _P, _P, _P, _I64, _I64]),
+    "mi_gemv_q4_0_f16": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
+    "mi_mul_mat_q4_0_f32": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
+    "mi_gemv_f16": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _I64]),
+    "mi_fa_decode_workspace_size": (_SZ, [_I64, _I64, _I64, _I64]),
+    "mi_fa_decode": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _SZ, _SZ, _SZ, _SZ, _F, _P, _P, _SZ]),
+    "mi_kv_lengths": (_I, [_P, _P, _I, _I64, _I64, _P]),
+}
+
+# every symbol the C ABI header declares (checked by the CPU tests)
+EXPORTED = tuple(_SIGS)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise OSError(f"libggml_mi355x.so is not built at {LIB_PATH}; run __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error():
+    return lib().mi_last_error().decode(errors="replace")
+
+
+def _call(name, *args):
+    r = getattr(lib(), name)(*args)
+    if r != MI_OK:
+        raise MiError(name, r, last_error())
+    return r
+
+
+def device_count():
+    n = _I(0)
+    lib().mi_device_count(ctypes.byref(n))
+    return n.value
+
+
+def device_name(dev=0):
+    buf = ctypes.create_string_buffer(256)
+    _call("mi_device_name", dev, buf, 256)
+    return buf.value.decode()
+
+
+# ---------------------------------------------------------------- memory
+
+class DeviceBuffer:
+    """A hipMalloc'd buffer; .ptr is the device address."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        p = _P()
+        _call("mi_malloc", ctypes.byref(p), max(self.nbytes, 1))
+        self.ptr = p.value
+
+    def free(self):
+        if self.ptr:
+            lib().mi_free(_P(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def upload(self, arr, stream=None, offset=0):
+        arr = np.ascontiguousarray(arr)
+        assert offset + arr.nbytes <= self.nbytes
+        _call("mi_memcpy_h2d", _P(self.ptr + offset), arr.ctypes.data, arr.nbytes, _P(stream))
+        return self
+
+    def download(self, dtype, count=None, stream=None, offset=0):
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        out = np.empty(count, dtype=dtype)
+        _call("mi_memcpy_d2h", out.ctypes.data, _P(self.ptr + offset), out.nbytes, _P(stream))
+        return out
+
+    def zero(self, stream=None):
+        _call("mi_memset", _P(self.ptr), 0, self.nbytes, _P(stream))
+        return self
+
+
+def to_device(arr, stream=None):
+    arr = np.ascontiguousarray(arr)
+    return DeviceBuffer(arr.nbytes).upload(arr, stream)
+
+
+class Stream:
+    def __init__(self):
+        p = _P()
+        _call("mi_stream_create", ctypes.byref(p))
+        self.ptr = p.value
+
+    def sync(self):
+        _call("mi_stream_sync", _P(self.ptr))
+
+    def destroy(self):
+        if self.ptr:
+            lib().mi_stream_destroy(_P(self.ptr))
+            self.ptr = None
+
+
+class Event:
+    def __init__(self):
+        p = _P()
+        _call("mi_event_create", ctypes.byref(p))
+        self.ptr = p.value
+
+    def record(self, stream=None):
+        _call("mi_event_record", _P(self.ptr), _P(stream))
+
+    def elapsed_ms(self, end):
+        ms = _F(0)
+        _call("mi_event_elapsed_ms", ctypes.byref(ms), _P(self.ptr), _P(end.ptr))
+        return ms.value
+
+    def destroy(self):
+        if self.ptr:
+            lib().mi_event_destroy(_P(self.ptr))
+            self.ptr = None
+
+
+def device_sync():
+    _call("mi_device_sync")
+
+
+# ---------------------------------------------------------------- prepack
+
+def q8_0_packed_size(n, k):
+    return lib().mi_q8_0_packed_size(n, k)
+
+
+def q4_0_packed_size(n, k):
+    return lib().mi_q4_0_packed_size(n, k)
+
+
+def prepack_q8_0_host(blocks, n, k):
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.empty(q8_0_packed_size(n, k), dtype=np.uint8)
+    _call("mi_prepack_q8_0_host", blocks.ctypes.data, out.ctypes.data, n, k)
+    return out
+
+
+def unpack_q8_0_host(packed, n, k):
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    out = np.empty(n * (k // 32) * 34, dtype=np.uint8)
+    _call("mi_unpack_q8_0_host", packed.ctypes.data, out.ctypes.data, n, k)
+    return out.reshape(n, -1)
+
+
+def prepack_q4_0_host(blocks, n, k):
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.empty(q4_0_packed_size(n, k), dtype=np.uint8)
+    _call("mi_prepack_q4_0_host", blocks.ctypes.data, out.ctypes.data, n, k)
+    return out
+
+
+def unpack_q4_0_host(packed, n, k):
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    out = np.empty(n * (k // 32) * 18, dtype=np.uint8)
+    _call("mi_unpack_q4_0_host", packed.ctypes.data, out.ctypes.data, n, k)
+    return out.reshape(n, -1)
+
+
+def prepack_q8_0(src_dev, dst_dev, n, k, stream=None):
+    _call("mi_prepack_q8_0", _P(stream), _P(src_dev), _P(dst_dev), n, k)
+
+
+def prepack_q4_0(src_dev, dst_dev, n, k, stream=None):
+    _call("mi_prepack_q4_0", _P(stream), _P(src_dev), _P(dst_dev), n, k)
+
+
+# ---------------------------------------------------------------- kernels (device pointers)
+
+def xq_size(m, k):
+    return lib().mi_xq_size(m, k)
+
+
+def xq_d_offset(m, k):
+    return lib().mi_xq_d_offset(m, k)
+
+
+def act_quant_q8_0(x, inv_s, m, k, xq, rounding=Q8_ROUND_X86, stream=None):
+    _call("mi_act_quant_q8_0", _P(stream), _P(x), _P(inv_s), m, k, _P(xq), rounding)
+
+
+def gemv_q8_0(w_packed, xq, y, n, k, m=1, stream=None):
+    _call("mi_gemv_q8_0", _P(stream), _P(w_packed), _P(xq), _P(y), n, k, m)
+
+
+def mul_mat_q8_0_f32(w_packed, x, inv_s, y, n, k, m=1, rounding=Q8_ROUND_X86, stream=None):
+    _call("mi_mul_mat_q8_0_f32", _P(stream), _P(w_packed), _P(x), _P(inv_s), _P(y), n, k, m, rounding)
+
+
+def q8_0_block_dots(w_packed, xq, out, n, k, stream=None):
+    _call("mi_q8_0_block_dots", _P(stream), _P(w_packed), _P(xq), _P(out), n, k)
+
+
+def gemv_q4_0_f16(w_packed, x16, y, n, k, m=1, stream=None):
+    _call("mi_gemv_q4_0_f16", _P(stream), _P(w_packed), _P(x16), _P(y), n, k, m)
+
+
+def mul_mat_q4_0_f32(w_packed, x, y, n, k, m=1, stream=None):
+    _call("mi_mul_mat_q4_0_f32", _P(stream), _P(w_packed), _P(x), _P(y), n, k, m)
+
+
+def gemv_f16(w, ldw, x, y, n, k, m=1, stream=None):
+    _call("mi_gemv_f16", _P(stream), _P(w), ldw, _P(x), _P(y), n, k, m)
+
+
+def fa_decode_workspace_size(n_kv, n_q_heads, n_kv_heads, d):
+    return lib().mi_fa_decode_workspace_size(n_kv, n_q_heads, n_kv_heads, d)
+
+
+def fa_decode(q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1, k_nb2, v_nb1, v_nb2, scale, out,
+              ws, ws_bytes, stream=None):
+    _call("mi_fa_decode", _P(stream), _P(q), _P(k), _P(v), _P(mask), _P(kv_len), n_kv, n_q_heads, n_kv_heads, d,
+          k_nb1, k_nb2, v_nb1, v_nb2, scale, _P(out), _P(ws), ws_bytes)
+
+
+def kv_lengths(mask, is_f16, n_kv, n_rows, out, stream=None):
+    _call("mi_kv_lengths", _P(stream), _P(mask), 1 if is_f16 else 0, n_kv, n_rows, _P(out))
