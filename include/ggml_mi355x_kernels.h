@@ -57,6 +57,12 @@ int mi_event_create(void **event);
 int mi_event_destroy(void *event);
 int mi_event_record(void *event, void *stream);
 int mi_event_elapsed_ms(float *ms, void *start, void *stop);
+/* stream capture into a HIP graph (launch-overhead-free replay of a fixed launch sequence);
+ * nothing captured may call hipMemsetAsync */
+int mi_graph_capture_begin(void *stream);
+int mi_graph_capture_end(void *stream, void **graph_exec);
+int mi_graph_launch(void *graph_exec, void *stream);
+int mi_graph_destroy(void *graph_exec);
 
 /* ------------------------------------------------------------------------
  * Weight prepack (replaces the set_tensor side layouts: FRACTAL_NZ via
@@ -103,10 +109,19 @@ int mi_act_quant_q8_0(void *stream, const float *x, const float *inv_s, int64_t 
  * ---------------------------------------------------------------------- */
 int mi_gemv_q8_0(void *stream, const void *w_packed, const void *xq, float *y, int64_t n, int64_t k,
                  int64_t m);
-/* fused chain: quantize x (with optional inv_s) in the kernel prologue, then GEMV;
- * the whole A8W8 branch of ggml_cann_mat_mul_fp (patch:1223-1281) in one launch */
+/* the whole A8W8 branch of ggml_cann_mat_mul_fp (patch:1223-1281): quantize x (with
+ * optional inv_s) then GEMV.  For m == 1 and k <= 4096 the quantization runs in the GEMV
+ * prologue (one launch, no workspace); otherwise ws must hold
+ * mi_mul_mat_q8_0_workspace_size(m, k) bytes for the quantized activation. */
+size_t mi_mul_mat_q8_0_workspace_size(int64_t m, int64_t k);
 int mi_mul_mat_q8_0_f32(void *stream, const void *w_packed, const float *x, const float *inv_s, float *y,
-                        int64_t n, int64_t k, int64_t m, int rounding);
+                        int64_t n, int64_t k, int64_t m, int rounding, void *ws, size_t ws_bytes);
+/* the same for up to four matrices of equal k that read one activation row (q/k/v or
+ * gate/up): rows of matrix i go to y[i]; a single launch when k <= 4096, otherwise one
+ * quantization into ws and one GEMV per matrix */
+int mi_mul_mat_q8_0_f32_multi(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
+                              float *const *y, int64_t k, const float *x, const float *inv_s, int rounding, void *ws,
+                              size_t ws_bytes);
 /* debug: exact per-block int32 dot products out[row][b] for activation row 0 */
 int mi_q8_0_block_dots(void *stream, const void *w_packed, const void *xq, int32_t *out, int64_t n, int64_t k);
 
@@ -142,7 +157,9 @@ int mi_gemv_f16(void *stream, const uint16_t *w, int64_t ldw, const float *x, fl
  * kv_len: device int32[1], effective KV length (ggml src[5]); used when
  *        0 < *kv_len < n_kv, else n_kv; may be NULL
  * out  : fp32 [n_q_heads][d]
- * ws   : workspace of mi_fa_decode_workspace_size() bytes (split partials)
+ * ws   : workspace of mi_fa_decode_workspace_size() bytes, 256-byte aligned (split partials and
+ *        per-kv-head arrival counters); it must be zero-filled once before its first use and is
+ *        left zeroed by every call, so calls sharing one workspace must be stream-ordered
  * d must be 64 or 128; n_q_heads % n_kv_heads == 0; group size <= 8.
  * ---------------------------------------------------------------------- */
 size_t mi_fa_decode_workspace_size(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d);
@@ -150,6 +167,33 @@ int mi_fa_decode(void *stream, const float *q, const void *k, const void *v, con
                  const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
                  size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out,
                  void *ws, size_t ws_bytes);
+
+/* ------------------------------------------------------------------------
+ * Decode-graph glue ops (one launch each; ggml-CPU semantics of
+ * ggml/src/ggml-cpu/ops.cpp): the ops a llama.cpp decode graph places around
+ * MUL_MAT and FLASH_ATTN_EXT, so that the whole token stays on the device.
+ * ---------------------------------------------------------------------- */
+/* y = x / sqrt(mean(x^2) + eps) [* w], rows of ne0 fp32 (ggml RMS_NORM [+ MUL]) */
+int mi_rms_norm(void *stream, const float *x, const float *w, float *y, int64_t ne0, int64_t nrows, float eps);
+/* d[i] = a[i] + b[i % nb] / a[i] * b[i % nb] (ggml ADD / MUL with row broadcast) */
+int mi_add_bcast(void *stream, const float *a, const float *b, float *d, int64_t n, int64_t nb);
+int mi_mul_bcast(void *stream, const float *a, const float *b, float *d, int64_t n, int64_t nb);
+/* neox RoPE of x[ne2 tokens][ne1 heads][ne0] (byte strides nb1, nb2 in, ob1, ob2 out), pos[ne2] */
+int mi_rope_neox(void *stream, const float *x, float *y, const int32_t *pos, int64_t ne0, int64_t ne1, int64_t ne2,
+                 int64_t n_dims, float freq_base, float freq_scale, float attn_factor, size_t nb1, size_t nb2,
+                 size_t ob1, size_t ob2);
+/* fp16 table rows idx[r] = src row r (ggml SET_ROWS into the KV cache); idx int64 or int32 */
+int mi_set_rows_f16(void *stream, const float *src, const void *idx, int idx_is_i64, uint16_t *dst, int64_t ne0,
+                    int64_t nrows, size_t snb1, size_t dnb1, int64_t n_dst_rows);
+/* dst row r = src row idx[r] as fp32 (ggml GET_ROWS, fp16 or fp32 table) */
+int mi_get_rows(void *stream, const void *src, int src_is_f16, const int32_t *idx, float *dst, int64_t ne0,
+                int64_t nrows, size_t snb1, int64_t n_src_rows);
+/* d = silu(g) * u (ggml GLU SWIGLU, split form) */
+int mi_swiglu(void *stream, const float *g, const float *u, float *d, int64_t n);
+/* index of the first maximum of each row (ggml ARGMAX) */
+int mi_argmax(void *stream, const float *x, int32_t *out, int64_t ne0, int64_t nrows);
+/* decode mask row from a device length: 0 for i < *len, -inf beyond */
+int mi_fill_mask_f16(void *stream, uint16_t *mask, const int32_t *len, int64_t n_kv);
 
 /* ------------------------------------------------------------------------
  * kv_lengths on the device (replaces the host scan set_input_kv_lengths,

@@ -1,0 +1,67 @@
+/*
+ * mi_qwen2.h -- a minimal Qwen2 decode driver over the ggml backend API.
+ *
+ * It stands in for the llama.cpp layers above the backend (model loader and
+ * graph builder, src/llama-model.cpp / llama-graph.cpp of llama.cpp @ 37b3a9e0),
+ * which are not part of this repository: it names tensors as llama.cpp's GGUF
+ * loader does, uploads them with ggml_backend_tensor_set (so the backend's
+ * prepack runs as it would under llama.cpp), builds the per-token graph with the
+ * same nodes as llama.cpp's Qwen2 builder (RMS_NORM, MUL, MUL_MAT, ADD, ROPE neox,
+ * SET_ROWS into an fp16 KV cache, FLASH_ATTN_EXT with the kv_lengths src[5] of
+ * patch:2934-2997, GLU swiglu, GET_ROWS, ARGMAX) and runs it with
+ * ggml_backend_graph_compute.  One token per step (bs = 1), greedy sampling.
+ */
+#ifndef MI_QWEN2_H
+#define MI_QWEN2_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mi_qwen2_hparams {
+    int32_t n_layer;
+    int32_t n_embd;
+    int32_t n_head;
+    int32_t n_head_kv;
+    int32_t head_dim;
+    int32_t n_ff;
+    int32_t n_vocab;
+    int32_t n_ctx;      /* KV cache capacity (positions) */
+    float rms_eps;
+    float rope_theta;
+    int32_t wtype;      /* ggml type id of the projection weights: 8 = Q8_0, 2 = Q4_0 */
+    int32_t use_bias;   /* q/k/v biases (Qwen2 has them) */
+} mi_qwen2_hparams;
+
+typedef struct mi_qwen2 mi_qwen2;
+
+/* model with uninitialised weights and a zeroed KV cache on HIP device `device` */
+mi_qwen2 *mi_qwen2_create(const mi_qwen2_hparams *hp, int device);
+void mi_qwen2_free(mi_qwen2 *m);
+const char *mi_qwen2_last_error(void);
+
+/* upload one tensor by its GGUF name (token_embd.weight, blk.N.attn_q.weight, ...,
+ * output_norm.weight); size must equal the tensor's ggml byte size */
+int mi_qwen2_set_tensor(mi_qwen2 *m, const char *name, const void *data, size_t size);
+/* SmoothQuant factors s (length = the weight's input dim) of one projection weight */
+int mi_qwen2_set_smooth(mi_qwen2 *m, const char *weight_name, const float *s, int64_t n);
+/* byte size and dims of a named tensor (dims[0] = ne0, dims[1] = ne1); -1 if unknown */
+int64_t mi_qwen2_tensor_nbytes(mi_qwen2 *m, const char *name, int64_t *dims);
+
+/* one decode step at position pos: writes the argmax token, optionally the logits [n_vocab] */
+int mi_qwen2_decode(mi_qwen2 *m, int32_t token, int32_t pos, int32_t *next_token, float *logits);
+/* the prompt (one token per step), then n_gen timed greedy decode steps: the first
+ * consumes the prompt's greedy continuation, out_tokens[i] is the token step i produces;
+ * the seconds of the n_gen steps are written to *gen_seconds when not NULL */
+int mi_qwen2_generate(mi_qwen2 *m, const int32_t *prompt, int32_t n_prompt, int32_t n_gen, int32_t *out_tokens,
+                      double *gen_seconds);
+/* forget the KV cache contents (positions restart at 0) */
+int mi_qwen2_reset(mi_qwen2 *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

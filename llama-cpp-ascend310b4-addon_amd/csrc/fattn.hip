@@ -6,18 +6,24 @@
 // split across workgroups (one per (split, kv head)); every K/V row is read once
 // and shared by all q heads of its GQA group; each workgroup keeps an online
 // softmax state (m, l, o) per q head and a log-sum-exp combine kernel merges
-// the splits.  Score order follows the reference and ggml: q rounded to fp16,
+// the splits (inside the last workgroup of a kv head when there are few splits,
+// else in a parallel combine kernel).  Score order follows the reference and ggml: q rounded to fp16,
 // s = (q.k) * scale, s += mask, online softmax, one final divide.
 #include "mi_common.h"
 
 #include <math.h>
+#include <stdlib.h>
 
 namespace {
 
 using namespace mi;
 
 constexpr int kNW = 4;  // waves per workgroup
-constexpr int kT = 4;   // positions per lane group per tile
+constexpr float kLog2e = 1.4426950408889634f;
+
+// 2^x with the hardware v_exp_f32 (arguments here are <= 0; -inf gives 0)
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+constexpr int kT = 8;   // positions per lane group per tile (all loads of a tile in flight together)
 
 template <int D>
 constexpr int part_stride() { return D + 4; }  // o[D], m, l, pad -> 16-byte aligned records
@@ -27,15 +33,27 @@ struct FaPlan {
     int n_splits;
 };
 
+// One workgroup per (split, kv head).  Aim at one workgroup per CU for long
+// contexts (chunk >= 64 positions, multiple of 64); short contexts get few
+// splits, and with at most kFusedMaxSplits splits the last workgroup of a kv
+// head merges the partials itself (no second launch).
+constexpr int kFusedMaxSplits = 16;
+constexpr int kMaxSplits = 1024;
+
 inline FaPlan fa_plan(int64_t n_kv, int64_t n_kv_heads) {
     const int64_t target_wg = 512;
     int64_t per = (n_kv * n_kv_heads + target_wg - 1) / target_wg;
-    if (per < 32) per = 32;
-    per = (per + 15) / 16 * 16;
+    per = (per + 63) / 64 * 64;
+    if (per < 64) per = 64;
+    while ((n_kv + per - 1) / per > kMaxSplits) per *= 2;
     FaPlan p;
     p.chunk = (int)per;
     p.n_splits = (int)((n_kv + per - 1) / per);
     return p;
+}
+
+inline size_t fa_part_bytes(int64_t n_q_heads, int64_t n_splits, int64_t d) {
+    return align_up((size_t)n_q_heads * n_splits * (d + 4) * sizeof(float), 256);
 }
 
 template <int LPR>
@@ -47,20 +65,21 @@ __device__ __forceinline__ void merge_state(float &m, float &l, float *o, int xo
     for (int i = 0; i < 8; i++) oo[i] = __shfl_xor(o[i], xor_mask, 64);
     const float mn = fmaxf(m, mo);
     if (mn == -INFINITY) return;
-    const float a = expf(m - mn);
-    const float b = expf(mo - mn);
+    const float a = fexp2(m - mn);
+    const float b = fexp2(mo - mn);
     l = l * a + lo * b;
 #pragma unroll
     for (int i = 0; i < 8; i++) o[i] = o[i] * a + oo[i] * b;
     m = mn;
 }
 
-template <int D, int GQ>
+template <int D, int GQ, bool MASK>
 __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, const uint8_t *__restrict__ kc,
                                                   const uint8_t *__restrict__ vc, const uint16_t *__restrict__ mask,
                                                   const int32_t *__restrict__ kv_len_p, int n_kv, size_t k_nb1,
                                                   size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, int chunk,
-                                                  int n_splits, float *__restrict__ part, float *__restrict__ out) {
+                                                  int n_splits, float *__restrict__ part, float *__restrict__ out,
+                                                  unsigned *__restrict__ counters) {
     constexpr int LPR = D / 8;     // lanes per position row (16 B = 8 halves per lane)
     constexpr int PPW = 64 / LPR;  // positions per wave step
     constexpr int NG = kNW * PPW;  // lane groups per workgroup
@@ -77,13 +96,14 @@ __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, c
     const int c = lane % LPR;
     const int g = wave * PPW + lane / LPR;
 
-    int eff = n_kv;
-    if (kv_len_p) {
-        const int kl = *kv_len_p;
-        if (kl > 0 && kl < n_kv) eff = kl;
-    }
+    // The effective length (ggml src[5]) bounds the tiles after the first: the first
+    // tile's K/V loads are issued against the physical length so that they do not
+    // wait for the kv_len load (the KV view handed in is at most a little longer
+    // than the used cache, so the speculative rows are few).
+    const int kl = kv_len_p ? *kv_len_p : n_kv;
+    const int eff = (kl > 0 && kl < n_kv) ? kl : n_kv;
     const int start = split * chunk;
-    const int end = min(start + chunk, eff);
+    const int end_phys = min(start + chunk, n_kv);
 
     uint32_t qh[GQ][4];
 #pragma unroll
@@ -108,24 +128,22 @@ __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, c
     const uint8_t *kb = kc + (size_t)kvh * k_nb2 + (size_t)c * 16;
     const uint8_t *vb = vc + (size_t)kvh * v_nb2 + (size_t)c * 16;
 
-    for (int p0 = start + g; p0 < end; p0 += NG * kT) {
+    // first tile: speculative (physical bound); later tiles stop at the effective length
+    const int end_eff = min(end_phys, eff);
+    for (int p0 = start + g, it = 0; p0 < (it == 0 ? end_phys : end_eff); p0 += NG * kT, it++) {
         int4 kr[kT], vr[kT];
         float mk[kT];
         bool val[kT];
 #pragma unroll
-        for (int t = 0; t < kT; t++) {
+        for (int t = 0; t < kT; t++) {  // branch-free loads (clamped rows) keep all 2*kT loads in flight
             const int p = p0 + t * NG;
-            val[t] = p < end;
-            if (val[t]) {
-                kr[t] = *(const int4 *)(kb + (size_t)p * k_nb1);
-                vr[t] = *(const int4 *)(vb + (size_t)p * v_nb1);
-                mk[t] = mask ? h2f(mask[p]) : 0.0f;
-            } else {
-                kr[t] = make_int4(0, 0, 0, 0);
-                vr[t] = make_int4(0, 0, 0, 0);
-                mk[t] = -INFINITY;
-            }
+            const int pc = min(p, end_phys - 1);
+            kr[t] = *(const int4 *)(kb + (size_t)pc * k_nb1);
+            vr[t] = *(const int4 *)(vb + (size_t)pc * v_nb1);
+            mk[t] = MASK ? h2f(mask[pc]) : 0.0f;
         }
+#pragma unroll
+        for (int t = 0; t < kT; t++) val[t] = p0 + t * NG < min(end_phys, eff);
         float s[GQ][kT];
 #pragma unroll
         for (int t = 0; t < kT; t++) {
@@ -137,18 +155,9 @@ __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, c
                 dsum = fdot2(qh[h][2], (uint32_t)kr[t].z, dsum);
                 dsum = fdot2(qh[h][3], (uint32_t)kr[t].w, dsum);
                 dsum = group_sum<LPR>(dsum);
-                const float sc = __fadd_rn(__fmul_rn(dsum, scale), mk[t]);
+                // ggml order: s = (q.k)*scale; s += mask; kept in log2 units for v_exp_f32
+                const float sc = __fadd_rn(__fmul_rn(dsum, scale), mk[t]) * kLog2e;
                 s[h][t] = val[t] ? sc : -INFINITY;
-            }
-        }
-        float vf[kT][8];
-#pragma unroll
-        for (int t = 0; t < kT; t++) {
-            const uint32_t w4[4] = {(uint32_t)vr[t].x, (uint32_t)vr[t].y, (uint32_t)vr[t].z, (uint32_t)vr[t].w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                vf[t][2 * i] = h2f((uint16_t)(w4[i] & 0xffffu));
-                vf[t][2 * i + 1] = h2f((uint16_t)(w4[i] >> 16));
             }
         }
 #pragma unroll
@@ -157,19 +166,30 @@ __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, c
 #pragma unroll
             for (int t = 1; t < kT; t++) mt = fmaxf(mt, s[h][t]);
             const float mn = fmaxf(m[h], mt);
-            if (mn == -INFINITY) continue;  // nothing unmasked yet (uniform in the lane group)
-            const float alpha = expf(m[h] - mn);
+            // nothing unmasked yet (uniform in the lane group): keep the empty state
+            const float alpha = mn == -INFINITY ? 1.0f : fexp2(m[h] - mn);
             l[h] *= alpha;
 #pragma unroll
             for (int i = 0; i < 8; i++) o[h][i] *= alpha;
 #pragma unroll
-            for (int t = 0; t < kT; t++) {
-                const float p = expf(s[h][t] - mn);
-                l[h] += p;
-#pragma unroll
-                for (int i = 0; i < 8; i++) o[h][i] = fmaf(p, vf[t][i], o[h][i]);
-            }
+            for (int t = 0; t < kT; t++) s[h][t] = mn == -INFINITY ? 0.0f : fexp2(s[h][t] - mn);
             m[h] = mn;
+        }
+#pragma unroll
+        for (int t = 0; t < kT; t++) {
+            const uint32_t w4[4] = {(uint32_t)vr[t].x, (uint32_t)vr[t].y, (uint32_t)vr[t].z, (uint32_t)vr[t].w};
+            float vf[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                vf[2 * i] = h2f((uint16_t)(w4[i] & 0xffffu));
+                vf[2 * i + 1] = h2f((uint16_t)(w4[i] >> 16));
+            }
+#pragma unroll
+            for (int h = 0; h < GQ; h++) {
+                l[h] += s[h][t];
+#pragma unroll
+                for (int i = 0; i < 8; i++) o[h][i] = fmaf(s[h][t], vf[i], o[h][i]);
+            }
         }
     }
 
@@ -204,7 +224,7 @@ __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, c
         if (M != -INFINITY) {
 #pragma unroll
             for (int w = 0; w < kNW; w++) {
-                const float e = expf(s_m[w][h] - M);
+                const float e = fexp2(s_m[w][h] - M);
                 L += s_l[w][h] * e;
                 acc += s_o[w][h][dd] * e;
             }
@@ -221,54 +241,170 @@ __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, c
             }
         }
     }
+    if (n_splits == 1 || counters == nullptr) return;
+
+    // Fused combine: the last workgroup of this kv head to finish merges all splits.
+    // Release the partials device-wide, count arrivals, and acquire before reading.
+    __shared__ int s_last;
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(&counters[kvh], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == (unsigned)(n_splits - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // every (head, split) m and l in one round of loads, then the weights
+    __shared__ float s_cm[GQ][kFusedMaxSplits];
+    __shared__ float s_cl[GQ][kFusedMaxSplits];
+    if (tid < GQ * n_splits) {
+        const int h = tid / n_splits, sp = tid % n_splits;
+        const float *rec = part + ((size_t)(kvh * GQ + h) * n_splits + sp) * PS;
+        s_cm[h][sp] = rec[D];
+        s_cl[h][sp] = rec[D + 1];
+    }
+    __syncthreads();
+    // all o loads of this thread's outputs issued together (clamped, branch-free)
+    constexpr int OPT = (GQ * D + 255) / 256;
+    float ov[OPT][kFusedMaxSplits];
+#pragma unroll
+    for (int oi = 0; oi < OPT; oi++) {
+        const int idx = min(tid + oi * 256, GQ * D - 1);
+        const float *ph = part + (size_t)(kvh * GQ + idx / D) * n_splits * PS + idx % D;
+#pragma unroll
+        for (int sp = 0; sp < kFusedMaxSplits; sp++) ov[oi][sp] = ph[(size_t)min(sp, n_splits - 1) * PS];
+    }
+#pragma unroll
+    for (int oi = 0; oi < OPT; oi++) {
+        const int idx = tid + oi * 256;
+        if (idx >= GQ * D) break;
+        const int h = idx / D;
+        float M = -INFINITY;
+        for (int sp = 0; sp < n_splits; sp++) M = fmaxf(M, s_cm[h][sp]);
+        float L = 0.0f, acc = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int sp = 0; sp < kFusedMaxSplits; sp++) {
+                const float ms = sp < n_splits ? s_cm[h][sp] : -INFINITY;
+                const float e = ms == -INFINITY ? 0.0f : fexp2(ms - M);
+                L += (sp < n_splits ? s_cl[h][sp] : 0.0f) * e;
+                acc += ov[oi][sp] * e;
+            }
+        }
+        out[(size_t)(kvh * GQ + h) * D + idx % D] = L == 0.0f ? 0.0f : acc / L;
+    }
+    if (tid == 0) __hip_atomic_store(&counters[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Parallel log-sum-exp combine for many splits: grid (q head, D/32 dim slices),
+// 256 threads = 32 dims x 8 split groups; split weights exp(m_s - M) in LDS.
 template <int D>
-__global__ __launch_bounds__(D) void k_fa_combine(const float *__restrict__ part, float *__restrict__ out,
-                                                  int n_splits) {
+__global__ __launch_bounds__(256) void k_fa_combine(const float *__restrict__ part, float *__restrict__ out,
+                                                    int n_splits) {
     constexpr int PS = part_stride<D>();
+    __shared__ float s_w[kMaxSplits];
+    __shared__ float s_red[8][32];
+    __shared__ float s_wave[4];
     const int h = blockIdx.x;
-    const int dd = threadIdx.x;
+    const int d0 = blockIdx.y * 32;
+    const int tid = threadIdx.x;
+    const int lane = tid % 64, wave = tid / 64;
     const float *ph = part + (size_t)h * n_splits * PS;
-    float M = -INFINITY;
-    for (int s = 0; s < n_splits; s++) M = fmaxf(M, ph[(size_t)s * PS + D]);
-    float L = 0.0f, acc = 0.0f;
-    if (M != -INFINITY) {
-        for (int s = 0; s < n_splits; s++) {
-            const float ms = ph[(size_t)s * PS + D];
-            if (ms == -INFINITY) continue;
-            const float e = expf(ms - M);
-            L += ph[(size_t)s * PS + D + 1] * e;
-            acc += ph[(size_t)s * PS + dd] * e;
+
+    float mx = -INFINITY;
+    for (int sp = tid; sp < n_splits; sp += 256) mx = fmaxf(mx, ph[(size_t)sp * PS + D]);
+    mx = group_max<64>(mx);
+    if (lane == 0) s_wave[wave] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(s_wave[0], s_wave[1]), fmaxf(s_wave[2], s_wave[3]));
+    __syncthreads();
+    float ls = 0.0f;
+    for (int sp = tid; sp < n_splits; sp += 256) {
+        const float ms = ph[(size_t)sp * PS + D];
+        const float w = (ms == -INFINITY || M == -INFINITY) ? 0.0f : fexp2(ms - M);
+        s_w[sp] = w;
+        ls += ph[(size_t)sp * PS + D + 1] * w;
+    }
+    ls = group_sum<64>(ls);
+    if (lane == 0) s_wave[wave] = ls;
+    __syncthreads();
+    const float L = s_wave[0] + s_wave[1] + s_wave[2] + s_wave[3];
+
+    const int dd = tid % 32, sg = tid / 32;
+    float a0 = 0.0f, a1 = 0.0f;
+    for (int base = 0; base < n_splits; base += 64) {
+        float ov[8], wv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {  // clamped, branch-free: all 8 loads in flight
+            const int sp = base + sg + 8 * u;
+            ov[u] = ph[(size_t)min(sp, n_splits - 1) * PS + d0 + dd];
+            wv[u] = sp < n_splits ? s_w[min(sp, n_splits - 1)] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u += 2) {
+            a0 = fmaf(ov[u], wv[u], a0);
+            a1 = fmaf(ov[u + 1], wv[u + 1], a1);
         }
     }
-    out[(size_t)h * D + dd] = L == 0.0f ? 0.0f : acc / L;
+    s_red[sg][dd] = a0 + a1;
+    __syncthreads();
+    if (tid < 32) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 8; g++) acc += s_red[g][tid];
+        out[(size_t)h * D + d0 + tid] = L == 0.0f ? 0.0f : acc / L;
+    }
 }
 
-template <int D, int GQ>
-int launch_split(hipStream_t st, const float *q, const void *k, const void *v, const uint16_t *mask,
-                 const int32_t *kv_len, int64_t n_kv, int64_t n_kv_heads, size_t k_nb1, size_t k_nb2, size_t v_nb1,
-                 size_t v_nb2, float scale, float *out, float *part, const FaPlan &p) {
-    hipLaunchKernelGGL((k_fa_split<D, GQ>), dim3((unsigned)p.n_splits, (unsigned)n_kv_heads), dim3(256), 0, st, q,
-                       (const uint8_t *)k, (const uint8_t *)v, mask, kv_len, (int)n_kv, k_nb1, k_nb2, v_nb1, v_nb2,
-                       scale, p.chunk, p.n_splits, part, out);
+// The last-workgroup combine needs an agent-scope release/acquire (an L2
+// write-back and invalidate on this cache hierarchy) in every workgroup, so it
+// is opt-in (MI_FA_FUSED_COMBINE=1); by default a second, parallel kernel combines.
+inline bool fused_combine_enabled() {
+    static const bool on = [] {
+        const char *e = getenv("MI_FA_FUSED_COMBINE");
+        return e && e[0] == '1';
+    }();
+    return on;
+}
+
+template <int D, int GQ, bool MASK>
+int launch_split_m(hipStream_t st, const float *q, const void *k, const void *v, const uint16_t *mask,
+                   const int32_t *kv_len, int64_t n_kv, int64_t n_kv_heads, size_t k_nb1, size_t k_nb2,
+                   size_t v_nb1, size_t v_nb2, float scale, float *out, float *part, unsigned *counters,
+                   const FaPlan &p) {
+    const bool fused = p.n_splits <= kFusedMaxSplits && fused_combine_enabled();
+    hipLaunchKernelGGL((k_fa_split<D, GQ, MASK>), dim3((unsigned)p.n_splits, (unsigned)n_kv_heads), dim3(256), 0, st,
+                       q, (const uint8_t *)k, (const uint8_t *)v, mask, kv_len, (int)n_kv, k_nb1, k_nb2, v_nb1, v_nb2,
+                       scale, p.chunk, p.n_splits, part, out, fused ? counters : nullptr);
     MI_CHECK_LAUNCH("k_fa_split");
-    if (p.n_splits > 1) {
-        hipLaunchKernelGGL((k_fa_combine<D>), dim3((unsigned)(n_kv_heads * GQ)), dim3(D), 0, st, part, out,
+    if (p.n_splits > 1 && !fused) {
+        hipLaunchKernelGGL((k_fa_combine<D>), dim3((unsigned)(n_kv_heads * GQ), D / 32), dim3(256), 0, st, part, out,
                            p.n_splits);
         MI_CHECK_LAUNCH("k_fa_combine");
     }
     return MI_OK;
 }
 
+template <int D, int GQ>
+int launch_split(hipStream_t st, const float *q, const void *k, const void *v, const uint16_t *mask,
+                 const int32_t *kv_len, int64_t n_kv, int64_t n_kv_heads, size_t k_nb1, size_t k_nb2, size_t v_nb1,
+                 size_t v_nb2, float scale, float *out, float *part, unsigned *counters, const FaPlan &p) {
+    if (mask)
+        return launch_split_m<D, GQ, true>(st, q, k, v, mask, kv_len, n_kv, n_kv_heads, k_nb1, k_nb2, v_nb1, v_nb2,
+                                           scale, out, part, counters, p);
+    return launch_split_m<D, GQ, false>(st, q, k, v, mask, kv_len, n_kv, n_kv_heads, k_nb1, k_nb2, v_nb1, v_nb2,
+                                        scale, out, part, counters, p);
+}
+
 template <int D>
 int launch_d(hipStream_t st, int gq, const float *q, const void *k, const void *v, const uint16_t *mask,
              const int32_t *kv_len, int64_t n_kv, int64_t n_kv_heads, size_t k_nb1, size_t k_nb2, size_t v_nb1,
-             size_t v_nb2, float scale, float *out, float *part, const FaPlan &p) {
+             size_t v_nb2, float scale, float *out, float *part, unsigned *counters, const FaPlan &p) {
 #define MI_FA_CASE(G)                                                                                          \
     case G:                                                                                                    \
         return launch_split<D, G>(st, q, k, v, mask, kv_len, n_kv, n_kv_heads, k_nb1, k_nb2, v_nb1, v_nb2, scale, \
-                                  out, part, p);
+                                  out, part, counters, p);
     switch (gq) {
         MI_FA_CASE(1)
         MI_FA_CASE(2)
@@ -312,7 +448,7 @@ extern "C" {
 size_t mi_fa_decode_workspace_size(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d) {
     if (n_kv <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || d <= 0) return 0;
     const FaPlan p = fa_plan(n_kv, n_kv_heads);
-    return (size_t)n_q_heads * p.n_splits * (d + 4) * sizeof(float);
+    return fa_part_bytes(n_q_heads, p.n_splits, d) + mi::align_up((size_t)n_kv_heads * sizeof(unsigned), 256);
 }
 
 int mi_fa_decode(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
@@ -329,17 +465,19 @@ int mi_fa_decode(void *stream, const float *q, const void *k, const void *v, con
                  "fa_decode: K/V base and strides must be 16-byte aligned");
     const FaPlan p = fa_plan(n_kv, n_kv_heads);
     const size_t need = mi_fa_decode_workspace_size(n_kv, n_q_heads, n_kv_heads, d);
-    if (p.n_splits > 1 && (!ws || ws_bytes < need)) {
-        mi::set_error("fa_decode: workspace %zu < %zu bytes", ws_bytes, need);
+    if (p.n_splits > 1 && (!ws || ws_bytes < need || !mi::aligned(ws, 256))) {
+        mi::set_error("fa_decode: workspace %zu < %zu bytes (or not 256-byte aligned)", ws_bytes, need);
         return MI_ERR_WORKSPACE;
     }
     const int gq = (int)(n_q_heads / n_kv_heads);
     hipStream_t st = (hipStream_t)stream;
+    float *part = (float *)ws;
+    unsigned *counters = ws ? (unsigned *)((uint8_t *)ws + fa_part_bytes(n_q_heads, p.n_splits, d)) : nullptr;
     if (d == 128)
         return launch_d<128>(st, gq, q, k, v, mask, kv_len, n_kv, n_kv_heads, k_nb1, k_nb2, v_nb1, v_nb2, scale, out,
-                             (float *)ws, p);
+                             part, counters, p);
     return launch_d<64>(st, gq, q, k, v, mask, kv_len, n_kv, n_kv_heads, k_nb1, k_nb2, v_nb1, v_nb2, scale, out,
-                        (float *)ws, p);
+                        part, counters, p);
 }
 
 int mi_kv_lengths(void *stream, const void *mask, int mask_is_f16, int64_t n_kv, int64_t n_rows, int32_t *out) {

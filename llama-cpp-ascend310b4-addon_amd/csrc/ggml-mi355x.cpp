@@ -1,0 +1,957 @@
+// ggml-mi355x.cpp -- the MI355X ggml backend: registry, device, buffer type,
+// buffers with weight prepack at upload, and graph_compute dispatching the
+// decode hot path to the gfx950 kernels through their C ABI.
+//
+// Reference behaviour mirrored (patch = patches/ascend310b4-llama-cpp.patch):
+//   get_alloc_size   pad to 256 B + planar side copy for Q8_0/Q4_0 matmul weights
+//                    (cf. ggml_cann_310b_a8w8_size / _nz_size, patch:1535-1562, 1810-1847)
+//   set_tensor       ND bytes at tensor->data, side copy built when the tensor is
+//                    complete; chunked and concurrent uploads through a per-tensor
+//                    tracker under a mutex (patch:1647-1653, 1700-1809)
+//   supports_op      MUL_MAT with M <= 8, FLASH_ATTN_EXT with one query row
+//                    (cf. patch:1925-1983), everything else false -> CPU fallback
+//   graph_compute    per-node dispatch on one stream (patch:1884-1922); runtime
+//                    errors abort like ACL_CHECK; GGML_MI355X_TRACE_NODE_SYNC=1
+//                    synchronizes and logs after every node (patch:1887-1921)
+// MI355X-specific: consecutive MUL_MATs sharing their activation run as one
+// grouped GEMV launch, RMS_NORM+MUL fuse, and a graph whose nodes did not change
+// since the last call is replayed as a captured HIP graph.
+#include "ggml-mi355x.h"
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "ggml-backend-impl.h"
+#include "ggml_mi355x_kernels.h"
+
+#define MI_HIP_CHECK(expr)                                                                                 \
+    do {                                                                                                   \
+        hipError_t e_ = (expr);                                                                            \
+        if (e_ != hipSuccess) GGML_ABORT("MI355X: %s failed: %s", #expr, hipGetErrorString(e_));          \
+    } while (0)
+
+#define MI_K_CHECK(expr)                                                                                   \
+    do {                                                                                                   \
+        int r_ = (expr);                                                                                   \
+        if (r_ != MI_OK) GGML_ABORT("MI355X: %s failed (%d): %s", #expr, r_, mi_last_error());            \
+    } while (0)
+
+namespace {
+
+// ------------------------------------------------------------------ env flags (read once)
+
+bool env_flag(const char *name, bool def) {
+    const char *v = getenv(name);
+    if (!v || !*v) return def;
+    std::string s(v);
+    for (auto &c : s) c = (char)tolower(c);
+    return !(s == "0" || s == "off" || s == "false" || s == "no" || s == "disable");
+}
+
+bool prepack_enabled() {
+    static const bool on = env_flag("GGML_MI355X_PREPACK", true);
+    return on;
+}
+bool graphs_enabled() {
+    static const bool on = env_flag("GGML_MI355X_GRAPHS", true) && !env_flag("GGML_MI355X_TRACE_NODE_SYNC", false);
+    return on;
+}
+bool trace_node_sync() {
+    static const bool on = env_flag("GGML_MI355X_TRACE_NODE_SYNC", false);
+    return on;
+}
+bool fusion_enabled() {
+    static const bool on = env_flag("GGML_MI355X_FUSION", true);
+    return on;
+}
+int q8_rounding() {
+    static const int r = [] {
+        const char *v = getenv("GGML_MI355X_Q8_ROUNDING");
+        return (v && strcmp(v, "ref") == 0) ? MI_Q8_ROUND_REF : MI_Q8_ROUND_X86;
+    }();
+    return r;
+}
+
+// ------------------------------------------------------------------ weights
+
+// Same weight classes as the CANN backend's is_matmul_weight (aclnn_ops.h): the
+// projection and output matrices of a transformer.
+bool is_matmul_weight(const ggml_tensor *t) {
+    static const char *suffixes[] = {"output.weight",   "attn_q.weight",   "attn_k.weight", "attn_v.weight",
+                                     "attn_output.weight", "ffn_gate.weight", "ffn_up.weight", "ffn_down.weight"};
+    const size_t ln = strlen(t->name);
+    for (const char *s : suffixes) {
+        const size_t ls = strlen(s);
+        if (ln >= ls && strcmp(t->name + ln - ls, s) == 0) return true;
+    }
+    return false;
+}
+
+bool prepack_eligible(const ggml_tensor *t) {
+    return prepack_enabled() && (t->type == GGML_TYPE_Q8_0 || t->type == GGML_TYPE_Q4_0) && t->ne[2] == 1 &&
+           t->ne[3] == 1 && t->view_src == nullptr && t->ne[0] % 32 == 0 && is_matmul_weight(t);
+}
+
+size_t side_offset(const ggml_tensor *t) { return GGML_PAD(ggml_nbytes(t), 256); }
+
+size_t packed_size(const ggml_tensor *t) {
+    return t->type == GGML_TYPE_Q8_0 ? mi_q8_0_packed_size(t->ne[1], t->ne[0]) : mi_q4_0_packed_size(t->ne[1], t->ne[0]);
+}
+
+struct TensorExtra {
+    void *packed = nullptr;  // planar side copy (device)
+    bool ready = false;      // side copy built
+    const float *inv_s = nullptr;  // SmoothQuant reciprocal factors (device), owned by the buffer
+};
+
+struct SetTracker {
+    std::mutex mtx;
+    size_t bytes_written = 0;
+    size_t total_bytes = 0;
+};
+
+// ------------------------------------------------------------------ device / buffer type
+
+struct DeviceCtx {
+    int device = 0;
+    std::string name;
+    std::string description;
+    ggml_backend_buffer_type buft;
+    std::string buft_name;
+};
+
+struct BufferCtx {
+    int device = 0;
+    void *dev_ptr = nullptr;
+    size_t size = 0;
+    hipStream_t stream = nullptr;  // upload / prepack stream of this buffer
+    std::mutex mtx;
+    std::unordered_map<const ggml_tensor *, std::unique_ptr<SetTracker>> trackers;
+    std::vector<std::unique_ptr<TensorExtra>> extras;
+    std::vector<void *> owned;  // SmoothQuant factor copies
+    std::unordered_map<std::string, void *> inv_s_by_content;
+};
+
+struct BackendCtx {
+    int device = 0;
+    std::string name;
+    hipStream_t stream = nullptr;
+    void *scratch = nullptr;
+    size_t scratch_size = 0;
+    void *fa_ws = nullptr;
+    size_t fa_ws_size = 0;
+    // captured replay of the last graph
+    hipGraphExec_t gexec = nullptr;
+    std::vector<uint64_t> signature;
+    int same_calls = 0;
+};
+
+void set_device(int dev) { MI_HIP_CHECK(hipSetDevice(dev)); }
+
+// ---- buffer iface
+
+void buffer_free(ggml_backend_buffer_t buffer) {
+    BufferCtx *ctx = (BufferCtx *)buffer->context;
+    set_device(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(ctx->dev_ptr);
+    for (void *p : ctx->owned) (void)hipFree(p);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+void *buffer_get_base(ggml_backend_buffer_t buffer) { return ((BufferCtx *)buffer->context)->dev_ptr; }
+
+enum ggml_status buffer_init_tensor(ggml_backend_buffer_t buffer, ggml_tensor *tensor) {
+    BufferCtx *ctx = (BufferCtx *)buffer->context;
+    if (tensor->view_src != nullptr) return GGML_STATUS_SUCCESS;
+    if (prepack_eligible(tensor)) {
+        std::lock_guard<std::mutex> lk(ctx->mtx);
+        auto ex = std::make_unique<TensorExtra>();
+        ex->packed = (char *)tensor->data + side_offset(tensor);
+        tensor->extra = ex.get();
+        ctx->extras.push_back(std::move(ex));
+    }
+    return GGML_STATUS_SUCCESS;
+}
+
+void build_side_copy(BufferCtx *ctx, ggml_tensor *tensor) {
+    TensorExtra *ex = (TensorExtra *)tensor->extra;
+    if (tensor->type == GGML_TYPE_Q8_0)
+        MI_K_CHECK(mi_prepack_q8_0(ctx->stream, tensor->data, ex->packed, tensor->ne[1], tensor->ne[0]));
+    else
+        MI_K_CHECK(mi_prepack_q4_0(ctx->stream, tensor->data, ex->packed, tensor->ne[1], tensor->ne[0]));
+    MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    ex->ready = true;
+}
+
+void buffer_set_tensor(ggml_backend_buffer_t buffer, ggml_tensor *tensor, const void *data, size_t offset,
+                       size_t size) {
+    BufferCtx *ctx = (BufferCtx *)buffer->context;
+    set_device(ctx->device);
+    MI_HIP_CHECK(hipMemcpyAsync((char *)tensor->data + offset, data, size, hipMemcpyHostToDevice, ctx->stream));
+    MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    if (!tensor->extra || tensor->view_src) return;
+
+    const size_t total = ggml_nbytes(tensor);
+    if (offset == 0 && size == total) {  // whole-tensor write
+        build_side_copy(ctx, tensor);
+        return;
+    }
+    // chunked write: count bytes per tensor, build the side copy once complete
+    SetTracker *tr;
+    {
+        std::lock_guard<std::mutex> lk(ctx->mtx);
+        auto &slot = ctx->trackers[tensor];
+        if (!slot) {
+            slot = std::make_unique<SetTracker>();
+            slot->total_bytes = total;
+        }
+        tr = slot.get();
+    }
+    bool complete;
+    {
+        std::lock_guard<std::mutex> lk(tr->mtx);
+        tr->bytes_written += size;
+        complete = tr->bytes_written >= tr->total_bytes;
+        if (complete) tr->bytes_written = 0;
+    }
+    if (complete) {
+        build_side_copy(ctx, tensor);
+        std::lock_guard<std::mutex> lk(ctx->mtx);
+        ctx->trackers.erase(tensor);
+    }
+}
+
+void buffer_get_tensor(ggml_backend_buffer_t buffer, const ggml_tensor *tensor, void *data, size_t offset,
+                       size_t size) {
+    BufferCtx *ctx = (BufferCtx *)buffer->context;
+    set_device(ctx->device);
+    MI_HIP_CHECK(hipMemcpyAsync(data, (const char *)tensor->data + offset, size, hipMemcpyDeviceToHost, ctx->stream));
+    MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+}
+
+void buffer_memset_tensor(ggml_backend_buffer_t buffer, ggml_tensor *tensor, uint8_t value, size_t offset,
+                          size_t size) {
+    BufferCtx *ctx = (BufferCtx *)buffer->context;
+    set_device(ctx->device);
+    MI_HIP_CHECK(hipMemsetAsync((char *)tensor->data + offset, value, size, ctx->stream));
+    MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+}
+
+bool buffer_cpy_tensor(ggml_backend_buffer_t buffer, const ggml_tensor *src, ggml_tensor *dst) {
+    if (!src->buffer || src->buffer->iface.get_base != buffer_get_base) return false;
+    BufferCtx *ctx = (BufferCtx *)buffer->context;
+    set_device(ctx->device);
+    MI_HIP_CHECK(hipMemcpyAsync(dst->data, src->data, ggml_nbytes(src), hipMemcpyDeviceToDevice, ctx->stream));
+    MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    if (dst->extra) build_side_copy(ctx, dst);
+    return true;
+}
+
+void buffer_clear(ggml_backend_buffer_t buffer, uint8_t value) {
+    BufferCtx *ctx = (BufferCtx *)buffer->context;
+    set_device(ctx->device);
+    MI_HIP_CHECK(hipMemsetAsync(ctx->dev_ptr, value, ctx->size, ctx->stream));
+    MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+}
+
+const ggml_backend_buffer_i kBufferIface = {
+    /* free_buffer   */ buffer_free,
+    /* get_base      */ buffer_get_base,
+    /* init_tensor   */ buffer_init_tensor,
+    /* memset_tensor */ buffer_memset_tensor,
+    /* set_tensor    */ buffer_set_tensor,
+    /* get_tensor    */ buffer_get_tensor,
+    /* cpy_tensor    */ buffer_cpy_tensor,
+    /* clear         */ buffer_clear,
+    /* reset         */ nullptr,
+};
+
+// ---- buffer type iface
+
+const char *buft_get_name(ggml_backend_buffer_type_t buft) {
+    return ((DeviceCtx *)buft->context)->buft_name.c_str();
+}
+
+ggml_backend_buffer_t buft_alloc_buffer(ggml_backend_buffer_type_t buft, size_t size) {
+    DeviceCtx *dctx = (DeviceCtx *)buft->context;
+    set_device(dctx->device);
+    BufferCtx *ctx = new BufferCtx();
+    ctx->device = dctx->device;
+    ctx->size = size;
+    if (hipMalloc(&ctx->dev_ptr, size ? size : 256) != hipSuccess) {
+        fprintf(stderr, "MI355X: hipMalloc of %zu bytes failed\n", size);
+        delete ctx;
+        return nullptr;
+    }
+    MI_HIP_CHECK(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+    return ggml_backend_buffer_init(buft, kBufferIface, ctx, size);
+}
+
+size_t buft_get_alignment(ggml_backend_buffer_type_t) { return 256; }
+size_t buft_get_max_size(ggml_backend_buffer_type_t) { return SIZE_MAX; }
+
+size_t buft_get_alloc_size(ggml_backend_buffer_type_t, const ggml_tensor *tensor) {
+    if (prepack_eligible(tensor)) return side_offset(tensor) + packed_size(tensor);
+    return ggml_nbytes(tensor);
+}
+
+bool buft_is_host(ggml_backend_buffer_type_t) { return false; }
+
+const ggml_backend_buffer_type_i kBuftIface = {
+    /* get_name       */ buft_get_name,
+    /* alloc_buffer   */ buft_alloc_buffer,
+    /* get_alignment  */ buft_get_alignment,
+    /* get_max_size   */ buft_get_max_size,
+    /* get_alloc_size */ buft_get_alloc_size,
+    /* is_host        */ buft_is_host,
+};
+
+// ------------------------------------------------------------------ supports_op
+
+bool is_f32_contig(const ggml_tensor *t) { return t && t->type == GGML_TYPE_F32 && ggml_is_contiguous(t); }
+
+bool supports_mul_mat(const ggml_tensor *op) {
+    const ggml_tensor *a = op->src[0], *b = op->src[1];
+    if (!is_f32_contig(b) || !is_f32_contig(op)) return false;
+    if (b->ne[1] < 1 || b->ne[1] > 8 || b->ne[2] != 1 || b->ne[3] != 1) return false;
+    if (a->ne[2] != 1 || a->ne[3] != 1) return false;
+    switch (a->type) {
+        case GGML_TYPE_Q8_0:
+        case GGML_TYPE_Q4_0:
+            // the planar side copy exists only for weights of this backend's buffers
+            return a->extra != nullptr && a->buffer && a->buffer->buft->iface.get_alloc_size == buft_get_alloc_size &&
+                   b->ne[0] * b->ne[1] * 2 <= 64 * 1024;
+        case GGML_TYPE_F16:
+            return a->nb[0] == 2 && a->nb[1] % 16 == 0 && a->ne[0] % 8 == 0 && b->ne[0] * b->ne[1] * 2 <= 64 * 1024;
+        default:
+            return false;
+    }
+}
+
+bool supports_fa(const ggml_tensor *op) {
+    const ggml_tensor *q = op->src[0], *k = op->src[1], *v = op->src[2], *mask = op->src[3];
+    const ggml_tensor *sinks = op->src[4], *kvl = op->src[5];
+    float max_bias, softcap;
+    memcpy(&max_bias, (const float *)op->op_params + 1, sizeof(float));
+    memcpy(&softcap, (const float *)op->op_params + 2, sizeof(float));
+    if (max_bias != 0.0f || softcap != 0.0f || sinks) return false;
+    if (!q || q->type != GGML_TYPE_F32 || op->type != GGML_TYPE_F32 || !ggml_is_contiguous(op)) return false;
+    if (q->ne[1] != 1 || q->ne[3] != 1 || q->nb[0] != 4 || (q->ne[2] > 1 && q->nb[2] != (size_t)q->ne[0] * 4))
+        return false;
+    if (k->type != GGML_TYPE_F16 || v->type != GGML_TYPE_F16) return false;
+    const int64_t d = q->ne[0];
+    if ((d != 64 && d != 128) || k->ne[0] != d || v->ne[0] != d) return false;
+    if (k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2] || k->ne[3] != 1 || v->ne[3] != 1) return false;
+    if (k->ne[2] < 1 || q->ne[2] % k->ne[2] != 0 || q->ne[2] / k->ne[2] > 8) return false;
+    if (k->nb[0] != 2 || v->nb[0] != 2 || k->nb[1] % 16 || k->nb[2] % 16 || v->nb[1] % 16 || v->nb[2] % 16) return false;
+    if (mask && (mask->type != GGML_TYPE_F16 || mask->ne[0] < k->ne[1] || mask->nb[0] != 2)) return false;
+    if (kvl && (kvl->type != GGML_TYPE_I32 || !ggml_is_contiguous(kvl) || ggml_nelements(kvl) < 1)) return false;
+    return true;
+}
+
+bool supports_op_impl(const ggml_tensor *op) {
+    switch (op->op) {
+        case GGML_OP_NONE:
+        case GGML_OP_RESHAPE:
+        case GGML_OP_VIEW:
+        case GGML_OP_PERMUTE:
+        case GGML_OP_TRANSPOSE:
+            return true;
+        case GGML_OP_MUL_MAT:
+            return supports_mul_mat(op);
+        case GGML_OP_FLASH_ATTN_EXT:
+            return supports_fa(op);
+        case GGML_OP_RMS_NORM:
+            return is_f32_contig(op->src[0]) && is_f32_contig(op);
+        case GGML_OP_ADD:
+        case GGML_OP_MUL: {
+            const ggml_tensor *a = op->src[0], *b = op->src[1];
+            if (!is_f32_contig(a) || !is_f32_contig(b) || !is_f32_contig(op)) return false;
+            return b->ne[0] == a->ne[0] && (ggml_nelements(b) == b->ne[0] || ggml_are_same_shape(a, b));
+        }
+        case GGML_OP_ROPE: {
+            const int mode = op->op_params[2];
+            float ext_factor;
+            memcpy(&ext_factor, (const float *)op->op_params + 7, sizeof(float));
+            return mode == GGML_ROPE_TYPE_NEOX && ext_factor == 0.0f && op->src[0]->type == GGML_TYPE_F32 &&
+                   op->src[0]->nb[0] == 4 && op->src[2] == nullptr && op->src[1]->type == GGML_TYPE_I32 &&
+                   is_f32_contig(op) && op->op_params[1] <= op->src[0]->ne[0];
+        }
+        case GGML_OP_SET_ROWS:
+            return op->type == GGML_TYPE_F16 && op->nb[0] == 2 && op->src[0]->type == GGML_TYPE_F32 &&
+                   op->src[0]->nb[0] == 4 && (op->src[1]->type == GGML_TYPE_I64 || op->src[1]->type == GGML_TYPE_I32) &&
+                   op->src[0]->ne[2] == 1 && op->src[0]->ne[3] == 1;
+        case GGML_OP_GET_ROWS:
+            return (op->src[0]->type == GGML_TYPE_F16 || op->src[0]->type == GGML_TYPE_F32) &&
+                   op->src[0]->nb[0] == ggml_type_size(op->src[0]->type) && op->src[1]->type == GGML_TYPE_I32 &&
+                   ggml_is_contiguous(op->src[1]) && op->src[1]->ne[1] == 1 && is_f32_contig(op);
+        case GGML_OP_GLU:
+            return ggml_get_glu_op(op) == GGML_GLU_OP_SWIGLU && op->op_params[1] == 0 && is_f32_contig(op->src[0]) &&
+                   is_f32_contig(op->src[1]) && is_f32_contig(op);
+        case GGML_OP_ARGMAX:
+            return is_f32_contig(op->src[0]) && op->type == GGML_TYPE_I32;
+        default:
+            return false;
+    }
+}
+
+// ------------------------------------------------------------------ graph compute
+
+bool is_noop(const ggml_tensor *t) {
+    return t->op == GGML_OP_NONE || t->op == GGML_OP_RESHAPE || t->op == GGML_OP_VIEW || t->op == GGML_OP_PERMUTE ||
+           t->op == GGML_OP_TRANSPOSE || ggml_is_empty(t);
+}
+
+const float *inv_s_of(const ggml_tensor *w) {
+    const TensorExtra *ex = (const TensorExtra *)w->extra;
+    return ex ? ex->inv_s : nullptr;
+}
+
+size_t fa_ws_need(const ggml_tensor *node) {
+    const ggml_tensor *q = node->src[0], *k = node->src[1];
+    return mi_fa_decode_workspace_size(k->ne[1], q->ne[2], k->ne[2], q->ne[0]);
+}
+
+size_t scratch_need(const ggml_tensor *node) {
+    if (node->op == GGML_OP_MUL_MAT && node->src[0]->type == GGML_TYPE_Q8_0)
+        return mi_mul_mat_q8_0_workspace_size(node->src[1]->ne[1], node->src[1]->ne[0]);
+    return 0;
+}
+
+void ensure_buffers(BackendCtx *ctx, ggml_cgraph *g) {
+    size_t need_s = 0, need_fa = 0;
+    for (int i = 0; i < ggml_graph_n_nodes(g); i++) {
+        ggml_tensor *n = ggml_graph_node(g, i);
+        if (n->op == GGML_OP_FLASH_ATTN_EXT) need_fa = std::max(need_fa, fa_ws_need(n));
+        need_s = std::max(need_s, scratch_need(n));
+    }
+    if (need_s > ctx->scratch_size) {
+        if (ctx->scratch) MI_HIP_CHECK(hipFree(ctx->scratch));
+        ctx->scratch_size = GGML_PAD(need_s, 1 << 20);
+        MI_HIP_CHECK(hipMalloc(&ctx->scratch, ctx->scratch_size));
+        ctx->signature.clear();
+    }
+    if (need_fa > ctx->fa_ws_size) {
+        if (ctx->fa_ws) MI_HIP_CHECK(hipFree(ctx->fa_ws));
+        ctx->fa_ws_size = GGML_PAD(need_fa, 1 << 20);
+        MI_HIP_CHECK(hipMalloc(&ctx->fa_ws, ctx->fa_ws_size));
+        // the workspace's arrival counters must start at zero (kernels leave them zeroed)
+        MI_HIP_CHECK(hipMemsetAsync(ctx->fa_ws, 0, ctx->fa_ws_size, ctx->stream));
+        MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+        ctx->signature.clear();
+    }
+}
+
+void run_mul_mat_q8_group(BackendCtx *ctx, ggml_tensor **nodes, int count) {
+    const ggml_tensor *b = nodes[0]->src[1];
+    const void *w[4];
+    int64_t n[4];
+    float *y[4];
+    for (int i = 0; i < count; i++) {
+        const TensorExtra *ex = (const TensorExtra *)nodes[i]->src[0]->extra;
+        w[i] = ex->packed;
+        n[i] = nodes[i]->src[0]->ne[1];
+        y[i] = (float *)nodes[i]->data;
+    }
+    MI_K_CHECK(mi_mul_mat_q8_0_f32_multi(ctx->stream, count, w, n, y, b->ne[0], (const float *)b->data,
+                                         inv_s_of(nodes[0]->src[0]), q8_rounding(), ctx->scratch,
+                                         ctx->scratch_size));
+}
+
+void run_mul_mat(BackendCtx *ctx, ggml_tensor *node) {
+    const ggml_tensor *a = node->src[0], *b = node->src[1];
+    const int64_t n = a->ne[1], k = a->ne[0], m = b->ne[1];
+    switch (a->type) {
+        case GGML_TYPE_Q8_0: {
+            const TensorExtra *ex = (const TensorExtra *)a->extra;
+            GGML_ASSERT(ex && ex->ready && "Q8_0 weight used before its upload completed");
+            MI_K_CHECK(mi_mul_mat_q8_0_f32(ctx->stream, ex->packed, (const float *)b->data, ex->inv_s,
+                                           (float *)node->data, n, k, m, q8_rounding(), ctx->scratch,
+                                           ctx->scratch_size));
+            break;
+        }
+        case GGML_TYPE_Q4_0: {
+            const TensorExtra *ex = (const TensorExtra *)a->extra;
+            GGML_ASSERT(ex && ex->ready && "Q4_0 weight used before its upload completed");
+            MI_K_CHECK(mi_mul_mat_q4_0_f32(ctx->stream, ex->packed, (const float *)b->data, (float *)node->data, n,
+                                           k, m));
+            break;
+        }
+        case GGML_TYPE_F16:
+            MI_K_CHECK(mi_gemv_f16(ctx->stream, (const uint16_t *)a->data, (int64_t)(a->nb[1] / 2),
+                                   (const float *)b->data, (float *)node->data, n, k, m));
+            break;
+        default:
+            GGML_ABORT("MI355X: MUL_MAT with %s weights is not supported", ggml_type_name(a->type));
+    }
+}
+
+void run_fa(BackendCtx *ctx, ggml_tensor *node) {
+    const ggml_tensor *q = node->src[0], *k = node->src[1], *v = node->src[2], *mask = node->src[3];
+    const ggml_tensor *kvl = node->src[5];
+    float scale;
+    memcpy(&scale, node->op_params, sizeof(float));
+    MI_K_CHECK(mi_fa_decode(ctx->stream, (const float *)q->data, k->data, v->data,
+                            mask ? (const uint16_t *)mask->data : nullptr, kvl ? (const int32_t *)kvl->data : nullptr,
+                            k->ne[1], q->ne[2], k->ne[2], q->ne[0], k->nb[1], k->nb[2], v->nb[1], v->nb[2], scale,
+                            (float *)node->data, ctx->fa_ws, ctx->fa_ws_size));
+}
+
+using UseMap = std::unordered_map<const ggml_tensor *, int>;
+
+// how many graph nodes read each tensor (directly)
+UseMap count_uses_all(ggml_cgraph *g) {
+    UseMap m;
+    for (int i = 0; i < ggml_graph_n_nodes(g); i++) {
+        const ggml_tensor *nd = ggml_graph_node(g, i);
+        for (int s = 0; s < GGML_MAX_SRC; s++)
+            if (nd->src[s]) m[nd->src[s]]++;
+    }
+    return m;
+}
+
+// Runs node i (and, when fused, the nodes it absorbs); returns the number of nodes consumed.
+int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const UseMap &uses) {
+    ggml_tensor *node = ggml_graph_node(g, i);
+    const int nn = ggml_graph_n_nodes(g);
+    void *st = ctx->stream;
+    switch (node->op) {
+        case GGML_OP_MUL_MAT: {
+            // consecutive Q8_0 GEMVs reading the same activation (q/k/v, gate/up): one grouped launch
+            if (fusion_enabled() && node->src[0]->type == GGML_TYPE_Q8_0 && node->src[1]->ne[1] == 1 &&
+                node->src[1]->ne[0] <= 4096) {
+                ggml_tensor *grp[4] = {node};
+                int cnt = 1;
+                while (cnt < 4 && i + cnt < nn) {
+                    ggml_tensor *nx = ggml_graph_node(g, i + cnt);
+                    if (nx->op != GGML_OP_MUL_MAT || nx->src[1] != node->src[1] ||
+                        nx->src[0]->type != GGML_TYPE_Q8_0 || !nx->src[0]->extra ||
+                        inv_s_of(nx->src[0]) != inv_s_of(node->src[0]))
+                        break;
+                    grp[cnt++] = nx;
+                }
+                if (cnt > 1) {
+                    for (int j = 0; j < cnt; j++)
+                        GGML_ASSERT(((const TensorExtra *)grp[j]->src[0]->extra)->ready);
+                    run_mul_mat_q8_group(ctx, grp, cnt);
+                    return cnt;
+                }
+            }
+            run_mul_mat(ctx, node);
+            return 1;
+        }
+        case GGML_OP_FLASH_ATTN_EXT:
+            run_fa(ctx, node);
+            return 1;
+        case GGML_OP_RMS_NORM: {
+            float eps;
+            memcpy(&eps, node->op_params, sizeof(float));
+            const ggml_tensor *x = node->src[0];
+            // RMS_NORM followed by MUL with the norm weight (broadcast row): one launch
+            if (fusion_enabled() && i + 1 < nn) {
+                ggml_tensor *nx = ggml_graph_node(g, i + 1);
+                if (nx->op == GGML_OP_MUL && nx->src[0] == node && is_f32_contig(nx->src[1]) &&
+                    ggml_nelements(nx->src[1]) == x->ne[0] && uses.count(node) && uses.at(node) == 1) {
+                    MI_K_CHECK(mi_rms_norm(st, (const float *)x->data, (const float *)nx->src[1]->data,
+                                           (float *)nx->data, x->ne[0], ggml_nrows(x), eps));
+                    return 2;
+                }
+            }
+            MI_K_CHECK(mi_rms_norm(st, (const float *)x->data, nullptr, (float *)node->data, x->ne[0], ggml_nrows(x),
+                                   eps));
+            return 1;
+        }
+        case GGML_OP_ADD:
+        case GGML_OP_MUL: {
+            const ggml_tensor *a = node->src[0], *b = node->src[1];
+            auto fn = node->op == GGML_OP_ADD ? mi_add_bcast : mi_mul_bcast;
+            MI_K_CHECK(fn(st, (const float *)a->data, (const float *)b->data, (float *)node->data, ggml_nelements(a),
+                          ggml_nelements(b)));
+            return 1;
+        }
+        case GGML_OP_ROPE: {
+            const ggml_tensor *x = node->src[0];
+            float freq_base, freq_scale, attn_factor;
+            memcpy(&freq_base, (const float *)node->op_params + 5, sizeof(float));
+            memcpy(&freq_scale, (const float *)node->op_params + 6, sizeof(float));
+            memcpy(&attn_factor, (const float *)node->op_params + 8, sizeof(float));
+            MI_K_CHECK(mi_rope_neox(st, (const float *)x->data, (float *)node->data, (const int32_t *)node->src[1]->data,
+                                    x->ne[0], x->ne[1], x->ne[2], node->op_params[1], freq_base, freq_scale,
+                                    attn_factor, x->nb[1], x->nb[2], node->nb[1], node->nb[2]));
+            return 1;
+        }
+        case GGML_OP_SET_ROWS: {
+            const ggml_tensor *src = node->src[0], *idx = node->src[1];
+            MI_K_CHECK(mi_set_rows_f16(st, (const float *)src->data, idx->data, idx->type == GGML_TYPE_I64,
+                                       (uint16_t *)node->data, src->ne[0], src->ne[1], src->nb[1], node->nb[1],
+                                       node->ne[1]));
+            return 1;
+        }
+        case GGML_OP_GET_ROWS: {
+            const ggml_tensor *src = node->src[0], *idx = node->src[1];
+            MI_K_CHECK(mi_get_rows(st, src->data, src->type == GGML_TYPE_F16, (const int32_t *)idx->data,
+                                   (float *)node->data, src->ne[0], idx->ne[0], src->nb[1], src->ne[1]));
+            return 1;
+        }
+        case GGML_OP_GLU:
+            MI_K_CHECK(mi_swiglu(st, (const float *)node->src[0]->data, (const float *)node->src[1]->data,
+                                 (float *)node->data, ggml_nelements(node)));
+            return 1;
+        case GGML_OP_ARGMAX: {
+            const ggml_tensor *x = node->src[0];
+            MI_K_CHECK(mi_argmax(st, (const float *)x->data, (int32_t *)node->data, x->ne[0], ggml_nrows(x)));
+            return 1;
+        }
+        default:
+            GGML_ABORT("MI355X: op %s is not supported", ggml_op_name(node->op));
+    }
+    return 1;
+}
+
+void run_graph_nodes(BackendCtx *ctx, ggml_cgraph *g) {
+    const int nn = ggml_graph_n_nodes(g);
+    const UseMap uses = count_uses_all(g);
+    for (int i = 0; i < nn;) {
+        ggml_tensor *node = ggml_graph_node(g, i);
+        if (is_noop(node)) {
+            i++;
+            continue;
+        }
+        if (trace_node_sync())
+            fprintf(stderr, "MI355X trace: node=%d name=%s op=%s ne=[%lld,%lld,%lld,%lld] begin\n", i, node->name,
+                    ggml_op_name(node->op), (long long)node->ne[0], (long long)node->ne[1], (long long)node->ne[2],
+                    (long long)node->ne[3]);
+        const int used = compute_node(ctx, g, i, uses);
+        if (trace_node_sync()) {
+            MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+            fprintf(stderr, "MI355X trace: node=%d name=%s op=%s complete\n", i, node->name, ggml_op_name(node->op));
+        }
+        i += used;
+    }
+}
+
+// everything the captured launches depend on: ops, data pointers, shapes, strides, params
+std::vector<uint64_t> graph_signature(ggml_cgraph *g) {
+    std::vector<uint64_t> sig;
+    for (int i = 0; i < ggml_graph_n_nodes(g); i++) {
+        const ggml_tensor *t = ggml_graph_node(g, i);
+        sig.push_back((uint64_t)t->op);
+        sig.push_back((uint64_t)(uintptr_t)t->data);
+        for (int d = 0; d < 4; d++) {
+            sig.push_back((uint64_t)t->ne[d]);
+            sig.push_back((uint64_t)t->nb[d]);
+        }
+        for (int p = 0; p < GGML_MAX_OP_PARAMS / 4; p++) sig.push_back((uint64_t)(uint32_t)t->op_params[p]);
+        for (int s = 0; s < GGML_MAX_SRC; s++) {
+            const ggml_tensor *src = t->src[s];
+            sig.push_back(src ? (uint64_t)(uintptr_t)src->data : 0);
+            if (src) {
+                sig.push_back((uint64_t)src->type);
+                for (int d = 0; d < 4; d++) sig.push_back((uint64_t)src->nb[d] ^ ((uint64_t)src->ne[d] << 32));
+                sig.push_back((uint64_t)(uintptr_t)src->extra);
+                if (src->extra) sig.push_back((uint64_t)(uintptr_t)((TensorExtra *)src->extra)->inv_s);
+            }
+        }
+    }
+    return sig;
+}
+
+// ---- backend iface
+
+const char *backend_get_name(ggml_backend_t backend) { return ((BackendCtx *)backend->context)->name.c_str(); }
+
+void backend_free(ggml_backend_t backend) {
+    BackendCtx *ctx = (BackendCtx *)backend->context;
+    set_device(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->gexec) (void)hipGraphExecDestroy(ctx->gexec);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->fa_ws) (void)hipFree(ctx->fa_ws);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    delete backend;
+}
+
+void backend_set_tensor_async(ggml_backend_t backend, ggml_tensor *tensor, const void *data, size_t offset,
+                              size_t size) {
+    BackendCtx *ctx = (BackendCtx *)backend->context;
+    if (tensor->extra) {  // weights need the side copy: go through the buffer path
+        ggml_backend_tensor_set(tensor, data, offset, size);
+        return;
+    }
+    MI_HIP_CHECK(hipMemcpyAsync((char *)tensor->data + offset, data, size, hipMemcpyHostToDevice, ctx->stream));
+}
+
+void backend_get_tensor_async(ggml_backend_t backend, const ggml_tensor *tensor, void *data, size_t offset,
+                              size_t size) {
+    BackendCtx *ctx = (BackendCtx *)backend->context;
+    MI_HIP_CHECK(hipMemcpyAsync(data, (const char *)tensor->data + offset, size, hipMemcpyDeviceToHost, ctx->stream));
+}
+
+void backend_synchronize(ggml_backend_t backend) {
+    BackendCtx *ctx = (BackendCtx *)backend->context;
+    set_device(ctx->device);
+    MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+}
+
+enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgraph) {
+    BackendCtx *ctx = (BackendCtx *)backend->context;
+    set_device(ctx->device);
+    ensure_buffers(ctx, cgraph);
+    if (!graphs_enabled()) {
+        run_graph_nodes(ctx, cgraph);
+        return GGML_STATUS_SUCCESS;
+    }
+    std::vector<uint64_t> sig = graph_signature(cgraph);
+    if (ctx->gexec && sig == ctx->signature) {
+        MI_HIP_CHECK(hipGraphLaunch(ctx->gexec, ctx->stream));
+        return GGML_STATUS_SUCCESS;
+    }
+    // a changed graph runs eagerly once; when the same graph comes back it is captured
+    if (sig != ctx->signature) {
+        ctx->signature = std::move(sig);
+        ctx->same_calls = 0;
+        if (ctx->gexec) {
+            MI_HIP_CHECK(hipGraphExecDestroy(ctx->gexec));
+            ctx->gexec = nullptr;
+        }
+        run_graph_nodes(ctx, cgraph);
+        return GGML_STATUS_SUCCESS;
+    }
+    hipGraph_t graph = nullptr;
+    MI_HIP_CHECK(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    run_graph_nodes(ctx, cgraph);
+    MI_HIP_CHECK(hipStreamEndCapture(ctx->stream, &graph));
+    MI_HIP_CHECK(hipGraphInstantiate(&ctx->gexec, graph, nullptr, nullptr, 0));
+    MI_HIP_CHECK(hipGraphDestroy(graph));
+    MI_HIP_CHECK(hipGraphLaunch(ctx->gexec, ctx->stream));
+    return GGML_STATUS_SUCCESS;
+}
+
+const ggml_backend_i kBackendIface = {
+    /* get_name           */ backend_get_name,
+    /* free               */ backend_free,
+    /* set_tensor_async   */ backend_set_tensor_async,
+    /* get_tensor_async   */ backend_get_tensor_async,
+    /* cpy_tensor_async   */ nullptr,
+    /* synchronize        */ backend_synchronize,
+    /* graph_plan_create  */ nullptr,
+    /* graph_plan_free    */ nullptr,
+    /* graph_plan_update  */ nullptr,
+    /* graph_plan_compute */ nullptr,
+    /* graph_compute      */ backend_graph_compute,
+    /* event_record       */ nullptr,
+    /* event_wait         */ nullptr,
+    /* graph_optimize     */ nullptr,
+};
+
+ggml_guid_t backend_guid() {
+    static ggml_guid guid = {{0x6d, 0x69, 0x33, 0x35, 0x35, 0x78, 0x2d, 0x67, 0x66, 0x78, 0x39, 0x35, 0x30, 0x2d,
+                              0x76, 0x31}};
+    return &guid;
+}
+
+// ---- device iface
+
+const char *dev_get_name(ggml_backend_dev_t dev) { return ((DeviceCtx *)dev->context)->name.c_str(); }
+const char *dev_get_description(ggml_backend_dev_t dev) { return ((DeviceCtx *)dev->context)->description.c_str(); }
+
+void dev_get_memory(ggml_backend_dev_t dev, size_t *free, size_t *total) {
+    set_device(((DeviceCtx *)dev->context)->device);
+    MI_HIP_CHECK(hipMemGetInfo(free, total));
+}
+
+enum ggml_backend_dev_type dev_get_type(ggml_backend_dev_t) { return GGML_BACKEND_DEVICE_TYPE_GPU; }
+
+void dev_get_props(ggml_backend_dev_t dev, ggml_backend_dev_props *props) {
+    props->name = dev_get_name(dev);
+    props->description = dev_get_description(dev);
+    props->type = GGML_BACKEND_DEVICE_TYPE_GPU;
+    props->device_id = nullptr;
+    dev_get_memory(dev, &props->memory_free, &props->memory_total);
+    props->caps = {/* async */ true, /* host_buffer */ false, /* buffer_from_host_ptr */ false, /* events */ false};
+}
+
+ggml_backend_t dev_init_backend(ggml_backend_dev_t dev, const char *) {
+    return ggml_backend_mi355x_init(((DeviceCtx *)dev->context)->device);
+}
+
+ggml_backend_buffer_type_t dev_get_buffer_type(ggml_backend_dev_t dev) { return &((DeviceCtx *)dev->context)->buft; }
+
+bool dev_supports_op(ggml_backend_dev_t, const ggml_tensor *op) { return supports_op_impl(op); }
+
+bool dev_supports_buft(ggml_backend_dev_t dev, ggml_backend_buffer_type_t buft) {
+    return buft->iface.get_name == buft_get_name && buft->context == dev->context;
+}
+
+bool dev_offload_op(ggml_backend_dev_t, const ggml_tensor *) { return false; }
+
+const ggml_backend_device_i kDeviceIface = {
+    /* get_name             */ dev_get_name,
+    /* get_description      */ dev_get_description,
+    /* get_memory           */ dev_get_memory,
+    /* get_type             */ dev_get_type,
+    /* get_props            */ dev_get_props,
+    /* init_backend         */ dev_init_backend,
+    /* get_buffer_type      */ dev_get_buffer_type,
+    /* get_host_buffer_type */ nullptr,
+    /* buffer_from_host_ptr */ nullptr,
+    /* supports_op          */ dev_supports_op,
+    /* supports_buft        */ dev_supports_buft,
+    /* offload_op           */ dev_offload_op,
+    /* event_new            */ nullptr,
+    /* event_free           */ nullptr,
+    /* event_synchronize    */ nullptr,
+};
+
+// ---- registry
+
+struct RegCtx {
+    std::vector<std::unique_ptr<DeviceCtx>> dev_ctx;
+    std::vector<std::unique_ptr<ggml_backend_device>> devs;
+};
+
+const char *reg_get_name(ggml_backend_reg_t) { return GGML_MI355X_NAME; }
+size_t reg_get_device_count(ggml_backend_reg_t reg) { return ((RegCtx *)reg->context)->devs.size(); }
+ggml_backend_dev_t reg_get_device(ggml_backend_reg_t reg, size_t index) {
+    RegCtx *ctx = (RegCtx *)reg->context;
+    GGML_ASSERT(index < ctx->devs.size());
+    return ctx->devs[index].get();
+}
+void *reg_get_proc_address(ggml_backend_reg_t, const char *name) {
+    if (strcmp(name, "ggml_backend_mi355x_set_smooth_factors") == 0) return (void *)ggml_backend_mi355x_set_smooth_factors;
+    return nullptr;
+}
+
+const ggml_backend_reg_i kRegIface = {reg_get_name, reg_get_device_count, reg_get_device, reg_get_proc_address};
+
+RegCtx *registry_ctx() {
+    static RegCtx *ctx = [] {
+        RegCtx *c = new RegCtx();
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+        for (int i = 0; i < n && i < GGML_MI355X_MAX_DEVICES; i++) {
+            auto d = std::make_unique<DeviceCtx>();
+            d->device = i;
+            d->name = std::string(GGML_MI355X_NAME) + std::to_string(i);
+            hipDeviceProp_t p;
+            if (hipGetDeviceProperties(&p, i) == hipSuccess)
+                d->description = std::string(p.name) + " (" + p.gcnArchName + ")";
+            else
+                d->description = "HIP device";
+            d->buft_name = d->name;
+            d->buft.iface = kBuftIface;
+            d->buft.context = d.get();
+            auto dev = std::make_unique<ggml_backend_device>();
+            dev->iface = kDeviceIface;
+            dev->reg = nullptr;
+            dev->context = d.get();
+            d->buft.device = dev.get();
+            c->dev_ctx.push_back(std::move(d));
+            c->devs.push_back(std::move(dev));
+        }
+        return c;
+    }();
+    return ctx;
+}
+
+}  // namespace
+
+extern "C" {
+
+ggml_backend_reg_t ggml_backend_mi355x_reg(void) {
+    static ggml_backend_reg reg = [] {
+        ggml_backend_reg r;
+        r.api_version = GGML_BACKEND_API_VERSION;
+        r.iface = kRegIface;
+        r.context = registry_ctx();
+        return r;
+    }();
+    static std::once_flag once;
+    std::call_once(once, [] {
+        for (auto &d : registry_ctx()->devs) d->reg = &reg;
+    });
+    return &reg;
+}
+
+int ggml_backend_mi355x_get_device_count(void) { return (int)registry_ctx()->devs.size(); }
+
+void ggml_backend_mi355x_get_device_description(int device, char *description, size_t description_size) {
+    RegCtx *c = registry_ctx();
+    if (device < 0 || device >= (int)c->dev_ctx.size()) {
+        snprintf(description, description_size, "invalid device");
+        return;
+    }
+    snprintf(description, description_size, "%s", c->dev_ctx[device]->description.c_str());
+}
+
+void ggml_backend_mi355x_get_device_memory(int device, size_t *free, size_t *total) {
+    set_device(device);
+    MI_HIP_CHECK(hipMemGetInfo(free, total));
+}
+
+ggml_backend_buffer_type_t ggml_backend_mi355x_buffer_type(int device) {
+    ggml_backend_mi355x_reg();
+    RegCtx *c = registry_ctx();
+    if (device < 0 || device >= (int)c->dev_ctx.size()) return nullptr;
+    return &c->dev_ctx[device]->buft;
+}
+
+ggml_backend_t ggml_backend_mi355x_init(int device) {
+    ggml_backend_reg_t reg = ggml_backend_mi355x_reg();
+    RegCtx *c = registry_ctx();
+    if (device < 0 || device >= (int)c->devs.size()) {
+        fprintf(stderr, "MI355X: invalid device %d\n", device);
+        return nullptr;
+    }
+    (void)reg;
+    set_device(device);
+    BackendCtx *ctx = new BackendCtx();
+    ctx->device = device;
+    ctx->name = std::string(GGML_MI355X_NAME) + std::to_string(device);
+    MI_HIP_CHECK(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+    return new ggml_backend{backend_guid(), kBackendIface, c->devs[device].get(), ctx};
+}
+
+bool ggml_backend_is_mi355x(ggml_backend_t backend) {
+    return backend != nullptr && backend->guid == backend_guid();
+}
+
+bool ggml_backend_mi355x_set_smooth_factors(struct ggml_tensor *weight, const float *s, int64_t n) {
+    if (!weight || !weight->extra || weight->type != GGML_TYPE_Q8_0 || n != weight->ne[0] || !s) return false;
+    BufferCtx *bctx = (BufferCtx *)weight->buffer->context;
+    std::vector<float> inv((size_t)n);
+    for (int64_t i = 0; i < n; i++) inv[i] = 1.0f / s[i];
+    const std::string key((const char *)inv.data(), inv.size() * sizeof(float));
+    std::lock_guard<std::mutex> lk(bctx->mtx);
+    void *dev = nullptr;
+    auto it = bctx->inv_s_by_content.find(key);
+    if (it != bctx->inv_s_by_content.end()) {
+        dev = it->second;
+    } else {
+        set_device(bctx->device);
+        MI_HIP_CHECK(hipMalloc(&dev, inv.size() * sizeof(float)));
+        MI_HIP_CHECK(hipMemcpy(dev, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice));
+        bctx->owned.push_back(dev);
+        bctx->inv_s_by_content.emplace(key, dev);
+    }
+    ((TensorExtra *)weight->extra)->inv_s = (const float *)dev;
+    return true;
+}
+
+#ifdef GGML_BACKEND_DL
+ggml_backend_reg_t ggml_backend_init(void) { return ggml_backend_mi355x_reg(); }
+#endif
+
+}  // extern "C"

@@ -1,0 +1,229 @@
+// glue.hip -- the small decode-graph ops around the hot path (one token, fp32
+// activations): RMSNorm (+ the following MUL by the norm weight), broadcast
+// ADD / MUL, neox RoPE, SET_ROWS into an fp16 KV cache, GET_ROWS from an fp16
+// or fp32 table, SwiGLU, ARGMAX.  Semantics follow the ggml-CPU ops
+// (ggml/src/ggml-cpu/ops.cpp of llama.cpp @ 37b3a9e0): rms_norm sums x*x in
+// double, rope builds theta by repeated multiplication with
+// powf(freq_base, -2/n_dims), argmax keeps the first maximum.
+#include "mi_common.h"
+
+#include <math.h>
+
+namespace {
+
+using namespace mi;
+
+// one workgroup per row; y = x / sqrt(mean(x^2) + eps) [* w]
+__global__ __launch_bounds__(256) void k_rms_norm(const float *__restrict__ x, const float *__restrict__ w,
+                                                  float *__restrict__ y, int ne0, float eps) {
+    const int row = blockIdx.x;
+    const float *xr = x + (size_t)row * ne0;
+    float *yr = y + (size_t)row * ne0;
+    double s = 0.0;
+    for (int i = threadIdx.x; i < ne0; i += 256) s += (double)(xr[i] * xr[i]);
+    __shared__ double sh[256];
+    sh[threadIdx.x] = s;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) sh[threadIdx.x] += sh[threadIdx.x + o];
+        __syncthreads();
+    }
+    const float mean = (float)(sh[0] / ne0);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int i = threadIdx.x; i < ne0; i += 256) {
+        const float v = xr[i] * scale;
+        yr[i] = w ? v * w[i] : v;
+    }
+}
+
+// dst[i] = a[i] (op) b[i % nb], contiguous rows of a; b broadcast along rows
+template <int OP>
+__global__ void k_binary_bcast(const float *__restrict__ a, const float *__restrict__ b, float *__restrict__ d,
+                               int64_t n, int64_t nb) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float bv = b[i % nb];
+    d[i] = OP == 0 ? a[i] + bv : a[i] * bv;
+}
+
+// neox RoPE on [ne0 = head_dim][ne1 = heads][ne2 = tokens] fp32, pos[ne2]
+__global__ void k_rope_neox(const float *__restrict__ x, float *__restrict__ y, const int32_t *__restrict__ pos,
+                            int ne0, int ne1, int n_dims, float theta_scale, float freq_scale, float attn_factor,
+                            size_t nb1, size_t nb2, size_t ob1, size_t ob2) {
+    const int i = threadIdx.x;  // pair index < n_dims/2
+    const int h = blockIdx.x;
+    const int t = blockIdx.y;
+    const char *xr = (const char *)x + (size_t)t * nb2 + (size_t)h * nb1;
+    char *yr = (char *)y + (size_t)t * ob2 + (size_t)h * ob1;
+    const int half = n_dims / 2;
+    if (i < half) {
+        float theta = (float)pos[t];
+        for (int k = 0; k < i; k++) theta *= theta_scale;  // same product order as the CPU cache
+        const float th = freq_scale * theta;
+        const float c = cosf(th) * attn_factor;
+        const float s = sinf(th) * attn_factor;
+        const float x0 = ((const float *)xr)[i];
+        const float x1 = ((const float *)xr)[i + half];
+        ((float *)yr)[i] = x0 * c - x1 * s;
+        ((float *)yr)[i + half] = x0 * s + x1 * c;
+    }
+    for (int j = n_dims + i; j < ne0; j += blockDim.x) ((float *)yr)[j] = ((const float *)xr)[j];
+}
+
+// dst rows idx[r] (fp16 table, row stride dnb1 bytes) = fp16(src row r)
+template <typename IDX>
+__global__ void k_set_rows_f16(const float *__restrict__ src, const IDX *__restrict__ idx, uint16_t *__restrict__ dst,
+                               int ne0, size_t snb1, size_t dnb1, int64_t n_dst_rows) {
+    const int r = blockIdx.x;
+    const int64_t dr = (int64_t)idx[r];
+    if (dr < 0 || dr >= n_dst_rows) return;
+    const float *s = (const float *)((const char *)src + (size_t)r * snb1);
+    uint16_t *d = (uint16_t *)((char *)dst + (size_t)dr * dnb1);
+    for (int i = threadIdx.x; i < ne0; i += blockDim.x) d[i] = f2h(s[i]);
+}
+
+template <typename T, typename IDX>
+__global__ void k_get_rows(const T *__restrict__ src, const IDX *__restrict__ idx, float *__restrict__ dst, int ne0,
+                           size_t snb1, int64_t n_src_rows) {
+    const int r = blockIdx.x;
+    int64_t sr = (int64_t)idx[r];
+    sr = sr < 0 ? 0 : (sr >= n_src_rows ? n_src_rows - 1 : sr);
+    const T *s = (const T *)((const char *)src + (size_t)sr * snb1);
+    float *d = dst + (size_t)r * ne0;
+    for (int i = threadIdx.x; i < ne0; i += blockDim.x) {
+        if constexpr (sizeof(T) == 2) d[i] = h2f(s[i]);
+        else d[i] = s[i];
+    }
+}
+
+// silu(g) * u with ggml's silu: x / (1 + exp(-x))
+__global__ void k_swiglu(const float *__restrict__ g, const float *__restrict__ u, float *__restrict__ d, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float x = g[i];
+    d[i] = (x / (1.0f + expf(-x))) * u[i];
+}
+
+// one workgroup per row: index of the first maximum
+__global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, int32_t *__restrict__ out, int ne0) {
+    const float *xr = x + (size_t)blockIdx.x * ne0;
+    float best = -INFINITY;
+    int bi = 0;
+    for (int i = threadIdx.x; i < ne0; i += 256) {
+        const float v = xr[i];
+        if (v > best) { best = v; bi = i; }
+    }
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    sv[threadIdx.x] = best;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) {
+            const float v2 = sv[threadIdx.x + o];
+            const int i2 = si[threadIdx.x + o];
+            if (v2 > sv[threadIdx.x] || (v2 == sv[threadIdx.x] && i2 < si[threadIdx.x])) {
+                sv[threadIdx.x] = v2;
+                si[threadIdx.x] = i2;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = si[0];
+}
+
+// fp16 decode mask row from the effective length: 0 for pos < len, -inf beyond
+__global__ void k_fill_mask(uint16_t *__restrict__ mask, const int32_t *__restrict__ len, int n_kv) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n_kv) mask[i] = i < *len ? (uint16_t)0 : (uint16_t)0xfc00u;
+}
+
+unsigned grid1(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
+
+}  // namespace
+
+extern "C" {
+
+int mi_rms_norm(void *stream, const float *x, const float *w, float *y, int64_t ne0, int64_t nrows, float eps) {
+    MI_CHECK_ARG(x && y && ne0 > 0 && nrows > 0, "rms_norm: bad arguments");
+    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned)nrows), dim3(256), 0, (hipStream_t)stream, x, w, y, (int)ne0, eps);
+    MI_CHECK_LAUNCH("k_rms_norm");
+    return MI_OK;
+}
+
+int mi_add_bcast(void *stream, const float *a, const float *b, float *d, int64_t n, int64_t nb) {
+    MI_CHECK_ARG(a && b && d && n > 0 && nb > 0, "add: bad arguments");
+    hipLaunchKernelGGL((k_binary_bcast<0>), dim3(grid1(n, 256)), dim3(256), 0, (hipStream_t)stream, a, b, d, n, nb);
+    MI_CHECK_LAUNCH("k_add");
+    return MI_OK;
+}
+
+int mi_mul_bcast(void *stream, const float *a, const float *b, float *d, int64_t n, int64_t nb) {
+    MI_CHECK_ARG(a && b && d && n > 0 && nb > 0, "mul: bad arguments");
+    hipLaunchKernelGGL((k_binary_bcast<1>), dim3(grid1(n, 256)), dim3(256), 0, (hipStream_t)stream, a, b, d, n, nb);
+    MI_CHECK_LAUNCH("k_mul");
+    return MI_OK;
+}
+
+int mi_rope_neox(void *stream, const float *x, float *y, const int32_t *pos, int64_t ne0, int64_t ne1, int64_t ne2,
+                 int64_t n_dims, float freq_base, float freq_scale, float attn_factor, size_t nb1, size_t nb2,
+                 size_t ob1, size_t ob2) {
+    // theta_scale on the host with the C library powf, as the CPU rope cache does
+    const float theta_scale = powf(freq_base, -2.0f / (float)n_dims);
+    MI_CHECK_ARG(x && y && pos && n_dims > 0 && n_dims % 2 == 0 && n_dims <= ne0 && n_dims <= 1024,
+                 "rope: bad arguments");
+    const int threads = (int)((n_dims / 2 + 63) / 64 * 64);
+    hipLaunchKernelGGL(k_rope_neox, dim3((unsigned)ne1, (unsigned)ne2), dim3(threads), 0, (hipStream_t)stream, x, y,
+                       pos, (int)ne0, (int)ne1, (int)n_dims, theta_scale, freq_scale, attn_factor, nb1, nb2, ob1, ob2);
+    MI_CHECK_LAUNCH("k_rope_neox");
+    return MI_OK;
+}
+
+int mi_set_rows_f16(void *stream, const float *src, const void *idx, int idx_is_i64, uint16_t *dst, int64_t ne0,
+                    int64_t nrows, size_t snb1, size_t dnb1, int64_t n_dst_rows) {
+    MI_CHECK_ARG(src && idx && dst && ne0 > 0 && nrows > 0, "set_rows: bad arguments");
+    if (idx_is_i64)
+        hipLaunchKernelGGL((k_set_rows_f16<int64_t>), dim3((unsigned)nrows), dim3(256), 0, (hipStream_t)stream, src,
+                           (const int64_t *)idx, dst, (int)ne0, snb1, dnb1, n_dst_rows);
+    else
+        hipLaunchKernelGGL((k_set_rows_f16<int32_t>), dim3((unsigned)nrows), dim3(256), 0, (hipStream_t)stream, src,
+                           (const int32_t *)idx, dst, (int)ne0, snb1, dnb1, n_dst_rows);
+    MI_CHECK_LAUNCH("k_set_rows_f16");
+    return MI_OK;
+}
+
+int mi_get_rows(void *stream, const void *src, int src_is_f16, const int32_t *idx, float *dst, int64_t ne0,
+                int64_t nrows, size_t snb1, int64_t n_src_rows) {
+    MI_CHECK_ARG(src && idx && dst && ne0 > 0 && nrows > 0, "get_rows: bad arguments");
+    if (src_is_f16)
+        hipLaunchKernelGGL((k_get_rows<uint16_t, int32_t>), dim3((unsigned)nrows), dim3(256), 0, (hipStream_t)stream,
+                           (const uint16_t *)src, idx, dst, (int)ne0, snb1, n_src_rows);
+    else
+        hipLaunchKernelGGL((k_get_rows<float, int32_t>), dim3((unsigned)nrows), dim3(256), 0, (hipStream_t)stream,
+                           (const float *)src, idx, dst, (int)ne0, snb1, n_src_rows);
+    MI_CHECK_LAUNCH("k_get_rows");
+    return MI_OK;
+}
+
+int mi_swiglu(void *stream, const float *g, const float *u, float *d, int64_t n) {
+    MI_CHECK_ARG(g && u && d && n > 0, "swiglu: bad arguments");
+    hipLaunchKernelGGL(k_swiglu, dim3(grid1(n, 256)), dim3(256), 0, (hipStream_t)stream, g, u, d, n);
+    MI_CHECK_LAUNCH("k_swiglu");
+    return MI_OK;
+}
+
+int mi_argmax(void *stream, const float *x, int32_t *out, int64_t ne0, int64_t nrows) {
+    MI_CHECK_ARG(x && out && ne0 > 0 && nrows > 0, "argmax: bad arguments");
+    hipLaunchKernelGGL(k_argmax, dim3((unsigned)nrows), dim3(256), 0, (hipStream_t)stream, x, out, (int)ne0);
+    MI_CHECK_LAUNCH("k_argmax");
+    return MI_OK;
+}
+
+int mi_fill_mask_f16(void *stream, uint16_t *mask, const int32_t *len, int64_t n_kv) {
+    MI_CHECK_ARG(mask && len && n_kv > 0, "fill_mask: bad arguments");
+    hipLaunchKernelGGL(k_fill_mask, dim3(grid1(n_kv, 256)), dim3(256), 0, (hipStream_t)stream, mask, len, (int)n_kv);
+    MI_CHECK_LAUNCH("k_fill_mask");
+    return MI_OK;
+}
+
+}  // extern "C"

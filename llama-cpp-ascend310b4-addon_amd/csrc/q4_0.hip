@@ -147,20 +147,87 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0(const uint8_t *__restrict__ q
     }
 }
 
+// fp16 activations read straight from global memory (2*k bytes per row, L1/L2
+// resident and shared by every workgroup): no LDS staging, no barrier.
+template <int G, int U, int M>
+__global__ __launch_bounds__(256) void k_gemv_q4_0_gx(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ wd,
+                                                      const uint16_t *__restrict__ x16, float *__restrict__ y, int n,
+                                                      int nb, int m) {
+    constexpr int RPB = 256 / G;
+    const int tid = threadIdx.x;
+    const int j = tid % G;
+    const int row = blockIdx.x * RPB + tid / G;
+    const bool row_ok = row < n;
+    const int k = nb * QK;
+    const size_t rbase = (size_t)min(row, n - 1) * nb;
+
+    float acc[M];
+#pragma unroll
+    for (int i = 0; i < M; i++) acc[i] = 0.0f;
+
+    for (int b0 = 0; b0 < nb; b0 += U * G) {
+        int4 wq[U];
+        uint32_t dw[U];
+        int4 xv[U][M][4];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int b = min(b0 + j + u * G, nb - 1);
+            wq[u] = ld_stream16(qs + (rbase + b) * 16);
+            dw[u] = wd[rbase + b];
+#pragma unroll
+            for (int i = 0; i < M; i++) {
+                const int4 *xp = (const int4 *)(x16 + (size_t)min(i, m - 1) * k + (size_t)b * QK);
+#pragma unroll
+                for (int c = 0; c < 4; c++) xv[u][i][c] = xp[c];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (b0 + j + u * G < nb) {
+                const float d = h2f((uint16_t)dw[u]);
+#pragma unroll
+                for (int i = 0; i < M; i++) {
+                    uint32_t xs[16];
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        xs[4 * c + 0] = (uint32_t)xv[u][i][c].x; xs[4 * c + 1] = (uint32_t)xv[u][i][c].y;
+                        xs[4 * c + 2] = (uint32_t)xv[u][i][c].z; xs[4 * c + 3] = (uint32_t)xv[u][i][c].w;
+                    }
+                    acc[i] = fmaf(d, q4_block_dot(wq[u], xs), acc[i]);
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < M; i++) {
+        const float s = group_sum<G>(acc[i]);
+        if (row_ok && j == 0 && i < m) y[(size_t)i * n + row] = s;
+    }
+}
+
 template <int G, int U, int M, bool F32X>
 int launch_gu(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16,
               const float *x32, float *y) {
     const Q4Planes p = q4_planes(n, k);
     constexpr int RPB = 256 / G;
     const size_t smem = (size_t)M * k * 2;
-    if (smem > 64 * 1024) {
+    if (F32X && smem > 64 * 1024) {
         set_error("gemv_q4_0: activation of %d x %lld does not fit in LDS", M, (long long)k);
         return MI_ERR_UNSUPPORTED;
     }
-    hipLaunchKernelGGL((k_gemv_q4_0<G, U, M, F32X>), dim3((unsigned)((n + RPB - 1) / RPB)), dim3(256), smem, st,
-                       base, (const uint16_t *)(base + p.plane), x16, x32, y, (int)n, (int)(k / QK), (int)m);
-    MI_CHECK_LAUNCH("k_gemv_q4_0");
-    return MI_OK;
+    if constexpr (!F32X) {
+        hipLaunchKernelGGL((k_gemv_q4_0_gx<G, U, M>), dim3((unsigned)((n + RPB - 1) / RPB)), dim3(256), 0, st, base,
+                           (const uint16_t *)(base + p.plane), x16, y, (int)n, (int)(k / QK), (int)m);
+        MI_CHECK_LAUNCH("k_gemv_q4_0_gx");
+        return MI_OK;
+    }
+    else {
+        hipLaunchKernelGGL((k_gemv_q4_0<G, U, M, true>), dim3((unsigned)((n + RPB - 1) / RPB)), dim3(256), smem, st,
+                           base, (const uint16_t *)(base + p.plane), x16, x32, y, (int)n, (int)(k / QK), (int)m);
+        MI_CHECK_LAUNCH("k_gemv_q4_0");
+        return MI_OK;
+    }
 }
 
 template <int G, int M, bool F32X>

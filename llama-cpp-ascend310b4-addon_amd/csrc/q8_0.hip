@@ -12,6 +12,7 @@
 // and W8a8DequantCustom (called at patch:1269-1270) with its casts.
 #include "mi_common.h"
 
+#include <limits.h>
 #include <string.h>
 
 namespace {
@@ -104,23 +105,35 @@ __global__ __launch_bounds__(256) void k_act_quant_q8_0(const float *__restrict_
 
 // ------------------------------------------------------------------ GEMV
 
-// Lane layout: G lanes per output row (power of two), RPB = 256/G rows per
-// 256-thread workgroup.  Lane j of a row handles blocks b = j, j+G, ..., U of
-// them per pass.  The U weight loads of the first pass (2 x 16 B + fp16 scale
-// each) use clamped addresses and no branches, so they are all in flight
-// before the activation is staged in LDS and the HBM latency overlaps the
-// prologue.  The activation rows (m <= M) live in LDS as int8 qs + fp32 d.
-template <int G, int U, int M, bool FUSED>
-__global__ __launch_bounds__(256) void k_gemv_q8_0(const uint8_t *__restrict__ qlo, const uint8_t *__restrict__ qhi,
-                                                   const uint16_t *__restrict__ wd,
-                                                   const int8_t *__restrict__ xq_qs, const uint16_t *__restrict__ xq_d,
-                                                   const float *__restrict__ x, const float *__restrict__ inv_s,
-                                                   float *__restrict__ y, int n, int nb, int m, int rounding) {
-    constexpr int RPB = 256 / G;
-    extern __shared__ __align__(16) uint8_t smem[];
-    int8_t *s_qs = (int8_t *)smem;                                          // [M][nb*32]
-    float *s_d = (float *)(smem + (((size_t)M * nb * QK + 15) / 16) * 16);  // [M][nb]
+// Lane layout (both GEMV kernels): G lanes per output row (power of two),
+// RPB = 256/G rows per 256-thread workgroup.  Lane j of a row handles blocks
+// b = j, j+G, ..., U of them per pass.  Weight loads use clamped addresses and
+// no branches, so all of a pass is in flight at once; the int32 block dots are
+// exact (v_dot4_i32_i8) and the fp32 scale d_w*d_x is applied per block.
 
+__device__ __forceinline__ int dot_block(const int4 &l4, const int4 &h4, const int4 &x0, const int4 &x1) {
+    int s = 0;
+    s = __builtin_amdgcn_sdot4(l4.x, x0.x, s, false);
+    s = __builtin_amdgcn_sdot4(l4.y, x0.y, s, false);
+    s = __builtin_amdgcn_sdot4(l4.z, x0.z, s, false);
+    s = __builtin_amdgcn_sdot4(l4.w, x0.w, s, false);
+    s = __builtin_amdgcn_sdot4(h4.x, x1.x, s, false);
+    s = __builtin_amdgcn_sdot4(h4.y, x1.y, s, false);
+    s = __builtin_amdgcn_sdot4(h4.z, x1.z, s, false);
+    s = __builtin_amdgcn_sdot4(h4.w, x1.w, s, false);
+    return s;
+}
+
+// Pre-quantized activations (planar xq) read straight from global memory: the
+// m*k bytes are shared by every workgroup and stay resident in L1/L2, so no LDS
+// staging and no barrier sit between the weight loads and the math.
+template <int G, int U, int M>
+__global__ __launch_bounds__(256) void k_gemv_q8_0_xq(const uint8_t *__restrict__ qlo, const uint8_t *__restrict__ qhi,
+                                                      const uint16_t *__restrict__ wd,
+                                                      const int8_t *__restrict__ xq_qs,
+                                                      const uint16_t *__restrict__ xq_d, float *__restrict__ y, int n,
+                                                      int nb, int m) {
+    constexpr int RPB = 256 / G;
     const int tid = threadIdx.x;
     const int j = tid % G;
     const int row = blockIdx.x * RPB + tid / G;
@@ -128,6 +141,95 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0(const uint8_t *__restrict__ q
     const int k = nb * QK;
     const size_t rbase = (size_t)min(row, n - 1) * nb;
 
+    float acc[M];
+#pragma unroll
+    for (int i = 0; i < M; i++) acc[i] = 0.0f;
+
+    for (int b0 = 0; b0 < nb; b0 += U * G) {
+        int4 lo[U], hi[U], xa[U][M], xb[U][M];
+        uint32_t dw[U], dx[U][M];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int b = min(b0 + j + u * G, nb - 1);
+            lo[u] = ld_stream16(qlo + (rbase + b) * 16);
+            hi[u] = ld_stream16(qhi + (rbase + b) * 16);
+            dw[u] = wd[rbase + b];
+#pragma unroll
+            for (int i = 0; i < M; i++) {
+                const int ii = min(i, m - 1);
+                const int4 *xs = (const int4 *)(xq_qs + (size_t)ii * k + (size_t)b * QK);
+                xa[u][i] = xs[0];
+                xb[u][i] = xs[1];
+                dx[u][i] = xq_d[(size_t)ii * nb + b];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (b0 + j + u * G < nb) {
+                const float dwf = h2f((uint16_t)dw[u]);
+#pragma unroll
+                for (int i = 0; i < M; i++) {
+                    const int s = dot_block(lo[u], hi[u], xa[u][i], xb[u][i]);
+                    acc[i] = fmaf((float)s, dwf * h2f((uint16_t)dx[u][i]), acc[i]);
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < M; i++) {
+        const float s = group_sum<G>(acc[i]);
+        if (row_ok && j == 0 && i < m) y[(size_t)i * n + row] = s;
+    }
+}
+
+// Up to four Q8_0 matrices of equal k stacked along the output rows (e.g. the
+// q/k/v or gate/up projections that read one activation): one launch, one
+// activation quantization per workgroup.
+struct Q8Set {
+    const uint8_t *qlo[4];
+    const uint8_t *qhi[4];
+    const uint16_t *d[4];
+    float *y[4];
+    int row_end[4];  // cumulative row counts; unused slots hold INT_MAX
+};
+
+__device__ __forceinline__ int q8set_index(const Q8Set &S, int r) {
+    return (r >= S.row_end[0]) + (r >= S.row_end[1]) + (r >= S.row_end[2]);
+}
+
+// Fused activation quantization, one activation row (m == 1), k <= 4096*XN/4:
+// the XN float4 of x (and of inv_s) that a thread quantizes are loaded first,
+// then the weights, so the quantization only waits for the (cache-resident)
+// activation; the weights are still in flight while it runs.
+template <int G, int U, int XN>
+__global__ __launch_bounds__(256) void k_gemv_q8_0_fused1(const Q8Set S, const float *__restrict__ x,
+                                                          const float *__restrict__ inv_s, int n_total, int nb,
+                                                          int rounding) {
+    constexpr int RPB = 256 / G;
+    extern __shared__ __align__(16) uint8_t smem[];
+    int8_t *s_qs = (int8_t *)smem;                                      // [nb*32]
+    float *s_d = (float *)(smem + (((size_t)nb * QK + 15) / 16) * 16);  // [nb]
+    const int tid = threadIdx.x;
+    const int j = tid % G;
+    const int grow = blockIdx.x * RPB + tid / G;
+    const bool row_ok = grow < n_total;
+    const int rc = min(grow, n_total - 1);
+    const int mi = q8set_index(S, rc);
+    const int row = rc - (mi ? S.row_end[mi - 1] : 0);
+    const uint8_t *qlo = mi == 0 ? S.qlo[0] : mi == 1 ? S.qlo[1] : mi == 2 ? S.qlo[2] : S.qlo[3];
+    const uint8_t *qhi = mi == 0 ? S.qhi[0] : mi == 1 ? S.qhi[1] : mi == 2 ? S.qhi[2] : S.qhi[3];
+    const uint16_t *wd = mi == 0 ? S.d[0] : mi == 1 ? S.d[1] : mi == 2 ? S.d[2] : S.d[3];
+    const int k4 = nb * (QK / 4);  // float4 count of x
+    const size_t rbase = (size_t)row * nb;
+
+    float4 xv[XN], sv[XN];
+#pragma unroll
+    for (int t = 0; t < XN; t++) {
+        const int f = min(tid + t * 256, k4 - 1);
+        xv[t] = ((const float4 *)x)[f];
+        if (inv_s) sv[t] = ((const float4 *)inv_s)[f];
+    }
     int4 lo[U], hi[U];
     uint32_t dw[U];
 #pragma unroll
@@ -137,71 +239,30 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0(const uint8_t *__restrict__ q
         hi[u] = ld_stream16(qhi + (rbase + b) * 16);
         dw[u] = wd[rbase + b];
     }
-
-    // ---- stage the activation rows in LDS
-    if constexpr (FUSED) {
-        const int total = m * nb;
-        const int sub = tid % 8;
-        for (int base = 0; base < total; base += 32) {  // uniform trip count across the workgroup
-            const int blk = base + tid / 8;
-            const bool valid = blk < total;
-            const int i = valid ? blk / nb : 0;
-            const int b = valid ? blk % nb : 0;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (valid) {
-                v = *(const float4 *)(x + (size_t)i * k + b * QK + sub * 4);
-                if (inv_s) {
-                    const float4 s = *(const float4 *)(inv_s + b * QK + sub * 4);
-                    v.x *= s.x; v.y *= s.y; v.z *= s.z; v.w *= s.w;
-                }
-            }
-            float d;
-            const uint32_t q = quant4(v.x, v.y, v.z, v.w, rounding, d);
-            if (valid) {
-                *(uint32_t *)(s_qs + (size_t)i * k + b * QK + sub * 4) = q;
-                if (sub == 0) s_d[i * nb + b] = h2f(f2h(d));
-            }
+#pragma unroll
+    for (int t = 0; t < XN; t++) {
+        const int f = tid + t * 256;  // float4 index; 8 consecutive threads form one 32-block
+        float4 v = xv[t];
+        if (inv_s) { v.x *= sv[t].x; v.y *= sv[t].y; v.z *= sv[t].z; v.w *= sv[t].w; }
+        float d;
+        const uint32_t q = quant4(v.x, v.y, v.z, v.w, rounding, d);
+        if (f < k4) {
+            *(uint32_t *)(s_qs + (size_t)f * 4) = q;
+            if ((f & 7) == 0) s_d[f >> 3] = h2f(f2h(d));
         }
-    } else {
-        const int qbytes = m * k;
-        for (int off = tid * 16; off < qbytes; off += 256 * 16)
-            *(int4 *)(s_qs + off) = *(const int4 *)(xq_qs + off);
-        for (int i = tid; i < m * nb; i += 256) s_d[i] = h2f(xq_d[i]);
     }
     __syncthreads();
 
-    float acc[M];
-#pragma unroll
-    for (int i = 0; i < M; i++) acc[i] = 0.0f;
-
-    auto consume = [&](int b, const int4 &l4, const int4 &h4, uint32_t dbits) {
-        const float dwf = h2f((uint16_t)dbits);
-#pragma unroll
-        for (int i = 0; i < M; i++) {
-            if (i < m) {
-                const int4 *xs = (const int4 *)(s_qs + (size_t)i * k + b * QK);
-                const int4 x0 = xs[0];
-                const int4 x1 = xs[1];
-                int s = 0;
-                s = __builtin_amdgcn_sdot4(l4.x, x0.x, s, false);
-                s = __builtin_amdgcn_sdot4(l4.y, x0.y, s, false);
-                s = __builtin_amdgcn_sdot4(l4.z, x0.z, s, false);
-                s = __builtin_amdgcn_sdot4(l4.w, x0.w, s, false);
-                s = __builtin_amdgcn_sdot4(h4.x, x1.x, s, false);
-                s = __builtin_amdgcn_sdot4(h4.y, x1.y, s, false);
-                s = __builtin_amdgcn_sdot4(h4.z, x1.z, s, false);
-                s = __builtin_amdgcn_sdot4(h4.w, x1.w, s, false);
-                acc[i] = fmaf((float)s, dwf * s_d[i * nb + b], acc[i]);
-            }
-        }
-    };
-
+    float acc = 0.0f;
 #pragma unroll
     for (int u = 0; u < U; u++) {
         const int b = j + u * G;
-        if (b < nb) consume(b, lo[u], hi[u], dw[u]);
+        if (b < nb) {
+            const int4 *xs = (const int4 *)(s_qs + (size_t)b * QK);
+            const int s = dot_block(lo[u], hi[u], xs[0], xs[1]);
+            acc = fmaf((float)s, h2f((uint16_t)dw[u]) * s_d[b], acc);
+        }
     }
-    // rows longer than U*G blocks: further passes
     for (int b0 = U * G; b0 < nb; b0 += U * G) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
@@ -213,14 +274,17 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0(const uint8_t *__restrict__ q
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int b = b0 + j + u * G;
-            if (b < nb) consume(b, lo[u], hi[u], dw[u]);
+            if (b < nb) {
+                const int4 *xs = (const int4 *)(s_qs + (size_t)b * QK);
+                const int s = dot_block(lo[u], hi[u], xs[0], xs[1]);
+                acc = fmaf((float)s, h2f((uint16_t)dw[u]) * s_d[b], acc);
+            }
         }
     }
-
-#pragma unroll
-    for (int i = 0; i < M; i++) {
-        const float s = group_sum<G>(acc[i]);
-        if (row_ok && j == 0 && i < m) y[(size_t)i * n + row] = s;
+    const float s = group_sum<G>(acc);
+    if (row_ok && j == 0) {
+        float *y = mi == 0 ? S.y[0] : mi == 1 ? S.y[1] : mi == 2 ? S.y[2] : S.y[3];
+        y[row] = s;
     }
 }
 
@@ -248,59 +312,125 @@ __global__ void k_q8_0_block_dots(const uint8_t *__restrict__ qlo, const uint8_t
 
 // ------------------------------------------------------------------ launch helpers
 
-template <int G, int U, int M, bool FUSED>
-int launch_gemv_gu(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
-                   const uint16_t *xq_d, const float *x, const float *inv_s, float *y, int rounding) {
+inline int pick_u(int64_t nb, int g) {
+    int64_t u = (nb + g - 1) / g;
+    if (u > 8) u = (u + 1) / 2 > 8 ? 8 : (u + 1) / 2;  // several passes of U blocks
+    return (int)u;
+}
+
+inline int pick_g(int64_t nb) { return nb <= 128 ? 16 : (nb <= 256 ? 32 : 64); }
+
+template <int G, int U, int M>
+int launch_xq_gu(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
+                 const uint16_t *xq_d, float *y) {
     const Q8Planes p = q8_planes(n, k);
-    const int nb = (int)(k / QK);
     constexpr int RPB = 256 / G;
-    const size_t smem = align_up((size_t)M * k, 16) + (size_t)M * nb * sizeof(float);
-    if (smem > 64 * 1024) {
-        set_error("gemv_q8_0: activation of %d x %lld does not fit in LDS", M, (long long)k);
-        return MI_ERR_UNSUPPORTED;
-    }
-    dim3 grid((unsigned)((n + RPB - 1) / RPB));
-    hipLaunchKernelGGL((k_gemv_q8_0<G, U, M, FUSED>), grid, dim3(256), smem, st, base, base + p.plane,
-                       (const uint16_t *)(base + 2 * p.plane), xq_qs, xq_d, x, inv_s, y, (int)n, nb, (int)m,
-                       rounding);
-    MI_CHECK_LAUNCH("k_gemv_q8_0");
+    hipLaunchKernelGGL((k_gemv_q8_0_xq<G, U, M>), dim3((unsigned)((n + RPB - 1) / RPB)), dim3(256), 0, st, base,
+                       base + p.plane, (const uint16_t *)(base + 2 * p.plane), xq_qs, xq_d, y, (int)n, (int)(k / QK),
+                       (int)m);
+    MI_CHECK_LAUNCH("k_gemv_q8_0_xq");
     return MI_OK;
 }
 
-template <int G, int M, bool FUSED>
-int launch_gemv_g(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
-                  const uint16_t *xq_d, const float *x, const float *inv_s, float *y, int rounding) {
-    const int64_t nb = k / QK;
-    int64_t u = (nb + G - 1) / G;
-    if (u > 8) u = (u + 1) / 2 > 8 ? 8 : (u + 1) / 2;  // several passes of U blocks
-#define MI_U_CASE(UU) \
-    case UU: return launch_gemv_gu<G, UU, M, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
-    switch (u) {
+template <int G, int M>
+int launch_xq_g(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
+                const uint16_t *xq_d, float *y) {
+#define MI_U_CASE(UU) case UU: return launch_xq_gu<G, UU, M>(st, base, n, k, m, xq_qs, xq_d, y);
+    switch (pick_u(k / QK, G)) {
         MI_U_CASE(1) MI_U_CASE(2) MI_U_CASE(3) MI_U_CASE(4) MI_U_CASE(5) MI_U_CASE(6) MI_U_CASE(7) MI_U_CASE(8)
     }
 #undef MI_U_CASE
     return MI_ERR_ARG;
 }
 
-template <int M, bool FUSED>
-int launch_gemv_m(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
-                  const uint16_t *xq_d, const float *x, const float *inv_s, float *y, int rounding) {
-    const int64_t nb = k / QK;
-    // lanes per row: at most 8 blocks per lane per pass, as few lanes per row as that allows
-    if (nb <= 128) return launch_gemv_g<16, M, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
-    if (nb <= 256) return launch_gemv_g<32, M, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
-    return launch_gemv_g<64, M, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
+template <int M>
+int launch_xq_m(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
+                const uint16_t *xq_d, float *y) {
+    switch (pick_g(k / QK)) {
+        case 16: return launch_xq_g<16, M>(st, base, n, k, m, xq_qs, xq_d, y);
+        case 32: return launch_xq_g<32, M>(st, base, n, k, m, xq_qs, xq_d, y);
+        default: return launch_xq_g<64, M>(st, base, n, k, m, xq_qs, xq_d, y);
+    }
 }
 
-template <bool FUSED>
-int launch_gemv(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
-                const uint16_t *xq_d, const float *x, const float *inv_s, float *y, int rounding) {
-    if (m == 1) return launch_gemv_m<1, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
-    if (m == 2) return launch_gemv_m<2, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
-    if (m >= 3 && m <= 4) return launch_gemv_m<4, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
-    if (m >= 5 && m <= 8) return launch_gemv_m<8, FUSED>(st, base, n, k, m, xq_qs, xq_d, x, inv_s, y, rounding);
+int launch_xq(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
+              const uint16_t *xq_d, float *y) {
+    if (m == 1) return launch_xq_m<1>(st, base, n, k, m, xq_qs, xq_d, y);
+    if (m == 2) return launch_xq_m<2>(st, base, n, k, m, xq_qs, xq_d, y);
+    if (m >= 3 && m <= 4) return launch_xq_m<4>(st, base, n, k, m, xq_qs, xq_d, y);
+    if (m >= 5 && m <= 8) return launch_xq_m<8>(st, base, n, k, m, xq_qs, xq_d, y);
     set_error("gemv_q8_0: m=%lld not in 1..8", (long long)m);
     return MI_ERR_ARG;
+}
+
+template <int G, int U, int XN>
+int launch_fused_gux(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *x, const float *inv_s,
+                     int rounding) {
+    constexpr int RPB = 256 / G;
+    const int nb = (int)(k / QK);
+    const size_t smem = align_up((size_t)k, 16) + (size_t)nb * sizeof(float);
+    hipLaunchKernelGGL((k_gemv_q8_0_fused1<G, U, XN>), dim3((unsigned)((n_total + RPB - 1) / RPB)), dim3(256), smem,
+                       st, S, x, inv_s, n_total, nb, rounding);
+    MI_CHECK_LAUNCH("k_gemv_q8_0_fused1");
+    return MI_OK;
+}
+
+template <int G, int XN>
+int launch_fused_gx(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *x, const float *inv_s,
+                    int rounding) {
+#define MI_U_CASE(UU) case UU: return launch_fused_gux<G, UU, XN>(st, S, n_total, k, x, inv_s, rounding);
+    switch (pick_u(k / QK, G)) {
+        MI_U_CASE(1) MI_U_CASE(2) MI_U_CASE(3) MI_U_CASE(4) MI_U_CASE(5) MI_U_CASE(6) MI_U_CASE(7) MI_U_CASE(8)
+    }
+#undef MI_U_CASE
+    return MI_ERR_ARG;
+}
+
+template <int XN>
+int launch_fused_x(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *x, const float *inv_s,
+                   int rounding) {
+    switch (pick_g(k / QK)) {
+        case 16: return launch_fused_gx<16, XN>(st, S, n_total, k, x, inv_s, rounding);
+        case 32: return launch_fused_gx<32, XN>(st, S, n_total, k, x, inv_s, rounding);
+        default: return launch_fused_gx<64, XN>(st, S, n_total, k, x, inv_s, rounding);
+    }
+}
+
+// one activation row with k <= 4096 (16 floats per thread): single fused launch
+int launch_fused(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *x, const float *inv_s,
+                 int rounding) {
+    const int64_t xn = (k / 4 + 255) / 256;
+    if (xn <= 1) return launch_fused_x<1>(st, S, n_total, k, x, inv_s, rounding);
+    if (xn <= 2) return launch_fused_x<2>(st, S, n_total, k, x, inv_s, rounding);
+    return launch_fused_x<4>(st, S, n_total, k, x, inv_s, rounding);
+}
+
+int make_set(Q8Set &S, int count, const void *const *w, const int64_t *n, float *const *y, int64_t k, int &n_total) {
+    MI_CHECK_ARG(count >= 1 && count <= 4, "mul_mat_q8_0: %d matrices (1..4 supported)", count);
+    int64_t acc = 0;
+    for (int i = 0; i < 4; i++) {
+        if (i < count) {
+            MI_CHECK_ARG(w[i] && y[i] && n[i] > 0, "mul_mat_q8_0: bad matrix %d", i);
+            MI_CHECK_ARG(mi::aligned(w[i], 256), "mul_mat_q8_0: packed weight %d not 256-byte aligned", i);
+            const Q8Planes p = q8_planes(n[i], k);
+            const uint8_t *base = (const uint8_t *)w[i];
+            S.qlo[i] = base;
+            S.qhi[i] = base + p.plane;
+            S.d[i] = (const uint16_t *)(base + 2 * p.plane);
+            S.y[i] = y[i];
+            acc += n[i];
+            S.row_end[i] = (int)acc;
+        } else {
+            S.qlo[i] = S.qlo[0];
+            S.qhi[i] = S.qhi[0];
+            S.d[i] = S.d[0];
+            S.y[i] = S.y[0];
+            S.row_end[i] = INT_MAX;
+        }
+    }
+    MI_CHECK_ARG(acc < (1ll << 31), "mul_mat_q8_0: too many rows");
+    n_total = (int)acc;
+    return MI_OK;
 }
 
 int check_shape(const char *what, int64_t n, int64_t k) {
@@ -381,18 +511,53 @@ int mi_gemv_q8_0(void *stream, const void *w_packed, const void *xq, float *y, i
     MI_CHECK_ARG(w_packed && xq && y, "gemv_q8_0: null pointer");
     MI_CHECK_ARG(mi::aligned(w_packed, 256) && mi::aligned(xq, 16), "gemv_q8_0: w_packed must be 256-byte, xq 16-byte aligned");
     const uint8_t *xb = (const uint8_t *)xq;
-    return launch_gemv<false>((hipStream_t)stream, (const uint8_t *)w_packed, n, k, m, (const int8_t *)xb,
-                              (const uint16_t *)(xb + mi_xq_d_offset(m, k)), nullptr, nullptr, y, 0);
+    return launch_xq((hipStream_t)stream, (const uint8_t *)w_packed, n, k, m, (const int8_t *)xb,
+                     (const uint16_t *)(xb + mi_xq_d_offset(m, k)), y);
+}
+
+size_t mi_mul_mat_q8_0_workspace_size(int64_t m, int64_t k) {
+    if (m == 1 && k <= 4096) return 0;
+    return mi_xq_size(m, k);
+}
+
+int mi_mul_mat_q8_0_f32_multi(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
+                              float *const *y, int64_t k, const float *x, const float *inv_s, int rounding, void *ws,
+                              size_t ws_bytes) {
+    MI_CHECK_ARG(w_packed && n && y && x, "mul_mat_q8_0_f32_multi: null pointer");
+    if (int r = check_shape("mul_mat_q8_0_f32_multi", 1, k)) return r;
+    MI_CHECK_ARG(mi::aligned(x, 16) && (!inv_s || mi::aligned(inv_s, 16)),
+                 "mul_mat_q8_0_f32_multi: x/inv_s must be 16-byte aligned");
+    Q8Set S;
+    int n_total = 0;
+    if (int r = make_set(S, n_mats, w_packed, n, y, k, n_total)) return r;
+    hipStream_t st = (hipStream_t)stream;
+    if (k <= 4096) return launch_fused(st, S, n_total, k, x, inv_s, rounding);
+    const size_t need = mi_xq_size(1, k);
+    if (!ws || ws_bytes < need || !mi::aligned(ws, 16)) {
+        mi::set_error("mul_mat_q8_0_f32_multi: workspace %zu < %zu bytes (or misaligned)", ws_bytes, need);
+        return MI_ERR_WORKSPACE;
+    }
+    if (int r = mi_act_quant_q8_0(stream, x, inv_s, 1, k, ws, rounding)) return r;
+    for (int i = 0; i < n_mats; i++)
+        if (int r = mi_gemv_q8_0(stream, w_packed[i], ws, y[i], n[i], k, 1)) return r;
+    return MI_OK;
 }
 
 int mi_mul_mat_q8_0_f32(void *stream, const void *w_packed, const float *x, const float *inv_s, float *y,
-                        int64_t n, int64_t k, int64_t m, int rounding) {
+                        int64_t n, int64_t k, int64_t m, int rounding, void *ws, size_t ws_bytes) {
     if (int r = check_shape("mul_mat_q8_0_f32", n, k)) return r;
     MI_CHECK_ARG(w_packed && x && y, "mul_mat_q8_0_f32: null pointer");
+    MI_CHECK_ARG(m >= 1 && m <= 8, "mul_mat_q8_0_f32: m=%lld not in 1..8", (long long)m);
     MI_CHECK_ARG(mi::aligned(w_packed, 256) && mi::aligned(x, 16) && (!inv_s || mi::aligned(inv_s, 16)),
                  "mul_mat_q8_0_f32: w_packed must be 256-byte, x/inv_s 16-byte aligned");
-    return launch_gemv<true>((hipStream_t)stream, (const uint8_t *)w_packed, n, k, m, nullptr, nullptr, x, inv_s, y,
-                             rounding);
+    if (m == 1) return mi_mul_mat_q8_0_f32_multi(stream, 1, &w_packed, &n, &y, k, x, inv_s, rounding, ws, ws_bytes);
+    const size_t need = mi_xq_size(m, k);
+    if (!ws || ws_bytes < need || !mi::aligned(ws, 16)) {
+        mi::set_error("mul_mat_q8_0_f32: workspace %zu < %zu bytes (or misaligned)", ws_bytes, need);
+        return MI_ERR_WORKSPACE;
+    }
+    if (int r = mi_act_quant_q8_0(stream, x, inv_s, m, k, ws, rounding)) return r;
+    return mi_gemv_q8_0(stream, w_packed, ws, y, n, k, m);
 }
 
 int mi_q8_0_block_dots(void *stream, const void *w_packed, const void *xq, int32_t *out, int64_t n, int64_t k) {

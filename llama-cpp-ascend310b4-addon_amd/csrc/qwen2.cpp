@@ -1,0 +1,305 @@
+// qwen2.cpp -- minimal Qwen2 decode driver over the ggml backend API (see mi_qwen2.h).
+//
+// Graph per token, following llama.cpp's Qwen2 builder: GET_ROWS(token_embd) ->
+// 28 x [RMS_NORM, MUL, q/k/v MUL_MAT (+bias ADD), ROPE neox, SET_ROWS K/V into the
+// fp16 cache, FLASH_ATTN_EXT (+kv_lengths src[5]), MUL_MAT o, ADD residual,
+// RMS_NORM, MUL, gate/up MUL_MAT, GLU swiglu, MUL_MAT down, ADD residual] ->
+// RMS_NORM, MUL, MUL_MAT(tied token_embd) -> ARGMAX.  The KV view handed to the
+// attention covers the used cache rounded up to 256 positions (as llama.cpp's
+// KV view is), so one graph serves 256 consecutive positions and the backend
+// replays it as a captured HIP graph.
+#include "mi_qwen2.h"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <chrono>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "ggml-backend.h"
+#include "ggml-mi355x.h"
+#include "ggml.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return -1;
+}
+
+struct Graph {
+    ggml_context *ctx = nullptr;
+    ggml_cgraph *gf = nullptr;
+    ggml_gallocr_t galloc = nullptr;
+    ggml_tensor *logits = nullptr;
+    ggml_tensor *argmax = nullptr;
+};
+
+}  // namespace
+
+struct mi_qwen2 {
+    mi_qwen2_hparams hp;
+    ggml_backend_t backend = nullptr;
+    ggml_context *wctx = nullptr;
+    ggml_backend_buffer_t wbuf = nullptr;
+    std::map<std::string, ggml_tensor *> tensors;
+    std::vector<ggml_tensor *> k_cache, v_cache;
+    ggml_tensor *inp = nullptr;  // I32 [4]: token, position, kv length, cache row
+    int32_t inp_host[4] = {0, 0, 0, 0};
+    std::map<int, Graph> graphs;  // by KV view length
+};
+
+namespace {
+
+ggml_tensor *W(mi_qwen2 *m, const std::string &name) {
+    auto it = m->tensors.find(name);
+    if (it == m->tensors.end()) GGML_ABORT("qwen2: missing tensor %s", name.c_str());
+    return it->second;
+}
+
+ggml_tensor *add_tensor(mi_qwen2 *m, const std::string &name, ggml_type type, int64_t ne0, int64_t ne1 = 1) {
+    ggml_tensor *t = ne1 == 1 ? ggml_new_tensor_1d(m->wctx, type, ne0) : ggml_new_tensor_2d(m->wctx, type, ne0, ne1);
+    ggml_set_name(t, name.c_str());
+    m->tensors[name] = t;
+    return t;
+}
+
+Graph build_graph(mi_qwen2 *m, int n_kv) {
+    const mi_qwen2_hparams &hp = m->hp;
+    const int hd = hp.head_dim, n_embd_kv = hp.n_head_kv * hd;
+    Graph G;
+    ggml_init_params ip = {0, nullptr, true};
+    G.ctx = ggml_init(ip);
+    ggml_context *ctx = G.ctx;
+    ggml_cgraph *gf = ggml_new_graph_custom(ctx, 16384, false);
+    G.gf = gf;
+
+    ggml_tensor *tok = ggml_view_1d(ctx, m->inp, 1, 0);
+    ggml_tensor *pos = ggml_view_1d(ctx, m->inp, 1, 4);
+    ggml_tensor *kvl = ggml_view_1d(ctx, m->inp, 1, 8);
+    ggml_tensor *kidx = ggml_view_1d(ctx, m->inp, 1, 12);
+    ggml_tensor *tok_embd = W(m, "token_embd.weight");
+
+    ggml_tensor *inpL = ggml_get_rows(ctx, tok_embd, tok);
+    const float kq_scale = 1.0f / sqrtf((float)hd);
+    for (int il = 0; il < hp.n_layer; il++) {
+        const std::string p = "blk." + std::to_string(il) + ".";
+        ggml_tensor *cur = ggml_rms_norm(ctx, inpL, hp.rms_eps);
+        cur = ggml_mul(ctx, cur, W(m, p + "attn_norm.weight"));
+        ggml_tensor *Q = ggml_mul_mat(ctx, W(m, p + "attn_q.weight"), cur);
+        ggml_tensor *K = ggml_mul_mat(ctx, W(m, p + "attn_k.weight"), cur);
+        ggml_tensor *V = ggml_mul_mat(ctx, W(m, p + "attn_v.weight"), cur);
+        ggml_build_forward_expand(gf, Q);  // q/k/v projections adjacent in node order
+        ggml_build_forward_expand(gf, K);
+        ggml_build_forward_expand(gf, V);
+        if (hp.use_bias) {
+            Q = ggml_add(ctx, Q, W(m, p + "attn_q.bias"));
+            K = ggml_add(ctx, K, W(m, p + "attn_k.bias"));
+            V = ggml_add(ctx, V, W(m, p + "attn_v.bias"));
+        }
+        Q = ggml_reshape_3d(ctx, Q, hd, hp.n_head, 1);
+        K = ggml_reshape_3d(ctx, K, hd, hp.n_head_kv, 1);
+        Q = ggml_rope_ext(ctx, Q, pos, nullptr, hd, GGML_ROPE_TYPE_NEOX, 0, hp.rope_theta, 1.0f, 0.0f, 1.0f, 0.0f,
+                          0.0f);
+        K = ggml_rope_ext(ctx, K, pos, nullptr, hd, GGML_ROPE_TYPE_NEOX, 0, hp.rope_theta, 1.0f, 0.0f, 1.0f, 0.0f,
+                          0.0f);
+        ggml_tensor *kc = m->k_cache[il], *vc = m->v_cache[il];
+        ggml_build_forward_expand(gf, ggml_set_rows(ctx, kc, ggml_reshape_2d(ctx, K, n_embd_kv, 1), kidx));
+        ggml_build_forward_expand(gf, ggml_set_rows(ctx, vc, V, kidx));
+        ggml_tensor *k = ggml_view_3d(ctx, kc, hd, n_kv, hp.n_head_kv, kc->nb[1], ggml_row_size(GGML_TYPE_F16, hd), 0);
+        ggml_tensor *v = ggml_view_3d(ctx, vc, hd, n_kv, hp.n_head_kv, vc->nb[1], ggml_row_size(GGML_TYPE_F16, hd), 0);
+        ggml_tensor *q = ggml_permute(ctx, Q, 0, 2, 1, 3);
+        ggml_tensor *att = ggml_flash_attn_ext(ctx, q, k, v, nullptr, kq_scale, 0.0f, 0.0f);
+        ggml_flash_attn_ext_add_kv_lengths(att, kvl);
+        ggml_flash_attn_ext_set_prec(att, GGML_PREC_F32);
+        cur = ggml_reshape_2d(ctx, att, hd * hp.n_head, 1);
+        cur = ggml_mul_mat(ctx, W(m, p + "attn_output.weight"), cur);
+        ggml_tensor *ffn_inp = ggml_add(ctx, cur, inpL);
+        cur = ggml_rms_norm(ctx, ffn_inp, hp.rms_eps);
+        cur = ggml_mul(ctx, cur, W(m, p + "ffn_norm.weight"));
+        ggml_tensor *g = ggml_mul_mat(ctx, W(m, p + "ffn_gate.weight"), cur);
+        ggml_tensor *u = ggml_mul_mat(ctx, W(m, p + "ffn_up.weight"), cur);
+        ggml_build_forward_expand(gf, g);  // gate/up adjacent
+        ggml_build_forward_expand(gf, u);
+        cur = ggml_swiglu_split(ctx, g, u);
+        cur = ggml_mul_mat(ctx, W(m, p + "ffn_down.weight"), cur);
+        inpL = ggml_add(ctx, cur, ffn_inp);
+    }
+    ggml_tensor *cur = ggml_rms_norm(ctx, inpL, hp.rms_eps);
+    cur = ggml_mul(ctx, cur, W(m, "output_norm.weight"));
+    G.logits = ggml_mul_mat(ctx, tok_embd, cur);  // tied output head
+    G.argmax = ggml_argmax(ctx, G.logits);
+    ggml_build_forward_expand(gf, G.argmax);
+
+    G.galloc = ggml_gallocr_new(ggml_backend_get_default_buffer_type(m->backend));
+    if (!ggml_gallocr_alloc_graph(G.galloc, gf)) GGML_ABORT("qwen2: graph allocation failed");
+    // every node must run on the backend (there is no CPU fallback in this driver)
+    for (int i = 0; i < ggml_graph_n_nodes(gf); i++) {
+        ggml_tensor *n = ggml_graph_node(gf, i);
+        if (!ggml_backend_supports_op(m->backend, n))
+            GGML_ABORT("qwen2: backend does not support node %s (%s)", n->name, ggml_op_name(n->op));
+    }
+    return G;
+}
+
+Graph &graph_for(mi_qwen2 *m, int32_t kv_len) {
+    int n_kv = (kv_len + 255) / 256 * 256;
+    if (n_kv > m->hp.n_ctx) n_kv = m->hp.n_ctx;
+    auto it = m->graphs.find(n_kv);
+    if (it != m->graphs.end()) return it->second;
+    return m->graphs.emplace(n_kv, build_graph(m, n_kv)).first->second;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *mi_qwen2_last_error(void) { return g_err; }
+
+mi_qwen2 *mi_qwen2_create(const mi_qwen2_hparams *hp, int device) {
+    if (!hp || hp->n_layer <= 0 || hp->n_embd <= 0 || hp->n_head <= 0 || hp->n_head_kv <= 0 ||
+        hp->n_head % hp->n_head_kv != 0 || hp->head_dim * hp->n_head != hp->n_embd || hp->n_ctx <= 0 ||
+        (hp->wtype != GGML_TYPE_Q8_0 && hp->wtype != GGML_TYPE_Q4_0)) {
+        fail("qwen2: invalid hyper-parameters");
+        return nullptr;
+    }
+    mi_qwen2 *m = new mi_qwen2();
+    m->hp = *hp;
+    m->backend = ggml_backend_mi355x_init(device);
+    if (!m->backend) {
+        delete m;
+        fail("qwen2: no MI355X device %d", device);
+        return nullptr;
+    }
+    ggml_init_params ip = {0, nullptr, true};
+    m->wctx = ggml_init(ip);
+    const ggml_type wt = (ggml_type)hp->wtype;
+    const int n_embd_kv = hp->n_head_kv * hp->head_dim;
+    add_tensor(m, "token_embd.weight", GGML_TYPE_F16, hp->n_embd, hp->n_vocab);
+    add_tensor(m, "output_norm.weight", GGML_TYPE_F32, hp->n_embd);
+    for (int il = 0; il < hp->n_layer; il++) {
+        const std::string p = "blk." + std::to_string(il) + ".";
+        add_tensor(m, p + "attn_norm.weight", GGML_TYPE_F32, hp->n_embd);
+        add_tensor(m, p + "attn_q.weight", wt, hp->n_embd, hp->n_embd);
+        add_tensor(m, p + "attn_k.weight", wt, hp->n_embd, n_embd_kv);
+        add_tensor(m, p + "attn_v.weight", wt, hp->n_embd, n_embd_kv);
+        if (hp->use_bias) {
+            add_tensor(m, p + "attn_q.bias", GGML_TYPE_F32, hp->n_embd);
+            add_tensor(m, p + "attn_k.bias", GGML_TYPE_F32, n_embd_kv);
+            add_tensor(m, p + "attn_v.bias", GGML_TYPE_F32, n_embd_kv);
+        }
+        add_tensor(m, p + "attn_output.weight", wt, hp->n_embd, hp->n_embd);
+        add_tensor(m, p + "ffn_norm.weight", GGML_TYPE_F32, hp->n_embd);
+        add_tensor(m, p + "ffn_gate.weight", wt, hp->n_embd, hp->n_ff);
+        add_tensor(m, p + "ffn_up.weight", wt, hp->n_embd, hp->n_ff);
+        add_tensor(m, p + "ffn_down.weight", wt, hp->n_ff, hp->n_embd);
+        ggml_tensor *kc = ggml_new_tensor_2d(m->wctx, GGML_TYPE_F16, n_embd_kv, hp->n_ctx);
+        ggml_tensor *vc = ggml_new_tensor_2d(m->wctx, GGML_TYPE_F16, n_embd_kv, hp->n_ctx);
+        ggml_set_name(kc, ("cache_k_l" + std::to_string(il)).c_str());
+        ggml_set_name(vc, ("cache_v_l" + std::to_string(il)).c_str());
+        m->k_cache.push_back(kc);
+        m->v_cache.push_back(vc);
+    }
+    m->inp = ggml_new_tensor_1d(m->wctx, GGML_TYPE_I32, 4);
+    ggml_set_name(m->inp, "inp_decode");
+    ggml_set_input(m->inp);
+    m->wbuf = ggml_backend_alloc_ctx_tensors_from_buft(m->wctx, ggml_backend_mi355x_buffer_type(device));
+    if (!m->wbuf) {
+        mi_qwen2_free(m);
+        fail("qwen2: weight buffer allocation failed");
+        return nullptr;
+    }
+    ggml_backend_buffer_set_usage(m->wbuf, GGML_BACKEND_BUFFER_USAGE_WEIGHTS);
+    mi_qwen2_reset(m);
+    return m;
+}
+
+void mi_qwen2_free(mi_qwen2 *m) {
+    if (!m) return;
+    for (auto &kv : m->graphs) {
+        ggml_gallocr_free(kv.second.galloc);
+        ggml_free(kv.second.ctx);
+    }
+    ggml_backend_buffer_free(m->wbuf);
+    ggml_free(m->wctx);
+    ggml_backend_free(m->backend);
+    delete m;
+}
+
+int mi_qwen2_reset(mi_qwen2 *m) {
+    for (size_t i = 0; i < m->k_cache.size(); i++) {
+        ggml_backend_tensor_memset(m->k_cache[i], 0, 0, ggml_nbytes(m->k_cache[i]));
+        ggml_backend_tensor_memset(m->v_cache[i], 0, 0, ggml_nbytes(m->v_cache[i]));
+    }
+    return 0;
+}
+
+int64_t mi_qwen2_tensor_nbytes(mi_qwen2 *m, const char *name, int64_t *dims) {
+    auto it = m->tensors.find(name);
+    if (it == m->tensors.end()) return -1;
+    if (dims) {
+        dims[0] = it->second->ne[0];
+        dims[1] = it->second->ne[1];
+    }
+    return (int64_t)ggml_nbytes(it->second);
+}
+
+int mi_qwen2_set_tensor(mi_qwen2 *m, const char *name, const void *data, size_t size) {
+    auto it = m->tensors.find(name);
+    if (it == m->tensors.end()) return fail("qwen2: unknown tensor %s", name);
+    if (size != ggml_nbytes(it->second))
+        return fail("qwen2: %s expects %zu bytes, got %zu", name, ggml_nbytes(it->second), size);
+    ggml_backend_tensor_set(it->second, data, 0, size);
+    return 0;
+}
+
+int mi_qwen2_set_smooth(mi_qwen2 *m, const char *weight_name, const float *s, int64_t n) {
+    auto it = m->tensors.find(weight_name);
+    if (it == m->tensors.end()) return fail("qwen2: unknown tensor %s", weight_name);
+    if (!ggml_backend_mi355x_set_smooth_factors(it->second, s, n))
+        return fail("qwen2: %s takes no SmoothQuant factors of length %lld", weight_name, (long long)n);
+    return 0;
+}
+
+int mi_qwen2_decode(mi_qwen2 *m, int32_t token, int32_t pos, int32_t *next_token, float *logits) {
+    if (pos < 0 || pos >= m->hp.n_ctx) return fail("qwen2: position %d outside the cache (%d)", pos, m->hp.n_ctx);
+    if (token < 0 || token >= m->hp.n_vocab) return fail("qwen2: token %d outside the vocabulary", token);
+    Graph &G = graph_for(m, pos + 1);
+    m->inp_host[0] = token;
+    m->inp_host[1] = pos;
+    m->inp_host[2] = pos + 1;
+    m->inp_host[3] = pos;
+    ggml_backend_tensor_set(m->inp, m->inp_host, 0, sizeof(m->inp_host));
+    if (ggml_backend_graph_compute(m->backend, G.gf) != GGML_STATUS_SUCCESS) return fail("qwen2: graph failed");
+    if (next_token) ggml_backend_tensor_get(G.argmax, next_token, 0, sizeof(int32_t));
+    if (logits) ggml_backend_tensor_get(G.logits, logits, 0, ggml_nbytes(G.logits));
+    return 0;
+}
+
+int mi_qwen2_generate(mi_qwen2 *m, const int32_t *prompt, int32_t n_prompt, int32_t n_gen, int32_t *out_tokens,
+                      double *gen_seconds) {
+    if (n_prompt < 1 || n_gen < 0 || n_prompt + n_gen > m->hp.n_ctx) return fail("qwen2: bad prompt/generation size");
+    int32_t next = 0;
+    for (int32_t i = 0; i < n_prompt; i++)
+        if (mi_qwen2_decode(m, prompt[i], i, &next, nullptr)) return -1;
+    // n_gen timed decode steps; the first one consumes the prompt's greedy continuation
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int32_t i = 0; i < n_gen; i++) {
+        if (mi_qwen2_decode(m, next, n_prompt + i, &next, nullptr)) return -1;
+        out_tokens[i] = next;
+    }
+    const auto t1 = std::chrono::steady_clock::now();
+    if (gen_seconds) *gen_seconds = std::chrono::duration<double>(t1 - t0).count();
+    return 0;
+}
+
+}  // extern "C"

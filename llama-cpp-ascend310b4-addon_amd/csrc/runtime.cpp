@@ -138,4 +138,30 @@ int mi_event_elapsed_ms(float *ms, void *start, void *stop) {
     return MI_OK;
 }
 
+int mi_graph_capture_begin(void *stream) {
+    HIP_RET(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    return MI_OK;
+}
+
+int mi_graph_capture_end(void *stream, void **graph_exec) {
+    hipGraph_t g = nullptr;
+    HIP_RET(hipStreamEndCapture((hipStream_t)stream, &g), "hipStreamEndCapture");
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    *graph_exec = (void *)ge;
+    return MI_OK;
+}
+
+int mi_graph_launch(void *graph_exec, void *stream) {
+    HIP_RET(hipGraphLaunch((hipGraphExec_t)graph_exec, (hipStream_t)stream), "hipGraphLaunch");
+    return MI_OK;
+}
+
+int mi_graph_destroy(void *graph_exec) {
+    HIP_RET(hipGraphExecDestroy((hipGraphExec_t)graph_exec), "hipGraphExecDestroy");
+    return MI_OK;
+}
+
 }  // extern "C"

@@ -58,6 +58,10 @@ _SIGS = {
     "mi_event_destroy": (_I, [_P]),
     "mi_event_record": (_I, [_P, _P]),
     "mi_event_elapsed_ms": (_I, [ctypes.POINTER(_F), _P, _P]),
+    "mi_graph_capture_begin": (_I, [_P]),
+    "mi_graph_capture_end": (_I, [_P, ctypes.POINTER(_P)]),
+    "mi_graph_launch": (_I, [_P, _P]),
+    "mi_graph_destroy": (_I, [_P]),
     "mi_q8_0_packed_size": (_SZ, [_I64, _I64]),
     "mi_q4_0_packed_size": (_SZ, [_I64, _I64]),
     "mi_prepack_q8_0": (_I, [_P, _P, _P, _I64, _I64]),
@@ -70,7 +74,8 @@ _SIGS = {
     "mi_xq_d_offset": (_SZ, [_I64, _I64]),
     "mi_act_quant_q8_0": (_I, [_P, _P, _P, _I64, _I64, _P, _I]),
     "mi_gemv_q8_0": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
-    "mi_mul_mat_q8_0_f32": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I]),
+    "mi_mul_mat_q8_0_workspace_size": (_SZ, [_I64, _I64]),
+    "mi_mul_mat_q8_0_f32": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ]),
     "mi_q8_0_block_dots": (_I, [_P, _P, _P, _P, _I64, _I64]),
     "mi_gemv_q4_0_f16": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
     "mi_mul_mat_q4_0_f32": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
@@ -78,6 +83,16 @@ _SIGS = {
     "mi_fa_decode_workspace_size": (_SZ, [_I64, _I64, _I64, _I64]),
     "mi_fa_decode": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _SZ, _SZ, _SZ, _SZ, _F, _P, _P, _SZ]),
     "mi_kv_lengths": (_I, [_P, _P, _I, _I64, _I64, _P]),
+    "mi_mul_mat_q8_0_f32_multi": (_I, [_P, _I, _P, _P, _P, _I64, _P, _P, _I, _P, _SZ]),
+    "mi_rms_norm": (_I, [_P, _P, _P, _P, _I64, _I64, _F]),
+    "mi_add_bcast": (_I, [_P, _P, _P, _P, _I64, _I64]),
+    "mi_mul_bcast": (_I, [_P, _P, _P, _P, _I64, _I64]),
+    "mi_rope_neox": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _F, _F, _SZ, _SZ, _SZ, _SZ]),
+    "mi_set_rows_f16": (_I, [_P, _P, _P, _I, _P, _I64, _I64, _SZ, _SZ, _I64]),
+    "mi_get_rows": (_I, [_P, _P, _I, _P, _P, _I64, _I64, _SZ, _I64]),
+    "mi_swiglu": (_I, [_P, _P, _P, _P, _I64]),
+    "mi_argmax": (_I, [_P, _P, _P, _I64, _I64]),
+    "mi_fill_mask_f16": (_I, [_P, _P, _P, _I64]),
 }
 
 # every symbol the C ABI header declares (checked by the CPU tests)
@@ -206,6 +221,36 @@ def device_sync():
     _call("mi_device_sync")
 
 
+class Graph:
+    """Captures every launch issued on `stream` inside the with-block into a HIP graph."""
+
+    def __init__(self, stream):
+        assert stream is not None and stream.ptr, "graph capture needs a created (non-null) stream"
+        self.stream = stream
+        self.exec = None
+
+    def __enter__(self):
+        _call("mi_graph_capture_begin", _P(self.stream.ptr))
+        return self
+
+    def __exit__(self, et, ev, tb):
+        p = _P()
+        r = lib().mi_graph_capture_end(_P(self.stream.ptr), ctypes.byref(p))
+        if et is None:
+            if r != MI_OK:
+                raise MiError("mi_graph_capture_end", r, last_error())
+            self.exec = p.value
+        return False
+
+    def launch(self):
+        _call("mi_graph_launch", _P(self.exec), _P(self.stream.ptr))
+
+    def destroy(self):
+        if self.exec:
+            lib().mi_graph_destroy(_P(self.exec))
+            self.exec = None
+
+
 # ---------------------------------------------------------------- prepack
 
 def q8_0_packed_size(n, k):
@@ -270,8 +315,13 @@ def gemv_q8_0(w_packed, xq, y, n, k, m=1, stream=None):
     _call("mi_gemv_q8_0", _P(stream), _P(w_packed), _P(xq), _P(y), n, k, m)
 
 
-def mul_mat_q8_0_f32(w_packed, x, inv_s, y, n, k, m=1, rounding=Q8_ROUND_X86, stream=None):
-    _call("mi_mul_mat_q8_0_f32", _P(stream), _P(w_packed), _P(x), _P(inv_s), _P(y), n, k, m, rounding)
+def mul_mat_q8_0_workspace_size(m, k):
+    return lib().mi_mul_mat_q8_0_workspace_size(m, k)
+
+
+def mul_mat_q8_0_f32(w_packed, x, inv_s, y, n, k, m=1, rounding=Q8_ROUND_X86, ws=None, ws_bytes=0, stream=None):
+    _call("mi_mul_mat_q8_0_f32", _P(stream), _P(w_packed), _P(x), _P(inv_s), _P(y), n, k, m, rounding, _P(ws),
+          ws_bytes)
 
 
 def q8_0_block_dots(w_packed, xq, out, n, k, stream=None):
@@ -302,3 +352,100 @@ def fa_decode(q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1, k_nb
 
 def kv_lengths(mask, is_f16, n_kv, n_rows, out, stream=None):
     _call("mi_kv_lengths", _P(stream), _P(mask), 1 if is_f16 else 0, n_kv, n_rows, _P(out))
+
+
+# ---------------------------------------------------------------- Qwen2 decode driver (mi_qwen2.h)
+
+class _QwenHP(ctypes.Structure):
+    _fields_ = [("n_layer", ctypes.c_int32), ("n_embd", ctypes.c_int32), ("n_head", ctypes.c_int32),
+                ("n_head_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("n_ff", ctypes.c_int32),
+                ("n_vocab", ctypes.c_int32), ("n_ctx", ctypes.c_int32), ("rms_eps", ctypes.c_float),
+                ("rope_theta", ctypes.c_float), ("wtype", ctypes.c_int32), ("use_bias", ctypes.c_int32)]
+
+
+_QWEN_SIGS = {
+    "mi_qwen2_create": (_P, [ctypes.POINTER(_QwenHP), _I]),
+    "mi_qwen2_free": (None, [_P]),
+    "mi_qwen2_last_error": (ctypes.c_char_p, []),
+    "mi_qwen2_set_tensor": (_I, [_P, ctypes.c_char_p, _P, _SZ]),
+    "mi_qwen2_set_smooth": (_I, [_P, ctypes.c_char_p, _P, _I64]),
+    "mi_qwen2_tensor_nbytes": (_I64, [_P, ctypes.c_char_p, _P]),
+    "mi_qwen2_decode": (_I, [_P, ctypes.c_int32, ctypes.c_int32, _P, _P]),
+    "mi_qwen2_generate": (_I, [_P, _P, ctypes.c_int32, ctypes.c_int32, _P, ctypes.POINTER(ctypes.c_double)]),
+    "mi_qwen2_reset": (_I, [_P]),
+}
+EXPORTED = EXPORTED + tuple(_QWEN_SIGS)
+
+
+def _qlib():
+    L = lib()
+    if not getattr(L, "_qwen_declared", False):
+        for name, (res, args) in _QWEN_SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        L._qwen_declared = True
+    return L
+
+
+class Qwen2Model:
+    """A Qwen2 model run through the ggml backend (ggml_backend_mi355x) one token per step."""
+
+    def __init__(self, hp, device=0):
+        L = _qlib()
+        h = _QwenHP()
+        for f, _ in _QwenHP._fields_:
+            setattr(h, f, hp[f])
+        self.hp = dict(hp)
+        self.ptr = L.mi_qwen2_create(ctypes.byref(h), device)
+        if not self.ptr:
+            raise MiError("mi_qwen2_create", -1, L.mi_qwen2_last_error().decode())
+        self.logits = np.empty(hp["n_vocab"], np.float32)
+
+    def _chk(self, name, r):
+        if r != 0:
+            raise MiError(name, r, _qlib().mi_qwen2_last_error().decode())
+
+    def set_tensor(self, name, arr):
+        arr = np.ascontiguousarray(arr)
+        self._chk("mi_qwen2_set_tensor", _qlib().mi_qwen2_set_tensor(self.ptr, name.encode(), arr.ctypes.data,
+                                                                    arr.nbytes))
+
+    def set_smooth(self, weight_name, s):
+        s = np.ascontiguousarray(s, np.float32)
+        self._chk("mi_qwen2_set_smooth", _qlib().mi_qwen2_set_smooth(self.ptr, weight_name.encode(), s.ctypes.data,
+                                                                    s.size))
+
+    def load(self, tensors, smooth=None):
+        for name, arr in tensors.items():
+            self.set_tensor(name, arr)
+        for name, s in (smooth or {}).items():
+            self.set_smooth(name, s)
+
+    def decode(self, token, pos, want_logits=False):
+        nxt = ctypes.c_int32(0)
+        self._chk("mi_qwen2_decode", _qlib().mi_qwen2_decode(self.ptr, int(token), int(pos), ctypes.byref(nxt),
+                                                             self.logits.ctypes.data if want_logits else None))
+        return (nxt.value, self.logits.copy()) if want_logits else nxt.value
+
+    def generate(self, prompt, n_gen):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(max(n_gen, 1), np.int32)
+        secs = ctypes.c_double(0.0)
+        self._chk("mi_qwen2_generate", _qlib().mi_qwen2_generate(self.ptr, prompt.ctypes.data, prompt.size, n_gen,
+                                                                 out.ctypes.data, ctypes.byref(secs)))
+        return out[:n_gen], secs.value
+
+    def reset(self):
+        self._chk("mi_qwen2_reset", _qlib().mi_qwen2_reset(self.ptr))
+
+    def free(self):
+        if self.ptr:
+            _qlib().mi_qwen2_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

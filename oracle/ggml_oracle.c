@@ -459,9 +459,14 @@ static float dot_q8_0_vnni(int64_t nb, const orc_block_q8_0 *x, const orc_block_
 
 void orc_mul_mat_q8_0_mt(const orc_block_q8_0 *w, const float *x, const float *inv_s, float *y,
                          int64_t n_rows, int64_t k, int n_threads) {
+    orc_mul_mat_q8_0_mt_variant(w, x, inv_s, y, n_rows, k, n_threads, ORC_Q8_ROUND_X86);
+}
+
+void orc_mul_mat_q8_0_mt_variant(const orc_block_q8_0 *w, const float *x, const float *inv_s, float *y,
+                                 int64_t n_rows, int64_t k, int n_threads, int variant) {
     const int64_t nb = k / ORC_QK8_0;
     orc_block_q8_0 *xq = (orc_block_q8_0 *)malloc((size_t)nb * sizeof(orc_block_q8_0));
-    orc_quantize_row_q8_0(x, inv_s, xq, k, ORC_Q8_ROUND_X86);
+    orc_quantize_row_q8_0(x, inv_s, xq, k, variant);
     const int vnni = cpu_has_vnni();
     const int avx2 = cpu_has_avx2();
 #pragma omp parallel for num_threads(n_threads) schedule(static)

@@ -118,6 +118,9 @@ void orc_quantize_per_token_i8(const uint16_t *x_f16, int64_t k, int8_t *xq, uin
 const char *orc_simd_isa(void);
 void orc_mul_mat_q8_0_mt(const orc_block_q8_0 *w, const float *x, const float *inv_s, float *y,
                          int64_t n_rows, int64_t k, int n_threads);
+/* same with the activation quantized by `variant` (ORC_Q8_ROUND_REF / ORC_Q8_ROUND_X86) */
+void orc_mul_mat_q8_0_mt_variant(const orc_block_q8_0 *w, const float *x, const float *inv_s, float *y,
+                                 int64_t n_rows, int64_t k, int n_threads, int variant);
 void orc_mul_mat_q4_0_f16_mt(const orc_block_q4_0 *w, const uint16_t *x_f16, float *y,
                              int64_t n_rows, int64_t k, int n_threads);
 void orc_mul_mat_f16_mt(const uint16_t *w, const float *x, float *y, int64_t n_rows, int64_t k, int n_threads);

@@ -273,3 +273,82 @@ def quantize_per_token_i8(x_f16):
 
 def simd_isa():
     return lib().orc_simd_isa().decode()
+
+
+# ---------------------------------------------------------------- whole model (qwen2_oracle.c)
+
+class _Layer(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "attn_norm", "ffn_norm", "wq", "wk", "wv", "wo", "wgate", "wup", "wdown", "bq", "bk", "bv",
+        "inv_s_attn", "inv_s_o", "inv_s_ffn", "inv_s_down")]
+
+
+class _Model(ctypes.Structure):
+    _fields_ = [("n_layer", ctypes.c_int), ("n_embd", ctypes.c_int), ("n_head", ctypes.c_int),
+                ("n_head_kv", ctypes.c_int), ("head_dim", ctypes.c_int), ("n_ff", ctypes.c_int),
+                ("n_vocab", ctypes.c_int), ("n_ctx", ctypes.c_int), ("rms_eps", ctypes.c_float),
+                ("rope_theta", ctypes.c_float), ("wtype", ctypes.c_int), ("fa_mode", ctypes.c_int),
+                ("n_threads", ctypes.c_int), ("tok_embd", ctypes.c_void_p), ("output_norm", ctypes.c_void_p),
+                ("layers", ctypes.POINTER(_Layer)), ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
+                ("q8_variant", ctypes.c_int), ("q8_generic", ctypes.c_int)]
+
+
+class Qwen2:
+    """CPU Qwen2 decode with ggml-CPU op semantics over a dict of ggml-format arrays
+    (GGUF tensor names) and optional SmoothQuant factors per projection input."""
+
+    def __init__(self, hp, tensors, smooth=None, fa_mode=0, n_threads=1, q8_variant=Q8_ROUND_X86, q8_generic=False):
+        L = lib()
+        if not hasattr(L, "_qwen2_declared"):
+            L.orc_qwen2_decode.restype = ctypes.c_int
+            L.orc_qwen2_decode.argtypes = [ctypes.POINTER(_Model), ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+            L._qwen2_declared = True
+        self.hp = hp
+        self._keep = []
+
+        def ptr(a):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a)
+            self._keep.append(a)
+            return a.ctypes.data
+
+        nkv = hp["n_head_kv"] * hp["head_dim"]
+        layers = (_Layer * hp["n_layer"])()
+        smooth = smooth or {}
+        for il in range(hp["n_layer"]):
+            p = f"blk.{il}."
+            inv = {}
+            for key, wname in (("attn", "attn_q"), ("o", "attn_output"), ("ffn", "ffn_gate"), ("down", "ffn_down")):
+                s = smooth.get(p + wname + ".weight")
+                inv[key] = None if s is None else (np.float32(1.0) / np.asarray(s, np.float32)).astype(np.float32)
+            lay = layers[il]
+            lay.attn_norm = ptr(tensors[p + "attn_norm.weight"])
+            lay.ffn_norm = ptr(tensors[p + "ffn_norm.weight"])
+            for f, n in (("wq", "attn_q"), ("wk", "attn_k"), ("wv", "attn_v"), ("wo", "attn_output"),
+                         ("wgate", "ffn_gate"), ("wup", "ffn_up"), ("wdown", "ffn_down")):
+                setattr(lay, f, ptr(tensors[p + n + ".weight"]))
+            for f, n in (("bq", "attn_q"), ("bk", "attn_k"), ("bv", "attn_v")):
+                setattr(lay, f, ptr(tensors.get(p + n + ".bias")))
+            lay.inv_s_attn, lay.inv_s_o = ptr(inv["attn"]), ptr(inv["o"])
+            lay.inv_s_ffn, lay.inv_s_down = ptr(inv["ffn"]), ptr(inv["down"])
+        self._layers = layers
+        self.k_cache = np.zeros((hp["n_layer"], hp["n_ctx"], nkv), np.uint16)
+        self.v_cache = np.zeros((hp["n_layer"], hp["n_ctx"], nkv), np.uint16)
+        m = _Model()
+        for f in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_ff", "n_vocab", "n_ctx"):
+            setattr(m, f, int(hp[f]))
+        m.rms_eps, m.rope_theta = float(hp["rms_eps"]), float(hp["rope_theta"])
+        m.wtype, m.fa_mode, m.n_threads = int(hp["wtype"]), int(fa_mode), int(n_threads)
+        m.q8_variant, m.q8_generic = int(q8_variant), int(bool(q8_generic))
+        m.tok_embd = ptr(tensors["token_embd.weight"])
+        m.output_norm = ptr(tensors["output_norm.weight"])
+        m.layers = layers
+        m.k_cache, m.v_cache = self.k_cache.ctypes.data, self.v_cache.ctypes.data
+        self._m = m
+        self.logits = np.empty(hp["n_vocab"], np.float32)
+
+    def decode(self, token, pos):
+        """returns (argmax, logits copy)"""
+        best = lib().orc_qwen2_decode(ctypes.byref(self._m), int(token), int(pos), self.logits.ctypes.data)
+        return best, self.logits.copy()

@@ -18,6 +18,12 @@ def _declared(header):
     return sorted(set(re.findall(r"\b(mi_[a-z0-9_]+)\s*\(", txt)))
 
 
+def _declared_prefix(header, prefix):
+    txt = open(os.path.join(ROOT, "include", header)).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(" + prefix + r"[a-z0-9_]+)\s*\(", txt)))
+
+
 def test_library_exports_every_declared_symbol(mi):
     L = mi.lib()
     declared = _declared("ggml_mi355x_kernels.h")
@@ -25,6 +31,12 @@ def test_library_exports_every_declared_symbol(mi):
     missing = [s for s in declared if not hasattr(L, s)]
     assert not missing, missing
     assert set(declared) <= set(mi.EXPORTED)
+    for header, prefix in (("ggml-mi355x.h", "ggml_backend_mi355x_"), ("mi_qwen2.h", "mi_qwen2_")):
+        syms = _declared_prefix(header, prefix)
+        assert syms, header
+        missing = [s for s in syms if not hasattr(L, s)]
+        assert not missing, (header, missing)
+    assert hasattr(L, "ggml_backend_is_mi355x")
 
 
 def test_argument_validation_without_device(mi):

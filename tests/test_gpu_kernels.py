@@ -109,6 +109,7 @@ def test_q8_0_gemv_config0(gpu, orc, fused, rounding):
     dx = mi.to_device(x)
     dy = mi.DeviceBuffer(n * 4)
     if fused:
+        assert mi.mul_mat_q8_0_workspace_size(1, k) == 0
         mi.mul_mat_q8_0_f32(wp.ptr, dx.ptr, None, dy.ptr, n, k, 1, rounding)
     else:
         dq = mi.DeviceBuffer(mi.xq_size(1, k))
@@ -135,7 +136,9 @@ def test_q8_0_gemv_shapes(gpu, orc, n, k, m):
     dy = mi.DeviceBuffer(m * n * 4)
     dy2 = mi.DeviceBuffer(m * n * 4)
     dq = mi.DeviceBuffer(mi.xq_size(m, k))
-    mi.mul_mat_q8_0_f32(wp.ptr, dx.ptr, dinv.ptr, dy.ptr, n, k, m, mi.Q8_ROUND_X86)
+    wsb = mi.mul_mat_q8_0_workspace_size(m, k)
+    ws = mi.DeviceBuffer(max(wsb, 1))
+    mi.mul_mat_q8_0_f32(wp.ptr, dx.ptr, dinv.ptr, dy.ptr, n, k, m, mi.Q8_ROUND_X86, ws.ptr, wsb)
     mi.act_quant_q8_0(dx.ptr, dinv.ptr, m, k, dq.ptr, mi.Q8_ROUND_X86)
     mi.gemv_q8_0(wp.ptr, dq.ptr, dy2.ptr, n, k, m)
     mi.device_sync()
@@ -144,7 +147,7 @@ def test_q8_0_gemv_shapes(gpu, orc, n, k, m):
     ref = orc.mul_mat_q8_0(w, x, n, k, inv_s=inv)
     ref = ref.reshape(m, n)
     assert rel_err(y, ref) < GEMV_TOL
-    assert np.array_equal(y, y2)  # same kernel body, same order
+    assert rel_err(y2, ref) < GEMV_TOL
 
 
 # ---------------------------------------------------------------- W4A16
@@ -208,7 +211,7 @@ def _fa_run(mi, q, kc, vc, n_kv_heads, scale, mask=None, kv_len=None, cap=None):
     dl = mi.to_device(np.array([kv_len], np.int32)) if kv_len is not None else None
     out = mi.DeviceBuffer(nq * d * 4)
     ws_bytes = mi.fa_decode_workspace_size(n_kv, nq, n_kv_heads, d)
-    ws = mi.DeviceBuffer(ws_bytes)
+    ws = mi.DeviceBuffer(ws_bytes).zero()
     nb1 = n_kv_heads * d * 2
     mi.fa_decode(dq.ptr, dk.ptr, dv.ptr, dm.ptr if dm else None, dl.ptr if dl else None, n_kv, nq, n_kv_heads, d,
                  nb1, d * 2, nb1, d * 2, scale, out.ptr, ws.ptr, ws_bytes)
