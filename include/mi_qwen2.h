@@ -58,6 +58,15 @@ int mi_qwen2_decode(mi_qwen2 *m, int32_t token, int32_t pos, int32_t *next_token
  * the seconds of the n_gen steps are written to *gen_seconds when not NULL */
 int mi_qwen2_generate(mi_qwen2 *m, const int32_t *prompt, int32_t n_prompt, int32_t n_gen, int32_t *out_tokens,
                       double *gen_seconds);
+/* n_steps greedy decode steps continuing from `token` at position `pos` (the cache holds
+ * positions < pos): step i feeds the previous step's argmax and writes it to out_tokens[i];
+ * the wall-clock seconds of the n_steps are written to *seconds when not NULL */
+int mi_qwen2_decode_steps(mi_qwen2 *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out_tokens,
+                          double *seconds);
+/* copy the first n_pos positions of layer `layer`'s K (is_v = 0) or V (is_v = 1) cache,
+ * fp16 [n_pos][n_head_kv*head_dim], into host memory dst of `size` bytes (the state a
+ * llama.cpp session save would write for this sequence) */
+int mi_qwen2_get_cache(mi_qwen2 *m, int32_t layer, int32_t is_v, int32_t n_pos, void *dst, size_t size);
 /* forget the KV cache contents (positions restart at 0) */
 int mi_qwen2_reset(mi_qwen2 *m);
 

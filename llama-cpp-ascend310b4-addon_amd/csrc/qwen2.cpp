@@ -285,20 +285,39 @@ int mi_qwen2_decode(mi_qwen2 *m, int32_t token, int32_t pos, int32_t *next_token
     return 0;
 }
 
+int mi_qwen2_decode_steps(mi_qwen2 *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out_tokens,
+                          double *seconds) {
+    if (n_steps < 0 || pos < 0 || pos + n_steps > m->hp.n_ctx) return fail("qwen2: bad decode range");
+    if (n_steps > 0 && !out_tokens) return fail("qwen2: out_tokens is NULL");
+    const auto t0 = std::chrono::steady_clock::now();
+    int32_t next = token;
+    for (int32_t i = 0; i < n_steps; i++) {
+        if (mi_qwen2_decode(m, next, pos + i, &next, nullptr)) return -1;
+        out_tokens[i] = next;
+    }
+    const auto t1 = std::chrono::steady_clock::now();
+    if (seconds) *seconds = std::chrono::duration<double>(t1 - t0).count();
+    return 0;
+}
+
 int mi_qwen2_generate(mi_qwen2 *m, const int32_t *prompt, int32_t n_prompt, int32_t n_gen, int32_t *out_tokens,
                       double *gen_seconds) {
-    if (n_prompt < 1 || n_gen < 0 || n_prompt + n_gen > m->hp.n_ctx) return fail("qwen2: bad prompt/generation size");
+    if (!prompt || n_prompt < 1 || n_gen < 0 || n_prompt + n_gen > m->hp.n_ctx)
+        return fail("qwen2: bad prompt/generation size");
     int32_t next = 0;
     for (int32_t i = 0; i < n_prompt; i++)
         if (mi_qwen2_decode(m, prompt[i], i, &next, nullptr)) return -1;
     // n_gen timed decode steps; the first one consumes the prompt's greedy continuation
-    const auto t0 = std::chrono::steady_clock::now();
-    for (int32_t i = 0; i < n_gen; i++) {
-        if (mi_qwen2_decode(m, next, n_prompt + i, &next, nullptr)) return -1;
-        out_tokens[i] = next;
-    }
-    const auto t1 = std::chrono::steady_clock::now();
-    if (gen_seconds) *gen_seconds = std::chrono::duration<double>(t1 - t0).count();
+    return mi_qwen2_decode_steps(m, next, n_prompt, n_gen, out_tokens, gen_seconds);
+}
+
+int mi_qwen2_get_cache(mi_qwen2 *m, int32_t layer, int32_t is_v, int32_t n_pos, void *dst, size_t size) {
+    if (layer < 0 || layer >= m->hp.n_layer) return fail("qwen2: layer %d out of range", layer);
+    if (n_pos < 0 || n_pos > m->hp.n_ctx) return fail("qwen2: n_pos %d outside the cache", n_pos);
+    ggml_tensor *c = is_v ? m->v_cache[layer] : m->k_cache[layer];
+    const size_t bytes = (size_t)n_pos * c->nb[1];
+    if (!dst || size != bytes) return fail("qwen2: cache copy needs %zu bytes, got %zu", bytes, size);
+    if (bytes) ggml_backend_tensor_get(c, dst, 0, bytes);
     return 0;
 }
 

@@ -324,6 +324,17 @@ def mul_mat_q8_0_f32(w_packed, x, inv_s, y, n, k, m=1, rounding=Q8_ROUND_X86, ws
           ws_bytes)
 
 
+def mul_mat_q8_0_f32_multi(w_packed, n, y, k, x, inv_s=None, rounding=Q8_ROUND_X86, ws=None, ws_bytes=0,
+                           stream=None):
+    """up to four Q8_0 matrices (device pointers w_packed[i], n[i] rows, outputs y[i]) on one activation row"""
+    cnt = len(w_packed)
+    wa = (ctypes.c_void_p * cnt)(*w_packed)
+    na = (ctypes.c_int64 * cnt)(*n)
+    ya = (ctypes.c_void_p * cnt)(*y)
+    _call("mi_mul_mat_q8_0_f32_multi", _P(stream), cnt, ctypes.cast(wa, ctypes.c_void_p), ctypes.cast(na, ctypes.c_void_p),
+          ctypes.cast(ya, ctypes.c_void_p), k, _P(x), _P(inv_s), rounding, _P(ws), ws_bytes)
+
+
 def q8_0_block_dots(w_packed, xq, out, n, k, stream=None):
     _call("mi_q8_0_block_dots", _P(stream), _P(w_packed), _P(xq), _P(out), n, k)
 
@@ -372,6 +383,9 @@ _QWEN_SIGS = {
     "mi_qwen2_tensor_nbytes": (_I64, [_P, ctypes.c_char_p, _P]),
     "mi_qwen2_decode": (_I, [_P, ctypes.c_int32, ctypes.c_int32, _P, _P]),
     "mi_qwen2_generate": (_I, [_P, _P, ctypes.c_int32, ctypes.c_int32, _P, ctypes.POINTER(ctypes.c_double)]),
+    "mi_qwen2_decode_steps": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P,
+                                  ctypes.POINTER(ctypes.c_double)]),
+    "mi_qwen2_get_cache": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, _SZ]),
     "mi_qwen2_reset": (_I, [_P]),
 }
 EXPORTED = EXPORTED + tuple(_QWEN_SIGS)
@@ -435,6 +449,21 @@ class Qwen2Model:
         self._chk("mi_qwen2_generate", _qlib().mi_qwen2_generate(self.ptr, prompt.ctypes.data, prompt.size, n_gen,
                                                                  out.ctypes.data, ctypes.byref(secs)))
         return out[:n_gen], secs.value
+
+    def decode_steps(self, token, pos, n_steps):
+        """greedy continuation from (token, pos) -> (tokens[n_steps], seconds)"""
+        out = np.empty(max(n_steps, 1), np.int32)
+        secs = ctypes.c_double(0.0)
+        self._chk("mi_qwen2_decode_steps", _qlib().mi_qwen2_decode_steps(self.ptr, int(token), int(pos), int(n_steps),
+                                                                         out.ctypes.data, ctypes.byref(secs)))
+        return out[:n_steps], secs.value
+
+    def get_cache(self, layer, is_v, n_pos):
+        """fp16 bits [n_pos, n_head_kv*head_dim] of one layer's K or V cache"""
+        out = np.empty((n_pos, self.hp["n_head_kv"] * self.hp["head_dim"]), np.uint16)
+        self._chk("mi_qwen2_get_cache", _qlib().mi_qwen2_get_cache(self.ptr, int(layer), int(is_v), int(n_pos),
+                                                                   out.ctypes.data, out.nbytes))
+        return out
 
     def reset(self):
         self._chk("mi_qwen2_reset", _qlib().mi_qwen2_reset(self.ptr))
