@@ -25,6 +25,7 @@ Synthetic data: random weights of the Qwen2.5-1.5B shape (28 layers, hidden 1536
 factors uniform in [0.5, 2] (no checkpoints exist offline).
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -61,6 +62,14 @@ def measure_roofline(mi, qs, hp, rng):
     st.sync()
     algo = 2 * n * (k // 32) * 34 + k * 4 + k * 4 + 2 * n * 4   # weights + x + 1/s + y
     launches = copies * 8
+    # argument tuples built once: the launch loop is then one C call per launch
+    fn = mi.lib().mi_mul_mat_q8_0_f32_multi
+    ns = (ctypes.c_int64 * 2)(n, n)
+    ys = (ctypes.c_void_p * 2)(y0.ptr, y1.ptr)
+    ws = [(ctypes.c_void_p * 2)(bufs[2 * c].ptr, bufs[2 * c + 1].ptr) for c in range(copies)]
+    args = [(mi._P(st.ptr), 2, ctypes.cast(w, ctypes.c_void_p), ctypes.cast(ns, ctypes.c_void_p),
+             ctypes.cast(ys, ctypes.c_void_p), k, mi._P(x.ptr), mi._P(inv_s.ptr), mi.Q8_ROUND_X86, None, 0)
+            for w in ws]
     e0, e1 = mi.Event(), mi.Event()
     samples = []
     for _ in range(3):
@@ -70,9 +79,8 @@ def measure_roofline(mi, qs, hp, rng):
             mi._call("mi_memcpy_d2d", mi._P(plug_b.ptr), mi._P(plug_a.ptr), 2 << 30, mi._P(st.ptr))
         e0.record(st.ptr)
         for i in range(launches):
-            c = i % copies
-            mi.mul_mat_q8_0_f32_multi([bufs[2 * c].ptr, bufs[2 * c + 1].ptr], [n, n], [y0.ptr, y1.ptr], k, x.ptr,
-                                      inv_s.ptr, mi.Q8_ROUND_X86, stream=st.ptr)
+            if fn(*args[i % copies]) != 0:
+                raise mi.MiError("mi_mul_mat_q8_0_f32_multi", -1, mi.last_error())
         e1.record(st.ptr)
         samples.append(e0.elapsed_ms(e1) * 1e3 / launches)
     avg_us = float(np.median(samples))

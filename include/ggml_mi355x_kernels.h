@@ -122,6 +122,36 @@ int mi_mul_mat_q8_0_f32(void *stream, const void *w_packed, const float *x, cons
 int mi_mul_mat_q8_0_f32_multi(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
                               float *const *y, int64_t k, const float *x, const float *inv_s, int rounding, void *ws,
                               size_t ws_bytes);
+/* ---- fused decode chains (the backend's graph fusions).  Each replaces a run of
+ * adjacent ggml nodes of llama.cpp's decode graph with one launch; the reference's
+ * evaluate_and_capture_cann_graph runs every node through ggml_cann_compute_forward
+ * one by one (patch:1897-1930). ---- */
+
+/* [RMS_NORM -> MUL(norm_w)] -> MUL_MAT x n_mats (Q8_0, one activation row, k <= 4096)
+ * -> optional ADD of add[i] (bias or residual, length n[i]) per matrix.  norm_w == NULL
+ * skips the RMSNorm (x is the activation itself). */
+int mi_mul_mat_q8_0_f32_fused(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
+                              float *const *y, const float *const *add, int64_t k, const float *x,
+                              const float *norm_w, float eps, const float *inv_s, int rounding);
+/* the attention-input chain of one token: [RMS_NORM -> MUL(norm_w)] -> q/k/v MUL_MATs
+ * (w_packed[0..2], n[0..2] rows, k <= 4096) -> ADD bias[i] (or NULL) -> neox ROPE of q
+ * and k (n_dims = head_dim, theta = pos[0] * freq_base^(-2i/head_dim), freq_scale,
+ * attn_factor; ext_factor 0) -> q fp32 into q_out[n[0]], k and v converted to fp16 into
+ * row kv_idx[0] (int32, or int64 when kv_idx_is_i64) of the caches (SET_ROWS); rows
+ * outside [0, n_cache_rows) are not written. */
+int mi_qkv_rope_kv_q8_0(void *stream, const void *const *w_packed, const int64_t *n, const float *const *bias,
+                        int64_t k, const float *x, const float *norm_w, float eps, const float *inv_s, int rounding,
+                        int64_t head_dim, const int32_t *pos, float freq_base, float freq_scale, float attn_factor,
+                        float *q_out, void *k_cache, size_t k_row_bytes, void *v_cache, size_t v_row_bytes,
+                        const void *kv_idx, int kv_idx_is_i64, int64_t n_cache_rows);
+/* GLU swiglu(g, u) of one row (k floats) times inv_s, quantized to Q8_0 into xq (the
+ * planar layout of mi_act_quant_q8_0 with m = 1): the input side of the down projection */
+int mi_swiglu_quant_q8_0(void *stream, const float *g, const float *u, const float *inv_s, int64_t k, void *xq,
+                         int rounding);
+/* mi_gemv_q8_0 with the ADD of a same-shape vector (residual) fused: y = W*xq + add */
+int mi_gemv_q8_0_add(void *stream, const void *w_packed, const void *xq, const float *add, float *y, int64_t n,
+                     int64_t k, int64_t m);
+
 /* debug: exact per-block int32 dot products out[row][b] for activation row 0 */
 int mi_q8_0_block_dots(void *stream, const void *w_packed, const void *xq, int32_t *out, int64_t n, int64_t k);
 
@@ -190,8 +220,11 @@ int mi_get_rows(void *stream, const void *src, int src_is_f16, const int32_t *id
                 int64_t nrows, size_t snb1, int64_t n_src_rows);
 /* d = silu(g) * u (ggml GLU SWIGLU, split form) */
 int mi_swiglu(void *stream, const float *g, const float *u, float *d, int64_t n);
-/* index of the first maximum of each row (ggml ARGMAX) */
-int mi_argmax(void *stream, const float *x, int32_t *out, int64_t ne0, int64_t nrows);
+/* index of the first maximum of each row (ggml ARGMAX; the first maximum is what
+ * llama.cpp's greedy sampler selects).  Two passes through a workspace of
+ * mi_argmax_workspace_size bytes (8-byte aligned, no initial contents needed). */
+size_t mi_argmax_workspace_size(int64_t ne0, int64_t nrows);
+int mi_argmax(void *stream, const float *x, int32_t *out, int64_t ne0, int64_t nrows, void *ws, size_t ws_bytes);
 /* decode mask row from a device length: 0 for i < *len, -inf beyond */
 int mi_fill_mask_f16(void *stream, uint16_t *mask, const int32_t *len, int64_t n_kv);
 

@@ -23,32 +23,47 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // 2^x with the hardware v_exp_f32 (arguments here are <= 0; -inf gives 0)
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
-constexpr int kT = 8;   // positions per lane group per tile (all loads of a tile in flight together)
 
 template <int D>
 constexpr int part_stride() { return D + 4; }  // o[D], m, l, pad -> 16-byte aligned records
 
 struct FaPlan {
-    int chunk;
+    int chunk;     // positions per workgroup
     int n_splits;
+    int kt;        // positions per lane group per tile (all loads of a tile in flight together)
 };
 
-// One workgroup per (split, kv head).  Aim at one workgroup per CU for long
-// contexts (chunk >= 64 positions, multiple of 64); short contexts get few
-// splits, and with at most kFusedMaxSplits splits the last workgroup of a kv
-// head merges the partials itself (no second launch).
+// One workgroup per (split, kv head), each with 4 waves of lane groups (one KV row
+// per lane group: 16 groups per workgroup at D = 128, 32 at D = 64).  A workgroup's
+// time is a chain of dependent steps per tile, so short contexts get one short tile
+// per workgroup and many workgroups; long contexts aim at ~512 workgroups with 8-deep
+// tiles.  With at most kFusedMaxSplits splits the last workgroup of a kv head can
+// merge the partials itself (opt-in).  MI_FA_CHUNK=<positions> overrides the chunk.
 constexpr int kFusedMaxSplits = 16;
 constexpr int kMaxSplits = 1024;
 
-inline FaPlan fa_plan(int64_t n_kv, int64_t n_kv_heads) {
+inline int fa_chunk_override() {
+    static const int v = [] {
+        const char *e = getenv("MI_FA_CHUNK");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
+inline FaPlan fa_plan(int64_t n_kv, int64_t n_kv_heads, int64_t d) {
+    const int64_t ng = 4 * 64 / (d / 8);  // lane groups per workgroup
     const int64_t target_wg = 512;
     int64_t per = (n_kv * n_kv_heads + target_wg - 1) / target_wg;
-    per = (per + 63) / 64 * 64;
-    if (per < 64) per = 64;
-    while ((n_kv + per - 1) / per > kMaxSplits) per *= 2;
+    if (fa_chunk_override() > 0) per = fa_chunk_override();
     FaPlan p;
-    p.chunk = (int)per;
-    p.n_splits = (int)((n_kv + per - 1) / per);
+    if (per <= ng) p.kt = 1;
+    else if (per <= 2 * ng) p.kt = 2;
+    else if (per <= 4 * ng) p.kt = 4;
+    else p.kt = 8;
+    int64_t chunk = (per + ng * p.kt - 1) / (ng * p.kt) * (ng * p.kt);
+    while ((n_kv + chunk - 1) / chunk > kMaxSplits) chunk *= 2;
+    p.chunk = (int)chunk;
+    p.n_splits = (int)((n_kv + chunk - 1) / chunk);
     return p;
 }
 
@@ -73,7 +88,7 @@ __device__ __forceinline__ void merge_state(float &m, float &l, float *o, int xo
     m = mn;
 }
 
-template <int D, int GQ, bool MASK>
+template <int D, int GQ, bool MASK, int kT>
 __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, const uint8_t *__restrict__ kc,
                                                   const uint8_t *__restrict__ vc, const uint16_t *__restrict__ mask,
                                                   const int32_t *__restrict__ kv_len_p, int n_kv, size_t k_nb1,
@@ -374,9 +389,18 @@ int launch_split_m(hipStream_t st, const float *q, const void *k, const void *v,
                    size_t v_nb1, size_t v_nb2, float scale, float *out, float *part, unsigned *counters,
                    const FaPlan &p) {
     const bool fused = p.n_splits <= kFusedMaxSplits && fused_combine_enabled();
-    hipLaunchKernelGGL((k_fa_split<D, GQ, MASK>), dim3((unsigned)p.n_splits, (unsigned)n_kv_heads), dim3(256), 0, st,
-                       q, (const uint8_t *)k, (const uint8_t *)v, mask, kv_len, (int)n_kv, k_nb1, k_nb2, v_nb1, v_nb2,
-                       scale, p.chunk, p.n_splits, part, out, fused ? counters : nullptr);
+    const dim3 grid((unsigned)p.n_splits, (unsigned)n_kv_heads);
+#define MI_FA_KT(KT)                                                                                          \
+    hipLaunchKernelGGL((k_fa_split<D, GQ, MASK, KT>), grid, dim3(256), 0, st, q, (const uint8_t *)k,          \
+                       (const uint8_t *)v, mask, kv_len, (int)n_kv, k_nb1, k_nb2, v_nb1, v_nb2, scale, p.chunk, \
+                       p.n_splits, part, out, fused ? counters : nullptr)
+    switch (p.kt) {
+        case 1: MI_FA_KT(1); break;
+        case 2: MI_FA_KT(2); break;
+        case 4: MI_FA_KT(4); break;
+        default: MI_FA_KT(8); break;
+    }
+#undef MI_FA_KT
     MI_CHECK_LAUNCH("k_fa_split");
     if (p.n_splits > 1 && !fused) {
         hipLaunchKernelGGL((k_fa_combine<D>), dim3((unsigned)(n_kv_heads * GQ), D / 32), dim3(256), 0, st, part, out,
@@ -447,7 +471,7 @@ extern "C" {
 
 size_t mi_fa_decode_workspace_size(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d) {
     if (n_kv <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || d <= 0) return 0;
-    const FaPlan p = fa_plan(n_kv, n_kv_heads);
+    const FaPlan p = fa_plan(n_kv, n_kv_heads, d);
     return fa_part_bytes(n_q_heads, p.n_splits, d) + mi::align_up((size_t)n_kv_heads * sizeof(unsigned), 256);
 }
 
@@ -463,7 +487,7 @@ int mi_fa_decode(void *stream, const float *q, const void *k, const void *v, con
     MI_CHECK_ARG(mi::aligned(k, 16) && mi::aligned(v, 16) && k_nb1 % 16 == 0 && k_nb2 % 16 == 0 && v_nb1 % 16 == 0 &&
                      v_nb2 % 16 == 0 && mi::aligned(q, 16) && mi::aligned(out, 16),
                  "fa_decode: K/V base and strides must be 16-byte aligned");
-    const FaPlan p = fa_plan(n_kv, n_kv_heads);
+    const FaPlan p = fa_plan(n_kv, n_kv_heads, d);
     const size_t need = mi_fa_decode_workspace_size(n_kv, n_q_heads, n_kv_heads, d);
     if (p.n_splits > 1 && (!ws || ws_bytes < need || !mi::aligned(ws, 256))) {
         mi::set_error("fa_decode: workspace %zu < %zu bytes (or not 256-byte aligned)", ws_bytes, need);

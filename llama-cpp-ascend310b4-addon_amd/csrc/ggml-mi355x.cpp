@@ -13,9 +13,12 @@
 //   graph_compute    per-node dispatch on one stream (patch:1884-1922); runtime
 //                    errors abort like ACL_CHECK; GGML_MI355X_TRACE_NODE_SYNC=1
 //                    synchronizes and logs after every node (patch:1887-1921)
-// MI355X-specific: consecutive MUL_MATs sharing their activation run as one
-// grouped GEMV launch, RMS_NORM+MUL fuse, and a graph whose nodes did not change
-// since the last call is replayed as a captured HIP graph.
+// MI355X-specific: runs of adjacent nodes of the decode graph fuse into single
+// launches (RMSNorm into the GEMV prologue; bias, residual, RoPE and the KV-cache
+// write into GEMV epilogues; SwiGLU into the next GEMV's activation quantization),
+// consecutive MUL_MATs sharing their activation run as one grouped GEMV launch,
+// and a graph whose nodes did not change since the last call is replayed as a
+// captured HIP graph.
 #include "ggml-mi355x.h"
 
 #include <hip/hip_runtime.h>
@@ -24,6 +27,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -69,10 +73,8 @@ bool trace_node_sync() {
     static const bool on = env_flag("GGML_MI355X_TRACE_NODE_SYNC", false);
     return on;
 }
-bool fusion_enabled() {
-    static const bool on = env_flag("GGML_MI355X_FUSION", true);
-    return on;
-}
+// read when a backend is created, so each backend instance keeps its own setting
+bool fusion_env() { return env_flag("GGML_MI355X_FUSION", true); }
 int q8_rounding() {
     static const int r = [] {
         const char *v = getenv("GGML_MI355X_Q8_ROUNDING");
@@ -143,6 +145,7 @@ struct BufferCtx {
 
 struct BackendCtx {
     int device = 0;
+    bool fuse = true;
     std::string name;
     hipStream_t stream = nullptr;
     void *scratch = nullptr;
@@ -320,6 +323,7 @@ const ggml_backend_buffer_type_i kBuftIface = {
 // ------------------------------------------------------------------ supports_op
 
 bool is_f32_contig(const ggml_tensor *t) { return t && t->type == GGML_TYPE_F32 && ggml_is_contiguous(t); }
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 bool supports_mul_mat(const ggml_tensor *op) {
     const ggml_tensor *a = op->src[0], *b = op->src[1];
@@ -425,7 +429,9 @@ size_t fa_ws_need(const ggml_tensor *node) {
 
 size_t scratch_need(const ggml_tensor *node) {
     if (node->op == GGML_OP_MUL_MAT && node->src[0]->type == GGML_TYPE_Q8_0)
-        return mi_mul_mat_q8_0_workspace_size(node->src[1]->ne[1], node->src[1]->ne[0]);
+        return std::max(mi_mul_mat_q8_0_workspace_size(node->src[1]->ne[1], node->src[1]->ne[0]),
+                        node->src[1]->ne[1] == 1 ? mi_xq_size(1, node->src[1]->ne[0]) : (size_t)0);
+    if (node->op == GGML_OP_ARGMAX) return mi_argmax_workspace_size(node->src[0]->ne[0], ggml_nrows(node->src[0]));
     return 0;
 }
 
@@ -508,28 +514,287 @@ void run_fa(BackendCtx *ctx, ggml_tensor *node) {
                             (float *)node->data, ctx->fa_ws, ctx->fa_ws_size));
 }
 
-using UseMap = std::unordered_map<const ggml_tensor *, int>;
+// ---- graph fusions
+//
+// Runs of adjacent nodes (no-op view nodes in between are skipped) that form one
+// of the decode chains below run as one fused launch, as ggml-cuda fuses adjacent
+// nodes.  A run is fused only when every intermediate tensor it does not write is
+// read by nothing outside the run, so skipping those writes is unobservable.
+//   attention input : RMS_NORM, MUL(w), MUL_MAT q/k/v, [ADD bias x3], ROPE q, ROPE k,
+//                     SET_ROWS k, SET_ROWS v             -> mi_qkv_rope_kv_q8_0
+//   normed matmuls  : RMS_NORM, MUL(w), MUL_MAT x1..4   -> mi_mul_mat_q8_0_f32_fused
+//   matmul + add    : MUL_MAT, ADD(vector)              -> fused epilogue add
+//   glu + matmul    : GLU swiglu, MUL_MAT, [ADD(vector)] -> mi_swiglu_quant_q8_0 +
+//                                                          mi_gemv_q8_0_add
 
-// how many graph nodes read each tensor (directly)
-UseMap count_uses_all(ggml_cgraph *g) {
-    UseMap m;
+using Consumers = std::unordered_map<const ggml_tensor *, std::vector<const ggml_tensor *>>;
+
+Consumers consumers_of(ggml_cgraph *g) {
+    Consumers c;
     for (int i = 0; i < ggml_graph_n_nodes(g); i++) {
         const ggml_tensor *nd = ggml_graph_node(g, i);
         for (int s = 0; s < GGML_MAX_SRC; s++)
-            if (nd->src[s]) m[nd->src[s]]++;
+            if (nd->src[s]) c[nd->src[s]].push_back(nd);
     }
-    return m;
+    return c;
+}
+
+bool is_view_op(const ggml_tensor *t) {
+    return t->op == GGML_OP_RESHAPE || t->op == GGML_OP_VIEW || t->op == GGML_OP_PERMUTE || t->op == GGML_OP_TRANSPOSE;
+}
+
+// non-view consumers of t, looking through view nodes
+void real_consumers(const Consumers &C, const ggml_tensor *t, std::vector<const ggml_tensor *> &out) {
+    auto it = C.find(t);
+    if (it == C.end()) return;
+    for (const ggml_tensor *c : it->second) {
+        if (is_view_op(c)) real_consumers(C, c, out);
+        else out.push_back(c);
+    }
+}
+
+bool only_consumed_by(const Consumers &C, const ggml_tensor *t, std::initializer_list<const ggml_tensor *> allowed) {
+    std::vector<const ggml_tensor *> v;
+    real_consumers(C, t, v);
+    if (v.empty()) return false;
+    for (const ggml_tensor *c : v) {
+        bool ok = false;
+        for (const ggml_tensor *a : allowed) ok = ok || c == a;
+        if (!ok) return false;
+    }
+    return true;
+}
+
+// the tensor t aliases, through whole-tensor views (same bytes, no offset)
+const ggml_tensor *alias_root(const ggml_tensor *t) {
+    while (is_view_op(t) && t->src[0] && t->view_offs == 0 && ggml_nbytes(t) == ggml_nbytes(t->src[0]) &&
+           ggml_is_contiguous(t) && ggml_is_contiguous(t->src[0]))
+        t = t->src[0];
+    return t;
+}
+
+int next_real(ggml_cgraph *g, int i) {
+    const int nn = ggml_graph_n_nodes(g);
+    while (i < nn && is_noop(ggml_graph_node(g, i))) i++;
+    return i;
+}
+
+bool is_row_vector(const ggml_tensor *t, int64_t n) {
+    return t && is_f32_contig(t) && ggml_nelements(t) == n && aligned16(t->data);
+}
+
+// a Q8_0 MUL_MAT on one activation row with the prepacked side copy ready
+bool q8_gemv_node(const ggml_tensor *n) {
+    if (n->op != GGML_OP_MUL_MAT) return false;
+    const ggml_tensor *a = n->src[0], *b = n->src[1];
+    const TensorExtra *ex = (const TensorExtra *)a->extra;
+    return a->type == GGML_TYPE_Q8_0 && ex && ex->ready && b->type == GGML_TYPE_F32 && ggml_nrows(b) == 1 &&
+           ggml_is_contiguous(b) && aligned16(b->data) && is_f32_contig(n);
+}
+
+bool rms_mul_head(ggml_cgraph *g, int i, const Consumers &C, int &j, const ggml_tensor *&x, const ggml_tensor *&nw,
+                  const ggml_tensor *&mul, float &eps) {
+    const ggml_tensor *rms = ggml_graph_node(g, i);
+    if (rms->op != GGML_OP_RMS_NORM) return false;
+    x = rms->src[0];
+    if (!is_f32_contig(x) || ggml_nrows(x) != 1 || x->ne[0] % 32 || x->ne[0] > 4096 || !aligned16(x->data)) return false;
+    memcpy(&eps, rms->op_params, sizeof(float));
+    j = next_real(g, i + 1);
+    if (j >= ggml_graph_n_nodes(g)) return false;
+    mul = ggml_graph_node(g, j);
+    if (mul->op != GGML_OP_MUL || mul->src[0] != rms || !is_row_vector(mul->src[1], x->ne[0])) return false;
+    if (!only_consumed_by(C, rms, {mul})) return false;
+    nw = mul->src[1];
+    return true;
+}
+
+int try_fuse_attn_in(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    const int nn = ggml_graph_n_nodes(g);
+    int j;
+    const ggml_tensor *x, *nw, *mul;
+    float eps;
+    if (!rms_mul_head(g, i, C, j, x, nw, mul, eps)) return 0;
+    const ggml_tensor *mm[3], *out[3], *bias[3] = {nullptr, nullptr, nullptr};
+    for (int t = 0; t < 3; t++) {
+        j = next_real(g, j + 1);
+        if (j >= nn) return 0;
+        mm[t] = ggml_graph_node(g, j);
+        if (!q8_gemv_node(mm[t]) || mm[t]->src[1] != mul || inv_s_of(mm[t]->src[0]) != inv_s_of(mm[0]->src[0]))
+            return 0;
+        out[t] = mm[t];
+    }
+    if (!only_consumed_by(C, mul, {mm[0], mm[1], mm[2]})) return 0;
+    int jb = next_real(g, j + 1);
+    if (jb < nn && ggml_graph_node(g, jb)->op == GGML_OP_ADD) {
+        for (int t = 0; t < 3; t++) {
+            if (jb >= nn) return 0;
+            const ggml_tensor *ad = ggml_graph_node(g, jb);
+            if (ad->op != GGML_OP_ADD || ad->src[0] != mm[t] || !is_row_vector(ad->src[1], mm[t]->ne[0]) ||
+                !is_f32_contig(ad) || !only_consumed_by(C, mm[t], {ad}))
+                return 0;
+            bias[t] = ad->src[1];
+            out[t] = ad;
+            j = jb;
+            jb = next_real(g, jb + 1);
+        }
+    }
+    const ggml_tensor *rope[2], *sr[2];
+    for (int t = 0; t < 2; t++) {
+        j = next_real(g, j + 1);
+        if (j >= nn) return 0;
+        rope[t] = ggml_graph_node(g, j);
+        if (rope[t]->op != GGML_OP_ROPE || !supports_op_impl(rope[t]) || alias_root(rope[t]->src[0]) != out[t] ||
+            !only_consumed_by(C, out[t], {rope[t]}))
+            return 0;
+    }
+    const ggml_tensor *r = rope[0];
+    const int64_t hd = r->src[0]->ne[0];
+    if (r->op_params[1] != hd || rope[1]->op_params[1] != hd || rope[1]->src[0]->ne[0] != hd || hd % 16 ||
+        rope[1]->src[1] != r->src[1] || ggml_nelements(r->src[1]) != 1 ||
+        memcmp(r->op_params + 5, rope[1]->op_params + 5, 4 * sizeof(int32_t)) != 0 ||
+        mm[0]->ne[0] % hd || mm[1]->ne[0] % hd || !is_f32_contig(rope[0]))
+        return 0;
+    for (int t = 0; t < 2; t++) {
+        j = next_real(g, j + 1);
+        if (j >= nn) return 0;
+        sr[t] = ggml_graph_node(g, j);
+        const ggml_tensor *src = t == 0 ? rope[1] : out[2];
+        if (sr[t]->op != GGML_OP_SET_ROWS || !supports_op_impl(sr[t]) || alias_root(sr[t]->src[0]) != src ||
+            ggml_nrows(sr[t]->src[0]) != 1 || sr[t]->src[0]->ne[0] != mm[t + 1]->ne[0] ||
+            ggml_nelements(sr[t]->src[1]) != 1 || (t == 1 && sr[1]->src[1] != sr[0]->src[1]))
+            return 0;
+    }
+    if (!only_consumed_by(C, rope[1], {sr[0]}) || !only_consumed_by(C, out[2], {sr[1]})) return 0;
+
+    const void *w[3];
+    int64_t n[3];
+    const float *bp[3];
+    for (int t = 0; t < 3; t++) {
+        w[t] = ((const TensorExtra *)mm[t]->src[0]->extra)->packed;
+        n[t] = mm[t]->src[0]->ne[1];
+        bp[t] = bias[t] ? (const float *)bias[t]->data : nullptr;
+    }
+    float freq_base, freq_scale, attn_factor;
+    memcpy(&freq_base, (const float *)r->op_params + 5, sizeof(float));
+    memcpy(&freq_scale, (const float *)r->op_params + 6, sizeof(float));
+    memcpy(&attn_factor, (const float *)r->op_params + 8, sizeof(float));
+    const ggml_tensor *idx = sr[0]->src[1];
+    MI_K_CHECK(mi_qkv_rope_kv_q8_0(ctx->stream, w, n, bp, x->ne[0], (const float *)x->data, (const float *)nw->data, eps,
+                                   inv_s_of(mm[0]->src[0]), q8_rounding(), hd, (const int32_t *)r->src[1]->data,
+                                   freq_base, freq_scale, attn_factor, (float *)rope[0]->data, sr[0]->data,
+                                   sr[0]->nb[1], sr[1]->data, sr[1]->nb[1], idx->data, idx->type == GGML_TYPE_I64,
+                                   std::min(sr[0]->ne[1], sr[1]->ne[1])));
+    return j + 1 - i;
+}
+
+int try_fuse_norm_matmuls(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    const int nn = ggml_graph_n_nodes(g);
+    int j;
+    const ggml_tensor *x, *nw, *mul;
+    float eps;
+    if (!rms_mul_head(g, i, C, j, x, nw, mul, eps)) return 0;
+    const ggml_tensor *mm[4] = {nullptr, nullptr, nullptr, nullptr};
+    int cnt = 0, last = j;
+    for (int jj = next_real(g, j + 1); jj < nn && cnt < 4; jj = next_real(g, jj + 1)) {
+        const ggml_tensor *nd = ggml_graph_node(g, jj);
+        if (!q8_gemv_node(nd) || nd->src[1] != mul || inv_s_of(nd->src[0]) != inv_s_of(mm[0] ? mm[0]->src[0] : nd->src[0]))
+            break;
+        mm[cnt++] = nd;
+        last = jj;
+    }
+    if (cnt == 0) return 0;
+    std::vector<const ggml_tensor *> cons;
+    real_consumers(C, mul, cons);
+    for (const ggml_tensor *c : cons) {
+        bool in = false;
+        for (int t = 0; t < cnt; t++) in = in || c == mm[t];
+        if (!in) return 0;
+    }
+    const void *w[4];
+    int64_t n[4];
+    float *y[4];
+    for (int t = 0; t < cnt; t++) {
+        w[t] = ((const TensorExtra *)mm[t]->src[0]->extra)->packed;
+        n[t] = mm[t]->src[0]->ne[1];
+        y[t] = (float *)mm[t]->data;
+    }
+    MI_K_CHECK(mi_mul_mat_q8_0_f32_fused(ctx->stream, cnt, w, n, y, nullptr, x->ne[0], (const float *)x->data,
+                                         (const float *)nw->data, eps, inv_s_of(mm[0]->src[0]), q8_rounding()));
+    return last + 1 - i;
+}
+
+// MUL_MAT (Q8_0, one row) followed by its only consumer ADD(mm, v) with a vector of the
+// output length; returns the ADD node and the vector
+const ggml_tensor *matmul_add_tail(ggml_cgraph *g, int j, const ggml_tensor *mm, const Consumers &C,
+                                   const ggml_tensor *&vec) {
+    const int k = next_real(g, j + 1);
+    if (k >= ggml_graph_n_nodes(g)) return nullptr;
+    const ggml_tensor *ad = ggml_graph_node(g, k);
+    if (ad->op != GGML_OP_ADD || !is_f32_contig(ad) || ggml_nelements(ad) != mm->ne[0]) return nullptr;
+    const ggml_tensor *other = ad->src[0] == mm ? ad->src[1] : (ad->src[1] == mm ? ad->src[0] : nullptr);
+    if (!other || other == mm || !is_row_vector(other, mm->ne[0]) || !only_consumed_by(C, mm, {ad})) return nullptr;
+    vec = other;
+    return ad;
+}
+
+int try_fuse_matmul_add(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    const ggml_tensor *mm = ggml_graph_node(g, i);
+    if (!q8_gemv_node(mm)) return 0;
+    const ggml_tensor *vec = nullptr;
+    const ggml_tensor *ad = matmul_add_tail(g, i, mm, C, vec);
+    if (!ad) return 0;
+    const int64_t k = mm->src[0]->ne[0];
+    const TensorExtra *ex = (const TensorExtra *)mm->src[0]->extra;
+    const void *w = ex->packed;
+    const int64_t n = mm->src[0]->ne[1];
+    float *y = (float *)ad->data;
+    const float *add = (const float *)vec->data;
+    if (k <= 4096) {
+        MI_K_CHECK(mi_mul_mat_q8_0_f32_fused(ctx->stream, 1, &w, &n, &y, &add, k, (const float *)mm->src[1]->data,
+                                             nullptr, 0.0f, ex->inv_s, q8_rounding()));
+    } else {
+        GGML_ASSERT(ctx->scratch_size >= mi_xq_size(1, k));
+        MI_K_CHECK(mi_act_quant_q8_0(ctx->stream, (const float *)mm->src[1]->data, ex->inv_s, 1, k, ctx->scratch,
+                                     q8_rounding()));
+        MI_K_CHECK(mi_gemv_q8_0_add(ctx->stream, w, ctx->scratch, add, y, n, k, 1));
+    }
+    return next_real(g, i + 1) + 1 - i;
+}
+
+int try_fuse_glu_matmul(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    const ggml_tensor *glu = ggml_graph_node(g, i);
+    if (glu->op != GGML_OP_GLU || !supports_op_impl(glu) || !glu->src[1] || ggml_nrows(glu) != 1 ||
+        !aligned16(glu->src[0]->data) || !aligned16(glu->src[1]->data))
+        return 0;
+    const int j = next_real(g, i + 1);
+    if (j >= ggml_graph_n_nodes(g)) return 0;
+    const ggml_tensor *mm = ggml_graph_node(g, j);
+    if (!q8_gemv_node(mm) || mm->src[1] != glu || !only_consumed_by(C, glu, {mm})) return 0;
+    const int64_t k = mm->src[0]->ne[0];
+    if (ctx->scratch_size < mi_xq_size(1, k)) return 0;
+    const TensorExtra *ex = (const TensorExtra *)mm->src[0]->extra;
+    const ggml_tensor *vec = nullptr;
+    const ggml_tensor *ad = matmul_add_tail(g, j, mm, C, vec);
+    MI_K_CHECK(mi_swiglu_quant_q8_0(ctx->stream, (const float *)glu->src[0]->data, (const float *)glu->src[1]->data,
+                                    ex->inv_s, k, ctx->scratch, q8_rounding()));
+    MI_K_CHECK(mi_gemv_q8_0_add(ctx->stream, ex->packed, ctx->scratch, ad ? (const float *)vec->data : nullptr,
+                                (float *)(ad ? ad->data : mm->data), mm->src[0]->ne[1], k, 1));
+    return (ad ? next_real(g, j + 1) : j) + 1 - i;
 }
 
 // Runs node i (and, when fused, the nodes it absorbs); returns the number of nodes consumed.
-int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const UseMap &uses) {
+int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
     ggml_tensor *node = ggml_graph_node(g, i);
     const int nn = ggml_graph_n_nodes(g);
     void *st = ctx->stream;
+    const bool fuse = ctx->fuse;
     switch (node->op) {
         case GGML_OP_MUL_MAT: {
+            if (fuse) {
+                if (int used = try_fuse_matmul_add(ctx, g, i, C)) return used;
+            }
             // consecutive Q8_0 GEMVs reading the same activation (q/k/v, gate/up): one grouped launch
-            if (fusion_enabled() && node->src[0]->type == GGML_TYPE_Q8_0 && node->src[1]->ne[1] == 1 &&
+            if (fuse && node->src[0]->type == GGML_TYPE_Q8_0 && node->src[1]->ne[1] == 1 &&
                 node->src[1]->ne[0] <= 4096) {
                 ggml_tensor *grp[4] = {node};
                 int cnt = 1;
@@ -555,14 +820,18 @@ int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const UseMap &uses) {
             run_fa(ctx, node);
             return 1;
         case GGML_OP_RMS_NORM: {
+            if (fuse) {
+                if (int used = try_fuse_attn_in(ctx, g, i, C)) return used;
+                if (int used = try_fuse_norm_matmuls(ctx, g, i, C)) return used;
+            }
             float eps;
             memcpy(&eps, node->op_params, sizeof(float));
             const ggml_tensor *x = node->src[0];
             // RMS_NORM followed by MUL with the norm weight (broadcast row): one launch
-            if (fusion_enabled() && i + 1 < nn) {
+            if (fuse && i + 1 < nn) {
                 ggml_tensor *nx = ggml_graph_node(g, i + 1);
                 if (nx->op == GGML_OP_MUL && nx->src[0] == node && is_f32_contig(nx->src[1]) &&
-                    ggml_nelements(nx->src[1]) == x->ne[0] && uses.count(node) && uses.at(node) == 1) {
+                    ggml_nelements(nx->src[1]) == x->ne[0] && only_consumed_by(C, node, {nx})) {
                     MI_K_CHECK(mi_rms_norm(st, (const float *)x->data, (const float *)nx->src[1]->data,
                                            (float *)nx->data, x->ne[0], ggml_nrows(x), eps));
                     return 2;
@@ -605,12 +874,16 @@ int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const UseMap &uses) {
             return 1;
         }
         case GGML_OP_GLU:
+            if (fuse) {
+                if (int used = try_fuse_glu_matmul(ctx, g, i, C)) return used;
+            }
             MI_K_CHECK(mi_swiglu(st, (const float *)node->src[0]->data, (const float *)node->src[1]->data,
                                  (float *)node->data, ggml_nelements(node)));
             return 1;
         case GGML_OP_ARGMAX: {
             const ggml_tensor *x = node->src[0];
-            MI_K_CHECK(mi_argmax(st, (const float *)x->data, (int32_t *)node->data, x->ne[0], ggml_nrows(x)));
+            MI_K_CHECK(mi_argmax(st, (const float *)x->data, (int32_t *)node->data, x->ne[0], ggml_nrows(x),
+                                 ctx->scratch, ctx->scratch_size));
             return 1;
         }
         default:
@@ -621,7 +894,7 @@ int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const UseMap &uses) {
 
 void run_graph_nodes(BackendCtx *ctx, ggml_cgraph *g) {
     const int nn = ggml_graph_n_nodes(g);
-    const UseMap uses = count_uses_all(g);
+    const Consumers C = consumers_of(g);
     for (int i = 0; i < nn;) {
         ggml_tensor *node = ggml_graph_node(g, i);
         if (is_noop(node)) {
@@ -632,10 +905,11 @@ void run_graph_nodes(BackendCtx *ctx, ggml_cgraph *g) {
             fprintf(stderr, "MI355X trace: node=%d name=%s op=%s ne=[%lld,%lld,%lld,%lld] begin\n", i, node->name,
                     ggml_op_name(node->op), (long long)node->ne[0], (long long)node->ne[1], (long long)node->ne[2],
                     (long long)node->ne[3]);
-        const int used = compute_node(ctx, g, i, uses);
+        const int used = compute_node(ctx, g, i, C);
         if (trace_node_sync()) {
             MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
-            fprintf(stderr, "MI355X trace: node=%d name=%s op=%s complete\n", i, node->name, ggml_op_name(node->op));
+            fprintf(stderr, "MI355X trace: node=%d name=%s op=%s complete (%d node%s)\n", i, node->name,
+                    ggml_op_name(node->op), used, used == 1 ? "" : "s");
         }
         i += used;
     }
@@ -919,6 +1193,7 @@ ggml_backend_t ggml_backend_mi355x_init(int device) {
     set_device(device);
     BackendCtx *ctx = new BackendCtx();
     ctx->device = device;
+    ctx->fuse = fusion_env();
     ctx->name = std::string(GGML_MI355X_NAME) + std::to_string(device);
     MI_HIP_CHECK(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
     return new ggml_backend{backend_guid(), kBackendIface, c->devs[device].get(), ctx};

@@ -7,6 +7,7 @@
 // powf(freq_base, -2/n_dims), argmax keeps the first maximum.
 #include "mi_common.h"
 
+#include <limits.h>
 #include <math.h>
 
 namespace {
@@ -20,7 +21,7 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float *__restrict__ x, c
     const float *xr = x + (size_t)row * ne0;
     float *yr = y + (size_t)row * ne0;
     double s = 0.0;
-    for (int i = threadIdx.x; i < ne0; i += 256) s += (double)(xr[i] * xr[i]);
+    for (int i = threadIdx.x; i < ne0; i += 256) s += (double)__fmul_rn(xr[i], xr[i]);
     __shared__ double sh[256];
     sh[threadIdx.x] = s;
     __syncthreads();
@@ -64,8 +65,8 @@ __global__ void k_rope_neox(const float *__restrict__ x, float *__restrict__ y, 
         const float s = sinf(th) * attn_factor;
         const float x0 = ((const float *)xr)[i];
         const float x1 = ((const float *)xr)[i + half];
-        ((float *)yr)[i] = x0 * c - x1 * s;
-        ((float *)yr)[i + half] = x0 * s + x1 * c;
+        ((float *)yr)[i] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));  // unfused, as the CPU loop
+        ((float *)yr)[i + half] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
     }
     for (int j = n_dims + i; j < ne0; j += blockDim.x) ((float *)yr)[j] = ((const float *)xr)[j];
 }
@@ -104,32 +105,59 @@ __global__ void k_swiglu(const float *__restrict__ g, const float *__restrict__ 
     d[i] = (x / (1.0f + expf(-x))) * u[i];
 }
 
-// one workgroup per row: index of the first maximum
-__global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, int32_t *__restrict__ out, int ne0) {
-    const float *xr = x + (size_t)blockIdx.x * ne0;
+// ARGMAX in two passes: per chunk of a row the first maximum (strict >, so NaN is
+// never taken and ties keep the lower index), then one workgroup per row over the
+// chunk results.  Partials are (value, index) pairs in the workspace.
+__device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+}
+
+__device__ __forceinline__ void argmax_block(float &best, int &bi) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) argmax_merge(best, bi, __shfl_xor(best, o, 64), __shfl_xor(bi, o, 64));
+    if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = best; si[threadIdx.x >> 6] = bi; }
+    __syncthreads();
+    best = sv[0];
+    bi = si[0];
+#pragma unroll
+    for (int w = 1; w < 4; w++) argmax_merge(best, bi, sv[w], si[w]);
+}
+
+__global__ __launch_bounds__(256) void k_argmax_part(const float *__restrict__ x, float2 *__restrict__ part, int ne0,
+                                                     int chunk, int nchunks) {
+    const int row = blockIdx.y, c = blockIdx.x;
+    const float *xr = x + (size_t)row * ne0;
+    const int start = c * chunk, end = min(start + chunk, ne0);
     float best = -INFINITY;
-    int bi = 0;
-    for (int i = threadIdx.x; i < ne0; i += 256) {
+    int bi = start;
+#pragma unroll 8
+    for (int i = start + (int)threadIdx.x; i < end; i += 256) {
         const float v = xr[i];
         if (v > best) { best = v; bi = i; }
     }
-    __shared__ float sv[256];
-    __shared__ int si[256];
-    sv[threadIdx.x] = best;
-    si[threadIdx.x] = bi;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if ((int)threadIdx.x < o) {
-            const float v2 = sv[threadIdx.x + o];
-            const int i2 = si[threadIdx.x + o];
-            if (v2 > sv[threadIdx.x] || (v2 == sv[threadIdx.x] && i2 < si[threadIdx.x])) {
-                sv[threadIdx.x] = v2;
-                si[threadIdx.x] = i2;
-            }
-        }
-        __syncthreads();
+    argmax_block(best, bi);
+    if (threadIdx.x == 0) part[(size_t)row * nchunks + c] = make_float2(best, __int_as_float(bi));
+}
+
+__global__ __launch_bounds__(256) void k_argmax_final(const float2 *__restrict__ part, int32_t *__restrict__ out,
+                                                      int nchunks) {
+    const int row = blockIdx.x;
+    float best = -INFINITY;
+    int bi = INT_MAX;
+    for (int c = threadIdx.x; c < nchunks; c += 256) {
+        const float2 p = part[(size_t)row * nchunks + c];
+        argmax_merge(best, bi, p.x, __float_as_int(p.y));
     }
-    if (threadIdx.x == 0) out[blockIdx.x] = si[0];
+    argmax_block(best, bi);
+    if (threadIdx.x == 0) out[row] = bi == INT_MAX ? 0 : bi;
+}
+
+inline int64_t argmax_chunk(int64_t ne0) {
+    int64_t c = (ne0 + 255) / 256;
+    c = (c + 1023) / 1024 * 1024;
+    return c < 2048 ? 2048 : c;
 }
 
 // fp16 decode mask row from the effective length: 0 for pos < len, -inf beyond
@@ -212,10 +240,27 @@ int mi_swiglu(void *stream, const float *g, const float *u, float *d, int64_t n)
     return MI_OK;
 }
 
-int mi_argmax(void *stream, const float *x, int32_t *out, int64_t ne0, int64_t nrows) {
-    MI_CHECK_ARG(x && out && ne0 > 0 && nrows > 0, "argmax: bad arguments");
-    hipLaunchKernelGGL(k_argmax, dim3((unsigned)nrows), dim3(256), 0, (hipStream_t)stream, x, out, (int)ne0);
-    MI_CHECK_LAUNCH("k_argmax");
+size_t mi_argmax_workspace_size(int64_t ne0, int64_t nrows) {
+    if (ne0 <= 0 || nrows <= 0) return 0;
+    const int64_t nchunks = (ne0 + argmax_chunk(ne0) - 1) / argmax_chunk(ne0);
+    return mi::align_up((size_t)(nchunks * nrows) * sizeof(float2), 256);
+}
+
+int mi_argmax(void *stream, const float *x, int32_t *out, int64_t ne0, int64_t nrows, void *ws, size_t ws_bytes) {
+    MI_CHECK_ARG(x && out && ne0 > 0 && nrows > 0 && ne0 < (1ll << 31) && nrows < 65536, "argmax: bad arguments");
+    const size_t need = mi_argmax_workspace_size(ne0, nrows);
+    if (!ws || ws_bytes < need || !mi::aligned(ws, 8)) {
+        mi::set_error("argmax: workspace %zu < %zu bytes (or misaligned)", ws_bytes, need);
+        return MI_ERR_WORKSPACE;
+    }
+    const int64_t chunk = argmax_chunk(ne0);
+    const int nchunks = (int)((ne0 + chunk - 1) / chunk);
+    hipLaunchKernelGGL(k_argmax_part, dim3((unsigned)nchunks, (unsigned)nrows), dim3(256), 0, (hipStream_t)stream, x,
+                       (float2 *)ws, (int)ne0, (int)chunk, nchunks);
+    MI_CHECK_LAUNCH("k_argmax_part");
+    hipLaunchKernelGGL(k_argmax_final, dim3((unsigned)nrows), dim3(256), 0, (hipStream_t)stream, (const float2 *)ws,
+                       out, nchunks);
+    MI_CHECK_LAUNCH("k_argmax_final");
     return MI_OK;
 }
 

@@ -13,6 +13,7 @@
 #include "mi_common.h"
 
 #include <limits.h>
+#include <math.h>
 #include <string.h>
 
 namespace {
@@ -131,8 +132,8 @@ template <int G, int U, int M>
 __global__ __launch_bounds__(256) void k_gemv_q8_0_xq(const uint8_t *__restrict__ qlo, const uint8_t *__restrict__ qhi,
                                                       const uint16_t *__restrict__ wd,
                                                       const int8_t *__restrict__ xq_qs,
-                                                      const uint16_t *__restrict__ xq_d, float *__restrict__ y, int n,
-                                                      int nb, int m) {
+                                                      const uint16_t *__restrict__ xq_d, float *__restrict__ y,
+                                                      const float *__restrict__ add, int n, int nb, int m) {
     constexpr int RPB = 256 / G;
     const int tid = threadIdx.x;
     const int j = tid % G;
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0_xq(const uint8_t *__restrict_
 #pragma unroll
     for (int i = 0; i < M; i++) {
         const float s = group_sum<G>(acc[i]);
-        if (row_ok && j == 0 && i < m) y[(size_t)i * n + row] = s;
+        if (row_ok && j == 0 && i < m) y[(size_t)i * n + row] = add ? s + add[(size_t)i * n + row] : s;
     }
 }
 
@@ -191,59 +192,81 @@ struct Q8Set {
     const uint8_t *qhi[4];
     const uint16_t *d[4];
     float *y[4];
-    int row_end[4];  // cumulative row counts; unused slots hold INT_MAX
+    const float *add[4];  // vector added to matrix i's results (bias or residual), or null
+    int row_end[4];       // cumulative row counts; unused slots hold INT_MAX
 };
 
 __device__ __forceinline__ int q8set_index(const Q8Set &S, int r) {
     return (r >= S.row_end[0]) + (r >= S.row_end[1]) + (r >= S.row_end[2]);
 }
 
-// Fused activation quantization, one activation row (m == 1), k <= 4096*XN/4:
-// the XN float4 of x (and of inv_s) that a thread quantizes are loaded first,
-// then the weights, so the quantization only waits for the (cache-resident)
-// activation; the weights are still in flight while it runs.
-template <int G, int U, int XN>
-__global__ __launch_bounds__(256) void k_gemv_q8_0_fused1(const Q8Set S, const float *__restrict__ x,
-                                                          const float *__restrict__ inv_s, int n_total, int nb,
-                                                          int rounding) {
-    constexpr int RPB = 256 / G;
-    extern __shared__ __align__(16) uint8_t smem[];
-    int8_t *s_qs = (int8_t *)smem;                                      // [nb*32]
-    float *s_d = (float *)(smem + (((size_t)nb * QK + 15) / 16) * 16);  // [nb]
-    const int tid = threadIdx.x;
-    const int j = tid % G;
-    const int grow = blockIdx.x * RPB + tid / G;
-    const bool row_ok = grow < n_total;
-    const int rc = min(grow, n_total - 1);
-    const int mi = q8set_index(S, rc);
-    const int row = rc - (mi ? S.row_end[mi - 1] : 0);
-    const uint8_t *qlo = mi == 0 ? S.qlo[0] : mi == 1 ? S.qlo[1] : mi == 2 ? S.qlo[2] : S.qlo[3];
-    const uint8_t *qhi = mi == 0 ? S.qhi[0] : mi == 1 ? S.qhi[1] : mi == 2 ? S.qhi[2] : S.qhi[3];
-    const uint16_t *wd = mi == 0 ? S.d[0] : mi == 1 ? S.d[1] : mi == 2 ? S.d[2] : S.d[3];
-    const int k4 = nb * (QK / 4);  // float4 count of x
-    const size_t rbase = (size_t)row * nb;
+__device__ __forceinline__ int q8set_row_start(const Q8Set &S, int i) {
+    return i == 0 ? 0 : i == 1 ? S.row_end[0] : i == 2 ? S.row_end[1] : S.row_end[2];
+}
 
-    float4 xv[XN], sv[XN];
+// member `f` of slot i, selected with constant indices only: indexing the by-value
+// kernel argument through a reference would copy it to scratch memory and turn the
+// weight pointers into flat addresses
+#define Q8SET_PICK(S, f, i) ((i) == 0 ? (S).f[0] : (i) == 1 ? (S).f[1] : (i) == 2 ? (S).f[2] : (S).f[3])
+
+// One activation row staged by a 256-thread workgroup: XN float4 per thread
+// (k <= 1024*XN), loaded before the weights so that the quantization waits only
+// for the cache-resident activation while the weight loads are in flight.
+template <int XN, bool NORM>
+struct XStage {
+    float4 xv[XN], sv[XN], nv[XN];
+};
+
+template <int XN, bool NORM>
+__device__ __forceinline__ void xstage_load(XStage<XN, NORM> &st, const float *__restrict__ x,
+                                            const float *__restrict__ norm_w, const float *__restrict__ inv_s, int k4,
+                                            int tid) {
 #pragma unroll
     for (int t = 0; t < XN; t++) {
         const int f = min(tid + t * 256, k4 - 1);
-        xv[t] = ((const float4 *)x)[f];
-        if (inv_s) sv[t] = ((const float4 *)inv_s)[f];
+        st.xv[t] = ((const float4 *)x)[f];
+        if constexpr (NORM) st.nv[t] = ((const float4 *)norm_w)[f];
+        if (inv_s) st.sv[t] = ((const float4 *)inv_s)[f];
     }
-    int4 lo[U], hi[U];
-    uint32_t dw[U];
+}
+
+// Optional RMSNorm with the norm weight (ggml rms_norm then mul: y = (x*scale)*w,
+// scale = 1/sqrtf(mean + eps), mean = (float)(sum of (double)(x*x) / k)), then the
+// SmoothQuant reciprocal, then Q8_0 quantization of each 32-block into LDS.  The
+// caller puts a barrier between this and the reads of s_qs / s_d.
+template <int XN, bool NORM>
+__device__ __forceinline__ void xstage_quant(XStage<XN, NORM> &st, const float *__restrict__ inv_s, int k4, float eps,
+                                             int rounding, int8_t *s_qs, float *s_d, double *s_red, int tid) {
+    float scale = 1.0f;
+    if constexpr (NORM) {
+        double ss = 0.0;
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-        const int b = min(j + u * G, nb - 1);
-        lo[u] = ld_stream16(qlo + (rbase + b) * 16);
-        hi[u] = ld_stream16(qhi + (rbase + b) * 16);
-        dw[u] = wd[rbase + b];
+        for (int t = 0; t < XN; t++) {
+            if (tid + t * 256 < k4) {
+                const float4 v = st.xv[t];
+                ss += (double)__fmul_rn(v.x, v.x);
+                ss += (double)__fmul_rn(v.y, v.y);
+                ss += (double)__fmul_rn(v.z, v.z);
+                ss += (double)__fmul_rn(v.w, v.w);
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if ((tid & 63) == 0) s_red[tid >> 6] = ss;
+        __syncthreads();
+        const double tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+        const float mean = (float)(tot / (double)(k4 * 4));
+        scale = 1.0f / sqrtf(mean + eps);
     }
 #pragma unroll
     for (int t = 0; t < XN; t++) {
         const int f = tid + t * 256;  // float4 index; 8 consecutive threads form one 32-block
-        float4 v = xv[t];
-        if (inv_s) { v.x *= sv[t].x; v.y *= sv[t].y; v.z *= sv[t].z; v.w *= sv[t].w; }
+        float4 v = st.xv[t];
+        if constexpr (NORM) {
+            v.x = (v.x * scale) * st.nv[t].x; v.y = (v.y * scale) * st.nv[t].y;
+            v.z = (v.z * scale) * st.nv[t].z; v.w = (v.w * scale) * st.nv[t].w;
+        }
+        if (inv_s) { v.x *= st.sv[t].x; v.y *= st.sv[t].y; v.z *= st.sv[t].z; v.w *= st.sv[t].w; }
         float d;
         const uint32_t q = quant4(v.x, v.y, v.z, v.w, rounding, d);
         if (f < k4) {
@@ -251,8 +274,14 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0_fused1(const Q8Set S, const f
             if ((f & 7) == 0) s_d[f >> 3] = h2f(f2h(d));
         }
     }
-    __syncthreads();
+}
 
+// Row dot of one lane over its blocks j, j+G, ...: the first pass's weights were
+// loaded by the caller (before the activation staging).
+template <int G, int U>
+__device__ __forceinline__ float q8_row_dot(const uint8_t *__restrict__ qlo, const uint8_t *__restrict__ qhi,
+                                            const uint16_t *__restrict__ wd, size_t rbase, int nb, int j, int4 (&lo)[U],
+                                            int4 (&hi)[U], uint32_t (&dw)[U], const int8_t *s_qs, const float *s_d) {
     float acc = 0.0f;
 #pragma unroll
     for (int u = 0; u < U; u++) {
@@ -281,10 +310,196 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0_fused1(const Q8Set S, const f
             }
         }
     }
-    const float s = group_sum<G>(acc);
+    return group_sum<G>(acc);
+}
+
+template <int G, int U>
+__device__ __forceinline__ void q8_first_pass(const uint8_t *__restrict__ qlo, const uint8_t *__restrict__ qhi,
+                                              const uint16_t *__restrict__ wd, size_t rbase, int nb, int j,
+                                              int4 (&lo)[U], int4 (&hi)[U], uint32_t (&dw)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int b = min(j + u * G, nb - 1);
+        lo[u] = ld_stream16(qlo + (rbase + b) * 16);
+        hi[u] = ld_stream16(qhi + (rbase + b) * 16);
+        dw[u] = wd[rbase + b];
+    }
+}
+
+// LDS layout of the fused kernels: [nb*32 int8 | nb fp32 scales | 4 doubles | 16 floats]
+inline size_t fused_smem(int nb) { return align_up((size_t)nb * QK, 16) + align_up((size_t)nb * 4, 16) + 32 + 64; }
+
+struct FusedLds {
+    int8_t *qs;
+    float *d;
+    double *red;
+    float *y;
+};
+
+__device__ __forceinline__ FusedLds fused_lds(uint8_t *smem, int nb) {
+    FusedLds L;
+    const size_t o1 = (((size_t)nb * QK + 15) / 16) * 16;
+    const size_t o2 = o1 + (((size_t)nb * 4 + 15) / 16) * 16;
+    L.qs = (int8_t *)smem;
+    L.d = (float *)(smem + o1);
+    L.red = (double *)(smem + o2);
+    L.y = (float *)(smem + o2 + 32);
+    return L;
+}
+
+// Fused activation quantization (optionally after RMSNorm * norm weight), one
+// activation row (m == 1), k <= 1024*XN; results plus the optional add vector.
+template <int G, int U, int XN, bool NORM>
+__global__ __launch_bounds__(256) void k_gemv_q8_0_fused1(const Q8Set S, const float *__restrict__ x,
+                                                          const float *__restrict__ norm_w, float eps,
+                                                          const float *__restrict__ inv_s, int n_total, int nb,
+                                                          int rounding) {
+    constexpr int RPB = 256 / G;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const FusedLds L = fused_lds(smem, nb);
+    const int tid = threadIdx.x;
+    const int j = tid % G;
+    const int grow = blockIdx.x * RPB + tid / G;
+    const bool row_ok = grow < n_total;
+    const int rc = min(grow, n_total - 1);
+    const int mi = q8set_index(S, rc);
+    const int row = rc - q8set_row_start(S, mi);
+    const uint8_t *qlo = Q8SET_PICK(S, qlo, mi);
+    const uint8_t *qhi = Q8SET_PICK(S, qhi, mi);
+    const uint16_t *wd = Q8SET_PICK(S, d, mi);
+    const int k4 = nb * (QK / 4);
+    const size_t rbase = (size_t)row * nb;
+
+    XStage<XN, NORM> st;
+    xstage_load(st, x, norm_w, inv_s, k4, tid);
+    int4 lo[U], hi[U];
+    uint32_t dw[U];
+    q8_first_pass<G, U>(qlo, qhi, wd, rbase, nb, j, lo, hi, dw);
+    xstage_quant(st, inv_s, k4, eps, rounding, L.qs, L.d, L.red, tid);
+    __syncthreads();
+    const float s = q8_row_dot<G, U>(qlo, qhi, wd, rbase, nb, j, lo, hi, dw, L.qs, L.d);
     if (row_ok && j == 0) {
-        float *y = mi == 0 ? S.y[0] : mi == 1 ? S.y[1] : mi == 2 ? S.y[2] : S.y[3];
-        y[row] = s;
+        const float *add = Q8SET_PICK(S, add, mi);
+        Q8SET_PICK(S, y, mi)[row] = add ? s + add[row] : s;
+    }
+}
+
+// q/k/v projections with the rest of the attention-input chain fused in: bias add,
+// neox RoPE of q and k (theta_i = pos * theta_scale^i by repeated multiplication,
+// products unfused as in the CPU loop), q written fp32, k and v converted to fp16
+// into their cache row.  16 lanes per row, 16 rows per workgroup; a workgroup on
+// the rotated rows owns 8 rotation pairs (i, i + hd/2) of one head, so each pair's
+// two results meet in LDS.
+struct RopeKV {
+    const float *bias[3];
+    float *q_out;
+    uint8_t *k_cache, *v_cache;
+    size_t k_row_bytes, v_row_bytes;
+    const int32_t *pos;
+    const void *kv_idx;
+    int kv_idx_i64;
+    int64_t n_cache_rows;
+    int hd, n_q, n_k, n_v;
+    float theta_scale, freq_scale, attn_factor;
+};
+
+template <int G, int U, int XN, bool NORM>
+__global__ __launch_bounds__(256) void k_gemv_q8_0_qkv_rope(const Q8Set S, const RopeKV R, const float *__restrict__ x,
+                                                            const float *__restrict__ norm_w, float eps,
+                                                            const float *__restrict__ inv_s, int nb, int rounding) {
+    constexpr int RPB = 256 / G;   // rows per workgroup
+    constexpr int HALF = RPB / 2;  // rotation pairs per workgroup
+    extern __shared__ __align__(16) uint8_t smem[];
+    const FusedLds L = fused_lds(smem, nb);
+    const int tid = threadIdx.x;
+    const int j = tid % G;
+    const int t = tid / G;
+    const int n_rope = R.n_q + R.n_k;
+    const int n_total = n_rope + R.n_v;
+    const int wg_per_head = R.hd / RPB;
+    const int b = blockIdx.x;
+    const bool rope = b < n_rope / RPB;
+    const int head = b / wg_per_head, chunk = b % wg_per_head;
+    const int grow = rope ? head * R.hd + (t / HALF) * (R.hd / 2) + chunk * HALF + (t % HALF) : b * RPB + t;
+    const int rc = min(grow, n_total - 1);
+    const int mi = q8set_index(S, rc);
+    const int row = rc - q8set_row_start(S, mi);
+    const uint8_t *qlo = Q8SET_PICK(S, qlo, mi);
+    const uint8_t *qhi = Q8SET_PICK(S, qhi, mi);
+    const uint16_t *wd = Q8SET_PICK(S, d, mi);
+    const int k4 = nb * (QK / 4);
+    const size_t rbase = (size_t)row * nb;
+
+    XStage<XN, NORM> st;
+    xstage_load(st, x, norm_w, inv_s, k4, tid);
+    int4 lo[U], hi[U];
+    uint32_t dw[U];
+    q8_first_pass<G, U>(qlo, qhi, wd, rbase, nb, j, lo, hi, dw);
+    xstage_quant(st, inv_s, k4, eps, rounding, L.qs, L.d, L.red, tid);
+    __syncthreads();
+    const float s = q8_row_dot<G, U>(qlo, qhi, wd, rbase, nb, j, lo, hi, dw, L.qs, L.d);
+    if (j == 0) {
+        const float *bias = mi == 0 ? R.bias[0] : mi == 1 ? R.bias[1] : R.bias[2];
+        L.y[t] = bias ? s + bias[row] : s;
+    }
+    __syncthreads();
+    const int64_t ci = R.kv_idx_i64 ? ((const int64_t *)R.kv_idx)[0] : (int64_t)((const int32_t *)R.kv_idx)[0];
+    const bool ci_ok = ci >= 0 && ci < R.n_cache_rows;
+    if (rope) {
+        if (tid < HALF) {
+            const int p = chunk * HALF + tid;  // rotation pair index < hd/2
+            float theta = (float)R.pos[0];
+            for (int i = 0; i < p; i++) theta *= R.theta_scale;
+            const float th = R.freq_scale * theta;
+            const float cs = cosf(th) * R.attn_factor;
+            const float sn = sinf(th) * R.attn_factor;
+            const float x0 = L.y[tid], x1 = L.y[tid + HALF];
+            const float y0 = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn));
+            const float y1 = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs));
+            const int r0 = head * R.hd + p;  // row in the stacked q|k space
+            if (r0 < R.n_q) {
+                R.q_out[r0] = y0;
+                R.q_out[r0 + R.hd / 2] = y1;
+            } else if (ci_ok) {
+                uint16_t *kr = (uint16_t *)(R.k_cache + (size_t)ci * R.k_row_bytes);
+                kr[r0 - R.n_q] = f2h(y0);
+                kr[r0 - R.n_q + R.hd / 2] = f2h(y1);
+            }
+        }
+    } else if (tid < RPB) {
+        const int vr = b * RPB + tid - n_rope;
+        if (vr < R.n_v && ci_ok) ((uint16_t *)(R.v_cache + (size_t)ci * R.v_row_bytes))[vr] = f2h(L.y[tid]);
+    }
+}
+
+// silu(g) * u (ggml swiglu: silu(x) = x / (1 + expf(-x))), times the SmoothQuant
+// reciprocal of the next projection, quantized to Q8_0: the GLU node and the down
+// projection's activation quantization in one pass.  grid: ceil(nblocks / 32) x 256.
+__global__ __launch_bounds__(256) void k_swiglu_quant_q8_0(const float *__restrict__ g, const float *__restrict__ u,
+                                                           const float *__restrict__ inv_s, int8_t *__restrict__ qs,
+                                                           uint16_t *__restrict__ dout, int64_t total_blocks,
+                                                           int rounding) {
+    const int64_t blk = (int64_t)blockIdx.x * 32 + threadIdx.x / 8;
+    const int sub = threadIdx.x % 8;
+    const bool valid = blk < total_blocks;
+    const int64_t e = (valid ? blk : 0) * QK + sub * 4;
+    float4 gv = make_float4(0.f, 0.f, 0.f, 0.f), uv = gv, sv = make_float4(1.f, 1.f, 1.f, 1.f);
+    if (valid) {
+        gv = *(const float4 *)(g + e);
+        uv = *(const float4 *)(u + e);
+        if (inv_s) sv = *(const float4 *)(inv_s + e);
+    }
+    float4 v;
+    v.x = (gv.x / (1.0f + expf(-gv.x))) * uv.x;
+    v.y = (gv.y / (1.0f + expf(-gv.y))) * uv.y;
+    v.z = (gv.z / (1.0f + expf(-gv.z))) * uv.z;
+    v.w = (gv.w / (1.0f + expf(-gv.w))) * uv.w;
+    if (inv_s) { v.x *= sv.x; v.y *= sv.y; v.z *= sv.z; v.w *= sv.w; }
+    float d;
+    const uint32_t q = quant4(v.x, v.y, v.z, v.w, rounding, d);
+    if (valid) {
+        *(uint32_t *)(qs + e) = q;
+        if (sub == 0) dout[blk] = f2h(d);
     }
 }
 
@@ -320,22 +535,40 @@ inline int pick_u(int64_t nb, int g) {
 
 inline int pick_g(int64_t nb) { return nb <= 128 ? 16 : (nb <= 256 ? 32 : 64); }
 
+// Lanes per row for a launch of n_rows rows: with MI_GEMV_MIN_WG=<n> set, wider rows
+// (fewer rows per workgroup) until the grid has n workgroups.  Off by default: the
+// small decode projections are bound by the latency chain of each workgroup (the
+// activation staging is repeated per workgroup), not by the number of CUs in use.
+inline int gemv_min_wg() {
+    static const int v = [] {
+        const char *e = getenv("MI_GEMV_MIN_WG");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
+inline int pick_g_rows(int64_t nb, int64_t n_rows) {
+    int g = pick_g(nb);
+    while (g < 64 && (n_rows + 256 / g - 1) / (256 / g) < gemv_min_wg()) g *= 2;
+    return g;
+}
+
 template <int G, int U, int M>
 int launch_xq_gu(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
-                 const uint16_t *xq_d, float *y) {
+                 const uint16_t *xq_d, float *y, const float *add) {
     const Q8Planes p = q8_planes(n, k);
     constexpr int RPB = 256 / G;
     hipLaunchKernelGGL((k_gemv_q8_0_xq<G, U, M>), dim3((unsigned)((n + RPB - 1) / RPB)), dim3(256), 0, st, base,
-                       base + p.plane, (const uint16_t *)(base + 2 * p.plane), xq_qs, xq_d, y, (int)n, (int)(k / QK),
-                       (int)m);
+                       base + p.plane, (const uint16_t *)(base + 2 * p.plane), xq_qs, xq_d, y, add, (int)n,
+                       (int)(k / QK), (int)m);
     MI_CHECK_LAUNCH("k_gemv_q8_0_xq");
     return MI_OK;
 }
 
 template <int G, int M>
 int launch_xq_g(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
-                const uint16_t *xq_d, float *y) {
-#define MI_U_CASE(UU) case UU: return launch_xq_gu<G, UU, M>(st, base, n, k, m, xq_qs, xq_d, y);
+                const uint16_t *xq_d, float *y, const float *add) {
+#define MI_U_CASE(UU) case UU: return launch_xq_gu<G, UU, M>(st, base, n, k, m, xq_qs, xq_d, y, add);
     switch (pick_u(k / QK, G)) {
         MI_U_CASE(1) MI_U_CASE(2) MI_U_CASE(3) MI_U_CASE(4) MI_U_CASE(5) MI_U_CASE(6) MI_U_CASE(7) MI_U_CASE(8)
     }
@@ -345,40 +578,40 @@ int launch_xq_g(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64
 
 template <int M>
 int launch_xq_m(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
-                const uint16_t *xq_d, float *y) {
+                const uint16_t *xq_d, float *y, const float *add) {
     switch (pick_g(k / QK)) {
-        case 16: return launch_xq_g<16, M>(st, base, n, k, m, xq_qs, xq_d, y);
-        case 32: return launch_xq_g<32, M>(st, base, n, k, m, xq_qs, xq_d, y);
-        default: return launch_xq_g<64, M>(st, base, n, k, m, xq_qs, xq_d, y);
+        case 16: return launch_xq_g<16, M>(st, base, n, k, m, xq_qs, xq_d, y, add);
+        case 32: return launch_xq_g<32, M>(st, base, n, k, m, xq_qs, xq_d, y, add);
+        default: return launch_xq_g<64, M>(st, base, n, k, m, xq_qs, xq_d, y, add);
     }
 }
 
 int launch_xq(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const int8_t *xq_qs,
-              const uint16_t *xq_d, float *y) {
-    if (m == 1) return launch_xq_m<1>(st, base, n, k, m, xq_qs, xq_d, y);
-    if (m == 2) return launch_xq_m<2>(st, base, n, k, m, xq_qs, xq_d, y);
-    if (m >= 3 && m <= 4) return launch_xq_m<4>(st, base, n, k, m, xq_qs, xq_d, y);
-    if (m >= 5 && m <= 8) return launch_xq_m<8>(st, base, n, k, m, xq_qs, xq_d, y);
+              const uint16_t *xq_d, float *y, const float *add = nullptr) {
+    if (m == 1) return launch_xq_m<1>(st, base, n, k, m, xq_qs, xq_d, y, add);
+    if (m == 2) return launch_xq_m<2>(st, base, n, k, m, xq_qs, xq_d, y, add);
+    if (m >= 3 && m <= 4) return launch_xq_m<4>(st, base, n, k, m, xq_qs, xq_d, y, add);
+    if (m >= 5 && m <= 8) return launch_xq_m<8>(st, base, n, k, m, xq_qs, xq_d, y, add);
     set_error("gemv_q8_0: m=%lld not in 1..8", (long long)m);
     return MI_ERR_ARG;
 }
 
-template <int G, int U, int XN>
-int launch_fused_gux(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *x, const float *inv_s,
-                     int rounding) {
+template <int G, int U, int XN, bool NORM>
+int launch_fused_gux(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *x, const float *norm_w,
+                     float eps, const float *inv_s, int rounding) {
     constexpr int RPB = 256 / G;
     const int nb = (int)(k / QK);
-    const size_t smem = align_up((size_t)k, 16) + (size_t)nb * sizeof(float);
-    hipLaunchKernelGGL((k_gemv_q8_0_fused1<G, U, XN>), dim3((unsigned)((n_total + RPB - 1) / RPB)), dim3(256), smem,
-                       st, S, x, inv_s, n_total, nb, rounding);
+    hipLaunchKernelGGL((k_gemv_q8_0_fused1<G, U, XN, NORM>), dim3((unsigned)((n_total + RPB - 1) / RPB)), dim3(256),
+                       fused_smem(nb), st, S, x, norm_w, eps, inv_s, n_total, nb, rounding);
     MI_CHECK_LAUNCH("k_gemv_q8_0_fused1");
     return MI_OK;
 }
 
-template <int G, int XN>
-int launch_fused_gx(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *x, const float *inv_s,
-                    int rounding) {
-#define MI_U_CASE(UU) case UU: return launch_fused_gux<G, UU, XN>(st, S, n_total, k, x, inv_s, rounding);
+template <int G, int XN, bool NORM>
+int launch_fused_gx(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *x, const float *norm_w,
+                    float eps, const float *inv_s, int rounding) {
+#define MI_U_CASE(UU) \
+    case UU: return launch_fused_gux<G, UU, XN, NORM>(st, S, n_total, k, x, norm_w, eps, inv_s, rounding);
     switch (pick_u(k / QK, G)) {
         MI_U_CASE(1) MI_U_CASE(2) MI_U_CASE(3) MI_U_CASE(4) MI_U_CASE(5) MI_U_CASE(6) MI_U_CASE(7) MI_U_CASE(8)
     }
@@ -386,26 +619,77 @@ int launch_fused_gx(hipStream_t st, const Q8Set &S, int n_total, int64_t k, cons
     return MI_ERR_ARG;
 }
 
-template <int XN>
-int launch_fused_x(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *x, const float *inv_s,
-                   int rounding) {
-    switch (pick_g(k / QK)) {
-        case 16: return launch_fused_gx<16, XN>(st, S, n_total, k, x, inv_s, rounding);
-        case 32: return launch_fused_gx<32, XN>(st, S, n_total, k, x, inv_s, rounding);
-        default: return launch_fused_gx<64, XN>(st, S, n_total, k, x, inv_s, rounding);
+template <int XN, bool NORM>
+int launch_fused_x(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *x, const float *norm_w,
+                   float eps, const float *inv_s, int rounding) {
+    switch (pick_g_rows(k / QK, n_total)) {
+        case 16: return launch_fused_gx<16, XN, NORM>(st, S, n_total, k, x, norm_w, eps, inv_s, rounding);
+        case 32: return launch_fused_gx<32, XN, NORM>(st, S, n_total, k, x, norm_w, eps, inv_s, rounding);
+        default: return launch_fused_gx<64, XN, NORM>(st, S, n_total, k, x, norm_w, eps, inv_s, rounding);
     }
 }
 
-// one activation row with k <= 4096 (16 floats per thread): single fused launch
-int launch_fused(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *x, const float *inv_s,
-                 int rounding) {
+template <bool NORM>
+int launch_fused_n(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *x, const float *norm_w,
+                   float eps, const float *inv_s, int rounding) {
     const int64_t xn = (k / 4 + 255) / 256;
-    if (xn <= 1) return launch_fused_x<1>(st, S, n_total, k, x, inv_s, rounding);
-    if (xn <= 2) return launch_fused_x<2>(st, S, n_total, k, x, inv_s, rounding);
-    return launch_fused_x<4>(st, S, n_total, k, x, inv_s, rounding);
+    if (xn <= 1) return launch_fused_x<1, NORM>(st, S, n_total, k, x, norm_w, eps, inv_s, rounding);
+    if (xn <= 2) return launch_fused_x<2, NORM>(st, S, n_total, k, x, norm_w, eps, inv_s, rounding);
+    return launch_fused_x<4, NORM>(st, S, n_total, k, x, norm_w, eps, inv_s, rounding);
 }
 
-int make_set(Q8Set &S, int count, const void *const *w, const int64_t *n, float *const *y, int64_t k, int &n_total) {
+// one activation row with k <= 4096 (16 floats per thread): single fused launch
+int launch_fused(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *x, const float *norm_w,
+                 float eps, const float *inv_s, int rounding) {
+    if (norm_w) return launch_fused_n<true>(st, S, n_total, k, x, norm_w, eps, inv_s, rounding);
+    return launch_fused_n<false>(st, S, n_total, k, x, nullptr, eps, inv_s, rounding);
+}
+
+template <int G, int U, int XN, bool NORM>
+int launch_qkv_gu(hipStream_t st, const Q8Set &S, const RopeKV &R, int64_t k, const float *x, const float *norm_w,
+                  float eps, const float *inv_s, int rounding) {
+    constexpr int RPB = 256 / G;
+    const int nb = (int)(k / QK);
+    const int n_rope = R.n_q + R.n_k;
+    const unsigned grid = (unsigned)(n_rope / RPB + (R.n_v + RPB - 1) / RPB);
+    hipLaunchKernelGGL((k_gemv_q8_0_qkv_rope<G, U, XN, NORM>), dim3(grid), dim3(256), fused_smem(nb), st, S, R, x,
+                       norm_w, eps, inv_s, nb, rounding);
+    MI_CHECK_LAUNCH("k_gemv_q8_0_qkv_rope");
+    return MI_OK;
+}
+
+template <int G, int XN, bool NORM>
+int launch_qkv_gx(hipStream_t st, const Q8Set &S, const RopeKV &R, int64_t k, const float *x, const float *norm_w,
+                  float eps, const float *inv_s, int rounding) {
+#define MI_U_CASE(UU) case UU: return launch_qkv_gu<G, UU, XN, NORM>(st, S, R, k, x, norm_w, eps, inv_s, rounding);
+    switch (pick_u(k / QK, G)) {
+        MI_U_CASE(1) MI_U_CASE(2) MI_U_CASE(3) MI_U_CASE(4) MI_U_CASE(5) MI_U_CASE(6) MI_U_CASE(7) MI_U_CASE(8)
+    }
+#undef MI_U_CASE
+    return MI_ERR_ARG;
+}
+
+template <int XN, bool NORM>
+int launch_qkv_x(hipStream_t st, int g, const Q8Set &S, const RopeKV &R, int64_t k, const float *x,
+                 const float *norm_w, float eps, const float *inv_s, int rounding) {
+    switch (g) {
+        case 16: return launch_qkv_gx<16, XN, NORM>(st, S, R, k, x, norm_w, eps, inv_s, rounding);
+        case 32: return launch_qkv_gx<32, XN, NORM>(st, S, R, k, x, norm_w, eps, inv_s, rounding);
+        default: return launch_qkv_gx<64, XN, NORM>(st, S, R, k, x, norm_w, eps, inv_s, rounding);
+    }
+}
+
+template <bool NORM>
+int launch_qkv_n(hipStream_t st, int g, const Q8Set &S, const RopeKV &R, int64_t k, const float *x,
+                 const float *norm_w, float eps, const float *inv_s, int rounding) {
+    const int64_t xn = (k / 4 + 255) / 256;
+    if (xn <= 1) return launch_qkv_x<1, NORM>(st, g, S, R, k, x, norm_w, eps, inv_s, rounding);
+    if (xn <= 2) return launch_qkv_x<2, NORM>(st, g, S, R, k, x, norm_w, eps, inv_s, rounding);
+    return launch_qkv_x<4, NORM>(st, g, S, R, k, x, norm_w, eps, inv_s, rounding);
+}
+
+int make_set(Q8Set &S, int count, const void *const *w, const int64_t *n, float *const *y, int64_t k, int &n_total,
+             const float *const *add = nullptr) {
     MI_CHECK_ARG(count >= 1 && count <= 4, "mul_mat_q8_0: %d matrices (1..4 supported)", count);
     int64_t acc = 0;
     for (int i = 0; i < 4; i++) {
@@ -418,6 +702,7 @@ int make_set(Q8Set &S, int count, const void *const *w, const int64_t *n, float 
             S.qhi[i] = base + p.plane;
             S.d[i] = (const uint16_t *)(base + 2 * p.plane);
             S.y[i] = y[i];
+            S.add[i] = add ? add[i] : nullptr;
             acc += n[i];
             S.row_end[i] = (int)acc;
         } else {
@@ -425,6 +710,7 @@ int make_set(Q8Set &S, int count, const void *const *w, const int64_t *n, float 
             S.qhi[i] = S.qhi[0];
             S.d[i] = S.d[0];
             S.y[i] = S.y[0];
+            S.add[i] = nullptr;
             S.row_end[i] = INT_MAX;
         }
     }
@@ -531,7 +817,7 @@ int mi_mul_mat_q8_0_f32_multi(void *stream, int n_mats, const void *const *w_pac
     int n_total = 0;
     if (int r = make_set(S, n_mats, w_packed, n, y, k, n_total)) return r;
     hipStream_t st = (hipStream_t)stream;
-    if (k <= 4096) return launch_fused(st, S, n_total, k, x, inv_s, rounding);
+    if (k <= 4096) return launch_fused(st, S, n_total, k, x, nullptr, 0.0f, inv_s, rounding);
     const size_t need = mi_xq_size(1, k);
     if (!ws || ws_bytes < need || !mi::aligned(ws, 16)) {
         mi::set_error("mul_mat_q8_0_f32_multi: workspace %zu < %zu bytes (or misaligned)", ws_bytes, need);
@@ -558,6 +844,91 @@ int mi_mul_mat_q8_0_f32(void *stream, const void *w_packed, const float *x, cons
     }
     if (int r = mi_act_quant_q8_0(stream, x, inv_s, m, k, ws, rounding)) return r;
     return mi_gemv_q8_0(stream, w_packed, ws, y, n, k, m);
+}
+
+int mi_mul_mat_q8_0_f32_fused(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
+                              float *const *y, const float *const *add, int64_t k, const float *x,
+                              const float *norm_w, float eps, const float *inv_s, int rounding) {
+    MI_CHECK_ARG(w_packed && n && y && x, "mul_mat_q8_0_f32_fused: null pointer");
+    if (int r = check_shape("mul_mat_q8_0_f32_fused", 1, k)) return r;
+    MI_CHECK_ARG(k <= 4096, "mul_mat_q8_0_f32_fused: k=%lld > 4096", (long long)k);
+    MI_CHECK_ARG(mi::aligned(x, 16) && (!inv_s || mi::aligned(inv_s, 16)) && (!norm_w || mi::aligned(norm_w, 16)),
+                 "mul_mat_q8_0_f32_fused: x/norm_w/inv_s must be 16-byte aligned");
+    Q8Set S;
+    int n_total = 0;
+    if (int r = make_set(S, n_mats, w_packed, n, y, k, n_total, add)) return r;
+    return launch_fused((hipStream_t)stream, S, n_total, k, x, norm_w, eps, inv_s, rounding);
+}
+
+int mi_qkv_rope_kv_q8_0(void *stream, const void *const *w_packed, const int64_t *n, const float *const *bias,
+                        int64_t k, const float *x, const float *norm_w, float eps, const float *inv_s, int rounding,
+                        int64_t head_dim, const int32_t *pos, float freq_base, float freq_scale, float attn_factor,
+                        float *q_out, void *k_cache, size_t k_row_bytes, void *v_cache, size_t v_row_bytes,
+                        const void *kv_idx, int kv_idx_is_i64, int64_t n_cache_rows) {
+    MI_CHECK_ARG(w_packed && n && bias && x && pos && q_out && k_cache && v_cache && kv_idx,
+                 "qkv_rope_kv_q8_0: null pointer");
+    if (int r = check_shape("qkv_rope_kv_q8_0", 1, k)) return r;
+    MI_CHECK_ARG(k <= 4096, "qkv_rope_kv_q8_0: k=%lld > 4096", (long long)k);
+    MI_CHECK_ARG(head_dim >= 16 && head_dim % 16 == 0 && head_dim <= 1024, "qkv_rope_kv_q8_0: head_dim %lld",
+                 (long long)head_dim);
+    MI_CHECK_ARG(n[0] > 0 && n[1] > 0 && n[2] > 0 && n[0] % head_dim == 0 && n[1] % head_dim == 0,
+                 "qkv_rope_kv_q8_0: q/k rows must be whole heads");
+    MI_CHECK_ARG(k_row_bytes >= (size_t)n[1] * 2 && v_row_bytes >= (size_t)n[2] * 2 && n_cache_rows > 0,
+                 "qkv_rope_kv_q8_0: cache rows too short");
+    MI_CHECK_ARG(mi::aligned(x, 16) && (!inv_s || mi::aligned(inv_s, 16)) && (!norm_w || mi::aligned(norm_w, 16)),
+                 "qkv_rope_kv_q8_0: x/norm_w/inv_s must be 16-byte aligned");
+    float *ys[3] = {q_out, q_out, q_out};  // unused by the kernel: results go through the epilogue
+    Q8Set S;
+    int n_total = 0;
+    if (int r = make_set(S, 3, w_packed, n, ys, k, n_total)) return r;
+    RopeKV R;
+    for (int i = 0; i < 3; i++) R.bias[i] = bias[i];
+    R.q_out = q_out;
+    R.k_cache = (uint8_t *)k_cache;
+    R.v_cache = (uint8_t *)v_cache;
+    R.k_row_bytes = k_row_bytes;
+    R.v_row_bytes = v_row_bytes;
+    R.pos = pos;
+    R.kv_idx = kv_idx;
+    R.kv_idx_i64 = kv_idx_is_i64;
+    R.n_cache_rows = n_cache_rows;
+    R.hd = (int)head_dim;
+    R.n_q = (int)n[0];
+    R.n_k = (int)n[1];
+    R.n_v = (int)n[2];
+    // theta_scale on the host with the C library powf, as the CPU rope cache does
+    R.theta_scale = powf(freq_base, -2.0f / (float)head_dim);
+    R.freq_scale = freq_scale;
+    R.attn_factor = attn_factor;
+    hipStream_t st = (hipStream_t)stream;
+    int g = pick_g_rows(k / QK, n_total);
+    while (g > 16 && head_dim % (256 / g) != 0) g /= 2;  // a workgroup's rows must tile the heads
+    if (norm_w) return launch_qkv_n<true>(st, g, S, R, k, x, norm_w, eps, inv_s, rounding);
+    return launch_qkv_n<false>(st, g, S, R, k, x, nullptr, eps, inv_s, rounding);
+}
+
+int mi_swiglu_quant_q8_0(void *stream, const float *g, const float *u, const float *inv_s, int64_t k, void *xq,
+                         int rounding) {
+    if (int r = check_shape("swiglu_quant_q8_0", 1, k)) return r;
+    MI_CHECK_ARG(g && u && xq, "swiglu_quant_q8_0: null pointer");
+    MI_CHECK_ARG(mi::aligned(g, 16) && mi::aligned(u, 16) && mi::aligned(xq, 16) && (!inv_s || mi::aligned(inv_s, 16)),
+                 "swiglu_quant_q8_0: pointers must be 16-byte aligned");
+    const int64_t nb = k / QK;
+    uint8_t *base = (uint8_t *)xq;
+    hipLaunchKernelGGL(k_swiglu_quant_q8_0, dim3((unsigned)((nb + 31) / 32)), dim3(256), 0, (hipStream_t)stream, g, u,
+                       inv_s, (int8_t *)base, (uint16_t *)(base + mi_xq_d_offset(1, k)), nb, rounding);
+    MI_CHECK_LAUNCH("k_swiglu_quant_q8_0");
+    return MI_OK;
+}
+
+int mi_gemv_q8_0_add(void *stream, const void *w_packed, const void *xq, const float *add, float *y, int64_t n,
+                     int64_t k, int64_t m) {
+    if (int r = check_shape("gemv_q8_0_add", n, k)) return r;
+    MI_CHECK_ARG(w_packed && xq && y, "gemv_q8_0_add: null pointer");
+    MI_CHECK_ARG(mi::aligned(w_packed, 256) && mi::aligned(xq, 16), "gemv_q8_0_add: w_packed must be 256-byte, xq 16-byte aligned");
+    const uint8_t *xb = (const uint8_t *)xq;
+    return launch_xq((hipStream_t)stream, (const uint8_t *)w_packed, n, k, m, (const int8_t *)xb,
+                     (const uint16_t *)(xb + mi_xq_d_offset(m, k)), y, add);
 }
 
 int mi_q8_0_block_dots(void *stream, const void *w_packed, const void *xq, int32_t *out, int64_t n, int64_t k) {

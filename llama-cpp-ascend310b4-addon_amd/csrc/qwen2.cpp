@@ -105,6 +105,9 @@ Graph build_graph(mi_qwen2 *m, int n_kv) {
             Q = ggml_add(ctx, Q, W(m, p + "attn_q.bias"));
             K = ggml_add(ctx, K, W(m, p + "attn_k.bias"));
             V = ggml_add(ctx, V, W(m, p + "attn_v.bias"));
+            ggml_build_forward_expand(gf, Q);  // bias adds adjacent, in q/k/v order
+            ggml_build_forward_expand(gf, K);
+            ggml_build_forward_expand(gf, V);
         }
         Q = ggml_reshape_3d(ctx, Q, hd, hp.n_head, 1);
         K = ggml_reshape_3d(ctx, K, hd, hp.n_head_kv, 1);
@@ -112,6 +115,8 @@ Graph build_graph(mi_qwen2 *m, int n_kv) {
                           0.0f);
         K = ggml_rope_ext(ctx, K, pos, nullptr, hd, GGML_ROPE_TYPE_NEOX, 0, hp.rope_theta, 1.0f, 0.0f, 1.0f, 0.0f,
                           0.0f);
+        ggml_build_forward_expand(gf, Q);  // rope q, rope k, then the two cache writes: the
+        ggml_build_forward_expand(gf, K);  // attention-input chain the backend fuses
         ggml_tensor *kc = m->k_cache[il], *vc = m->v_cache[il];
         ggml_build_forward_expand(gf, ggml_set_rows(ctx, kc, ggml_reshape_2d(ctx, K, n_embd_kv, 1), kidx));
         ggml_build_forward_expand(gf, ggml_set_rows(ctx, vc, V, kidx));

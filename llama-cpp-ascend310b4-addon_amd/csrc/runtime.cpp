@@ -148,7 +148,7 @@ int mi_graph_capture_end(void *stream, void **graph_exec) {
     HIP_RET(hipStreamEndCapture((hipStream_t)stream, &g), "hipStreamEndCapture");
     hipGraphExec_t ge = nullptr;
     hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
-    hipGraphDestroy(g);
+    (void)hipGraphDestroy(g);
     if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
     *graph_exec = (void *)ge;
     return MI_OK;

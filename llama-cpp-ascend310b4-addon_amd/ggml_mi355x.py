@@ -91,7 +91,13 @@ _SIGS = {
     "mi_set_rows_f16": (_I, [_P, _P, _P, _I, _P, _I64, _I64, _SZ, _SZ, _I64]),
     "mi_get_rows": (_I, [_P, _P, _I, _P, _P, _I64, _I64, _SZ, _I64]),
     "mi_swiglu": (_I, [_P, _P, _P, _P, _I64]),
-    "mi_argmax": (_I, [_P, _P, _P, _I64, _I64]),
+    "mi_argmax_workspace_size": (_SZ, [_I64, _I64]),
+    "mi_argmax": (_I, [_P, _P, _P, _I64, _I64, _P, _SZ]),
+    "mi_mul_mat_q8_0_f32_fused": (_I, [_P, _I, _P, _P, _P, _P, _I64, _P, _P, _F, _P, _I]),
+    "mi_qkv_rope_kv_q8_0": (_I, [_P, _P, _P, _P, _I64, _P, _P, _F, _P, _I, _I64, _P, _F, _F, _F, _P, _P, _SZ, _P, _SZ,
+                                 _P, _I, _I64]),
+    "mi_swiglu_quant_q8_0": (_I, [_P, _P, _P, _P, _I64, _P, _I]),
+    "mi_gemv_q8_0_add": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64]),
     "mi_fill_mask_f16": (_I, [_P, _P, _P, _I64]),
 }
 

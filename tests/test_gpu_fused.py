@@ -1,0 +1,266 @@
+"""GPU parity of the decode-graph glue kernels and of the fused decode chains, called
+through the C ABI, against numpy restatements of the ggml-CPU ops (ggml/src/ggml-cpu/ops.cpp
+of llama.cpp @ 37b3a9e0) composed with the oracle's Q8_0 matmul.
+
+Bars: RMSNorm within 1 ulp (the double sum's order differs); RoPE within 2e-6 relative
+(device cosf/sinf against the host's); ARGMAX exact (first maximum); SwiGLU+quantize
+with Q8_0 scales exact and at most one int8 step on <0.1% of the elements (device expf
+is not the host's); fused GEMV chains within the GEMV bar (1e-3 relative); fp16 cache
+rows within 2 fp16 ulps of the reference; cache rows other than the target untouched.
+"""
+import numpy as np
+import pytest
+
+from synth import f16_bits, q8_0_weights, rel_err, xq_to_blocks
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-3
+F32 = np.float32
+
+
+def rms_norm_ref(x, w, eps):
+    """ggml rms_norm then mul: (float)(sum of (double)(x*x) / n), y = (x * scale) * w"""
+    x = np.asarray(x, F32)
+    sq = (x * x).astype(np.float64)
+    mean = F32(np.sum(sq) / x.size)
+    scale = F32(1.0) / np.sqrt(F32(mean + F32(eps)))
+    y = (x * scale).astype(F32)
+    return (y * w).astype(F32) if w is not None else y
+
+
+def rope_neox_ref(x, pos, hd, base):
+    """x [heads, hd] fp32; theta_i = pos * theta_scale^i by repeated float multiplication"""
+    ts = F32(np.power(F32(base), F32(-2.0) / F32(hd)))
+    th = np.empty(hd // 2, F32)
+    t = F32(pos)
+    for i in range(hd // 2):
+        th[i] = t
+        t = F32(t * ts)
+    c = np.cos(th.astype(np.float64)).astype(F32)
+    s = np.sin(th.astype(np.float64)).astype(F32)
+    x0, x1 = x[:, : hd // 2], x[:, hd // 2:]
+    return np.concatenate([(x0 * c - x1 * s).astype(F32), (x0 * s + x1 * c).astype(F32)], axis=1)
+
+
+def _packed_q8(mi, w, n, k):
+    src = mi.to_device(w)
+    dst = mi.DeviceBuffer(mi.q8_0_packed_size(n, k)).zero()
+    mi.prepack_q8_0(src.ptr, dst.ptr, n, k)
+    mi.device_sync()
+    src.free()
+    return dst
+
+
+def _ptrs(*bufs):
+    import ctypes
+    return (ctypes.c_void_p * len(bufs))(*[b.ptr if b is not None else None for b in bufs])
+
+
+def _i64s(*v):
+    import ctypes
+    return (ctypes.c_int64 * len(v))(*v)
+
+
+def ulp_diff(a, b):
+    ai = np.asarray(a, F32).view(np.int32).astype(np.int64)
+    bi = np.asarray(b, F32).view(np.int32).astype(np.int64)
+    return np.abs(ai - bi)
+
+
+# ---------------------------------------------------------------- glue kernels
+
+@pytest.mark.parametrize("ne0,nrows", [(1536, 1), (3584, 2), (96, 3)])
+def test_rms_norm(gpu, ne0, nrows):
+    mi = gpu
+    rng = np.random.default_rng(ne0)
+    x = (rng.standard_normal((nrows, ne0)) * 0.3).astype(F32)
+    w = rng.uniform(0.8, 1.2, ne0).astype(F32)
+    dx, dw, dy = mi.to_device(x), mi.to_device(w), mi.DeviceBuffer(x.nbytes)
+    mi._call("mi_rms_norm", None, mi._P(dx.ptr), mi._P(dw.ptr), mi._P(dy.ptr), ne0, nrows, F32(1e-6))
+    mi.device_sync()
+    y = dy.download(F32).reshape(nrows, ne0)
+    for r in range(nrows):
+        assert ulp_diff(y[r], rms_norm_ref(x[r], w, 1e-6)).max() <= 1
+
+
+@pytest.mark.parametrize("hd,heads,pos", [(128, 12, 0), (128, 2, 517), (64, 4, 32767)])
+def test_rope_neox(gpu, hd, heads, pos):
+    mi = gpu
+    rng = np.random.default_rng(pos + hd)
+    x = rng.standard_normal((heads, hd)).astype(F32)
+    dx, dy = mi.to_device(x), mi.DeviceBuffer(x.nbytes)
+    dp = mi.to_device(np.array([pos], np.int32))
+    mi._call("mi_rope_neox", None, mi._P(dx.ptr), mi._P(dy.ptr), mi._P(dp.ptr), hd, heads, 1, hd, F32(1e6), F32(1.0),
+             F32(1.0), hd * 4, hd * heads * 4, hd * 4, hd * heads * 4)
+    mi.device_sync()
+    y = dy.download(F32).reshape(heads, hd)
+    ref = rope_neox_ref(x, pos, hd, 1e6)
+    assert rel_err(y, ref) < 2e-6
+
+
+@pytest.mark.parametrize("ne0,nrows", [(151936, 1), (1000, 3), (2049, 2), (4096 * 300 + 7, 1)])
+def test_argmax_first_maximum(gpu, ne0, nrows):
+    mi = gpu
+    rng = np.random.default_rng(ne0 + nrows)
+    x = rng.standard_normal((nrows, ne0)).astype(F32)
+    if nrows >= 2:
+        x[1, :] = -np.inf                      # all -inf: index 0
+    x[0, ne0 // 3] = 50.0                      # tie of the maximum: the lower index wins
+    x[0, ne0 - 1] = 50.0
+    x[0, 5] = np.nan                           # NaN is never the maximum
+    if nrows >= 3:
+        x[2, 0] = 99.0                         # maximum at the first element
+    ws_bytes = mi.lib().mi_argmax_workspace_size(ne0, nrows)
+    dx, do, dws = mi.to_device(x), mi.DeviceBuffer(4 * nrows), mi.DeviceBuffer(ws_bytes)
+    mi._call("mi_argmax", None, mi._P(dx.ptr), mi._P(do.ptr), ne0, nrows, mi._P(dws.ptr), ws_bytes)
+    mi.device_sync()
+    got = do.download(np.int32)
+    ref = [int(np.argmax(np.where(np.isnan(r), -np.inf, r))) for r in x]
+    assert list(got) == ref
+
+
+def test_argmax_rejects_small_workspace(gpu):
+    mi = gpu
+    dx, do = mi.DeviceBuffer(4 * 5000), mi.DeviceBuffer(4)
+    with pytest.raises(mi.MiError):
+        mi._call("mi_argmax", None, mi._P(dx.ptr), mi._P(do.ptr), 5000, 1, None, 0)
+
+
+# ---------------------------------------------------------------- fused chains
+
+def _q8_ref(orc, blocks, x, n, k, inv):
+    return orc.mul_mat_q8_0(blocks, x, n, k, inv_s=inv, variant=orc.Q8_ROUND_X86)
+
+
+@pytest.mark.parametrize("norm", [True, False])
+@pytest.mark.parametrize("ns,k", [((8960, 8960), 1536), ((1536,), 1536), ((3584, 512, 512), 3584)])
+def test_fused_norm_matmuls_add(gpu, orc, norm, ns, k):
+    mi = gpu
+    rng = np.random.default_rng(sum(ns) + k + norm)
+    x = (rng.standard_normal(k) * 0.5).astype(F32)
+    nw = rng.uniform(0.8, 1.2, k).astype(F32)
+    inv = (1.0 / rng.uniform(0.5, 2.0, k)).astype(F32)
+    ws = [q8_0_weights(rng, n, k) for n in ns]
+    adds = [rng.standard_normal(n).astype(F32) if i % 2 == 0 else None for i, n in enumerate(ns)]
+    pw = [_packed_q8(mi, w, n, k) for w, n in zip(ws, ns)]
+    ys = [mi.DeviceBuffer(4 * n) for n in ns]
+    da = [mi.to_device(a) if a is not None else None for a in adds]
+    dx, dnw, dinv = mi.to_device(x), mi.to_device(nw), mi.to_device(inv)
+    mi._call("mi_mul_mat_q8_0_f32_fused", None, len(ns), _ptrs(*pw), _i64s(*ns), _ptrs(*ys), _ptrs(*da), k,
+             mi._P(dx.ptr), mi._P(dnw.ptr if norm else None), F32(1e-6), mi._P(dinv.ptr), mi.Q8_ROUND_X86)
+    mi.device_sync()
+    xin = rms_norm_ref(x, nw, 1e-6) if norm else x
+    for i, n in enumerate(ns):
+        ref = _q8_ref(orc, ws[i], xin, n, k, inv)
+        if adds[i] is not None:
+            ref = (ref + adds[i]).astype(F32)
+        assert rel_err(ys[i].download(F32), ref) < GEMV_TOL, f"matrix {i}"
+
+
+@pytest.mark.parametrize("idx_i64", [False, True])
+@pytest.mark.parametrize("cfg", [dict(k=1536, hq=12, hkv=2, hd=128, pos=517, row=517, bias=True),
+                                 dict(k=3584, hq=28, hkv=4, hd=128, pos=3, row=9, bias=True),
+                                 dict(k=256, hq=4, hkv=2, hd=64, pos=0, row=0, bias=False),
+                                 dict(k=512, hq=64, hkv=8, hd=128, pos=40, row=1, bias=True)])
+def test_qkv_rope_kv(gpu, orc, cfg, idx_i64):
+    """the shapes cover 64, 32 and 16 lanes per row (the launch picks the width from the row count)"""
+    mi = gpu
+    k, hq, hkv, hd = cfg["k"], cfg["hq"], cfg["hkv"], cfg["hd"]
+    nq, nkv = hq * hd, hkv * hd
+    n_cache = 640
+    rng = np.random.default_rng(k + hq + cfg["pos"] + idx_i64)
+    x = (rng.standard_normal(k) * 0.5).astype(F32)
+    nw = rng.uniform(0.8, 1.2, k).astype(F32)
+    inv = (1.0 / rng.uniform(0.5, 2.0, k)).astype(F32)
+    ns = (nq, nkv, nkv)
+    ws = [q8_0_weights(rng, n, k) for n in ns]
+    bs = [(rng.standard_normal(n) * 0.02).astype(F32) if cfg["bias"] else None for n in ns]
+    pw = [_packed_q8(mi, w, n, k) for w, n in zip(ws, ns)]
+    db = [mi.to_device(b) if b is not None else None for b in bs]
+    dx, dnw, dinv = mi.to_device(x), mi.to_device(nw), mi.to_device(inv)
+    dq = mi.DeviceBuffer(4 * nq)
+    kc = mi.DeviceBuffer(n_cache * nkv * 2).zero()
+    vc = mi.DeviceBuffer(n_cache * nkv * 2).zero()
+    dpos = mi.to_device(np.array([cfg["pos"]], np.int32))
+    didx = mi.to_device(np.array([cfg["row"]], np.int64 if idx_i64 else np.int32))
+    mi._call("mi_qkv_rope_kv_q8_0", None, _ptrs(*pw), _i64s(*ns), _ptrs(*db), k, mi._P(dx.ptr), mi._P(dnw.ptr),
+             F32(1e-6), mi._P(dinv.ptr), mi.Q8_ROUND_X86, hd, mi._P(dpos.ptr), F32(1e6), F32(1.0), F32(1.0),
+             mi._P(dq.ptr), mi._P(kc.ptr), nkv * 2, mi._P(vc.ptr), nkv * 2, mi._P(didx.ptr), int(idx_i64), n_cache)
+    mi.device_sync()
+    xn = rms_norm_ref(x, nw, 1e-6)
+    proj = []
+    for i, n in enumerate(ns):
+        y = _q8_ref(orc, ws[i], xn, n, k, inv)
+        proj.append((y + bs[i]).astype(F32) if bs[i] is not None else y)
+    q_ref = rope_neox_ref(proj[0].reshape(hq, hd), cfg["pos"], hd, 1e6).reshape(-1)
+    k_ref = rope_neox_ref(proj[1].reshape(hkv, hd), cfg["pos"], hd, 1e6).reshape(-1)
+    assert rel_err(dq.download(F32), q_ref) < GEMV_TOL
+    kcache = kc.download(np.uint16).reshape(n_cache, nkv)
+    vcache = vc.download(np.uint16).reshape(n_cache, nkv)
+    for name, cache, ref in (("k", kcache, k_ref), ("v", vcache, proj[2])):
+        got = cache[cfg["row"]].view(np.float16).astype(np.float64)
+        tol = 2 * np.abs(ref.astype(np.float16).astype(np.float64)) * 2.0 ** -10 + 1e-7
+        assert np.all(np.abs(got - ref) <= tol + GEMV_TOL * np.sqrt(np.mean(ref.astype(np.float64) ** 2))), name
+        others = np.delete(cache, cfg["row"], axis=0)
+        assert not others.any(), f"{name} cache rows other than {cfg['row']} were written"
+
+
+def test_qkv_rope_kv_skips_out_of_range_row(gpu):
+    mi = gpu
+    rng = np.random.default_rng(7)
+    k, hd, ns = 256, 64, (256, 128, 128)
+    ws = [q8_0_weights(rng, n, k) for n in ns]
+    pw = [_packed_q8(mi, w, n, k) for w, n in zip(ws, ns)]
+    dx = mi.to_device(rng.standard_normal(k).astype(F32))
+    dq = mi.DeviceBuffer(4 * ns[0])
+    kc = mi.DeviceBuffer(8 * 128 * 2).zero()
+    vc = mi.DeviceBuffer(8 * 128 * 2).zero()
+    dpos = mi.to_device(np.array([3], np.int32))
+    didx = mi.to_device(np.array([8], np.int32))   # one past the last cache row
+    mi._call("mi_qkv_rope_kv_q8_0", None, _ptrs(*pw), _i64s(*ns), _ptrs(None, None, None), k, mi._P(dx.ptr), None,
+             F32(1e-6), None, mi.Q8_ROUND_X86, hd, mi._P(dpos.ptr), F32(1e4), F32(1.0), F32(1.0), mi._P(dq.ptr),
+             mi._P(kc.ptr), 256, mi._P(vc.ptr), 256, mi._P(didx.ptr), 0, 8)
+    mi.device_sync()
+    assert not kc.download(np.uint16).any() and not vc.download(np.uint16).any()
+
+
+@pytest.mark.parametrize("k", [8960, 18944, 512])
+def test_swiglu_quant(gpu, orc, k):
+    mi = gpu
+    rng = np.random.default_rng(k)
+    g = (rng.standard_normal(k) * 2).astype(F32)
+    u = rng.standard_normal(k).astype(F32)
+    inv = (1.0 / rng.uniform(0.5, 2.0, k)).astype(F32)
+    dg, du, dinv = mi.to_device(g), mi.to_device(u), mi.to_device(inv)
+    dq = mi.DeviceBuffer(mi.xq_size(1, k))
+    mi._call("mi_swiglu_quant_q8_0", None, mi._P(dg.ptr), mi._P(du.ptr), mi._P(dinv.ptr), k, mi._P(dq.ptr),
+             mi.Q8_ROUND_X86)
+    mi.device_sync()
+    silu = (g.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64)))).astype(F32)
+    v = (silu * u).astype(F32)
+    ref = orc.quantize_row_q8_0(v, inv_s=inv, variant=orc.Q8_ROUND_X86).reshape(k // 32, 34)
+    qs = dq.download(np.int8, k)
+    d = dq.download(np.uint16, k // 32, offset=mi.xq_d_offset(1, k))
+    got = xq_to_blocks(qs, d, k).reshape(k // 32, 34)
+    d_same = np.mean(np.all(got[:, :2] == ref[:, :2], axis=1))
+    dq_ = np.abs(got[:, 2:].view(np.int8).astype(int) - ref[:, 2:].view(np.int8).astype(int))
+    assert d_same >= 0.99 and dq_.max() <= 1 and np.mean(dq_ > 0) < 1e-3
+
+
+def test_gemv_q8_0_add_equals_gemv_plus_vector(gpu):
+    mi = gpu
+    rng = np.random.default_rng(11)
+    n, k = 1536, 8960
+    w = q8_0_weights(rng, n, k)
+    pw = _packed_q8(mi, w, n, k)
+    x = rng.standard_normal(k).astype(F32)
+    add = rng.standard_normal(n).astype(F32)
+    dx, da = mi.to_device(x), mi.to_device(add)
+    dq = mi.DeviceBuffer(mi.xq_size(1, k))
+    y0, y1 = mi.DeviceBuffer(4 * n), mi.DeviceBuffer(4 * n)
+    mi.act_quant_q8_0(dx.ptr, None, 1, k, dq.ptr, mi.Q8_ROUND_X86)
+    mi.gemv_q8_0(pw.ptr, dq.ptr, y0.ptr, n, k, 1)
+    mi._call("mi_gemv_q8_0_add", None, mi._P(pw.ptr), mi._P(dq.ptr), mi._P(da.ptr), mi._P(y1.ptr), n, k, 1)
+    mi.device_sync()
+    assert np.array_equal(y1.download(F32), (y0.download(F32) + add).astype(F32))

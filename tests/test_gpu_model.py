@@ -79,3 +79,30 @@ def test_qwen2_1p5b_width_two_layers(gpu, orc):
     err, rel, spread, mism = _run(gpu, orc, hp, n_prompt=16, n_gen=16, seed=5)
     assert rel < _bar(spread)
     assert mism == 0
+
+
+def test_fused_graph_matches_unfused(gpu, monkeypatch):
+    """The backend's fused launches against its node-by-node path on the same graph."""
+    mi = gpu
+    hp = qs.qwen2_1p5b(n_layer=2, n_ctx=64)
+    tensors, smooth = qs.synth(hp, seed=9, qk_gain=6.0)
+    fused = mi.Qwen2Model(hp)
+    fused.load(tensors, smooth)
+    monkeypatch.setenv("GGML_MI355X_FUSION", "0")
+    plain = mi.Qwen2Model(hp)
+    plain.load(tensors, smooth)
+    rng = np.random.default_rng(10)
+    tok_f = tok_p = None
+    worst = 0.0
+    identical = True
+    for pos in range(24):
+        t = int(rng.integers(0, hp["n_vocab"])) if pos < 8 else tok_f
+        tok_f, lf = fused.decode(t, pos, want_logits=True)
+        tok_p, lp = plain.decode(t, pos, want_logits=True)
+        identical = identical and np.array_equal(lf, lp)
+        worst = max(worst, float(np.abs(lf - lp).max() / np.abs(lp).max()))
+        assert tok_f == tok_p, f"position {pos}"
+    print(f"fused vs node-by-node: logits bit-identical {identical}, max rel {worst:.3e}")
+    assert worst < 1e-4
+    fused.free()
+    plain.free()
