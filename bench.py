@@ -43,7 +43,8 @@ SEED = 1234
 
 
 def measure_roofline(mi, qs, hp, rng):
-    """grouped gate+up Q8_0 GEMV of one layer, HBM-cold, live HIP-event timing"""
+    """the model's gate+up launch (RMSNorm * w, SmoothQuant, Q8_0 quantization fused, two
+    8960 x 1536 matrices), HBM-cold, live HIP-event timing on the launch stream"""
     n, k = hp["n_ff"], hp["n_embd"]
     psz = mi.q8_0_packed_size(n, k)
     st = mi.Stream()
@@ -56,20 +57,23 @@ def measure_roofline(mi, qs, hp, rng):
         mi.prepack_q8_0(src.ptr, b.ptr, n, k, stream=st.ptr)
         bufs.append(b)
     x = mi.to_device(rng.standard_normal(k).astype(np.float32))
+    nw = mi.to_device(rng.uniform(0.8, 1.2, k).astype(np.float32))
     inv_s = mi.to_device((1.0 / rng.uniform(0.5, 2.0, k)).astype(np.float32))
     y0, y1 = mi.DeviceBuffer(n * 4), mi.DeviceBuffer(n * 4)
     plug_a, plug_b = mi.DeviceBuffer(2 << 30), mi.DeviceBuffer(2 << 30)
     st.sync()
-    algo = 2 * n * (k // 32) * 34 + k * 4 + k * 4 + 2 * n * 4   # weights + x + 1/s + y
+    # weights + x + norm weight + 1/s + outputs
+    algo = 2 * n * (k // 32) * 34 + 3 * k * 4 + 2 * n * 4
     launches = copies * 8
     # argument tuples built once: the launch loop is then one C call per launch
-    fn = mi.lib().mi_mul_mat_q8_0_f32_multi
+    fn = mi.lib().mi_mul_mat_q8_0_f32_fused
     ns = (ctypes.c_int64 * 2)(n, n)
     ys = (ctypes.c_void_p * 2)(y0.ptr, y1.ptr)
+    adds = (ctypes.c_void_p * 2)(None, None)
     ws = [(ctypes.c_void_p * 2)(bufs[2 * c].ptr, bufs[2 * c + 1].ptr) for c in range(copies)]
     args = [(mi._P(st.ptr), 2, ctypes.cast(w, ctypes.c_void_p), ctypes.cast(ns, ctypes.c_void_p),
-             ctypes.cast(ys, ctypes.c_void_p), k, mi._P(x.ptr), mi._P(inv_s.ptr), mi.Q8_ROUND_X86, None, 0)
-            for w in ws]
+             ctypes.cast(ys, ctypes.c_void_p), ctypes.cast(adds, ctypes.c_void_p), k, mi._P(x.ptr), mi._P(nw.ptr),
+             ctypes.c_float(hp["rms_eps"]), mi._P(inv_s.ptr), mi.Q8_ROUND_X86) for w in ws]
     e0, e1 = mi.Event(), mi.Event()
     samples = []
     for _ in range(3):
@@ -80,17 +84,23 @@ def measure_roofline(mi, qs, hp, rng):
         e0.record(st.ptr)
         for i in range(launches):
             if fn(*args[i % copies]) != 0:
-                raise mi.MiError("mi_mul_mat_q8_0_f32_multi", -1, mi.last_error())
+                raise mi.MiError("mi_mul_mat_q8_0_f32_fused", -1, mi.last_error())
         e1.record(st.ptr)
         samples.append(e0.elapsed_ms(e1) * 1e3 / launches)
     avg_us = float(np.median(samples))
-    for b in bufs + [src, x, inv_s, y0, y1, plug_a, plug_b]:
+    for b in bufs + [src, x, nw, inv_s, y0, y1, plug_a, plug_b]:
         b.free()
     st.destroy()
     achieved = algo / avg_us / 1e3
-    return {"kernel": "k_gemv_q8_0_fused1: grouped gate+up A8W8 Q8_0 GEMV, 2 x (N=8960, K=1536), act-quant fused, "
-                      "HBM-cold", "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "avg_us": round(avg_us, 3),
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_gate_up_q8_0.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    return {"kernel": "k_gemv_q8_0_fused1<16,3,2,true>: the gate+up launch of every layer (RMSNorm*w, SmoothQuant "
+                      "and Q8_0 act-quant fused; 2 x Q8_0 8960x1536), HBM-cold", "bound": "hbm",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "avg_us": round(avg_us, 3),
             "algorithmic_bytes": algo, "launches": launches, "weight_copies": copies}
 
 
@@ -127,6 +137,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying HIP graphs")
     ap.add_argument("--no-roofline", action="store_true", help="skip the standalone roofline leg")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="run only the roofline leg (short program for rocprofv3 counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); how the decode path "
@@ -143,6 +155,9 @@ def main():
 
     warm = max(args.warmup, 0)
     hp = qs.qwen2_1p5b(n_ctx=PREFILL + warm + args.steps)
+    if args.roofline_only:
+        print(json.dumps({"roofline": measure_roofline(mi, qs, hp, np.random.default_rng(SEED + 1))}))
+        return
     tensors, smooth = qs.synth(hp, seed=SEED)
     model = mi.Qwen2Model(hp)
     model.load(tensors, smooth)
