@@ -30,7 +30,9 @@ constexpr int part_stride() { return D + 4; }  // o[D], m, l, pad -> 16-byte ali
 struct FaPlan {
     int chunk;     // positions per workgroup
     int n_splits;
-    int kt;        // positions per lane group per tile (all loads of a tile in flight together)
+    int kt;        // VALU kernel: positions per lane group per tile (all loads of a tile in flight together)
+    int nbw;       // MFMA kernel: 16-position blocks per wave
+    bool mfma;
 };
 
 // One workgroup per (split, kv head), each with 4 waves of lane groups (one KV row
@@ -50,12 +52,33 @@ inline int fa_chunk_override() {
     return v;
 }
 
-inline FaPlan fa_plan(int64_t n_kv, int64_t n_kv_heads, int64_t d) {
+inline bool fa_valu_forced() {
+    static const bool v = [] {
+        const char *e = getenv("MI_FA_VALU");
+        return e && e[0] == '1';
+    }();
+    return v;
+}
+
+inline FaPlan fa_plan(int64_t n_kv, int64_t n_kv_heads, int64_t d, int64_t gq) {
     const int64_t ng = 4 * 64 / (d / 8);  // lane groups per workgroup
     const int64_t target_wg = 512;
     int64_t per = (n_kv * n_kv_heads + target_wg - 1) / target_wg;
     if (fa_chunk_override() > 0) per = fa_chunk_override();
     FaPlan p;
+    p.mfma = !fa_valu_forced() && gq <= 16;
+    if (p.mfma) {
+        // 4 waves x nbw blocks of 16 positions per workgroup
+        p.kt = 1;
+        p.nbw = per <= 64 ? 1 : per <= 128 ? 2 : per <= 256 ? 4 : 8;
+        int64_t chunk = 64 * p.nbw;
+        while ((n_kv + chunk - 1) / chunk > kMaxSplits) chunk *= 2;
+        p.chunk = (int)chunk;
+        p.nbw = (int)(chunk / 64);
+        p.n_splits = (int)((n_kv + chunk - 1) / chunk);
+        return p;
+    }
+    p.nbw = 0;
     if (per <= ng) p.kt = 1;
     else if (per <= 2 * ng) p.kt = 2;
     else if (per <= 4 * ng) p.kt = 4;
@@ -312,6 +335,220 @@ __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, c
     if (tid == 0) __hip_atomic_store(&counters[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---------------------------------------------------------------- MFMA flash-decoding
+//
+// One workgroup per (split, kv head); each of its 4 waves walks its own run of
+// 16-position blocks with v_mfma_f32_16x16x16_f16:
+//   S^T[16 pos x 16 heads] = K[16 pos x D] . Q^T      (A = K rows, B = q, fp16 like ggml)
+//   O[16 heads x 16 dims] += P^T[heads x pos] . V      (8 tiles at D = 128)
+// The C layout of the score MFMA (lane (g, c): positions 4g..4g+3 of head c) is the A
+// layout P^T needs, so probabilities go from the softmax straight into the PV MFMA.
+// The k index of both products is permuted so that every lane's loads are contiguous
+// 16-byte chunks: lane (g, c) reads K row c at dims [D/4*g, D/4*(g+1)) and V rows
+// 4g..4g+3 at dims [D/16*c, D/16*(c+1)); output tile t column c is dim D/16*c + t.
+// P is split into fp16 hi + lo parts (two MFMAs) so the PV product keeps fp32-level
+// accuracy.  Online softmax per head in log2 units; the waves merge through LDS.
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+template <int N>
+struct U32s {
+    uint32_t w[N];
+};
+
+template <int NB>  // bytes per load group: 64 / 32 (K) or 16 / 8 (V)
+__device__ __forceinline__ void ld_bytes(uint32_t *dst, const uint8_t *src) {
+    if constexpr (NB % 16 == 0) {
+#pragma unroll
+        for (int i = 0; i < NB / 16; i++) {
+            const int4 v = *(const int4 *)(src + 16 * i);
+            dst[4 * i] = (uint32_t)v.x; dst[4 * i + 1] = (uint32_t)v.y;
+            dst[4 * i + 2] = (uint32_t)v.z; dst[4 * i + 3] = (uint32_t)v.w;
+        }
+    } else {
+        const int2 v = *(const int2 *)src;
+        dst[0] = (uint32_t)v.x; dst[1] = (uint32_t)v.y;
+    }
+}
+
+__device__ __forceinline__ half4_t h4(uint32_t a, uint32_t b) {
+    uint32_t t[2] = {a, b};
+    return __builtin_bit_cast(half4_t, t);
+}
+
+template <int D, int GQ, bool MASK, int NBW>
+__global__ __launch_bounds__(256) void k_fa_mfma(const float *__restrict__ q, const uint8_t *__restrict__ kc,
+                                                 const uint8_t *__restrict__ vc, const uint16_t *__restrict__ mask,
+                                                 const int32_t *__restrict__ kv_len_p, int n_kv, size_t k_nb1,
+                                                 size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, int chunk,
+                                                 int n_splits, float *__restrict__ part, float *__restrict__ out) {
+    constexpr int KS = D / 16;    // k-steps of the score product
+    constexpr int KW = D / 8;     // K dwords per lane per block (D/4 halves)
+    constexpr int VT = D / 16;    // output tiles = V halves per lane per row
+    constexpr int VW = D / 32;    // V dwords per lane per row
+    constexpr int PS = part_stride<D>();
+    __shared__ float s_m[4][16];
+    __shared__ float s_l[4][16];
+    __shared__ __align__(16) float s_o[4][GQ][D];
+
+    const int split = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int g = lane >> 4;
+    const int c = lane & 15;
+
+    const int kl = kv_len_p ? *kv_len_p : n_kv;
+    const int eff = (kl > 0 && kl < n_kv) ? kl : n_kv;
+    const int start = split * chunk;
+    const int end_phys = min(start + chunk, n_kv);
+    const int end_eff = min(end_phys, eff);
+    const int wstart = start + wave * NBW * 16;
+
+    // q fragment (B operand): lane (g, c) holds head c, dims D/4*g + 4s .. +3 for step s
+    half4_t qf[KS];
+    {
+        const float *qh = q + (size_t)(kvh * GQ + min(c, GQ - 1)) * D + (D / 4) * g;
+#pragma unroll
+        for (int s2 = 0; s2 < KS; s2++) {
+            const float4 v = *(const float4 *)(qh + 4 * s2);
+            const uint32_t a = (uint32_t)f2h(v.x) | ((uint32_t)f2h(v.y) << 16);
+            const uint32_t b = (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16);
+            qf[s2] = c < GQ ? h4(a, b) : h4(0u, 0u);
+        }
+    }
+
+    const uint8_t *kb = kc + (size_t)kvh * k_nb2 + (size_t)(D / 2) * g;
+    const uint8_t *vb = vc + (size_t)kvh * v_nb2 + (size_t)(D / 8) * c;
+    const int last = end_phys - 1;
+
+    float m = -INFINITY, l = 0.0f;
+    float4_t o[VT];
+#pragma unroll
+    for (int t = 0; t < VT; t++) o[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    U32s<KW> kr[2];
+    U32s<VW> vr[2][4];
+    auto issue = [&](int blk, int buf) {
+        const int p0 = wstart + blk * 16;
+        ld_bytes<D / 2>(kr[buf].w, kb + (size_t)min(p0 + c, last) * k_nb1);
+#pragma unroll
+        for (int r = 0; r < 4; r++) ld_bytes<D / 8>(vr[buf][r].w, vb + (size_t)min(p0 + 4 * g + r, last) * v_nb1);
+    };
+    issue(0, 0);
+    if (NBW > 1) issue(1, 1);
+#pragma unroll
+    for (int blk = 0; blk < NBW; blk++) {
+        const int buf = blk & 1;
+        const int p0 = wstart + blk * 16;
+        float mk[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (MASK) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) mk[r] = h2f(mask[min(p0 + 4 * g + r, last)]);
+        }
+        float4_t sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s2 = 0; s2 < KS; s2++)
+            sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(h4(kr[buf].w[2 * s2], kr[buf].w[2 * s2 + 1]), qf[s2], sacc,
+                                                         0, 0, 0);
+        float sc[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const bool ok = c < GQ && p0 + 4 * g + r < end_eff;
+            // ggml order: s = (q.k)*scale; s += mask; kept in log2 units for v_exp_f32
+            const float v = __fadd_rn(__fmul_rn(sacc[r], scale), mk[r]) * kLog2e;
+            sc[r] = ok ? v : -INFINITY;
+        }
+        float bm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+        const float mn = fmaxf(m, bm);
+        const float alpha = mn == -INFINITY ? 1.0f : fexp2(m - mn);
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) p[r] = mn == -INFINITY ? 0.0f : fexp2(sc[r] - mn);
+        l = l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+        m = mn;
+        // rescale the output rows: row 4g+r belongs to head 4g+r, whose alpha sits in lane 4g+r
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float a = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+            for (int t = 0; t < VT; t++) o[t][r] *= a;
+        }
+        half_t ph[4], pl[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            ph[r] = (half_t)p[r];
+            pl[r] = (half_t)(p[r] - (float)ph[r]);
+        }
+        const half4_t ahi = {ph[0], ph[1], ph[2], ph[3]};
+        const half4_t alo = {pl[0], pl[1], pl[2], pl[3]};
+#pragma unroll
+        for (int t = 0; t < VT; t++) {
+            // column c of tile t is dim D/16*c + t: half t of each of the lane's 4 V rows
+            const int wd = t >> 1;
+            uint32_t a0, a1;
+            if (t & 1) {
+                a0 = (vr[buf][0].w[wd] >> 16) | (vr[buf][1].w[wd] & 0xffff0000u);
+                a1 = (vr[buf][2].w[wd] >> 16) | (vr[buf][3].w[wd] & 0xffff0000u);
+            } else {
+                a0 = (vr[buf][0].w[wd] & 0xffffu) | (vr[buf][1].w[wd] << 16);
+                a1 = (vr[buf][2].w[wd] & 0xffffu) | (vr[buf][3].w[wd] << 16);
+            }
+            const half4_t bv = h4(a0, a1);
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(ahi, bv, o[t], 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(alo, bv, o[t], 0, 0, 0);
+        }
+        if (blk + 2 < NBW) issue(blk + 2, buf);
+    }
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+
+    if (g == 0) {
+        s_m[wave][c] = m;
+        s_l[wave][c] = l;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int h = 4 * g + r;
+        if (h < GQ) {
+#pragma unroll
+            for (int t = 0; t < VT; t++) s_o[wave][h][(D / 16) * c + t] = o[t][r];
+        }
+    }
+    __syncthreads();
+
+    for (int idx = tid; idx < GQ * D; idx += 256) {
+        const int h = idx / D;
+        const int dd = idx % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, s_m[w][h]);
+        float L = 0.0f, acc = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float e = fexp2(s_m[w][h] - M);
+                L += s_l[w][h] * e;
+                acc += s_o[w][h][dd] * e;
+            }
+        }
+        const int qh_idx = kvh * GQ + h;
+        if (n_splits == 1) {
+            out[(size_t)qh_idx * D + dd] = L == 0.0f ? 0.0f : acc / L;
+        } else {
+            float *rec = part + ((size_t)qh_idx * n_splits + split) * PS;
+            rec[dd] = acc;
+            if (dd == 0) {
+                rec[D] = M;
+                rec[D + 1] = L;
+            }
+        }
+    }
+}
+
 // Parallel log-sum-exp combine for many splits: grid (q head, D/32 dim slices),
 // 256 threads = 32 dims x 8 split groups; split weights exp(m_s - M) in LDS.
 template <int D>
@@ -388,8 +625,28 @@ int launch_split_m(hipStream_t st, const float *q, const void *k, const void *v,
                    const int32_t *kv_len, int64_t n_kv, int64_t n_kv_heads, size_t k_nb1, size_t k_nb2,
                    size_t v_nb1, size_t v_nb2, float scale, float *out, float *part, unsigned *counters,
                    const FaPlan &p) {
-    const bool fused = p.n_splits <= kFusedMaxSplits && fused_combine_enabled();
     const dim3 grid((unsigned)p.n_splits, (unsigned)n_kv_heads);
+    if (p.mfma) {
+#define MI_FA_NBW(NB)                                                                                         \
+    hipLaunchKernelGGL((k_fa_mfma<D, GQ, MASK, NB>), grid, dim3(256), 0, st, q, (const uint8_t *)k,             \
+                       (const uint8_t *)v, mask, kv_len, (int)n_kv, k_nb1, k_nb2, v_nb1, v_nb2, scale, p.chunk, \
+                       p.n_splits, part, out)
+        switch (p.nbw) {
+            case 1: MI_FA_NBW(1); break;
+            case 2: MI_FA_NBW(2); break;
+            case 4: MI_FA_NBW(4); break;
+            default: MI_FA_NBW(8); break;
+        }
+#undef MI_FA_NBW
+        MI_CHECK_LAUNCH("k_fa_mfma");
+        if (p.n_splits > 1) {
+            hipLaunchKernelGGL((k_fa_combine<D>), dim3((unsigned)(n_kv_heads * GQ), D / 32), dim3(256), 0, st, part,
+                               out, p.n_splits);
+            MI_CHECK_LAUNCH("k_fa_combine");
+        }
+        return MI_OK;
+    }
+    const bool fused = p.n_splits <= kFusedMaxSplits && fused_combine_enabled();
 #define MI_FA_KT(KT)                                                                                          \
     hipLaunchKernelGGL((k_fa_split<D, GQ, MASK, KT>), grid, dim3(256), 0, st, q, (const uint8_t *)k,          \
                        (const uint8_t *)v, mask, kv_len, (int)n_kv, k_nb1, k_nb2, v_nb1, v_nb2, scale, p.chunk, \
@@ -471,7 +728,7 @@ extern "C" {
 
 size_t mi_fa_decode_workspace_size(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d) {
     if (n_kv <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || d <= 0) return 0;
-    const FaPlan p = fa_plan(n_kv, n_kv_heads, d);
+    const FaPlan p = fa_plan(n_kv, n_kv_heads, d, n_q_heads / n_kv_heads);
     return fa_part_bytes(n_q_heads, p.n_splits, d) + mi::align_up((size_t)n_kv_heads * sizeof(unsigned), 256);
 }
 
@@ -487,7 +744,7 @@ int mi_fa_decode(void *stream, const float *q, const void *k, const void *v, con
     MI_CHECK_ARG(mi::aligned(k, 16) && mi::aligned(v, 16) && k_nb1 % 16 == 0 && k_nb2 % 16 == 0 && v_nb1 % 16 == 0 &&
                      v_nb2 % 16 == 0 && mi::aligned(q, 16) && mi::aligned(out, 16),
                  "fa_decode: K/V base and strides must be 16-byte aligned");
-    const FaPlan p = fa_plan(n_kv, n_kv_heads, d);
+    const FaPlan p = fa_plan(n_kv, n_kv_heads, d, n_q_heads / n_kv_heads);
     const size_t need = mi_fa_decode_workspace_size(n_kv, n_q_heads, n_kv_heads, d);
     if (p.n_splits > 1 && (!ws || ws_bytes < need || !mi::aligned(ws, 256))) {
         mi::set_error("fa_decode: workspace %zu < %zu bytes (or not 256-byte aligned)", ws_bytes, need);
