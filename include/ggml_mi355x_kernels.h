@@ -163,9 +163,17 @@ int mi_q8_0_block_dots(void *stream, const void *w_packed, const void *xq, int32
  * ---------------------------------------------------------------------- */
 int mi_gemv_q4_0_f16(void *stream, const void *w_packed, const uint16_t *x_f16, float *y, int64_t n, int64_t k,
                      int64_t m);
-/* same with fp32 activations converted to fp16 (RNE) in the prologue */
+/* the same with the ADD of a same-shape vector (residual) fused: y = W*x + add */
+int mi_gemv_q4_0_f16_add(void *stream, const void *w_packed, const uint16_t *x_f16, const float *add, float *y,
+                         int64_t n, int64_t k, int64_t m);
+/* the MUL_MAT of the ggml graph (src1 fp32): the activation is converted to fp16 (RNE, as
+ * ggml converts src1) into LDS when m*k*2 <= 64 KB (no workspace), otherwise into ws of
+ * mi_mul_mat_q4_0_workspace_size(m, k) bytes */
+size_t mi_mul_mat_q4_0_workspace_size(int64_t m, int64_t k);
 int mi_mul_mat_q4_0_f32(void *stream, const void *w_packed, const float *x, float *y, int64_t n, int64_t k,
-                        int64_t m);
+                        int64_t m, void *ws, size_t ws_bytes);
+/* fp32 -> fp16 round-to-nearest-even of n values (n % 4 == 0) */
+int mi_cast_f32_f16(void *stream, const float *x, uint16_t *y, int64_t n);
 
 /* ------------------------------------------------------------------------
  * F16 GEMV (replaces cast + aclnnMatmul(FRACTAL_NZ) + cast, patch:1286-1309,
@@ -190,13 +198,25 @@ int mi_gemv_f16(void *stream, const uint16_t *w, int64_t ldw, const float *x, fl
  * ws   : workspace of mi_fa_decode_workspace_size() bytes, 256-byte aligned (split partials and
  *        per-kv-head arrival counters); it must be zero-filled once before its first use and is
  *        left zeroed by every call, so calls sharing one workspace must be stream-ordered
- * d must be 64 or 128; n_q_heads % n_kv_heads == 0; group size <= 8.
+ * d must be 64 or 128; n_q_heads % n_kv_heads == 0; group size <= 8 (<= 16 on the MFMA path).
  * ---------------------------------------------------------------------- */
 size_t mi_fa_decode_workspace_size(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d);
 int mi_fa_decode(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
                  const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
                  size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out,
                  void *ws, size_t ws_bytes);
+/* n_seq independent sequences in one launch (ggml FLASH_ATTN_EXT with one query row per
+ * stream, ne[3] = n_seq: llama.cpp's per-sequence KV streams).  Sequence s uses
+ * q + s*q_seq and out + s*out_seq (floats), k + s*k_seq and v + s*v_seq (bytes),
+ * mask + s*mask_seq (elements) and kv_len[s].  No reference counterpart: the reference
+ * decodes one sequence (patch:1957-1983 requires one query row). */
+size_t mi_fa_decode_batch_workspace_size(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                                         int64_t n_seq);
+int mi_fa_decode_batch(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
+                       const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                       size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out,
+                       int64_t n_seq, size_t q_seq, size_t k_seq, size_t v_seq, size_t mask_seq, size_t out_seq,
+                       void *ws, size_t ws_bytes);
 
 /* ------------------------------------------------------------------------
  * Decode-graph glue ops (one launch each; ggml-CPU semantics of
@@ -227,6 +247,10 @@ size_t mi_argmax_workspace_size(int64_t ne0, int64_t nrows);
 int mi_argmax(void *stream, const float *x, int32_t *out, int64_t ne0, int64_t nrows, void *ws, size_t ws_bytes);
 /* decode mask row from a device length: 0 for i < *len, -inf beyond */
 int mi_fill_mask_f16(void *stream, uint16_t *mask, const int32_t *len, int64_t n_kv);
+/* rows x row_elems fp16 values uniform in [-scale, scale) (row stride in bytes), from a
+ * counter-based hash of seed and the element index; synthetic KV-cache contents */
+int mi_fill_f16_uniform(void *stream, void *dst, int64_t rows, int64_t row_elems, size_t row_stride, uint64_t seed,
+                        float scale);
 
 /* ------------------------------------------------------------------------
  * kv_lengths on the device (replaces the host scan set_input_kv_lengths,

@@ -9,7 +9,8 @@
  * same nodes as llama.cpp's Qwen2 builder (RMS_NORM, MUL, MUL_MAT, ADD, ROPE neox,
  * SET_ROWS into an fp16 KV cache, FLASH_ATTN_EXT with the kv_lengths src[5] of
  * patch:2934-2997, GLU swiglu, GET_ROWS, ARGMAX) and runs it with
- * ggml_backend_graph_compute.  One token per step (bs = 1), greedy sampling.
+ * ggml_backend_graph_compute.  Each step decodes one token for each of n_seq independent
+ * sequences (bs = n_seq; each sequence owns n_ctx cache positions), greedy sampling.
  */
 #ifndef MI_QWEN2_H
 #define MI_QWEN2_H
@@ -34,6 +35,7 @@ typedef struct mi_qwen2_hparams {
     float rope_theta;
     int32_t wtype;      /* ggml type id of the projection weights: 8 = Q8_0, 2 = Q4_0 */
     int32_t use_bias;   /* q/k/v biases (Qwen2 has them) */
+    int32_t n_seq;      /* independent sequences decoded together, 1..8 (0 = 1) */
 } mi_qwen2_hparams;
 
 typedef struct mi_qwen2 mi_qwen2;
@@ -51,8 +53,17 @@ int mi_qwen2_set_smooth(mi_qwen2 *m, const char *weight_name, const float *s, in
 /* byte size and dims of a named tensor (dims[0] = ne0, dims[1] = ne1); -1 if unknown */
 int64_t mi_qwen2_tensor_nbytes(mi_qwen2 *m, const char *name, int64_t *dims);
 
-/* one decode step at position pos: writes the argmax token, optionally the logits [n_vocab] */
+int32_t mi_qwen2_n_seq(const mi_qwen2 *m);
+
+/* one decode step at position pos (n_seq == 1): writes the argmax token, optionally the logits [n_vocab] */
 int mi_qwen2_decode(mi_qwen2 *m, int32_t token, int32_t pos, int32_t *next_token, float *logits);
+/* one decode step of all n_seq sequences: tokens[s] at position pos[s]; writes next_tokens[n_seq]
+ * and optionally logits [n_seq][n_vocab] */
+int mi_qwen2_decode_batch(mi_qwen2 *m, const int32_t *tokens, const int32_t *pos, int32_t *next_tokens,
+                          float *logits);
+/* n_steps greedy steps of all sequences from tokens[s] at pos[s]; out_tokens [n_steps][n_seq] */
+int mi_qwen2_decode_steps_batch(mi_qwen2 *m, const int32_t *tokens, const int32_t *pos, int32_t n_steps,
+                                int32_t *out_tokens, double *seconds);
 /* the prompt (one token per step), then n_gen timed greedy decode steps: the first
  * consumes the prompt's greedy continuation, out_tokens[i] is the token step i produces;
  * the seconds of the n_gen steps are written to *gen_seconds when not NULL */
@@ -67,6 +78,14 @@ int mi_qwen2_decode_steps(mi_qwen2 *m, int32_t token, int32_t pos, int32_t n_ste
  * fp16 [n_pos][n_head_kv*head_dim], into host memory dst of `size` bytes (the state a
  * llama.cpp session save would write for this sequence) */
 int mi_qwen2_get_cache(mi_qwen2 *m, int32_t layer, int32_t is_v, int32_t n_pos, void *dst, size_t size);
+/* the same for sequence seq, and its inverse (the state a session load would restore) */
+int mi_qwen2_get_cache_seq(mi_qwen2 *m, int32_t layer, int32_t is_v, int32_t seq, int32_t n_pos, void *dst,
+                           size_t size);
+int mi_qwen2_set_cache_seq(mi_qwen2 *m, int32_t layer, int32_t is_v, int32_t seq, int32_t n_pos, const void *src,
+                           size_t size);
+/* synthetic context: positions < n_pos of every layer's K and V cache of every sequence set to
+ * fp16 values uniform in [-scale, scale) on the device (decode timing at long contexts) */
+int mi_qwen2_fill_cache(mi_qwen2 *m, int32_t n_pos, uint64_t seed, float scale);
 /* forget the KV cache contents (positions restart at 0) */
 int mi_qwen2_reset(mi_qwen2 *m);
 

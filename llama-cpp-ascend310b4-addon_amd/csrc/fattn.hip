@@ -111,13 +111,31 @@ __device__ __forceinline__ void merge_state(float &m, float &l, float *o, int xo
     m = mn;
 }
 
+// Sequences (grid z) are independent problems: per-sequence strides of q / out
+// (floats), K / V (bytes) and mask (elements); kv_len and the partials are indexed by
+// sequence.
+struct FaSeq {
+    size_t q, k, v, mask, out;
+};
+
 template <int D, int GQ, bool MASK, int kT>
 __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, const uint8_t *__restrict__ kc,
                                                   const uint8_t *__restrict__ vc, const uint16_t *__restrict__ mask,
                                                   const int32_t *__restrict__ kv_len_p, int n_kv, size_t k_nb1,
                                                   size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, int chunk,
                                                   int n_splits, float *__restrict__ part, float *__restrict__ out,
-                                                  unsigned *__restrict__ counters) {
+                                                  unsigned *__restrict__ counters, const FaSeq sq) {
+    {
+        const int seq = blockIdx.z;
+        q += (size_t)seq * sq.q;
+        kc += (size_t)seq * sq.k;
+        vc += (size_t)seq * sq.v;
+        if (MASK) mask += (size_t)seq * sq.mask;
+        if (kv_len_p) kv_len_p += seq;
+        out += (size_t)seq * sq.out;
+        part += (size_t)seq * gridDim.y * GQ * n_splits * part_stride<D>();
+        if (counters) counters += (size_t)seq * gridDim.y;
+    }
     constexpr int LPR = D / 8;     // lanes per position row (16 B = 8 halves per lane)
     constexpr int PPW = 64 / LPR;  // positions per wave step
     constexpr int NG = kNW * PPW;  // lane groups per workgroup
@@ -381,7 +399,18 @@ __global__ __launch_bounds__(256) void k_fa_mfma(const float *__restrict__ q, co
                                                  const uint8_t *__restrict__ vc, const uint16_t *__restrict__ mask,
                                                  const int32_t *__restrict__ kv_len_p, int n_kv, size_t k_nb1,
                                                  size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, int chunk,
-                                                 int n_splits, float *__restrict__ part, float *__restrict__ out) {
+                                                 int n_splits, float *__restrict__ part, float *__restrict__ out,
+                                                 const FaSeq sq) {
+    {
+        const int seq = blockIdx.z;
+        q += (size_t)seq * sq.q;
+        kc += (size_t)seq * sq.k;
+        vc += (size_t)seq * sq.v;
+        if (MASK) mask += (size_t)seq * sq.mask;
+        if (kv_len_p) kv_len_p += seq;
+        out += (size_t)seq * sq.out;
+        part += (size_t)seq * gridDim.y * GQ * n_splits * part_stride<D>();
+    }
     constexpr int KS = D / 16;    // k-steps of the score product
     constexpr int KW = D / 8;     // K dwords per lane per block (D/4 halves)
     constexpr int VT = D / 16;    // output tiles = V halves per lane per row
@@ -553,8 +582,10 @@ __global__ __launch_bounds__(256) void k_fa_mfma(const float *__restrict__ q, co
 // 256 threads = 32 dims x 8 split groups; split weights exp(m_s - M) in LDS.
 template <int D>
 __global__ __launch_bounds__(256) void k_fa_combine(const float *__restrict__ part, float *__restrict__ out,
-                                                    int n_splits) {
+                                                    int n_splits, size_t out_seq) {
     constexpr int PS = part_stride<D>();
+    part += (size_t)blockIdx.z * gridDim.x * n_splits * PS;
+    out += (size_t)blockIdx.z * out_seq;
     __shared__ float s_w[kMaxSplits];
     __shared__ float s_red[8][32];
     __shared__ float s_wave[4];
@@ -620,17 +651,28 @@ inline bool fused_combine_enabled() {
     return on;
 }
 
+struct FaArgs {
+    const float *q;
+    const void *k, *v;
+    const uint16_t *mask;
+    const int32_t *kv_len;
+    int64_t n_kv, n_kv_heads, n_seq;
+    size_t k_nb1, k_nb2, v_nb1, v_nb2;
+    float scale;
+    float *out, *part;
+    unsigned *counters;
+    FaSeq sq;
+};
+
 template <int D, int GQ, bool MASK>
-int launch_split_m(hipStream_t st, const float *q, const void *k, const void *v, const uint16_t *mask,
-                   const int32_t *kv_len, int64_t n_kv, int64_t n_kv_heads, size_t k_nb1, size_t k_nb2,
-                   size_t v_nb1, size_t v_nb2, float scale, float *out, float *part, unsigned *counters,
-                   const FaPlan &p) {
-    const dim3 grid((unsigned)p.n_splits, (unsigned)n_kv_heads);
+int launch_split_m(hipStream_t st, const FaArgs &a, const FaPlan &p) {
+    const dim3 grid((unsigned)p.n_splits, (unsigned)a.n_kv_heads, (unsigned)a.n_seq);
+    const uint8_t *kb = (const uint8_t *)a.k, *vb = (const uint8_t *)a.v;
     if (p.mfma) {
-#define MI_FA_NBW(NB)                                                                                         \
-    hipLaunchKernelGGL((k_fa_mfma<D, GQ, MASK, NB>), grid, dim3(256), 0, st, q, (const uint8_t *)k,             \
-                       (const uint8_t *)v, mask, kv_len, (int)n_kv, k_nb1, k_nb2, v_nb1, v_nb2, scale, p.chunk, \
-                       p.n_splits, part, out)
+#define MI_FA_NBW(NB)                                                                                          \
+    hipLaunchKernelGGL((k_fa_mfma<D, GQ, MASK, NB>), grid, dim3(256), 0, st, a.q, kb, vb, a.mask, a.kv_len,      \
+                       (int)a.n_kv, a.k_nb1, a.k_nb2, a.v_nb1, a.v_nb2, a.scale, p.chunk, p.n_splits, a.part, a.out, \
+                       a.sq)
         switch (p.nbw) {
             case 1: MI_FA_NBW(1); break;
             case 2: MI_FA_NBW(2); break;
@@ -639,53 +681,40 @@ int launch_split_m(hipStream_t st, const float *q, const void *k, const void *v,
         }
 #undef MI_FA_NBW
         MI_CHECK_LAUNCH("k_fa_mfma");
-        if (p.n_splits > 1) {
-            hipLaunchKernelGGL((k_fa_combine<D>), dim3((unsigned)(n_kv_heads * GQ), D / 32), dim3(256), 0, st, part,
-                               out, p.n_splits);
-            MI_CHECK_LAUNCH("k_fa_combine");
+    } else {
+        const bool fused = p.n_splits <= kFusedMaxSplits && fused_combine_enabled();
+#define MI_FA_KT(KT)                                                                                           \
+    hipLaunchKernelGGL((k_fa_split<D, GQ, MASK, KT>), grid, dim3(256), 0, st, a.q, kb, vb, a.mask, a.kv_len,     \
+                       (int)a.n_kv, a.k_nb1, a.k_nb2, a.v_nb1, a.v_nb2, a.scale, p.chunk, p.n_splits, a.part, a.out, \
+                       fused ? a.counters : nullptr, a.sq)
+        switch (p.kt) {
+            case 1: MI_FA_KT(1); break;
+            case 2: MI_FA_KT(2); break;
+            case 4: MI_FA_KT(4); break;
+            default: MI_FA_KT(8); break;
         }
-        return MI_OK;
-    }
-    const bool fused = p.n_splits <= kFusedMaxSplits && fused_combine_enabled();
-#define MI_FA_KT(KT)                                                                                          \
-    hipLaunchKernelGGL((k_fa_split<D, GQ, MASK, KT>), grid, dim3(256), 0, st, q, (const uint8_t *)k,          \
-                       (const uint8_t *)v, mask, kv_len, (int)n_kv, k_nb1, k_nb2, v_nb1, v_nb2, scale, p.chunk, \
-                       p.n_splits, part, out, fused ? counters : nullptr)
-    switch (p.kt) {
-        case 1: MI_FA_KT(1); break;
-        case 2: MI_FA_KT(2); break;
-        case 4: MI_FA_KT(4); break;
-        default: MI_FA_KT(8); break;
-    }
 #undef MI_FA_KT
-    MI_CHECK_LAUNCH("k_fa_split");
-    if (p.n_splits > 1 && !fused) {
-        hipLaunchKernelGGL((k_fa_combine<D>), dim3((unsigned)(n_kv_heads * GQ), D / 32), dim3(256), 0, st, part, out,
-                           p.n_splits);
+        MI_CHECK_LAUNCH("k_fa_split");
+        if (fused) return MI_OK;
+    }
+    if (p.n_splits > 1) {
+        hipLaunchKernelGGL((k_fa_combine<D>), dim3((unsigned)(a.n_kv_heads * GQ), D / 32, (unsigned)a.n_seq),
+                           dim3(256), 0, st, a.part, a.out, p.n_splits, a.sq.out);
         MI_CHECK_LAUNCH("k_fa_combine");
     }
     return MI_OK;
 }
 
 template <int D, int GQ>
-int launch_split(hipStream_t st, const float *q, const void *k, const void *v, const uint16_t *mask,
-                 const int32_t *kv_len, int64_t n_kv, int64_t n_kv_heads, size_t k_nb1, size_t k_nb2, size_t v_nb1,
-                 size_t v_nb2, float scale, float *out, float *part, unsigned *counters, const FaPlan &p) {
-    if (mask)
-        return launch_split_m<D, GQ, true>(st, q, k, v, mask, kv_len, n_kv, n_kv_heads, k_nb1, k_nb2, v_nb1, v_nb2,
-                                           scale, out, part, counters, p);
-    return launch_split_m<D, GQ, false>(st, q, k, v, mask, kv_len, n_kv, n_kv_heads, k_nb1, k_nb2, v_nb1, v_nb2,
-                                        scale, out, part, counters, p);
+int launch_split(hipStream_t st, const FaArgs &a, const FaPlan &p) {
+    if (a.mask) return launch_split_m<D, GQ, true>(st, a, p);
+    return launch_split_m<D, GQ, false>(st, a, p);
 }
 
 template <int D>
-int launch_d(hipStream_t st, int gq, const float *q, const void *k, const void *v, const uint16_t *mask,
-             const int32_t *kv_len, int64_t n_kv, int64_t n_kv_heads, size_t k_nb1, size_t k_nb2, size_t v_nb1,
-             size_t v_nb2, float scale, float *out, float *part, unsigned *counters, const FaPlan &p) {
-#define MI_FA_CASE(G)                                                                                          \
-    case G:                                                                                                    \
-        return launch_split<D, G>(st, q, k, v, mask, kv_len, n_kv, n_kv_heads, k_nb1, k_nb2, v_nb1, v_nb2, scale, \
-                                  out, part, counters, p);
+int launch_d(hipStream_t st, int gq, const FaArgs &a, const FaPlan &p) {
+#define MI_FA_CASE(G) \
+    case G: return launch_split<D, G>(st, a, p);
     switch (gq) {
         MI_FA_CASE(1)
         MI_FA_CASE(2)
@@ -726,39 +755,73 @@ __global__ __launch_bounds__(256) void k_kv_lengths(const void *__restrict__ mas
 
 extern "C" {
 
-size_t mi_fa_decode_workspace_size(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d) {
-    if (n_kv <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || d <= 0) return 0;
+size_t mi_fa_decode_batch_workspace_size(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                                         int64_t n_seq) {
+    if (n_kv <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || d <= 0 || n_seq <= 0) return 0;
     const FaPlan p = fa_plan(n_kv, n_kv_heads, d, n_q_heads / n_kv_heads);
-    return fa_part_bytes(n_q_heads, p.n_splits, d) + mi::align_up((size_t)n_kv_heads * sizeof(unsigned), 256);
+    return fa_part_bytes(n_q_heads * n_seq, p.n_splits, d) +
+           mi::align_up((size_t)(n_kv_heads * n_seq) * sizeof(unsigned), 256);
+}
+
+size_t mi_fa_decode_workspace_size(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d) {
+    return mi_fa_decode_batch_workspace_size(n_kv, n_q_heads, n_kv_heads, d, 1);
+}
+
+int mi_fa_decode_batch(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
+                       const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                       size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out,
+                       int64_t n_seq, size_t q_seq, size_t k_seq, size_t v_seq, size_t mask_seq, size_t out_seq,
+                       void *ws, size_t ws_bytes) {
+    MI_CHECK_ARG(q && k && v && out, "fa_decode: null pointer");
+    MI_CHECK_ARG(n_kv > 0 && n_kv < (1ll << 31) && n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0,
+                 "fa_decode: bad heads/length n_kv=%lld nq=%lld nkv=%lld", (long long)n_kv, (long long)n_q_heads,
+                 (long long)n_kv_heads);
+    MI_CHECK_ARG(n_seq >= 1 && n_seq <= 65535, "fa_decode: n_seq=%lld", (long long)n_seq);
+    MI_CHECK_ARG(d == 64 || d == 128, "fa_decode: head dim %lld not supported (64, 128)", (long long)d);
+    MI_CHECK_ARG(mi::aligned(k, 16) && mi::aligned(v, 16) && k_nb1 % 16 == 0 && k_nb2 % 16 == 0 && v_nb1 % 16 == 0 &&
+                     v_nb2 % 16 == 0 && mi::aligned(q, 16) && mi::aligned(out, 16) && k_seq % 16 == 0 &&
+                     v_seq % 16 == 0 && q_seq % 4 == 0 && out_seq % 4 == 0,
+                 "fa_decode: K/V base and strides must be 16-byte aligned");
+    const FaPlan p = fa_plan(n_kv, n_kv_heads, d, n_q_heads / n_kv_heads);
+    const size_t need = mi_fa_decode_batch_workspace_size(n_kv, n_q_heads, n_kv_heads, d, n_seq);
+    if (p.n_splits > 1 && (!ws || ws_bytes < need || !mi::aligned(ws, 256))) {
+        mi::set_error("fa_decode: workspace %zu < %zu bytes (or not 256-byte aligned)", ws_bytes, need);
+        return MI_ERR_WORKSPACE;
+    }
+    FaArgs a;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.mask = mask;
+    a.kv_len = kv_len;
+    a.n_kv = n_kv;
+    a.n_kv_heads = n_kv_heads;
+    a.n_seq = n_seq;
+    a.k_nb1 = k_nb1;
+    a.k_nb2 = k_nb2;
+    a.v_nb1 = v_nb1;
+    a.v_nb2 = v_nb2;
+    a.scale = scale;
+    a.out = out;
+    a.part = (float *)ws;
+    a.counters = ws ? (unsigned *)((uint8_t *)ws + fa_part_bytes(n_q_heads * n_seq, p.n_splits, d)) : nullptr;
+    a.sq.q = q_seq;
+    a.sq.k = k_seq;
+    a.sq.v = v_seq;
+    a.sq.mask = mask_seq;
+    a.sq.out = out_seq;
+    const int gq = (int)(n_q_heads / n_kv_heads);
+    hipStream_t st = (hipStream_t)stream;
+    if (d == 128) return launch_d<128>(st, gq, a, p);
+    return launch_d<64>(st, gq, a, p);
 }
 
 int mi_fa_decode(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
                  const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
                  size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out, void *ws,
                  size_t ws_bytes) {
-    MI_CHECK_ARG(q && k && v && out, "fa_decode: null pointer");
-    MI_CHECK_ARG(n_kv > 0 && n_kv < (1ll << 31) && n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0,
-                 "fa_decode: bad heads/length n_kv=%lld nq=%lld nkv=%lld", (long long)n_kv, (long long)n_q_heads,
-                 (long long)n_kv_heads);
-    MI_CHECK_ARG(d == 64 || d == 128, "fa_decode: head dim %lld not supported (64, 128)", (long long)d);
-    MI_CHECK_ARG(mi::aligned(k, 16) && mi::aligned(v, 16) && k_nb1 % 16 == 0 && k_nb2 % 16 == 0 && v_nb1 % 16 == 0 &&
-                     v_nb2 % 16 == 0 && mi::aligned(q, 16) && mi::aligned(out, 16),
-                 "fa_decode: K/V base and strides must be 16-byte aligned");
-    const FaPlan p = fa_plan(n_kv, n_kv_heads, d, n_q_heads / n_kv_heads);
-    const size_t need = mi_fa_decode_workspace_size(n_kv, n_q_heads, n_kv_heads, d);
-    if (p.n_splits > 1 && (!ws || ws_bytes < need || !mi::aligned(ws, 256))) {
-        mi::set_error("fa_decode: workspace %zu < %zu bytes (or not 256-byte aligned)", ws_bytes, need);
-        return MI_ERR_WORKSPACE;
-    }
-    const int gq = (int)(n_q_heads / n_kv_heads);
-    hipStream_t st = (hipStream_t)stream;
-    float *part = (float *)ws;
-    unsigned *counters = ws ? (unsigned *)((uint8_t *)ws + fa_part_bytes(n_q_heads, p.n_splits, d)) : nullptr;
-    if (d == 128)
-        return launch_d<128>(st, gq, q, k, v, mask, kv_len, n_kv, n_kv_heads, k_nb1, k_nb2, v_nb1, v_nb2, scale, out,
-                             part, counters, p);
-    return launch_d<64>(st, gq, q, k, v, mask, kv_len, n_kv, n_kv_heads, k_nb1, k_nb2, v_nb1, v_nb2, scale, out,
-                        part, counters, p);
+    return mi_fa_decode_batch(stream, q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1, k_nb2, v_nb1,
+                              v_nb2, scale, out, 1, 0, 0, 0, 0, 0, ws, ws_bytes);
 }
 
 int mi_kv_lengths(void *stream, const void *mask, int mask_is_f16, int64_t n_kv, int64_t n_rows, int32_t *out) {

@@ -334,8 +334,7 @@ bool supports_mul_mat(const ggml_tensor *op) {
         case GGML_TYPE_Q8_0:
         case GGML_TYPE_Q4_0:
             // the planar side copy exists only for weights of this backend's buffers
-            return a->extra != nullptr && a->buffer && a->buffer->buft->iface.get_alloc_size == buft_get_alloc_size &&
-                   b->ne[0] * b->ne[1] * 2 <= 64 * 1024;
+            return a->extra != nullptr && a->buffer && a->buffer->buft->iface.get_alloc_size == buft_get_alloc_size;
         case GGML_TYPE_F16:
             return a->nb[0] == 2 && a->nb[1] % 16 == 0 && a->ne[0] % 8 == 0 && b->ne[0] * b->ne[1] * 2 <= 64 * 1024;
         default:
@@ -351,16 +350,21 @@ bool supports_fa(const ggml_tensor *op) {
     memcpy(&softcap, (const float *)op->op_params + 2, sizeof(float));
     if (max_bias != 0.0f || softcap != 0.0f || sinks) return false;
     if (!q || q->type != GGML_TYPE_F32 || op->type != GGML_TYPE_F32 || !ggml_is_contiguous(op)) return false;
-    if (q->ne[1] != 1 || q->ne[3] != 1 || q->nb[0] != 4 || (q->ne[2] > 1 && q->nb[2] != (size_t)q->ne[0] * 4))
-        return false;
+    // one query row per head and stream; streams (ne[3]) are independent sequences
+    const int64_t n_seq = q->ne[3];
+    if (q->ne[1] != 1 || q->nb[0] != 4 || (q->ne[2] > 1 && q->nb[2] != (size_t)q->ne[0] * 4) || q->nb[3] % 4) return false;
     if (k->type != GGML_TYPE_F16 || v->type != GGML_TYPE_F16) return false;
     const int64_t d = q->ne[0];
     if ((d != 64 && d != 128) || k->ne[0] != d || v->ne[0] != d) return false;
-    if (k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2] || k->ne[3] != 1 || v->ne[3] != 1) return false;
+    if (k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2] || k->ne[3] != n_seq || v->ne[3] != n_seq) return false;
     if (k->ne[2] < 1 || q->ne[2] % k->ne[2] != 0 || q->ne[2] / k->ne[2] > 8) return false;
-    if (k->nb[0] != 2 || v->nb[0] != 2 || k->nb[1] % 16 || k->nb[2] % 16 || v->nb[1] % 16 || v->nb[2] % 16) return false;
-    if (mask && (mask->type != GGML_TYPE_F16 || mask->ne[0] < k->ne[1] || mask->nb[0] != 2)) return false;
-    if (kvl && (kvl->type != GGML_TYPE_I32 || !ggml_is_contiguous(kvl) || ggml_nelements(kvl) < 1)) return false;
+    if (k->nb[0] != 2 || v->nb[0] != 2 || k->nb[1] % 16 || k->nb[2] % 16 || v->nb[1] % 16 || v->nb[2] % 16 ||
+        (n_seq > 1 && (k->nb[3] % 16 || v->nb[3] % 16)))
+        return false;
+    if (mask && (mask->type != GGML_TYPE_F16 || mask->ne[0] < k->ne[1] || mask->nb[0] != 2 ||
+                 (mask->ne[3] != 1 && mask->ne[3] != n_seq)))
+        return false;
+    if (kvl && (kvl->type != GGML_TYPE_I32 || !ggml_is_contiguous(kvl) || ggml_nelements(kvl) < n_seq)) return false;
     return true;
 }
 
@@ -424,13 +428,15 @@ const float *inv_s_of(const ggml_tensor *w) {
 
 size_t fa_ws_need(const ggml_tensor *node) {
     const ggml_tensor *q = node->src[0], *k = node->src[1];
-    return mi_fa_decode_workspace_size(k->ne[1], q->ne[2], k->ne[2], q->ne[0]);
+    return mi_fa_decode_batch_workspace_size(k->ne[1], q->ne[2], k->ne[2], q->ne[0], q->ne[3]);
 }
 
 size_t scratch_need(const ggml_tensor *node) {
     if (node->op == GGML_OP_MUL_MAT && node->src[0]->type == GGML_TYPE_Q8_0)
         return std::max(mi_mul_mat_q8_0_workspace_size(node->src[1]->ne[1], node->src[1]->ne[0]),
                         node->src[1]->ne[1] == 1 ? mi_xq_size(1, node->src[1]->ne[0]) : (size_t)0);
+    if (node->op == GGML_OP_MUL_MAT && node->src[0]->type == GGML_TYPE_Q4_0)
+        return mi_mul_mat_q4_0_workspace_size(node->src[1]->ne[1], node->src[1]->ne[0]);
     if (node->op == GGML_OP_ARGMAX) return mi_argmax_workspace_size(node->src[0]->ne[0], ggml_nrows(node->src[0]));
     return 0;
 }
@@ -491,7 +497,7 @@ void run_mul_mat(BackendCtx *ctx, ggml_tensor *node) {
             const TensorExtra *ex = (const TensorExtra *)a->extra;
             GGML_ASSERT(ex && ex->ready && "Q4_0 weight used before its upload completed");
             MI_K_CHECK(mi_mul_mat_q4_0_f32(ctx->stream, ex->packed, (const float *)b->data, (float *)node->data, n,
-                                           k, m));
+                                           k, m, ctx->scratch, ctx->scratch_size));
             break;
         }
         case GGML_TYPE_F16:
@@ -508,10 +514,14 @@ void run_fa(BackendCtx *ctx, ggml_tensor *node) {
     const ggml_tensor *kvl = node->src[5];
     float scale;
     memcpy(&scale, node->op_params, sizeof(float));
-    MI_K_CHECK(mi_fa_decode(ctx->stream, (const float *)q->data, k->data, v->data,
-                            mask ? (const uint16_t *)mask->data : nullptr, kvl ? (const int32_t *)kvl->data : nullptr,
-                            k->ne[1], q->ne[2], k->ne[2], q->ne[0], k->nb[1], k->nb[2], v->nb[1], v->nb[2], scale,
-                            (float *)node->data, ctx->fa_ws, ctx->fa_ws_size));
+    // output [d, n_head, 1, n_seq] contiguous; per-sequence strides of the inputs
+    const size_t mask_seq = mask && mask->ne[3] > 1 ? mask->nb[3] / 2 : 0;
+    MI_K_CHECK(mi_fa_decode_batch(ctx->stream, (const float *)q->data, k->data, v->data,
+                                  mask ? (const uint16_t *)mask->data : nullptr,
+                                  kvl ? (const int32_t *)kvl->data : nullptr, k->ne[1], q->ne[2], k->ne[2], q->ne[0],
+                                  k->nb[1], k->nb[2], v->nb[1], v->nb[2], scale, (float *)node->data, q->ne[3],
+                                  q->nb[3] / 4, k->nb[3], v->nb[3], mask_seq, (size_t)(q->ne[0] * q->ne[2]),
+                                  ctx->fa_ws, ctx->fa_ws_size));
 }
 
 // ---- graph fusions

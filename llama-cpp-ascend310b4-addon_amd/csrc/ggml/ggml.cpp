@@ -327,6 +327,17 @@ struct ggml_tensor *ggml_reshape_3d(struct ggml_context *ctx, struct ggml_tensor
     return r;
 }
 
+struct ggml_tensor *ggml_reshape_4d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0, int64_t ne1,
+                                    int64_t ne2, int64_t ne3) {
+    GGML_ASSERT(ggml_is_contiguous(a) && ggml_nelements(a) == ne0 * ne1 * ne2 * ne3);
+    const int64_t ne[4] = {ne0, ne1, ne2, ne3};
+    ggml_tensor *r = new_tensor_impl(ctx, a->type, 4, ne, a, 0);
+    snprintf(r->name, sizeof(r->name), "%.53s (reshaped)", a->name);
+    r->op = GGML_OP_RESHAPE;
+    r->src[0] = a;
+    return r;
+}
+
 static ggml_tensor *view_impl(ggml_context *ctx, ggml_tensor *a, int n_dims, const int64_t *ne, size_t offset) {
     ggml_tensor *r = new_tensor_impl(ctx, a->type, n_dims, ne, a, offset);
     snprintf(r->name, sizeof(r->name), "%.57s (view)", a->name);

@@ -196,6 +196,8 @@ GGML_API struct ggml_tensor *ggml_reshape_2d(struct ggml_context *ctx, struct gg
                                              int64_t ne1);
 GGML_API struct ggml_tensor *ggml_reshape_3d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0,
                                              int64_t ne1, int64_t ne2);
+GGML_API struct ggml_tensor *ggml_reshape_4d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0,
+                                             int64_t ne1, int64_t ne2, int64_t ne3);
 GGML_API struct ggml_tensor *ggml_view_1d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0,
                                           size_t offset);
 GGML_API struct ggml_tensor *ggml_view_2d(struct ggml_context *ctx, struct ggml_tensor *a, int64_t ne0, int64_t ne1,

@@ -166,6 +166,21 @@ __global__ void k_fill_mask(uint16_t *__restrict__ mask, const int32_t *__restri
     if (i < n_kv) mask[i] = i < *len ? (uint16_t)0 : (uint16_t)0xfc00u;
 }
 
+// rows of fp16 values uniform in [-scale, scale) from a counter-based hash (SplitMix64
+// finalizer of seed + element index): synthetic KV-cache contents of a given length
+__global__ void k_fill_f16_uniform(uint8_t *__restrict__ dst, int64_t rows, int64_t row_elems, size_t row_stride,
+                                   uint64_t seed, float scale) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * row_elems) return;
+    const int64_t r = i / row_elems, e = i % row_elems;
+    uint64_t z = seed + 0x9E3779B97F4A7C15ull * (uint64_t)(i + 1);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    const float u = (float)(z >> 40) * (1.0f / 16777216.0f);  // [0, 1)
+    ((uint16_t *)(dst + (size_t)r * row_stride))[e] = f2h((2.0f * u - 1.0f) * scale);
+}
+
 unsigned grid1(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
 
 }  // namespace
@@ -261,6 +276,18 @@ int mi_argmax(void *stream, const float *x, int32_t *out, int64_t ne0, int64_t n
     hipLaunchKernelGGL(k_argmax_final, dim3((unsigned)nrows), dim3(256), 0, (hipStream_t)stream, (const float2 *)ws,
                        out, nchunks);
     MI_CHECK_LAUNCH("k_argmax_final");
+    return MI_OK;
+}
+
+int mi_fill_f16_uniform(void *stream, void *dst, int64_t rows, int64_t row_elems, size_t row_stride, uint64_t seed,
+                        float scale) {
+    MI_CHECK_ARG(dst && rows >= 0 && row_elems > 0 && row_stride >= (size_t)row_elems * 2 && mi::aligned(dst, 2) &&
+                     row_stride % 2 == 0,
+                 "fill_f16_uniform: bad arguments");
+    if (rows == 0) return MI_OK;
+    hipLaunchKernelGGL(k_fill_f16_uniform, dim3(grid1(rows * row_elems, 256)), dim3(256), 0, (hipStream_t)stream,
+                       (uint8_t *)dst, rows, row_elems, row_stride, seed, scale);
+    MI_CHECK_LAUNCH("k_fill_f16_uniform");
     return MI_OK;
 }
 

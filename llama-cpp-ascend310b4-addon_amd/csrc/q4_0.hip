@@ -148,32 +148,39 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0(const uint8_t *__restrict__ q
 }
 
 // fp16 activations read straight from global memory (2*k bytes per row, L1/L2
-// resident and shared by every workgroup): no LDS staging, no barrier.
-template <int G, int U, int M>
+// resident and shared by every workgroup): no LDS staging, no barrier.  R rows per
+// lane group (rows r, r + 256/G, ...) reuse each activation chunk R times.
+template <int G, int U, int M, int R>
 __global__ __launch_bounds__(256) void k_gemv_q4_0_gx(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ wd,
-                                                      const uint16_t *__restrict__ x16, float *__restrict__ y, int n,
-                                                      int nb, int m) {
-    constexpr int RPB = 256 / G;
+                                                      const uint16_t *__restrict__ x16, float *__restrict__ y,
+                                                      const float *__restrict__ add, int n, int nb, int m) {
+    constexpr int RG = 256 / G;
     const int tid = threadIdx.x;
     const int j = tid % G;
-    const int row = blockIdx.x * RPB + tid / G;
-    const bool row_ok = row < n;
+    const int row0 = blockIdx.x * RG * R + tid / G;
     const int k = nb * QK;
-    const size_t rbase = (size_t)min(row, n - 1) * nb;
-
-    float acc[M];
+    size_t rb[R];
 #pragma unroll
-    for (int i = 0; i < M; i++) acc[i] = 0.0f;
+    for (int r = 0; r < R; r++) rb[r] = (size_t)min(row0 + r * RG, n - 1) * nb;
+
+    float acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int i = 0; i < M; i++) acc[r][i] = 0.0f;
 
     for (int b0 = 0; b0 < nb; b0 += U * G) {
-        int4 wq[U];
-        uint32_t dw[U];
+        int4 wq[U][R];
+        uint32_t dw[U][R];
         int4 xv[U][M][4];
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int b = min(b0 + j + u * G, nb - 1);
-            wq[u] = ld_stream16(qs + (rbase + b) * 16);
-            dw[u] = wd[rbase + b];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                wq[u][r] = ld_stream16(qs + (rb[r] + b) * 16);
+                dw[u][r] = wd[rb[r] + b];
+            }
 #pragma unroll
             for (int i = 0; i < M; i++) {
                 const int4 *xp = (const int4 *)(x16 + (size_t)min(i, m - 1) * k + (size_t)b * QK);
@@ -184,7 +191,6 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_gx(const uint8_t *__restrict_
 #pragma unroll
         for (int u = 0; u < U; u++) {
             if (b0 + j + u * G < nb) {
-                const float d = h2f((uint16_t)dw[u]);
 #pragma unroll
                 for (int i = 0; i < M; i++) {
                     uint32_t xs[16];
@@ -193,73 +199,115 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_gx(const uint8_t *__restrict_
                         xs[4 * c + 0] = (uint32_t)xv[u][i][c].x; xs[4 * c + 1] = (uint32_t)xv[u][i][c].y;
                         xs[4 * c + 2] = (uint32_t)xv[u][i][c].z; xs[4 * c + 3] = (uint32_t)xv[u][i][c].w;
                     }
-                    acc[i] = fmaf(d, q4_block_dot(wq[u], xs), acc[i]);
+#pragma unroll
+                    for (int r = 0; r < R; r++)
+                        acc[r][i] = fmaf(h2f((uint16_t)dw[u][r]), q4_block_dot(wq[u][r], xs), acc[r][i]);
                 }
             }
         }
     }
 
 #pragma unroll
-    for (int i = 0; i < M; i++) {
-        const float s = group_sum<G>(acc[i]);
-        if (row_ok && j == 0 && i < m) y[(size_t)i * n + row] = s;
+    for (int r = 0; r < R; r++) {
+        const int row = row0 + r * RG;
+#pragma unroll
+        for (int i = 0; i < M; i++) {
+            const float s = group_sum<G>(acc[r][i]);
+            if (row < n && j == 0 && i < m) y[(size_t)i * n + row] = add ? s + add[(size_t)i * n + row] : s;
+        }
     }
 }
 
-template <int G, int U, int M, bool F32X>
-int launch_gu(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16,
-              const float *x32, float *y) {
+// fp32 -> fp16 (round to nearest even, as ggml's activation conversion)
+__global__ __launch_bounds__(256) void k_cast_f16(const float *__restrict__ x, uint16_t *__restrict__ y, int64_t n4) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const float4 v = ((const float4 *)x)[i];
+    ((uint2 *)y)[i] = make_uint2((uint32_t)f2h(v.x) | ((uint32_t)f2h(v.y) << 16),
+                                 (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16));
+}
+
+inline int q4_pick_u(int64_t nb, int g) {
+    int64_t u = (nb + g - 1) / g;
+    if (u > 8) u = (u + 1) / 2 > 8 ? 8 : (u + 1) / 2;
+    return (int)u;
+}
+
+// activation staged in LDS as fp16 from fp32 (m*k*2 <= 64 KB)
+template <int G, int U, int M>
+int launch_lds_gu(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const float *x32, float *y) {
     const Q4Planes p = q4_planes(n, k);
     constexpr int RPB = 256 / G;
     const size_t smem = (size_t)M * k * 2;
-    if (F32X && smem > 64 * 1024) {
-        set_error("gemv_q4_0: activation of %d x %lld does not fit in LDS", M, (long long)k);
-        return MI_ERR_UNSUPPORTED;
-    }
-    if constexpr (!F32X) {
-        hipLaunchKernelGGL((k_gemv_q4_0_gx<G, U, M>), dim3((unsigned)((n + RPB - 1) / RPB)), dim3(256), 0, st, base,
-                           (const uint16_t *)(base + p.plane), x16, y, (int)n, (int)(k / QK), (int)m);
-        MI_CHECK_LAUNCH("k_gemv_q4_0_gx");
-        return MI_OK;
-    }
-    else {
-        hipLaunchKernelGGL((k_gemv_q4_0<G, U, M, true>), dim3((unsigned)((n + RPB - 1) / RPB)), dim3(256), smem, st,
-                           base, (const uint16_t *)(base + p.plane), x16, x32, y, (int)n, (int)(k / QK), (int)m);
-        MI_CHECK_LAUNCH("k_gemv_q4_0");
-        return MI_OK;
-    }
+    hipLaunchKernelGGL((k_gemv_q4_0<G, U, M, true>), dim3((unsigned)((n + RPB - 1) / RPB)), dim3(256), smem, st, base,
+                       (const uint16_t *)(base + p.plane), nullptr, x32, y, (int)n, (int)(k / QK), (int)m);
+    MI_CHECK_LAUNCH("k_gemv_q4_0");
+    return MI_OK;
 }
 
-template <int G, int M, bool F32X>
-int launch_g(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16,
-             const float *x32, float *y) {
-    const int64_t nb = k / QK;
-    int64_t u = (nb + G - 1) / G;
-    if (u > 8) u = (u + 1) / 2 > 8 ? 8 : (u + 1) / 2;
-#define MI_U_CASE(UU) case UU: return launch_gu<G, UU, M, F32X>(st, base, n, k, m, x16, x32, y);
-    switch (u) {
+template <int G, int M>
+int launch_lds_g(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const float *x32, float *y) {
+#define MI_U_CASE(UU) case UU: return launch_lds_gu<G, UU, M>(st, base, n, k, m, x32, y);
+    switch (q4_pick_u(k / QK, G)) {
         MI_U_CASE(1) MI_U_CASE(2) MI_U_CASE(3) MI_U_CASE(4) MI_U_CASE(5) MI_U_CASE(6) MI_U_CASE(7) MI_U_CASE(8)
     }
 #undef MI_U_CASE
     return MI_ERR_ARG;
 }
 
-template <int M, bool F32X>
-int launch_m(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16,
-             const float *x32, float *y) {
+template <int M>
+int launch_lds_m(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const float *x32, float *y) {
     const int64_t nb = k / QK;
-    if (nb <= 128) return launch_g<16, M, F32X>(st, base, n, k, m, x16, x32, y);
-    if (nb <= 256) return launch_g<32, M, F32X>(st, base, n, k, m, x16, x32, y);
-    return launch_g<64, M, F32X>(st, base, n, k, m, x16, x32, y);
+    if (nb <= 128) return launch_lds_g<16, M>(st, base, n, k, m, x32, y);
+    if (nb <= 256) return launch_lds_g<32, M>(st, base, n, k, m, x32, y);
+    return launch_lds_g<64, M>(st, base, n, k, m, x32, y);
 }
 
-template <bool F32X>
-int launch(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16,
-           const float *x32, float *y) {
-    if (m == 1) return launch_m<1, F32X>(st, base, n, k, m, x16, x32, y);
-    if (m == 2) return launch_m<2, F32X>(st, base, n, k, m, x16, x32, y);
-    if (m >= 3 && m <= 4) return launch_m<4, F32X>(st, base, n, k, m, x16, x32, y);
-    if (m >= 5 && m <= 8) return launch_m<8, F32X>(st, base, n, k, m, x16, x32, y);
+int launch_lds(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const float *x32, float *y) {
+    if ((size_t)m * k * 2 > 64 * 1024) {
+        set_error("gemv_q4_0: activation of %lld x %lld does not fit in LDS", (long long)m, (long long)k);
+        return MI_ERR_UNSUPPORTED;
+    }
+    if (m == 1) return launch_lds_m<1>(st, base, n, k, m, x32, y);
+    if (m == 2) return launch_lds_m<2>(st, base, n, k, m, x32, y);
+    if (m >= 3 && m <= 4) return launch_lds_m<4>(st, base, n, k, m, x32, y);
+    if (m >= 5 && m <= 8) return launch_lds_m<8>(st, base, n, k, m, x32, y);
+    set_error("gemv_q4_0: m=%lld not in 1..8", (long long)m);
+    return MI_ERR_ARG;
+}
+
+// fp16 activation in global memory: 64 lanes per row, two rows per lane group for
+// tall matrices (each activation chunk then feeds two weight blocks)
+template <int U, int M, int R>
+int launch_gx_ur(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16, float *y,
+                 const float *add) {
+    constexpr int G = 64, RPW = (256 / G) * R;
+    const Q4Planes p = q4_planes(n, k);
+    hipLaunchKernelGGL((k_gemv_q4_0_gx<G, U, M, R>), dim3((unsigned)((n + RPW - 1) / RPW)), dim3(256), 0, st, base,
+                       (const uint16_t *)(base + p.plane), x16, y, add, (int)n, (int)(k / QK), (int)m);
+    MI_CHECK_LAUNCH("k_gemv_q4_0_gx");
+    return MI_OK;
+}
+
+template <int M, int R>
+int launch_gx_mr(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16, float *y,
+                 const float *add) {
+#define MI_U_CASE(UU) case UU: return launch_gx_ur<UU, M, R>(st, base, n, k, m, x16, y, add);
+    switch (q4_pick_u(k / QK, 64)) {
+        MI_U_CASE(1) MI_U_CASE(2) MI_U_CASE(3) MI_U_CASE(4) MI_U_CASE(5) MI_U_CASE(6) MI_U_CASE(7) MI_U_CASE(8)
+    }
+#undef MI_U_CASE
+    return MI_ERR_ARG;
+}
+
+int launch_gx(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16, float *y,
+              const float *add = nullptr) {
+    const bool tall = n >= 2048;
+    if (m == 1) return tall ? launch_gx_mr<1, 2>(st, base, n, k, m, x16, y, add)
+                            : launch_gx_mr<1, 1>(st, base, n, k, m, x16, y, add);
+    if (m == 2) return launch_gx_mr<2, 1>(st, base, n, k, m, x16, y, add);
+    if (m >= 3 && m <= 4) return launch_gx_mr<4, 1>(st, base, n, k, m, x16, y, add);
+    if (m >= 5 && m <= 8) return launch_gx_mr<8, 1>(st, base, n, k, m, x16, y, add);
     set_error("gemv_q4_0: m=%lld not in 1..8", (long long)m);
     return MI_ERR_ARG;
 }
@@ -322,15 +370,46 @@ int mi_gemv_q4_0_f16(void *stream, const void *w_packed, const uint16_t *x_f16, 
     if (int r = check_shape("gemv_q4_0_f16", n, k)) return r;
     MI_CHECK_ARG(w_packed && x_f16 && y, "gemv_q4_0_f16: null pointer");
     MI_CHECK_ARG(mi::aligned(w_packed, 256) && mi::aligned(x_f16, 16), "gemv_q4_0_f16: w_packed must be 256-byte, x 16-byte aligned");
-    return launch<false>((hipStream_t)stream, (const uint8_t *)w_packed, n, k, m, x_f16, nullptr, y);
+    return launch_gx((hipStream_t)stream, (const uint8_t *)w_packed, n, k, m, x_f16, y);
+}
+
+int mi_gemv_q4_0_f16_add(void *stream, const void *w_packed, const uint16_t *x_f16, const float *add, float *y,
+                         int64_t n, int64_t k, int64_t m) {
+    if (int r = check_shape("gemv_q4_0_f16_add", n, k)) return r;
+    MI_CHECK_ARG(w_packed && x_f16 && y, "gemv_q4_0_f16_add: null pointer");
+    MI_CHECK_ARG(mi::aligned(w_packed, 256) && mi::aligned(x_f16, 16), "gemv_q4_0_f16_add: w_packed must be 256-byte, x 16-byte aligned");
+    return launch_gx((hipStream_t)stream, (const uint8_t *)w_packed, n, k, m, x_f16, y, add);
+}
+
+size_t mi_mul_mat_q4_0_workspace_size(int64_t m, int64_t k) {
+    if (m * k * 2 <= 64 * 1024) return 0;
+    return mi::align_up((size_t)m * k * 2, 256);
 }
 
 int mi_mul_mat_q4_0_f32(void *stream, const void *w_packed, const float *x, float *y, int64_t n, int64_t k,
-                        int64_t m) {
+                        int64_t m, void *ws, size_t ws_bytes) {
     if (int r = check_shape("mul_mat_q4_0_f32", n, k)) return r;
     MI_CHECK_ARG(w_packed && x && y, "mul_mat_q4_0_f32: null pointer");
+    MI_CHECK_ARG(m >= 1 && m <= 8, "mul_mat_q4_0_f32: m=%lld not in 1..8", (long long)m);
     MI_CHECK_ARG(mi::aligned(w_packed, 256) && mi::aligned(x, 16), "mul_mat_q4_0_f32: w_packed must be 256-byte, x 16-byte aligned");
-    return launch<true>((hipStream_t)stream, (const uint8_t *)w_packed, n, k, m, nullptr, x, y);
+    hipStream_t st = (hipStream_t)stream;
+    const size_t need = mi_mul_mat_q4_0_workspace_size(m, k);
+    if (need == 0) return launch_lds(st, (const uint8_t *)w_packed, n, k, m, x, y);
+    if (!ws || ws_bytes < need || !mi::aligned(ws, 16)) {
+        mi::set_error("mul_mat_q4_0_f32: workspace %zu < %zu bytes (or misaligned)", ws_bytes, need);
+        return MI_ERR_WORKSPACE;
+    }
+    if (int r = mi_cast_f32_f16(stream, x, (uint16_t *)ws, m * k)) return r;
+    return launch_gx(st, (const uint8_t *)w_packed, n, k, m, (const uint16_t *)ws, y);
+}
+
+int mi_cast_f32_f16(void *stream, const float *x, uint16_t *y, int64_t n) {
+    MI_CHECK_ARG(x && y && n > 0 && n % 4 == 0, "cast_f32_f16: bad arguments");
+    MI_CHECK_ARG(mi::aligned(x, 16) && mi::aligned(y, 8), "cast_f32_f16: x must be 16-byte, y 8-byte aligned");
+    const int64_t n4 = n / 4;
+    hipLaunchKernelGGL(k_cast_f16, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x, y, n4);
+    MI_CHECK_LAUNCH("k_cast_f16");
+    return MI_OK;
 }
 
 }  // extern "C"

@@ -1,13 +1,16 @@
 // qwen2.cpp -- minimal Qwen2 decode driver over the ggml backend API (see mi_qwen2.h).
 //
-// Graph per token, following llama.cpp's Qwen2 builder: GET_ROWS(token_embd) ->
-// 28 x [RMS_NORM, MUL, q/k/v MUL_MAT (+bias ADD), ROPE neox, SET_ROWS K/V into the
+// Graph per step, following llama.cpp's Qwen2 builder: GET_ROWS(token_embd) ->
+// n_layer x [RMS_NORM, MUL, q/k/v MUL_MAT (+bias ADD), ROPE neox, SET_ROWS K/V into the
 // fp16 cache, FLASH_ATTN_EXT (+kv_lengths src[5]), MUL_MAT o, ADD residual,
 // RMS_NORM, MUL, gate/up MUL_MAT, GLU swiglu, MUL_MAT down, ADD residual] ->
-// RMS_NORM, MUL, MUL_MAT(tied token_embd) -> ARGMAX.  The KV view handed to the
-// attention covers the used cache rounded up to 256 positions (as llama.cpp's
-// KV view is), so one graph serves 256 consecutive positions and the backend
-// replays it as a captured HIP graph.
+// RMS_NORM, MUL, MUL_MAT(tied token_embd) -> ARGMAX.  A step decodes one token for
+// each of n_seq independent sequences (one ubatch of n_seq tokens).  Each sequence
+// owns n_ctx rows of every layer's cache; the attention sees the caches as n_seq
+// streams (ggml ne[3]), as llama.cpp's per-sequence KV streams.  The KV view covers
+// the longest used cache rounded up to 256 positions (as llama.cpp's KV view is), so
+// one graph serves 256 consecutive positions and the backend replays it as a captured
+// HIP graph.
 #include "mi_qwen2.h"
 
 #include <math.h>
@@ -15,6 +18,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <chrono>
 #include <map>
 #include <string>
@@ -23,6 +27,7 @@
 #include "ggml-backend.h"
 #include "ggml-mi355x.h"
 #include "ggml.h"
+#include "ggml_mi355x_kernels.h"
 
 namespace {
 
@@ -48,13 +53,14 @@ struct Graph {
 
 struct mi_qwen2 {
     mi_qwen2_hparams hp;
+    int n_seq = 1;
     ggml_backend_t backend = nullptr;
     ggml_context *wctx = nullptr;
     ggml_backend_buffer_t wbuf = nullptr;
     std::map<std::string, ggml_tensor *> tensors;
-    std::vector<ggml_tensor *> k_cache, v_cache;
-    ggml_tensor *inp = nullptr;  // I32 [4]: token, position, kv length, cache row
-    int32_t inp_host[4] = {0, 0, 0, 0};
+    std::vector<ggml_tensor *> k_cache, v_cache;  // F16 [n_embd_kv, n_ctx * n_seq]
+    ggml_tensor *inp = nullptr;  // I32 [4 * n_seq]: tokens, positions, kv lengths, cache rows
+    std::vector<int32_t> inp_host;
     std::map<int, Graph> graphs;  // by KV view length
 };
 
@@ -75,6 +81,7 @@ ggml_tensor *add_tensor(mi_qwen2 *m, const std::string &name, ggml_type type, in
 
 Graph build_graph(mi_qwen2 *m, int n_kv) {
     const mi_qwen2_hparams &hp = m->hp;
+    const int S = m->n_seq;
     const int hd = hp.head_dim, n_embd_kv = hp.n_head_kv * hd;
     Graph G;
     ggml_init_params ip = {0, nullptr, true};
@@ -83,10 +90,10 @@ Graph build_graph(mi_qwen2 *m, int n_kv) {
     ggml_cgraph *gf = ggml_new_graph_custom(ctx, 16384, false);
     G.gf = gf;
 
-    ggml_tensor *tok = ggml_view_1d(ctx, m->inp, 1, 0);
-    ggml_tensor *pos = ggml_view_1d(ctx, m->inp, 1, 4);
-    ggml_tensor *kvl = ggml_view_1d(ctx, m->inp, 1, 8);
-    ggml_tensor *kidx = ggml_view_1d(ctx, m->inp, 1, 12);
+    ggml_tensor *tok = ggml_view_1d(ctx, m->inp, S, 0);
+    ggml_tensor *pos = ggml_view_1d(ctx, m->inp, S, 4 * (size_t)S);
+    ggml_tensor *kvl = ggml_view_1d(ctx, m->inp, S, 8 * (size_t)S);
+    ggml_tensor *kidx = ggml_view_1d(ctx, m->inp, S, 12 * (size_t)S);
     ggml_tensor *tok_embd = W(m, "token_embd.weight");
 
     ggml_tensor *inpL = ggml_get_rows(ctx, tok_embd, tok);
@@ -109,8 +116,8 @@ Graph build_graph(mi_qwen2 *m, int n_kv) {
             ggml_build_forward_expand(gf, K);
             ggml_build_forward_expand(gf, V);
         }
-        Q = ggml_reshape_3d(ctx, Q, hd, hp.n_head, 1);
-        K = ggml_reshape_3d(ctx, K, hd, hp.n_head_kv, 1);
+        Q = ggml_reshape_3d(ctx, Q, hd, hp.n_head, S);
+        K = ggml_reshape_3d(ctx, K, hd, hp.n_head_kv, S);
         Q = ggml_rope_ext(ctx, Q, pos, nullptr, hd, GGML_ROPE_TYPE_NEOX, 0, hp.rope_theta, 1.0f, 0.0f, 1.0f, 0.0f,
                           0.0f);
         K = ggml_rope_ext(ctx, K, pos, nullptr, hd, GGML_ROPE_TYPE_NEOX, 0, hp.rope_theta, 1.0f, 0.0f, 1.0f, 0.0f,
@@ -118,15 +125,19 @@ Graph build_graph(mi_qwen2 *m, int n_kv) {
         ggml_build_forward_expand(gf, Q);  // rope q, rope k, then the two cache writes: the
         ggml_build_forward_expand(gf, K);  // attention-input chain the backend fuses
         ggml_tensor *kc = m->k_cache[il], *vc = m->v_cache[il];
-        ggml_build_forward_expand(gf, ggml_set_rows(ctx, kc, ggml_reshape_2d(ctx, K, n_embd_kv, 1), kidx));
+        ggml_build_forward_expand(gf, ggml_set_rows(ctx, kc, ggml_reshape_2d(ctx, K, n_embd_kv, S), kidx));
         ggml_build_forward_expand(gf, ggml_set_rows(ctx, vc, V, kidx));
-        ggml_tensor *k = ggml_view_3d(ctx, kc, hd, n_kv, hp.n_head_kv, kc->nb[1], ggml_row_size(GGML_TYPE_F16, hd), 0);
-        ggml_tensor *v = ggml_view_3d(ctx, vc, hd, n_kv, hp.n_head_kv, vc->nb[1], ggml_row_size(GGML_TYPE_F16, hd), 0);
-        ggml_tensor *q = ggml_permute(ctx, Q, 0, 2, 1, 3);
+        // sequence s's cache is rows [s*n_ctx, (s+1)*n_ctx): stream s of the 4-D view
+        const size_t seq_bytes = (size_t)hp.n_ctx * kc->nb[1];
+        ggml_tensor *k = ggml_view_4d(ctx, kc, hd, n_kv, hp.n_head_kv, S, kc->nb[1], ggml_row_size(GGML_TYPE_F16, hd),
+                                      seq_bytes, 0);
+        ggml_tensor *v = ggml_view_4d(ctx, vc, hd, n_kv, hp.n_head_kv, S, vc->nb[1], ggml_row_size(GGML_TYPE_F16, hd),
+                                      seq_bytes, 0);
+        ggml_tensor *q = ggml_permute(ctx, ggml_reshape_4d(ctx, Q, hd, hp.n_head, 1, S), 0, 2, 1, 3);
         ggml_tensor *att = ggml_flash_attn_ext(ctx, q, k, v, nullptr, kq_scale, 0.0f, 0.0f);
         ggml_flash_attn_ext_add_kv_lengths(att, kvl);
         ggml_flash_attn_ext_set_prec(att, GGML_PREC_F32);
-        cur = ggml_reshape_2d(ctx, att, hd * hp.n_head, 1);
+        cur = ggml_reshape_2d(ctx, att, hd * hp.n_head, S);
         cur = ggml_mul_mat(ctx, W(m, p + "attn_output.weight"), cur);
         ggml_tensor *ffn_inp = ggml_add(ctx, cur, inpL);
         cur = ggml_rms_norm(ctx, ffn_inp, hp.rms_eps);
@@ -164,6 +175,13 @@ Graph &graph_for(mi_qwen2 *m, int32_t kv_len) {
     return m->graphs.emplace(n_kv, build_graph(m, n_kv)).first->second;
 }
 
+int check_cache_args(mi_qwen2 *m, int32_t layer, int32_t seq, int32_t n_pos) {
+    if (layer < 0 || layer >= m->hp.n_layer) return fail("qwen2: layer %d out of range", layer);
+    if (seq < 0 || seq >= m->n_seq) return fail("qwen2: sequence %d out of range", seq);
+    if (n_pos < 0 || n_pos > m->hp.n_ctx) return fail("qwen2: n_pos %d outside the cache", n_pos);
+    return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -173,12 +191,15 @@ const char *mi_qwen2_last_error(void) { return g_err; }
 mi_qwen2 *mi_qwen2_create(const mi_qwen2_hparams *hp, int device) {
     if (!hp || hp->n_layer <= 0 || hp->n_embd <= 0 || hp->n_head <= 0 || hp->n_head_kv <= 0 ||
         hp->n_head % hp->n_head_kv != 0 || hp->head_dim * hp->n_head != hp->n_embd || hp->n_ctx <= 0 ||
-        (hp->wtype != GGML_TYPE_Q8_0 && hp->wtype != GGML_TYPE_Q4_0)) {
+        hp->n_seq < 0 || hp->n_seq > 8 || (hp->wtype != GGML_TYPE_Q8_0 && hp->wtype != GGML_TYPE_Q4_0)) {
         fail("qwen2: invalid hyper-parameters");
         return nullptr;
     }
     mi_qwen2 *m = new mi_qwen2();
     m->hp = *hp;
+    m->n_seq = hp->n_seq > 0 ? hp->n_seq : 1;
+    m->hp.n_seq = m->n_seq;
+    m->inp_host.assign(4 * (size_t)m->n_seq, 0);
     m->backend = ggml_backend_mi355x_init(device);
     if (!m->backend) {
         delete m;
@@ -207,14 +228,14 @@ mi_qwen2 *mi_qwen2_create(const mi_qwen2_hparams *hp, int device) {
         add_tensor(m, p + "ffn_gate.weight", wt, hp->n_embd, hp->n_ff);
         add_tensor(m, p + "ffn_up.weight", wt, hp->n_embd, hp->n_ff);
         add_tensor(m, p + "ffn_down.weight", wt, hp->n_ff, hp->n_embd);
-        ggml_tensor *kc = ggml_new_tensor_2d(m->wctx, GGML_TYPE_F16, n_embd_kv, hp->n_ctx);
-        ggml_tensor *vc = ggml_new_tensor_2d(m->wctx, GGML_TYPE_F16, n_embd_kv, hp->n_ctx);
+        ggml_tensor *kc = ggml_new_tensor_2d(m->wctx, GGML_TYPE_F16, n_embd_kv, (int64_t)hp->n_ctx * m->n_seq);
+        ggml_tensor *vc = ggml_new_tensor_2d(m->wctx, GGML_TYPE_F16, n_embd_kv, (int64_t)hp->n_ctx * m->n_seq);
         ggml_set_name(kc, ("cache_k_l" + std::to_string(il)).c_str());
         ggml_set_name(vc, ("cache_v_l" + std::to_string(il)).c_str());
         m->k_cache.push_back(kc);
         m->v_cache.push_back(vc);
     }
-    m->inp = ggml_new_tensor_1d(m->wctx, GGML_TYPE_I32, 4);
+    m->inp = ggml_new_tensor_1d(m->wctx, GGML_TYPE_I32, 4 * (int64_t)m->n_seq);
     ggml_set_name(m->inp, "inp_decode");
     ggml_set_input(m->inp);
     m->wbuf = ggml_backend_alloc_ctx_tensors_from_buft(m->wctx, ggml_backend_mi355x_buffer_type(device));
@@ -248,6 +269,8 @@ int mi_qwen2_reset(mi_qwen2 *m) {
     return 0;
 }
 
+int32_t mi_qwen2_n_seq(const mi_qwen2 *m) { return m->n_seq; }
+
 int64_t mi_qwen2_tensor_nbytes(mi_qwen2 *m, const char *name, int64_t *dims) {
     auto it = m->tensors.find(name);
     if (it == m->tensors.end()) return -1;
@@ -275,38 +298,68 @@ int mi_qwen2_set_smooth(mi_qwen2 *m, const char *weight_name, const float *s, in
     return 0;
 }
 
-int mi_qwen2_decode(mi_qwen2 *m, int32_t token, int32_t pos, int32_t *next_token, float *logits) {
-    if (pos < 0 || pos >= m->hp.n_ctx) return fail("qwen2: position %d outside the cache (%d)", pos, m->hp.n_ctx);
-    if (token < 0 || token >= m->hp.n_vocab) return fail("qwen2: token %d outside the vocabulary", token);
-    Graph &G = graph_for(m, pos + 1);
-    m->inp_host[0] = token;
-    m->inp_host[1] = pos;
-    m->inp_host[2] = pos + 1;
-    m->inp_host[3] = pos;
-    ggml_backend_tensor_set(m->inp, m->inp_host, 0, sizeof(m->inp_host));
+int mi_qwen2_decode_batch(mi_qwen2 *m, const int32_t *tokens, const int32_t *pos, int32_t *next_tokens,
+                          float *logits) {
+    const int S = m->n_seq;
+    if (!tokens || !pos) return fail("qwen2: tokens/positions are NULL");
+    int32_t max_len = 0;
+    for (int s = 0; s < S; s++) {
+        if (pos[s] < 0 || pos[s] >= m->hp.n_ctx)
+            return fail("qwen2: position %d of sequence %d outside the cache (%d)", pos[s], s, m->hp.n_ctx);
+        if (tokens[s] < 0 || tokens[s] >= m->hp.n_vocab)
+            return fail("qwen2: token %d of sequence %d outside the vocabulary", tokens[s], s);
+        max_len = std::max(max_len, pos[s] + 1);
+    }
+    Graph &G = graph_for(m, max_len);
+    for (int s = 0; s < S; s++) {
+        m->inp_host[s] = tokens[s];
+        m->inp_host[S + s] = pos[s];
+        m->inp_host[2 * S + s] = pos[s] + 1;
+        m->inp_host[3 * S + s] = s * m->hp.n_ctx + pos[s];
+    }
+    ggml_backend_tensor_set(m->inp, m->inp_host.data(), 0, m->inp_host.size() * sizeof(int32_t));
     if (ggml_backend_graph_compute(m->backend, G.gf) != GGML_STATUS_SUCCESS) return fail("qwen2: graph failed");
-    if (next_token) ggml_backend_tensor_get(G.argmax, next_token, 0, sizeof(int32_t));
+    if (next_tokens) ggml_backend_tensor_get(G.argmax, next_tokens, 0, (size_t)S * sizeof(int32_t));
     if (logits) ggml_backend_tensor_get(G.logits, logits, 0, ggml_nbytes(G.logits));
     return 0;
 }
 
-int mi_qwen2_decode_steps(mi_qwen2 *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out_tokens,
-                          double *seconds) {
-    if (n_steps < 0 || pos < 0 || pos + n_steps > m->hp.n_ctx) return fail("qwen2: bad decode range");
+int mi_qwen2_decode(mi_qwen2 *m, int32_t token, int32_t pos, int32_t *next_token, float *logits) {
+    if (m->n_seq != 1) return fail("qwen2: mi_qwen2_decode needs n_seq == 1 (use mi_qwen2_decode_batch)");
+    return mi_qwen2_decode_batch(m, &token, &pos, next_token, logits);
+}
+
+int mi_qwen2_decode_steps_batch(mi_qwen2 *m, const int32_t *tokens, const int32_t *pos, int32_t n_steps,
+                                int32_t *out_tokens, double *seconds) {
+    const int S = m->n_seq;
+    if (n_steps < 0 || !tokens || !pos) return fail("qwen2: bad decode range");
+    for (int s = 0; s < S; s++)
+        if (pos[s] < 0 || pos[s] + n_steps > m->hp.n_ctx) return fail("qwen2: bad decode range");
     if (n_steps > 0 && !out_tokens) return fail("qwen2: out_tokens is NULL");
+    std::vector<int32_t> cur(tokens, tokens + S), p(pos, pos + S), nxt(S);
     const auto t0 = std::chrono::steady_clock::now();
-    int32_t next = token;
     for (int32_t i = 0; i < n_steps; i++) {
-        if (mi_qwen2_decode(m, next, pos + i, &next, nullptr)) return -1;
-        out_tokens[i] = next;
+        if (mi_qwen2_decode_batch(m, cur.data(), p.data(), nxt.data(), nullptr)) return -1;
+        for (int s = 0; s < S; s++) {
+            out_tokens[(size_t)i * S + s] = nxt[s];
+            cur[s] = nxt[s];
+            p[s]++;
+        }
     }
     const auto t1 = std::chrono::steady_clock::now();
     if (seconds) *seconds = std::chrono::duration<double>(t1 - t0).count();
     return 0;
 }
 
+int mi_qwen2_decode_steps(mi_qwen2 *m, int32_t token, int32_t pos, int32_t n_steps, int32_t *out_tokens,
+                          double *seconds) {
+    if (m->n_seq != 1) return fail("qwen2: mi_qwen2_decode_steps needs n_seq == 1");
+    return mi_qwen2_decode_steps_batch(m, &token, &pos, n_steps, out_tokens, seconds);
+}
+
 int mi_qwen2_generate(mi_qwen2 *m, const int32_t *prompt, int32_t n_prompt, int32_t n_gen, int32_t *out_tokens,
                       double *gen_seconds) {
+    if (m->n_seq != 1) return fail("qwen2: mi_qwen2_generate needs n_seq == 1");
     if (!prompt || n_prompt < 1 || n_gen < 0 || n_prompt + n_gen > m->hp.n_ctx)
         return fail("qwen2: bad prompt/generation size");
     int32_t next = 0;
@@ -316,13 +369,44 @@ int mi_qwen2_generate(mi_qwen2 *m, const int32_t *prompt, int32_t n_prompt, int3
     return mi_qwen2_decode_steps(m, next, n_prompt, n_gen, out_tokens, gen_seconds);
 }
 
-int mi_qwen2_get_cache(mi_qwen2 *m, int32_t layer, int32_t is_v, int32_t n_pos, void *dst, size_t size) {
-    if (layer < 0 || layer >= m->hp.n_layer) return fail("qwen2: layer %d out of range", layer);
-    if (n_pos < 0 || n_pos > m->hp.n_ctx) return fail("qwen2: n_pos %d outside the cache", n_pos);
+int mi_qwen2_get_cache_seq(mi_qwen2 *m, int32_t layer, int32_t is_v, int32_t seq, int32_t n_pos, void *dst,
+                           size_t size) {
+    if (check_cache_args(m, layer, seq, n_pos)) return -1;
     ggml_tensor *c = is_v ? m->v_cache[layer] : m->k_cache[layer];
     const size_t bytes = (size_t)n_pos * c->nb[1];
     if (!dst || size != bytes) return fail("qwen2: cache copy needs %zu bytes, got %zu", bytes, size);
-    if (bytes) ggml_backend_tensor_get(c, dst, 0, bytes);
+    if (bytes) ggml_backend_tensor_get(c, dst, (size_t)seq * m->hp.n_ctx * c->nb[1], bytes);
+    return 0;
+}
+
+int mi_qwen2_set_cache_seq(mi_qwen2 *m, int32_t layer, int32_t is_v, int32_t seq, int32_t n_pos, const void *src,
+                           size_t size) {
+    if (check_cache_args(m, layer, seq, n_pos)) return -1;
+    ggml_tensor *c = is_v ? m->v_cache[layer] : m->k_cache[layer];
+    const size_t bytes = (size_t)n_pos * c->nb[1];
+    if (!src || size != bytes) return fail("qwen2: cache copy needs %zu bytes, got %zu", bytes, size);
+    if (bytes) ggml_backend_tensor_set(c, src, (size_t)seq * m->hp.n_ctx * c->nb[1], bytes);
+    return 0;
+}
+
+int mi_qwen2_get_cache(mi_qwen2 *m, int32_t layer, int32_t is_v, int32_t n_pos, void *dst, size_t size) {
+    return mi_qwen2_get_cache_seq(m, layer, is_v, 0, n_pos, dst, size);
+}
+
+int mi_qwen2_fill_cache(mi_qwen2 *m, int32_t n_pos, uint64_t seed, float scale) {
+    if (n_pos < 0 || n_pos > m->hp.n_ctx) return fail("qwen2: n_pos %d outside the cache", n_pos);
+    for (int il = 0; il < m->hp.n_layer; il++) {
+        for (int kv = 0; kv < 2; kv++) {
+            ggml_tensor *c = kv ? m->v_cache[il] : m->k_cache[il];
+            for (int s = 0; s < m->n_seq; s++) {
+                uint8_t *base = (uint8_t *)c->data + (size_t)s * m->hp.n_ctx * c->nb[1];
+                const uint64_t sd = seed + 0x1000003ull * (uint64_t)((il * 2 + kv) * m->n_seq + s);
+                if (mi_fill_f16_uniform(nullptr, base, n_pos, c->ne[0], c->nb[1], sd, scale))
+                    return fail("qwen2: cache fill failed: %s", mi_last_error());
+            }
+        }
+    }
+    if (mi_device_sync()) return fail("qwen2: cache fill failed: %s", mi_last_error());
     return 0;
 }
 

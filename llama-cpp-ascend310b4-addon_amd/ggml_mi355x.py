@@ -78,11 +78,17 @@ _SIGS = {
     "mi_mul_mat_q8_0_f32": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _SZ]),
     "mi_q8_0_block_dots": (_I, [_P, _P, _P, _P, _I64, _I64]),
     "mi_gemv_q4_0_f16": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
-    "mi_mul_mat_q4_0_f32": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
+    "mi_mul_mat_q4_0_f32": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ]),
+    "mi_mul_mat_q4_0_workspace_size": (_SZ, [_I64, _I64]),
+    "mi_gemv_q4_0_f16_add": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64]),
+    "mi_cast_f32_f16": (_I, [_P, _P, _P, _I64]),
     "mi_gemv_f16": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _I64]),
     "mi_fa_decode_workspace_size": (_SZ, [_I64, _I64, _I64, _I64]),
     "mi_fa_decode": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _SZ, _SZ, _SZ, _SZ, _F, _P, _P, _SZ]),
     "mi_kv_lengths": (_I, [_P, _P, _I, _I64, _I64, _P]),
+    "mi_fa_decode_batch_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
+    "mi_fa_decode_batch": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _SZ, _SZ, _SZ, _SZ, _F, _P, _I64, _SZ,
+                                _SZ, _SZ, _SZ, _SZ, _P, _SZ]),
     "mi_mul_mat_q8_0_f32_multi": (_I, [_P, _I, _P, _P, _P, _I64, _P, _P, _I, _P, _SZ]),
     "mi_rms_norm": (_I, [_P, _P, _P, _P, _I64, _I64, _F]),
     "mi_add_bcast": (_I, [_P, _P, _P, _P, _I64, _I64]),
@@ -99,6 +105,7 @@ _SIGS = {
     "mi_swiglu_quant_q8_0": (_I, [_P, _P, _P, _P, _I64, _P, _I]),
     "mi_gemv_q8_0_add": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64]),
     "mi_fill_mask_f16": (_I, [_P, _P, _P, _I64]),
+    "mi_fill_f16_uniform": (_I, [_P, _P, _I64, _I64, _SZ, ctypes.c_uint64, _F]),
 }
 
 # every symbol the C ABI header declares (checked by the CPU tests)
@@ -349,8 +356,12 @@ def gemv_q4_0_f16(w_packed, x16, y, n, k, m=1, stream=None):
     _call("mi_gemv_q4_0_f16", _P(stream), _P(w_packed), _P(x16), _P(y), n, k, m)
 
 
-def mul_mat_q4_0_f32(w_packed, x, y, n, k, m=1, stream=None):
-    _call("mi_mul_mat_q4_0_f32", _P(stream), _P(w_packed), _P(x), _P(y), n, k, m)
+def mul_mat_q4_0_workspace_size(m, k):
+    return lib().mi_mul_mat_q4_0_workspace_size(m, k)
+
+
+def mul_mat_q4_0_f32(w_packed, x, y, n, k, m=1, ws=None, ws_bytes=0, stream=None):
+    _call("mi_mul_mat_q4_0_f32", _P(stream), _P(w_packed), _P(x), _P(y), n, k, m, _P(ws), ws_bytes)
 
 
 def gemv_f16(w, ldw, x, y, n, k, m=1, stream=None):
@@ -367,6 +378,17 @@ def fa_decode(q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1, k_nb
           k_nb1, k_nb2, v_nb1, v_nb2, scale, _P(out), _P(ws), ws_bytes)
 
 
+def fa_decode_batch_workspace_size(n_kv, n_q_heads, n_kv_heads, d, n_seq):
+    return lib().mi_fa_decode_batch_workspace_size(n_kv, n_q_heads, n_kv_heads, d, n_seq)
+
+
+def fa_decode_batch(q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1, k_nb2, v_nb1, v_nb2, scale, out,
+                    n_seq, q_seq, k_seq, v_seq, mask_seq, out_seq, ws, ws_bytes, stream=None):
+    _call("mi_fa_decode_batch", _P(stream), _P(q), _P(k), _P(v), _P(mask), _P(kv_len), n_kv, n_q_heads, n_kv_heads,
+          d, k_nb1, k_nb2, v_nb1, v_nb2, scale, _P(out), n_seq, q_seq, k_seq, v_seq, mask_seq, out_seq, _P(ws),
+          ws_bytes)
+
+
 def kv_lengths(mask, is_f16, n_kv, n_rows, out, stream=None):
     _call("mi_kv_lengths", _P(stream), _P(mask), 1 if is_f16 else 0, n_kv, n_rows, _P(out))
 
@@ -377,7 +399,8 @@ class _QwenHP(ctypes.Structure):
     _fields_ = [("n_layer", ctypes.c_int32), ("n_embd", ctypes.c_int32), ("n_head", ctypes.c_int32),
                 ("n_head_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("n_ff", ctypes.c_int32),
                 ("n_vocab", ctypes.c_int32), ("n_ctx", ctypes.c_int32), ("rms_eps", ctypes.c_float),
-                ("rope_theta", ctypes.c_float), ("wtype", ctypes.c_int32), ("use_bias", ctypes.c_int32)]
+                ("rope_theta", ctypes.c_float), ("wtype", ctypes.c_int32), ("use_bias", ctypes.c_int32),
+                ("n_seq", ctypes.c_int32)]
 
 
 _QWEN_SIGS = {
@@ -391,6 +414,12 @@ _QWEN_SIGS = {
     "mi_qwen2_generate": (_I, [_P, _P, ctypes.c_int32, ctypes.c_int32, _P, ctypes.POINTER(ctypes.c_double)]),
     "mi_qwen2_decode_steps": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P,
                                   ctypes.POINTER(ctypes.c_double)]),
+    "mi_qwen2_n_seq": (ctypes.c_int32, [_P]),
+    "mi_qwen2_decode_batch": (_I, [_P, _P, _P, _P, _P]),
+    "mi_qwen2_decode_steps_batch": (_I, [_P, _P, _P, ctypes.c_int32, _P, ctypes.POINTER(ctypes.c_double)]),
+    "mi_qwen2_get_cache_seq": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, _SZ]),
+    "mi_qwen2_set_cache_seq": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, _SZ]),
+    "mi_qwen2_fill_cache": (_I, [_P, ctypes.c_int32, ctypes.c_uint64, ctypes.c_float]),
     "mi_qwen2_get_cache": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, _SZ]),
     "mi_qwen2_reset": (_I, [_P]),
 }
@@ -415,12 +444,13 @@ class Qwen2Model:
         L = _qlib()
         h = _QwenHP()
         for f, _ in _QwenHP._fields_:
-            setattr(h, f, hp[f])
+            setattr(h, f, hp.get(f, 1 if f == "n_seq" else 0))
         self.hp = dict(hp)
         self.ptr = L.mi_qwen2_create(ctypes.byref(h), device)
         if not self.ptr:
             raise MiError("mi_qwen2_create", -1, L.mi_qwen2_last_error().decode())
-        self.logits = np.empty(hp["n_vocab"], np.float32)
+        self.n_seq = int(L.mi_qwen2_n_seq(self.ptr))
+        self.logits = np.empty(hp["n_vocab"] * self.n_seq, np.float32)
 
     def _chk(self, name, r):
         if r != 0:
@@ -463,6 +493,42 @@ class Qwen2Model:
         self._chk("mi_qwen2_decode_steps", _qlib().mi_qwen2_decode_steps(self.ptr, int(token), int(pos), int(n_steps),
                                                                          out.ctypes.data, ctypes.byref(secs)))
         return out[:n_steps], secs.value
+
+    def decode_batch(self, tokens, pos, want_logits=False):
+        """one step of all sequences -> next tokens [n_seq] (and logits [n_seq, n_vocab])"""
+        t = np.ascontiguousarray(tokens, np.int32)
+        p = np.ascontiguousarray(pos, np.int32)
+        assert t.size == self.n_seq and p.size == self.n_seq
+        nxt = np.empty(self.n_seq, np.int32)
+        self._chk("mi_qwen2_decode_batch", _qlib().mi_qwen2_decode_batch(
+            self.ptr, t.ctypes.data, p.ctypes.data, nxt.ctypes.data, self.logits.ctypes.data if want_logits else None))
+        if want_logits:
+            return nxt, self.logits.reshape(self.n_seq, -1).copy()
+        return nxt
+
+    def decode_steps_batch(self, tokens, pos, n_steps):
+        """greedy continuation of all sequences -> (tokens [n_steps, n_seq], seconds)"""
+        t = np.ascontiguousarray(tokens, np.int32)
+        p = np.ascontiguousarray(pos, np.int32)
+        out = np.empty((max(n_steps, 1), self.n_seq), np.int32)
+        secs = ctypes.c_double(0.0)
+        self._chk("mi_qwen2_decode_steps_batch", _qlib().mi_qwen2_decode_steps_batch(
+            self.ptr, t.ctypes.data, p.ctypes.data, int(n_steps), out.ctypes.data, ctypes.byref(secs)))
+        return out[:n_steps], secs.value
+
+    def get_cache_seq(self, layer, is_v, seq, n_pos):
+        out = np.empty((n_pos, self.hp["n_head_kv"] * self.hp["head_dim"]), np.uint16)
+        self._chk("mi_qwen2_get_cache_seq", _qlib().mi_qwen2_get_cache_seq(
+            self.ptr, int(layer), int(is_v), int(seq), int(n_pos), out.ctypes.data, out.nbytes))
+        return out
+
+    def set_cache_seq(self, layer, is_v, seq, data):
+        data = np.ascontiguousarray(data, np.uint16)
+        self._chk("mi_qwen2_set_cache_seq", _qlib().mi_qwen2_set_cache_seq(
+            self.ptr, int(layer), int(is_v), int(seq), int(data.shape[0]), data.ctypes.data, data.nbytes))
+
+    def fill_cache(self, n_pos, seed=0, scale=1.0):
+        self._chk("mi_qwen2_fill_cache", _qlib().mi_qwen2_fill_cache(self.ptr, int(n_pos), int(seed), float(scale)))
 
     def get_cache(self, layer, is_v, n_pos):
         """fp16 bits [n_pos, n_head_kv*head_dim] of one layer's K or V cache"""

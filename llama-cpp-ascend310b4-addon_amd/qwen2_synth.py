@@ -21,14 +21,14 @@ GGML_TYPE_Q8_0 = 8
 
 def qwen2_1p5b(n_ctx=576, **kw):
     hp = dict(n_layer=28, n_embd=1536, n_head=12, n_head_kv=2, head_dim=128, n_ff=8960, n_vocab=151936,
-              n_ctx=n_ctx, rms_eps=1e-6, rope_theta=1e6, wtype=GGML_TYPE_Q8_0, use_bias=1)
+              n_ctx=n_ctx, rms_eps=1e-6, rope_theta=1e6, wtype=GGML_TYPE_Q8_0, use_bias=1, n_seq=1)
     hp.update(kw)
     return hp
 
 
 def qwen2_7b(n_ctx=32768 + 128, **kw):
     hp = dict(n_layer=28, n_embd=3584, n_head=28, n_head_kv=4, head_dim=128, n_ff=18944, n_vocab=152064,
-              n_ctx=n_ctx, rms_eps=1e-6, rope_theta=1e6, wtype=GGML_TYPE_Q4_0, use_bias=1)
+              n_ctx=n_ctx, rms_eps=1e-6, rope_theta=1e6, wtype=GGML_TYPE_Q4_0, use_bias=1, n_seq=1)
     hp.update(kw)
     return hp
 

@@ -152,8 +152,11 @@ def test_q8_0_gemv_shapes(gpu, orc, n, k, m):
 
 # ---------------------------------------------------------------- W4A16
 
-@pytest.mark.parametrize("n,k,m", [(1536, 8960, 1), (8960, 1536, 1), (7, 32, 1), (512, 3584, 8), (100, 18944, 1)])
+@pytest.mark.parametrize("n,k,m", [(1536, 8960, 1), (8960, 1536, 1), (7, 32, 1), (512, 3584, 8), (100, 18944, 1),
+                                   (4608, 3584, 1), (2049, 256, 1), (300, 18944, 8), (3584, 4096, 5)])
 def test_w4a16_gemv(gpu, orc, n, k, m):
+    """fp16 activations from global memory (one or two rows per lane group) and the fp32
+    MUL_MAT path (fp16 staging in LDS, or through a workspace when m*k*2 > 64 KB)"""
     mi = gpu
     rng = np.random.default_rng(n + k + m)
     w = q4_0_weights(rng, n, k)
@@ -166,7 +169,9 @@ def test_w4a16_gemv(gpu, orc, n, k, m):
     x32 = x16.view(np.float16).astype(np.float32)
     dx32 = mi.to_device(x32)
     dy32 = mi.DeviceBuffer(m * n * 4)
-    mi.mul_mat_q4_0_f32(wp.ptr, dx32.ptr, dy32.ptr, n, k, m)
+    wsb = mi.mul_mat_q4_0_workspace_size(m, k)
+    ws = mi.DeviceBuffer(max(wsb, 16))
+    mi.mul_mat_q4_0_f32(wp.ptr, dx32.ptr, dy32.ptr, n, k, m, ws=ws.ptr, ws_bytes=wsb)
     mi.device_sync()
     y = dy.download(np.float32).reshape(m, n)
     for i in range(m):
@@ -176,7 +181,7 @@ def test_w4a16_gemv(gpu, orc, n, k, m):
         print(f"w4a16 {n}x{k} row {i}: rel_err vs ggml-cpu {err:.3e}, vs fp64 {rel_err(y[i], ref64):.3e}")
         assert err < GEMV_TOL
         assert rel_err(y[i], ref64) < 1e-5
-    assert np.array_equal(dy32.download(np.float32).reshape(m, n), y)
+    assert rel_err(dy32.download(np.float32).reshape(m, n), y) < 1e-5
 
 
 # ---------------------------------------------------------------- F16
@@ -307,3 +312,37 @@ def test_kv_lengths_device(gpu, orc):
         mi.kv_lengths(dm.ptr, is_f16, n_kv, rows, out.ptr)
         mi.device_sync()
         assert np.array_equal(out.download(np.int32), orc.kv_lengths(mk, is_f16=is_f16))
+
+
+@pytest.mark.parametrize("use_mask", [False, True])
+def test_fa_decode_batch_sequences(gpu, orc, use_mask):
+    """Independent sequences in one launch (grid z), each with its own cache region, length
+    and mask row; against the oracle run per sequence."""
+    mi = gpu
+    n_seq, L, nq, nkv, d = 3, 1100, 28, 4, 128
+    stride_rows = 1200                 # cache positions per sequence (> the view length L)
+    lens = [1100, 37, 700]
+    rng = np.random.default_rng(55 + use_mask)
+    q = rng.standard_normal((n_seq, nq, d)).astype(np.float32)
+    kc = f16_bits(rng.standard_normal((n_seq, stride_rows, nkv, d)))
+    vc = f16_bits(rng.standard_normal((n_seq, stride_rows, nkv, d)))
+    mask = np.zeros((n_seq, L), np.float32)
+    for s in range(n_seq):
+        mask[s, lens[s]:] = -np.inf
+    mask[0, 5] = -np.inf
+    m16 = f16_bits(mask)
+    dq, dk, dv = mi.to_device(q), mi.to_device(kc), mi.to_device(vc)
+    dm = mi.to_device(m16) if use_mask else None
+    dl = mi.to_device(np.array(lens, np.int32))
+    out = mi.DeviceBuffer(n_seq * nq * d * 4)
+    wsb = mi.fa_decode_batch_workspace_size(L, nq, nkv, d, n_seq)
+    ws = mi.DeviceBuffer(wsb).zero()
+    nb1 = nkv * d * 2
+    seq_bytes = stride_rows * nb1
+    mi.fa_decode_batch(dq.ptr, dk.ptr, dv.ptr, dm.ptr if dm else None, dl.ptr, L, nq, nkv, d, nb1, d * 2, nb1, d * 2,
+                       1 / np.sqrt(d), out.ptr, n_seq, nq * d, seq_bytes, seq_bytes, L, nq * d, ws.ptr, wsb)
+    mi.device_sync()
+    o = out.download(np.float32).reshape(n_seq, nq, d)
+    for s in range(n_seq):
+        _check_fa(orc, o[s], q[s], np.ascontiguousarray(kc[s, :L]), np.ascontiguousarray(vc[s, :L]), nkv,
+                  1 / np.sqrt(d), mask=m16[s] if use_mask else None, kv_len=lens[s], label=f"seq {s}")
