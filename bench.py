@@ -129,6 +129,95 @@ def cpu_baseline(qs, hp, tensors, smooth, model, token, pos, gpu_tokens, budget_
             "greedy_agreement": f"{agree}/{len(toks)}", "first_divergence": first_diff}
 
 
+def measure_fa(mi, hp, n_seq, n_kv, rng):
+    """flash-decoding at the model's attention shape over n_seq synthetic caches of n_kv
+    positions (fresh buffers rotated, HBM-cold): KV-read GB/s of split + combine"""
+    nq, nkv, d = hp["n_head"], hp["n_head_kv"], hp["head_dim"]
+    st = mi.Stream()
+    kv_bytes = n_seq * n_kv * nkv * d * 2
+    copies = max(2, int(np.ceil(2 * MALL_BYTES / (2 * kv_bytes))) + 1)
+    caches = []
+    for c in range(copies):
+        kb, vb = mi.DeviceBuffer(kv_bytes), mi.DeviceBuffer(kv_bytes)
+        for b, sd in ((kb, 2 * c), (vb, 2 * c + 1)):
+            mi._call("mi_fill_f16_uniform", mi._P(st.ptr), mi._P(b.ptr), n_seq * n_kv, nkv * d, nkv * d * 2,
+                     ctypes.c_uint64(sd), ctypes.c_float(1.0))
+        caches.append((kb, vb))
+    q = mi.to_device(rng.standard_normal((n_seq, nq, d)).astype(np.float32))
+    out = mi.DeviceBuffer(n_seq * nq * d * 4)
+    wsb = mi.fa_decode_batch_workspace_size(n_kv, nq, nkv, d, n_seq)
+    ws = mi.DeviceBuffer(wsb).zero(stream=st.ptr)
+    nb1 = nkv * d * 2
+    seq_b = n_kv * nb1
+    run = lambda kb, vb: mi.fa_decode_batch(q.ptr, kb.ptr, vb.ptr, None, None, n_kv, nq, nkv, d, nb1, d * 2, nb1,
+                                            d * 2, 1.0 / np.sqrt(d), out.ptr, n_seq, nq * d, seq_b, seq_b, 0, nq * d,
+                                            ws.ptr, wsb, stream=st.ptr)
+    for kb, vb in caches:
+        run(kb, vb)
+    st.sync()
+    e0, e1 = mi.Event(), mi.Event()
+    launches = 4 * copies
+    e0.record(st.ptr)
+    for i in range(launches):
+        run(*caches[i % copies])
+    e1.record(st.ptr)
+    st.sync()
+    us = e0.elapsed_ms(e1) * 1e3 / launches
+    algo = 2 * kv_bytes + 2 * n_seq * nq * d * 4
+    for kb, vb in caches:
+        kb.free()
+        vb.free()
+    st.destroy()
+    return {"kernel": "k_fa_mfma + k_fa_combine (flash-decoding, MFMA)", "n_seq": n_seq, "n_kv": n_kv,
+            "heads": f"{nq}q/{nkv}kv", "avg_us": round(us, 2), "algorithmic_bytes": algo,
+            "achieved": round(algo / us / 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(algo / us / 1e3 / HBM_PEAK_GBS, 4), "bound": "hbm"}
+
+
+def run_7b(args, mi, qs):
+    """Qwen2.5-7B-shaped W4A16 decode at a 32768-position context, bs = --batch sequences"""
+    S = args.batch
+    n_ctx = 32768
+    warm = max(args.warmup, 1)
+    hp = qs.qwen2_7b(n_ctx=n_ctx, n_seq=S)
+    tensors, _ = qs.synth(hp, seed=SEED)
+    model = mi.Qwen2Model(hp)
+    model.load(tensors)
+    weight_bytes = qs.weight_bytes(hp)
+    del tensors
+    n_fill = n_ctx - args.steps - warm
+    model.fill_cache(n_fill, seed=SEED, scale=1.0)
+    rng = np.random.default_rng(SEED + 2)
+    toks = rng.integers(0, hp["n_vocab"], S).astype(np.int32)
+    pos = np.full(S, n_fill, np.int32)
+    wt, _ = model.decode_steps_batch(toks, pos, warm)
+    toks, pos = wt[-1], pos + warm
+    mi.device_sync()
+    t0 = time.perf_counter()
+    out, _ = model.decode_steps_batch(toks, pos, args.steps)
+    mi.device_sync()
+    el = time.perf_counter() - t0
+    model.free()
+    kv_step = qs.kv_bytes_per_position(hp) * S * (int(pos[0]) + args.steps // 2)
+    step_bytes = weight_bytes + kv_step
+    fa = None if args.no_roofline else measure_fa(mi, hp, S, n_ctx, rng)
+    return {
+        "metric": f"decode tok/s, Qwen2.5-7B-shape W4A16 bs={S} at context 32768",
+        "value": round(S * args.steps / el, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": warm,
+        "ms_per_step": round(el * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "W4A16 (int4 g32 weights x fp16 activations, fp32 accumulate), fp16 KV and head",
+        "data": "synthetic (random weights of the named shape, random KV-cache contents of the named length)",
+        "config": {"workload": f"Qwen2.5-7B-shaped Q4_0 W4A16 whole-model greedy decode, {S} independent sequence(s), "
+                               "28 layers, hidden 3584, 28q/4kv heads x 128, FFN 18944, vocab 152064 tied fp16 head; "
+                               f"KV cache of {int(pos[0])} positions per sequence, then the timed tokens",
+                   "batch": S, "context": n_ctx, "bytes_per_step": step_bytes, "kv_bytes_per_step": kv_step,
+                   "step_GBps": round(step_bytes * args.steps / el / 1e9, 1),
+                   "kv_GBps_in_step": round(kv_step * args.steps / el / 1e9, 1),
+                   "step_roofline_frac": round(step_bytes * args.steps / el / 1e9 / HBM_PEAK_GBS, 4)},
+        "roofline": fa, "cpu_baseline": None,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -139,6 +228,9 @@ def main():
     ap.add_argument("--no-roofline", action="store_true", help="skip the standalone roofline leg")
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the roofline leg (short program for rocprofv3 counter passes)")
+    ap.add_argument("--workload", default="qwen2-1.5b-a8w8", choices=["qwen2-1.5b-a8w8", "qwen2-7b-w4a16"],
+                    help="qwen2-7b-w4a16: the 7B-shaped W4A16 decode at a 32K context (see --batch)")
+    ap.add_argument("--batch", type=int, default=1, help="independent sequences for qwen2-7b-w4a16 (1..8)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); how the decode path "
@@ -152,6 +244,10 @@ def main():
     if mi.device_count() < 1:
         print("bench.py: no HIP device: " + mi.last_error(), file=sys.stderr)
         sys.exit(1)
+
+    if args.workload == "qwen2-7b-w4a16":
+        print(json.dumps(run_7b(args, mi, qs)))
+        return
 
     warm = max(args.warmup, 0)
     hp = qs.qwen2_1p5b(n_ctx=PREFILL + warm + args.steps)
