@@ -14,26 +14,63 @@ namespace {
 
 using namespace mi;
 
-// one workgroup per row; y = x / sqrt(mean(x^2) + eps) [* w]
+// one workgroup per row; y = x / sqrt(mean(x^2) + eps) [* w].  Rows of up to 4096
+// floats are held in registers (4 float4 per thread, all loads issued before the
+// first add), the x*x terms summed in double as ggml does; longer rows loop.
 __global__ __launch_bounds__(256) void k_rms_norm(const float *__restrict__ x, const float *__restrict__ w,
                                                   float *__restrict__ y, int ne0, float eps) {
     const int row = blockIdx.x;
     const float *xr = x + (size_t)row * ne0;
     float *yr = y + (size_t)row * ne0;
+    const int tid = threadIdx.x;
+    __shared__ double s_red[4];
     double s = 0.0;
-    for (int i = threadIdx.x; i < ne0; i += 256) s += (double)__fmul_rn(xr[i], xr[i]);
-    __shared__ double sh[256];
-    sh[threadIdx.x] = s;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if ((int)threadIdx.x < o) sh[threadIdx.x] += sh[threadIdx.x + o];
-        __syncthreads();
+    const bool vec = (ne0 % 4) == 0 && ne0 <= 4096 && (((uintptr_t)xr | (uintptr_t)yr | (uintptr_t)w) & 15) == 0;
+    float4 xv[4], wv[4];
+    if (vec) {
+        const int n4 = ne0 / 4;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int f = min(tid + t * 256, n4 - 1);
+            xv[t] = ((const float4 *)xr)[f];
+            if (w) wv[t] = ((const float4 *)w)[f];
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            if (tid + t * 256 < n4) {
+                s += (double)__fmul_rn(xv[t].x, xv[t].x);
+                s += (double)__fmul_rn(xv[t].y, xv[t].y);
+                s += (double)__fmul_rn(xv[t].z, xv[t].z);
+                s += (double)__fmul_rn(xv[t].w, xv[t].w);
+            }
+        }
+    } else {
+        for (int i = tid; i < ne0; i += 256) s += (double)__fmul_rn(xr[i], xr[i]);
     }
-    const float mean = (float)(sh[0] / ne0);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    if ((tid & 63) == 0) s_red[tid >> 6] = s;
+    __syncthreads();
+    const double tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    const float mean = (float)(tot / ne0);
     const float scale = 1.0f / sqrtf(mean + eps);
-    for (int i = threadIdx.x; i < ne0; i += 256) {
-        const float v = xr[i] * scale;
-        yr[i] = w ? v * w[i] : v;
+    if (vec) {
+        const int n4 = ne0 / 4;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int f = tid + t * 256;
+            if (f < n4) {
+                float4 v = xv[t];
+                v.x = v.x * scale; v.y = v.y * scale; v.z = v.z * scale; v.w = v.w * scale;
+                if (w) { v.x *= wv[t].x; v.y *= wv[t].y; v.z *= wv[t].z; v.w *= wv[t].w; }
+                ((float4 *)yr)[f] = v;
+            }
+        }
+    } else {
+        for (int i = tid; i < ne0; i += 256) {
+            const float v = xr[i] * scale;
+            yr[i] = w ? v * w[i] : v;
+        }
     }
 }
 

@@ -218,6 +218,117 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_gx(const uint8_t *__restrict_
     }
 }
 
+// Several activation rows (2..16: a batch of sequences) on the matrix cores:
+// v_mfma_f32_16x16x16_f16 with A = 16 weight rows x 16 k and B = 16 k x the
+// activation rows (columns past m are zero).  Lane (g, c) of a wave loads one dword
+// of block b of weight row c: bytes 4g..4g+3 hold elements 4g..4g+3 (low nibbles,
+// the first k-step) and 16+4g..16+4g+3 (high nibbles, the second), turned into exact
+// fp16 (nib - 8).  The two MFMAs give the block's exact-product fp32 partial for 16
+// rows x 16 columns; it is scaled by the block scale of its row and accumulated.  The
+// C layout puts rows 4g..4g+3 and column c in lane (g, c).  KS waves of a workgroup
+// split k (partials reduced through LDS); with KS = 1 each wave owns 16 rows.
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ half4_t q4_nibbles(uint32_t v, int hi) {
+    const uint32_t s = hi ? v >> 4 : v;
+    const uint32_t p01 = 0x64006400u | (s & 0xfu) | ((s & 0xf00u) << 8);
+    const uint32_t p23 = 0x64006400u | ((s >> 16) & 0xfu) | ((s >> 8) & 0xf0000u);
+    const half2_t off = {(half_t)1032.0f, (half_t)1032.0f};
+    const half2_t a = u2h2(p01) - off, b = u2h2(p23) - off;
+    return half4_t{a.x, a.y, b.x, b.y};
+}
+
+template <int U>
+struct Q4MStage {
+    uint32_t w[U];
+    uint32_t d[U][4];  // fp16 scales of the lane's 4 output rows
+    half4_t x0[U], x1[U];
+};
+
+template <int KS, int U, bool XF32>
+__global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma(const uint8_t *__restrict__ qs,
+                                                             const uint16_t *__restrict__ wd,
+                                                             const void *__restrict__ xin, float *__restrict__ y,
+                                                             const float *__restrict__ add, int n, int nb, int m) {
+    __shared__ float s_acc[KS][64][4];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int row0 = blockIdx.x * 16;
+    const int k = nb * QK;
+    const int per = (nb + KS - 1) / KS;  // k range of this wave, in blocks
+    const int b_lo = wave * per, b_hi = min(nb, b_lo + per);
+    const size_t arow = (size_t)min(row0 + c, n - 1) * nb;
+    size_t drow[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) drow[i] = (size_t)min(row0 + 4 * g + i, n - 1) * nb;
+    const bool col_ok = c < m;
+    const size_t xoff = (size_t)min(c, m - 1) * k + 4 * g;
+
+    auto load = [&](Q4MStage<U> &st, int b0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int b = min(b0 + u, b_hi - 1);
+            st.w[u] = *(const uint32_t *)(qs + (arow + b) * 16 + 4 * g);
+#pragma unroll
+            for (int i = 0; i < 4; i++) st.d[u][i] = wd[drow[i] + b];
+            if constexpr (XF32) {
+                // fp32 activation rounded to fp16 (RNE) as ggml converts src1
+                const float *xr = (const float *)xin + xoff + (size_t)b * QK;
+                const float4 a0 = *(const float4 *)xr, a1 = *(const float4 *)(xr + 16);
+                st.x0[u] = half4_t{(half_t)a0.x, (half_t)a0.y, (half_t)a0.z, (half_t)a0.w};
+                st.x1[u] = half4_t{(half_t)a1.x, (half_t)a1.y, (half_t)a1.z, (half_t)a1.w};
+            } else {
+                const uint16_t *xr = (const uint16_t *)xin + xoff + (size_t)b * QK;
+                st.x0[u] = __builtin_bit_cast(half4_t, *(const uint2 *)xr);
+                st.x1[u] = __builtin_bit_cast(half4_t, *(const uint2 *)(xr + 16));
+            }
+        }
+    };
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const Q4MStage<U> &st, int b0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (b0 + u < b_hi) {
+                float4_t t = {0.f, 0.f, 0.f, 0.f};
+                const half4_t z = {0, 0, 0, 0};
+                t = __builtin_amdgcn_mfma_f32_16x16x16f16(q4_nibbles(st.w[u], 0), col_ok ? st.x0[u] : z, t, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x16f16(q4_nibbles(st.w[u], 1), col_ok ? st.x1[u] : z, t, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[i] = fmaf(h2f((uint16_t)st.d[u][i]), t[i], acc[i]);
+            }
+        }
+    };
+    if (b_lo < b_hi) {
+        // two register stages: the next U blocks are in flight while the current ones compute
+        Q4MStage<U> sa, sb;
+        load(sa, b_lo);
+        for (int b0 = b_lo; b0 < b_hi; b0 += 2 * U) {
+            if (b0 + U < b_hi) load(sb, b0 + U);
+            compute(sa, b0);
+            if (b0 + U >= b_hi) break;
+            if (b0 + 2 * U < b_hi) load(sa, b0 + 2 * U);
+            compute(sb, b0 + U);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) s_acc[wave][lane][i] = acc[i];
+    __syncthreads();
+    if (wave != 0 || !col_ok) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < KS; w++) v += s_acc[w][lane][i];
+        const int row = row0 + 4 * g + i;
+        if (row < n) {
+            const size_t o = (size_t)c * n + row;
+            y[o] = add ? v + add[o] : v;
+        }
+    }
+}
+
 // fp32 -> fp16 (round to nearest even, as ggml's activation conversion)
 __global__ __launch_bounds__(256) void k_cast_f16(const float *__restrict__ x, uint16_t *__restrict__ y, int64_t n4) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -272,7 +383,7 @@ int launch_lds(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_
     if (m == 2) return launch_lds_m<2>(st, base, n, k, m, x32, y);
     if (m >= 3 && m <= 4) return launch_lds_m<4>(st, base, n, k, m, x32, y);
     if (m >= 5 && m <= 8) return launch_lds_m<8>(st, base, n, k, m, x32, y);
-    set_error("gemv_q4_0: m=%lld not in 1..8", (long long)m);
+    set_error("gemv_q4_0: m=%lld not in 1..16", (long long)m);
     return MI_ERR_ARG;
 }
 
@@ -300,15 +411,33 @@ int launch_gx_mr(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int6
     return MI_ERR_ARG;
 }
 
+// one 16-row tile per workgroup, k split over 4 (short rows) or 8 waves
+template <bool XF32>
+int launch_mfma(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const void *x, float *y,
+                const float *add) {
+    const Q4Planes p = q4_planes(n, k);
+    const int nb = (int)(k / QK);
+    const unsigned tiles = (unsigned)((n + 15) / 16);
+    if (nb <= 128)
+        hipLaunchKernelGGL((k_gemv_q4_0_mfma<4, 8, XF32>), dim3(tiles), dim3(256), 0, st, base,
+                           (const uint16_t *)(base + p.plane), x, y, add, (int)n, nb, (int)m);
+    else
+        hipLaunchKernelGGL((k_gemv_q4_0_mfma<8, 8, XF32>), dim3(tiles), dim3(512), 0, st, base,
+                           (const uint16_t *)(base + p.plane), x, y, add, (int)n, nb, (int)m);
+    MI_CHECK_LAUNCH("k_gemv_q4_0_mfma");
+    return MI_OK;
+}
+
 int launch_gx(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16, float *y,
               const float *add = nullptr) {
+    if (m >= 2 && m <= 16) return launch_mfma<false>(st, base, n, k, m, x16, y, add);
     const bool tall = n >= 2048;
     if (m == 1) return tall ? launch_gx_mr<1, 2>(st, base, n, k, m, x16, y, add)
                             : launch_gx_mr<1, 1>(st, base, n, k, m, x16, y, add);
     if (m == 2) return launch_gx_mr<2, 1>(st, base, n, k, m, x16, y, add);
     if (m >= 3 && m <= 4) return launch_gx_mr<4, 1>(st, base, n, k, m, x16, y, add);
     if (m >= 5 && m <= 8) return launch_gx_mr<8, 1>(st, base, n, k, m, x16, y, add);
-    set_error("gemv_q4_0: m=%lld not in 1..8", (long long)m);
+    set_error("gemv_q4_0: m=%lld not in 1..16", (long long)m);
     return MI_ERR_ARG;
 }
 
@@ -382,7 +511,7 @@ int mi_gemv_q4_0_f16_add(void *stream, const void *w_packed, const uint16_t *x_f
 }
 
 size_t mi_mul_mat_q4_0_workspace_size(int64_t m, int64_t k) {
-    if (m * k * 2 <= 64 * 1024) return 0;
+    if (m > 1 || k * 2 <= 64 * 1024) return 0;  // matrix cores read fp32 rows directly
     return mi::align_up((size_t)m * k * 2, 256);
 }
 
@@ -390,9 +519,10 @@ int mi_mul_mat_q4_0_f32(void *stream, const void *w_packed, const float *x, floa
                         int64_t m, void *ws, size_t ws_bytes) {
     if (int r = check_shape("mul_mat_q4_0_f32", n, k)) return r;
     MI_CHECK_ARG(w_packed && x && y, "mul_mat_q4_0_f32: null pointer");
-    MI_CHECK_ARG(m >= 1 && m <= 8, "mul_mat_q4_0_f32: m=%lld not in 1..8", (long long)m);
+    MI_CHECK_ARG(m >= 1 && m <= 16, "mul_mat_q4_0_f32: m=%lld not in 1..16", (long long)m);
     MI_CHECK_ARG(mi::aligned(w_packed, 256) && mi::aligned(x, 16), "mul_mat_q4_0_f32: w_packed must be 256-byte, x 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
+    if (m > 1) return launch_mfma<true>(st, (const uint8_t *)w_packed, n, k, m, x, y, nullptr);
     const size_t need = mi_mul_mat_q4_0_workspace_size(m, k);
     if (need == 0) return launch_lds(st, (const uint8_t *)w_packed, n, k, m, x, y);
     if (!ws || ws_bytes < need || !mi::aligned(ws, 16)) {

@@ -153,7 +153,8 @@ def test_q8_0_gemv_shapes(gpu, orc, n, k, m):
 # ---------------------------------------------------------------- W4A16
 
 @pytest.mark.parametrize("n,k,m", [(1536, 8960, 1), (8960, 1536, 1), (7, 32, 1), (512, 3584, 8), (100, 18944, 1),
-                                   (4608, 3584, 1), (2049, 256, 1), (300, 18944, 8), (3584, 4096, 5)])
+                                   (4608, 3584, 1), (2049, 256, 1), (300, 18944, 8), (3584, 4096, 5),
+                                   (1030, 3584, 16), (77, 160, 2)])
 def test_w4a16_gemv(gpu, orc, n, k, m):
     """fp16 activations from global memory (one or two rows per lane group) and the fp32
     MUL_MAT path (fp16 staging in LDS, or through a workspace when m*k*2 > 64 KB)"""
