@@ -166,6 +166,27 @@ int mi_gemv_q4_0_f16(void *stream, const void *w_packed, const uint16_t *x_f16, 
 /* the same with the ADD of a same-shape vector (residual) fused: y = W*x + add */
 int mi_gemv_q4_0_f16_add(void *stream, const void *w_packed, const uint16_t *x_f16, const float *add, float *y,
                          int64_t n, int64_t k, int64_t m);
+/* W4A16 decode chains, one activation row (m = 1, k <= 4096; without the norm the
+ * first one takes k <= 32512), the counterparts of the
+ * Q8_0 chains above (node sequences of the Qwen2 graph builder, per-node dispatch
+ * patch:1897-1930 in the reference):
+ * [RMS_NORM -> MUL(norm_w)] -> n_mats MUL_MATs sharing src1 (stacked rows) -> ADD add[i]
+ * (residual or bias, or NULL) */
+int mi_mul_mat_q4_0_f32_fused(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
+                              float *const *y, const float *const *add, int64_t k, const float *x,
+                              const float *norm_w, float eps);
+/* [RMS_NORM -> MUL(norm_w)] -> gate and up MUL_MATs (n rows each) -> GLU swiglu
+ * (silu(gate) * up) -> fp16 h_out[n] (RNE, the conversion the down projection's MUL_MAT
+ * applies to its src1) */
+int mi_gate_up_swiglu_q4_0(void *stream, const void *w_gate, const void *w_up, int64_t n, int64_t k, const float *x,
+                           const float *norm_w, float eps, uint16_t *h_out);
+/* the attention-input chain of mi_qkv_rope_kv_q8_0 with Q4_0 weights (head_dim <= 128,
+ * n[2] even) */
+int mi_qkv_rope_kv_q4_0(void *stream, const void *const *w_packed, const int64_t *n, const float *const *bias,
+                        int64_t k, const float *x, const float *norm_w, float eps, int64_t head_dim,
+                        const int32_t *pos, float freq_base, float freq_scale, float attn_factor, float *q_out,
+                        void *k_cache, size_t k_row_bytes, void *v_cache, size_t v_row_bytes, const void *kv_idx,
+                        int kv_idx_is_i64, int64_t n_cache_rows);
 /* the MUL_MAT of the ggml graph (src1 fp32): the activation is converted to fp16 (RNE, as
  * ggml converts src1) into LDS when m*k*2 <= 64 KB (no workspace), otherwise into ws of
  * mi_mul_mat_q4_0_workspace_size(m, k) bytes */

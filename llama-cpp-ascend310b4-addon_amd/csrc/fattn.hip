@@ -212,7 +212,7 @@ __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, c
                 dsum = fdot2(qh[h][3], (uint32_t)kr[t].w, dsum);
                 dsum = group_sum<LPR>(dsum);
                 // ggml order: s = (q.k)*scale; s += mask; kept in log2 units for v_exp_f32
-                const float sc = __fadd_rn(__fmul_rn(dsum, scale), mk[t]) * kLog2e;
+                const float sc = mul_add_rn(dsum, scale, mk[t]) * kLog2e;
                 s[h][t] = val[t] ? sc : -INFINITY;
             }
         }
@@ -486,7 +486,7 @@ __global__ __launch_bounds__(256) void k_fa_mfma(const float *__restrict__ q, co
         for (int r = 0; r < 4; r++) {
             const bool ok = c < GQ && p0 + 4 * g + r < end_eff;
             // ggml order: s = (q.k)*scale; s += mask; kept in log2 units for v_exp_f32
-            const float v = __fadd_rn(__fmul_rn(sacc[r], scale), mk[r]) * kLog2e;
+            const float v = mul_add_rn(sacc[r], scale, mk[r]) * kLog2e;
             sc[r] = ok ? v : -INFINITY;
         }
         float bm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));

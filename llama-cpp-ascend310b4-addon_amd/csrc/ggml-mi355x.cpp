@@ -438,6 +438,7 @@ size_t scratch_need(const ggml_tensor *node) {
     if (node->op == GGML_OP_MUL_MAT && node->src[0]->type == GGML_TYPE_Q4_0)
         return mi_mul_mat_q4_0_workspace_size(node->src[1]->ne[1], node->src[1]->ne[0]);
     if (node->op == GGML_OP_ARGMAX) return mi_argmax_workspace_size(node->src[0]->ne[0], ggml_nrows(node->src[0]));
+    if (node->op == GGML_OP_GLU && ggml_nrows(node) == 1) return (size_t)ggml_nelements(node) * 2;  // fp16 row
     return 0;
 }
 
@@ -589,17 +590,34 @@ int next_real(ggml_cgraph *g, int i) {
     return i;
 }
 
+// byte ranges of a and b intersect (ggml's allocator may place a node's output in the
+// memory of an input whose last consumer ran before it: a fused launch that still reads
+// that input from other workgroups while writing the output must not run then)
+bool overlaps(const ggml_tensor *a, const ggml_tensor *b) {
+    const uintptr_t a0 = (uintptr_t)a->data, a1 = a0 + ggml_nbytes(a);
+    const uintptr_t b0 = (uintptr_t)b->data, b1 = b0 + ggml_nbytes(b);
+    return a0 < b1 && b0 < a1;
+}
+
 bool is_row_vector(const ggml_tensor *t, int64_t n) {
     return t && is_f32_contig(t) && ggml_nelements(t) == n && aligned16(t->data);
 }
 
-// a Q8_0 MUL_MAT on one activation row with the prepacked side copy ready
-bool q8_gemv_node(const ggml_tensor *n) {
+// a Q8_0 or Q4_0 MUL_MAT (type t) on one activation row with the prepacked side copy ready
+bool gemv_node(const ggml_tensor *n, ggml_type t) {
     if (n->op != GGML_OP_MUL_MAT) return false;
     const ggml_tensor *a = n->src[0], *b = n->src[1];
     const TensorExtra *ex = (const TensorExtra *)a->extra;
-    return a->type == GGML_TYPE_Q8_0 && ex && ex->ready && b->type == GGML_TYPE_F32 && ggml_nrows(b) == 1 &&
+    return a->type == t && ex && ex->ready && b->type == GGML_TYPE_F32 && ggml_nrows(b) == 1 &&
            ggml_is_contiguous(b) && aligned16(b->data) && is_f32_contig(n);
+}
+bool q8_gemv_node(const ggml_tensor *n) { return gemv_node(n, GGML_TYPE_Q8_0); }
+
+// the weight format of a fusable one-row MUL_MAT, or GGML_TYPE_COUNT
+ggml_type gemv_type(const ggml_tensor *n) {
+    if (gemv_node(n, GGML_TYPE_Q8_0)) return GGML_TYPE_Q8_0;
+    if (gemv_node(n, GGML_TYPE_Q4_0)) return GGML_TYPE_Q4_0;
+    return GGML_TYPE_COUNT;
 }
 
 bool rms_mul_head(ggml_cgraph *g, int i, const Consumers &C, int &j, const ggml_tensor *&x, const ggml_tensor *&nw,
@@ -625,11 +643,14 @@ int try_fuse_attn_in(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C)
     float eps;
     if (!rms_mul_head(g, i, C, j, x, nw, mul, eps)) return 0;
     const ggml_tensor *mm[3], *out[3], *bias[3] = {nullptr, nullptr, nullptr};
+    ggml_type wt = GGML_TYPE_COUNT;
     for (int t = 0; t < 3; t++) {
         j = next_real(g, j + 1);
         if (j >= nn) return 0;
         mm[t] = ggml_graph_node(g, j);
-        if (!q8_gemv_node(mm[t]) || mm[t]->src[1] != mul || inv_s_of(mm[t]->src[0]) != inv_s_of(mm[0]->src[0]))
+        if (t == 0) wt = gemv_type(mm[0]);
+        if (wt == GGML_TYPE_COUNT || !gemv_node(mm[t], wt) || mm[t]->src[1] != mul ||
+            inv_s_of(mm[t]->src[0]) != inv_s_of(mm[0]->src[0]))
             return 0;
         out[t] = mm[t];
     }
@@ -664,6 +685,7 @@ int try_fuse_attn_in(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C)
         memcmp(r->op_params + 5, rope[1]->op_params + 5, 4 * sizeof(int32_t)) != 0 ||
         mm[0]->ne[0] % hd || mm[1]->ne[0] % hd || !is_f32_contig(rope[0]))
         return 0;
+    if (wt == GGML_TYPE_Q4_0 && (hd > 128 || mm[2]->ne[0] % 2)) return 0;
     for (int t = 0; t < 2; t++) {
         j = next_real(g, j + 1);
         if (j >= nn) return 0;
@@ -675,6 +697,7 @@ int try_fuse_attn_in(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C)
             return 0;
     }
     if (!only_consumed_by(C, rope[1], {sr[0]}) || !only_consumed_by(C, out[2], {sr[1]})) return 0;
+    if (overlaps(rope[0], x) || overlaps(rope[0], nw)) return 0;
 
     const void *w[3];
     int64_t n[3];
@@ -689,12 +712,53 @@ int try_fuse_attn_in(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C)
     memcpy(&freq_scale, (const float *)r->op_params + 6, sizeof(float));
     memcpy(&attn_factor, (const float *)r->op_params + 8, sizeof(float));
     const ggml_tensor *idx = sr[0]->src[1];
+    if (wt == GGML_TYPE_Q4_0) {
+        MI_K_CHECK(mi_qkv_rope_kv_q4_0(ctx->stream, w, n, bp, x->ne[0], (const float *)x->data, (const float *)nw->data,
+                                       eps, hd, (const int32_t *)r->src[1]->data, freq_base, freq_scale, attn_factor,
+                                       (float *)rope[0]->data, sr[0]->data, sr[0]->nb[1], sr[1]->data, sr[1]->nb[1],
+                                       idx->data, idx->type == GGML_TYPE_I64, std::min(sr[0]->ne[1], sr[1]->ne[1])));
+        return j + 1 - i;
+    }
     MI_K_CHECK(mi_qkv_rope_kv_q8_0(ctx->stream, w, n, bp, x->ne[0], (const float *)x->data, (const float *)nw->data, eps,
                                    inv_s_of(mm[0]->src[0]), q8_rounding(), hd, (const int32_t *)r->src[1]->data,
                                    freq_base, freq_scale, attn_factor, (float *)rope[0]->data, sr[0]->data,
                                    sr[0]->nb[1], sr[1]->data, sr[1]->nb[1], idx->data, idx->type == GGML_TYPE_I64,
                                    std::min(sr[0]->ne[1], sr[1]->ne[1])));
     return j + 1 - i;
+}
+
+const ggml_tensor *matmul_add_tail(ggml_cgraph *g, int j, const ggml_tensor *mm, const Consumers &C,
+                                   const ggml_tensor *&vec);
+
+// W4A16 FFN: [norm] -> gate, up (mm[0], mm[1], nodes up to index last) -> GLU swiglu ->
+// down MUL_MAT [-> ADD residual]: the GLU output goes to scratch as fp16 (the conversion
+// the down projection's MUL_MAT applies to its src1), so the chain is two launches.
+int try_fuse_gate_up_down_q4(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C, int last,
+                             const ggml_tensor *const *mm, const ggml_tensor *x, const ggml_tensor *nw, float eps) {
+    const int nn = ggml_graph_n_nodes(g);
+    const int jg = next_real(g, last + 1);
+    if (jg >= nn) return 0;
+    const ggml_tensor *glu = ggml_graph_node(g, jg);
+    if (glu->op != GGML_OP_GLU || !supports_op_impl(glu) || glu->src[0] != mm[0] || glu->src[1] != mm[1] ||
+        mm[0]->ne[0] != mm[1]->ne[0] || !only_consumed_by(C, mm[0], {glu}) || !only_consumed_by(C, mm[1], {glu}))
+        return 0;
+    const int jd = next_real(g, jg + 1);
+    if (jd >= nn) return 0;
+    const ggml_tensor *down = ggml_graph_node(g, jd);
+    const int64_t nf = mm[0]->ne[0];
+    if (!gemv_node(down, GGML_TYPE_Q4_0) || down->src[1] != glu || !only_consumed_by(C, glu, {down}) ||
+        down->src[0]->ne[0] != nf || nf / 32 > 1016 || ctx->scratch_size < (size_t)nf * 2)
+        return 0;
+    const ggml_tensor *vec = nullptr;
+    const ggml_tensor *ad = matmul_add_tail(g, jd, down, C, vec);
+    uint16_t *h = (uint16_t *)ctx->scratch;
+    MI_K_CHECK(mi_gate_up_swiglu_q4_0(ctx->stream, ((const TensorExtra *)mm[0]->src[0]->extra)->packed,
+                                      ((const TensorExtra *)mm[1]->src[0]->extra)->packed, nf, x->ne[0],
+                                      (const float *)x->data, nw ? (const float *)nw->data : nullptr, eps, h));
+    MI_K_CHECK(mi_gemv_q4_0_f16_add(ctx->stream, ((const TensorExtra *)down->src[0]->extra)->packed, h,
+                                    ad ? (const float *)vec->data : nullptr, (float *)(ad ? ad->data : down->data),
+                                    down->src[0]->ne[1], nf, 1));
+    return (ad ? next_real(g, jd + 1) : jd) + 1 - i;
 }
 
 int try_fuse_norm_matmuls(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
@@ -705,14 +769,19 @@ int try_fuse_norm_matmuls(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumer
     if (!rms_mul_head(g, i, C, j, x, nw, mul, eps)) return 0;
     const ggml_tensor *mm[4] = {nullptr, nullptr, nullptr, nullptr};
     int cnt = 0, last = j;
+    ggml_type wt = GGML_TYPE_COUNT;
     for (int jj = next_real(g, j + 1); jj < nn && cnt < 4; jj = next_real(g, jj + 1)) {
         const ggml_tensor *nd = ggml_graph_node(g, jj);
-        if (!q8_gemv_node(nd) || nd->src[1] != mul || inv_s_of(nd->src[0]) != inv_s_of(mm[0] ? mm[0]->src[0] : nd->src[0]))
+        if (cnt == 0) wt = gemv_type(nd);
+        if (wt == GGML_TYPE_COUNT || !gemv_node(nd, wt) || nd->src[1] != mul ||
+            inv_s_of(nd->src[0]) != inv_s_of(mm[0] ? mm[0]->src[0] : nd->src[0]))
             break;
         mm[cnt++] = nd;
         last = jj;
     }
     if (cnt == 0) return 0;
+    for (int t = 0; t < cnt; t++)
+        if (overlaps(mm[t], x) || overlaps(mm[t], nw)) return 0;
     std::vector<const ggml_tensor *> cons;
     real_consumers(C, mul, cons);
     for (const ggml_tensor *c : cons) {
@@ -727,6 +796,14 @@ int try_fuse_norm_matmuls(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumer
         w[t] = ((const TensorExtra *)mm[t]->src[0]->extra)->packed;
         n[t] = mm[t]->src[0]->ne[1];
         y[t] = (float *)mm[t]->data;
+    }
+    if (wt == GGML_TYPE_Q4_0) {
+        if (cnt == 2) {
+            if (int used = try_fuse_gate_up_down_q4(ctx, g, i, C, last, mm, x, nw, eps)) return used;
+        }
+        MI_K_CHECK(mi_mul_mat_q4_0_f32_fused(ctx->stream, cnt, w, n, y, nullptr, x->ne[0], (const float *)x->data,
+                                             (const float *)nw->data, eps));
+        return last + 1 - i;
     }
     MI_K_CHECK(mi_mul_mat_q8_0_f32_fused(ctx->stream, cnt, w, n, y, nullptr, x->ne[0], (const float *)x->data,
                                          (const float *)nw->data, eps, inv_s_of(mm[0]->src[0]), q8_rounding()));
@@ -749,17 +826,24 @@ const ggml_tensor *matmul_add_tail(ggml_cgraph *g, int j, const ggml_tensor *mm,
 
 int try_fuse_matmul_add(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
     const ggml_tensor *mm = ggml_graph_node(g, i);
-    if (!q8_gemv_node(mm)) return 0;
+    const ggml_type wt = gemv_type(mm);
+    if (wt == GGML_TYPE_COUNT) return 0;
+    const int64_t k = mm->src[0]->ne[0];
+    if (wt == GGML_TYPE_Q4_0 && k / 32 > 1016) return 0;
     const ggml_tensor *vec = nullptr;
     const ggml_tensor *ad = matmul_add_tail(g, i, mm, C, vec);
     if (!ad) return 0;
-    const int64_t k = mm->src[0]->ne[0];
+    // one launch reads the whole activation in every workgroup and writes the sum
+    if ((wt == GGML_TYPE_Q4_0 || k <= 4096) && overlaps(ad, mm->src[1])) return 0;
     const TensorExtra *ex = (const TensorExtra *)mm->src[0]->extra;
     const void *w = ex->packed;
     const int64_t n = mm->src[0]->ne[1];
     float *y = (float *)ad->data;
     const float *add = (const float *)vec->data;
-    if (k <= 4096) {
+    if (wt == GGML_TYPE_Q4_0) {
+        MI_K_CHECK(mi_mul_mat_q4_0_f32_fused(ctx->stream, 1, &w, &n, &y, &add, k, (const float *)mm->src[1]->data,
+                                             nullptr, 0.0f));
+    } else if (k <= 4096) {
         MI_K_CHECK(mi_mul_mat_q8_0_f32_fused(ctx->stream, 1, &w, &n, &y, &add, k, (const float *)mm->src[1]->data,
                                              nullptr, 0.0f, ex->inv_s, q8_rounding()));
     } else {

@@ -38,14 +38,14 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float *__restrict__ x, c
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             if (tid + t * 256 < n4) {
-                s += (double)__fmul_rn(xv[t].x, xv[t].x);
-                s += (double)__fmul_rn(xv[t].y, xv[t].y);
-                s += (double)__fmul_rn(xv[t].z, xv[t].z);
-                s += (double)__fmul_rn(xv[t].w, xv[t].w);
+                s += (double)sq_rn(xv[t].x);
+                s += (double)sq_rn(xv[t].y);
+                s += (double)sq_rn(xv[t].z);
+                s += (double)sq_rn(xv[t].w);
             }
         }
     } else {
-        for (int i = tid; i < ne0; i += 256) s += (double)__fmul_rn(xr[i], xr[i]);
+        for (int i = tid; i < ne0; i += 256) s += (double)sq_rn(xr[i]);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
@@ -102,8 +102,8 @@ __global__ void k_rope_neox(const float *__restrict__ x, float *__restrict__ y, 
         const float s = sinf(th) * attn_factor;
         const float x0 = ((const float *)xr)[i];
         const float x1 = ((const float *)xr)[i + half];
-        ((float *)yr)[i] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));  // unfused, as the CPU loop
-        ((float *)yr)[i + half] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+        ((float *)yr)[i] = mul_sub_mul_rn(x0, c, x1, s);  // unfused, as the CPU loop
+        ((float *)yr)[i + half] = mul_add_mul_rn(x0, s, x1, c);
     }
     for (int j = n_dims + i; j < ne0; j += blockDim.x) ((float *)yr)[j] = ((const float *)xr)[j];
 }

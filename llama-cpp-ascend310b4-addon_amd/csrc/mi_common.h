@@ -41,7 +41,12 @@ __device__ __forceinline__ float h2f(uint16_t h) {
     return (float)v;
 }
 
-__device__ __forceinline__ uint16_t f2h(float f) {  // round to nearest even (hardware default mode)
+// fp32 -> fp16, round to nearest even, from the already rounded fp32 value: the empty asm
+// keeps the compiler from folding the producing multiply or add into a mixed-precision
+// v_fma_mixlo_f16 (one rounding straight to fp16, which differs from the fp32-then-fp16
+// rounding of ggml's fp32 tensors converted to fp16 in rare double-rounding cases)
+__device__ __forceinline__ uint16_t f2h(float f) {
+    asm volatile("" : "+v"(f));
     half_t v = (half_t)f;
     return __builtin_bit_cast(uint16_t, v);
 }
@@ -52,6 +57,28 @@ __device__ __forceinline__ uint32_t h22u(half2_t h) { return __builtin_bit_cast(
 // fp32 += a.x*b.x + a.y*b.y with exact fp16 products (v_dot2_f32_f16)
 __device__ __forceinline__ float fdot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(u2h2(a), u2h2(b), c, false);
+}
+
+// Products rounded before the add or subtract, as C built with -ffp-contract=off computes
+// them (HIP contracts a*b+c into an FMA by default, and its __fmul_rn / __fadd_rn are
+// plain operators that do not prevent it).
+__device__ __forceinline__ float mul_add_rn(float a, float b, float c) {
+#pragma clang fp contract(off)
+    return a * b + c;
+}
+__device__ __forceinline__ float mul_sub_mul_rn(float a, float b, float c, float d) {  // a*b - c*d
+#pragma clang fp contract(off)
+    return a * b - c * d;
+}
+__device__ __forceinline__ float mul_add_mul_rn(float a, float b, float c, float d) {  // a*b + c*d
+#pragma clang fp contract(off)
+    return a * b + c * d;
+}
+// x*x rounded to float, for sums (double)(x*x) as ggml's rms_norm forms them (a contracted
+// fpext(x*x) + sum would square in double)
+__device__ __forceinline__ float sq_rn(float a) {
+#pragma clang fp contract(off)
+    return a * a;
 }
 
 // DPP move helpers (row = 16 lanes)

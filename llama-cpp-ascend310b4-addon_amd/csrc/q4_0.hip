@@ -8,8 +8,16 @@
 // (experiments/w4a16-gemv/source/w4a16_gemv_qwen.cpp:127-148).
 // Replaces the add-on's add_custom W4A16 operator (same file, :24-180).
 #include "mi_common.h"
+#include "decode_common.h"
 
+#include <limits.h>
+#include <math.h>
+#include <stdlib.h>
 #include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <unordered_map>
 
 namespace {
 
@@ -338,6 +346,403 @@ __global__ __launch_bounds__(256) void k_cast_f16(const float *__restrict__ x, u
                                  (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16));
 }
 
+// ---------------------------------------------------------------- one activation row
+// The activation row lives in registers and weight rows stream past it.  Lane l of a
+// wave owns the blocks l + 64*(ks + WPR*i), i < KB, of every row (WPR waves split k,
+// ks = the wave's slice), so its activation blocks are loaded once per workgroup (from
+// an fp16 copy of the row staged in LDS) and each row costs the lane only its weight
+// loads: 16 nibble bytes and one fp16 scale per block.  The unit of work is a pair of
+// rows; the next pair's weights are in flight while the current pair is reduced, and
+// the grid is sized to what the GPU holds at once (each pair group walks the units
+// with a grid stride).
+//
+// The activation pairs are kept in the order in which four nibble pairs come out of a
+// weight dword with one shift and one AND-OR each (dword t holds elements 4t+b in the
+// low and 16+4t+b in the high nibble of byte b):
+//   xs[4t+0] = (x[4t],    x[4t+2])     <- (v      ) & 0x000f000f
+//   xs[4t+1] = (x[4t+1],  x[4t+3])     <- (v >>  8) & 0x000f000f
+//   xs[4t+2] = (x[16+4t], x[16+4t+2])  <- (v >>  4) & 0x000f000f
+//   xs[4t+3] = (x[17+4t], x[19+4t])    <- (v >> 12) & 0x000f000f
+// OR 0x6400 makes each nibble the exact fp16 1024 + nib; subtracting 1032 gives nib - 8.
+// magic: 0x64006400 held in a VGPR by the caller, so that each AND-OR is one
+// v_and_or_b32 (gfx9 VOP3 takes no literal and one scalar operand)
+__device__ __forceinline__ float q4_dot_xr(const int4 q, const uint32_t *xs, uint32_t magic) {
+    const half2_t off = {(half_t)1032.0f, (half_t)1032.0f};
+    const uint32_t qq[4] = {(uint32_t)q.x, (uint32_t)q.y, (uint32_t)q.z, (uint32_t)q.w};
+    float s = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const uint32_t v = qq[t];
+        const uint32_t a = (v & 0x000f000fu) | magic;
+        const uint32_t c = ((v >> 8) & 0x000f000fu) | magic;
+        const uint32_t b = ((v >> 4) & 0x000f000fu) | magic;
+        const uint32_t d = ((v >> 12) & 0x000f000fu) | magic;
+        s = fdot2(h22u(u2h2(a) - off), xs[4 * t + 0], s);
+        s = fdot2(h22u(u2h2(c) - off), xs[4 * t + 1], s);
+        s = fdot2(h22u(u2h2(b) - off), xs[4 * t + 2], s);
+        s = fdot2(h22u(u2h2(d) - off), xs[4 * t + 3], s);
+    }
+    return s;
+}
+
+// up to four weight matrices stacked along the output rows (rows [row_end[i-1],
+// row_end[i]) belong to matrix i; unused entries hold INT_MAX)
+struct Q4Set {
+    const uint8_t *qs[4];
+    const uint16_t *d[4];
+    const float *add[4];  // residual or bias of the matrix's output rows, or NULL
+    float *y[4];
+    int row_end[4];
+};
+
+// Selecting a matrix's pointer: the four candidates pass through an empty asm
+// statement first, so the select works on register values.  A select between plain
+// loads of the by-value kernel argument would be rewritten into a load from a computed
+// address, which copies the struct to scratch memory.
+template <class T>
+__device__ __forceinline__ T opaque_s(T v) {
+    if constexpr (sizeof(T) == 8) {
+        uint64_t u = (uint64_t)v;
+        asm volatile("" : "+s"(u));
+        return (T)u;
+    } else {
+        uint32_t u = (uint32_t)v;
+        asm volatile("" : "+s"(u));
+        return (T)u;
+    }
+}
+
+template <class T>
+__device__ __forceinline__ T pick4(int i, T a0, T a1, T a2, T a3) {
+    return i >= 3 ? a3 : i >= 2 ? a2 : i >= 1 ? a1 : a0;
+}
+
+#define Q4SET_PICK(S, f, i) \
+    pick4((i), opaque_s((S).f[0]), opaque_s((S).f[1]), opaque_s((S).f[2]), opaque_s((S).f[3]))
+
+__device__ __forceinline__ int q4set_index(const Q4Set &S, int r) {
+    return (r >= S.row_end[0]) + (r >= S.row_end[1]) + (r >= S.row_end[2]);
+}
+__device__ __forceinline__ int q4set_row_start(const Q4Set &S, int i) {
+    return pick4(i, 0, opaque_s(S.row_end[0]), opaque_s(S.row_end[1]), opaque_s(S.row_end[2]));
+}
+
+// unit modes: which two rows a unit holds and what its epilogue does
+constexpr int XR_PAIRS = 0;  // rows 2u, 2u+1; y = W x (+ add)
+constexpr int XR_GLU = 1;    // gate row u and up row u; h[u] = fp16(silu(g) * u)
+constexpr int XR_ROPE = 2;   // q/k rotation pairs (i, i + hd/2) of one head, then v row pairs
+
+template <int UM>
+__device__ __forceinline__ void xr_rows(const Q4Set &S, const RopeKV &R, int u, int n_rows, int &r0, int &r1,
+                                        bool &ok1) {
+    if constexpr (UM == XR_PAIRS) {
+        r0 = 2 * u;
+        r1 = 2 * u + 1;
+        ok1 = r1 < n_rows;
+        if (!ok1) r1 = r0;
+    } else if constexpr (UM == XR_GLU) {
+        r0 = u;
+        r1 = S.row_end[0] + u;
+        ok1 = true;
+    } else {
+        const int half = R.hd / 2, n_pairs = (R.n_q + R.n_k) / 2;
+        if (u < n_pairs) {
+            r0 = (u / half) * R.hd + u % half;
+            r1 = r0 + half;
+        } else {
+            r0 = R.n_q + R.n_k + 2 * (u - n_pairs);
+            r1 = r0 + 1;
+        }
+        ok1 = true;
+    }
+}
+
+template <int KB>
+struct XrRows {
+    int4 w[2][KB];
+    uint32_t d[2][KB];
+};
+
+// global-address-space accesses from integer addresses (the picked pointers are
+// plain integers after the register select; a generic pointer would give flat loads,
+// which also count against the LDS counter)
+#define MI_GLOBAL __attribute__((address_space(1)))
+__device__ __forceinline__ int4 ldg_stream16(uint64_t a) {
+    const int4v_t v = __builtin_nontemporal_load((const MI_GLOBAL int4v_t *)a);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ldg_u16(uint64_t a) { return *(const MI_GLOBAL uint16_t *)a; }
+__device__ __forceinline__ float ldg_f32(uint64_t a) { return *(const MI_GLOBAL float *)a; }
+__device__ __forceinline__ void stg_f32(uint64_t a, float v) { *(MI_GLOBAL float *)a = v; }
+__device__ __forceinline__ void stg_u16(uint64_t a, uint16_t v) { *(MI_GLOBAL uint16_t *)a = v; }
+
+// weights of rows r0, r1 at the lane's blocks; with dummy every lane reads block 0 of
+// r0 (one cache line: keeps the instruction count, and so the wait counts, identical
+// on the last step)
+template <int KB>
+__device__ __forceinline__ void xr_load(XrRows<KB> &W, const Q4Set &S, int r0, int r1, const int *bidx, bool dummy,
+                                        int nb) {
+#pragma unroll
+    for (int rr = 0; rr < 2; rr++) {
+        const int r = rr ? r1 : r0;
+        const int mi = q4set_index(S, r);
+        const uint64_t base = (uint64_t)(r - q4set_row_start(S, mi)) * (uint64_t)nb;
+        const uint64_t qs = (uint64_t)Q4SET_PICK(S, qs, mi) + base * 16;
+        const uint64_t dp = (uint64_t)Q4SET_PICK(S, d, mi) + base * 2;
+#pragma unroll
+        for (int i = 0; i < KB; i++) {
+            const uint64_t b = dummy ? 0 : (uint64_t)bidx[i];
+            W.w[rr][i] = ldg_stream16(qs + b * 16);
+            W.d[rr][i] = ldg_u16(dp + b * 2);
+        }
+    }
+}
+
+template <int KB>
+__device__ __forceinline__ void xr_dot(const XrRows<KB> &W, const uint32_t (*xr)[16], const bool *bval, float &s0,
+                                       float &s1, uint32_t magic) {
+    s0 = 0.0f;
+    s1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KB; i++) {
+        const float a = q4_dot_xr(W.w[0][i], xr[i], magic);
+        const float b = q4_dot_xr(W.w[1][i], xr[i], magic);
+        const float t0 = fmaf(h2f((uint16_t)W.d[0][i]), a, s0);
+        const float t1 = fmaf(h2f((uint16_t)W.d[1][i]), b, s1);
+        s0 = bval[i] ? t0 : s0;
+        s1 = bval[i] ? t1 : s1;
+    }
+}
+
+struct XrRope {  // per-lane rotation of pair index p = lane (p < hd/2 <= 64)
+    float cs, sn;
+    int64_t ci;
+    bool ci_ok;
+};
+
+// epilogue of one unit with its two row sums (lane 0 of the reducing wave writes; every
+// lane of that wave calls it, for the shuffles)
+template <int UM>
+__device__ __forceinline__ void xr_store(const Q4Set &S, const RopeKV &R, const XrRope &rp, uint16_t *h_out, int u,
+                                         int r0, int r1, bool ok1, float s0, float s1, int lane) {
+    const int m0 = q4set_index(S, r0), m1 = q4set_index(S, r1);
+    const int l0 = r0 - q4set_row_start(S, m0), l1 = r1 - q4set_row_start(S, m1);
+    const uint64_t a0 = (uint64_t)Q4SET_PICK(S, add, m0);
+    const uint64_t a1 = (uint64_t)Q4SET_PICK(S, add, m1);
+    if constexpr (UM == XR_ROPE) {
+        const int half = R.hd / 2, n_pairs = (R.n_q + R.n_k) / 2;
+        const float cs = __shfl(rp.cs, u % half, 64), sn = __shfl(rp.sn, u % half, 64);
+        if (lane != 0) return;
+        const float x0 = a0 ? s0 + ldg_f32(a0 + 4 * (uint64_t)l0) : s0;
+        const float x1 = a1 ? s1 + ldg_f32(a1 + 4 * (uint64_t)l1) : s1;
+        if (u < n_pairs) {
+            const float y0 = mul_sub_mul_rn(x0, cs, x1, sn);
+            const float y1 = mul_add_mul_rn(x0, sn, x1, cs);
+            if (r0 < R.n_q) {
+                R.q_out[r0] = y0;
+                R.q_out[r1] = y1;
+            } else if (rp.ci_ok) {
+                uint16_t *kr = (uint16_t *)(R.k_cache + (size_t)rp.ci * R.k_row_bytes);
+                kr[r0 - R.n_q] = f2h(y0);
+                kr[r1 - R.n_q] = f2h(y1);
+            }
+        } else if (rp.ci_ok) {
+            uint16_t *vr = (uint16_t *)(R.v_cache + (size_t)rp.ci * R.v_row_bytes);
+            vr[r0 - R.n_q - R.n_k] = f2h(x0);
+            vr[r1 - R.n_q - R.n_k] = f2h(x1);
+        }
+    } else if constexpr (UM == XR_GLU) {
+        if (lane != 0) return;
+        const float g = a0 ? s0 + ldg_f32(a0 + 4 * (uint64_t)l0) : s0;
+        const float v = a1 ? s1 + ldg_f32(a1 + 4 * (uint64_t)l1) : s1;
+        h_out[u] = f2h((g / (1.0f + expf(-g))) * v);
+    } else {
+        if (lane != 0) return;
+        const uint64_t y0 = (uint64_t)Q4SET_PICK(S, y, m0), y1 = (uint64_t)Q4SET_PICK(S, y, m1);
+        stg_f32(y0 + 4 * (uint64_t)l0, a0 ? s0 + ldg_f32(a0 + 4 * (uint64_t)l0) : s0);
+        if (ok1) stg_f32(y1 + 4 * (uint64_t)l1, a1 ? s1 + ldg_f32(a1 + 4 * (uint64_t)l1) : s1);
+    }
+}
+
+// KB blocks per lane and WPR waves per row pair (k <= 64*32*WPR*KB); XF32: the
+// activation is fp32 (rounded to fp16 RNE, as ggml converts src1), else fp16; XN > 0:
+// RMSNorm with norm_w first (fp32 activation of k <= 1024*XN).
+template <int KB, int WPR, bool XF32, int XN, int UM>
+__global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void *__restrict__ xin,
+                                                      const float *__restrict__ norm_w, float eps, int nb,
+                                                      int n_units, int n_rows, const RopeKV R,
+                                                      uint16_t *__restrict__ h_out) {
+    constexpr int PG = 4 / WPR;  // pair groups per workgroup
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int k = nb * QK;
+    uint16_t *s_x = (uint16_t *)smem;
+    float *s_red = (float *)(smem + (size_t)k * 2);  // [2][4][2]
+    double *s_nred = (double *)(s_red + 16);        // [4]
+    const int tid = threadIdx.x, lane = tid & 63;
+    // the unit, row and matrix indices are wave-uniform: scalar registers and scalar selects
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));
+    const int pg = wave / WPR, ks = wave % WPR;
+    int bidx[KB];
+    bool bval[KB];
+#pragma unroll
+    for (int i = 0; i < KB; i++) {
+        const int b = lane + 64 * (ks + WPR * i);
+        bval[i] = b < nb;
+        bidx[i] = min(b, nb - 1);
+    }
+    const int stride = gridDim.x * PG;
+    const int u_first = blockIdx.x * PG + pg;
+
+    // the first unit's weights go out before the activation is staged
+    XrRows<KB> wa, wb;
+    int r0, r1;
+    bool ok1;
+    xr_rows<UM>(S, R, min(u_first, n_units - 1), n_rows, r0, r1, ok1);
+    xr_load<KB>(wa, S, r0, r1, bidx, false, nb);
+
+    const int k4 = k / 4;
+    if constexpr (XN > 0) {
+        XStage<XN, true> st;
+        xstage_load(st, (const float *)xin, norm_w, nullptr, k4, tid);
+        const float scale = xstage_scale(st, k4, eps, s_nred, tid);
+#pragma unroll
+        for (int t = 0; t < XN; t++) {
+            const int f = tid + t * 256;
+            const float4 v = xstage_value(st, scale, t);
+            if (f < k4)
+                ((uint2 *)s_x)[f] = make_uint2((uint32_t)f2h(v.x) | ((uint32_t)f2h(v.y) << 16),
+                                               (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16));
+        }
+    } else if constexpr (XF32) {
+        for (int f = tid; f < k4; f += 256) {
+            const float4 v = ((const float4 *)xin)[f];
+            ((uint2 *)s_x)[f] = make_uint2((uint32_t)f2h(v.x) | ((uint32_t)f2h(v.y) << 16),
+                                           (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16));
+        }
+    } else {
+        for (int f = tid; f < k / 8; f += 256) ((int4 *)s_x)[f] = ((const int4 *)xin)[f];
+    }
+
+    XrRope rp;
+    if constexpr (UM == XR_ROPE) {
+        float theta = (float)R.pos[0];
+        for (int i = 0; i < lane && i < R.hd / 2; i++) theta *= R.theta_scale;
+        const float th = R.freq_scale * theta;
+        rp.cs = cosf(th) * R.attn_factor;
+        rp.sn = sinf(th) * R.attn_factor;
+        rp.ci = R.kv_idx_i64 ? ((const int64_t *)R.kv_idx)[0] : (int64_t)((const int32_t *)R.kv_idx)[0];
+        rp.ci_ok = rp.ci >= 0 && rp.ci < R.n_cache_rows;
+    }
+    __syncthreads();
+
+    uint32_t xr[KB][16];
+#pragma unroll
+    for (int i = 0; i < KB; i++) {
+        const uint4 *p = (const uint4 *)(s_x + (size_t)bidx[i] * QK);
+        const uint4 q0 = p[0], q1 = p[1], q2 = p[2], q3 = p[3];
+        const uint32_t w[16] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w,
+                                q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, q3.z, q3.w};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            xr[i][4 * t + 0] = (w[2 * t] & 0xffffu) | (w[2 * t + 1] << 16);
+            xr[i][4 * t + 1] = (w[2 * t] >> 16) | (w[2 * t + 1] & 0xffff0000u);
+            xr[i][4 * t + 2] = (w[8 + 2 * t] & 0xffffu) | (w[9 + 2 * t] << 16);
+            xr[i][4 * t + 3] = (w[8 + 2 * t] >> 16) | (w[9 + 2 * t] & 0xffff0000u);
+        }
+    }
+
+    if constexpr (WPR == 1) {
+        // one pair group per wave, no workgroup barriers past this point
+        if (u_first >= n_units) return;
+        int u = u_first;
+        for (;;) {
+            const int ub = u + stride;
+            const bool more_b = ub < n_units;
+            int q0, q1;
+            bool qok;
+            xr_rows<UM>(S, R, more_b ? ub : u, n_rows, q0, q1, qok);
+            xr_load<KB>(wb, S, q0, q1, bidx, !more_b, nb);
+            __builtin_amdgcn_sched_barrier(0);  // the next pair's loads issue before this pair's math
+            float s0, s1;
+            xr_dot<KB>(wa, xr, bval, s0, s1, magic);
+            s0 = group_sum<64>(s0);
+            s1 = group_sum<64>(s1);
+            xr_store<UM>(S, R, rp, h_out, u, r0, r1, ok1, s0, s1, lane);
+            if (!more_b) break;
+            u = ub;
+            r0 = q0; r1 = q1; ok1 = qok;
+
+            const int ua = u + stride;
+            const bool more_a = ua < n_units;
+            xr_rows<UM>(S, R, more_a ? ua : u, n_rows, q0, q1, qok);
+            xr_load<KB>(wa, S, q0, q1, bidx, !more_a, nb);
+            __builtin_amdgcn_sched_barrier(0);  // the next pair's loads issue before this pair's math
+            xr_dot<KB>(wb, xr, bval, s0, s1, magic);
+            s0 = group_sum<64>(s0);
+            s1 = group_sum<64>(s1);
+            xr_store<UM>(S, R, rp, h_out, u, r0, r1, ok1, s0, s1, lane);
+            if (!more_a) break;
+            u = ua;
+            r0 = q0; r1 = q1; ok1 = qok;
+        }
+    } else {
+        // WPR waves share a unit: the trip count is uniform over the workgroup (units past
+        // the end are computed on a clamped unit and not stored), partial sums meet in LDS
+        int base = blockIdx.x * PG;
+        int par = 0;
+        auto finish = [&](int u, int a0, int a1, bool aok, float s0, float s1) {
+            s0 = group_sum<64>(s0);
+            s1 = group_sum<64>(s1);
+            if (lane == 0) {
+                s_red[(par * 4 + wave) * 2 + 0] = s0;
+                s_red[(par * 4 + wave) * 2 + 1] = s1;
+            }
+            __syncthreads();
+            if (ks == 0 && u < n_units) {
+                float t0 = 0.0f, t1 = 0.0f;
+#pragma unroll
+                for (int w = 0; w < WPR; w++) {
+                    t0 += s_red[(par * 4 + pg * WPR + w) * 2 + 0];
+                    t1 += s_red[(par * 4 + pg * WPR + w) * 2 + 1];
+                }
+                xr_store<UM>(S, R, rp, h_out, u, a0, a1, aok, t0, t1, lane);
+            }
+            par ^= 1;
+        };
+        if (base >= n_units) return;  // uniform over the workgroup
+        for (;;) {
+            const int u = base + pg;
+            const int nbase = base + stride;
+            const bool more_b = nbase < n_units;  // uniform
+            int q0, q1;
+            bool qok;
+            xr_rows<UM>(S, R, min(more_b ? nbase + pg : u, n_units - 1), n_rows, q0, q1, qok);
+            xr_load<KB>(wb, S, q0, q1, bidx, !more_b, nb);
+            __builtin_amdgcn_sched_barrier(0);  // the next pair's loads issue before this pair's math
+            float s0, s1;
+            xr_dot<KB>(wa, xr, bval, s0, s1, magic);
+            finish(u, r0, r1, ok1, s0, s1);
+            if (!more_b) break;
+            base = nbase;
+            r0 = q0; r1 = q1; ok1 = qok;
+
+            const int u2 = base + pg;
+            const int nbase2 = base + stride;
+            const bool more_a = nbase2 < n_units;
+            xr_rows<UM>(S, R, min(more_a ? nbase2 + pg : u2, n_units - 1), n_rows, q0, q1, qok);
+            xr_load<KB>(wa, S, q0, q1, bidx, !more_a, nb);
+            __builtin_amdgcn_sched_barrier(0);  // the next pair's loads issue before this pair's math
+            xr_dot<KB>(wb, xr, bval, s0, s1, magic);
+            finish(u2, r0, r1, ok1, s0, s1);
+            if (!more_a) break;
+            base = nbase2;
+            r0 = q0; r1 = q1; ok1 = qok;
+        }
+    }
+}
+
 inline int q4_pick_u(int64_t nb, int g) {
     int64_t u = (nb + g - 1) / g;
     if (u > 8) u = (u + 1) / 2 > 8 ? 8 : (u + 1) / 2;
@@ -428,9 +833,153 @@ int launch_mfma(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64
     return MI_OK;
 }
 
+// ---- one activation row: launch of k_gemv_q4_0_xr
+struct XrShape {
+    int kb, wpr;
+};
+
+// blocks per lane and waves per row pair for nb blocks per row (nb <= 64*wpr*kb)
+inline bool xr_shape(int64_t nb, XrShape &s) {
+    if (nb <= 64) s = {1, 1};
+    else if (nb <= 128) s = {2, 1};
+    else if (nb <= 256) s = {2, 2};
+    else if (nb <= 384) s = {3, 2};
+    else if (nb <= 512) s = {2, 4};
+    else if (nb <= 768) s = {3, 4};
+    else if (nb <= 1016) s = {4, 4};  // the fp16 row and the reduction slots within 64 KB of LDS
+    else return false;
+    return true;
+}
+
+inline size_t xr_smem(int64_t k) { return (size_t)k * 2 + 16 * sizeof(float) + 4 * sizeof(double); }
+
+// workgroups resident at once on the current device for this kernel and LDS size
+int xr_resident(const void *fn, size_t smem) {
+    static std::mutex mu;
+    static std::unordered_map<uint64_t, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    const uint64_t key = ((uint64_t)(uintptr_t)fn * 31 + smem) * 64 + (uint64_t)dev;
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        auto it = cache.find(key);
+        if (it != cache.end()) return it->second;
+    }
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, smem) != hipSuccess || per_cu < 1) per_cu = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+    int r = per_cu * cus;
+    if (const char *e = getenv("MI_Q4_XR_GRID")) r = (int)(r * atof(e));  // experiments: resident multiple
+    if (r < 1) r = 1;
+    std::lock_guard<std::mutex> lk(mu);
+    cache[key] = r;
+    return r;
+}
+
+template <int KB, int WPR, bool XF32, int XN, int UM>
+int launch_xr(hipStream_t st, const Q4Set &S, const void *x, const float *norm_w, float eps, int nb, int n_units,
+              int n_rows, const RopeKV &R, uint16_t *h) {
+    constexpr int PG = 4 / WPR;
+    const size_t smem = xr_smem((int64_t)nb * QK);
+    auto fn = k_gemv_q4_0_xr<KB, WPR, XF32, XN, UM>;
+    const int want = (n_units + PG - 1) / PG;
+    const int grid = std::min(want, xr_resident((const void *)fn, smem));
+    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), smem, st, S, x, norm_w, eps, nb, n_units, n_rows, R, h);
+    MI_CHECK_LAUNCH("k_gemv_q4_0_xr");
+    return MI_OK;
+}
+
+// shapes for any k up to 32768 (fp16 or fp32 activation, no norm)
+template <bool XF32, int UM>
+int launch_xr_any(hipStream_t st, const XrShape &sh, const Q4Set &S, const void *x, int nb, int n_units, int n_rows,
+                  const RopeKV &R, uint16_t *h) {
+#define MI_XR_CASE(KB, WPR) \
+    if (sh.kb == KB && sh.wpr == WPR) return launch_xr<KB, WPR, XF32, 0, UM>(st, S, x, nullptr, 0.0f, nb, n_units, n_rows, R, h);
+    MI_XR_CASE(1, 1) MI_XR_CASE(2, 1) MI_XR_CASE(2, 2) MI_XR_CASE(3, 2) MI_XR_CASE(2, 4) MI_XR_CASE(3, 4)
+    MI_XR_CASE(4, 4)
+#undef MI_XR_CASE
+    set_error("gemv_q4_0: no kernel for %d blocks per row", nb);
+    return MI_ERR_UNSUPPORTED;
+}
+
+// short rows (k <= 4096: one wave per row pair) with the optional RMSNorm
+template <int UM>
+int launch_xr_short(hipStream_t st, const Q4Set &S, const void *x, const float *norm_w, float eps, int nb,
+                    int n_units, int n_rows, const RopeKV &R, uint16_t *h) {
+    const int k4 = nb * QK / 4;
+    if (!norm_w) {
+        if (nb <= 64) return launch_xr<1, 1, true, 0, UM>(st, S, x, nullptr, eps, nb, n_units, n_rows, R, h);
+        return launch_xr<2, 1, true, 0, UM>(st, S, x, nullptr, eps, nb, n_units, n_rows, R, h);
+    }
+#define MI_XR_CASE(XN)                                                                                         \
+    if (k4 <= 256 * XN) {                                                                                      \
+        if (nb <= 64) return launch_xr<1, 1, true, XN, UM>(st, S, x, norm_w, eps, nb, n_units, n_rows, R, h); \
+        return launch_xr<2, 1, true, XN, UM>(st, S, x, norm_w, eps, nb, n_units, n_rows, R, h);               \
+    }
+    MI_XR_CASE(1) MI_XR_CASE(2) MI_XR_CASE(4)
+#undef MI_XR_CASE
+    set_error("gemv_q4_0: k=%d too long for the fused norm", nb * QK);
+    return MI_ERR_UNSUPPORTED;
+}
+
+// stacks n_mats matrices (packed Q4_0, n[i] rows of k) into a Q4Set
+int make_q4set(Q4Set &S, int n_mats, const void *const *w, const int64_t *n, float *const *y,
+               const float *const *add, int64_t k, int &n_total) {
+    MI_CHECK_ARG(n_mats >= 1 && n_mats <= 4, "gemv_q4_0: %d matrices (1..4)", n_mats);
+    int64_t tot = 0;
+    for (int i = 0; i < 4; i++) {
+        if (i < n_mats) {
+            MI_CHECK_ARG(w[i] && n[i] > 0 && mi::aligned(w[i], 256), "gemv_q4_0: matrix %d: null, empty or misaligned", i);
+            const Q4Planes p = q4_planes(n[i], k);
+            S.qs[i] = (const uint8_t *)w[i];
+            S.d[i] = (const uint16_t *)((const uint8_t *)w[i] + p.plane);
+            S.add[i] = add ? add[i] : nullptr;
+            S.y[i] = y ? y[i] : nullptr;
+            tot += n[i];
+            MI_CHECK_ARG(tot < (1ll << 30), "gemv_q4_0: too many rows");
+            S.row_end[i] = (int)tot;
+        } else {
+            S.qs[i] = S.qs[0];
+            S.d[i] = S.d[0];
+            S.add[i] = nullptr;
+            S.y[i] = nullptr;
+            S.row_end[i] = INT_MAX;
+        }
+    }
+    n_total = (int)tot;
+    return MI_OK;
+}
+
+// y = W x (+ add) for one activation row through the register-resident kernel
+int launch_xr_gemv(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, const void *x, bool xf32, float *y,
+                   const float *add) {
+    XrShape sh;
+    if (!xr_shape(k / QK, sh)) return MI_ERR_UNSUPPORTED;
+    Q4Set S;
+    int n_total = 0;
+    const void *w[1] = {base};
+    const int64_t nn[1] = {n};
+    float *ys[1] = {y};
+    const float *as[1] = {add};
+    if (int r = make_q4set(S, 1, w, nn, ys, as, k, n_total)) return r;
+    RopeKV R{};
+    const int units = (n_total + 1) / 2;
+    if (xf32) return launch_xr_any<true, XR_PAIRS>(st, sh, S, x, (int)(k / QK), units, n_total, R, nullptr);
+    return launch_xr_any<false, XR_PAIRS>(st, sh, S, x, (int)(k / QK), units, n_total, R, nullptr);
+}
+
+inline bool xr_enabled() {
+    static const bool on = [] {
+        const char *e = getenv("MI_Q4_XR");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
 int launch_gx(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16, float *y,
               const float *add = nullptr) {
     if (m >= 2 && m <= 16) return launch_mfma<false>(st, base, n, k, m, x16, y, add);
+    if (m == 1 && xr_enabled() && k / QK <= 1016) return launch_xr_gemv(st, base, n, k, x16, false, y, add);
     const bool tall = n >= 2048;
     if (m == 1) return tall ? launch_gx_mr<1, 2>(st, base, n, k, m, x16, y, add)
                             : launch_gx_mr<1, 1>(st, base, n, k, m, x16, y, add);
@@ -523,6 +1072,7 @@ int mi_mul_mat_q4_0_f32(void *stream, const void *w_packed, const float *x, floa
     MI_CHECK_ARG(mi::aligned(w_packed, 256) && mi::aligned(x, 16), "mul_mat_q4_0_f32: w_packed must be 256-byte, x 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     if (m > 1) return launch_mfma<true>(st, (const uint8_t *)w_packed, n, k, m, x, y, nullptr);
+    if (xr_enabled() && k / QK <= 1016) return launch_xr_gemv(st, (const uint8_t *)w_packed, n, k, x, true, y, nullptr);
     const size_t need = mi_mul_mat_q4_0_workspace_size(m, k);
     if (need == 0) return launch_lds(st, (const uint8_t *)w_packed, n, k, m, x, y);
     if (!ws || ws_bytes < need || !mi::aligned(ws, 16)) {
@@ -531,6 +1081,88 @@ int mi_mul_mat_q4_0_f32(void *stream, const void *w_packed, const float *x, floa
     }
     if (int r = mi_cast_f32_f16(stream, x, (uint16_t *)ws, m * k)) return r;
     return launch_gx(st, (const uint8_t *)w_packed, n, k, m, (const uint16_t *)ws, y);
+}
+
+int mi_mul_mat_q4_0_f32_fused(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
+                              float *const *y, const float *const *add, int64_t k, const float *x,
+                              const float *norm_w, float eps) {
+    MI_CHECK_ARG(w_packed && n && y && x, "mul_mat_q4_0_f32_fused: null pointer");
+    if (int r = check_shape("mul_mat_q4_0_f32_fused", 1, k)) return r;
+    MI_CHECK_ARG(k <= (norm_w ? 4096 : 1016 * QK), "mul_mat_q4_0_f32_fused: k=%lld too long", (long long)k);
+    MI_CHECK_ARG(mi::aligned(x, 16) && (!norm_w || mi::aligned(norm_w, 16)),
+                 "mul_mat_q4_0_f32_fused: x/norm_w must be 16-byte aligned");
+    for (int i = 0; i < n_mats && i < 4; i++) MI_CHECK_ARG(y[i], "mul_mat_q4_0_f32_fused: y[%d] is NULL", i);
+    Q4Set S;
+    int n_total = 0;
+    if (int r = make_q4set(S, n_mats, w_packed, n, y, add, k, n_total)) return r;
+    RopeKV R{};
+    if (!norm_w && k > 4096) {
+        XrShape sh;
+        xr_shape(k / QK, sh);
+        return launch_xr_any<true, XR_PAIRS>((hipStream_t)stream, sh, S, x, (int)(k / QK), (n_total + 1) / 2, n_total,
+                                             R, nullptr);
+    }
+    return launch_xr_short<XR_PAIRS>((hipStream_t)stream, S, x, norm_w, eps, (int)(k / QK), (n_total + 1) / 2,
+                                     n_total, R, nullptr);
+}
+
+int mi_gate_up_swiglu_q4_0(void *stream, const void *w_gate, const void *w_up, int64_t n, int64_t k, const float *x,
+                           const float *norm_w, float eps, uint16_t *h_out) {
+    MI_CHECK_ARG(w_gate && w_up && x && h_out, "gate_up_swiglu_q4_0: null pointer");
+    if (int r = check_shape("gate_up_swiglu_q4_0", n, k)) return r;
+    MI_CHECK_ARG(k <= 4096, "gate_up_swiglu_q4_0: k=%lld > 4096", (long long)k);
+    MI_CHECK_ARG(mi::aligned(x, 16) && (!norm_w || mi::aligned(norm_w, 16)),
+                 "gate_up_swiglu_q4_0: x/norm_w must be 16-byte aligned");
+    Q4Set S;
+    int n_total = 0;
+    const void *w[2] = {w_gate, w_up};
+    const int64_t nn[2] = {n, n};
+    if (int r = make_q4set(S, 2, w, nn, nullptr, nullptr, k, n_total)) return r;
+    RopeKV R{};
+    return launch_xr_short<XR_GLU>((hipStream_t)stream, S, x, norm_w, eps, (int)(k / QK), (int)n, n_total, R, h_out);
+}
+
+int mi_qkv_rope_kv_q4_0(void *stream, const void *const *w_packed, const int64_t *n, const float *const *bias,
+                        int64_t k, const float *x, const float *norm_w, float eps, int64_t head_dim,
+                        const int32_t *pos, float freq_base, float freq_scale, float attn_factor, float *q_out,
+                        void *k_cache, size_t k_row_bytes, void *v_cache, size_t v_row_bytes, const void *kv_idx,
+                        int kv_idx_is_i64, int64_t n_cache_rows) {
+    MI_CHECK_ARG(w_packed && n && bias && x && pos && q_out && k_cache && v_cache && kv_idx,
+                 "qkv_rope_kv_q4_0: null pointer");
+    if (int r = check_shape("qkv_rope_kv_q4_0", 1, k)) return r;
+    MI_CHECK_ARG(k <= 4096, "qkv_rope_kv_q4_0: k=%lld > 4096", (long long)k);
+    MI_CHECK_ARG(head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 128, "qkv_rope_kv_q4_0: head_dim %lld (even, <= 128)",
+                 (long long)head_dim);
+    MI_CHECK_ARG(n[0] > 0 && n[1] > 0 && n[2] > 0 && n[0] % head_dim == 0 && n[1] % head_dim == 0 && n[2] % 2 == 0,
+                 "qkv_rope_kv_q4_0: q/k rows must be whole heads, v rows even");
+    MI_CHECK_ARG(k_row_bytes >= (size_t)n[1] * 2 && v_row_bytes >= (size_t)n[2] * 2 && n_cache_rows > 0,
+                 "qkv_rope_kv_q4_0: cache rows too short");
+    MI_CHECK_ARG(mi::aligned(x, 16) && (!norm_w || mi::aligned(norm_w, 16)),
+                 "qkv_rope_kv_q4_0: x/norm_w must be 16-byte aligned");
+    Q4Set S;
+    int n_total = 0;
+    if (int r = make_q4set(S, 3, w_packed, n, nullptr, bias, k, n_total)) return r;
+    RopeKV R{};
+    R.q_out = q_out;
+    R.k_cache = (uint8_t *)k_cache;
+    R.v_cache = (uint8_t *)v_cache;
+    R.k_row_bytes = k_row_bytes;
+    R.v_row_bytes = v_row_bytes;
+    R.pos = pos;
+    R.kv_idx = kv_idx;
+    R.kv_idx_i64 = kv_idx_is_i64;
+    R.n_cache_rows = n_cache_rows;
+    R.hd = (int)head_dim;
+    R.n_q = (int)n[0];
+    R.n_k = (int)n[1];
+    R.n_v = (int)n[2];
+    // theta_scale on the host with the C library powf, as the CPU rope cache does
+    R.theta_scale = powf(freq_base, -2.0f / (float)head_dim);
+    R.freq_scale = freq_scale;
+    R.attn_factor = attn_factor;
+    const int units = (R.n_q + R.n_k) / 2 + R.n_v / 2;
+    return launch_xr_short<XR_ROPE>((hipStream_t)stream, S, x, norm_w, eps, (int)(k / QK), units, n_total, R,
+                                    nullptr);
 }
 
 int mi_cast_f32_f16(void *stream, const float *x, uint16_t *y, int64_t n) {

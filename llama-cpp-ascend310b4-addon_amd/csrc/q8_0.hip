@@ -11,6 +11,7 @@
 // (experiments/a8w8/custom_ops_nz/op_kernel/matmul_w8a8_i32_custom.cpp:15-48)
 // and W8a8DequantCustom (called at patch:1269-1270) with its casts.
 #include "mi_common.h"
+#include "decode_common.h"
 
 #include <limits.h>
 #include <math.h>
@@ -209,63 +210,16 @@ __device__ __forceinline__ int q8set_row_start(const Q8Set &S, int i) {
 // weight pointers into flat addresses
 #define Q8SET_PICK(S, f, i) ((i) == 0 ? (S).f[0] : (i) == 1 ? (S).f[1] : (i) == 2 ? (S).f[2] : (S).f[3])
 
-// One activation row staged by a 256-thread workgroup: XN float4 per thread
-// (k <= 1024*XN), loaded before the weights so that the quantization waits only
-// for the cache-resident activation while the weight loads are in flight.
-template <int XN, bool NORM>
-struct XStage {
-    float4 xv[XN], sv[XN], nv[XN];
-};
-
-template <int XN, bool NORM>
-__device__ __forceinline__ void xstage_load(XStage<XN, NORM> &st, const float *__restrict__ x,
-                                            const float *__restrict__ norm_w, const float *__restrict__ inv_s, int k4,
-                                            int tid) {
-#pragma unroll
-    for (int t = 0; t < XN; t++) {
-        const int f = min(tid + t * 256, k4 - 1);
-        st.xv[t] = ((const float4 *)x)[f];
-        if constexpr (NORM) st.nv[t] = ((const float4 *)norm_w)[f];
-        if (inv_s) st.sv[t] = ((const float4 *)inv_s)[f];
-    }
-}
-
-// Optional RMSNorm with the norm weight (ggml rms_norm then mul: y = (x*scale)*w,
-// scale = 1/sqrtf(mean + eps), mean = (float)(sum of (double)(x*x) / k)), then the
-// SmoothQuant reciprocal, then Q8_0 quantization of each 32-block into LDS.  The
-// caller puts a barrier between this and the reads of s_qs / s_d.
+// RMSNorm (optional), then the SmoothQuant reciprocal, then Q8_0 quantization of each
+// 32-block into LDS.  The caller puts a barrier between this and the reads of s_qs / s_d.
 template <int XN, bool NORM>
 __device__ __forceinline__ void xstage_quant(XStage<XN, NORM> &st, const float *__restrict__ inv_s, int k4, float eps,
                                              int rounding, int8_t *s_qs, float *s_d, double *s_red, int tid) {
-    float scale = 1.0f;
-    if constexpr (NORM) {
-        double ss = 0.0;
-#pragma unroll
-        for (int t = 0; t < XN; t++) {
-            if (tid + t * 256 < k4) {
-                const float4 v = st.xv[t];
-                ss += (double)__fmul_rn(v.x, v.x);
-                ss += (double)__fmul_rn(v.y, v.y);
-                ss += (double)__fmul_rn(v.z, v.z);
-                ss += (double)__fmul_rn(v.w, v.w);
-            }
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        if ((tid & 63) == 0) s_red[tid >> 6] = ss;
-        __syncthreads();
-        const double tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-        const float mean = (float)(tot / (double)(k4 * 4));
-        scale = 1.0f / sqrtf(mean + eps);
-    }
+    const float scale = xstage_scale(st, k4, eps, s_red, tid);
 #pragma unroll
     for (int t = 0; t < XN; t++) {
         const int f = tid + t * 256;  // float4 index; 8 consecutive threads form one 32-block
-        float4 v = st.xv[t];
-        if constexpr (NORM) {
-            v.x = (v.x * scale) * st.nv[t].x; v.y = (v.y * scale) * st.nv[t].y;
-            v.z = (v.z * scale) * st.nv[t].z; v.w = (v.w * scale) * st.nv[t].w;
-        }
+        float4 v = xstage_value(st, scale, t);
         if (inv_s) { v.x *= st.sv[t].x; v.y *= st.sv[t].y; v.z *= st.sv[t].z; v.w *= st.sv[t].w; }
         float d;
         const uint32_t q = quant4(v.x, v.y, v.z, v.w, rounding, d);
@@ -384,44 +338,23 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0_fused1(const Q8Set S, const f
     }
 }
 
-// q/k/v projections with the rest of the attention-input chain fused in: bias add,
-// neox RoPE of q and k (theta_i = pos * theta_scale^i by repeated multiplication,
-// products unfused as in the CPU loop), q written fp32, k and v converted to fp16
-// into their cache row.  16 lanes per row, 16 rows per workgroup; a workgroup on
-// the rotated rows owns 8 rotation pairs (i, i + hd/2) of one head, so each pair's
-// two results meet in LDS.
-struct RopeKV {
-    const float *bias[3];
-    float *q_out;
-    uint8_t *k_cache, *v_cache;
-    size_t k_row_bytes, v_row_bytes;
-    const int32_t *pos;
-    const void *kv_idx;
-    int kv_idx_i64;
-    int64_t n_cache_rows;
-    int hd, n_q, n_k, n_v;
-    float theta_scale, freq_scale, attn_factor;
-};
-
+// q/k/v projections with the rest of the attention-input chain fused in (bias add,
+// neox RoPE of q and k, q written fp32, k and v converted to fp16 into their cache
+// row); the row mapping and epilogue are shared with the W4A16 kernel (RopeKV).
 template <int G, int U, int XN, bool NORM>
 __global__ __launch_bounds__(256) void k_gemv_q8_0_qkv_rope(const Q8Set S, const RopeKV R, const float *__restrict__ x,
                                                             const float *__restrict__ norm_w, float eps,
                                                             const float *__restrict__ inv_s, int nb, int rounding) {
-    constexpr int RPB = 256 / G;   // rows per workgroup
-    constexpr int HALF = RPB / 2;  // rotation pairs per workgroup
+    constexpr int RPB = 256 / G;  // rows per workgroup
     extern __shared__ __align__(16) uint8_t smem[];
     const FusedLds L = fused_lds(smem, nb);
     const int tid = threadIdx.x;
     const int j = tid % G;
     const int t = tid / G;
-    const int n_rope = R.n_q + R.n_k;
-    const int n_total = n_rope + R.n_v;
-    const int wg_per_head = R.hd / RPB;
+    const int n_total = R.n_q + R.n_k + R.n_v;
     const int b = blockIdx.x;
-    const bool rope = b < n_rope / RPB;
-    const int head = b / wg_per_head, chunk = b % wg_per_head;
-    const int grow = rope ? head * R.hd + (t / HALF) * (R.hd / 2) + chunk * HALF + (t % HALF) : b * RPB + t;
-    const int rc = min(grow, n_total - 1);
+    RopeKVPlace pl;
+    const int rc = min(rope_kv_row<RPB>(R, b, t, pl), n_total - 1);
     const int mi = q8set_index(S, rc);
     const int row = rc - q8set_row_start(S, mi);
     const uint8_t *qlo = Q8SET_PICK(S, qlo, mi);
@@ -443,33 +376,7 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0_qkv_rope(const Q8Set S, const
         L.y[t] = bias ? s + bias[row] : s;
     }
     __syncthreads();
-    const int64_t ci = R.kv_idx_i64 ? ((const int64_t *)R.kv_idx)[0] : (int64_t)((const int32_t *)R.kv_idx)[0];
-    const bool ci_ok = ci >= 0 && ci < R.n_cache_rows;
-    if (rope) {
-        if (tid < HALF) {
-            const int p = chunk * HALF + tid;  // rotation pair index < hd/2
-            float theta = (float)R.pos[0];
-            for (int i = 0; i < p; i++) theta *= R.theta_scale;
-            const float th = R.freq_scale * theta;
-            const float cs = cosf(th) * R.attn_factor;
-            const float sn = sinf(th) * R.attn_factor;
-            const float x0 = L.y[tid], x1 = L.y[tid + HALF];
-            const float y0 = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn));
-            const float y1 = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs));
-            const int r0 = head * R.hd + p;  // row in the stacked q|k space
-            if (r0 < R.n_q) {
-                R.q_out[r0] = y0;
-                R.q_out[r0 + R.hd / 2] = y1;
-            } else if (ci_ok) {
-                uint16_t *kr = (uint16_t *)(R.k_cache + (size_t)ci * R.k_row_bytes);
-                kr[r0 - R.n_q] = f2h(y0);
-                kr[r0 - R.n_q + R.hd / 2] = f2h(y1);
-            }
-        }
-    } else if (tid < RPB) {
-        const int vr = b * RPB + tid - n_rope;
-        if (vr < R.n_v && ci_ok) ((uint16_t *)(R.v_cache + (size_t)ci * R.v_row_bytes))[vr] = f2h(L.y[tid]);
-    }
+    rope_kv_epilogue<RPB>(R, L.y, b, tid, pl);
 }
 
 // silu(g) * u (ggml swiglu: silu(x) = x / (1 + expf(-x))), times the SmoothQuant

@@ -264,3 +264,139 @@ def test_gemv_q8_0_add_equals_gemv_plus_vector(gpu):
     mi._call("mi_gemv_q8_0_add", None, mi._P(pw.ptr), mi._P(dq.ptr), mi._P(da.ptr), mi._P(y1.ptr), n, k, 1)
     mi.device_sync()
     assert np.array_equal(y1.download(F32), (y0.download(F32) + add).astype(F32))
+
+
+# ---------------------------------------------------------------- W4A16 chains (one activation row)
+
+def _packed_q4(mi, w, n, k):
+    src = mi.to_device(w)
+    dst = mi.DeviceBuffer(mi.q4_0_packed_size(n, k)).zero()
+    mi.prepack_q4_0(src.ptr, dst.ptr, n, k)
+    mi.device_sync()
+    src.free()
+    return dst
+
+
+def _q4_ref(orc, w, x, n, k):
+    """ggml MUL_MAT of a Q4_0 weight and an fp32 row: src1 converted to fp16 (RNE)"""
+    return orc.mul_mat_q4_0_f16(w, f16_bits(x), n, k)
+
+
+@pytest.mark.parametrize("norm", [True, False])
+@pytest.mark.parametrize("ns,k", [((18944, 18944), 3584), ((3584,), 3584), ((3584, 512, 512), 3584),
+                                  ((1536,), 1536), ((7, 9), 256), ((66,), 4096)])
+def test_q4_fused_norm_matmuls_add(gpu, orc, norm, ns, k):
+    from synth import q4_0_weights
+    mi = gpu
+    rng = np.random.default_rng(sum(ns) + k + norm)
+    x = (rng.standard_normal(k) * 0.5).astype(F32)
+    nw = rng.uniform(0.8, 1.2, k).astype(F32)
+    ws = [q4_0_weights(rng, n, k) for n in ns]
+    adds = [rng.standard_normal(n).astype(F32) if i % 2 == 0 else None for i, n in enumerate(ns)]
+    pw = [_packed_q4(mi, w, n, k) for w, n in zip(ws, ns)]
+    ys = [mi.DeviceBuffer(4 * n) for n in ns]
+    da = [mi.to_device(a) if a is not None else None for a in adds]
+    dx, dnw = mi.to_device(x), mi.to_device(nw)
+    mi._call("mi_mul_mat_q4_0_f32_fused", None, len(ns), _ptrs(*pw), _i64s(*ns), _ptrs(*ys), _ptrs(*da), k,
+             mi._P(dx.ptr), mi._P(dnw.ptr if norm else None), F32(1e-6))
+    mi.device_sync()
+    xin = rms_norm_ref(x, nw, 1e-6) if norm else x
+    for i, n in enumerate(ns):
+        ref = _q4_ref(orc, ws[i], xin, n, k)
+        if adds[i] is not None:
+            ref = (ref + adds[i]).astype(F32)
+        err = rel_err(ys[i].download(F32), ref)
+        print(f"q4 fused {ns} k={k} norm={norm} matrix {i}: rel_err {err:.2e}")
+        assert err < GEMV_TOL, f"matrix {i}"
+
+
+@pytest.mark.parametrize("n,k", [(18944, 3584), (8960, 1536), (33, 512)])
+def test_q4_gate_up_swiglu(gpu, orc, n, k):
+    """h = fp16(silu(gate) * up): the GLU output as the down projection's MUL_MAT converts it"""
+    from synth import q4_0_weights
+    mi = gpu
+    rng = np.random.default_rng(n + k)
+    x = (rng.standard_normal(k) * 0.5).astype(F32)
+    nw = rng.uniform(0.8, 1.2, k).astype(F32)
+    wg, wu = q4_0_weights(rng, n, k), q4_0_weights(rng, n, k)
+    pg, pu = _packed_q4(mi, wg, n, k), _packed_q4(mi, wu, n, k)
+    dx, dnw = mi.to_device(x), mi.to_device(nw)
+    dh = mi.DeviceBuffer(2 * n)
+    mi._call("mi_gate_up_swiglu_q4_0", None, mi._P(pg.ptr), mi._P(pu.ptr), n, k, mi._P(dx.ptr), mi._P(dnw.ptr),
+             F32(1e-6), mi._P(dh.ptr))
+    mi.device_sync()
+    xn = rms_norm_ref(x, nw, 1e-6)
+    g = _q4_ref(orc, wg, xn, n, k)
+    u = _q4_ref(orc, wu, xn, n, k)
+    h = ((g / (1.0 + np.exp(-g.astype(np.float64)))).astype(F32) * u).astype(F32)
+    got = dh.download(np.uint16).view(np.float16).astype(F32)
+    err = rel_err(got, h)
+    print(f"gate_up_swiglu {n}x{k}: rel_err {err:.2e}")
+    assert err < GEMV_TOL
+
+
+@pytest.mark.parametrize("idx_i64", [False, True])
+@pytest.mark.parametrize("cfg", [dict(k=3584, hq=28, hkv=4, hd=128, pos=32767, row=32767, bias=True),
+                                 dict(k=1536, hq=12, hkv=2, hd=128, pos=517, row=517, bias=True),
+                                 dict(k=256, hq=4, hkv=2, hd=64, pos=0, row=0, bias=False),
+                                 dict(k=512, hq=6, hkv=3, hd=32, pos=40, row=1, bias=True)])
+def test_q4_qkv_rope_kv(gpu, orc, cfg, idx_i64):
+    from synth import q4_0_weights
+    mi = gpu
+    k, hq, hkv, hd = cfg["k"], cfg["hq"], cfg["hkv"], cfg["hd"]
+    nq, nkv = hq * hd, hkv * hd
+    n_cache = max(640, cfg["row"] + 1)
+    rng = np.random.default_rng(k + hq + cfg["pos"] + idx_i64)
+    x = (rng.standard_normal(k) * 0.5).astype(F32)
+    nw = rng.uniform(0.8, 1.2, k).astype(F32)
+    ns = (nq, nkv, nkv)
+    ws = [q4_0_weights(rng, n, k) for n in ns]
+    bs = [(rng.standard_normal(n) * 0.02).astype(F32) if cfg["bias"] else None for n in ns]
+    pw = [_packed_q4(mi, w, n, k) for w, n in zip(ws, ns)]
+    db = [mi.to_device(b) if b is not None else None for b in bs]
+    dx, dnw = mi.to_device(x), mi.to_device(nw)
+    dq = mi.DeviceBuffer(4 * nq)
+    kc = mi.DeviceBuffer(n_cache * nkv * 2).zero()
+    vc = mi.DeviceBuffer(n_cache * nkv * 2).zero()
+    dpos = mi.to_device(np.array([cfg["pos"]], np.int32))
+    didx = mi.to_device(np.array([cfg["row"]], np.int64 if idx_i64 else np.int32))
+    mi._call("mi_qkv_rope_kv_q4_0", None, _ptrs(*pw), _i64s(*ns), _ptrs(*db), k, mi._P(dx.ptr), mi._P(dnw.ptr),
+             F32(1e-6), hd, mi._P(dpos.ptr), F32(1e6), F32(1.0), F32(1.0), mi._P(dq.ptr), mi._P(kc.ptr), nkv * 2,
+             mi._P(vc.ptr), nkv * 2, mi._P(didx.ptr), int(idx_i64), n_cache)
+    mi.device_sync()
+    xn = rms_norm_ref(x, nw, 1e-6)
+    proj = []
+    for i, n in enumerate(ns):
+        y = _q4_ref(orc, ws[i], xn, n, k)
+        proj.append((y + bs[i]).astype(F32) if bs[i] is not None else y)
+    q_ref = rope_neox_ref(proj[0].reshape(hq, hd), cfg["pos"], hd, 1e6).reshape(-1)
+    k_ref = rope_neox_ref(proj[1].reshape(hkv, hd), cfg["pos"], hd, 1e6).reshape(-1)
+    assert rel_err(dq.download(F32), q_ref) < GEMV_TOL
+    kcache = kc.download(np.uint16).reshape(n_cache, nkv)
+    vcache = vc.download(np.uint16).reshape(n_cache, nkv)
+    for name, cache, ref in (("k", kcache, k_ref), ("v", vcache, proj[2])):
+        got = cache[cfg["row"]].view(np.float16).astype(np.float64)
+        tol = 2 * np.abs(ref.astype(np.float16).astype(np.float64)) * 2.0 ** -10 + 1e-7
+        assert np.all(np.abs(got - ref) <= tol + GEMV_TOL * np.sqrt(np.mean(ref.astype(np.float64) ** 2))), name
+        others = np.delete(cache, cfg["row"], axis=0)
+        assert not others.any(), f"{name} cache rows other than {cfg['row']} were written"
+
+
+def test_q4_qkv_rope_kv_skips_out_of_range_row(gpu):
+    from synth import q4_0_weights
+    mi = gpu
+    rng = np.random.default_rng(8)
+    k, hd, ns = 256, 64, (256, 128, 128)
+    ws = [q4_0_weights(rng, n, k) for n in ns]
+    pw = [_packed_q4(mi, w, n, k) for w, n in zip(ws, ns)]
+    dx = mi.to_device(rng.standard_normal(k).astype(F32))
+    dq = mi.DeviceBuffer(4 * ns[0])
+    kc = mi.DeviceBuffer(8 * 128 * 2).zero()
+    vc = mi.DeviceBuffer(8 * 128 * 2).zero()
+    dpos = mi.to_device(np.array([3], np.int32))
+    didx = mi.to_device(np.array([-1], np.int32))   # before the first cache row
+    mi._call("mi_qkv_rope_kv_q4_0", None, _ptrs(*pw), _i64s(*ns), _ptrs(None, None, None), k, mi._P(dx.ptr), None,
+             F32(1e-6), hd, mi._P(dpos.ptr), F32(1e4), F32(1.0), F32(1.0), mi._P(dq.ptr), mi._P(kc.ptr), 256,
+             mi._P(vc.ptr), 256, mi._P(didx.ptr), 0, 8)
+    mi.device_sync()
+    assert not kc.download(np.uint16).any() and not vc.download(np.uint16).any()

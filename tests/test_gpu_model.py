@@ -81,10 +81,20 @@ def test_qwen2_1p5b_width_two_layers(gpu, orc):
     assert mism == 0
 
 
-def test_fused_graph_matches_unfused(gpu, monkeypatch):
+def test_qwen2_7b_width_two_layers_q4_0(gpu, orc):
+    """Qwen2.5-7B width with W4A16 projections (hidden 3584, 28/4 heads of 128, FFN 18944,
+    vocab 152064), two layers: the fused W4A16 chains at their real shapes."""
+    hp = qs.qwen2_7b(n_layer=2, n_ctx=64)
+    err, rel, spread, mism = _run(gpu, orc, hp, n_prompt=8, n_gen=8, seed=6)
+    assert rel < 2e-3
+    assert mism == 0
+
+
+@pytest.mark.parametrize("wtype", [qs.GGML_TYPE_Q8_0, qs.GGML_TYPE_Q4_0])
+def test_fused_graph_matches_unfused(gpu, monkeypatch, wtype):
     """The backend's fused launches against its node-by-node path on the same graph."""
     mi = gpu
-    hp = qs.qwen2_1p5b(n_layer=2, n_ctx=64)
+    hp = qs.qwen2_1p5b(n_layer=2, n_ctx=64, wtype=wtype)
     tensors, smooth = qs.synth(hp, seed=9, qk_gain=6.0)
     fused = mi.Qwen2Model(hp)
     fused.load(tensors, smooth)
