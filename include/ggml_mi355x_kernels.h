@@ -138,12 +138,13 @@ int mi_mul_mat_q8_0_f32_fused(void *stream, int n_mats, const void *const *w_pac
  * and k (n_dims = head_dim, theta = pos[0] * freq_base^(-2i/head_dim), freq_scale,
  * attn_factor; ext_factor 0) -> q fp32 into q_out[n[0]], k and v converted to fp16 into
  * row kv_idx[0] (int32, or int64 when kv_idx_is_i64) of the caches (SET_ROWS); rows
- * outside [0, n_cache_rows) are not written. */
+ * outside [0, n_cache_rows) are not written.  rope_table: mi_rope_table's output for
+ * pos[0] and the same parameters, or NULL to form the angles in the launch. */
 int mi_qkv_rope_kv_q8_0(void *stream, const void *const *w_packed, const int64_t *n, const float *const *bias,
                         int64_t k, const float *x, const float *norm_w, float eps, const float *inv_s, int rounding,
                         int64_t head_dim, const int32_t *pos, float freq_base, float freq_scale, float attn_factor,
                         float *q_out, void *k_cache, size_t k_row_bytes, void *v_cache, size_t v_row_bytes,
-                        const void *kv_idx, int kv_idx_is_i64, int64_t n_cache_rows);
+                        const void *kv_idx, int kv_idx_is_i64, int64_t n_cache_rows, const float *rope_table);
 /* GLU swiglu(g, u) of one row (k floats) times inv_s, quantized to Q8_0 into xq (the
  * planar layout of mi_act_quant_q8_0 with m = 1): the input side of the down projection */
 int mi_swiglu_quant_q8_0(void *stream, const float *g, const float *u, const float *inv_s, int64_t k, void *xq,
@@ -167,7 +168,7 @@ int mi_gemv_q4_0_f16(void *stream, const void *w_packed, const uint16_t *x_f16, 
 int mi_gemv_q4_0_f16_add(void *stream, const void *w_packed, const uint16_t *x_f16, const float *add, float *y,
                          int64_t n, int64_t k, int64_t m);
 /* W4A16 decode chains, one activation row (m = 1, k <= 4096; without the norm the
- * first one takes k <= 32512), the counterparts of the
+ * first one takes k <= 32256), the counterparts of the
  * Q8_0 chains above (node sequences of the Qwen2 graph builder, per-node dispatch
  * patch:1897-1930 in the reference):
  * [RMS_NORM -> MUL(norm_w)] -> n_mats MUL_MATs sharing src1 (stacked rows) -> ADD add[i]
@@ -186,7 +187,7 @@ int mi_qkv_rope_kv_q4_0(void *stream, const void *const *w_packed, const int64_t
                         int64_t k, const float *x, const float *norm_w, float eps, int64_t head_dim,
                         const int32_t *pos, float freq_base, float freq_scale, float attn_factor, float *q_out,
                         void *k_cache, size_t k_row_bytes, void *v_cache, size_t v_row_bytes, const void *kv_idx,
-                        int kv_idx_is_i64, int64_t n_cache_rows);
+                        int kv_idx_is_i64, int64_t n_cache_rows, const float *rope_table);
 /* the MUL_MAT of the ggml graph (src1 fp32): the activation is converted to fp16 (RNE, as
  * ggml converts src1) into LDS when m*k*2 <= 64 KB (no workspace), otherwise into ws of
  * mi_mul_mat_q4_0_workspace_size(m, k) bytes */
@@ -253,6 +254,12 @@ int mi_mul_bcast(void *stream, const float *a, const float *b, float *d, int64_t
 int mi_rope_neox(void *stream, const float *x, float *y, const int32_t *pos, int64_t ne0, int64_t ne1, int64_t ne2,
                  int64_t n_dims, float freq_base, float freq_scale, float attn_factor, size_t nb1, size_t nb2,
                  size_t ob1, size_t ob2);
+/* the rotation table of mi_rope_neox for one position: table[p] = cos(theta_p) *
+ * attn_factor, table[head_dim/2 + p] = sin(theta_p) * attn_factor (p < head_dim/2).  The
+ * fused q/k/v chains take it instead of forming the angles per launch (the backend
+ * builds it once per graph, as the CPU backend builds its rope cache once per node). */
+int mi_rope_table(void *stream, const int32_t *pos, int64_t head_dim, float freq_base, float freq_scale,
+                  float attn_factor, float *table);
 /* fp16 table rows idx[r] = src row r (ggml SET_ROWS into the KV cache); idx int64 or int32 */
 int mi_set_rows_f16(void *stream, const float *src, const void *idx, int idx_is_i64, uint16_t *dst, int64_t ne0,
                     int64_t nrows, size_t snb1, size_t dnb1, int64_t n_dst_rows);

@@ -84,7 +84,19 @@ struct RopeKV {
     int64_t n_cache_rows;
     int hd, n_q, n_k, n_v;
     float theta_scale, freq_scale, attn_factor;
+    const float *tab;  // [2][hd/2] cos, sin (mi_rope_table), or NULL: formed per launch
 };
+
+// The table entries (cos, sin) of rotation pair p, loaded early: branch-free (without a
+// table the loads read pos[0], and the values are not used).
+__device__ __forceinline__ void rope_tab_prefetch(const RopeKV &R, int p, float &cs, float &sn) {
+    const int half = R.hd / 2;
+    p = min(max(p, 0), half - 1);
+    const float *c = R.tab ? R.tab + p : (const float *)R.pos;
+    const float *s = R.tab ? R.tab + half + p : (const float *)R.pos;
+    cs = *c;
+    sn = *s;
+}
 
 // Row mapping of a workgroup of RPB rows.  A workgroup on the rotated rows (q and k)
 // owns HALF = RPB/2 rotation pairs (i, i + hd/2) of one head, so each pair's two
@@ -111,7 +123,7 @@ __device__ __forceinline__ int rope_kv_row(const RopeKV &R, int b, int t, RopeKV
 // has synchronised after writing them).
 template <int RPB>
 __device__ __forceinline__ void rope_kv_epilogue(const RopeKV &R, const float *y, int b, int tid,
-                                                 const RopeKVPlace &pl) {
+                                                 const RopeKVPlace &pl, float tab_cs, float tab_sn) {
     constexpr int HALF = RPB / 2;
     const int n_rope = R.n_q + R.n_k;
     const int64_t ci = R.kv_idx_i64 ? ((const int64_t *)R.kv_idx)[0] : (int64_t)((const int32_t *)R.kv_idx)[0];
@@ -119,11 +131,14 @@ __device__ __forceinline__ void rope_kv_epilogue(const RopeKV &R, const float *y
     if (pl.rope) {
         if (tid < HALF) {
             const int p = pl.chunk * HALF + tid;  // rotation pair index < hd/2
-            float theta = (float)R.pos[0];
-            for (int i = 0; i < p; i++) theta *= R.theta_scale;
-            const float th = R.freq_scale * theta;
-            const float cs = cosf(th) * R.attn_factor;
-            const float sn = sinf(th) * R.attn_factor;
+            float cs = tab_cs, sn = tab_sn;
+            if (!R.tab) {
+                float theta = (float)R.pos[0];
+                for (int i = 0; i < p; i++) theta *= R.theta_scale;
+                const float th = R.freq_scale * theta;
+                cs = cosf(th) * R.attn_factor;
+                sn = sinf(th) * R.attn_factor;
+            }
             const float x0 = y[tid], x1 = y[tid + HALF];
             const float y0 = mul_sub_mul_rn(x0, cs, x1, sn);
             const float y1 = mul_add_mul_rn(x0, sn, x1, cs);

@@ -353,6 +353,72 @@ __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, c
     if (tid == 0) __hip_atomic_store(&counters[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Last-arrival merge for the MFMA kernel, without an L2 write-back: every workgroup
+// writes its partial record with agent-scope atomic stores (written through to the
+// device coherence point), waits for them, then counts its arrival; the workgroup that
+// arrives last reads all records with agent-scope atomic loads and merges them.  The
+// counter goes back to zero for the next launch.
+__device__ __forceinline__ void st_coherent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int D, int GQ>
+__device__ __forceinline__ void fa_merge_last(const float *part, float *out, unsigned *counter, int kvh, int n_splits,
+                                              int tid) {
+    constexpr int PS = part_stride<D>();
+    __shared__ int s_last;
+    __shared__ float s_cm[GQ][kFusedMaxSplits];
+    __shared__ float s_cl[GQ][kFusedMaxSplits];
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);  // this workgroup's record stores are complete
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == (unsigned)(n_splits - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (tid < GQ * n_splits) {
+        const int h = tid / n_splits, sp = tid % n_splits;
+        const float *rec = part + ((size_t)(kvh * GQ + h) * n_splits + sp) * PS;
+        s_cm[h][sp] = ld_coherent(rec + D);
+        s_cl[h][sp] = ld_coherent(rec + D + 1);
+    }
+    __syncthreads();
+    constexpr int OPT = (GQ * D + 255) / 256;
+    float ov[OPT][kFusedMaxSplits];
+#pragma unroll
+    for (int oi = 0; oi < OPT; oi++) {
+        const int idx = min(tid + oi * 256, GQ * D - 1);
+        const float *ph = part + (size_t)(kvh * GQ + idx / D) * n_splits * PS + idx % D;
+#pragma unroll
+        for (int sp = 0; sp < kFusedMaxSplits; sp++) ov[oi][sp] = ld_coherent(ph + (size_t)min(sp, n_splits - 1) * PS);
+    }
+#pragma unroll
+    for (int oi = 0; oi < OPT; oi++) {
+        const int idx = tid + oi * 256;
+        if (idx >= GQ * D) break;
+        const int h = idx / D;
+        float M = -INFINITY;
+        for (int sp = 0; sp < n_splits; sp++) M = fmaxf(M, s_cm[h][sp]);
+        float L = 0.0f, acc = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int sp = 0; sp < kFusedMaxSplits; sp++) {
+                const float ms = sp < n_splits ? s_cm[h][sp] : -INFINITY;
+                const float e = ms == -INFINITY ? 0.0f : fexp2(ms - M);
+                L += (sp < n_splits ? s_cl[h][sp] : 0.0f) * e;
+                acc += ov[oi][sp] * e;
+            }
+        }
+        out[(size_t)(kvh * GQ + h) * D + idx % D] = L == 0.0f ? 0.0f : acc / L;
+    }
+    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---------------------------------------------------------------- MFMA flash-decoding
 //
 // One workgroup per (split, kv head); each of its 4 waves walks its own run of
@@ -400,7 +466,7 @@ __global__ __launch_bounds__(256) void k_fa_mfma(const float *__restrict__ q, co
                                                  const int32_t *__restrict__ kv_len_p, int n_kv, size_t k_nb1,
                                                  size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, int chunk,
                                                  int n_splits, float *__restrict__ part, float *__restrict__ out,
-                                                 const FaSeq sq) {
+                                                 unsigned *__restrict__ counters, const FaSeq sq) {
     {
         const int seq = blockIdx.z;
         q += (size_t)seq * sq.q;
@@ -410,6 +476,7 @@ __global__ __launch_bounds__(256) void k_fa_mfma(const float *__restrict__ q, co
         if (kv_len_p) kv_len_p += seq;
         out += (size_t)seq * sq.out;
         part += (size_t)seq * gridDim.y * GQ * n_splits * part_stride<D>();
+        if (counters) counters += (size_t)seq * gridDim.y;
     }
     constexpr int KS = D / 16;    // k-steps of the score product
     constexpr int KW = D / 8;     // K dwords per lane per block (D/4 halves)
@@ -567,6 +634,13 @@ __global__ __launch_bounds__(256) void k_fa_mfma(const float *__restrict__ q, co
         const int qh_idx = kvh * GQ + h;
         if (n_splits == 1) {
             out[(size_t)qh_idx * D + dd] = L == 0.0f ? 0.0f : acc / L;
+        } else if (counters) {
+            float *rec = part + ((size_t)qh_idx * n_splits + split) * PS;
+            st_coherent(rec + dd, acc);
+            if (dd == 0) {
+                st_coherent(rec + D, M);
+                st_coherent(rec + D + 1, L);
+            }
         } else {
             float *rec = part + ((size_t)qh_idx * n_splits + split) * PS;
             rec[dd] = acc;
@@ -576,6 +650,7 @@ __global__ __launch_bounds__(256) void k_fa_mfma(const float *__restrict__ q, co
             }
         }
     }
+    if (n_splits > 1 && counters) fa_merge_last<D, GQ>(part, out, counters + kvh, kvh, n_splits, tid);
 }
 
 // Parallel log-sum-exp combine for many splits: grid (q head, D/32 dim slices),
@@ -651,6 +726,18 @@ inline bool fused_combine_enabled() {
     return on;
 }
 
+// MI_FA_MERGE=1: the MFMA kernel merges its splits itself (last arrival) when they fit.
+// Off by default: the serial tail of the last workgroup (arrival atomic, then the
+// partials' loads) measured slower than the separate combine launch (Qwen2.5-1.5B shape,
+// 512 positions: 951 vs 995 tokens/s).
+inline bool mfma_merge_enabled() {
+    static const bool on = [] {
+        const char *e = getenv("MI_FA_MERGE");
+        return e && e[0] == '1';
+    }();
+    return on;
+}
+
 struct FaArgs {
     const float *q;
     const void *k, *v;
@@ -669,10 +756,11 @@ int launch_split_m(hipStream_t st, const FaArgs &a, const FaPlan &p) {
     const dim3 grid((unsigned)p.n_splits, (unsigned)a.n_kv_heads, (unsigned)a.n_seq);
     const uint8_t *kb = (const uint8_t *)a.k, *vb = (const uint8_t *)a.v;
     if (p.mfma) {
+        const bool merged = p.n_splits <= kFusedMaxSplits && a.counters && mfma_merge_enabled();
 #define MI_FA_NBW(NB)                                                                                          \
     hipLaunchKernelGGL((k_fa_mfma<D, GQ, MASK, NB>), grid, dim3(256), 0, st, a.q, kb, vb, a.mask, a.kv_len,      \
                        (int)a.n_kv, a.k_nb1, a.k_nb2, a.v_nb1, a.v_nb2, a.scale, p.chunk, p.n_splits, a.part, a.out, \
-                       a.sq)
+                       merged ? a.counters : nullptr, a.sq)
         switch (p.nbw) {
             case 1: MI_FA_NBW(1); break;
             case 2: MI_FA_NBW(2); break;
@@ -681,6 +769,7 @@ int launch_split_m(hipStream_t st, const FaArgs &a, const FaPlan &p) {
         }
 #undef MI_FA_NBW
         MI_CHECK_LAUNCH("k_fa_mfma");
+        if (merged) return MI_OK;
     } else {
         const bool fused = p.n_splits <= kFusedMaxSplits && fused_combine_enabled();
 #define MI_FA_KT(KT)                                                                                           \

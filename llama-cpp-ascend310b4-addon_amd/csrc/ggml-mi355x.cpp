@@ -152,6 +152,15 @@ struct BackendCtx {
     size_t scratch_size = 0;
     void *fa_ws = nullptr;
     size_t fa_ws_size = 0;
+    // the rotation table of the current graph's position (built by its first fused q/k/v
+    // chain, read by every layer's)
+    float *rope_tab = nullptr;  // [2][512]
+    struct {
+        const void *pos = nullptr;
+        int64_t hd = 0;
+        float freq_base = 0, freq_scale = 0, attn_factor = 0;
+        bool valid = false;
+    } rope_key;
     // captured replay of the last graph
     hipGraphExec_t gexec = nullptr;
     std::vector<uint64_t> signature;
@@ -455,6 +464,7 @@ void ensure_buffers(BackendCtx *ctx, ggml_cgraph *g) {
         MI_HIP_CHECK(hipMalloc(&ctx->scratch, ctx->scratch_size));
         ctx->signature.clear();
     }
+    if (!ctx->rope_tab) MI_HIP_CHECK(hipMalloc(&ctx->rope_tab, 2 * 512 * sizeof(float)));
     if (need_fa > ctx->fa_ws_size) {
         if (ctx->fa_ws) MI_HIP_CHECK(hipFree(ctx->fa_ws));
         ctx->fa_ws_size = GGML_PAD(need_fa, 1 << 20);
@@ -636,6 +646,26 @@ bool rms_mul_head(ggml_cgraph *g, int i, const Consumers &C, int &j, const ggml_
     return true;
 }
 
+// the rotation table for (pos tensor, head_dim, rope parameters), built on the stream at
+// its first use in this graph run
+const float *rope_table_for(BackendCtx *ctx, const void *pos, int64_t hd, float freq_base, float freq_scale,
+                            float attn_factor) {
+    if (!ctx->rope_tab || hd > 1024) return nullptr;
+    auto &k = ctx->rope_key;
+    if (k.valid && k.pos == pos && k.hd == hd && k.freq_base == freq_base && k.freq_scale == freq_scale &&
+        k.attn_factor == attn_factor)
+        return ctx->rope_tab;
+    MI_K_CHECK(mi_rope_table(ctx->stream, (const int32_t *)pos, hd, freq_base, freq_scale, attn_factor,
+                             ctx->rope_tab));
+    k.pos = pos;
+    k.hd = hd;
+    k.freq_base = freq_base;
+    k.freq_scale = freq_scale;
+    k.attn_factor = attn_factor;
+    k.valid = true;
+    return ctx->rope_tab;
+}
+
 int try_fuse_attn_in(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
     const int nn = ggml_graph_n_nodes(g);
     int j;
@@ -712,18 +742,20 @@ int try_fuse_attn_in(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C)
     memcpy(&freq_scale, (const float *)r->op_params + 6, sizeof(float));
     memcpy(&attn_factor, (const float *)r->op_params + 8, sizeof(float));
     const ggml_tensor *idx = sr[0]->src[1];
+    const float *tab = rope_table_for(ctx, r->src[1]->data, hd, freq_base, freq_scale, attn_factor);
     if (wt == GGML_TYPE_Q4_0) {
         MI_K_CHECK(mi_qkv_rope_kv_q4_0(ctx->stream, w, n, bp, x->ne[0], (const float *)x->data, (const float *)nw->data,
                                        eps, hd, (const int32_t *)r->src[1]->data, freq_base, freq_scale, attn_factor,
                                        (float *)rope[0]->data, sr[0]->data, sr[0]->nb[1], sr[1]->data, sr[1]->nb[1],
-                                       idx->data, idx->type == GGML_TYPE_I64, std::min(sr[0]->ne[1], sr[1]->ne[1])));
+                                       idx->data, idx->type == GGML_TYPE_I64, std::min(sr[0]->ne[1], sr[1]->ne[1]),
+                                       tab));
         return j + 1 - i;
     }
     MI_K_CHECK(mi_qkv_rope_kv_q8_0(ctx->stream, w, n, bp, x->ne[0], (const float *)x->data, (const float *)nw->data, eps,
                                    inv_s_of(mm[0]->src[0]), q8_rounding(), hd, (const int32_t *)r->src[1]->data,
                                    freq_base, freq_scale, attn_factor, (float *)rope[0]->data, sr[0]->data,
                                    sr[0]->nb[1], sr[1]->data, sr[1]->nb[1], idx->data, idx->type == GGML_TYPE_I64,
-                                   std::min(sr[0]->ne[1], sr[1]->ne[1])));
+                                   std::min(sr[0]->ne[1], sr[1]->ne[1]), tab));
     return j + 1 - i;
 }
 
@@ -747,7 +779,7 @@ int try_fuse_gate_up_down_q4(BackendCtx *ctx, ggml_cgraph *g, int i, const Consu
     const ggml_tensor *down = ggml_graph_node(g, jd);
     const int64_t nf = mm[0]->ne[0];
     if (!gemv_node(down, GGML_TYPE_Q4_0) || down->src[1] != glu || !only_consumed_by(C, glu, {down}) ||
-        down->src[0]->ne[0] != nf || nf / 32 > 1016 || ctx->scratch_size < (size_t)nf * 2)
+        down->src[0]->ne[0] != nf || nf / 32 > 1008 || ctx->scratch_size < (size_t)nf * 2)
         return 0;
     const ggml_tensor *vec = nullptr;
     const ggml_tensor *ad = matmul_add_tail(g, jd, down, C, vec);
@@ -829,7 +861,7 @@ int try_fuse_matmul_add(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers 
     const ggml_type wt = gemv_type(mm);
     if (wt == GGML_TYPE_COUNT) return 0;
     const int64_t k = mm->src[0]->ne[0];
-    if (wt == GGML_TYPE_Q4_0 && k / 32 > 1016) return 0;
+    if (wt == GGML_TYPE_Q4_0 && k / 32 > 1008) return 0;
     const ggml_tensor *vec = nullptr;
     const ggml_tensor *ad = matmul_add_tail(g, i, mm, C, vec);
     if (!ad) return 0;
@@ -989,6 +1021,7 @@ int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
 void run_graph_nodes(BackendCtx *ctx, ggml_cgraph *g) {
     const int nn = ggml_graph_n_nodes(g);
     const Consumers C = consumers_of(g);
+    ctx->rope_key.valid = false;  // the position input may have changed since the last run
     for (int i = 0; i < nn;) {
         ggml_tensor *node = ggml_graph_node(g, i);
         if (is_noop(node)) {
@@ -1046,6 +1079,7 @@ void backend_free(ggml_backend_t backend) {
     if (ctx->gexec) (void)hipGraphExecDestroy(ctx->gexec);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->fa_ws) (void)hipFree(ctx->fa_ws);
+    if (ctx->rope_tab) (void)hipFree(ctx->rope_tab);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     delete backend;

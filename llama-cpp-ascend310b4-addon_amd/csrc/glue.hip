@@ -108,6 +108,29 @@ __global__ void k_rope_neox(const float *__restrict__ x, float *__restrict__ y, 
     for (int j = n_dims + i; j < ne0; j += blockDim.x) ((float *)yr)[j] = ((const float *)xr)[j];
 }
 
+// The neox rotation table of one position: tab[p] = cos(theta_p) * attn_factor,
+// tab[n_pairs + p] = sin(theta_p) * attn_factor, theta_p = freq_scale * (pos * theta_scale^p)
+// with the power formed by p repeated multiplications (the CPU rope cache's order): one
+// thread walks the chain into LDS, then every thread converts its pairs.
+__global__ __launch_bounds__(256) void k_rope_table(const int32_t *__restrict__ pos, float *__restrict__ tab,
+                                                    int n_pairs, float theta_scale, float freq_scale,
+                                                    float attn_factor) {
+    __shared__ float s_theta[512];
+    if (threadIdx.x == 0) {
+        float t = (float)pos[0];
+        for (int p = 0; p < n_pairs; p++) {
+            s_theta[p] = t;
+            t *= theta_scale;
+        }
+    }
+    __syncthreads();
+    for (int p = threadIdx.x; p < n_pairs; p += 256) {
+        const float th = freq_scale * s_theta[p];
+        tab[p] = cosf(th) * attn_factor;
+        tab[n_pairs + p] = sinf(th) * attn_factor;
+    }
+}
+
 // dst rows idx[r] (fp16 table, row stride dnb1 bytes) = fp16(src row r)
 template <typename IDX>
 __global__ void k_set_rows_f16(const float *__restrict__ src, const IDX *__restrict__ idx, uint16_t *__restrict__ dst,
@@ -256,6 +279,16 @@ int mi_rope_neox(void *stream, const float *x, float *y, const int32_t *pos, int
     hipLaunchKernelGGL(k_rope_neox, dim3((unsigned)ne1, (unsigned)ne2), dim3(threads), 0, (hipStream_t)stream, x, y,
                        pos, (int)ne0, (int)ne1, (int)n_dims, theta_scale, freq_scale, attn_factor, nb1, nb2, ob1, ob2);
     MI_CHECK_LAUNCH("k_rope_neox");
+    return MI_OK;
+}
+
+int mi_rope_table(void *stream, const int32_t *pos, int64_t head_dim, float freq_base, float freq_scale,
+                  float attn_factor, float *table) {
+    MI_CHECK_ARG(pos && table && head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 1024, "rope_table: bad arguments");
+    const float theta_scale = powf(freq_base, -2.0f / (float)head_dim);
+    hipLaunchKernelGGL(k_rope_table, dim3(1), dim3(256), 0, (hipStream_t)stream, pos, table, (int)(head_dim / 2),
+                       theta_scale, freq_scale, attn_factor);
+    MI_CHECK_LAUNCH("k_rope_table");
     return MI_OK;
 }
 

@@ -461,6 +461,7 @@ template <int KB>
 struct XrRows {
     int4 w[2][KB];
     uint32_t d[2][KB];
+    float a[2];  // the rows' add / bias values (read with the weights, used in the epilogue)
 };
 
 // global-address-space accesses from integer addresses (the picked pointers are
@@ -489,6 +490,9 @@ __device__ __forceinline__ void xr_load(XrRows<KB> &W, const Q4Set &S, int r0, i
         const uint64_t base = (uint64_t)(r - q4set_row_start(S, mi)) * (uint64_t)nb;
         const uint64_t qs = (uint64_t)Q4SET_PICK(S, qs, mi) + base * 16;
         const uint64_t dp = (uint64_t)Q4SET_PICK(S, d, mi) + base * 2;
+        const uint64_t ap = (uint64_t)Q4SET_PICK(S, add, mi);
+        // without an add vector the load reads the row's first weight bytes (unused)
+        W.a[rr] = ldg_f32(ap ? ap + 4 * (uint64_t)(r - q4set_row_start(S, mi)) : qs);
 #pragma unroll
         for (int i = 0; i < KB; i++) {
             const uint64_t b = dummy ? 0 : (uint64_t)bidx[i];
@@ -514,8 +518,8 @@ __device__ __forceinline__ void xr_dot(const XrRows<KB> &W, const uint32_t (*xr)
     }
 }
 
-struct XrRope {  // per-lane rotation of pair index p = lane (p < hd/2 <= 64)
-    float cs, sn;
+struct XrRope {
+    const float *tab;  // LDS [2][64]: cos and sin of rotation pair p < hd/2 <= 64
     int64_t ci;
     bool ci_ok;
 };
@@ -524,17 +528,18 @@ struct XrRope {  // per-lane rotation of pair index p = lane (p < hd/2 <= 64)
 // lane of that wave calls it, for the shuffles)
 template <int UM>
 __device__ __forceinline__ void xr_store(const Q4Set &S, const RopeKV &R, const XrRope &rp, uint16_t *h_out, int u,
-                                         int r0, int r1, bool ok1, float s0, float s1, int lane) {
+                                         int r0, int r1, bool ok1, float s0, float s1, float av0, float av1,
+                                         int lane) {
     const int m0 = q4set_index(S, r0), m1 = q4set_index(S, r1);
     const int l0 = r0 - q4set_row_start(S, m0), l1 = r1 - q4set_row_start(S, m1);
-    const uint64_t a0 = (uint64_t)Q4SET_PICK(S, add, m0);
-    const uint64_t a1 = (uint64_t)Q4SET_PICK(S, add, m1);
+    const bool a0 = Q4SET_PICK(S, add, m0) != nullptr;
+    const bool a1 = Q4SET_PICK(S, add, m1) != nullptr;
     if constexpr (UM == XR_ROPE) {
         const int half = R.hd / 2, n_pairs = (R.n_q + R.n_k) / 2;
-        const float cs = __shfl(rp.cs, u % half, 64), sn = __shfl(rp.sn, u % half, 64);
         if (lane != 0) return;
-        const float x0 = a0 ? s0 + ldg_f32(a0 + 4 * (uint64_t)l0) : s0;
-        const float x1 = a1 ? s1 + ldg_f32(a1 + 4 * (uint64_t)l1) : s1;
+        const float cs = rp.tab[u % half], sn = rp.tab[64 + u % half];
+        const float x0 = a0 ? s0 + av0 : s0;
+        const float x1 = a1 ? s1 + av1 : s1;
         if (u < n_pairs) {
             const float y0 = mul_sub_mul_rn(x0, cs, x1, sn);
             const float y1 = mul_add_mul_rn(x0, sn, x1, cs);
@@ -553,21 +558,22 @@ __device__ __forceinline__ void xr_store(const Q4Set &S, const RopeKV &R, const 
         }
     } else if constexpr (UM == XR_GLU) {
         if (lane != 0) return;
-        const float g = a0 ? s0 + ldg_f32(a0 + 4 * (uint64_t)l0) : s0;
-        const float v = a1 ? s1 + ldg_f32(a1 + 4 * (uint64_t)l1) : s1;
+        const float g = a0 ? s0 + av0 : s0;
+        const float v = a1 ? s1 + av1 : s1;
         h_out[u] = f2h((g / (1.0f + expf(-g))) * v);
     } else {
         if (lane != 0) return;
         const uint64_t y0 = (uint64_t)Q4SET_PICK(S, y, m0), y1 = (uint64_t)Q4SET_PICK(S, y, m1);
-        stg_f32(y0 + 4 * (uint64_t)l0, a0 ? s0 + ldg_f32(a0 + 4 * (uint64_t)l0) : s0);
-        if (ok1) stg_f32(y1 + 4 * (uint64_t)l1, a1 ? s1 + ldg_f32(a1 + 4 * (uint64_t)l1) : s1);
+        stg_f32(y0 + 4 * (uint64_t)l0, a0 ? s0 + av0 : s0);
+        if (ok1) stg_f32(y1 + 4 * (uint64_t)l1, a1 ? s1 + av1 : s1);
     }
 }
 
 // KB blocks per lane and WPR waves per row pair (k <= 64*32*WPR*KB); XF32: the
 // activation is fp32 (rounded to fp16 RNE, as ggml converts src1), else fp16; XN > 0:
-// RMSNorm with norm_w first (fp32 activation of k <= 1024*XN).
-template <int KB, int WPR, bool XF32, int XN, int UM>
+// the fp32 activation (k <= 1024*XN) is loaded into registers before the weights, so
+// that staging it (with the RMSNorm by norm_w when NORM) waits only for those loads.
+template <int KB, int WPR, bool XF32, int XN, bool NORM, int UM>
 __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void *__restrict__ xin,
                                                       const float *__restrict__ norm_w, float eps, int nb,
                                                       int n_units, int n_rows, const RopeKV R,
@@ -578,6 +584,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
     uint16_t *s_x = (uint16_t *)smem;
     float *s_red = (float *)(smem + (size_t)k * 2);  // [2][4][2]
     double *s_nred = (double *)(s_red + 16);        // [4]
+    float *s_rope = (float *)(s_nred + 4);          // [2][64]: cos, sin of rotation pair p
     const int tid = threadIdx.x, lane = tid & 63;
     // the unit, row and matrix indices are wave-uniform: scalar registers and scalar selects
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -595,17 +602,35 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
     const int stride = gridDim.x * PG;
     const int u_first = blockIdx.x * PG + pg;
 
+    const int k4 = k / 4;
+    // The rotation's position and cache row, then a short activation, are loaded before
+    // the weights: loads retire in order, so their consumers wait only for them.  The
+    // index z is an opaque per-lane zero: the values stay in vector registers (a uniform
+    // load would be moved to scalar registers at once, waiting for it there).
+    int z = 0;
+    asm volatile("" : "+v"(z));
+    int pos0 = 0;
+    int32_t ci_lo = 0, ci_hi = 0;
+    float tab_cs = 0.0f, tab_sn = 0.0f;
+    if constexpr (UM == XR_ROPE) {
+        // branch-free: the high word's load reads word 0 again for an int32 index
+        pos0 = R.pos[z];
+        ci_lo = ((const int32_t *)R.kv_idx)[z];
+        ci_hi = ((const int32_t *)R.kv_idx)[z + (R.kv_idx_i64 ? 1 : 0)];
+        rope_tab_prefetch(R, lane + z, tab_cs, tab_sn);
+    }
+    XStage<(XN > 0 ? XN : 1), NORM> st;
+    if constexpr (XN > 0) xstage_load(st, (const float *)xin, norm_w, nullptr, k4, tid);
+
     // the first unit's weights go out before the activation is staged
     XrRows<KB> wa, wb;
     int r0, r1;
     bool ok1;
     xr_rows<UM>(S, R, min(u_first, n_units - 1), n_rows, r0, r1, ok1);
     xr_load<KB>(wa, S, r0, r1, bidx, false, nb);
+    __builtin_amdgcn_sched_barrier(0);  // nothing that waits on a load moves above the weight loads
 
-    const int k4 = k / 4;
     if constexpr (XN > 0) {
-        XStage<XN, true> st;
-        xstage_load(st, (const float *)xin, norm_w, nullptr, k4, tid);
         const float scale = xstage_scale(st, k4, eps, s_nred, tid);
 #pragma unroll
         for (int t = 0; t < XN; t++) {
@@ -627,13 +652,25 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
 
     XrRope rp;
     if constexpr (UM == XR_ROPE) {
-        float theta = (float)R.pos[0];
-        for (int i = 0; i < lane && i < R.hd / 2; i++) theta *= R.theta_scale;
-        const float th = R.freq_scale * theta;
-        rp.cs = cosf(th) * R.attn_factor;
-        rp.sn = sinf(th) * R.attn_factor;
-        rp.ci = R.kv_idx_i64 ? ((const int64_t *)R.kv_idx)[0] : (int64_t)((const int32_t *)R.kv_idx)[0];
-        rp.ci_ok = rp.ci >= 0 && rp.ci < R.n_cache_rows;
+        // the rotation table, once per workgroup (wave 0, lane p): theta_p by p repeated
+        // multiplications, as the CPU rope cache forms it
+        if (wave == 0) {
+            if (R.tab) {
+                s_rope[lane] = tab_cs;
+                s_rope[64 + lane] = tab_sn;
+            } else {
+                float theta = (float)pos0;
+                for (int i = 0; i < lane && i < R.hd / 2; i++) theta *= R.theta_scale;
+                const float th = R.freq_scale * theta;
+                s_rope[lane] = cosf(th) * R.attn_factor;
+                s_rope[64 + lane] = sinf(th) * R.attn_factor;
+            }
+        }
+        const int64_t ci =
+            R.kv_idx_i64 ? (int64_t)(((uint64_t)(uint32_t)ci_hi << 32) | (uint32_t)ci_lo) : (int64_t)ci_lo;
+        rp.tab = s_rope;
+        rp.ci = ci;
+        rp.ci_ok = ci >= 0 && ci < R.n_cache_rows;
     }
     __syncthreads();
 
@@ -669,7 +706,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
             xr_dot<KB>(wa, xr, bval, s0, s1, magic);
             s0 = group_sum<64>(s0);
             s1 = group_sum<64>(s1);
-            xr_store<UM>(S, R, rp, h_out, u, r0, r1, ok1, s0, s1, lane);
+            xr_store<UM>(S, R, rp, h_out, u, r0, r1, ok1, s0, s1, wa.a[0], wa.a[1], lane);
             if (!more_b) break;
             u = ub;
             r0 = q0; r1 = q1; ok1 = qok;
@@ -682,7 +719,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
             xr_dot<KB>(wb, xr, bval, s0, s1, magic);
             s0 = group_sum<64>(s0);
             s1 = group_sum<64>(s1);
-            xr_store<UM>(S, R, rp, h_out, u, r0, r1, ok1, s0, s1, lane);
+            xr_store<UM>(S, R, rp, h_out, u, r0, r1, ok1, s0, s1, wb.a[0], wb.a[1], lane);
             if (!more_a) break;
             u = ua;
             r0 = q0; r1 = q1; ok1 = qok;
@@ -692,7 +729,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
         // the end are computed on a clamped unit and not stored), partial sums meet in LDS
         int base = blockIdx.x * PG;
         int par = 0;
-        auto finish = [&](int u, int a0, int a1, bool aok, float s0, float s1) {
+        auto finish = [&](int u, int a0, int a1, bool aok, float s0, float s1, float av0, float av1) {
             s0 = group_sum<64>(s0);
             s1 = group_sum<64>(s1);
             if (lane == 0) {
@@ -707,7 +744,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
                     t0 += s_red[(par * 4 + pg * WPR + w) * 2 + 0];
                     t1 += s_red[(par * 4 + pg * WPR + w) * 2 + 1];
                 }
-                xr_store<UM>(S, R, rp, h_out, u, a0, a1, aok, t0, t1, lane);
+                xr_store<UM>(S, R, rp, h_out, u, a0, a1, aok, t0, t1, av0, av1, lane);
             }
             par ^= 1;
         };
@@ -723,7 +760,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
             __builtin_amdgcn_sched_barrier(0);  // the next pair's loads issue before this pair's math
             float s0, s1;
             xr_dot<KB>(wa, xr, bval, s0, s1, magic);
-            finish(u, r0, r1, ok1, s0, s1);
+            finish(u, r0, r1, ok1, s0, s1, wa.a[0], wa.a[1]);
             if (!more_b) break;
             base = nbase;
             r0 = q0; r1 = q1; ok1 = qok;
@@ -735,7 +772,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
             xr_load<KB>(wa, S, q0, q1, bidx, !more_a, nb);
             __builtin_amdgcn_sched_barrier(0);  // the next pair's loads issue before this pair's math
             xr_dot<KB>(wb, xr, bval, s0, s1, magic);
-            finish(u2, r0, r1, ok1, s0, s1);
+            finish(u2, r0, r1, ok1, s0, s1, wb.a[0], wb.a[1]);
             if (!more_a) break;
             base = nbase2;
             r0 = q0; r1 = q1; ok1 = qok;
@@ -846,12 +883,12 @@ inline bool xr_shape(int64_t nb, XrShape &s) {
     else if (nb <= 384) s = {3, 2};
     else if (nb <= 512) s = {2, 4};
     else if (nb <= 768) s = {3, 4};
-    else if (nb <= 1016) s = {4, 4};  // the fp16 row and the reduction slots within 64 KB of LDS
+    else if (nb <= 1008) s = {4, 4};  // the fp16 row and the reduction slots within 64 KB of LDS
     else return false;
     return true;
 }
 
-inline size_t xr_smem(int64_t k) { return (size_t)k * 2 + 16 * sizeof(float) + 4 * sizeof(double); }
+inline size_t xr_smem(int64_t k) { return (size_t)k * 2 + 16 * sizeof(float) + 4 * sizeof(double) + 128 * sizeof(float); }
 
 // workgroups resident at once on the current device for this kernel and LDS size
 int xr_resident(const void *fn, size_t smem) {
@@ -876,12 +913,12 @@ int xr_resident(const void *fn, size_t smem) {
     return r;
 }
 
-template <int KB, int WPR, bool XF32, int XN, int UM>
+template <int KB, int WPR, bool XF32, int XN, bool NORM, int UM>
 int launch_xr(hipStream_t st, const Q4Set &S, const void *x, const float *norm_w, float eps, int nb, int n_units,
               int n_rows, const RopeKV &R, uint16_t *h) {
     constexpr int PG = 4 / WPR;
     const size_t smem = xr_smem((int64_t)nb * QK);
-    auto fn = k_gemv_q4_0_xr<KB, WPR, XF32, XN, UM>;
+    auto fn = k_gemv_q4_0_xr<KB, WPR, XF32, XN, NORM, UM>;
     const int want = (n_units + PG - 1) / PG;
     const int grid = std::min(want, xr_resident((const void *)fn, smem));
     hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), smem, st, S, x, norm_w, eps, nb, n_units, n_rows, R, h);
@@ -893,8 +930,9 @@ int launch_xr(hipStream_t st, const Q4Set &S, const void *x, const float *norm_w
 template <bool XF32, int UM>
 int launch_xr_any(hipStream_t st, const XrShape &sh, const Q4Set &S, const void *x, int nb, int n_units, int n_rows,
                   const RopeKV &R, uint16_t *h) {
-#define MI_XR_CASE(KB, WPR) \
-    if (sh.kb == KB && sh.wpr == WPR) return launch_xr<KB, WPR, XF32, 0, UM>(st, S, x, nullptr, 0.0f, nb, n_units, n_rows, R, h);
+#define MI_XR_CASE(KB, WPR)           \
+    if (sh.kb == KB && sh.wpr == WPR) \
+        return launch_xr<KB, WPR, XF32, 0, false, UM>(st, S, x, nullptr, 0.0f, nb, n_units, n_rows, R, h);
     MI_XR_CASE(1, 1) MI_XR_CASE(2, 1) MI_XR_CASE(2, 2) MI_XR_CASE(3, 2) MI_XR_CASE(2, 4) MI_XR_CASE(3, 4)
     MI_XR_CASE(4, 4)
 #undef MI_XR_CASE
@@ -902,23 +940,27 @@ int launch_xr_any(hipStream_t st, const XrShape &sh, const Q4Set &S, const void 
     return MI_ERR_UNSUPPORTED;
 }
 
-// short rows (k <= 4096: one wave per row pair) with the optional RMSNorm
+// short fp32 rows (k <= 4096: one wave per row pair, the activation through registers)
+// with the optional RMSNorm
+template <int XN, bool NORM, int UM>
+int launch_xr_short_xn(hipStream_t st, const Q4Set &S, const void *x, const float *norm_w, float eps, int nb,
+                       int n_units, int n_rows, const RopeKV &R, uint16_t *h) {
+    if (nb <= 64) return launch_xr<1, 1, true, XN, NORM, UM>(st, S, x, norm_w, eps, nb, n_units, n_rows, R, h);
+    return launch_xr<2, 1, true, XN, NORM, UM>(st, S, x, norm_w, eps, nb, n_units, n_rows, R, h);
+}
+
 template <int UM>
 int launch_xr_short(hipStream_t st, const Q4Set &S, const void *x, const float *norm_w, float eps, int nb,
                     int n_units, int n_rows, const RopeKV &R, uint16_t *h) {
     const int k4 = nb * QK / 4;
-    if (!norm_w) {
-        if (nb <= 64) return launch_xr<1, 1, true, 0, UM>(st, S, x, nullptr, eps, nb, n_units, n_rows, R, h);
-        return launch_xr<2, 1, true, 0, UM>(st, S, x, nullptr, eps, nb, n_units, n_rows, R, h);
-    }
-#define MI_XR_CASE(XN)                                                                                         \
-    if (k4 <= 256 * XN) {                                                                                      \
-        if (nb <= 64) return launch_xr<1, 1, true, XN, UM>(st, S, x, norm_w, eps, nb, n_units, n_rows, R, h); \
-        return launch_xr<2, 1, true, XN, UM>(st, S, x, norm_w, eps, nb, n_units, n_rows, R, h);               \
+#define MI_XR_CASE(XN)                                                                                    \
+    if (k4 <= 256 * XN) {                                                                                 \
+        if (norm_w) return launch_xr_short_xn<XN, true, UM>(st, S, x, norm_w, eps, nb, n_units, n_rows, R, h); \
+        return launch_xr_short_xn<XN, false, UM>(st, S, x, nullptr, eps, nb, n_units, n_rows, R, h);      \
     }
     MI_XR_CASE(1) MI_XR_CASE(2) MI_XR_CASE(4)
 #undef MI_XR_CASE
-    set_error("gemv_q4_0: k=%d too long for the fused norm", nb * QK);
+    set_error("gemv_q4_0: k=%d too long for the one-wave kernel", nb * QK);
     return MI_ERR_UNSUPPORTED;
 }
 
@@ -964,6 +1006,8 @@ int launch_xr_gemv(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, co
     if (int r = make_q4set(S, 1, w, nn, ys, as, k, n_total)) return r;
     RopeKV R{};
     const int units = (n_total + 1) / 2;
+    if (xf32 && k <= 4096) return launch_xr_short<XR_PAIRS>(st, S, x, nullptr, 0.0f, (int)(k / QK), units, n_total, R,
+                                                             nullptr);
     if (xf32) return launch_xr_any<true, XR_PAIRS>(st, sh, S, x, (int)(k / QK), units, n_total, R, nullptr);
     return launch_xr_any<false, XR_PAIRS>(st, sh, S, x, (int)(k / QK), units, n_total, R, nullptr);
 }
@@ -979,7 +1023,7 @@ inline bool xr_enabled() {
 int launch_gx(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16, float *y,
               const float *add = nullptr) {
     if (m >= 2 && m <= 16) return launch_mfma<false>(st, base, n, k, m, x16, y, add);
-    if (m == 1 && xr_enabled() && k / QK <= 1016) return launch_xr_gemv(st, base, n, k, x16, false, y, add);
+    if (m == 1 && xr_enabled() && k / QK <= 1008) return launch_xr_gemv(st, base, n, k, x16, false, y, add);
     const bool tall = n >= 2048;
     if (m == 1) return tall ? launch_gx_mr<1, 2>(st, base, n, k, m, x16, y, add)
                             : launch_gx_mr<1, 1>(st, base, n, k, m, x16, y, add);
@@ -1072,7 +1116,7 @@ int mi_mul_mat_q4_0_f32(void *stream, const void *w_packed, const float *x, floa
     MI_CHECK_ARG(mi::aligned(w_packed, 256) && mi::aligned(x, 16), "mul_mat_q4_0_f32: w_packed must be 256-byte, x 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     if (m > 1) return launch_mfma<true>(st, (const uint8_t *)w_packed, n, k, m, x, y, nullptr);
-    if (xr_enabled() && k / QK <= 1016) return launch_xr_gemv(st, (const uint8_t *)w_packed, n, k, x, true, y, nullptr);
+    if (xr_enabled() && k / QK <= 1008) return launch_xr_gemv(st, (const uint8_t *)w_packed, n, k, x, true, y, nullptr);
     const size_t need = mi_mul_mat_q4_0_workspace_size(m, k);
     if (need == 0) return launch_lds(st, (const uint8_t *)w_packed, n, k, m, x, y);
     if (!ws || ws_bytes < need || !mi::aligned(ws, 16)) {
@@ -1088,7 +1132,7 @@ int mi_mul_mat_q4_0_f32_fused(void *stream, int n_mats, const void *const *w_pac
                               const float *norm_w, float eps) {
     MI_CHECK_ARG(w_packed && n && y && x, "mul_mat_q4_0_f32_fused: null pointer");
     if (int r = check_shape("mul_mat_q4_0_f32_fused", 1, k)) return r;
-    MI_CHECK_ARG(k <= (norm_w ? 4096 : 1016 * QK), "mul_mat_q4_0_f32_fused: k=%lld too long", (long long)k);
+    MI_CHECK_ARG(k <= (norm_w ? 4096 : 1008 * QK), "mul_mat_q4_0_f32_fused: k=%lld too long", (long long)k);
     MI_CHECK_ARG(mi::aligned(x, 16) && (!norm_w || mi::aligned(norm_w, 16)),
                  "mul_mat_q4_0_f32_fused: x/norm_w must be 16-byte aligned");
     for (int i = 0; i < n_mats && i < 4; i++) MI_CHECK_ARG(y[i], "mul_mat_q4_0_f32_fused: y[%d] is NULL", i);
@@ -1126,7 +1170,7 @@ int mi_qkv_rope_kv_q4_0(void *stream, const void *const *w_packed, const int64_t
                         int64_t k, const float *x, const float *norm_w, float eps, int64_t head_dim,
                         const int32_t *pos, float freq_base, float freq_scale, float attn_factor, float *q_out,
                         void *k_cache, size_t k_row_bytes, void *v_cache, size_t v_row_bytes, const void *kv_idx,
-                        int kv_idx_is_i64, int64_t n_cache_rows) {
+                        int kv_idx_is_i64, int64_t n_cache_rows, const float *rope_table) {
     MI_CHECK_ARG(w_packed && n && bias && x && pos && q_out && k_cache && v_cache && kv_idx,
                  "qkv_rope_kv_q4_0: null pointer");
     if (int r = check_shape("qkv_rope_kv_q4_0", 1, k)) return r;
@@ -1160,6 +1204,7 @@ int mi_qkv_rope_kv_q4_0(void *stream, const void *const *w_packed, const int64_t
     R.theta_scale = powf(freq_base, -2.0f / (float)head_dim);
     R.freq_scale = freq_scale;
     R.attn_factor = attn_factor;
+    R.tab = rope_table;
     const int units = (R.n_q + R.n_k) / 2 + R.n_v / 2;
     return launch_xr_short<XR_ROPE>((hipStream_t)stream, S, x, norm_w, eps, (int)(k / QK), units, n_total, R,
                                     nullptr);

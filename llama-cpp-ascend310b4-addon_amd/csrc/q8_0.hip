@@ -355,6 +355,8 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0_qkv_rope(const Q8Set S, const
     const int b = blockIdx.x;
     RopeKVPlace pl;
     const int rc = min(rope_kv_row<RPB>(R, b, t, pl), n_total - 1);
+    float tab_cs, tab_sn;
+    rope_tab_prefetch(R, pl.chunk * (RPB / 2) + tid % (RPB / 2), tab_cs, tab_sn);
     const int mi = q8set_index(S, rc);
     const int row = rc - q8set_row_start(S, mi);
     const uint8_t *qlo = Q8SET_PICK(S, qlo, mi);
@@ -376,7 +378,7 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0_qkv_rope(const Q8Set S, const
         L.y[t] = bias ? s + bias[row] : s;
     }
     __syncthreads();
-    rope_kv_epilogue<RPB>(R, L.y, b, tid, pl);
+    rope_kv_epilogue<RPB>(R, L.y, b, tid, pl, tab_cs, tab_sn);
 }
 
 // silu(g) * u (ggml swiglu: silu(x) = x / (1 + expf(-x))), times the SmoothQuant
@@ -771,7 +773,7 @@ int mi_qkv_rope_kv_q8_0(void *stream, const void *const *w_packed, const int64_t
                         int64_t k, const float *x, const float *norm_w, float eps, const float *inv_s, int rounding,
                         int64_t head_dim, const int32_t *pos, float freq_base, float freq_scale, float attn_factor,
                         float *q_out, void *k_cache, size_t k_row_bytes, void *v_cache, size_t v_row_bytes,
-                        const void *kv_idx, int kv_idx_is_i64, int64_t n_cache_rows) {
+                        const void *kv_idx, int kv_idx_is_i64, int64_t n_cache_rows, const float *rope_table) {
     MI_CHECK_ARG(w_packed && n && bias && x && pos && q_out && k_cache && v_cache && kv_idx,
                  "qkv_rope_kv_q8_0: null pointer");
     if (int r = check_shape("qkv_rope_kv_q8_0", 1, k)) return r;
@@ -807,6 +809,7 @@ int mi_qkv_rope_kv_q8_0(void *stream, const void *const *w_packed, const int64_t
     R.theta_scale = powf(freq_base, -2.0f / (float)head_dim);
     R.freq_scale = freq_scale;
     R.attn_factor = attn_factor;
+    R.tab = rope_table;
     hipStream_t st = (hipStream_t)stream;
     int g = pick_g_rows(k / QK, n_total);
     while (g > 16 && head_dim % (256 / g) != 0) g /= 2;  // a workgroup's rows must tile the heads

@@ -103,9 +103,10 @@ _SIGS = {
     "mi_mul_mat_q4_0_f32_fused": (_I, [_P, _I, _P, _P, _P, _P, _I64, _P, _P, _F]),
     "mi_gate_up_swiglu_q4_0": (_I, [_P, _P, _P, _I64, _I64, _P, _P, _F, _P]),
     "mi_qkv_rope_kv_q4_0": (_I, [_P, _P, _P, _P, _I64, _P, _P, _F, _I64, _P, _F, _F, _F, _P, _P, _SZ, _P, _SZ,
-                                 _P, _I, _I64]),
+                                 _P, _I, _I64, _P]),
+    "mi_rope_table": (_I, [_P, _P, _I64, _F, _F, _F, _P]),
     "mi_qkv_rope_kv_q8_0": (_I, [_P, _P, _P, _P, _I64, _P, _P, _F, _P, _I, _I64, _P, _F, _F, _F, _P, _P, _SZ, _P, _SZ,
-                                 _P, _I, _I64]),
+                                 _P, _I, _I64, _P]),
     "mi_swiglu_quant_q8_0": (_I, [_P, _P, _P, _P, _I64, _P, _I]),
     "mi_gemv_q8_0_add": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64]),
     "mi_fill_mask_f16": (_I, [_P, _P, _P, _I64]),

@@ -29,9 +29,18 @@ def rms_norm_ref(x, w, eps):
     return (y * w).astype(F32) if w is not None else y
 
 
+def _powf(a, b):
+    """the C library powf, as the host code forms theta_scale"""
+    import ctypes
+    libm = ctypes.CDLL("libm.so.6")
+    libm.powf.restype = ctypes.c_float
+    libm.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+    return F32(libm.powf(F32(a), F32(b)))
+
+
 def rope_neox_ref(x, pos, hd, base):
     """x [heads, hd] fp32; theta_i = pos * theta_scale^i by repeated float multiplication"""
-    ts = F32(np.power(F32(base), F32(-2.0) / F32(hd)))
+    ts = _powf(base, F32(-2.0) / F32(hd))
     th = np.empty(hd // 2, F32)
     t = F32(pos)
     for i in range(hd // 2):
@@ -99,6 +108,35 @@ def test_rope_neox(gpu, hd, heads, pos):
     assert rel_err(y, ref) < 2e-6
 
 
+def _rope_table(mi, dpos, hd, base, freq_scale=1.0, attn_factor=1.0):
+    tab = mi.DeviceBuffer(4 * hd)
+    mi._call("mi_rope_table", None, mi._P(dpos.ptr), hd, F32(base), F32(freq_scale), F32(attn_factor),
+             mi._P(tab.ptr))
+    return tab
+
+
+@pytest.mark.parametrize("hd,pos,base,fs,af", [(128, 0, 1e6, 1.0, 1.0), (128, 32767, 1e6, 1.0, 1.0),
+                                               (64, 517, 1e4, 0.5, 1.1), (1024, 77, 1e6, 1.0, 1.0)])
+def test_rope_table(gpu, hd, pos, base, fs, af):
+    """cos/sin of theta_p = freq_scale * (pos * theta_scale^p), the power by repeated float
+    multiplication; within 2 ulps of the host's double-precision cos/sin of the same angle"""
+    mi = gpu
+    dpos = mi.to_device(np.array([pos], np.int32))
+    tab = _rope_table(mi, dpos, hd, base, fs, af)
+    mi.device_sync()
+    got = tab.download(F32).reshape(2, hd // 2)
+    ts = _powf(base, F32(-2.0) / F32(hd))
+    th = np.empty(hd // 2, F32)
+    t = F32(pos)
+    for i in range(hd // 2):
+        th[i] = F32(F32(fs) * t)
+        t = F32(t * ts)
+    ref_c = (np.cos(th.astype(np.float64)).astype(F32) * F32(af)).astype(F32)
+    ref_s = (np.sin(th.astype(np.float64)).astype(F32) * F32(af)).astype(F32)
+    tol = 2 * np.spacing(np.float32(1.0)) * af + 1e-7
+    assert np.max(np.abs(got[0] - ref_c)) <= tol and np.max(np.abs(got[1] - ref_s)) <= tol
+
+
 @pytest.mark.parametrize("ne0,nrows", [(151936, 1), (1000, 3), (2049, 2), (4096 * 300 + 7, 1)])
 def test_argmax_first_maximum(gpu, ne0, nrows):
     mi = gpu
@@ -158,13 +196,15 @@ def test_fused_norm_matmuls_add(gpu, orc, norm, ns, k):
         assert rel_err(ys[i].download(F32), ref) < GEMV_TOL, f"matrix {i}"
 
 
+@pytest.mark.parametrize("table", [False, True])
 @pytest.mark.parametrize("idx_i64", [False, True])
 @pytest.mark.parametrize("cfg", [dict(k=1536, hq=12, hkv=2, hd=128, pos=517, row=517, bias=True),
                                  dict(k=3584, hq=28, hkv=4, hd=128, pos=3, row=9, bias=True),
                                  dict(k=256, hq=4, hkv=2, hd=64, pos=0, row=0, bias=False),
                                  dict(k=512, hq=64, hkv=8, hd=128, pos=40, row=1, bias=True)])
-def test_qkv_rope_kv(gpu, orc, cfg, idx_i64):
-    """the shapes cover 64, 32 and 16 lanes per row (the launch picks the width from the row count)"""
+def test_qkv_rope_kv(gpu, orc, cfg, idx_i64, table):
+    """the shapes cover 64, 32 and 16 lanes per row (the launch picks the width from the row count);
+    the angles formed in the launch or read from mi_rope_table"""
     mi = gpu
     k, hq, hkv, hd = cfg["k"], cfg["hq"], cfg["hkv"], cfg["hd"]
     nq, nkv = hq * hd, hkv * hd
@@ -184,9 +224,11 @@ def test_qkv_rope_kv(gpu, orc, cfg, idx_i64):
     vc = mi.DeviceBuffer(n_cache * nkv * 2).zero()
     dpos = mi.to_device(np.array([cfg["pos"]], np.int32))
     didx = mi.to_device(np.array([cfg["row"]], np.int64 if idx_i64 else np.int32))
+    tab = _rope_table(mi, dpos, hd, 1e6) if table else None
     mi._call("mi_qkv_rope_kv_q8_0", None, _ptrs(*pw), _i64s(*ns), _ptrs(*db), k, mi._P(dx.ptr), mi._P(dnw.ptr),
              F32(1e-6), mi._P(dinv.ptr), mi.Q8_ROUND_X86, hd, mi._P(dpos.ptr), F32(1e6), F32(1.0), F32(1.0),
-             mi._P(dq.ptr), mi._P(kc.ptr), nkv * 2, mi._P(vc.ptr), nkv * 2, mi._P(didx.ptr), int(idx_i64), n_cache)
+             mi._P(dq.ptr), mi._P(kc.ptr), nkv * 2, mi._P(vc.ptr), nkv * 2, mi._P(didx.ptr), int(idx_i64), n_cache,
+             mi._P(tab.ptr if tab is not None else None))
     mi.device_sync()
     xn = rms_norm_ref(x, nw, 1e-6)
     proj = []
@@ -220,7 +262,7 @@ def test_qkv_rope_kv_skips_out_of_range_row(gpu):
     didx = mi.to_device(np.array([8], np.int32))   # one past the last cache row
     mi._call("mi_qkv_rope_kv_q8_0", None, _ptrs(*pw), _i64s(*ns), _ptrs(None, None, None), k, mi._P(dx.ptr), None,
              F32(1e-6), None, mi.Q8_ROUND_X86, hd, mi._P(dpos.ptr), F32(1e4), F32(1.0), F32(1.0), mi._P(dq.ptr),
-             mi._P(kc.ptr), 256, mi._P(vc.ptr), 256, mi._P(didx.ptr), 0, 8)
+             mi._P(kc.ptr), 256, mi._P(vc.ptr), 256, mi._P(didx.ptr), 0, 8, None)
     mi.device_sync()
     assert not kc.download(np.uint16).any() and not vc.download(np.uint16).any()
 
@@ -335,12 +377,13 @@ def test_q4_gate_up_swiglu(gpu, orc, n, k):
     assert err < GEMV_TOL
 
 
+@pytest.mark.parametrize("table", [False, True])
 @pytest.mark.parametrize("idx_i64", [False, True])
 @pytest.mark.parametrize("cfg", [dict(k=3584, hq=28, hkv=4, hd=128, pos=32767, row=32767, bias=True),
                                  dict(k=1536, hq=12, hkv=2, hd=128, pos=517, row=517, bias=True),
                                  dict(k=256, hq=4, hkv=2, hd=64, pos=0, row=0, bias=False),
                                  dict(k=512, hq=6, hkv=3, hd=32, pos=40, row=1, bias=True)])
-def test_q4_qkv_rope_kv(gpu, orc, cfg, idx_i64):
+def test_q4_qkv_rope_kv(gpu, orc, cfg, idx_i64, table):
     from synth import q4_0_weights
     mi = gpu
     k, hq, hkv, hd = cfg["k"], cfg["hq"], cfg["hkv"], cfg["hd"]
@@ -360,9 +403,10 @@ def test_q4_qkv_rope_kv(gpu, orc, cfg, idx_i64):
     vc = mi.DeviceBuffer(n_cache * nkv * 2).zero()
     dpos = mi.to_device(np.array([cfg["pos"]], np.int32))
     didx = mi.to_device(np.array([cfg["row"]], np.int64 if idx_i64 else np.int32))
+    tab = _rope_table(mi, dpos, hd, 1e6) if table else None
     mi._call("mi_qkv_rope_kv_q4_0", None, _ptrs(*pw), _i64s(*ns), _ptrs(*db), k, mi._P(dx.ptr), mi._P(dnw.ptr),
              F32(1e-6), hd, mi._P(dpos.ptr), F32(1e6), F32(1.0), F32(1.0), mi._P(dq.ptr), mi._P(kc.ptr), nkv * 2,
-             mi._P(vc.ptr), nkv * 2, mi._P(didx.ptr), int(idx_i64), n_cache)
+             mi._P(vc.ptr), nkv * 2, mi._P(didx.ptr), int(idx_i64), n_cache, mi._P(tab.ptr if tab is not None else None))
     mi.device_sync()
     xn = rms_norm_ref(x, nw, 1e-6)
     proj = []
@@ -397,6 +441,6 @@ def test_q4_qkv_rope_kv_skips_out_of_range_row(gpu):
     didx = mi.to_device(np.array([-1], np.int32))   # before the first cache row
     mi._call("mi_qkv_rope_kv_q4_0", None, _ptrs(*pw), _i64s(*ns), _ptrs(None, None, None), k, mi._P(dx.ptr), None,
              F32(1e-6), hd, mi._P(dpos.ptr), F32(1e4), F32(1.0), F32(1.0), mi._P(dq.ptr), mi._P(kc.ptr), 256,
-             mi._P(vc.ptr), 256, mi._P(didx.ptr), 0, 8)
+             mi._P(vc.ptr), 256, mi._P(didx.ptr), 0, 8, None)
     mi.device_sync()
     assert not kc.download(np.uint16).any() and not vc.download(np.uint16).any()
