@@ -779,7 +779,7 @@ int try_fuse_gate_up_down_q4(BackendCtx *ctx, ggml_cgraph *g, int i, const Consu
     const ggml_tensor *down = ggml_graph_node(g, jd);
     const int64_t nf = mm[0]->ne[0];
     if (!gemv_node(down, GGML_TYPE_Q4_0) || down->src[1] != glu || !only_consumed_by(C, glu, {down}) ||
-        down->src[0]->ne[0] != nf || nf / 32 > 1008 || ctx->scratch_size < (size_t)nf * 2)
+        down->src[0]->ne[0] != nf || nf / 32 > 1024 || ctx->scratch_size < (size_t)nf * 2)
         return 0;
     const ggml_tensor *vec = nullptr;
     const ggml_tensor *ad = matmul_add_tail(g, jd, down, C, vec);

@@ -581,8 +581,8 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
     constexpr int PG = 4 / WPR;  // pair groups per workgroup
     extern __shared__ __align__(16) uint8_t smem[];
     const int k = nb * QK;
-    uint16_t *s_x = (uint16_t *)smem;
-    float *s_red = (float *)(smem + (size_t)k * 2);  // [2][4][2]
+    uint16_t *s_x = (uint16_t *)smem;                              // the fp16 row (fp32 input only)
+    float *s_red = (float *)(smem + (XF32 ? (size_t)k * 2 : 0));  // [2][4][2]
     double *s_nred = (double *)(s_red + 16);        // [4]
     float *s_rope = (float *)(s_nred + 4);          // [2][64]: cos, sin of rotation pair p
     const int tid = threadIdx.x, lane = tid & 63;
@@ -619,8 +619,19 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
         ci_hi = ((const int32_t *)R.kv_idx)[z + (R.kv_idx_i64 ? 1 : 0)];
         rope_tab_prefetch(R, lane + z, tab_cs, tab_sn);
     }
+    // An fp32 row is staged once per workgroup as fp16 in LDS (XN > 0: through registers,
+    // with the RMSNorm when NORM); an fp16 row is not staged: each lane loads its own
+    // blocks straight into registers.
     XStage<(XN > 0 ? XN : 1), NORM> st;
     if constexpr (XN > 0) xstage_load(st, (const float *)xin, norm_w, nullptr, k4, tid);
+    constexpr int KH = XF32 ? 1 : KB;
+    uint4 xh[KH][4];
+    if constexpr (!XF32) {
+#pragma unroll
+        for (int i = 0; i < KB; i++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) xh[i][c] = ((const uint4 *)xin)[(size_t)bidx[i] * 4 + c];
+    }
 
     // the first unit's weights go out before the activation is staged
     XrRows<KB> wa, wb;
@@ -631,7 +642,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
     __builtin_amdgcn_sched_barrier(0);  // nothing that waits on a load moves above the weight loads
 
     if constexpr (XN > 0) {
-        const float scale = xstage_scale(st, k4, eps, s_nred, tid);
+        const float scale = xstage_scale(st, k4, eps, s_nred, tid);  // 1 without NORM
 #pragma unroll
         for (int t = 0; t < XN; t++) {
             const int f = tid + t * 256;
@@ -646,8 +657,6 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
             ((uint2 *)s_x)[f] = make_uint2((uint32_t)f2h(v.x) | ((uint32_t)f2h(v.y) << 16),
                                            (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16));
         }
-    } else {
-        for (int f = tid; f < k / 8; f += 256) ((int4 *)s_x)[f] = ((const int4 *)xin)[f];
     }
 
     XrRope rp;
@@ -672,13 +681,18 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
         rp.ci = ci;
         rp.ci_ok = ci >= 0 && ci < R.n_cache_rows;
     }
-    __syncthreads();
+    if constexpr (XF32 || UM == XR_ROPE) __syncthreads();
 
     uint32_t xr[KB][16];
 #pragma unroll
     for (int i = 0; i < KB; i++) {
-        const uint4 *p = (const uint4 *)(s_x + (size_t)bidx[i] * QK);
-        const uint4 q0 = p[0], q1 = p[1], q2 = p[2], q3 = p[3];
+        uint4 q0, q1, q2, q3;
+        if constexpr (XF32) {
+            const uint4 *p = (const uint4 *)(s_x + (size_t)bidx[i] * QK);
+            q0 = p[0]; q1 = p[1]; q2 = p[2]; q3 = p[3];
+        } else {
+            q0 = xh[i][0]; q1 = xh[i][1]; q2 = xh[i][2]; q3 = xh[i][3];
+        }
         const uint32_t w[16] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w,
                                 q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, q3.z, q3.w};
 #pragma unroll
@@ -883,12 +897,14 @@ inline bool xr_shape(int64_t nb, XrShape &s) {
     else if (nb <= 384) s = {3, 2};
     else if (nb <= 512) s = {2, 4};
     else if (nb <= 768) s = {3, 4};
-    else if (nb <= 1008) s = {4, 4};  // the fp16 row and the reduction slots within 64 KB of LDS
+    else if (nb <= 1024) s = {4, 4};
     else return false;
     return true;
 }
 
-inline size_t xr_smem(int64_t k) { return (size_t)k * 2 + 16 * sizeof(float) + 4 * sizeof(double) + 128 * sizeof(float); }
+inline size_t xr_smem(int64_t k, bool f32_row) {
+    return (f32_row ? (size_t)k * 2 : 0) + 16 * sizeof(float) + 4 * sizeof(double) + 128 * sizeof(float);
+}
 
 // workgroups resident at once on the current device for this kernel and LDS size
 int xr_resident(const void *fn, size_t smem) {
@@ -917,7 +933,7 @@ template <int KB, int WPR, bool XF32, int XN, bool NORM, int UM>
 int launch_xr(hipStream_t st, const Q4Set &S, const void *x, const float *norm_w, float eps, int nb, int n_units,
               int n_rows, const RopeKV &R, uint16_t *h) {
     constexpr int PG = 4 / WPR;
-    const size_t smem = xr_smem((int64_t)nb * QK);
+    const size_t smem = xr_smem((int64_t)nb * QK, XF32);
     auto fn = k_gemv_q4_0_xr<KB, WPR, XF32, XN, NORM, UM>;
     const int want = (n_units + PG - 1) / PG;
     const int grid = std::min(want, xr_resident((const void *)fn, smem));
@@ -1023,7 +1039,12 @@ inline bool xr_enabled() {
 int launch_gx(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16, float *y,
               const float *add = nullptr) {
     if (m >= 2 && m <= 16) return launch_mfma<false>(st, base, n, k, m, x16, y, add);
-    if (m == 1 && xr_enabled() && k / QK <= 1008) return launch_xr_gemv(st, base, n, k, x16, false, y, add);
+    // One fp16 row: with an add vector (the fused chains' residual launch, which must
+    // match the node-by-node path bit for bit) always the register kernel; without,
+    // the register kernel for long rows and the fp16-from-global kernel below 512 blocks
+    // per row, where it measured faster.
+    if (m == 1 && xr_enabled() && k / QK <= 1024 && (add || k / QK >= 512))
+        return launch_xr_gemv(st, base, n, k, x16, false, y, add);
     const bool tall = n >= 2048;
     if (m == 1) return tall ? launch_gx_mr<1, 2>(st, base, n, k, m, x16, y, add)
                             : launch_gx_mr<1, 1>(st, base, n, k, m, x16, y, add);
@@ -1116,6 +1137,8 @@ int mi_mul_mat_q4_0_f32(void *stream, const void *w_packed, const float *x, floa
     MI_CHECK_ARG(mi::aligned(w_packed, 256) && mi::aligned(x, 16), "mul_mat_q4_0_f32: w_packed must be 256-byte, x 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     if (m > 1) return launch_mfma<true>(st, (const uint8_t *)w_packed, n, k, m, x, y, nullptr);
+    // one fp32 row: the register kernel (the fused chains' arithmetic, so that fused and
+    // node-by-node graphs agree bit for bit) while the fp16 row fits 64 KB of LDS
     if (xr_enabled() && k / QK <= 1008) return launch_xr_gemv(st, (const uint8_t *)w_packed, n, k, x, true, y, nullptr);
     const size_t need = mi_mul_mat_q4_0_workspace_size(m, k);
     if (need == 0) return launch_lds(st, (const uint8_t *)w_packed, n, k, m, x, y);
@@ -1132,6 +1155,7 @@ int mi_mul_mat_q4_0_f32_fused(void *stream, int n_mats, const void *const *w_pac
                               const float *norm_w, float eps) {
     MI_CHECK_ARG(w_packed && n && y && x, "mul_mat_q4_0_f32_fused: null pointer");
     if (int r = check_shape("mul_mat_q4_0_f32_fused", 1, k)) return r;
+    // the fp16 copy of the row and the reduction slots fit 64 KB of LDS up to 1008 blocks
     MI_CHECK_ARG(k <= (norm_w ? 4096 : 1008 * QK), "mul_mat_q4_0_f32_fused: k=%lld too long", (long long)k);
     MI_CHECK_ARG(mi::aligned(x, 16) && (!norm_w || mi::aligned(norm_w, 16)),
                  "mul_mat_q4_0_f32_fused: x/norm_w must be 16-byte aligned");

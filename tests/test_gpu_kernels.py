@@ -157,7 +157,7 @@ def test_q8_0_gemv_shapes(gpu, orc, n, k, m):
                                    (1030, 3584, 16), (77, 160, 2), (5, 16384, 1), (33, 8192, 1),
                                    (9, 32000, 1), (9, 32768, 1), (50, 33792, 1), (3, 64, 1)])
 def test_w4a16_gemv(gpu, orc, n, k, m):
-    """one activation row: the register-resident kernel for k <= 32256 (every blocks-per-
+    """one activation row: the register-resident kernel for k <= 32768 (every blocks-per-
     lane / waves-per-row shape; odd n leaves the last row pair half empty), beyond that the
     fp16-from-global kernel through a workspace; several rows: the matrix-core kernel"""
     mi = gpu
