@@ -133,6 +133,16 @@ int mi_mul_mat_q8_0_f32_multi(void *stream, int n_mats, const void *const *w_pac
 int mi_mul_mat_q8_0_f32_fused(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
                               float *const *y, const float *const *add, int64_t k, const float *x,
                               const float *norm_w, float eps, const float *inv_s, int rounding);
+/* FLASH_ATTN_EXT (one token, one sequence) -> MUL_MAT(Q8_0) [-> ADD(add)]: the projection
+ * of an attention output left in split form by mi_fa_decode_partials.  Every workgroup
+ * merges the n_splits records (the log-sum-exp combine of mi_fa_decode) for its whole
+ * activation row in its prologue, so no combine launch and no attention-output tensor.
+ * k = n_heads * head_dim <= 2048, n_splits <= 16, head_dim % 4 == 0; add may be NULL.
+ * Replaces the reference's attention output handed to the o projection
+ * (patch:1370-1432, then ggml_cann_mat_mul_fp patch:1188-1355). */
+int mi_mul_mat_q8_0_f32_lse(void *stream, const void *w_packed, int64_t n, float *y, const float *add,
+                            const float *part, int64_t n_splits, int64_t n_heads, int64_t head_dim,
+                            const float *inv_s, int rounding);
 /* the attention-input chain of one token: [RMS_NORM -> MUL(norm_w)] -> q/k/v MUL_MATs
  * (w_packed[0..2], n[0..2] rows, k <= 4096) -> ADD bias[i] (or NULL) -> neox ROPE of q
  * and k (n_dims = head_dim, theta = pos[0] * freq_base^(-2i/head_dim), freq_scale,
@@ -239,6 +249,18 @@ int mi_fa_decode_batch(void *stream, const float *q, const void *k, const void *
                        size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out,
                        int64_t n_seq, size_t q_seq, size_t k_seq, size_t v_seq, size_t mask_seq, size_t out_seq,
                        void *ws, size_t ws_bytes);
+/* The split half of mi_fa_decode alone, for a consumer that merges the splits itself
+ * (mi_mul_mat_q8_0_f32_lse): every split writes its record to ws and no combine runs.
+ * Record of q head h, split s: floats ws[(h*S + s)*(d+4) + i], i < d: the unnormalised
+ * output sum_j e^(s_j - m) v_j; [d]: m, the split's running maximum in log2 units
+ * (scores times log2(e)), -inf for a split with no position; [d+1]: l = sum_j e^(s_j - m).
+ * S = mi_fa_decode_num_splits(); ws as for mi_fa_decode (its size, 256-byte alignment).
+ * No reference counterpart: the reference streams the whole KV length per head, no splits. */
+int64_t mi_fa_decode_num_splits(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d);
+int mi_fa_decode_partials(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
+                          const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                          size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, void *ws,
+                          size_t ws_bytes);
 
 /* ------------------------------------------------------------------------
  * Decode-graph glue ops (one launch each; ggml-CPU semantics of

@@ -286,7 +286,7 @@ __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, c
             }
         }
         const int qh_idx = kvh * GQ + h;
-        if (n_splits == 1) {
+        if (n_splits == 1 && out) {
             out[(size_t)qh_idx * D + dd] = L == 0.0f ? 0.0f : acc / L;
         } else {
             float *rec = part + ((size_t)qh_idx * n_splits + split) * PS;
@@ -632,7 +632,7 @@ __global__ __launch_bounds__(256) void k_fa_mfma(const float *__restrict__ q, co
             }
         }
         const int qh_idx = kvh * GQ + h;
-        if (n_splits == 1) {
+        if (n_splits == 1 && out) {
             out[(size_t)qh_idx * D + dd] = L == 0.0f ? 0.0f : acc / L;
         } else if (counters) {
             float *rec = part + ((size_t)qh_idx * n_splits + split) * PS;
@@ -749,17 +749,20 @@ struct FaArgs {
     float *out, *part;
     unsigned *counters;
     FaSeq sq;
+    bool partials_only;  // write every split's (o, m, l) record, no combine, out unused
 };
 
 template <int D, int GQ, bool MASK>
 int launch_split_m(hipStream_t st, const FaArgs &a, const FaPlan &p) {
     const dim3 grid((unsigned)p.n_splits, (unsigned)a.n_kv_heads, (unsigned)a.n_seq);
     const uint8_t *kb = (const uint8_t *)a.k, *vb = (const uint8_t *)a.v;
+    float *const out = a.partials_only ? nullptr : a.out;
     if (p.mfma) {
-        const bool merged = p.n_splits <= kFusedMaxSplits && a.counters && mfma_merge_enabled();
+        const bool merged =
+            !a.partials_only && p.n_splits <= kFusedMaxSplits && a.counters && mfma_merge_enabled();
 #define MI_FA_NBW(NB)                                                                                          \
     hipLaunchKernelGGL((k_fa_mfma<D, GQ, MASK, NB>), grid, dim3(256), 0, st, a.q, kb, vb, a.mask, a.kv_len,      \
-                       (int)a.n_kv, a.k_nb1, a.k_nb2, a.v_nb1, a.v_nb2, a.scale, p.chunk, p.n_splits, a.part, a.out, \
+                       (int)a.n_kv, a.k_nb1, a.k_nb2, a.v_nb1, a.v_nb2, a.scale, p.chunk, p.n_splits, a.part, out,   \
                        merged ? a.counters : nullptr, a.sq)
         switch (p.nbw) {
             case 1: MI_FA_NBW(1); break;
@@ -771,10 +774,10 @@ int launch_split_m(hipStream_t st, const FaArgs &a, const FaPlan &p) {
         MI_CHECK_LAUNCH("k_fa_mfma");
         if (merged) return MI_OK;
     } else {
-        const bool fused = p.n_splits <= kFusedMaxSplits && fused_combine_enabled();
+        const bool fused = !a.partials_only && p.n_splits <= kFusedMaxSplits && fused_combine_enabled();
 #define MI_FA_KT(KT)                                                                                           \
     hipLaunchKernelGGL((k_fa_split<D, GQ, MASK, KT>), grid, dim3(256), 0, st, a.q, kb, vb, a.mask, a.kv_len,     \
-                       (int)a.n_kv, a.k_nb1, a.k_nb2, a.v_nb1, a.v_nb2, a.scale, p.chunk, p.n_splits, a.part, a.out, \
+                       (int)a.n_kv, a.k_nb1, a.k_nb2, a.v_nb1, a.v_nb2, a.scale, p.chunk, p.n_splits, a.part, out,   \
                        fused ? a.counters : nullptr, a.sq)
         switch (p.kt) {
             case 1: MI_FA_KT(1); break;
@@ -786,7 +789,7 @@ int launch_split_m(hipStream_t st, const FaArgs &a, const FaPlan &p) {
         MI_CHECK_LAUNCH("k_fa_split");
         if (fused) return MI_OK;
     }
-    if (p.n_splits > 1) {
+    if (p.n_splits > 1 && !a.partials_only) {
         hipLaunchKernelGGL((k_fa_combine<D>), dim3((unsigned)(a.n_kv_heads * GQ), D / 32, (unsigned)a.n_seq),
                            dim3(256), 0, st, a.part, a.out, p.n_splits, a.sq.out);
         MI_CHECK_LAUNCH("k_fa_combine");
@@ -856,12 +859,12 @@ size_t mi_fa_decode_workspace_size(int64_t n_kv, int64_t n_q_heads, int64_t n_kv
     return mi_fa_decode_batch_workspace_size(n_kv, n_q_heads, n_kv_heads, d, 1);
 }
 
-int mi_fa_decode_batch(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
-                       const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
-                       size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out,
-                       int64_t n_seq, size_t q_seq, size_t k_seq, size_t v_seq, size_t mask_seq, size_t out_seq,
-                       void *ws, size_t ws_bytes) {
-    MI_CHECK_ARG(q && k && v && out, "fa_decode: null pointer");
+static int fa_decode_run(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
+                         const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                         size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out,
+                         int64_t n_seq, size_t q_seq, size_t k_seq, size_t v_seq, size_t mask_seq, size_t out_seq,
+                         void *ws, size_t ws_bytes, bool partials_only) {
+    MI_CHECK_ARG(q && k && v && (out || partials_only), "fa_decode: null pointer");
     MI_CHECK_ARG(n_kv > 0 && n_kv < (1ll << 31) && n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0,
                  "fa_decode: bad heads/length n_kv=%lld nq=%lld nkv=%lld", (long long)n_kv, (long long)n_q_heads,
                  (long long)n_kv_heads);
@@ -873,7 +876,7 @@ int mi_fa_decode_batch(void *stream, const float *q, const void *k, const void *
                  "fa_decode: K/V base and strides must be 16-byte aligned");
     const FaPlan p = fa_plan(n_kv, n_kv_heads, d, n_q_heads / n_kv_heads);
     const size_t need = mi_fa_decode_batch_workspace_size(n_kv, n_q_heads, n_kv_heads, d, n_seq);
-    if (p.n_splits > 1 && (!ws || ws_bytes < need || !mi::aligned(ws, 256))) {
+    if ((p.n_splits > 1 || partials_only) && (!ws || ws_bytes < need || !mi::aligned(ws, 256))) {
         mi::set_error("fa_decode: workspace %zu < %zu bytes (or not 256-byte aligned)", ws_bytes, need);
         return MI_ERR_WORKSPACE;
     }
@@ -899,10 +902,33 @@ int mi_fa_decode_batch(void *stream, const float *q, const void *k, const void *
     a.sq.v = v_seq;
     a.sq.mask = mask_seq;
     a.sq.out = out_seq;
+    a.partials_only = partials_only;
     const int gq = (int)(n_q_heads / n_kv_heads);
     hipStream_t st = (hipStream_t)stream;
     if (d == 128) return launch_d<128>(st, gq, a, p);
     return launch_d<64>(st, gq, a, p);
+}
+
+int mi_fa_decode_batch(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
+                       const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                       size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out,
+                       int64_t n_seq, size_t q_seq, size_t k_seq, size_t v_seq, size_t mask_seq, size_t out_seq,
+                       void *ws, size_t ws_bytes) {
+    return fa_decode_run(stream, q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1, k_nb2, v_nb1, v_nb2,
+                         scale, out, n_seq, q_seq, k_seq, v_seq, mask_seq, out_seq, ws, ws_bytes, false);
+}
+
+int64_t mi_fa_decode_num_splits(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d) {
+    if (n_kv <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || d <= 0 || n_q_heads % n_kv_heads) return 0;
+    return fa_plan(n_kv, n_kv_heads, d, n_q_heads / n_kv_heads).n_splits;
+}
+
+int mi_fa_decode_partials(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
+                          const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                          size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, void *ws,
+                          size_t ws_bytes) {
+    return fa_decode_run(stream, q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1, k_nb2, v_nb1, v_nb2,
+                         scale, nullptr, 1, 0, 0, 0, 0, 0, ws, ws_bytes, true);
 }
 
 int mi_fa_decode(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,

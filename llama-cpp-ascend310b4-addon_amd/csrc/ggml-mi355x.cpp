@@ -547,6 +547,8 @@ void run_fa(BackendCtx *ctx, ggml_tensor *node) {
 //   matmul + add    : MUL_MAT, ADD(vector)              -> fused epilogue add
 //   glu + matmul    : GLU swiglu, MUL_MAT, [ADD(vector)] -> mi_swiglu_quant_q8_0 +
 //                                                          mi_gemv_q8_0_add
+//   attention + o   : FLASH_ATTN_EXT, MUL_MAT, [ADD]     -> mi_fa_decode_partials +
+//                                                          mi_mul_mat_q8_0_f32_lse
 
 using Consumers = std::unordered_map<const ggml_tensor *, std::vector<const ggml_tensor *>>;
 
@@ -908,6 +910,44 @@ int try_fuse_glu_matmul(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers 
     return (ad ? next_real(g, j + 1) : j) + 1 - i;
 }
 
+// FLASH_ATTN_EXT (one token, one sequence) whose output only feeds a Q8_0 projection
+// [+ ADD]: the attention leaves its splits' records in the FA workspace and the
+// projection merges them in its prologue (no combine launch, no attention-output write).
+// Opt-in (MI_FUSE_FA_O=1): every projection workgroup then reads all splits' records
+// (12 splits x 12 heads x 528 B at a 768-row KV view), which measured slower than the
+// separate combine launch on the Qwen2.5-1.5B shape (6.97 us against 3.45 + 3.17 us).
+int try_fuse_fa_o(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    static const bool on = env_flag("MI_FUSE_FA_O", false);
+    if (!on) return 0;
+    const ggml_tensor *fa = ggml_graph_node(g, i);
+    const ggml_tensor *q = fa->src[0], *k = fa->src[1], *v = fa->src[2], *mask = fa->src[3];
+    if (q->ne[1] != 1 || q->ne[3] != 1 || !ggml_is_contiguous(fa)) return 0;
+    const int64_t d = q->ne[0], n_head = q->ne[2];
+    const int j = next_real(g, i + 1);
+    if (j >= ggml_graph_n_nodes(g)) return 0;
+    const ggml_tensor *mm = ggml_graph_node(g, j);
+    if (!q8_gemv_node(mm) || alias_root(mm->src[1]) != fa || !only_consumed_by(C, fa, {mm})) return 0;
+    const int64_t kk = mm->src[0]->ne[0];
+    if (kk != d * n_head || kk > 2048 || d % 4) return 0;
+    const int64_t S = mi_fa_decode_num_splits(k->ne[1], n_head, k->ne[2], d);
+    if (S < 1 || S > 16) return 0;
+    if (ctx->fa_ws_size < mi_fa_decode_workspace_size(k->ne[1], n_head, k->ne[2], d)) return 0;
+    const ggml_tensor *vec = nullptr;
+    const ggml_tensor *ad = matmul_add_tail(g, j, mm, C, vec);
+    float scale;
+    memcpy(&scale, fa->op_params, sizeof(float));
+    const ggml_tensor *kvl = fa->src[5];
+    MI_K_CHECK(mi_fa_decode_partials(ctx->stream, (const float *)q->data, k->data, v->data,
+                                     mask ? (const uint16_t *)mask->data : nullptr,
+                                     kvl ? (const int32_t *)kvl->data : nullptr, k->ne[1], n_head, k->ne[2], d,
+                                     k->nb[1], k->nb[2], v->nb[1], v->nb[2], scale, ctx->fa_ws, ctx->fa_ws_size));
+    const TensorExtra *ex = (const TensorExtra *)mm->src[0]->extra;
+    MI_K_CHECK(mi_mul_mat_q8_0_f32_lse(ctx->stream, ex->packed, mm->src[0]->ne[1], (float *)(ad ? ad->data : mm->data),
+                                       ad ? (const float *)vec->data : nullptr, (const float *)ctx->fa_ws, S, n_head,
+                                       d, ex->inv_s, q8_rounding()));
+    return (ad ? next_real(g, j + 1) : j) + 1 - i;
+}
+
 // Runs node i (and, when fused, the nodes it absorbs); returns the number of nodes consumed.
 int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
     ggml_tensor *node = ggml_graph_node(g, i);
@@ -943,6 +983,9 @@ int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
             return 1;
         }
         case GGML_OP_FLASH_ATTN_EXT:
+            if (fuse) {
+                if (int used = try_fuse_fa_o(ctx, g, i, C)) return used;
+            }
             run_fa(ctx, node);
             return 1;
         case GGML_OP_RMS_NORM: {

@@ -337,6 +337,170 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma(const uint8_t *__res
     }
 }
 
+// Several activation rows on the matrix cores with the activation as the A operand:
+// D[16 rows of x][16 weight rows] += X[16 x 16 k] . W^T[16 k x 16 weight rows].  Lane
+// (g, c) supplies dword g of a block of weight row c (its low nibbles are the first
+// 16-k step, its high nibbles the second) and the activation row c's matching values;
+// it receives weight row c's results for activation rows 4g..4g+3, so it applies one
+// block scale (row c's) per block.  The activation comes converted to fp16 in the
+// order in which a weight dword's nibbles come out (see q4_dot_xr):
+//   xp[row][block][g][8] = x[4g], x[4g+2], x[4g+1], x[4g+3], x[16+4g], x[18+4g], x[17+4g], x[19+4g]
+// one 16-byte load per block.  k is split over KS waves (partials reduced in LDS).
+template <bool XF32>
+__global__ __launch_bounds__(256) void k_perm_f16(const void *__restrict__ x, uint4 *__restrict__ xp, int m, int nb) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (row, block, g)
+    if (i >= (int64_t)m * nb * 4) return;
+    const int g = (int)(i & 3);
+    const int64_t rb = i >> 2;  // row * nb + block
+    uint16_t h[8];
+    const int idx[8] = {4 * g, 4 * g + 2, 4 * g + 1, 4 * g + 3, 16 + 4 * g, 18 + 4 * g, 17 + 4 * g, 19 + 4 * g};
+    if constexpr (XF32) {
+        const float *xb = (const float *)x + rb * QK;
+#pragma unroll
+        for (int j = 0; j < 8; j++) h[j] = f2h(xb[idx[j]]);
+    } else {
+        const uint16_t *xb = (const uint16_t *)x + rb * QK;
+#pragma unroll
+        for (int j = 0; j < 8; j++) h[j] = xb[idx[j]];
+    }
+    xp[i] = make_uint4((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16),
+                       (uint32_t)h[4] | ((uint32_t)h[5] << 16), (uint32_t)h[6] | ((uint32_t)h[7] << 16));
+}
+
+// Groups of 4 blocks: lane (g, c) loads block 4j+g of weight row c whole (16 bytes; the
+// 4 g-lanes of a row read 64 contiguous bytes) and the 4 scales of row c's group (8
+// bytes).  A 4x4 dword transpose through the wave's LDS slot then gives lane (g, c)
+// dword g of each of the group's 4 blocks, the operand the matrix core wants.
+template <int UG, int TW>
+struct Q4XStage {
+    uint4 w[UG][TW];   // block 4j+g of row c of each tile
+    uint2 d[UG][TW];   // fp16 scales of row c, blocks 4j..4j+3, of each tile
+    uint4 x[UG][4];    // activation row c, blocks 4j..4j+3, slot g (shared by the tiles)
+};
+
+// TW 16-row tiles per wave share each activation load; k is split over KS waves.
+template <int KS, int UG, int TW>
+__global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const uint8_t *__restrict__ qs,
+                                                              const uint16_t *__restrict__ wd,
+                                                              const uint4 *__restrict__ xp, float *__restrict__ y,
+                                                              const float *__restrict__ add, int n, int nb, int m) {
+    __shared__ float s_acc[KS][TW][64][4];
+    __shared__ uint32_t s_t[KS][16][4][4];  // per wave: [row c][dword][block in group]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int row0 = blockIdx.x * 16 * TW;
+    const int ng = nb / 4;               // whole groups (nb % 4 == 0)
+    const int per = (ng + KS - 1) / KS;  // groups of this wave
+    const int j_lo = wave * per, j_hi = min(ng, j_lo + per);
+    size_t wrow[TW];
+#pragma unroll
+    for (int t = 0; t < TW; t++) wrow[t] = (size_t)min(row0 + 16 * t + c, n - 1) * nb;
+    const bool x_ok = c < m;
+    const uint4 *xrow = xp + (size_t)min(c, m - 1) * nb * 4 + g;
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));
+    const half2_t off = {(half_t)1032.0f, (half_t)1032.0f};
+
+    auto load = [&](Q4XStage<UG, TW> &st, int j0) {
+#pragma unroll
+        for (int u = 0; u < UG; u++) {
+            const int j = min(j0 + u, j_hi - 1);
+#pragma unroll
+            for (int t = 0; t < TW; t++) {
+                st.w[u][t] = *(const uint4 *)(qs + (wrow[t] + 4 * j + g) * 16);
+                st.d[u][t] = *(const uint2 *)(wd + wrow[t] + 4 * j);
+            }
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) st.x[u][jj] = xrow[(size_t)(4 * j + jj) * 4];
+        }
+    };
+    float4_t acc[TW];
+#pragma unroll
+    for (int t = 0; t < TW; t++) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const Q4XStage<UG, TW> &st, int j0) {
+#pragma unroll
+        for (int u = 0; u < UG; u++) {
+            const bool valid = j0 + u < j_hi;
+            const half4_t z = {0, 0, 0, 0};
+#pragma unroll
+            for (int t = 0; t < TW; t++) {
+                // transpose: lane (g, c) has dwords 0..3 of block g; wants dword g of blocks 0..3.
+                // One wave writes and reads its own slot: LDS executes a wave's operations in
+                // order, so only the compiler needs fencing.
+                s_t[wave][c][0][g] = st.w[u][t].x;
+                s_t[wave][c][1][g] = st.w[u][t].y;
+                s_t[wave][c][2][g] = st.w[u][t].z;
+                s_t[wave][c][3][g] = st.w[u][t].w;
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                __builtin_amdgcn_wave_barrier();
+                const uint4 wt = *(const uint4 *)&s_t[wave][c][g][0];
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                __builtin_amdgcn_wave_barrier();
+                const uint32_t ww[4] = {wt.x, wt.y, wt.z, wt.w};
+                const uint32_t dd[4] = {st.d[u][t].x & 0xffffu, st.d[u][t].x >> 16, st.d[u][t].y & 0xffffu,
+                                        st.d[u][t].y >> 16};
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const uint32_t v = ww[jj];
+                    const half2_t a0 = u2h2((v & 0x000f000fu) | magic) - off;
+                    const half2_t a1 = u2h2(((v >> 8) & 0x000f000fu) | magic) - off;
+                    const half2_t b0h = u2h2(((v >> 4) & 0x000f000fu) | magic) - off;
+                    const half2_t b1h = u2h2(((v >> 12) & 0x000f000fu) | magic) - off;
+                    const half4_t wlo = {a0.x, a0.y, a1.x, a1.y};
+                    const half4_t whi = {b0h.x, b0h.y, b1h.x, b1h.y};
+                    const uint4 xv = st.x[u][jj];
+                    const half4_t xlo = x_ok ? __builtin_bit_cast(half4_t, make_uint2(xv.x, xv.y)) : z;
+                    const half4_t xhi = x_ok ? __builtin_bit_cast(half4_t, make_uint2(xv.z, xv.w)) : z;
+                    float4_t r = {0.f, 0.f, 0.f, 0.f};
+                    r = __builtin_amdgcn_mfma_f32_16x16x16f16(xlo, wlo, r, 0, 0, 0);
+                    r = __builtin_amdgcn_mfma_f32_16x16x16f16(xhi, whi, r, 0, 0, 0);
+                    const float ds = valid ? h2f((uint16_t)dd[jj]) : 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[t][i] = fmaf(ds, r[i], acc[t][i]);
+                }
+            }
+        }
+    };
+    if (j_lo < j_hi) {
+        // two register stages; the prefetches are unconditional (clamped: past the end they
+        // re-read the last group, a cache hit, and its scales are zeroed), since a load
+        // under a branch makes the compiler wait for every load at the join
+        Q4XStage<UG, TW> sa, sb;
+        load(sa, j_lo);
+        for (int j0 = j_lo; j0 < j_hi; j0 += 2 * UG) {
+            load(sb, j0 + UG);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(sa, j0);
+            load(sa, j0 + 2 * UG);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(sb, j0 + UG);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < TW; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) s_acc[wave][t][lane][i] = acc[t][i];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int t = 0; t < TW; t++) {
+        const int row = row0 + 16 * t + c;
+        if (row >= n) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = 4 * g + i;  // activation row
+            if (r < m) {
+                float v = 0.0f;
+#pragma unroll
+                for (int w = 0; w < KS; w++) v += s_acc[w][t][lane][i];
+                const size_t o = (size_t)r * n + row;
+                y[o] = add ? v + add[o] : v;
+            }
+        }
+    }
+}
+
 // fp32 -> fp16 (round to nearest even, as ggml's activation conversion)
 __global__ __launch_bounds__(256) void k_cast_f16(const float *__restrict__ x, uint16_t *__restrict__ y, int64_t n4) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -1036,6 +1200,56 @@ inline bool xr_enabled() {
     return on;
 }
 
+// activation rows converted into ws as permuted fp16, then the A-operand matrix-core kernel
+int launch_mfma_x(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const void *x, bool xf32,
+                  float *y, const float *add, void *ws) {
+    const Q4Planes p = q4_planes(n, k);
+    const int nb = (int)(k / QK);
+    const int64_t units = m * nb * 4;
+    if (xf32)
+        hipLaunchKernelGGL((k_perm_f16<true>), dim3((unsigned)((units + 255) / 256)), dim3(256), 0, st, x, (uint4 *)ws,
+                           (int)m, nb);
+    else
+        hipLaunchKernelGGL((k_perm_f16<false>), dim3((unsigned)((units + 255) / 256)), dim3(256), 0, st, x,
+                           (uint4 *)ws, (int)m, nb);
+    MI_CHECK_LAUNCH("k_perm_f16");
+    static const int tw_env = [] {
+        const char *e = getenv("MI_Q4_MFMA_TW");
+        return e ? atoi(e) : 0;
+    }();
+    const int tw = tw_env == 1 || tw_env == 2 ? tw_env : (n >= 8192 ? 2 : 1);
+    const unsigned wgs = (unsigned)((n + 16 * tw - 1) / (16 * tw));
+    const uint16_t *dpl = (const uint16_t *)(base + p.plane);
+    static const int ks_env = [] {
+        const char *e = getenv("MI_Q4_MFMA_KS");
+        return e ? atoi(e) : 0;
+    }();
+    const int ks = ks_env == 2 || ks_env == 4 || ks_env == 8 || ks_env == 16 ? ks_env : 4;
+#define MI_MX(KS, TW) \
+    hipLaunchKernelGGL((k_gemv_q4_0_mfma_x<KS, 2, TW>), dim3(wgs), dim3(64 * KS), 0, st, base, dpl, (const uint4 *)ws, \
+                       y, add, (int)n, nb, (int)m)
+#define MI_MX_KS(KS) \
+    if (ks == KS) {  \
+        if (tw == 2) MI_MX(KS, 2); else MI_MX(KS, 1); \
+    }
+    MI_MX_KS(2) else MI_MX_KS(4) else MI_MX_KS(8) else MI_MX_KS(16)
+#undef MI_MX_KS
+#undef MI_MX
+    MI_CHECK_LAUNCH("k_gemv_q4_0_mfma_x");
+    return MI_OK;
+}
+
+inline bool mfma_x_enabled() {
+    static const bool on = [] {
+        const char *e = getenv("MI_Q4_MFMA_X");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+// the grouped kernel needs whole groups of 4 blocks per row
+inline bool mfma_x_ok(int64_t k) { return mfma_x_enabled() && (k / QK) % 4 == 0; }
+
 int launch_gx(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16, float *y,
               const float *add = nullptr) {
     if (m >= 2 && m <= 16) return launch_mfma<false>(st, base, n, k, m, x16, y, add);
@@ -1125,7 +1339,8 @@ int mi_gemv_q4_0_f16_add(void *stream, const void *w_packed, const uint16_t *x_f
 }
 
 size_t mi_mul_mat_q4_0_workspace_size(int64_t m, int64_t k) {
-    if (m > 1 || k * 2 <= 64 * 1024) return 0;  // matrix cores read fp32 rows directly
+    if (m > 1) return mfma_x_ok(k) ? mi::align_up((size_t)m * k * 2, 256) : 0;  // permuted fp16 rows
+    if (k * 2 <= 64 * 1024) return 0;
     return mi::align_up((size_t)m * k * 2, 256);
 }
 
@@ -1136,7 +1351,15 @@ int mi_mul_mat_q4_0_f32(void *stream, const void *w_packed, const float *x, floa
     MI_CHECK_ARG(m >= 1 && m <= 16, "mul_mat_q4_0_f32: m=%lld not in 1..16", (long long)m);
     MI_CHECK_ARG(mi::aligned(w_packed, 256) && mi::aligned(x, 16), "mul_mat_q4_0_f32: w_packed must be 256-byte, x 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
-    if (m > 1) return launch_mfma<true>(st, (const uint8_t *)w_packed, n, k, m, x, y, nullptr);
+    if (m > 1) {
+        if (!mfma_x_ok(k)) return launch_mfma<true>(st, (const uint8_t *)w_packed, n, k, m, x, y, nullptr);
+        const size_t need = mi_mul_mat_q4_0_workspace_size(m, k);
+        if (!ws || ws_bytes < need || !mi::aligned(ws, 16)) {
+            mi::set_error("mul_mat_q4_0_f32: workspace %zu < %zu bytes (or misaligned)", ws_bytes, need);
+            return MI_ERR_WORKSPACE;
+        }
+        return launch_mfma_x(st, (const uint8_t *)w_packed, n, k, m, x, true, y, nullptr, ws);
+    }
     // one fp32 row: the register kernel (the fused chains' arithmetic, so that fused and
     // node-by-node graphs agree bit for bit) while the fp16 row fits 64 KB of LDS
     if (xr_enabled() && k / QK <= 1008) return launch_xr_gemv(st, (const uint8_t *)w_packed, n, k, x, true, y, nullptr);

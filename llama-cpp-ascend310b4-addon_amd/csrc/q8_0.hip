@@ -213,9 +213,8 @@ __device__ __forceinline__ int q8set_row_start(const Q8Set &S, int i) {
 // RMSNorm (optional), then the SmoothQuant reciprocal, then Q8_0 quantization of each
 // 32-block into LDS.  The caller puts a barrier between this and the reads of s_qs / s_d.
 template <int XN, bool NORM>
-__device__ __forceinline__ void xstage_quant(XStage<XN, NORM> &st, const float *__restrict__ inv_s, int k4, float eps,
-                                             int rounding, int8_t *s_qs, float *s_d, double *s_red, int tid) {
-    const float scale = xstage_scale(st, k4, eps, s_red, tid);
+__device__ __forceinline__ void xstage_quant(XStage<XN, NORM> &st, const float *__restrict__ inv_s, int k4,
+                                             float scale, int rounding, int8_t *s_qs, float *s_d, int tid) {
 #pragma unroll
     for (int t = 0; t < XN; t++) {
         const int f = tid + t * 256;  // float4 index; 8 consecutive threads form one 32-block
@@ -329,7 +328,92 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0_fused1(const Q8Set S, const f
     int4 lo[U], hi[U];
     uint32_t dw[U];
     q8_first_pass<G, U>(qlo, qhi, wd, rbase, nb, j, lo, hi, dw);
-    xstage_quant(st, inv_s, k4, eps, rounding, L.qs, L.d, L.red, tid);
+    const float scale = xstage_scale(st, k4, eps, L.red, tid);  // 1 without NORM
+    xstage_quant(st, inv_s, k4, scale, rounding, L.qs, L.d, tid);
+    __syncthreads();
+    const float s = q8_row_dot<G, U>(qlo, qhi, wd, rbase, nb, j, lo, hi, dw, L.qs, L.d);
+    if (row_ok && j == 0) {
+        const float *add = Q8SET_PICK(S, add, mi);
+        Q8SET_PICK(S, y, mi)[row] = add ? s + add[row] : s;
+    }
+}
+
+// The projection of an attention output still in flash-decoding split form: every
+// workgroup merges the splits' records (log-sum-exp combine) for the whole row in its
+// prologue, then scales by the SmoothQuant reciprocal and quantizes as fused1 does.
+// x[h*hd + i] = (sum_s w_s o_s[i]) / (sum_s w_s l_s), w_s = 2^(m_s - max_s m_s), 0 for a
+// split with no position (m_s = -inf), and x = 0 when the weight sum is 0.  One kernel
+// boundary replaces the combine launch; up to MAXS splits, k <= 1024*XN.
+template <int G, int U, int XN, int MAXS>
+__global__ __launch_bounds__(256) void k_gemv_q8_0_lse(const Q8Set S, const float *__restrict__ part, int n_splits,
+                                                       int hd, const float *__restrict__ inv_s, int n_total, int nb,
+                                                       int rounding) {
+    constexpr int RPB = 256 / G;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const FusedLds L = fused_lds(smem, nb);
+    const int tid = threadIdx.x;
+    const int j = tid % G;
+    const int grow = blockIdx.x * RPB + tid / G;
+    const bool row_ok = grow < n_total;
+    const int rc = min(grow, n_total - 1);
+    const int mi = q8set_index(S, rc);
+    const int row = rc - q8set_row_start(S, mi);
+    const uint8_t *qlo = Q8SET_PICK(S, qlo, mi);
+    const uint8_t *qhi = Q8SET_PICK(S, qhi, mi);
+    const uint16_t *wd = Q8SET_PICK(S, d, mi);
+    const int k4 = nb * (QK / 4);
+    const size_t rbase = (size_t)row * nb;
+    const int hd4 = hd / 4, ps = hd + 4;
+
+    // every split's record for this thread's float4s, loaded before the weights
+    float4 os[XN][MAXS], sv[XN];
+    float ms[XN][MAXS], ls[XN][MAXS];
+#pragma unroll
+    for (int t = 0; t < XN; t++) {
+        const int f = min(tid + t * 256, k4 - 1);
+        const float *ph = part + (size_t)(f / hd4) * n_splits * ps;
+#pragma unroll
+        for (int s = 0; s < MAXS; s++) {
+            const float *r = ph + (size_t)min(s, n_splits - 1) * ps;
+            os[t][s] = ((const float4 *)r)[f % hd4];
+            ms[t][s] = r[hd];
+            ls[t][s] = r[hd + 1];
+        }
+        if (inv_s) sv[t] = ((const float4 *)inv_s)[f];
+    }
+    int4 lo[U], hi[U];
+    uint32_t dw[U];
+    q8_first_pass<G, U>(qlo, qhi, wd, rbase, nb, j, lo, hi, dw);
+
+#pragma unroll
+    for (int t = 0; t < XN; t++) {
+        const int f = tid + t * 256;  // 8 consecutive threads form one 32-block
+        float mx = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < MAXS; s++)
+            if (s < n_splits) mx = fmaxf(mx, ms[t][s]);
+        float l = 0.0f;
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int s = 0; s < MAXS; s++) {
+            const float w = (s < n_splits && ms[t][s] != -INFINITY && mx != -INFINITY)
+                                ? __builtin_amdgcn_exp2f(ms[t][s] - mx) : 0.0f;
+            l = fmaf(ls[t][s], w, l);
+            a.x = fmaf(os[t][s].x, w, a.x);
+            a.y = fmaf(os[t][s].y, w, a.y);
+            a.z = fmaf(os[t][s].z, w, a.z);
+            a.w = fmaf(os[t][s].w, w, a.w);
+        }
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (l != 0.0f) v = make_float4(a.x / l, a.y / l, a.z / l, a.w / l);
+        if (inv_s) { v.x *= sv[t].x; v.y *= sv[t].y; v.z *= sv[t].z; v.w *= sv[t].w; }
+        float d;
+        const uint32_t q = quant4(v.x, v.y, v.z, v.w, rounding, d);
+        if (f < k4) {
+            *(uint32_t *)(L.qs + (size_t)f * 4) = q;
+            if ((f & 7) == 0) L.d[f >> 3] = h2f(f2h(d));
+        }
+    }
     __syncthreads();
     const float s = q8_row_dot<G, U>(qlo, qhi, wd, rbase, nb, j, lo, hi, dw, L.qs, L.d);
     if (row_ok && j == 0) {
@@ -370,7 +454,8 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0_qkv_rope(const Q8Set S, const
     int4 lo[U], hi[U];
     uint32_t dw[U];
     q8_first_pass<G, U>(qlo, qhi, wd, rbase, nb, j, lo, hi, dw);
-    xstage_quant(st, inv_s, k4, eps, rounding, L.qs, L.d, L.red, tid);
+    const float scale = xstage_scale(st, k4, eps, L.red, tid);  // 1 without NORM
+    xstage_quant(st, inv_s, k4, scale, rounding, L.qs, L.d, tid);
     __syncthreads();
     const float s = q8_row_dot<G, U>(qlo, qhi, wd, rbase, nb, j, lo, hi, dw, L.qs, L.d);
     if (j == 0) {
@@ -552,6 +637,38 @@ int launch_fused(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const f
                  float eps, const float *inv_s, int rounding) {
     if (norm_w) return launch_fused_n<true>(st, S, n_total, k, x, norm_w, eps, inv_s, rounding);
     return launch_fused_n<false>(st, S, n_total, k, x, nullptr, eps, inv_s, rounding);
+}
+
+template <int U, int XN, int MAXS>
+int launch_lse_u(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *part, int n_splits, int hd,
+                 const float *inv_s, int rounding) {
+    constexpr int G = 16, RPB = 256 / G;
+    const int nb = (int)(k / QK);
+    hipLaunchKernelGGL((k_gemv_q8_0_lse<G, U, XN, MAXS>), dim3((unsigned)((n_total + RPB - 1) / RPB)), dim3(256),
+                       fused_smem(nb), st, S, part, n_splits, hd, inv_s, n_total, nb, rounding);
+    MI_CHECK_LAUNCH("k_gemv_q8_0_lse");
+    return MI_OK;
+}
+
+template <int XN, int MAXS>
+int launch_lse_x(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *part, int n_splits, int hd,
+                 const float *inv_s, int rounding) {
+    switch (pick_u(k / QK, 16)) {  // k <= 2048: at most 4 blocks per lane
+        case 1: return launch_lse_u<1, XN, MAXS>(st, S, n_total, k, part, n_splits, hd, inv_s, rounding);
+        case 2: return launch_lse_u<2, XN, MAXS>(st, S, n_total, k, part, n_splits, hd, inv_s, rounding);
+        case 3: return launch_lse_u<3, XN, MAXS>(st, S, n_total, k, part, n_splits, hd, inv_s, rounding);
+        default: return launch_lse_u<4, XN, MAXS>(st, S, n_total, k, part, n_splits, hd, inv_s, rounding);
+    }
+}
+
+int launch_lse(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *part, int n_splits, int hd,
+               const float *inv_s, int rounding) {
+    const bool x1 = k <= 1024;
+    if (n_splits <= 4)
+        return x1 ? launch_lse_x<1, 4>(st, S, n_total, k, part, n_splits, hd, inv_s, rounding)
+                  : launch_lse_x<2, 4>(st, S, n_total, k, part, n_splits, hd, inv_s, rounding);
+    return x1 ? launch_lse_x<1, 16>(st, S, n_total, k, part, n_splits, hd, inv_s, rounding)
+              : launch_lse_x<2, 16>(st, S, n_total, k, part, n_splits, hd, inv_s, rounding);
 }
 
 template <int G, int U, int XN, bool NORM>
@@ -767,6 +884,26 @@ int mi_mul_mat_q8_0_f32_fused(void *stream, int n_mats, const void *const *w_pac
     int n_total = 0;
     if (int r = make_set(S, n_mats, w_packed, n, y, k, n_total, add)) return r;
     return launch_fused((hipStream_t)stream, S, n_total, k, x, norm_w, eps, inv_s, rounding);
+}
+
+int mi_mul_mat_q8_0_f32_lse(void *stream, const void *w_packed, int64_t n, float *y, const float *add,
+                            const float *part, int64_t n_splits, int64_t n_heads, int64_t head_dim,
+                            const float *inv_s, int rounding) {
+    MI_CHECK_ARG(w_packed && y && part, "mul_mat_q8_0_f32_lse: null pointer");
+    MI_CHECK_ARG(n_heads > 0 && head_dim > 0 && head_dim % 4 == 0 && head_dim <= 1024,
+                 "mul_mat_q8_0_f32_lse: bad heads %lld x %lld", (long long)n_heads, (long long)head_dim);
+    const int64_t k = n_heads * head_dim;
+    if (int r = check_shape("mul_mat_q8_0_f32_lse", n, k)) return r;
+    MI_CHECK_ARG(k <= 2048, "mul_mat_q8_0_f32_lse: k=%lld > 2048", (long long)k);
+    MI_CHECK_ARG(n_splits >= 1 && n_splits <= 16, "mul_mat_q8_0_f32_lse: %lld splits not in 1..16",
+                 (long long)n_splits);
+    MI_CHECK_ARG(mi::aligned(part, 16) && (!inv_s || mi::aligned(inv_s, 16)),
+                 "mul_mat_q8_0_f32_lse: part/inv_s must be 16-byte aligned");
+    Q8Set S;
+    int n_total = 0;
+    const float *adds[1] = {add};
+    if (int r = make_set(S, 1, &w_packed, &n, &y, k, n_total, adds)) return r;
+    return launch_lse((hipStream_t)stream, S, n_total, k, part, (int)n_splits, (int)head_dim, inv_s, rounding);
 }
 
 int mi_qkv_rope_kv_q8_0(void *stream, const void *const *w_packed, const int64_t *n, const float *const *bias,

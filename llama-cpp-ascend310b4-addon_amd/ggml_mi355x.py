@@ -89,6 +89,8 @@ _SIGS = {
     "mi_fa_decode_batch_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "mi_fa_decode_batch": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _SZ, _SZ, _SZ, _SZ, _F, _P, _I64, _SZ,
                                 _SZ, _SZ, _SZ, _SZ, _P, _SZ]),
+    "mi_fa_decode_num_splits": (_I64, [_I64, _I64, _I64, _I64]),
+    "mi_fa_decode_partials": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _SZ, _SZ, _SZ, _SZ, _F, _P, _SZ]),
     "mi_mul_mat_q8_0_f32_multi": (_I, [_P, _I, _P, _P, _P, _I64, _P, _P, _I, _P, _SZ]),
     "mi_rms_norm": (_I, [_P, _P, _P, _P, _I64, _I64, _F]),
     "mi_add_bcast": (_I, [_P, _P, _P, _P, _I64, _I64]),
@@ -100,6 +102,7 @@ _SIGS = {
     "mi_argmax_workspace_size": (_SZ, [_I64, _I64]),
     "mi_argmax": (_I, [_P, _P, _P, _I64, _I64, _P, _SZ]),
     "mi_mul_mat_q8_0_f32_fused": (_I, [_P, _I, _P, _P, _P, _P, _I64, _P, _P, _F, _P, _I]),
+    "mi_mul_mat_q8_0_f32_lse": (_I, [_P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _I]),
     "mi_mul_mat_q4_0_f32_fused": (_I, [_P, _I, _P, _P, _P, _P, _I64, _P, _P, _F]),
     "mi_gate_up_swiglu_q4_0": (_I, [_P, _P, _P, _I64, _I64, _P, _P, _F, _P]),
     "mi_qkv_rope_kv_q4_0": (_I, [_P, _P, _P, _P, _I64, _P, _P, _F, _I64, _P, _F, _F, _F, _P, _P, _SZ, _P, _SZ,

@@ -308,6 +308,78 @@ def test_gemv_q8_0_add_equals_gemv_plus_vector(gpu):
     assert np.array_equal(y1.download(F32), (y0.download(F32) + add).astype(F32))
 
 
+def _fa_splits(mi, n_kv, nq, nkv, d):
+    return int(mi.lib().mi_fa_decode_num_splits(n_kv, nq, nkv, d))
+
+
+# (n_kv, q heads, kv heads, head dim, kv_len, mask): 1, 4, 11 (two empty), 13, 16 splits
+@pytest.mark.parametrize("L,nq,nkv,d,kv_len,masked", [(64, 12, 2, 128, None, False), (200, 12, 2, 128, None, False),
+                                                      (700, 12, 2, 128, 517, False), (777, 8, 4, 64, None, False),
+                                                      (1024, 12, 2, 128, None, True)])
+def test_fa_partials_into_q8_projection(gpu, orc, L, nq, nkv, d, kv_len, masked):
+    """Attention left in split form, merged in the o projection's prologue (+ residual):
+    against the oracle's exact attention through the oracle's Q8_0 matmul (GEMV bar), and
+    against the unfused FA + combine + fused GEMV launches of this library."""
+    mi = gpu
+    S = _fa_splits(mi, L, nq, nkv, d)
+    assert 1 <= S <= 16
+    k = nq * d
+    n = k
+    rng = np.random.default_rng(L + nq + d)
+    q = rng.standard_normal((nq, d)).astype(F32)
+    kc = f16_bits(rng.standard_normal((L, nkv, d)))
+    vc = f16_bits(rng.standard_normal((L, nkv, d)))
+    mask = None
+    if masked:
+        mf = np.zeros(L, F32)
+        mf[L - 100:] = -np.inf
+        mf[10:20] = -np.inf
+        mf[33] = -2.5
+        mask = f16_bits(mf)
+    w = q8_0_weights(rng, n, k)
+    inv = (1.0 / rng.uniform(0.5, 2.0, k)).astype(F32)
+    add = rng.standard_normal(n).astype(F32)
+    pw = _packed_q8(mi, w, n, k)
+    dq, dk, dv = mi.to_device(q), mi.to_device(kc), mi.to_device(vc)
+    dm = mi.to_device(mask) if mask is not None else None
+    dl = mi.to_device(np.array([kv_len], np.int32)) if kv_len is not None else None
+    dinv, dadd = mi.to_device(inv), mi.to_device(add)
+    wsb = mi.fa_decode_workspace_size(L, nq, nkv, d)
+    ws = mi.DeviceBuffer(wsb).zero()
+    nb1 = nkv * d * 2
+    y = mi.DeviceBuffer(4 * n)
+    P = mi._P
+    mi._call("mi_fa_decode_partials", None, P(dq.ptr), P(dk.ptr), P(dv.ptr), P(dm.ptr if dm else None),
+             P(dl.ptr if dl else None), L, nq, nkv, d, nb1, d * 2, nb1, d * 2, F32(1 / np.sqrt(d)), P(ws.ptr), wsb)
+    mi._call("mi_mul_mat_q8_0_f32_lse", None, P(pw.ptr), n, P(y.ptr), P(dadd.ptr), P(ws.ptr), S, nq, d,
+             P(dinv.ptr), mi.Q8_ROUND_X86)
+    # the unfused launches on the same inputs
+    att = mi.DeviceBuffer(4 * k)
+    ws2 = mi.DeviceBuffer(wsb).zero()
+    y2 = mi.DeviceBuffer(4 * n)
+    mi.fa_decode(dq.ptr, dk.ptr, dv.ptr, dm.ptr if dm else None, dl.ptr if dl else None, L, nq, nkv, d, nb1, d * 2,
+                 nb1, d * 2, 1 / np.sqrt(d), att.ptr, ws2.ptr, wsb)
+    mi._call("mi_mul_mat_q8_0_f32_fused", None, 1, _ptrs(pw), _i64s(n), _ptrs(y2), _ptrs(dadd), k, P(att.ptr),
+             P(None), F32(0.0), P(dinv.ptr), mi.Q8_ROUND_X86)
+    mi.device_sync()
+    got, unfused = y.download(F32), y2.download(F32)
+    exact = orc.flash_attn_ext_1tok(q, kc, vc, nkv, F32(1 / np.sqrt(d)), mask=mask, kv_len=kv_len, mode=1)
+    ref = (_q8_ref(orc, w, exact.reshape(-1).astype(F32), n, k, inv) + add).astype(F32)
+    e_ref, e_unf = rel_err(got, ref), rel_err(got, unfused)
+    print(f"lse projection S={S}: rel vs oracle {e_ref:.2e}, vs unfused {e_unf:.2e}")
+    assert e_ref < GEMV_TOL
+    assert e_unf < GEMV_TOL
+
+
+def test_q8_lse_projection_rejects_bad_shapes(gpu):
+    mi = gpu
+    P = mi._P
+    with pytest.raises(mi.MiError):  # more splits than the prologue merges
+        mi._call("mi_mul_mat_q8_0_f32_lse", None, P(256), 1536, P(256), P(None), P(256), 17, 12, 128, P(None), 0)
+    with pytest.raises(mi.MiError):  # k above 2048
+        mi._call("mi_mul_mat_q8_0_f32_lse", None, P(256), 3584, P(256), P(None), P(256), 4, 28, 128, P(None), 0)
+
+
 # ---------------------------------------------------------------- W4A16 chains (one activation row)
 
 def _packed_q4(mi, w, n, k):

@@ -118,6 +118,35 @@ def test_fused_graph_matches_unfused(gpu, monkeypatch, wtype):
     plain.free()
 
 
+@pytest.mark.parametrize("wtype", [qs.GGML_TYPE_Q8_0, qs.GGML_TYPE_Q4_0])
+def test_fused_graph_matches_unfused_long_context(gpu, monkeypatch, wtype):
+    """As above from a 600-position cache (KV view of 768 rows: 12 attention splits, merged
+    in the o projection's prologue on the A8W8 path)."""
+    mi = gpu
+    hp = qs.qwen2_1p5b(n_layer=2, n_ctx=1024, wtype=wtype)
+    tensors, smooth = qs.synth(hp, seed=19, qk_gain=6.0)
+    fused = mi.Qwen2Model(hp)
+    fused.load(tensors, smooth)
+    monkeypatch.setenv("GGML_MI355X_FUSION", "0")
+    plain = mi.Qwen2Model(hp)
+    plain.load(tensors, smooth)
+    start = 600
+    fused.fill_cache(start, seed=3, scale=1.0)
+    plain.fill_cache(start, seed=3, scale=1.0)
+    tok = 17
+    worst = 0.0
+    for pos in range(start, start + 8):
+        tok_f, lf = fused.decode(tok, pos, want_logits=True)
+        tok_p, lp = plain.decode(tok, pos, want_logits=True)
+        worst = max(worst, float(np.abs(lf - lp).max() / np.abs(lp).max()))
+        assert tok_f == tok_p, f"position {pos}"
+        tok = tok_f
+    print(f"fused vs node-by-node at context {start}: max rel {worst:.3e}")
+    assert worst < 1e-4
+    fused.free()
+    plain.free()
+
+
 @pytest.mark.parametrize("wtype", [qs.GGML_TYPE_Q4_0, qs.GGML_TYPE_Q8_0])
 def test_qwen2_batch_of_sequences(gpu, orc, wtype):
     """Three sequences decoded together (one ubatch of 3 tokens per step, per-sequence KV
