@@ -143,6 +143,17 @@ int mi_mul_mat_q8_0_f32_fused(void *stream, int n_mats, const void *const *w_pac
 int mi_mul_mat_q8_0_f32_lse(void *stream, const void *w_packed, int64_t n, float *y, const float *add,
                             const float *part, int64_t n_splits, int64_t n_heads, int64_t head_dim,
                             const float *inv_s, int rounding);
+/* Several activation rows (m in 1..16: the tokens of one ubatch, e.g. one per sequence) through
+ * n_mats Q4_0 MUL_MATs of equal k that read the same activation (q/k/v, gate/up), in one launch
+ * after one fp16 conversion of the activation: y[i] = W_i x (+ bias[i] broadcast over the rows)
+ * (+ add[i], a full [m][n[i]] tensor: the residual), each optional (bias / add or their entries
+ * may be NULL).  x: fp32 [m][k]; with up != NULL the activation is ggml swiglu(x, up) =
+ * x / (1 + expf(-x)) * up (the GLU node before the down projection).  k % 128 == 0; ws of
+ * m*k*2 bytes, 16-byte aligned.  Replaces, per matrix, the ggml_cann_mat_mul_fp route for a
+ * batch of rows (patch:1207) and the ADD / GLU nodes around it. */
+int mi_mul_mat_q4_0_f32_batch(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
+                              float *const *y, const float *const *bias, const float *const *add, int64_t k,
+                              int64_t m, const float *x, const float *up, void *ws, size_t ws_bytes);
 /* the attention-input chain of one token: [RMS_NORM -> MUL(norm_w)] -> q/k/v MUL_MATs
  * (w_packed[0..2], n[0..2] rows, k <= 4096) -> ADD bias[i] (or NULL) -> neox ROPE of q
  * and k (n_dims = head_dim, theta = pos[0] * freq_base^(-2i/head_dim), freq_scale,
@@ -276,6 +287,16 @@ int mi_mul_bcast(void *stream, const float *a, const float *b, float *d, int64_t
 int mi_rope_neox(void *stream, const float *x, float *y, const int32_t *pos, int64_t ne0, int64_t ne1, int64_t ne2,
                  int64_t n_dims, float freq_base, float freq_scale, float attn_factor, size_t nb1, size_t nb2,
                  size_t ob1, size_t ob2);
+/* ROPE q, ROPE k (neox over all head_dim dims; activation row r at position pos[r]), then
+ * SET_ROWS of the rotated k and of v (fp32 -> fp16) into cache rows kv_idx[r] (skipped when
+ * outside [0, n_cache_rows)): the four nodes after the q/k/v projections of a ubatch of m
+ * tokens in one launch.  q [m][n_head_q*head_dim], k [m][n_head_k*head_dim], v [m][n_v]
+ * fp32; q_out like q.  Per element the arithmetic of mi_rope_neox and mi_set_rows_f16.
+ * Replaces the CANN RoPE and KV writes (patch:1360-1363, 1179-1184). */
+int mi_rope_kv_rows(void *stream, const float *q, const float *k, const float *v, float *q_out, void *k_cache,
+                    size_t k_row_bytes, void *v_cache, size_t v_row_bytes, const int32_t *pos, const void *kv_idx,
+                    int kv_idx_is_i64, int64_t n_cache_rows, int64_t m, int64_t head_dim, int64_t n_head_q,
+                    int64_t n_head_k, int64_t n_v, float freq_base, float freq_scale, float attn_factor);
 /* the rotation table of mi_rope_neox for one position: table[p] = cos(theta_p) *
  * attn_factor, table[head_dim/2 + p] = sin(theta_p) * attn_factor (p < head_dim/2).  The
  * fused q/k/v chains take it instead of forming the angles per launch (the backend

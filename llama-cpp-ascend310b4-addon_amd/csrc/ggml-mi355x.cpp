@@ -549,6 +549,9 @@ void run_fa(BackendCtx *ctx, ggml_tensor *node) {
 //                                                          mi_gemv_q8_0_add
 //   attention + o   : FLASH_ATTN_EXT, MUL_MAT, [ADD]     -> mi_fa_decode_partials +
 //                                                          mi_mul_mat_q8_0_f32_lse
+//   ubatch (Q4_0)   : MUL_MAT x1..4 [ADD bias each] or MUL_MAT ADD(residual), and
+//                     GLU swiglu, MUL_MAT, [ADD]          -> mi_mul_mat_q4_0_f32_batch
+//   rope + kv write : ROPE q, ROPE k, SET_ROWS k, SET_ROWS v -> mi_rope_kv_rows
 
 using Consumers = std::unordered_map<const ggml_tensor *, std::vector<const ggml_tensor *>>;
 
@@ -948,6 +951,154 @@ int try_fuse_fa_o(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
     return (ad ? next_real(g, j + 1) : j) + 1 - i;
 }
 
+// ---- several activation rows (a ubatch of tokens) through Q4_0 weights
+
+// a Q4_0 MUL_MAT on 2..16 contiguous fp32 activation rows with the prepacked copy ready
+bool q4_batch_node(const ggml_tensor *n) {
+    if (n->op != GGML_OP_MUL_MAT) return false;
+    const ggml_tensor *a = n->src[0], *b = n->src[1];
+    const TensorExtra *ex = (const TensorExtra *)a->extra;
+    const int64_t m = ggml_nrows(b);
+    return a->type == GGML_TYPE_Q4_0 && ex && ex->ready && b->type == GGML_TYPE_F32 && ggml_is_contiguous(b) &&
+           b->ne[1] == m && m >= 2 && m <= 16 && a->ne[0] % 128 == 0 && is_f32_contig(n);
+}
+
+// ADD(mm, other) as mm's only consumer: other is a bias row of mm's width (broadcast over
+// the rows) or a tensor of mm's shape (the residual)
+const ggml_tensor *batch_add_tail(ggml_cgraph *g, int j, const ggml_tensor *mm, const Consumers &C,
+                                  const ggml_tensor *&other, bool &is_bias) {
+    const int k = next_real(g, j + 1);
+    if (k >= ggml_graph_n_nodes(g)) return nullptr;
+    const ggml_tensor *ad = ggml_graph_node(g, k);
+    if (ad->op != GGML_OP_ADD || ad->src[0] != mm || !is_f32_contig(ad) || !ggml_are_same_shape(ad, mm)) return nullptr;
+    const ggml_tensor *o = ad->src[1];
+    if (!is_f32_contig(o) || o == mm || !only_consumed_by(C, mm, {ad})) return nullptr;
+    if (ggml_nelements(o) == mm->ne[0] && o->ne[0] == mm->ne[0]) is_bias = true;
+    else if (ggml_are_same_shape(o, mm)) is_bias = false;
+    else return nullptr;
+    other = o;
+    return ad;
+}
+
+// MUL_MAT x 1..4 (Q4_0, same activation rows) [-> ADD bias per matrix, in order] or
+// MUL_MAT -> ADD(residual): one conversion of the activation, one launch
+int try_fuse_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    const int nn = ggml_graph_n_nodes(g);
+    ggml_tensor *mm0 = ggml_graph_node(g, i);
+    if (!q4_batch_node(mm0)) return 0;
+    const ggml_tensor *mm[4] = {mm0};
+    int cnt = 1, last = i;
+    while (cnt < 4) {
+        const int j = next_real(g, last + 1);
+        if (j >= nn) break;
+        const ggml_tensor *nx = ggml_graph_node(g, j);
+        if (!q4_batch_node(nx) || nx->src[1] != mm0->src[1] || nx->src[0]->ne[0] != mm0->src[0]->ne[0]) break;
+        mm[cnt++] = nx;
+        last = j;
+    }
+    // the ADD of each matrix's output, adjacent after the group in matrix order
+    const ggml_tensor *ad[4] = {}, *other[4] = {};
+    bool bias[4] = {};
+    int tail = last;
+    bool all_add = true;
+    for (int t = 0; t < cnt && all_add; t++) {
+        const ggml_tensor *a = batch_add_tail(g, tail, mm[t], C, other[t], bias[t]);
+        if (!a || (cnt > 1 && !bias[t])) all_add = false;
+        ad[t] = a;
+        if (a) tail = next_real(g, tail + 1);
+    }
+    if (!all_add) tail = last;
+    if (cnt == 1 && !all_add) return 0;  // a lone matmul takes the plain path
+    const void *w[4];
+    int64_t n[4];
+    float *y[4];
+    const float *bv[4], *av[4];
+    for (int t = 0; t < cnt; t++) {
+        w[t] = ((const TensorExtra *)mm[t]->src[0]->extra)->packed;
+        n[t] = mm[t]->src[0]->ne[1];
+        y[t] = (float *)(all_add ? ad[t]->data : mm[t]->data);
+        bv[t] = all_add && bias[t] ? (const float *)other[t]->data : nullptr;
+        av[t] = all_add && !bias[t] ? (const float *)other[t]->data : nullptr;
+    }
+    const int64_t k = mm0->src[0]->ne[0], m = ggml_nrows(mm0->src[1]);
+    MI_K_CHECK(mi_mul_mat_q4_0_f32_batch(ctx->stream, cnt, w, n, y, bv, av, k, m, (const float *)mm0->src[1]->data,
+                                         nullptr, ctx->scratch, ctx->scratch_size));
+    return tail + 1 - i;
+}
+
+// GLU swiglu (gate, up: 2..16 rows) -> MUL_MAT(Q4_0) [-> ADD residual]: the swiglu is
+// formed while the activation is converted for the matrix cores
+int try_fuse_glu_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    const ggml_tensor *glu = ggml_graph_node(g, i);
+    if (glu->op != GGML_OP_GLU || !supports_op_impl(glu) || !glu->src[1] || !is_f32_contig(glu->src[0]) ||
+        !is_f32_contig(glu->src[1]) || !ggml_are_same_shape(glu->src[0], glu->src[1]))
+        return 0;
+    const int j = next_real(g, i + 1);
+    if (j >= ggml_graph_n_nodes(g)) return 0;
+    const ggml_tensor *mm = ggml_graph_node(g, j);
+    if (!q4_batch_node(mm) || mm->src[1] != glu || !only_consumed_by(C, glu, {mm})) return 0;
+    const ggml_tensor *other = nullptr;
+    bool is_bias = false;
+    const ggml_tensor *ad = batch_add_tail(g, j, mm, C, other, is_bias);
+    const void *w = ((const TensorExtra *)mm->src[0]->extra)->packed;
+    const int64_t n = mm->src[0]->ne[1], k = mm->src[0]->ne[0], m = ggml_nrows(glu);
+    float *y = (float *)(ad ? ad->data : mm->data);
+    const float *bv = ad && is_bias ? (const float *)other->data : nullptr;
+    const float *av = ad && !is_bias ? (const float *)other->data : nullptr;
+    MI_K_CHECK(mi_mul_mat_q4_0_f32_batch(ctx->stream, 1, &w, &n, &y, &bv, &av, k, m, (const float *)glu->src[0]->data,
+                                         (const float *)glu->src[1]->data, ctx->scratch, ctx->scratch_size));
+    return (ad ? next_real(g, j + 1) : j) + 1 - i;
+}
+
+// ROPE q, ROPE k (same positions and parameters, all head dims rotated), SET_ROWS of the
+// rotated k, SET_ROWS of v (same row indices): one launch over the ubatch's rows
+int try_fuse_rope_kv(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    const int nn = ggml_graph_n_nodes(g);
+    const ggml_tensor *rope[2], *sr[2];
+    int j = i;
+    for (int t = 0; t < 2; t++) {
+        if (t) j = next_real(g, j + 1);
+        if (j >= nn) return 0;
+        rope[t] = ggml_graph_node(g, j);
+        const ggml_tensor *x = rope[t]->src[0];
+        if (rope[t]->op != GGML_OP_ROPE || !supports_op_impl(rope[t]) || !is_f32_contig(x) || !is_f32_contig(rope[t]) ||
+            rope[t]->op_params[1] != x->ne[0] || x->ne[3] != 1)
+            return 0;
+    }
+    const int64_t hd = rope[0]->src[0]->ne[0], m = rope[0]->src[0]->ne[2];
+    const ggml_tensor *pos = rope[0]->src[1];
+    if (rope[1]->src[0]->ne[0] != hd || rope[1]->src[0]->ne[2] != m || rope[1]->src[1] != pos ||
+        ggml_nelements(pos) != m || hd > 256 ||
+        memcmp(rope[0]->op_params + 5, rope[1]->op_params + 5, 4 * sizeof(int32_t)) != 0)
+        return 0;
+    for (int t = 0; t < 2; t++) {
+        j = next_real(g, j + 1);
+        if (j >= nn) return 0;
+        sr[t] = ggml_graph_node(g, j);
+        const ggml_tensor *src = sr[t]->src[0];
+        if (sr[t]->op != GGML_OP_SET_ROWS || !supports_op_impl(sr[t]) || !is_f32_contig(src) || ggml_nrows(src) != m ||
+            ggml_nelements(sr[t]->src[1]) != m || (t == 1 && sr[1]->src[1] != sr[0]->src[1]))
+            return 0;
+    }
+    if (alias_root(sr[0]->src[0]) != rope[1] || sr[0]->src[0]->ne[0] != rope[1]->src[0]->ne[1] * hd ||
+        !only_consumed_by(C, rope[1], {sr[0]}))
+        return 0;
+    const ggml_tensor *v = sr[1]->src[0];
+    // q_out is written while other workgroups read k and v
+    if (overlaps(rope[0], alias_root(rope[1]->src[0])) || overlaps(rope[0], v)) return 0;
+    float freq_base, freq_scale, attn_factor;
+    memcpy(&freq_base, (const float *)rope[0]->op_params + 5, sizeof(float));
+    memcpy(&freq_scale, (const float *)rope[0]->op_params + 6, sizeof(float));
+    memcpy(&attn_factor, (const float *)rope[0]->op_params + 8, sizeof(float));
+    const ggml_tensor *idx = sr[0]->src[1];
+    MI_K_CHECK(mi_rope_kv_rows(ctx->stream, (const float *)rope[0]->src[0]->data, (const float *)rope[1]->src[0]->data,
+                               (const float *)v->data, (float *)rope[0]->data, sr[0]->data, sr[0]->nb[1], sr[1]->data,
+                               sr[1]->nb[1], (const int32_t *)pos->data, idx->data, idx->type == GGML_TYPE_I64,
+                               std::min(sr[0]->ne[1], sr[1]->ne[1]), m, hd, rope[0]->src[0]->ne[1],
+                               rope[1]->src[0]->ne[1], v->ne[0], freq_base, freq_scale, attn_factor));
+    return j + 1 - i;
+}
+
 // Runs node i (and, when fused, the nodes it absorbs); returns the number of nodes consumed.
 int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
     ggml_tensor *node = ggml_graph_node(g, i);
@@ -958,6 +1109,7 @@ int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
         case GGML_OP_MUL_MAT: {
             if (fuse) {
                 if (int used = try_fuse_matmul_add(ctx, g, i, C)) return used;
+                if (int used = try_fuse_q4_batch(ctx, g, i, C)) return used;
             }
             // consecutive Q8_0 GEMVs reading the same activation (q/k/v, gate/up): one grouped launch
             if (fuse && node->src[0]->type == GGML_TYPE_Q8_0 && node->src[1]->ne[1] == 1 &&
@@ -1019,6 +1171,9 @@ int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
             return 1;
         }
         case GGML_OP_ROPE: {
+            if (fuse) {
+                if (int used = try_fuse_rope_kv(ctx, g, i, C)) return used;
+            }
             const ggml_tensor *x = node->src[0];
             float freq_base, freq_scale, attn_factor;
             memcpy(&freq_base, (const float *)node->op_params + 5, sizeof(float));
@@ -1045,6 +1200,7 @@ int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
         case GGML_OP_GLU:
             if (fuse) {
                 if (int used = try_fuse_glu_matmul(ctx, g, i, C)) return used;
+                if (int used = try_fuse_glu_q4_batch(ctx, g, i, C)) return used;
             }
             MI_K_CHECK(mi_swiglu(st, (const float *)node->src[0]->data, (const float *)node->src[1]->data,
                                  (float *)node->data, ggml_nelements(node)));

@@ -143,6 +143,49 @@ __global__ void k_set_rows_f16(const float *__restrict__ src, const IDX *__restr
     for (int i = threadIdx.x; i < ne0; i += blockDim.x) d[i] = f2h(s[i]);
 }
 
+// ROPE q and ROPE k (neox over all hd dims, position pos[r] for activation row r), then
+// SET_ROWS of the rotated k and of v into their fp16 cache rows kv_idx[r]: the four nodes
+// after the q/k/v projections in one launch for m rows.  Per element the arithmetic of
+// k_rope_neox and k_set_rows_f16.  grid (n_hq + n_hk + ceil(n_v / 128), m), 128 threads.
+template <typename IDX>
+__global__ __launch_bounds__(128) void k_rope_kv_rows(const float *__restrict__ q, const float *__restrict__ k,
+                                                      const float *__restrict__ v, float *__restrict__ q_out,
+                                                      uint8_t *__restrict__ kc, uint8_t *__restrict__ vc,
+                                                      const int32_t *__restrict__ pos, const IDX *__restrict__ kv_idx,
+                                                      int hd, int n_hq, int n_hk, int n_v, size_t k_row_bytes,
+                                                      size_t v_row_bytes, int64_t n_cache_rows, float theta_scale,
+                                                      float freq_scale, float attn_factor) {
+    const int b = blockIdx.x, r = blockIdx.y, i = threadIdx.x;
+    const int64_t ci = (int64_t)kv_idx[r];
+    const bool ci_ok = ci >= 0 && ci < n_cache_rows;
+    if (b < n_hq + n_hk) {
+        const int half = hd / 2;
+        if (i >= half) return;
+        const bool is_q = b < n_hq;
+        const float *xr = is_q ? q + ((size_t)r * n_hq + b) * hd : k + ((size_t)r * n_hk + (b - n_hq)) * hd;
+        float theta = (float)pos[r];
+        for (int t = 0; t < i; t++) theta *= theta_scale;  // same product order as the CPU cache
+        const float th = freq_scale * theta;
+        const float c = cosf(th) * attn_factor;
+        const float s = sinf(th) * attn_factor;
+        const float x0 = xr[i], x1 = xr[i + half];
+        const float y0 = mul_sub_mul_rn(x0, c, x1, s);
+        const float y1 = mul_add_mul_rn(x0, s, x1, c);
+        if (is_q) {
+            float *yr = q_out + ((size_t)r * n_hq + b) * hd;
+            yr[i] = y0;
+            yr[i + half] = y1;
+        } else if (ci_ok) {
+            uint16_t *kr = (uint16_t *)(kc + (size_t)ci * k_row_bytes) + (size_t)(b - n_hq) * hd;
+            kr[i] = f2h(y0);
+            kr[i + half] = f2h(y1);
+        }
+    } else {
+        const int j = (b - n_hq - n_hk) * 128 + i;
+        if (j < n_v && ci_ok) ((uint16_t *)(vc + (size_t)ci * v_row_bytes))[j] = f2h(v[(size_t)r * n_v + j]);
+    }
+}
+
 template <typename T, typename IDX>
 __global__ void k_get_rows(const T *__restrict__ src, const IDX *__restrict__ idx, float *__restrict__ dst, int ne0,
                            size_t snb1, int64_t n_src_rows) {
@@ -279,6 +322,30 @@ int mi_rope_neox(void *stream, const float *x, float *y, const int32_t *pos, int
     hipLaunchKernelGGL(k_rope_neox, dim3((unsigned)ne1, (unsigned)ne2), dim3(threads), 0, (hipStream_t)stream, x, y,
                        pos, (int)ne0, (int)ne1, (int)n_dims, theta_scale, freq_scale, attn_factor, nb1, nb2, ob1, ob2);
     MI_CHECK_LAUNCH("k_rope_neox");
+    return MI_OK;
+}
+
+int mi_rope_kv_rows(void *stream, const float *q, const float *k, const float *v, float *q_out, void *k_cache,
+                    size_t k_row_bytes, void *v_cache, size_t v_row_bytes, const int32_t *pos, const void *kv_idx,
+                    int kv_idx_is_i64, int64_t n_cache_rows, int64_t m, int64_t head_dim, int64_t n_head_q,
+                    int64_t n_head_k, int64_t n_v, float freq_base, float freq_scale, float attn_factor) {
+    MI_CHECK_ARG(q && k && v && q_out && k_cache && v_cache && pos && kv_idx, "rope_kv_rows: null pointer");
+    MI_CHECK_ARG(m >= 1 && m <= 65535 && head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 256 && n_head_q > 0 &&
+                     n_head_k > 0 && n_v > 0 && n_head_q + n_head_k + (n_v + 127) / 128 < (1 << 30),
+                 "rope_kv_rows: bad shape");
+    MI_CHECK_ARG(k_row_bytes >= (size_t)(n_head_k * head_dim * 2) && v_row_bytes >= (size_t)(n_v * 2),
+                 "rope_kv_rows: cache rows too short");
+    const float theta_scale = powf(freq_base, -2.0f / (float)head_dim);
+    const dim3 grid((unsigned)(n_head_q + n_head_k + (n_v + 127) / 128), (unsigned)m);
+#define MI_RKV(IDX)                                                                                                \
+    hipLaunchKernelGGL((k_rope_kv_rows<IDX>), grid, dim3(128), 0, (hipStream_t)stream, q, k, v, q_out,             \
+                       (uint8_t *)k_cache, (uint8_t *)v_cache, pos, (const IDX *)kv_idx, (int)head_dim,            \
+                       (int)n_head_q, (int)n_head_k, (int)n_v, k_row_bytes, v_row_bytes, n_cache_rows, theta_scale, \
+                       freq_scale, attn_factor)
+    if (kv_idx_is_i64) MI_RKV(int64_t);
+    else MI_RKV(int32_t);
+#undef MI_RKV
+    MI_CHECK_LAUNCH("k_rope_kv_rows");
     return MI_OK;
 }
 

@@ -337,6 +337,51 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma(const uint8_t *__res
     }
 }
 
+// Selecting a matrix's pointer: the four candidates pass through an empty asm
+// statement first, so the select works on register values.  A select between plain
+// loads of the by-value kernel argument would be rewritten into a load from a computed
+// address, which copies the struct to scratch memory.
+template <class T>
+__device__ __forceinline__ T opaque_s(T v) {
+    if constexpr (sizeof(T) == 8) {
+        uint64_t u = (uint64_t)v;
+        asm volatile("" : "+s"(u));
+        return (T)u;
+    } else {
+        uint32_t u = (uint32_t)v;
+        asm volatile("" : "+s"(u));
+        return (T)u;
+    }
+}
+
+template <class T>
+__device__ __forceinline__ T pick4(int i, T a0, T a1, T a2, T a3) {
+    return i >= 3 ? a3 : i >= 2 ? a2 : i >= 1 ? a1 : a0;
+}
+
+// global-address-space accesses from integer addresses (the picked pointers are
+// plain integers after the register select; a generic pointer would give flat loads,
+// which also count against the LDS counter)
+#define MI_GLOBAL __attribute__((address_space(1)))
+__device__ __forceinline__ int4 ldg_stream16(uint64_t a) {
+    const int4v_t v = __builtin_nontemporal_load((const MI_GLOBAL int4v_t *)a);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ldg_u16(uint64_t a) { return *(const MI_GLOBAL uint16_t *)a; }
+__device__ __forceinline__ float ldg_f32(uint64_t a) { return *(const MI_GLOBAL float *)a; }
+__device__ __forceinline__ void stg_f32(uint64_t a, float v) { *(MI_GLOBAL float *)a = v; }
+__device__ __forceinline__ void stg_u16(uint64_t a, uint16_t v) { *(MI_GLOBAL uint16_t *)a = v; }
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 ldg_u4(uint64_t a) {
+    const u32x4_t v = *(const MI_GLOBAL u32x4_t *)a;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ldg_u2(uint64_t a) {
+    const u32x2_t v = *(const MI_GLOBAL u32x2_t *)a;
+    return make_uint2(v.x, v.y);
+}
+
 // Several activation rows on the matrix cores with the activation as the A operand:
 // D[16 rows of x][16 weight rows] += X[16 x 16 k] . W^T[16 k x 16 weight rows].  Lane
 // (g, c) supplies dword g of a block of weight row c (its low nibbles are the first
@@ -346,18 +391,32 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma(const uint8_t *__res
 // order in which a weight dword's nibbles come out (see q4_dot_xr):
 //   xp[row][block][g][8] = x[4g], x[4g+2], x[4g+1], x[4g+3], x[16+4g], x[18+4g], x[17+4g], x[19+4g]
 // one 16-byte load per block.  k is split over KS waves (partials reduced in LDS).
-template <bool XF32>
-__global__ __launch_bounds__(256) void k_perm_f16(const void *__restrict__ x, uint4 *__restrict__ xp, int m, int nb) {
+// activation sources of k_perm_f16
+constexpr int PERM_F16 = 0;   // fp16 rows
+constexpr int PERM_F32 = 1;   // fp32 rows, rounded to fp16 (RNE) as ggml converts src1
+constexpr int PERM_GLU = 2;   // fp32 gate and up rows: fp16(silu(g) * u), ggml swiglu then the conversion
+
+template <int MODE>
+__global__ __launch_bounds__(256) void k_perm_f16(const void *__restrict__ x, const float *__restrict__ up,
+                                                  uint4 *__restrict__ xp, int m, int nb) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (row, block, g)
     if (i >= (int64_t)m * nb * 4) return;
     const int g = (int)(i & 3);
     const int64_t rb = i >> 2;  // row * nb + block
     uint16_t h[8];
     const int idx[8] = {4 * g, 4 * g + 2, 4 * g + 1, 4 * g + 3, 16 + 4 * g, 18 + 4 * g, 17 + 4 * g, 19 + 4 * g};
-    if constexpr (XF32) {
+    if constexpr (MODE == PERM_F32) {
         const float *xb = (const float *)x + rb * QK;
 #pragma unroll
         for (int j = 0; j < 8; j++) h[j] = f2h(xb[idx[j]]);
+    } else if constexpr (MODE == PERM_GLU) {
+        const float *gb = (const float *)x + rb * QK;
+        const float *ub = up + rb * QK;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float gv = gb[idx[j]];
+            h[j] = f2h((gv / (1.0f + expf(-gv))) * ub[idx[j]]);
+        }
     } else {
         const uint16_t *xb = (const uint16_t *)x + rb * QK;
 #pragma unroll
@@ -366,6 +425,23 @@ __global__ __launch_bounds__(256) void k_perm_f16(const void *__restrict__ x, ui
     xp[i] = make_uint4((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16),
                        (uint32_t)h[4] | ((uint32_t)h[5] << 16), (uint32_t)h[6] | ((uint32_t)h[7] << 16));
 }
+
+// Matrices of one batched launch (equal k, one activation): workgroups [wg_end[i-1],
+// wg_end[i]) take matrix i's tiles.  Per output row: y = W x (+ bias[row]) (+ add[r][row]),
+// bias broadcast over the activation rows (ggml ADD of a bias row), add a full [m][n]
+// tensor (the residual).
+struct Q4BSet {
+    const uint8_t *qs[4];
+    const uint16_t *wd[4];
+    float *y[4];
+    const float *bias[4];
+    const float *add[4];
+    int n[4];
+    int wg_end[4];  // cumulative workgroup counts; unused slots INT_MAX
+};
+
+#define Q4B_PICK(S, f, i) \
+    pick4((i), opaque_s((S).f[0]), opaque_s((S).f[1]), opaque_s((S).f[2]), opaque_s((S).f[3]))
 
 // Groups of 4 blocks: lane (g, c) loads block 4j+g of weight row c whole (16 bytes; the
 // 4 g-lanes of a row read 64 contiguous bytes) and the 4 scales of row c's group (8
@@ -378,24 +454,30 @@ struct Q4XStage {
     uint4 x[UG][4];    // activation row c, blocks 4j..4j+3, slot g (shared by the tiles)
 };
 
-// TW 16-row tiles per wave share each activation load; k is split over KS waves.
+// TW 16-row tiles per wave share each activation load; k is split over KS waves.  A
+// matrix's tiles never straddle into the next matrix (n[i] % (16*TW) == 0 but for the
+// last).
 template <int KS, int UG, int TW>
-__global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const uint8_t *__restrict__ qs,
-                                                              const uint16_t *__restrict__ wd,
-                                                              const uint4 *__restrict__ xp, float *__restrict__ y,
-                                                              const float *__restrict__ add, int n, int nb, int m) {
+__global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, const uint4 *__restrict__ xp, int nb,
+                                                              int m) {
     __shared__ float s_acc[KS][TW][64][4];
     __shared__ uint32_t s_t[KS][16][4][4];  // per wave: [row c][dword][block in group]
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
-    const int row0 = blockIdx.x * 16 * TW;
+    const int b = blockIdx.x;
+    const int mi = (b >= S.wg_end[0]) + (b >= S.wg_end[1]) + (b >= S.wg_end[2]);
+    const int wg0 = pick4(mi, 0, opaque_s(S.wg_end[0]), opaque_s(S.wg_end[1]), opaque_s(S.wg_end[2]));
+    const int n = Q4B_PICK(S, n, mi);
+    const uint64_t qs = (uint64_t)Q4B_PICK(S, qs, mi);
+    const uint64_t wd = (uint64_t)Q4B_PICK(S, wd, mi);
+    const int row0 = (b - wg0) * 16 * TW;
     const int ng = nb / 4;               // whole groups (nb % 4 == 0)
     const int per = (ng + KS - 1) / KS;  // groups of this wave
     const int j_lo = wave * per, j_hi = min(ng, j_lo + per);
-    size_t wrow[TW];
+    uint64_t wrow[TW];
 #pragma unroll
-    for (int t = 0; t < TW; t++) wrow[t] = (size_t)min(row0 + 16 * t + c, n - 1) * nb;
+    for (int t = 0; t < TW; t++) wrow[t] = (uint64_t)min(row0 + 16 * t + c, n - 1) * nb;
     const bool x_ok = c < m;
     const uint4 *xrow = xp + (size_t)min(c, m - 1) * nb * 4 + g;
     uint32_t magic = 0x64006400u;
@@ -408,8 +490,8 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const uint8_t *__r
             const int j = min(j0 + u, j_hi - 1);
 #pragma unroll
             for (int t = 0; t < TW; t++) {
-                st.w[u][t] = *(const uint4 *)(qs + (wrow[t] + 4 * j + g) * 16);
-                st.d[u][t] = *(const uint2 *)(wd + wrow[t] + 4 * j);
+                st.w[u][t] = ldg_u4(qs + (wrow[t] + 4 * j + g) * 16);
+                st.d[u][t] = ldg_u2(wd + (wrow[t] + 4 * j) * 2);
             }
 #pragma unroll
             for (int jj = 0; jj < 4; jj++) st.x[u][jj] = xrow[(size_t)(4 * j + jj) * 4];
@@ -483,10 +565,14 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const uint8_t *__r
         for (int i = 0; i < 4; i++) s_acc[wave][t][lane][i] = acc[t][i];
     __syncthreads();
     if (wave != 0) return;
+    const uint64_t y = (uint64_t)Q4B_PICK(S, y, mi);
+    const uint64_t bias = (uint64_t)Q4B_PICK(S, bias, mi);
+    const uint64_t add = (uint64_t)Q4B_PICK(S, add, mi);
 #pragma unroll
     for (int t = 0; t < TW; t++) {
         const int row = row0 + 16 * t + c;
         if (row >= n) continue;
+        const float bv = bias ? ldg_f32(bias + 4 * (uint64_t)row) : 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int r = 4 * g + i;  // activation row
@@ -494,8 +580,10 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const uint8_t *__r
                 float v = 0.0f;
 #pragma unroll
                 for (int w = 0; w < KS; w++) v += s_acc[w][t][lane][i];
-                const size_t o = (size_t)r * n + row;
-                y[o] = add ? v + add[o] : v;
+                const uint64_t o = (uint64_t)r * n + row;
+                if (bias) v = v + bv;
+                if (add) v = v + ldg_f32(add + 4 * o);
+                stg_f32(y + 4 * o, v);
             }
         }
     }
@@ -559,28 +647,6 @@ struct Q4Set {
     int row_end[4];
 };
 
-// Selecting a matrix's pointer: the four candidates pass through an empty asm
-// statement first, so the select works on register values.  A select between plain
-// loads of the by-value kernel argument would be rewritten into a load from a computed
-// address, which copies the struct to scratch memory.
-template <class T>
-__device__ __forceinline__ T opaque_s(T v) {
-    if constexpr (sizeof(T) == 8) {
-        uint64_t u = (uint64_t)v;
-        asm volatile("" : "+s"(u));
-        return (T)u;
-    } else {
-        uint32_t u = (uint32_t)v;
-        asm volatile("" : "+s"(u));
-        return (T)u;
-    }
-}
-
-template <class T>
-__device__ __forceinline__ T pick4(int i, T a0, T a1, T a2, T a3) {
-    return i >= 3 ? a3 : i >= 2 ? a2 : i >= 1 ? a1 : a0;
-}
-
 #define Q4SET_PICK(S, f, i) \
     pick4((i), opaque_s((S).f[0]), opaque_s((S).f[1]), opaque_s((S).f[2]), opaque_s((S).f[3]))
 
@@ -628,18 +694,6 @@ struct XrRows {
     float a[2];  // the rows' add / bias values (read with the weights, used in the epilogue)
 };
 
-// global-address-space accesses from integer addresses (the picked pointers are
-// plain integers after the register select; a generic pointer would give flat loads,
-// which also count against the LDS counter)
-#define MI_GLOBAL __attribute__((address_space(1)))
-__device__ __forceinline__ int4 ldg_stream16(uint64_t a) {
-    const int4v_t v = __builtin_nontemporal_load((const MI_GLOBAL int4v_t *)a);
-    return make_int4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ uint32_t ldg_u16(uint64_t a) { return *(const MI_GLOBAL uint16_t *)a; }
-__device__ __forceinline__ float ldg_f32(uint64_t a) { return *(const MI_GLOBAL float *)a; }
-__device__ __forceinline__ void stg_f32(uint64_t a, float v) { *(MI_GLOBAL float *)a = v; }
-__device__ __forceinline__ void stg_u16(uint64_t a, uint16_t v) { *(MI_GLOBAL uint16_t *)a = v; }
 
 // weights of rows r0, r1 at the lane's blocks; with dummy every lane reads block 0 of
 // r0 (one cache line: keeps the instruction count, and so the wait counts, identical
@@ -1200,34 +1254,64 @@ inline bool xr_enabled() {
     return on;
 }
 
-// activation rows converted into ws as permuted fp16, then the A-operand matrix-core kernel
-int launch_mfma_x(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const void *x, bool xf32,
-                  float *y, const float *add, void *ws) {
-    const Q4Planes p = q4_planes(n, k);
+// Activation rows converted into ws as permuted fp16 (once for the whole set), then
+// the A-operand matrix-core kernel over every matrix of the set in one launch.  mode:
+// PERM_F32 / PERM_F16 / PERM_GLU (x the gate rows, up the up rows).
+int launch_mfma_set(hipStream_t st, int count, const uint8_t *const *base, const int64_t *n, float *const *y,
+                    const float *const *bias, const float *const *add, int64_t k, int64_t m, const void *x, int mode,
+                    const float *up, void *ws) {
     const int nb = (int)(k / QK);
     const int64_t units = m * nb * 4;
-    if (xf32)
-        hipLaunchKernelGGL((k_perm_f16<true>), dim3((unsigned)((units + 255) / 256)), dim3(256), 0, st, x, (uint4 *)ws,
-                           (int)m, nb);
+    const dim3 pg((unsigned)((units + 255) / 256));
+    if (mode == PERM_F32)
+        hipLaunchKernelGGL((k_perm_f16<PERM_F32>), pg, dim3(256), 0, st, x, up, (uint4 *)ws, (int)m, nb);
+    else if (mode == PERM_GLU)
+        hipLaunchKernelGGL((k_perm_f16<PERM_GLU>), pg, dim3(256), 0, st, x, up, (uint4 *)ws, (int)m, nb);
     else
-        hipLaunchKernelGGL((k_perm_f16<false>), dim3((unsigned)((units + 255) / 256)), dim3(256), 0, st, x,
-                           (uint4 *)ws, (int)m, nb);
+        hipLaunchKernelGGL((k_perm_f16<PERM_F16>), pg, dim3(256), 0, st, x, up, (uint4 *)ws, (int)m, nb);
     MI_CHECK_LAUNCH("k_perm_f16");
     static const int tw_env = [] {
         const char *e = getenv("MI_Q4_MFMA_TW");
         return e ? atoi(e) : 0;
     }();
-    const int tw = tw_env == 1 || tw_env == 2 ? tw_env : (n >= 8192 ? 2 : 1);
-    const unsigned wgs = (unsigned)((n + 16 * tw - 1) / (16 * tw));
-    const uint16_t *dpl = (const uint16_t *)(base + p.plane);
     static const int ks_env = [] {
         const char *e = getenv("MI_Q4_MFMA_KS");
         return e ? atoi(e) : 0;
     }();
+    // two tiles per wave for the tall matrices (gate / up), where the shared activation
+    // load pays; a set uses one tile width, so it takes two only if every matrix is tall
+    bool tall = true;
+    for (int i = 0; i < count; i++) tall = tall && n[i] >= 8192;
+    int tw = tw_env == 1 || tw_env == 2 ? tw_env : (tall ? 2 : 1);
+    for (int i = 0; i + 1 < count; i++)
+        if (n[i] % (16 * tw)) tw = 1;  // a tile must not straddle two matrices
     const int ks = ks_env == 2 || ks_env == 4 || ks_env == 8 || ks_env == 16 ? ks_env : 4;
-#define MI_MX(KS, TW) \
-    hipLaunchKernelGGL((k_gemv_q4_0_mfma_x<KS, 2, TW>), dim3(wgs), dim3(64 * KS), 0, st, base, dpl, (const uint4 *)ws, \
-                       y, add, (int)n, nb, (int)m)
+    Q4BSet S;
+    int wgs = 0;
+    for (int i = 0; i < 4; i++) {
+        if (i < count) {
+            const Q4Planes p = q4_planes(n[i], k);
+            S.qs[i] = base[i];
+            S.wd[i] = (const uint16_t *)(base[i] + p.plane);
+            S.y[i] = y[i];
+            S.bias[i] = bias ? bias[i] : nullptr;
+            S.add[i] = add ? add[i] : nullptr;
+            S.n[i] = (int)n[i];
+            wgs += (int)((n[i] + 16 * tw - 1) / (16 * tw));
+            S.wg_end[i] = wgs;
+        } else {
+            S.qs[i] = S.qs[0];
+            S.wd[i] = S.wd[0];
+            S.y[i] = S.y[0];
+            S.bias[i] = nullptr;
+            S.add[i] = nullptr;
+            S.n[i] = S.n[0];
+            S.wg_end[i] = INT_MAX;
+        }
+    }
+#define MI_MX(KS, TW)                                                                                          \
+    hipLaunchKernelGGL((k_gemv_q4_0_mfma_x<KS, 2, TW>), dim3((unsigned)wgs), dim3(64 * KS), 0, st, S,            \
+                       (const uint4 *)ws, nb, (int)m)
 #define MI_MX_KS(KS) \
     if (ks == KS) {  \
         if (tw == 2) MI_MX(KS, 2); else MI_MX(KS, 1); \
@@ -1237,6 +1321,12 @@ int launch_mfma_x(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int
 #undef MI_MX
     MI_CHECK_LAUNCH("k_gemv_q4_0_mfma_x");
     return MI_OK;
+}
+
+int launch_mfma_x(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const void *x, bool xf32,
+                  float *y, const float *add, void *ws) {
+    return launch_mfma_set(st, 1, &base, &n, &y, nullptr, add ? &add : nullptr, k, m, x, xf32 ? PERM_F32 : PERM_F16,
+                           nullptr, ws);
 }
 
 inline bool mfma_x_enabled() {
@@ -1371,6 +1461,34 @@ int mi_mul_mat_q4_0_f32(void *stream, const void *w_packed, const float *x, floa
     }
     if (int r = mi_cast_f32_f16(stream, x, (uint16_t *)ws, m * k)) return r;
     return launch_gx(st, (const uint8_t *)w_packed, n, k, m, (const uint16_t *)ws, y);
+}
+
+int mi_mul_mat_q4_0_f32_batch(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
+                              float *const *y, const float *const *bias, const float *const *add, int64_t k,
+                              int64_t m, const float *x, const float *up, void *ws, size_t ws_bytes) {
+    MI_CHECK_ARG(n_mats >= 1 && n_mats <= 4, "mul_mat_q4_0_f32_batch: %d matrices (1..4)", n_mats);
+    MI_CHECK_ARG(w_packed && n && y && x, "mul_mat_q4_0_f32_batch: null pointer");
+    MI_CHECK_ARG(m >= 1 && m <= 16, "mul_mat_q4_0_f32_batch: m=%lld not in 1..16", (long long)m);
+    MI_CHECK_ARG(k % (4 * QK) == 0, "mul_mat_q4_0_f32_batch: k=%lld not a multiple of 128", (long long)k);
+    int64_t rows = 0;
+    const uint8_t *base[4];
+    for (int i = 0; i < n_mats; i++) {
+        if (int r = check_shape("mul_mat_q4_0_f32_batch", n[i], k)) return r;
+        MI_CHECK_ARG(w_packed[i] && y[i], "mul_mat_q4_0_f32_batch: matrix %d: null pointer", i);
+        MI_CHECK_ARG(mi::aligned(w_packed[i], 256), "mul_mat_q4_0_f32_batch: packed weight %d not 256-byte aligned",
+                     i);
+        base[i] = (const uint8_t *)w_packed[i];
+        rows += n[i];
+    }
+    MI_CHECK_ARG(rows < (1ll << 31), "mul_mat_q4_0_f32_batch: too many rows");
+    MI_CHECK_ARG(mi::aligned(x, 4) && (!up || mi::aligned(up, 4)), "mul_mat_q4_0_f32_batch: misaligned activation");
+    const size_t need = (size_t)m * k * 2;
+    if (!ws || ws_bytes < need || !mi::aligned(ws, 16)) {
+        mi::set_error("mul_mat_q4_0_f32_batch: workspace %zu < %zu bytes (or misaligned)", ws_bytes, need);
+        return MI_ERR_WORKSPACE;
+    }
+    return launch_mfma_set((hipStream_t)stream, n_mats, base, n, y, bias, add, k, m, x, up ? PERM_GLU : PERM_F32, up,
+                           ws);
 }
 
 int mi_mul_mat_q4_0_f32_fused(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,

@@ -11,7 +11,7 @@ rows within 2 fp16 ulps of the reference; cache rows other than the target untou
 import numpy as np
 import pytest
 
-from synth import f16_bits, q8_0_weights, rel_err, xq_to_blocks
+from synth import f16_bits, q4_0_weights, q8_0_weights, rel_err, xq_to_blocks
 
 pytestmark = pytest.mark.gpu
 
@@ -135,6 +135,60 @@ def test_rope_table(gpu, hd, pos, base, fs, af):
     ref_s = (np.sin(th.astype(np.float64)).astype(F32) * F32(af)).astype(F32)
     tol = 2 * np.spacing(np.float32(1.0)) * af + 1e-7
     assert np.max(np.abs(got[0] - ref_c)) <= tol and np.max(np.abs(got[1] - ref_s)) <= tol
+
+
+@pytest.mark.parametrize("idx_i64", [False, True])
+@pytest.mark.parametrize("m,hd,nhq,nhk,nv", [(8, 128, 28, 4, 512), (3, 64, 4, 2, 128), (1, 128, 12, 2, 256)])
+def test_rope_kv_rows(gpu, m, hd, nhq, nhk, nv, idx_i64):
+    """ROPE q, ROPE k, SET_ROWS k, SET_ROWS v of a ubatch in one launch: bit-identical to
+    mi_rope_neox + mi_set_rows_f16, within 2e-6 of the host rotation; a cache index outside
+    the cache is skipped and no other cache row changes."""
+    mi = gpu
+    P = mi._P
+    rng = np.random.default_rng(m * 1000 + hd + nhq + idx_i64)
+    n_rows_cache = 64
+    q = rng.standard_normal((m, nhq * hd)).astype(F32)
+    k = rng.standard_normal((m, nhk * hd)).astype(F32)
+    v = rng.standard_normal((m, nv)).astype(F32)
+    pos = rng.integers(0, 40000, m).astype(np.int32)
+    idx = rng.permutation(n_rows_cache)[:m].astype(np.int64 if idx_i64 else np.int32)
+    if m > 2:
+        idx[1] = n_rows_cache + 5  # outside the cache: not written
+    kc0 = f16_bits(rng.standard_normal((n_rows_cache, nhk * hd)))
+    vc0 = f16_bits(rng.standard_normal((n_rows_cache, nv)))
+    dq, dk, dv, dp, di = (mi.to_device(a) for a in (q, k, v, pos, idx))
+    dkc, dvc = mi.to_device(kc0), mi.to_device(vc0)
+    dqo = mi.DeviceBuffer(q.nbytes)
+    mi._call("mi_rope_kv_rows", None, P(dq.ptr), P(dk.ptr), P(dv.ptr), P(dqo.ptr), P(dkc.ptr), nhk * hd * 2,
+             P(dvc.ptr), nv * 2, P(dp.ptr), P(di.ptr), int(idx_i64), n_rows_cache, m, hd, nhq, nhk, nv, F32(1e6),
+             F32(1.0), F32(1.0))
+    # node-by-node on the device
+    dq2, dk2 = mi.DeviceBuffer(q.nbytes), mi.DeviceBuffer(k.nbytes)
+    dkc2, dvc2 = mi.to_device(kc0), mi.to_device(vc0)
+    for src, dst, nh in ((dq, dq2, nhq), (dk, dk2, nhk)):
+        mi._call("mi_rope_neox", None, P(src.ptr), P(dst.ptr), P(dp.ptr), hd, nh, m, hd, F32(1e6), F32(1.0), F32(1.0),
+                 hd * 4, nh * hd * 4, hd * 4, nh * hd * 4)
+    mi._call("mi_set_rows_f16", None, P(dk2.ptr), P(di.ptr), int(idx_i64), P(dkc2.ptr), nhk * hd, m, nhk * hd * 4,
+             nhk * hd * 2, n_rows_cache)
+    mi._call("mi_set_rows_f16", None, P(dv.ptr), P(di.ptr), int(idx_i64), P(dvc2.ptr), nv, m, nv * 4, nv * 2,
+             n_rows_cache)
+    mi.device_sync()
+    qo, kc, vc = dqo.download(F32).reshape(m, -1), dkc.download(np.uint16).reshape(n_rows_cache, -1), \
+        dvc.download(np.uint16).reshape(n_rows_cache, -1)
+    assert np.array_equal(qo, dq2.download(F32).reshape(m, -1))
+    assert np.array_equal(kc, dkc2.download(np.uint16).reshape(n_rows_cache, -1))
+    assert np.array_equal(vc, dvc2.download(np.uint16).reshape(n_rows_cache, -1))
+    written = [int(i) for i in idx if 0 <= i < n_rows_cache]
+    untouched = [r for r in range(n_rows_cache) if r not in written]
+    assert np.array_equal(kc[untouched], kc0[untouched]) and np.array_equal(vc[untouched], vc0[untouched])
+    for r in range(m):
+        ref_q = rope_neox_ref(q[r].reshape(nhq, hd), int(pos[r]), hd, 1e6).reshape(-1)
+        assert rel_err(qo[r], ref_q) < 2e-6
+        if 0 <= idx[r] < n_rows_cache:
+            ref_k = rope_neox_ref(k[r].reshape(nhk, hd), int(pos[r]), hd, 1e6).reshape(-1)
+            kf = kc[idx[r]].view(np.float16).astype(F32)
+            assert np.max(np.abs(kf - ref_k) / np.maximum(np.abs(ref_k), 1e-3)) < 2e-3
+            assert np.array_equal(vc[idx[r]], f16_bits(v[r]))
 
 
 @pytest.mark.parametrize("ne0,nrows", [(151936, 1), (1000, 3), (2049, 2), (4096 * 300 + 7, 1)])
@@ -394,6 +448,81 @@ def _packed_q4(mi, w, n, k):
 def _q4_ref(orc, w, x, n, k):
     """ggml MUL_MAT of a Q4_0 weight and an fp32 row: src1 converted to fp16 (RNE)"""
     return orc.mul_mat_q4_0_f16(w, f16_bits(x), n, k)
+
+
+# (rows per matrix, k, activation rows, epilogue): q/k/v + bias, gate/up, down + residual
+# after the GLU, o + residual, ragged last matrix
+@pytest.mark.parametrize("ns,k,m,mode", [((3584, 512, 512), 3584, 8, "bias"), ((18944, 18944), 3584, 5, "none"),
+                                         ((3584,), 18944, 8, "glu_add"), ((3584,), 3584, 16, "add"),
+                                         ((96, 40), 256, 3, "bias"), ((1536,), 8960, 2, "glu")])
+def test_q4_batch_set(gpu, orc, ns, k, m, mode):
+    """Several activation rows through up to four Q4_0 matrices in one launch: bit-identical
+    to one mi_mul_mat_q4_0_f32 launch per matrix followed by the ADD (the graph's node-by-node
+    path), and within the GEMV bar of the oracle's ggml MUL_MAT (src1 rounded to fp16)."""
+    mi = gpu
+    P = mi._P
+    rng = np.random.default_rng(sum(ns) + k + m)
+    ws = [q4_0_weights(rng, n, k) for n in ns]
+    pw = [_packed_q4(mi, w, n, k) for w, n in zip(ws, ns)]
+    x = rng.standard_normal((m, k)).astype(F32)
+    up = rng.standard_normal((m, k)).astype(F32) if mode.startswith("glu") else None
+    bias = [rng.standard_normal(n).astype(F32) for n in ns] if mode == "bias" else None
+    add = [rng.standard_normal((m, n)).astype(F32) for n in ns] if mode.endswith("add") else None
+    dx = mi.to_device(x)
+    dup = mi.to_device(up) if up is not None else None
+    db = [mi.to_device(b) for b in bias] if bias else None
+    da = [mi.to_device(a) for a in add] if add else None
+    ys = [mi.DeviceBuffer(4 * m * n) for n in ns]
+    wsb = mi.mul_mat_q4_0_workspace_size(m, k)
+    wbuf = mi.DeviceBuffer(wsb)
+    mi._call("mi_mul_mat_q4_0_f32_batch", None, len(ns), _ptrs(*pw), _i64s(*ns), _ptrs(*ys),
+             _ptrs(*db) if db else None, _ptrs(*da) if da else None, k, m, P(dx.ptr), P(dup.ptr if dup else None),
+             P(wbuf.ptr), wsb)
+    # node-by-node: GLU, then one launch per matrix, then the ADD
+    act = x
+    if up is not None:
+        dh = mi.DeviceBuffer(4 * m * k)
+        mi._call("mi_swiglu", None, P(dx.ptr), P(dup.ptr), P(dh.ptr), m * k)
+        mi.device_sync()
+        act_dev = dh
+        act = dh.download(F32).reshape(m, k)  # the oracle matmul takes the GLU node's output
+    else:
+        act_dev = dx
+    plain = []
+    for t, n in enumerate(ns):
+        yb = mi.DeviceBuffer(4 * m * n)
+        mi.mul_mat_q4_0_f32(pw[t].ptr, act_dev.ptr, yb.ptr, n, k, m, ws=wbuf.ptr, ws_bytes=wsb)
+        mi.device_sync()
+        v = yb.download(F32).reshape(m, n)
+        if bias:
+            v = (v + bias[t]).astype(F32)
+        if add:
+            v = (v + add[t]).astype(F32)
+        plain.append(v)
+    mi.device_sync()
+    for t, n in enumerate(ns):
+        got = ys[t].download(F32).reshape(m, n)
+        assert np.array_equal(got, plain[t]), f"matrix {t}: fused differs from node-by-node"
+        for r in range(m):
+            ref = _q4_ref(orc, ws[t], act[r], n, k)
+            if bias:
+                ref = (ref + bias[t]).astype(F32)
+            if add:
+                ref = (ref + add[t][r]).astype(F32)
+            assert rel_err(got[r], ref) < GEMV_TOL, f"matrix {t} row {r}"
+
+
+def test_q4_batch_set_rejects_bad_shapes(gpu):
+    mi = gpu
+    P = mi._P
+    w = _ptrs(mi.DeviceBuffer(256))
+    y = _ptrs(mi.DeviceBuffer(256))
+    with pytest.raises(mi.MiError):  # k not a multiple of 128
+        mi._call("mi_mul_mat_q4_0_f32_batch", None, 1, w, _i64s(16), y, None, None, 96, 2, P(256), P(None), P(256),
+                 1 << 20)
+    with pytest.raises(mi.MiError):  # 17 activation rows
+        mi._call("mi_mul_mat_q4_0_f32_batch", None, 1, w, _i64s(16), y, None, None, 128, 17, P(256), P(None), P(256),
+                 1 << 20)
 
 
 @pytest.mark.parametrize("norm", [True, False])

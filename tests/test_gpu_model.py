@@ -120,8 +120,7 @@ def test_fused_graph_matches_unfused(gpu, monkeypatch, wtype):
 
 @pytest.mark.parametrize("wtype", [qs.GGML_TYPE_Q8_0, qs.GGML_TYPE_Q4_0])
 def test_fused_graph_matches_unfused_long_context(gpu, monkeypatch, wtype):
-    """As above from a 600-position cache (KV view of 768 rows: 12 attention splits, merged
-    in the o projection's prologue on the A8W8 path)."""
+    """As above from a 600-position cache (KV view of 768 rows: 12 attention splits)."""
     mi = gpu
     hp = qs.qwen2_1p5b(n_layer=2, n_ctx=1024, wtype=wtype)
     tensors, smooth = qs.synth(hp, seed=19, qk_gain=6.0)
@@ -143,6 +142,32 @@ def test_fused_graph_matches_unfused_long_context(gpu, monkeypatch, wtype):
         tok = tok_f
     print(f"fused vs node-by-node at context {start}: max rel {worst:.3e}")
     assert worst < 1e-4
+    fused.free()
+    plain.free()
+
+
+@pytest.mark.parametrize("wtype", [qs.GGML_TYPE_Q4_0, qs.GGML_TYPE_Q8_0])
+def test_fused_graph_matches_unfused_batch(gpu, monkeypatch, wtype):
+    """A ubatch of 4 sequences (one token each): the backend's fused launches (grouped
+    q/k/v + bias, gate/up, GLU + down + residual on the Q4_0 path) against its node-by-node
+    path, logits bit-identical."""
+    mi = gpu
+    n_seq = 4
+    hp = qs.qwen2_1p5b(n_layer=2, n_ctx=64, wtype=wtype, n_seq=n_seq)
+    tensors, smooth = qs.synth(hp, seed=29, qk_gain=6.0)
+    fused = mi.Qwen2Model(hp)
+    fused.load(tensors, smooth)
+    monkeypatch.setenv("GGML_MI355X_FUSION", "0")
+    plain = mi.Qwen2Model(hp)
+    plain.load(tensors, smooth)
+    rng = np.random.default_rng(30)
+    toks = rng.integers(0, hp["n_vocab"], n_seq)
+    for pos in range(12):
+        tf, lf = fused.decode_batch(toks, [pos] * n_seq, want_logits=True)
+        tp, lp = plain.decode_batch(toks, [pos] * n_seq, want_logits=True)
+        assert np.array_equal(lf, lp), f"position {pos}: max rel {np.abs(lf - lp).max() / np.abs(lp).max():.3e}"
+        assert np.array_equal(tf, tp)
+        toks = tf
     fused.free()
     plain.free()
 
