@@ -14,6 +14,8 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 namespace {
 
 using namespace mi;
@@ -60,23 +62,29 @@ inline bool fa_valu_forced() {
     return v;
 }
 
-inline FaPlan fa_plan(int64_t n_kv, int64_t n_kv_heads, int64_t d, int64_t gq) {
+inline FaPlan fa_plan(int64_t n_kv, int64_t n_kv_heads, int64_t d, int64_t gq, int64_t n_seq = 1) {
     const int64_t ng = 4 * 64 / (d / 8);  // lane groups per workgroup
-    const int64_t target_wg = 512;
-    int64_t per = (n_kv * n_kv_heads + target_wg - 1) / target_wg;
+    const int64_t target_wg = 512;        // over all sequences of the launch
+    int64_t per = (n_kv * n_kv_heads * n_seq + target_wg - 1) / target_wg;
     if (fa_chunk_override() > 0) per = fa_chunk_override();
     FaPlan p;
     p.mfma = !fa_valu_forced() && gq <= 16;
     if (p.mfma) {
         // 4 waves x nbw blocks of 16 positions per workgroup
         p.kt = 1;
+        // at most 8 blocks per wave (fully unrolled, 3 waves per SIMD); longer runs (a
+        // runtime loop at 2 waves per SIMD, measured slower) only when the split count
+        // would exceed kMaxSplits (over 512K positions)
         p.nbw = per <= 64 ? 1 : per <= 128 ? 2 : per <= 256 ? 4 : 8;
         int64_t chunk = 64 * p.nbw;
         while ((n_kv + chunk - 1) / chunk > kMaxSplits) chunk *= 2;
-        p.chunk = (int)chunk;
-        p.nbw = (int)(chunk / 64);
-        p.n_splits = (int)((n_kv + chunk - 1) / chunk);
-        return p;
+        if (chunk <= 64 * 32) {  // a run of at most 32 blocks per wave (the kernel's instances)
+            p.chunk = (int)chunk;
+            p.nbw = (int)(chunk / 64);
+            p.n_splits = (int)((n_kv + chunk - 1) / chunk);
+            return p;
+        }
+        p.mfma = false;  // over 2M positions: the VALU kernel, whose chunk is a runtime loop
     }
     p.nbw = 0;
     if (per <= ng) p.kt = 1;
@@ -532,11 +540,9 @@ __global__ __launch_bounds__(256) void k_fa_mfma(const float *__restrict__ q, co
 #pragma unroll
         for (int r = 0; r < 4; r++) ld_bytes<D / 8>(vr[buf][r].w, vb + (size_t)min(p0 + 4 * g + r, last) * v_nb1);
     };
-    issue(0, 0);
-    if (NBW > 1) issue(1, 1);
-#pragma unroll
-    for (int blk = 0; blk < NBW; blk++) {
-        const int buf = blk & 1;
+    // one 16-position block: scores, online softmax, P.V (buffer buf holds its K / V)
+    auto step = [&](int blk, auto bufc) {
+        constexpr int buf = decltype(bufc)::value;
         const int p0 = wstart + blk * 16;
         float mk[4] = {0.f, 0.f, 0.f, 0.f};
         if constexpr (MASK) {
@@ -597,7 +603,23 @@ __global__ __launch_bounds__(256) void k_fa_mfma(const float *__restrict__ q, co
             o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(ahi, bv, o[t], 0, 0, 0);
             o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(alo, bv, o[t], 0, 0, 0);
         }
-        if (blk + 2 < NBW) issue(blk + 2, buf);
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    issue(0, 0);
+    if constexpr (NBW == 1) {
+        step(0, B0{});
+    } else {
+        // two register stages; the next pair's loads are unconditional (past the run they
+        // re-read its last row: cache hits, masked), so no wait gathers every load
+        issue(1, 1);
+#pragma unroll(NBW <= 8 ? NBW / 2 : 1)
+        for (int blk = 0; blk < NBW; blk += 2) {
+            step(blk, B0{});
+            issue(blk + 2, 0);
+            step(blk + 1, B1{});
+            issue(blk + 3, 1);
+        }
     }
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
@@ -768,7 +790,9 @@ int launch_split_m(hipStream_t st, const FaArgs &a, const FaPlan &p) {
             case 1: MI_FA_NBW(1); break;
             case 2: MI_FA_NBW(2); break;
             case 4: MI_FA_NBW(4); break;
-            default: MI_FA_NBW(8); break;
+            case 8: MI_FA_NBW(8); break;
+            case 16: MI_FA_NBW(16); break;
+            default: MI_FA_NBW(32); break;
         }
 #undef MI_FA_NBW
         MI_CHECK_LAUNCH("k_fa_mfma");
@@ -850,7 +874,7 @@ extern "C" {
 size_t mi_fa_decode_batch_workspace_size(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
                                          int64_t n_seq) {
     if (n_kv <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || d <= 0 || n_seq <= 0) return 0;
-    const FaPlan p = fa_plan(n_kv, n_kv_heads, d, n_q_heads / n_kv_heads);
+    const FaPlan p = fa_plan(n_kv, n_kv_heads, d, n_q_heads / n_kv_heads, n_seq);
     return fa_part_bytes(n_q_heads * n_seq, p.n_splits, d) +
            mi::align_up((size_t)(n_kv_heads * n_seq) * sizeof(unsigned), 256);
 }
@@ -874,7 +898,7 @@ static int fa_decode_run(void *stream, const float *q, const void *k, const void
                      v_nb2 % 16 == 0 && mi::aligned(q, 16) && mi::aligned(out, 16) && k_seq % 16 == 0 &&
                      v_seq % 16 == 0 && q_seq % 4 == 0 && out_seq % 4 == 0,
                  "fa_decode: K/V base and strides must be 16-byte aligned");
-    const FaPlan p = fa_plan(n_kv, n_kv_heads, d, n_q_heads / n_kv_heads);
+    const FaPlan p = fa_plan(n_kv, n_kv_heads, d, n_q_heads / n_kv_heads, n_seq);
     const size_t need = mi_fa_decode_batch_workspace_size(n_kv, n_q_heads, n_kv_heads, d, n_seq);
     if ((p.n_splits > 1 || partials_only) && (!ws || ws_bytes < need || !mi::aligned(ws, 256))) {
         mi::set_error("fa_decode: workspace %zu < %zu bytes (or not 256-byte aligned)", ws_bytes, need);

@@ -317,6 +317,46 @@ def test_kv_lengths_device(gpu, orc):
         assert np.array_equal(out.download(np.int32), orc.kv_lengths(mk, is_f16=is_f16))
 
 
+def test_fa_decode_batch_eight_sequences(gpu, orc):
+    """Eight sequences in one launch (the plan spreads ~512 workgroups over all of them:
+    8 blocks of 16 positions per wave), ragged kv lengths, the last split partly past the
+    view."""
+    mi = gpu
+    n_seq, L, nq, nkv, d = 8, 12000, 28, 4, 128
+    lens = [L, 37, 1234, L, L - 1, 2048, 2049, 5000]
+    rng = np.random.default_rng(L)
+    q = rng.standard_normal((n_seq, nq, d)).astype(np.float32)
+    kc = f16_bits(rng.standard_normal((n_seq, L, nkv, d)))
+    vc = f16_bits(rng.standard_normal((n_seq, L, nkv, d)))
+    dq, dk, dv = mi.to_device(q), mi.to_device(kc), mi.to_device(vc)
+    dl = mi.to_device(np.array(lens, np.int32))
+    out = mi.DeviceBuffer(n_seq * nq * d * 4)
+    wsb = mi.fa_decode_batch_workspace_size(L, nq, nkv, d, n_seq)
+    ws = mi.DeviceBuffer(wsb).zero()
+    nb1 = nkv * d * 2
+    seq_bytes = L * nb1
+    mi.fa_decode_batch(dq.ptr, dk.ptr, dv.ptr, None, dl.ptr, L, nq, nkv, d, nb1, d * 2, nb1, d * 2, 1 / np.sqrt(d),
+                       out.ptr, n_seq, nq * d, seq_bytes, seq_bytes, 0, nq * d, ws.ptr, wsb)
+    mi.device_sync()
+    o = out.download(np.float32).reshape(n_seq, nq, d)
+    for s in range(n_seq):
+        _check_fa(orc, o[s], q[s], kc[s], vc[s], nkv, 1 / np.sqrt(d), kv_len=lens[s], label=f"seq {s}")
+
+
+@pytest.mark.parametrize("L", [600_000, 1_100_000])
+def test_fa_decode_longest_views(gpu, orc, L):
+    """Views past 512K positions, where the split count cap lengthens each wave's run to
+    16 (L=600000) or 32 (L=1100000) blocks; the last split partly past the view."""
+    mi = gpu
+    nq, nkv, d = 2, 1, 64
+    rng = np.random.default_rng(L)
+    q = rng.standard_normal((nq, d)).astype(np.float32)
+    kc = f16_bits(rng.standard_normal((L, nkv, d)) * 0.5)
+    vc = f16_bits(rng.standard_normal((L, nkv, d)))
+    o = _fa_run(mi, q, kc, vc, nkv, 1 / np.sqrt(d))
+    _check_fa(orc, o, q, kc, vc, nkv, 1 / np.sqrt(d), label=f"L={L}")
+
+
 @pytest.mark.parametrize("use_mask", [False, True])
 def test_fa_decode_batch_sequences(gpu, orc, use_mask):
     """Independent sequences in one launch (grid z), each with its own cache region, length
