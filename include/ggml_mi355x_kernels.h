@@ -148,12 +148,15 @@ int mi_mul_mat_q8_0_f32_lse(void *stream, const void *w_packed, int64_t n, float
  * after one fp16 conversion of the activation: y[i] = W_i x (+ bias[i] broadcast over the rows)
  * (+ add[i], a full [m][n[i]] tensor: the residual), each optional (bias / add or their entries
  * may be NULL).  x: fp32 [m][k]; with up != NULL the activation is ggml swiglu(x, up) =
- * x / (1 + expf(-x)) * up (the GLU node before the down projection).  k % 128 == 0; ws of
- * m*k*2 bytes, 16-byte aligned.  Replaces, per matrix, the ggml_cann_mat_mul_fp route for a
- * batch of rows (patch:1207) and the ADD / GLU nodes around it. */
+ * x / (1 + expf(-x)) * up (the GLU node before the down projection); with norm_w != NULL it
+ * is RMS_NORM(x, eps) * norm_w per row (k <= 4096, x and norm_w 16-byte aligned); up and
+ * norm_w exclusive.  k % 128 == 0; ws of m*k*2 bytes, 16-byte aligned.  Replaces, per
+ * matrix, the ggml_cann_mat_mul_fp route for a batch of rows (patch:1207) and the
+ * RMS_NORM / MUL / ADD / GLU nodes around it. */
 int mi_mul_mat_q4_0_f32_batch(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
                               float *const *y, const float *const *bias, const float *const *add, int64_t k,
-                              int64_t m, const float *x, const float *up, void *ws, size_t ws_bytes);
+                              int64_t m, const float *x, const float *up, const float *norm_w, float eps, void *ws,
+                              size_t ws_bytes);
 /* the attention-input chain of one token: [RMS_NORM -> MUL(norm_w)] -> q/k/v MUL_MATs
  * (w_packed[0..2], n[0..2] rows, k <= 4096) -> ADD bias[i] (or NULL) -> neox ROPE of q
  * and k (n_dims = head_dim, theta = pos[0] * freq_base^(-2i/head_dim), freq_scale,

@@ -549,8 +549,8 @@ void run_fa(BackendCtx *ctx, ggml_tensor *node) {
 //                                                          mi_gemv_q8_0_add
 //   attention + o   : FLASH_ATTN_EXT, MUL_MAT, [ADD]     -> mi_fa_decode_partials +
 //                                                          mi_mul_mat_q8_0_f32_lse
-//   ubatch (Q4_0)   : MUL_MAT x1..4 [ADD bias each] or MUL_MAT ADD(residual), and
-//                     GLU swiglu, MUL_MAT, [ADD]          -> mi_mul_mat_q4_0_f32_batch
+//   ubatch (Q4_0)   : [RMS_NORM, MUL(w)] MUL_MAT x1..4 [ADD bias each] or MUL_MAT
+//                     ADD(residual), and GLU swiglu, MUL_MAT, [ADD] -> mi_mul_mat_q4_0_f32_batch
 //   rope + kv write : ROPE q, ROPE k, SET_ROWS k, SET_ROWS v -> mi_rope_kv_rows
 
 using Consumers = std::unordered_map<const ggml_tensor *, std::vector<const ggml_tensor *>>;
@@ -981,13 +981,20 @@ const ggml_tensor *batch_add_tail(ggml_cgraph *g, int j, const ggml_tensor *mm, 
 }
 
 // MUL_MAT x 1..4 (Q4_0, same activation rows) [-> ADD bias per matrix, in order] or
-// MUL_MAT -> ADD(residual): one conversion of the activation, one launch
-int try_fuse_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+// MUL_MAT -> ADD(residual): one conversion of the activation, one launch.  The group
+// starts at node i0; with norm (RMS_NORM -> MUL(norm_w) at node i, the MUL being the
+// matmuls' activation and read by nothing else) the norm runs in the conversion.
+struct BatchNorm {
+    const ggml_tensor *x = nullptr, *w = nullptr;
+    float eps = 0.0f;
+};
+
+int fuse_q4_batch_at(BackendCtx *ctx, ggml_cgraph *g, int i, int i0, const Consumers &C, const BatchNorm &norm) {
     const int nn = ggml_graph_n_nodes(g);
-    ggml_tensor *mm0 = ggml_graph_node(g, i);
+    ggml_tensor *mm0 = ggml_graph_node(g, i0);
     if (!q4_batch_node(mm0)) return 0;
     const ggml_tensor *mm[4] = {mm0};
-    int cnt = 1, last = i;
+    int cnt = 1, last = i0;
     while (cnt < 4) {
         const int j = next_real(g, last + 1);
         if (j >= nn) break;
@@ -1008,7 +1015,14 @@ int try_fuse_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C
         if (a) tail = next_real(g, tail + 1);
     }
     if (!all_add) tail = last;
-    if (cnt == 1 && !all_add) return 0;  // a lone matmul takes the plain path
+    if (cnt == 1 && !all_add && !norm.w) return 0;  // a lone matmul takes the plain path
+    if (norm.w) {
+        std::vector<const ggml_tensor *> cs;
+        real_consumers(C, mm0->src[1], cs);
+        if (cs.size() != (size_t)cnt) return 0;  // the normed activation is read only by the group
+        for (const ggml_tensor *c : cs)
+            if (std::find(mm, mm + cnt, c) == mm + cnt) return 0;
+    }
     const void *w[4];
     int64_t n[4];
     float *y[4];
@@ -1021,9 +1035,39 @@ int try_fuse_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C
         av[t] = all_add && !bias[t] ? (const float *)other[t]->data : nullptr;
     }
     const int64_t k = mm0->src[0]->ne[0], m = ggml_nrows(mm0->src[1]);
-    MI_K_CHECK(mi_mul_mat_q4_0_f32_batch(ctx->stream, cnt, w, n, y, bv, av, k, m, (const float *)mm0->src[1]->data,
-                                         nullptr, ctx->scratch, ctx->scratch_size));
+    const float *x = (const float *)(norm.w ? norm.x->data : mm0->src[1]->data);
+    MI_K_CHECK(mi_mul_mat_q4_0_f32_batch(ctx->stream, cnt, w, n, y, bv, av, k, m, x, nullptr,
+                                         norm.w ? (const float *)norm.w->data : nullptr, norm.eps, ctx->scratch,
+                                         ctx->scratch_size));
     return tail + 1 - i;
+}
+
+int try_fuse_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    return fuse_q4_batch_at(ctx, g, i, i, C, BatchNorm{});
+}
+
+// RMS_NORM (2..16 rows, k <= 4096) -> MUL(norm_w row) -> the Q4_0 group of try_fuse_q4_batch
+int try_fuse_norm_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    const int nn = ggml_graph_n_nodes(g);
+    const ggml_tensor *rms = ggml_graph_node(g, i);
+    const ggml_tensor *x = rms->src[0];
+    const int64_t m = ggml_nrows(x);
+    if (!is_f32_contig(x) || m < 2 || m > 16 || x->ne[1] != m || x->ne[0] > 4096 || x->ne[0] % 128 ||
+        !aligned16(x->data))
+        return 0;
+    const int j = next_real(g, i + 1);
+    if (j >= nn) return 0;
+    const ggml_tensor *mul = ggml_graph_node(g, j);
+    if (mul->op != GGML_OP_MUL || mul->src[0] != rms || !is_row_vector(mul->src[1], x->ne[0]) ||
+        !only_consumed_by(C, rms, {mul}))
+        return 0;
+    const int i0 = next_real(g, j + 1);
+    if (i0 >= nn || ggml_graph_node(g, i0)->src[1] != mul) return 0;
+    BatchNorm norm;
+    norm.x = x;
+    norm.w = mul->src[1];
+    memcpy(&norm.eps, rms->op_params, sizeof(float));
+    return fuse_q4_batch_at(ctx, g, i, i0, C, norm);
 }
 
 // GLU swiglu (gate, up: 2..16 rows) -> MUL_MAT(Q4_0) [-> ADD residual]: the swiglu is
@@ -1046,7 +1090,8 @@ int try_fuse_glu_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumer
     const float *bv = ad && is_bias ? (const float *)other->data : nullptr;
     const float *av = ad && !is_bias ? (const float *)other->data : nullptr;
     MI_K_CHECK(mi_mul_mat_q4_0_f32_batch(ctx->stream, 1, &w, &n, &y, &bv, &av, k, m, (const float *)glu->src[0]->data,
-                                         (const float *)glu->src[1]->data, ctx->scratch, ctx->scratch_size));
+                                         (const float *)glu->src[1]->data, nullptr, 0.0f, ctx->scratch,
+                                         ctx->scratch_size));
     return (ad ? next_real(g, j + 1) : j) + 1 - i;
 }
 
@@ -1144,6 +1189,7 @@ int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
             if (fuse) {
                 if (int used = try_fuse_attn_in(ctx, g, i, C)) return used;
                 if (int used = try_fuse_norm_matmuls(ctx, g, i, C)) return used;
+                if (int used = try_fuse_norm_q4_batch(ctx, g, i, C)) return used;
             }
             float eps;
             memcpy(&eps, node->op_params, sizeof(float));

@@ -426,6 +426,62 @@ __global__ __launch_bounds__(256) void k_perm_f16(const void *__restrict__ x, co
                        (uint32_t)h[4] | ((uint32_t)h[5] << 16), (uint32_t)h[6] | ((uint32_t)h[7] << 16));
 }
 
+// RMS_NORM -> MUL(w) of each activation row, then the permuted fp16 conversion of
+// k_perm_f16: one workgroup per row forms the row's scale with the loads, order and
+// reduction of the RMSNorm kernel's vector path (k <= 4096), then converts
+// (x * scale) * w, as that kernel writes it and the matmul converts it.
+__global__ __launch_bounds__(256) void k_perm_norm_f16(const float *__restrict__ x, const float *__restrict__ w,
+                                                       float eps, uint4 *__restrict__ xp, int nb) {
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const int ne0 = nb * QK, n4 = ne0 / 4;
+    const float *xr = x + (size_t)row * ne0;
+    __shared__ double s_red[4];
+    __shared__ uint2 s_h[1024];  // the converted row, 4 halves per float4
+    float4 xv[4], wv[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int f = min(tid + t * 256, n4 - 1);
+        xv[t] = ((const float4 *)xr)[f];
+        wv[t] = ((const float4 *)w)[f];
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        if (tid + t * 256 < n4) {
+            s += (double)sq_rn(xv[t].x);
+            s += (double)sq_rn(xv[t].y);
+            s += (double)sq_rn(xv[t].z);
+            s += (double)sq_rn(xv[t].w);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    if ((tid & 63) == 0) s_red[tid >> 6] = s;
+    __syncthreads();
+    const double tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    const float mean = (float)(tot / ne0);
+    const float scale = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int f = tid + t * 256;
+        if (f < n4) {
+            const float4 v = xv[t];
+            const uint32_t h0 = f2h((v.x * scale) * wv[t].x), h1 = f2h((v.y * scale) * wv[t].y);
+            const uint32_t h2 = f2h((v.z * scale) * wv[t].z), h3 = f2h((v.w * scale) * wv[t].w);
+            s_h[f] = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+        }
+    }
+    __syncthreads();
+    // unit (block b, slot g): halves 4g, 4g+2, 4g+1, 4g+3 and the same + 16 (float4s 8b+g, 8b+4+g)
+    for (int u = tid; u < nb * 4; u += 256) {
+        const int g = u & 3, b = u >> 2;
+        const uint2 lo = s_h[8 * b + g], hi = s_h[8 * b + 4 + g];
+        xp[(size_t)row * nb * 4 + u] =
+            make_uint4((lo.x & 0xffffu) | (lo.y << 16), (lo.x >> 16) | (lo.y & 0xffff0000u),
+                       (hi.x & 0xffffu) | (hi.y << 16), (hi.x >> 16) | (hi.y & 0xffff0000u));
+    }
+}
+
 // Matrices of one batched launch (equal k, one activation): workgroups [wg_end[i-1],
 // wg_end[i]) take matrix i's tiles.  Per output row: y = W x (+ bias[row]) (+ add[r][row]),
 // bias broadcast over the activation rows (ggml ADD of a bias row), add a full [m][n]
@@ -1259,11 +1315,14 @@ inline bool xr_enabled() {
 // PERM_F32 / PERM_F16 / PERM_GLU (x the gate rows, up the up rows).
 int launch_mfma_set(hipStream_t st, int count, const uint8_t *const *base, const int64_t *n, float *const *y,
                     const float *const *bias, const float *const *add, int64_t k, int64_t m, const void *x, int mode,
-                    const float *up, void *ws) {
+                    const float *up, void *ws, const float *norm_w = nullptr, float eps = 0.0f) {
     const int nb = (int)(k / QK);
     const int64_t units = m * nb * 4;
     const dim3 pg((unsigned)((units + 255) / 256));
-    if (mode == PERM_F32)
+    if (norm_w)
+        hipLaunchKernelGGL(k_perm_norm_f16, dim3((unsigned)m), dim3(256), 0, st, (const float *)x, norm_w, eps,
+                           (uint4 *)ws, nb);
+    else if (mode == PERM_F32)
         hipLaunchKernelGGL((k_perm_f16<PERM_F32>), pg, dim3(256), 0, st, x, up, (uint4 *)ws, (int)m, nb);
     else if (mode == PERM_GLU)
         hipLaunchKernelGGL((k_perm_f16<PERM_GLU>), pg, dim3(256), 0, st, x, up, (uint4 *)ws, (int)m, nb);
@@ -1465,7 +1524,8 @@ int mi_mul_mat_q4_0_f32(void *stream, const void *w_packed, const float *x, floa
 
 int mi_mul_mat_q4_0_f32_batch(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
                               float *const *y, const float *const *bias, const float *const *add, int64_t k,
-                              int64_t m, const float *x, const float *up, void *ws, size_t ws_bytes) {
+                              int64_t m, const float *x, const float *up, const float *norm_w, float eps, void *ws,
+                              size_t ws_bytes) {
     MI_CHECK_ARG(n_mats >= 1 && n_mats <= 4, "mul_mat_q4_0_f32_batch: %d matrices (1..4)", n_mats);
     MI_CHECK_ARG(w_packed && n && y && x, "mul_mat_q4_0_f32_batch: null pointer");
     MI_CHECK_ARG(m >= 1 && m <= 16, "mul_mat_q4_0_f32_batch: m=%lld not in 1..16", (long long)m);
@@ -1482,13 +1542,16 @@ int mi_mul_mat_q4_0_f32_batch(void *stream, int n_mats, const void *const *w_pac
     }
     MI_CHECK_ARG(rows < (1ll << 31), "mul_mat_q4_0_f32_batch: too many rows");
     MI_CHECK_ARG(mi::aligned(x, 4) && (!up || mi::aligned(up, 4)), "mul_mat_q4_0_f32_batch: misaligned activation");
+    MI_CHECK_ARG(!(up && norm_w), "mul_mat_q4_0_f32_batch: up and norm_w are exclusive");
+    MI_CHECK_ARG(!norm_w || (k <= 4096 && mi::aligned(x, 16) && mi::aligned(norm_w, 16)),
+                 "mul_mat_q4_0_f32_batch: the fused RMSNorm needs k <= 4096 and 16-byte aligned x / norm_w");
     const size_t need = (size_t)m * k * 2;
     if (!ws || ws_bytes < need || !mi::aligned(ws, 16)) {
         mi::set_error("mul_mat_q4_0_f32_batch: workspace %zu < %zu bytes (or misaligned)", ws_bytes, need);
         return MI_ERR_WORKSPACE;
     }
     return launch_mfma_set((hipStream_t)stream, n_mats, base, n, y, bias, add, k, m, x, up ? PERM_GLU : PERM_F32, up,
-                           ws);
+                           ws, norm_w, eps);
 }
 
 int mi_mul_mat_q4_0_f32_fused(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,

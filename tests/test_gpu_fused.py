@@ -454,7 +454,9 @@ def _q4_ref(orc, w, x, n, k):
 # after the GLU, o + residual, ragged last matrix
 @pytest.mark.parametrize("ns,k,m,mode", [((3584, 512, 512), 3584, 8, "bias"), ((18944, 18944), 3584, 5, "none"),
                                          ((3584,), 18944, 8, "glu_add"), ((3584,), 3584, 16, "add"),
-                                         ((96, 40), 256, 3, "bias"), ((1536,), 8960, 2, "glu")])
+                                         ((96, 40), 256, 3, "bias"), ((1536,), 8960, 2, "glu"),
+                                         ((3584, 512, 512), 3584, 8, "norm_bias"), ((18944, 18944), 3584, 8, "norm"),
+                                         ((256,), 4096, 3, "norm")])
 def test_q4_batch_set(gpu, orc, ns, k, m, mode):
     """Several activation rows through up to four Q4_0 matrices in one launch: bit-identical
     to one mi_mul_mat_q4_0_f32 launch per matrix followed by the ADD (the graph's node-by-node
@@ -466,10 +468,12 @@ def test_q4_batch_set(gpu, orc, ns, k, m, mode):
     pw = [_packed_q4(mi, w, n, k) for w, n in zip(ws, ns)]
     x = rng.standard_normal((m, k)).astype(F32)
     up = rng.standard_normal((m, k)).astype(F32) if mode.startswith("glu") else None
-    bias = [rng.standard_normal(n).astype(F32) for n in ns] if mode == "bias" else None
+    bias = [rng.standard_normal(n).astype(F32) for n in ns] if mode.endswith("bias") else None
     add = [rng.standard_normal((m, n)).astype(F32) for n in ns] if mode.endswith("add") else None
+    nw = rng.uniform(0.8, 1.2, k).astype(F32) if mode.startswith("norm") else None
     dx = mi.to_device(x)
     dup = mi.to_device(up) if up is not None else None
+    dnw = mi.to_device(nw) if nw is not None else None
     db = [mi.to_device(b) for b in bias] if bias else None
     da = [mi.to_device(a) for a in add] if add else None
     ys = [mi.DeviceBuffer(4 * m * n) for n in ns]
@@ -477,7 +481,7 @@ def test_q4_batch_set(gpu, orc, ns, k, m, mode):
     wbuf = mi.DeviceBuffer(wsb)
     mi._call("mi_mul_mat_q4_0_f32_batch", None, len(ns), _ptrs(*pw), _i64s(*ns), _ptrs(*ys),
              _ptrs(*db) if db else None, _ptrs(*da) if da else None, k, m, P(dx.ptr), P(dup.ptr if dup else None),
-             P(wbuf.ptr), wsb)
+             P(dnw.ptr if dnw else None), F32(1e-6), P(wbuf.ptr), wsb)
     # node-by-node: GLU, then one launch per matrix, then the ADD
     act = x
     if up is not None:
@@ -486,6 +490,14 @@ def test_q4_batch_set(gpu, orc, ns, k, m, mode):
         mi.device_sync()
         act_dev = dh
         act = dh.download(F32).reshape(m, k)  # the oracle matmul takes the GLU node's output
+    elif nw is not None:
+        dh = mi.DeviceBuffer(4 * m * k)
+        mi._call("mi_rms_norm", None, P(dx.ptr), P(dnw.ptr), P(dh.ptr), k, m, F32(1e-6))
+        mi.device_sync()
+        act_dev = dh
+        act = dh.download(F32).reshape(m, k)
+        for r in range(m):
+            assert ulp_diff(act[r], rms_norm_ref(x[r], nw, 1e-6)).max() <= 1
     else:
         act_dev = dx
     plain = []
@@ -518,11 +530,14 @@ def test_q4_batch_set_rejects_bad_shapes(gpu):
     w = _ptrs(mi.DeviceBuffer(256))
     y = _ptrs(mi.DeviceBuffer(256))
     with pytest.raises(mi.MiError):  # k not a multiple of 128
-        mi._call("mi_mul_mat_q4_0_f32_batch", None, 1, w, _i64s(16), y, None, None, 96, 2, P(256), P(None), P(256),
-                 1 << 20)
+        mi._call("mi_mul_mat_q4_0_f32_batch", None, 1, w, _i64s(16), y, None, None, 96, 2, P(256), P(None), P(None),
+                 F32(0), P(256), 1 << 20)
     with pytest.raises(mi.MiError):  # 17 activation rows
-        mi._call("mi_mul_mat_q4_0_f32_batch", None, 1, w, _i64s(16), y, None, None, 128, 17, P(256), P(None), P(256),
-                 1 << 20)
+        mi._call("mi_mul_mat_q4_0_f32_batch", None, 1, w, _i64s(16), y, None, None, 128, 17, P(256), P(None), P(None),
+                 F32(0), P(256), 1 << 20)
+    with pytest.raises(mi.MiError):  # RMSNorm of a row longer than 4096
+        mi._call("mi_mul_mat_q4_0_f32_batch", None, 1, w, _i64s(16), y, None, None, 4224, 2, P(256), P(None), P(256),
+                 F32(1e-6), P(256), 1 << 20)
 
 
 @pytest.mark.parametrize("norm", [True, False])
