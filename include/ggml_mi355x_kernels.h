@@ -169,6 +169,16 @@ int mi_qkv_rope_kv_q8_0(void *stream, const void *const *w_packed, const int64_t
                         int64_t head_dim, const int32_t *pos, float freq_base, float freq_scale, float attn_factor,
                         float *q_out, void *k_cache, size_t k_row_bytes, void *v_cache, size_t v_row_bytes,
                         const void *kv_idx, int kv_idx_is_i64, int64_t n_cache_rows, const float *rope_table);
+/* [RMS_NORM -> MUL(norm_w)] -> gate and up MUL_MATs (Q8_0, n_ff x k each, one activation
+ * row, k <= 2048, SmoothQuant inv_s of both) -> GLU swiglu -> the down projection's Q8_0
+ * activation quantization (its SmoothQuant inv_s_down, length n_ff, or NULL) in one
+ * launch: xq as mi_act_quant_q8_0 writes it for (1, n_ff), ready for mi_gemv_q8_0_add.
+ * n_ff % 32 == 0.  Bit-identical to mi_mul_mat_q8_0_f32_fused then mi_swiglu_quant_q8_0.
+ * Replaces the CANN gate/up matmuls and the SwiGLU node before the down projection
+ * (patch:1188-1355 per matmul). */
+int mi_gate_up_swiglu_q8_0(void *stream, const void *w_gate, const void *w_up, int64_t n_ff, int64_t k,
+                           const float *x, const float *norm_w, float eps, const float *inv_s,
+                           const float *inv_s_down, int rounding, void *xq);
 /* GLU swiglu(g, u) of one row (k floats) times inv_s, quantized to Q8_0 into xq (the
  * planar layout of mi_act_quant_q8_0 with m = 1): the input side of the down projection */
 int mi_swiglu_quant_q8_0(void *stream, const float *g, const float *u, const float *inv_s, int64_t k, void *xq,

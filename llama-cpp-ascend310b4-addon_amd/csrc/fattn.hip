@@ -37,6 +37,7 @@ struct FaPlan {
     bool mfma;
 };
 
+
 // One workgroup per (split, kv head), each with 4 waves of lane groups (one KV row
 // per lane group: 16 groups per workgroup at D = 128, 32 at D = 64).  A workgroup's
 // time is a chain of dependent steps per tile, so short contexts get one short tile
@@ -468,8 +469,8 @@ __device__ __forceinline__ half4_t h4(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(half4_t, t);
 }
 
-template <int D, int GQ, bool MASK, int NBW>
-__global__ __launch_bounds__(256) void k_fa_mfma(const float *__restrict__ q, const uint8_t *__restrict__ kc,
+template <int D, int GQ, bool MASK, int NBW, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void k_fa_mfma(const float *__restrict__ q, const uint8_t *__restrict__ kc,
                                                  const uint8_t *__restrict__ vc, const uint16_t *__restrict__ mask,
                                                  const int32_t *__restrict__ kv_len_p, int n_kv, size_t k_nb1,
                                                  size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, int chunk,
@@ -491,9 +492,9 @@ __global__ __launch_bounds__(256) void k_fa_mfma(const float *__restrict__ q, co
     constexpr int VT = D / 16;    // output tiles = V halves per lane per row
     constexpr int VW = D / 32;    // V dwords per lane per row
     constexpr int PS = part_stride<D>();
-    __shared__ float s_m[4][16];
-    __shared__ float s_l[4][16];
-    __shared__ __align__(16) float s_o[4][GQ][D];
+    __shared__ float s_m[NW][16];
+    __shared__ float s_l[NW][16];
+    __shared__ __align__(16) float s_o[NW][GQ][D];
 
     const int split = blockIdx.x;
     const int kvh = blockIdx.y;
@@ -638,16 +639,16 @@ __global__ __launch_bounds__(256) void k_fa_mfma(const float *__restrict__ q, co
     }
     __syncthreads();
 
-    for (int idx = tid; idx < GQ * D; idx += 256) {
+    for (int idx = tid; idx < GQ * D; idx += 64 * NW) {
         const int h = idx / D;
         const int dd = idx % D;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < 4; w++) M = fmaxf(M, s_m[w][h]);
+        for (int w = 0; w < NW; w++) M = fmaxf(M, s_m[w][h]);
         float L = 0.0f, acc = 0.0f;
         if (M != -INFINITY) {
 #pragma unroll
-            for (int w = 0; w < 4; w++) {
+            for (int w = 0; w < NW; w++) {
                 const float e = fexp2(s_m[w][h] - M);
                 L += s_l[w][h] * e;
                 acc += s_o[w][h][dd] * e;
@@ -672,7 +673,9 @@ __global__ __launch_bounds__(256) void k_fa_mfma(const float *__restrict__ q, co
             }
         }
     }
-    if (n_splits > 1 && counters) fa_merge_last<D, GQ>(part, out, counters + kvh, kvh, n_splits, tid);
+    if constexpr (NW == 4) {
+        if (n_splits > 1 && counters) fa_merge_last<D, GQ>(part, out, counters + kvh, kvh, n_splits, tid);
+    }
 }
 
 // Parallel log-sum-exp combine for many splits: grid (q head, D/32 dim slices),

@@ -798,6 +798,41 @@ int try_fuse_gate_up_down_q4(BackendCtx *ctx, ggml_cgraph *g, int i, const Consu
     return (ad ? next_real(g, jd + 1) : jd) + 1 - i;
 }
 
+// A8W8 FFN: [norm] -> gate, up -> GLU swiglu -> down MUL_MAT [-> ADD residual]: gate/up
+// write the down projection's quantized activation directly (two launches).  Opt-in
+// (MI_FUSE_GU_SWIGLU=1): a workgroup must own whole 32-row blocks of both matrices, so
+// the 1.5B shape gets 280 workgroups on 256 CUs, and the launch measured 10.9 us against
+// 8.2 + 2.6 us for the gate/up GEMV and the separate swiglu-quantize launch.
+int try_fuse_gate_up_down_q8(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C, int last,
+                             const ggml_tensor *const *mm, const ggml_tensor *x, const ggml_tensor *nw, float eps) {
+    static const bool on = env_flag("MI_FUSE_GU_SWIGLU", false);
+    if (!on) return 0;
+    const int nn = ggml_graph_n_nodes(g);
+    const int jg = next_real(g, last + 1);
+    if (jg >= nn) return 0;
+    const ggml_tensor *glu = ggml_graph_node(g, jg);
+    if (glu->op != GGML_OP_GLU || !supports_op_impl(glu) || glu->src[0] != mm[0] || glu->src[1] != mm[1] ||
+        mm[0]->ne[0] != mm[1]->ne[0] || !only_consumed_by(C, mm[0], {glu}) || !only_consumed_by(C, mm[1], {glu}))
+        return 0;
+    const int jd = next_real(g, jg + 1);
+    if (jd >= nn) return 0;
+    const ggml_tensor *down = ggml_graph_node(g, jd);
+    const int64_t nf = mm[0]->ne[0], k = x->ne[0];
+    if (!q8_gemv_node(down) || down->src[1] != glu || !only_consumed_by(C, glu, {down}) || down->src[0]->ne[0] != nf ||
+        nf % 32 || k > 2048 || ctx->scratch_size < mi_xq_size(1, nf))
+        return 0;
+    const ggml_tensor *vec = nullptr;
+    const ggml_tensor *ad = matmul_add_tail(g, jd, down, C, vec);
+    const TensorExtra *exd = (const TensorExtra *)down->src[0]->extra;
+    MI_K_CHECK(mi_gate_up_swiglu_q8_0(ctx->stream, ((const TensorExtra *)mm[0]->src[0]->extra)->packed,
+                                      ((const TensorExtra *)mm[1]->src[0]->extra)->packed, nf, k,
+                                      (const float *)x->data, nw ? (const float *)nw->data : nullptr, eps,
+                                      inv_s_of(mm[0]->src[0]), exd->inv_s, q8_rounding(), ctx->scratch));
+    MI_K_CHECK(mi_gemv_q8_0_add(ctx->stream, exd->packed, ctx->scratch, ad ? (const float *)vec->data : nullptr,
+                                (float *)(ad ? ad->data : down->data), down->src[0]->ne[1], nf, 1));
+    return (ad ? next_real(g, jd + 1) : jd) + 1 - i;
+}
+
 int try_fuse_norm_matmuls(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
     const int nn = ggml_graph_n_nodes(g);
     int j;
@@ -841,6 +876,9 @@ int try_fuse_norm_matmuls(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumer
         MI_K_CHECK(mi_mul_mat_q4_0_f32_fused(ctx->stream, cnt, w, n, y, nullptr, x->ne[0], (const float *)x->data,
                                              (const float *)nw->data, eps));
         return last + 1 - i;
+    }
+    if (cnt == 2) {
+        if (int used = try_fuse_gate_up_down_q8(ctx, g, i, C, last, mm, x, nw, eps)) return used;
     }
     MI_K_CHECK(mi_mul_mat_q8_0_f32_fused(ctx->stream, cnt, w, n, y, nullptr, x->ne[0], (const float *)x->data,
                                          (const float *)nw->data, eps, inv_s_of(mm[0]->src[0]), q8_rounding()));

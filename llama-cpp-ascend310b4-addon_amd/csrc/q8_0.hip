@@ -338,6 +338,70 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0_fused1(const Q8Set S, const f
     }
 }
 
+// Gate and up projections of one activation row (RMSNorm and SmoothQuant fused as in
+// fused1) with the swiglu and the down projection's Q8_0 activation quantization in the
+// epilogue.  A workgroup owns 32 consecutive h indices: gate rows 32b.. and up rows 32b..,
+// as four passes of 16 row slots, so the quantization block is whole.  Each row's dot
+// is fused1's (G = 16 lanes, same block order and reduction), so h and its quantization
+// equal the unfused GEMVs followed by the swiglu-quantize kernel bit for bit.
+template <int U, int XN, bool NORM>
+__global__ __launch_bounds__(256) void k_gemv_q8_0_gu_swiglu(const Q8Set S, const float *__restrict__ x,
+                                                             const float *__restrict__ norm_w, float eps,
+                                                             const float *__restrict__ inv_s,
+                                                             const float *__restrict__ inv_s_down,
+                                                             int8_t *__restrict__ xq_qs, uint16_t *__restrict__ xq_d,
+                                                             int nb, int rounding) {
+    constexpr int G = 16;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const FusedLds L = fused_lds(smem, nb);
+    __shared__ float s_gu[64];  // gate h 0..31, then up h 0..31
+    const int tid = threadIdx.x;
+    const int j = tid % G, slot = tid / G;
+    const int hb = blockIdx.x;  // h indices 32hb .. 32hb+31
+    const int k4 = nb * (QK / 4);
+
+    XStage<XN, NORM> st;
+    xstage_load(st, x, norm_w, inv_s, k4, tid);
+    int4 lo[4][U], hi[4][U];
+    uint32_t dw[4][U];
+    size_t rbase[4];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        rbase[p] = (size_t)(32 * hb + 16 * (p & 1) + slot) * nb;
+        if (p < 2) q8_first_pass<G, U>(S.qlo[0], S.qhi[0], S.d[0], rbase[p], nb, j, lo[p], hi[p], dw[p]);
+        else q8_first_pass<G, U>(S.qlo[1], S.qhi[1], S.d[1], rbase[p], nb, j, lo[p], hi[p], dw[p]);
+    }
+    const float scale = xstage_scale(st, k4, eps, L.red, tid);  // 1 without NORM
+    xstage_quant(st, inv_s, k4, scale, rounding, L.qs, L.d, tid);
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const float s = p < 2 ? q8_row_dot<G, U>(S.qlo[0], S.qhi[0], S.d[0], rbase[p], nb, j, lo[p], hi[p], dw[p],
+                                                 L.qs, L.d)
+                              : q8_row_dot<G, U>(S.qlo[1], S.qhi[1], S.d[1], rbase[p], nb, j, lo[p], hi[p], dw[p],
+                                                 L.qs, L.d);
+        if (j == 0) s_gu[16 * p + slot] = s;
+    }
+    __syncthreads();
+    if (tid < 8) {  // 4 consecutive h values per lane, 8 lanes per 32-block (as the swiglu-quantize kernel)
+        const int i = 4 * tid;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float gv = s_gu[i + e], uv = s_gu[32 + i + e];
+            v[e] = (gv / (1.0f + expf(-gv))) * uv;
+        }
+        if (inv_s_down) {
+            const float4 sv = ((const float4 *)inv_s_down)[8 * hb + tid];
+            v[0] *= sv.x; v[1] *= sv.y; v[2] *= sv.z; v[3] *= sv.w;
+        }
+        float d;
+        const uint32_t q = quant4(v[0], v[1], v[2], v[3], rounding, d);
+        *(uint32_t *)(xq_qs + (size_t)32 * hb + i) = q;
+        if (tid == 0) xq_d[hb] = f2h(d);
+    }
+}
+
 // The projection of an attention output still in flash-decoding split form: every
 // workgroup merges the splits' records (log-sum-exp combine) for the whole row in its
 // prologue, then scales by the SmoothQuant reciprocal and quantizes as fused1 does.
@@ -884,6 +948,56 @@ int mi_mul_mat_q8_0_f32_fused(void *stream, int n_mats, const void *const *w_pac
     int n_total = 0;
     if (int r = make_set(S, n_mats, w_packed, n, y, k, n_total, add)) return r;
     return launch_fused((hipStream_t)stream, S, n_total, k, x, norm_w, eps, inv_s, rounding);
+}
+
+int mi_gate_up_swiglu_q8_0(void *stream, const void *w_gate, const void *w_up, int64_t n_ff, int64_t k,
+                           const float *x, const float *norm_w, float eps, const float *inv_s,
+                           const float *inv_s_down, int rounding, void *xq) {
+    MI_CHECK_ARG(w_gate && w_up && x && xq, "gate_up_swiglu_q8_0: null pointer");
+    if (int r = check_shape("gate_up_swiglu_q8_0", n_ff, k)) return r;
+    MI_CHECK_ARG(n_ff % QK == 0, "gate_up_swiglu_q8_0: n_ff=%lld not a multiple of 32", (long long)n_ff);
+    MI_CHECK_ARG(k <= 2048, "gate_up_swiglu_q8_0: k=%lld > 2048", (long long)k);
+    MI_CHECK_ARG(mi::aligned(w_gate, 256) && mi::aligned(w_up, 256), "gate_up_swiglu_q8_0: packed weights not 256-byte aligned");
+    MI_CHECK_ARG(mi::aligned(x, 16) && (!norm_w || mi::aligned(norm_w, 16)) && (!inv_s || mi::aligned(inv_s, 16)) &&
+                     (!inv_s_down || mi::aligned(inv_s_down, 16)) && mi::aligned(xq, 4),
+                 "gate_up_swiglu_q8_0: misaligned vectors");
+    const Q8Planes p = q8_planes(n_ff, k);
+    Q8Set S;
+    const uint8_t *wb[2] = {(const uint8_t *)w_gate, (const uint8_t *)w_up};
+    for (int i = 0; i < 4; i++) {
+        const uint8_t *b = wb[i < 2 ? i : 0];
+        S.qlo[i] = b;
+        S.qhi[i] = b + p.plane;
+        S.d[i] = (const uint16_t *)(b + 2 * p.plane);
+        S.y[i] = nullptr;
+        S.add[i] = nullptr;
+        S.row_end[i] = INT_MAX;
+    }
+    const int nb = (int)(k / QK);
+    const int xn = (int)((k / 4 + 255) / 256);
+    int8_t *qs = (int8_t *)xq;
+    uint16_t *dq = (uint16_t *)((uint8_t *)xq + mi_xq_d_offset(1, n_ff));
+    hipStream_t st = (hipStream_t)stream;
+    const dim3 grid((unsigned)(n_ff / QK));
+#define MI_GUS(UU, XX, NN)                                                                                         \
+    hipLaunchKernelGGL((k_gemv_q8_0_gu_swiglu<UU, XX, NN>), grid, dim3(256), fused_smem(nb), st, S, x, norm_w, eps, \
+                       inv_s, inv_s_down, qs, dq, nb, rounding)
+#define MI_GUS_U(XX, NN)                        \
+    switch (pick_u(nb, 16)) {                   \
+        case 1: MI_GUS(1, XX, NN); break;       \
+        case 2: MI_GUS(2, XX, NN); break;       \
+        case 3: MI_GUS(3, XX, NN); break;       \
+        default: MI_GUS(4, XX, NN); break;      \
+    }
+    if (norm_w) {
+        if (xn <= 1) { MI_GUS_U(1, true) } else { MI_GUS_U(2, true) }
+    } else {
+        if (xn <= 1) { MI_GUS_U(1, false) } else { MI_GUS_U(2, false) }
+    }
+#undef MI_GUS_U
+#undef MI_GUS
+    MI_CHECK_LAUNCH("k_gemv_q8_0_gu_swiglu");
+    return MI_OK;
 }
 
 int mi_mul_mat_q8_0_f32_lse(void *stream, const void *w_packed, int64_t n, float *y, const float *add,

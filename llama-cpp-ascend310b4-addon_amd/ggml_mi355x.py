@@ -103,6 +103,7 @@ _SIGS = {
     "mi_argmax": (_I, [_P, _P, _P, _I64, _I64, _P, _SZ]),
     "mi_mul_mat_q8_0_f32_fused": (_I, [_P, _I, _P, _P, _P, _P, _I64, _P, _P, _F, _P, _I]),
     "mi_mul_mat_q8_0_f32_lse": (_I, [_P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _I]),
+    "mi_gate_up_swiglu_q8_0": (_I, [_P, _P, _P, _I64, _I64, _P, _P, _F, _P, _P, _I, _P]),
     "mi_mul_mat_q4_0_f32_batch": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _F, _P, _SZ]),
     "mi_rope_kv_rows": (_I, [_P, _P, _P, _P, _P, _P, _SZ, _P, _SZ, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _F,
                              _F, _F]),

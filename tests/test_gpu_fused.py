@@ -344,6 +344,47 @@ def test_swiglu_quant(gpu, orc, k):
     assert d_same >= 0.99 and dq_.max() <= 1 and np.mean(dq_ > 0) < 1e-3
 
 
+@pytest.mark.parametrize("norm", [True, False])
+@pytest.mark.parametrize("nff,k", [(8960, 1536), (4864, 896), (11008, 2048), (512, 256)])
+def test_gate_up_swiglu_q8_0(gpu, orc, nff, k, norm):
+    """Normed gate+up with the swiglu and the down projection's activation quantization in
+    the epilogue: the quantized activation is byte-identical to the fused gate/up GEMV
+    followed by the swiglu-quantize kernel, and its blocks follow the oracle's quantizer
+    of the oracle's gate/up (scales exact on >= 99% of blocks, int8 within one step)."""
+    mi = gpu
+    P = mi._P
+    rng = np.random.default_rng(nff + k + norm)
+    x = (rng.standard_normal(k) * 0.5).astype(F32)
+    nw = rng.uniform(0.8, 1.2, k).astype(F32)
+    inv = (1.0 / rng.uniform(0.5, 2.0, k)).astype(F32)
+    inv_d = (1.0 / rng.uniform(0.5, 2.0, nff)).astype(F32)
+    wg, wu = q8_0_weights(rng, nff, k), q8_0_weights(rng, nff, k)
+    pg, pu = _packed_q8(mi, wg, nff, k), _packed_q8(mi, wu, nff, k)
+    dx, dnw, dinv, dinvd = mi.to_device(x), mi.to_device(nw), mi.to_device(inv), mi.to_device(inv_d)
+    xq = mi.DeviceBuffer(mi.xq_size(1, nff))
+    mi._call("mi_gate_up_swiglu_q8_0", None, P(pg.ptr), P(pu.ptr), nff, k, P(dx.ptr), P(dnw.ptr if norm else None),
+             F32(1e-6), P(dinv.ptr), P(dinvd.ptr), mi.Q8_ROUND_X86, P(xq.ptr))
+    yg, yu = mi.DeviceBuffer(4 * nff), mi.DeviceBuffer(4 * nff)
+    mi._call("mi_mul_mat_q8_0_f32_fused", None, 2, _ptrs(pg, pu), _i64s(nff, nff), _ptrs(yg, yu), None, k,
+             P(dx.ptr), P(dnw.ptr if norm else None), F32(1e-6), P(dinv.ptr), mi.Q8_ROUND_X86)
+    xq2 = mi.DeviceBuffer(mi.xq_size(1, nff))
+    mi._call("mi_swiglu_quant_q8_0", None, P(yg.ptr), P(yu.ptr), P(dinvd.ptr), nff, P(xq2.ptr), mi.Q8_ROUND_X86)
+    mi.device_sync()
+    doff = mi.xq_d_offset(1, nff)
+    qs, d = xq.download(np.int8, nff), xq.download(np.uint16, nff // 32, offset=doff)
+    assert np.array_equal(qs, xq2.download(np.int8, nff))
+    assert np.array_equal(d, xq2.download(np.uint16, nff // 32, offset=doff))
+    xin = rms_norm_ref(x, nw, 1e-6) if norm else x
+    g = _q8_ref(orc, wg, xin, nff, k, inv)
+    u = _q8_ref(orc, wu, xin, nff, k, inv)
+    v = ((g.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64)))).astype(F32) * u).astype(F32)
+    ref = orc.quantize_row_q8_0(v, inv_s=inv_d, variant=orc.Q8_ROUND_X86).reshape(nff // 32, 34)
+    got = xq_to_blocks(qs, d, nff).reshape(nff // 32, 34)
+    d_same = np.mean(np.all(got[:, :2] == ref[:, :2], axis=1))
+    dq_ = np.abs(got[:, 2:].view(np.int8).astype(int) - ref[:, 2:].view(np.int8).astype(int))
+    assert d_same >= 0.99 and dq_.max() <= 1 and np.mean(dq_ > 0) < 1e-2
+
+
 def test_gemv_q8_0_add_equals_gemv_plus_vector(gpu):
     mi = gpu
     rng = np.random.default_rng(11)
