@@ -48,11 +48,7 @@ __device__ __forceinline__ float xstage_scale(const XStage<XN, NORM> &st, int k4
                 ss += (double)sq_rn(v.w);
             }
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        if ((tid & 63) == 0) s_red[tid >> 6] = ss;
-        __syncthreads();
-        const double tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+        const double tot = block_sum_d256(ss, s_red, tid);
         const float mean = (float)(tot / (double)(k4 * 4));
         return 1.0f / sqrtf(mean + eps);
     }

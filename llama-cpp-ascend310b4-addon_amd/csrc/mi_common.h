@@ -119,6 +119,39 @@ __device__ __forceinline__ float group_max(float v) {
     return v;
 }
 
+// 64-bit DPP move of a double (both halves through the 32-bit DPP path)
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const int2 p = __builtin_bit_cast(int2, v);
+    int2 r;
+    r.x = __builtin_amdgcn_update_dpp(0, p.x, CTRL, 0xf, 0xf, true);
+    r.y = __builtin_amdgcn_update_dpp(0, p.y, CTRL, 0xf, 0xf, true);
+    return __builtin_bit_cast(double, r);
+}
+
+__device__ __forceinline__ double readlane_d(double v, int lane) {
+    const int2 p = __builtin_bit_cast(int2, v);
+    int2 r;
+    r.x = __builtin_amdgcn_readlane(p.x, lane);
+    r.y = __builtin_amdgcn_readlane(p.y, lane);
+    return __builtin_bit_cast(double, r);
+}
+
+// Sum of one double per thread over a 256-thread workgroup, in one fixed order (every
+// RMSNorm of this library sums its squares through it, so fused and standalone norms
+// agree bit for bit): rows of 16 lanes by DPP, the 4 row sums of a wave by readlane,
+// the 4 wave sums through s_red[4] after one barrier.  Every thread must call it.
+__device__ __forceinline__ double block_sum_d256(double v, double *s_red, int tid) {
+    v += dpp_d<DPP_QUAD_1032>(v);
+    v += dpp_d<DPP_QUAD_2301>(v);
+    v += dpp_d<DPP_ROW_HALF_MIRROR>(v);
+    v += dpp_d<DPP_ROW_MIRROR>(v);
+    const double w = (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+    if ((tid & 63) == 0) s_red[tid >> 6] = w;
+    __syncthreads();
+    return (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+}
+
 // streaming (read-once) 16-byte load of weights
 typedef int int4v_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ int4 ld_stream16(const void *p) {

@@ -454,11 +454,7 @@ __global__ __launch_bounds__(256) void k_perm_norm_f16(const float *__restrict__
             s += (double)sq_rn(xv[t].w);
         }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-    if ((tid & 63) == 0) s_red[tid >> 6] = s;
-    __syncthreads();
-    const double tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    const double tot = block_sum_d256(s, s_red, tid);
     const float mean = (float)(tot / ne0);
     const float scale = 1.0f / sqrtf(mean + eps);
 #pragma unroll
