@@ -436,8 +436,9 @@ __device__ __forceinline__ void fa_merge_last(const float *part, float *out, uns
 //   O[16 heads x 16 dims] += P^T[heads x pos] . V      (8 tiles at D = 128)
 // The C layout of the score MFMA (lane (g, c): positions 4g..4g+3 of head c) is the A
 // layout P^T needs, so probabilities go from the softmax straight into the PV MFMA.
-// The k index of both products is permuted so that every lane's loads are contiguous
-// 16-byte chunks: lane (g, c) reads K row c at dims [D/4*g, D/4*(g+1)) and V rows
+// The k index of both products is permuted so that every load instruction reads
+// contiguous bytes: lane (g, c) reads K row c in 16-byte chunks at dims 32i + 8g .. +7
+// (the 4 g-lanes of a row cover 64 contiguous bytes per instruction) and V rows
 // 4g..4g+3 at dims [D/16*c, D/16*(c+1)); output tile t column c is dim D/16*c + t.
 // P is split into fp16 hi + lo parts (two MFMAs) so the PV product keeps fp32-level
 // accuracy.  Online softmax per head in log2 units; the waves merge through LDS.
@@ -461,6 +462,18 @@ __device__ __forceinline__ void ld_bytes(uint32_t *dst, const uint8_t *src) {
     } else {
         const int2 v = *(const int2 *)src;
         dst[0] = (uint32_t)v.x; dst[1] = (uint32_t)v.y;
+    }
+}
+
+// K row slice of lane group g: NC 16-byte chunks at byte offsets 64i + 16g, so that one
+// load instruction covers a contiguous 64-byte piece of each of its 16 rows
+template <int NC>
+__device__ __forceinline__ void ld_k_chunks(uint32_t *dst, const uint8_t *src) {
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+        const int4 v = *(const int4 *)(src + 64 * i);
+        dst[4 * i] = (uint32_t)v.x; dst[4 * i + 1] = (uint32_t)v.y;
+        dst[4 * i + 2] = (uint32_t)v.z; dst[4 * i + 3] = (uint32_t)v.w;
     }
 }
 
@@ -511,20 +524,21 @@ __global__ __launch_bounds__(64 * NW) void k_fa_mfma(const float *__restrict__ q
     const int end_eff = min(end_phys, eff);
     const int wstart = start + wave * NBW * 16;
 
-    // q fragment (B operand): lane (g, c) holds head c, dims D/4*g + 4s .. +3 for step s
+    // q fragment (B operand): lane (g, c) holds head c, dims 32*(s/2) + 8g + 4*(s%2) .. +3
+    // for step s, the dims its K chunks hold
     half4_t qf[KS];
     {
-        const float *qh = q + (size_t)(kvh * GQ + min(c, GQ - 1)) * D + (D / 4) * g;
+        const float *qh = q + (size_t)(kvh * GQ + min(c, GQ - 1)) * D + 8 * g;
 #pragma unroll
         for (int s2 = 0; s2 < KS; s2++) {
-            const float4 v = *(const float4 *)(qh + 4 * s2);
+            const float4 v = *(const float4 *)(qh + 32 * (s2 / 2) + 4 * (s2 % 2));
             const uint32_t a = (uint32_t)f2h(v.x) | ((uint32_t)f2h(v.y) << 16);
             const uint32_t b = (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16);
             qf[s2] = c < GQ ? h4(a, b) : h4(0u, 0u);
         }
     }
 
-    const uint8_t *kb = kc + (size_t)kvh * k_nb2 + (size_t)(D / 2) * g;
+    const uint8_t *kb = kc + (size_t)kvh * k_nb2 + (size_t)16 * g;
     const uint8_t *vb = vc + (size_t)kvh * v_nb2 + (size_t)(D / 8) * c;
     const int last = end_phys - 1;
 
@@ -537,7 +551,7 @@ __global__ __launch_bounds__(64 * NW) void k_fa_mfma(const float *__restrict__ q
     U32s<VW> vr[2][4];
     auto issue = [&](int blk, int buf) {
         const int p0 = wstart + blk * 16;
-        ld_bytes<D / 2>(kr[buf].w, kb + (size_t)min(p0 + c, last) * k_nb1);
+        ld_k_chunks<D / 32>(kr[buf].w, kb + (size_t)min(p0 + c, last) * k_nb1);
 #pragma unroll
         for (int r = 0; r < 4; r++) ld_bytes<D / 8>(vr[buf][r].w, vb + (size_t)min(p0 + 4 * g + r, last) * v_nb1);
     };
