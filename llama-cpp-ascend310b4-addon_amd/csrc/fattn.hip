@@ -692,65 +692,68 @@ __global__ __launch_bounds__(64 * NW) void k_fa_mfma(const float *__restrict__ q
     }
 }
 
-// Parallel log-sum-exp combine for many splits: grid (q head, D/32 dim slices),
-// 256 threads = 32 dims x 8 split groups; split weights exp(m_s - M) in LDS.
+// Parallel log-sum-exp combine: grid (q head, D/32 dim slices, sequence), 256 threads =
+// 32 dims x 8 split groups.  A thread merges splits g, g+8, ... of its group itself
+// (online: running maximum, rescaled sums), loading every split's m, l and output value
+// of a 64-split chunk at once, so a chunk costs one round trip; the 8 groups then merge
+// through LDS.  w_s = 2^(m_s - M), 0 for a split with no position; out = sum w_s o_s /
+// sum w_s l_s, 0 when no split has a position.
 template <int D>
 __global__ __launch_bounds__(256) void k_fa_combine(const float *__restrict__ part, float *__restrict__ out,
                                                     int n_splits, size_t out_seq) {
     constexpr int PS = part_stride<D>();
     part += (size_t)blockIdx.z * gridDim.x * n_splits * PS;
     out += (size_t)blockIdx.z * out_seq;
-    __shared__ float s_w[kMaxSplits];
-    __shared__ float s_red[8][32];
-    __shared__ float s_wave[4];
+    __shared__ float s_m[8][32], s_l[8][32], s_a[8][32];
     const int h = blockIdx.x;
     const int d0 = blockIdx.y * 32;
     const int tid = threadIdx.x;
-    const int lane = tid % 64, wave = tid / 64;
-    const float *ph = part + (size_t)h * n_splits * PS;
-
-    float mx = -INFINITY;
-    for (int sp = tid; sp < n_splits; sp += 256) mx = fmaxf(mx, ph[(size_t)sp * PS + D]);
-    mx = group_max<64>(mx);
-    if (lane == 0) s_wave[wave] = mx;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(s_wave[0], s_wave[1]), fmaxf(s_wave[2], s_wave[3]));
-    __syncthreads();
-    float ls = 0.0f;
-    for (int sp = tid; sp < n_splits; sp += 256) {
-        const float ms = ph[(size_t)sp * PS + D];
-        const float w = (ms == -INFINITY || M == -INFINITY) ? 0.0f : fexp2(ms - M);
-        s_w[sp] = w;
-        ls += ph[(size_t)sp * PS + D + 1] * w;
-    }
-    ls = group_sum<64>(ls);
-    if (lane == 0) s_wave[wave] = ls;
-    __syncthreads();
-    const float L = s_wave[0] + s_wave[1] + s_wave[2] + s_wave[3];
-
     const int dd = tid % 32, sg = tid / 32;
-    float a0 = 0.0f, a1 = 0.0f;
+    const float *ph = part + (size_t)h * n_splits * PS;
+    float M = -INFINITY, L = 0.0f, A = 0.0f;
     for (int base = 0; base < n_splits; base += 64) {
-        float ov[8], wv[8];
+        float mv[8], lv[8], ov[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {  // clamped, branch-free: all 8 loads in flight
+        for (int u = 0; u < 8; u++) {  // clamped, branch-free: all loads of the chunk in flight
             const int sp = base + sg + 8 * u;
-            ov[u] = ph[(size_t)min(sp, n_splits - 1) * PS + d0 + dd];
-            wv[u] = sp < n_splits ? s_w[min(sp, n_splits - 1)] : 0.0f;
+            const float *rec = ph + (size_t)min(sp, n_splits - 1) * PS;
+            mv[u] = sp < n_splits ? rec[D] : -INFINITY;
+            lv[u] = rec[D + 1];
+            ov[u] = rec[d0 + dd];
         }
+        float cm = M;
 #pragma unroll
-        for (int u = 0; u < 8; u += 2) {
-            a0 = fmaf(ov[u], wv[u], a0);
-            a1 = fmaf(ov[u + 1], wv[u + 1], a1);
+        for (int u = 0; u < 8; u++) cm = fmaxf(cm, mv[u]);
+        if (cm == -INFINITY) continue;
+        const float r = M == -INFINITY ? 0.0f : fexp2(M - cm);
+        L *= r;
+        A *= r;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float w = mv[u] == -INFINITY ? 0.0f : fexp2(mv[u] - cm);
+            L = fmaf(lv[u], w, L);
+            A = fmaf(ov[u], w, A);
         }
+        M = cm;
     }
-    s_red[sg][dd] = a0 + a1;
+    s_m[sg][dd] = M;
+    s_l[sg][dd] = L;
+    s_a[sg][dd] = A;
     __syncthreads();
     if (tid < 32) {
-        float acc = 0.0f;
+        float mm = -INFINITY;
 #pragma unroll
-        for (int g = 0; g < 8; g++) acc += s_red[g][tid];
-        out[(size_t)h * D + d0 + tid] = L == 0.0f ? 0.0f : acc / L;
+        for (int g = 0; g < 8; g++) mm = fmaxf(mm, s_m[g][tid]);
+        float ll = 0.0f, aa = 0.0f;
+        if (mm != -INFINITY) {
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                const float w = s_m[g][tid] == -INFINITY ? 0.0f : fexp2(s_m[g][tid] - mm);
+                ll = fmaf(s_l[g][tid], w, ll);
+                aa = fmaf(s_a[g][tid], w, aa);
+            }
+        }
+        out[(size_t)h * D + d0 + tid] = ll == 0.0f ? 0.0f : aa / ll;
     }
 }
 
