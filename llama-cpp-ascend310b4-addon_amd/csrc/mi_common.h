@@ -152,6 +152,14 @@ __device__ __forceinline__ double block_sum_d256(double v, double *s_red, int ti
     return (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
 }
 
+// Entry i of a 4-entry array member of a by-value kernel argument, indexed through its
+// address: one scalar load from the kernel-argument segment (i must be wave-uniform).
+// A select between the four entries would cost a compare-and-select chain per use.
+template <class T>
+__device__ __forceinline__ T karg_at(const T (&a)[4], int i) {
+    return (&a[0])[i];
+}
+
 // streaming (read-once) 16-byte load of weights
 typedef int int4v_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ int4 ld_stream16(const void *p) {

@@ -337,10 +337,11 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma(const uint8_t *__res
     }
 }
 
-// Selecting a matrix's pointer: the four candidates pass through an empty asm
-// statement first, so the select works on register values.  A select between plain
-// loads of the by-value kernel argument would be rewritten into a load from a computed
-// address, which copies the struct to scratch memory.
+// Selecting a matrix's pointer once at a workgroup's start: the four candidates pass
+// through an empty asm statement first, so the select works on values already in scalar
+// registers.  Without it the compiler turns the select into a load from a computed
+// kernel-argument address, whose latency then sits in front of the first weight loads
+// (karg_at makes that load on purpose where a selection repeats inside a loop).
 template <class T>
 __device__ __forceinline__ T opaque_s(T v) {
     if constexpr (sizeof(T) == 8) {
@@ -492,6 +493,8 @@ struct Q4BSet {
     int wg_end[4];  // cumulative workgroup counts; unused slots INT_MAX
 };
 
+// selected once per workgroup: a register select (see opaque_s), not a kernel-argument
+// load whose latency would sit in front of the first weight loads
 #define Q4B_PICK(S, f, i) \
     pick4((i), opaque_s((S).f[0]), opaque_s((S).f[1]), opaque_s((S).f[2]), opaque_s((S).f[3]))
 
@@ -699,14 +702,16 @@ struct Q4Set {
     int row_end[4];
 };
 
-#define Q4SET_PICK(S, f, i) \
-    pick4((i), opaque_s((S).f[0]), opaque_s((S).f[1]), opaque_s((S).f[2]), opaque_s((S).f[3]))
+// The register kernel selects a unit's matrix once per unit inside its loop: a scalar
+// load from the kernel-argument segment per pointer (hidden behind the previous unit's
+// math) costs far fewer scalar instructions than a select chain.
+#define Q4SET_PICK(S, f, i) karg_at((S).f, (i))
 
 __device__ __forceinline__ int q4set_index(const Q4Set &S, int r) {
     return (r >= S.row_end[0]) + (r >= S.row_end[1]) + (r >= S.row_end[2]);
 }
 __device__ __forceinline__ int q4set_row_start(const Q4Set &S, int i) {
-    return pick4(i, 0, opaque_s(S.row_end[0]), opaque_s(S.row_end[1]), opaque_s(S.row_end[2]));
+    return i == 0 ? 0 : karg_at(S.row_end, i - 1);
 }
 
 // unit modes: which two rows a unit holds and what its epilogue does

@@ -205,9 +205,9 @@ __device__ __forceinline__ int q8set_row_start(const Q8Set &S, int i) {
     return i == 0 ? 0 : i == 1 ? S.row_end[0] : i == 2 ? S.row_end[1] : S.row_end[2];
 }
 
-// member `f` of slot i, selected with constant indices only: indexing the by-value
-// kernel argument through a reference would copy it to scratch memory and turn the
-// weight pointers into flat addresses
+// member `f` of slot i, selected once per workgroup with constant indices (the values
+// are already in scalar registers; a load from the kernel-argument segment would put its
+// latency in front of the first weight loads)
 #define Q8SET_PICK(S, f, i) ((i) == 0 ? (S).f[0] : (i) == 1 ? (S).f[1] : (i) == 2 ? (S).f[2] : (S).f[3])
 
 // RMSNorm (optional), then the SmoothQuant reciprocal, then Q8_0 quantization of each
