@@ -670,24 +670,40 @@ __global__ __launch_bounds__(256) void k_cast_f16(const float *__restrict__ x, u
 //   xs[4t+1] = (x[4t+1],  x[4t+3])     <- (v >>  8) & 0x000f000f
 //   xs[4t+2] = (x[16+4t], x[16+4t+2])  <- (v >>  4) & 0x000f000f
 //   xs[4t+3] = (x[17+4t], x[19+4t])    <- (v >> 12) & 0x000f000f
-// OR 0x6400 makes each nibble the exact fp16 1024 + nib; subtracting 1032 gives nib - 8.
-// magic: 0x64006400 held in a VGPR by the caller, so that each AND-OR is one
-// v_and_or_b32 (gfx9 VOP3 takes no literal and one scalar operand)
-__device__ __forceinline__ float q4_dot_xr(const int4 q, const uint32_t *xs, uint32_t magic) {
-    const half2_t off = {(half_t)1032.0f, (half_t)1032.0f};
+// Shifted to mantissa bits 6..9 and ORed with 0x4C00 (16.0), each nibble becomes the
+// exact fp16 16 + nib (the binade [16, 32) has a 1/64 step).  The dot runs on those
+// values and the offset comes out once per block: sum (nib - 8) x = sum (16 + nib) x -
+// 24 * sum x, with sum x of the lane's block formed once per kernel (q4_xr_block_sum).
+// The fp16 products are exact in fp32 and the partial sums stay within ~25x the block's
+// activation magnitude, so the result keeps fp32-level accuracy; per nibble pair this is
+// a shift and an AND-OR, with no fp16 subtraction.  magic: 0x4C004C00 held in a VGPR by
+// the caller, so that each AND-OR is one v_and_or_b32 (gfx9 VOP3 takes no literal and
+// one scalar operand).
+__device__ __forceinline__ float q4_dot_xr(const int4 q, const uint32_t *xs, uint32_t magic, float xsum) {
     const uint32_t qq[4] = {(uint32_t)q.x, (uint32_t)q.y, (uint32_t)q.z, (uint32_t)q.w};
     float s = 0.0f;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
         const uint32_t v = qq[t];
-        const uint32_t a = (v & 0x000f000fu) | magic;
-        const uint32_t c = ((v >> 8) & 0x000f000fu) | magic;
-        const uint32_t b = ((v >> 4) & 0x000f000fu) | magic;
-        const uint32_t d = ((v >> 12) & 0x000f000fu) | magic;
-        s = fdot2(h22u(u2h2(a) - off), xs[4 * t + 0], s);
-        s = fdot2(h22u(u2h2(c) - off), xs[4 * t + 1], s);
-        s = fdot2(h22u(u2h2(b) - off), xs[4 * t + 2], s);
-        s = fdot2(h22u(u2h2(d) - off), xs[4 * t + 3], s);
+        const uint32_t a = ((v << 6) & 0x03c003c0u) | magic;  // low nibbles of bytes 0, 2
+        const uint32_t c = ((v >> 2) & 0x03c003c0u) | magic;  // low nibbles of bytes 1, 3
+        const uint32_t b = ((v << 2) & 0x03c003c0u) | magic;  // high nibbles of bytes 0, 2
+        const uint32_t d = ((v >> 6) & 0x03c003c0u) | magic;  // high nibbles of bytes 1, 3
+        s = fdot2(a, xs[4 * t + 0], s);
+        s = fdot2(c, xs[4 * t + 1], s);
+        s = fdot2(b, xs[4 * t + 2], s);
+        s = fdot2(d, xs[4 * t + 3], s);
+    }
+    return fmaf(-24.0f, xsum, s);
+}
+
+// sum of the 32 activation values of one block (the lane's 16 permuted pairs)
+__device__ __forceinline__ float q4_xr_block_sum(const uint32_t *xs) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const half2_t h = u2h2(xs[j]);
+        s += (float)h.x + (float)h.y;
     }
     return s;
 }
@@ -778,14 +794,14 @@ __device__ __forceinline__ void xr_load(XrRows<KB> &W, const Q4Set &S, int r0, i
 }
 
 template <int KB>
-__device__ __forceinline__ void xr_dot(const XrRows<KB> &W, const uint32_t (*xr)[16], const bool *bval, float &s0,
-                                       float &s1, uint32_t magic) {
+__device__ __forceinline__ void xr_dot(const XrRows<KB> &W, const uint32_t (*xr)[16], const float *xsum,
+                                       const bool *bval, float &s0, float &s1, uint32_t magic) {
     s0 = 0.0f;
     s1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < KB; i++) {
-        const float a = q4_dot_xr(W.w[0][i], xr[i], magic);
-        const float b = q4_dot_xr(W.w[1][i], xr[i], magic);
+        const float a = q4_dot_xr(W.w[0][i], xr[i], magic, xsum[i]);
+        const float b = q4_dot_xr(W.w[1][i], xr[i], magic, xsum[i]);
         const float t0 = fmaf(h2f((uint16_t)W.d[0][i]), a, s0);
         const float t1 = fmaf(h2f((uint16_t)W.d[1][i]), b, s1);
         s0 = bval[i] ? t0 : s0;
@@ -863,7 +879,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
     const int tid = threadIdx.x, lane = tid & 63;
     // the unit, row and matrix indices are wave-uniform: scalar registers and scalar selects
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    uint32_t magic = 0x64006400u;
+    uint32_t magic = 0x4C004C00u;
     asm volatile("" : "+v"(magic));
     const int pg = wave / WPR, ks = wave % WPR;
     int bidx[KB];
@@ -978,6 +994,9 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
             xr[i][4 * t + 3] = (w[8 + 2 * t] >> 16) | (w[9 + 2 * t] & 0xffff0000u);
         }
     }
+    float xsum[KB];
+#pragma unroll
+    for (int i = 0; i < KB; i++) xsum[i] = q4_xr_block_sum(xr[i]);
 
     if constexpr (WPR == 1) {
         // one pair group per wave, no workgroup barriers past this point
@@ -992,7 +1011,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
             xr_load<KB>(wb, S, q0, q1, bidx, !more_b, nb);
             __builtin_amdgcn_sched_barrier(0);  // the next pair's loads issue before this pair's math
             float s0, s1;
-            xr_dot<KB>(wa, xr, bval, s0, s1, magic);
+            xr_dot<KB>(wa, xr, xsum, bval, s0, s1, magic);
             s0 = group_sum<64>(s0);
             s1 = group_sum<64>(s1);
             xr_store<UM>(S, R, rp, h_out, u, r0, r1, ok1, s0, s1, wa.a[0], wa.a[1], lane);
@@ -1005,7 +1024,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
             xr_rows<UM>(S, R, more_a ? ua : u, n_rows, q0, q1, qok);
             xr_load<KB>(wa, S, q0, q1, bidx, !more_a, nb);
             __builtin_amdgcn_sched_barrier(0);  // the next pair's loads issue before this pair's math
-            xr_dot<KB>(wb, xr, bval, s0, s1, magic);
+            xr_dot<KB>(wb, xr, xsum, bval, s0, s1, magic);
             s0 = group_sum<64>(s0);
             s1 = group_sum<64>(s1);
             xr_store<UM>(S, R, rp, h_out, u, r0, r1, ok1, s0, s1, wb.a[0], wb.a[1], lane);
@@ -1048,7 +1067,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
             xr_load<KB>(wb, S, q0, q1, bidx, !more_b, nb);
             __builtin_amdgcn_sched_barrier(0);  // the next pair's loads issue before this pair's math
             float s0, s1;
-            xr_dot<KB>(wa, xr, bval, s0, s1, magic);
+            xr_dot<KB>(wa, xr, xsum, bval, s0, s1, magic);
             finish(u, r0, r1, ok1, s0, s1, wa.a[0], wa.a[1]);
             if (!more_b) break;
             base = nbase;
@@ -1060,7 +1079,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_xr(const Q4Set S, const void 
             xr_rows<UM>(S, R, min(more_a ? nbase2 + pg : u2, n_units - 1), n_rows, q0, q1, qok);
             xr_load<KB>(wa, S, q0, q1, bidx, !more_a, nb);
             __builtin_amdgcn_sched_barrier(0);  // the next pair's loads issue before this pair's math
-            xr_dot<KB>(wb, xr, bval, s0, s1, magic);
+            xr_dot<KB>(wb, xr, xsum, bval, s0, s1, magic);
             finish(u2, r0, r1, ok1, s0, s1, wb.a[0], wb.a[1]);
             if (!more_a) break;
             base = nbase2;
