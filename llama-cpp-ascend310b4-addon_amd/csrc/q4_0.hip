@@ -236,6 +236,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_0_gx(const uint8_t *__restrict_
 // C layout puts rows 4g..4g+3 and column c in lane (g, c).  KS waves of a workgroup
 // split k (partials reduced through LDS); with KS = 1 each wave owns 16 rows.
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ half4_t q4_nibbles(uint32_t v, int hi) {
@@ -384,11 +385,11 @@ __device__ __forceinline__ uint2 ldg_u2(uint64_t a) {
 }
 
 // Several activation rows on the matrix cores with the activation as the A operand:
-// D[16 rows of x][16 weight rows] += X[16 x 16 k] . W^T[16 k x 16 weight rows].  Lane
-// (g, c) supplies dword g of a block of weight row c (its low nibbles are the first
-// 16-k step, its high nibbles the second) and the activation row c's matching values;
-// it receives weight row c's results for activation rows 4g..4g+3, so it applies one
-// block scale (row c's) per block.  The activation comes converted to fp16 in the
+// D[16 rows of x][16 weight rows] += X[16 x 32 k] . W^T[32 k x 16 weight rows], one
+// v_mfma_f32_16x16x32_f16 per block.  Lane (g, c) supplies dword g of a block of weight
+// row c (k slots 0..3 its low nibbles, 4..7 its high nibbles) and the activation row c's
+// matching values; it receives weight row c's results for activation rows 4g..4g+3, so
+// it applies one block scale (row c's) per block.  The activation comes converted to fp16 in the
 // order in which a weight dword's nibbles come out (see q4_dot_xr):
 //   xp[row][block][g][8] = x[4g], x[4g+2], x[4g+1], x[4g+3], x[16+4g], x[18+4g], x[17+4g], x[19+4g]
 // one 16-byte load per block.  k is split over KS waves (partials reduced in LDS).
@@ -533,11 +534,16 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, co
     uint64_t wrow[TW];
 #pragma unroll
     for (int t = 0; t < TW; t++) wrow[t] = (uint64_t)min(row0 + 16 * t + c, n - 1) * nb;
-    const bool x_ok = c < m;
+    // activation rows past m (lanes c >= m) re-read row m - 1: their products land only in
+    // output rows >= m, which are never stored
     const uint4 *xrow = xp + (size_t)min(c, m - 1) * nb * 4 + g;
-    uint32_t magic = 0x64006400u;
+    // nibble q becomes fp16 16 + q (exponent of 16, q in the top mantissa bits); the 24
+    // this adds to each weight (q - 8) leaves through one more product per block with a
+    // constant -24 operand, shared by the TW tiles
+    uint32_t magic = 0x4C004C00u;
     asm volatile("" : "+v"(magic));
-    const half2_t off = {(half_t)1032.0f, (half_t)1032.0f};
+    const uint32_t m24 = 0xCE00CE00u;  // fp16 -24, -24
+    const half8_t neg24 = __builtin_bit_cast(half8_t, make_uint4(m24, m24, m24, m24));
 
     auto load = [&](Q4XStage<UG, TW> &st, int j0) {
 #pragma unroll
@@ -559,7 +565,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, co
 #pragma unroll
         for (int u = 0; u < UG; u++) {
             const bool valid = j0 + u < j_hi;
-            const half4_t z = {0, 0, 0, 0};
+            uint32_t ww[TW][4];
 #pragma unroll
             for (int t = 0; t < TW; t++) {
                 // transpose: lane (g, c) has dwords 0..3 of block g; wants dword g of blocks 0..3.
@@ -574,25 +580,27 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, co
                 const uint4 wt = *(const uint4 *)&s_t[wave][c][g][0];
                 __atomic_signal_fence(__ATOMIC_SEQ_CST);
                 __builtin_amdgcn_wave_barrier();
-                const uint32_t ww[4] = {wt.x, wt.y, wt.z, wt.w};
-                const uint32_t dd[4] = {st.d[u][t].x & 0xffffu, st.d[u][t].x >> 16, st.d[u][t].y & 0xffffu,
-                                        st.d[u][t].y >> 16};
+                ww[t][0] = wt.x;
+                ww[t][1] = wt.y;
+                ww[t][2] = wt.z;
+                ww[t][3] = wt.w;
+            }
 #pragma unroll
-                for (int jj = 0; jj < 4; jj++) {
-                    const uint32_t v = ww[jj];
-                    const half2_t a0 = u2h2((v & 0x000f000fu) | magic) - off;
-                    const half2_t a1 = u2h2(((v >> 8) & 0x000f000fu) | magic) - off;
-                    const half2_t b0h = u2h2(((v >> 4) & 0x000f000fu) | magic) - off;
-                    const half2_t b1h = u2h2(((v >> 12) & 0x000f000fu) | magic) - off;
-                    const half4_t wlo = {a0.x, a0.y, a1.x, a1.y};
-                    const half4_t whi = {b0h.x, b0h.y, b1h.x, b1h.y};
-                    const uint4 xv = st.x[u][jj];
-                    const half4_t xlo = x_ok ? __builtin_bit_cast(half4_t, make_uint2(xv.x, xv.y)) : z;
-                    const half4_t xhi = x_ok ? __builtin_bit_cast(half4_t, make_uint2(xv.z, xv.w)) : z;
-                    float4_t r = {0.f, 0.f, 0.f, 0.f};
-                    r = __builtin_amdgcn_mfma_f32_16x16x16f16(xlo, wlo, r, 0, 0, 0);
-                    r = __builtin_amdgcn_mfma_f32_16x16x16f16(xhi, whi, r, 0, 0, 0);
-                    const float ds = valid ? h2f((uint16_t)dd[jj]) : 0.0f;
+            for (int jj = 0; jj < 4; jj++) {
+                // k slots 0..7 of lane group g: the low nibbles of bytes 0, 2, 1, 3 of dword g,
+                // then the high nibbles in the same order (the activation is permuted to match)
+                const half8_t x8 = __builtin_bit_cast(half8_t, st.x[u][jj]);
+                const float4_t corr =
+                    __builtin_amdgcn_mfma_f32_16x16x32_f16(x8, neg24, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < TW; t++) {
+                    const uint32_t v = ww[t][jj];
+                    const uint4 wq = make_uint4(((v << 6) & 0x03c003c0u) | magic, ((v >> 2) & 0x03c003c0u) | magic,
+                                                ((v << 2) & 0x03c003c0u) | magic, ((v >> 6) & 0x03c003c0u) | magic);
+                    const float4_t r =
+                        __builtin_amdgcn_mfma_f32_16x16x32_f16(x8, __builtin_bit_cast(half8_t, wq), corr, 0, 0, 0);
+                    const uint32_t dw = jj < 2 ? st.d[u][t].x : st.d[u][t].y;
+                    const float ds = valid ? h2f((uint16_t)(jj & 1 ? dw >> 16 : dw & 0xffffu)) : 0.0f;
 #pragma unroll
                     for (int i = 0; i < 4; i++) acc[t][i] = fmaf(ds, r[i], acc[t][i]);
                 }
