@@ -501,19 +501,23 @@ struct Q4BSet {
 
 // Groups of 4 blocks: lane (g, c) loads block 4j+g of weight row c whole (16 bytes; the
 // 4 g-lanes of a row read 64 contiguous bytes) and the 4 scales of row c's group (8
-// bytes).  A 4x4 dword transpose through the wave's LDS slot then gives lane (g, c)
-// dword g of each of the group's 4 blocks, the operand the matrix core wants.
-template <int UG, int TW>
+// bytes; with SP the 8 scales of the stage's two groups in one 16-byte load).  A 4x4
+// dword transpose through the wave's LDS slot then gives lane (g, c) dword g of each of
+// the group's 4 blocks, the operand the matrix core wants.
+template <int UG, int TW, bool SP>
 struct Q4XStage {
     uint4 w[UG][TW];   // block 4j+g of row c of each tile
-    uint2 d[UG][TW];   // fp16 scales of row c, blocks 4j..4j+3, of each tile
+    uint2 d[UG][TW];   // fp16 scales of row c, blocks 4j..4j+3, of each tile (without SP)
+    uint4 dp[TW];      // fp16 scales of row c, blocks 4jp..4jp+7 (with SP)
     uint4 x[UG][4];    // activation row c, blocks 4j..4j+3, slot g (shared by the tiles)
 };
 
 // TW 16-row tiles per wave share each activation load; k is split over KS waves.  A
 // matrix's tiles never straddle into the next matrix (n[i] % (16*TW) == 0 but for the
-// last).
-template <int KS, int UG, int TW>
+// last).  SP (two groups per stage, at least two groups per row) loads the scales of a
+// stage's groups j0, j0+1 together from group jp = min(j0, ng - 2), which stays inside
+// the row.
+template <int KS, int UG, int TW, bool SP>
 __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, const uint4 *__restrict__ xp, int nb,
                                                               int m) {
     __shared__ float s_acc[KS][TW][64][4];
@@ -545,14 +549,20 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, co
     const uint32_t m24 = 0xCE00CE00u;  // fp16 -24, -24
     const half8_t neg24 = __builtin_bit_cast(half8_t, make_uint4(m24, m24, m24, m24));
 
-    auto load = [&](Q4XStage<UG, TW> &st, int j0) {
+    static_assert(!SP || UG == 2, "scale pairs cover the two groups of a stage");
+    auto load = [&](Q4XStage<UG, TW, SP> &st, int j0) {
+        if constexpr (SP) {
+            const int jp = min(j0, ng - 2);
+#pragma unroll
+            for (int t = 0; t < TW; t++) st.dp[t] = ldg_u4(wd + (wrow[t] + 4 * jp) * 2);
+        }
 #pragma unroll
         for (int u = 0; u < UG; u++) {
             const int j = min(j0 + u, j_hi - 1);
 #pragma unroll
             for (int t = 0; t < TW; t++) {
                 st.w[u][t] = ldg_u4(qs + (wrow[t] + 4 * j + g) * 16);
-                st.d[u][t] = ldg_u2(wd + (wrow[t] + 4 * j) * 2);
+                if constexpr (!SP) st.d[u][t] = ldg_u2(wd + (wrow[t] + 4 * j) * 2);
             }
 #pragma unroll
             for (int jj = 0; jj < 4; jj++) st.x[u][jj] = xrow[(size_t)(4 * j + jj) * 4];
@@ -561,10 +571,12 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, co
     float4_t acc[TW];
 #pragma unroll
     for (int t = 0; t < TW; t++) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
-    auto compute = [&](const Q4XStage<UG, TW> &st, int j0) {
+    auto compute = [&](const Q4XStage<UG, TW, SP> &st, int j0) {
+        const int jp = min(j0, ng - 2);
 #pragma unroll
         for (int u = 0; u < UG; u++) {
             const bool valid = j0 + u < j_hi;
+            const bool hi_half = SP && j0 + u - jp >= 1;  // group j0+u is the pair's second
             uint32_t ww[TW][4];
 #pragma unroll
             for (int t = 0; t < TW; t++) {
@@ -599,7 +611,12 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, co
                                                 ((v << 2) & 0x03c003c0u) | magic, ((v >> 6) & 0x03c003c0u) | magic);
                     const float4_t r =
                         __builtin_amdgcn_mfma_f32_16x16x32_f16(x8, __builtin_bit_cast(half8_t, wq), corr, 0, 0, 0);
-                    const uint32_t dw = jj < 2 ? st.d[u][t].x : st.d[u][t].y;
+                    uint2 d2;
+                    if constexpr (SP)
+                        d2 = hi_half ? make_uint2(st.dp[t].z, st.dp[t].w) : make_uint2(st.dp[t].x, st.dp[t].y);
+                    else
+                        d2 = st.d[u][t];
+                    const uint32_t dw = jj < 2 ? d2.x : d2.y;
                     const float ds = valid ? h2f((uint16_t)(jj & 1 ? dw >> 16 : dw & 0xffffu)) : 0.0f;
 #pragma unroll
                     for (int i = 0; i < 4; i++) acc[t][i] = fmaf(ds, r[i], acc[t][i]);
@@ -611,7 +628,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, co
         // two register stages; the prefetches are unconditional (clamped: past the end they
         // re-read the last group, a cache hit, and its scales are zeroed), since a load
         // under a branch makes the compiler wait for every load at the join
-        Q4XStage<UG, TW> sa, sb;
+        Q4XStage<UG, TW, SP> sa, sb;
         load(sa, j_lo);
         for (int j0 = j_lo; j0 < j_hi; j0 += 2 * UG) {
             load(sb, j0 + UG);
@@ -1373,6 +1390,7 @@ int launch_mfma_set(hipStream_t st, int count, const uint8_t *const *base, const
     for (int i = 0; i + 1 < count; i++)
         if (n[i] % (16 * tw)) tw = 1;  // a tile must not straddle two matrices
     const int ks = ks_env == 2 || ks_env == 4 || ks_env == 8 || ks_env == 16 ? ks_env : 4;
+    const bool sp = nb / 4 >= 2;  // scale pairs need two groups per row
     Q4BSet S;
     int wgs = 0;
     for (int i = 0; i < 4; i++) {
@@ -1396,15 +1414,21 @@ int launch_mfma_set(hipStream_t st, int count, const uint8_t *const *base, const
             S.wg_end[i] = INT_MAX;
         }
     }
-#define MI_MX(KS, TW)                                                                                          \
-    hipLaunchKernelGGL((k_gemv_q4_0_mfma_x<KS, 2, TW>), dim3((unsigned)wgs), dim3(64 * KS), 0, st, S,            \
+#define MI_MX(KS, TW, SPV)                                                                                      \
+    hipLaunchKernelGGL((k_gemv_q4_0_mfma_x<KS, 2, TW, SPV>), dim3((unsigned)wgs), dim3(64 * KS), 0, st, S,        \
                        (const uint4 *)ws, nb, (int)m)
-#define MI_MX_KS(KS) \
-    if (ks == KS) {  \
-        if (tw == 2) MI_MX(KS, 2); else MI_MX(KS, 1); \
+#define MI_MX_TW(KS, TW)              \
+    {                                 \
+        if (sp) MI_MX(KS, TW, true);  \
+        else MI_MX(KS, TW, false);    \
+    }
+#define MI_MX_KS(KS)                               \
+    if (ks == KS) {                                \
+        if (tw == 2) MI_MX_TW(KS, 2) else MI_MX_TW(KS, 1) \
     }
     MI_MX_KS(2) else MI_MX_KS(4) else MI_MX_KS(8) else MI_MX_KS(16)
 #undef MI_MX_KS
+#undef MI_MX_TW
 #undef MI_MX
     MI_CHECK_LAUNCH("k_gemv_q4_0_mfma_x");
     return MI_OK;
