@@ -1382,11 +1382,11 @@ int launch_mfma_set(hipStream_t st, int count, const uint8_t *const *base, const
         const char *e = getenv("MI_Q4_MFMA_KS");
         return e ? atoi(e) : 0;
     }();
-    // two tiles per wave for the tall matrices (gate / up), where the shared activation
-    // load pays; a set uses one tile width, so it takes two only if every matrix is tall
-    bool tall = true;
-    for (int i = 0; i < count; i++) tall = tall && n[i] >= 8192;
-    int tw = tw_env == 1 || tw_env == 2 ? tw_env : (tall ? 2 : 1);
+    // two tiles per wave when the set has at least 4096 rows (gate / up, q/k/v), where the
+    // shared activation load pays; below that, one tile keeps enough workgroups
+    int64_t rows = 0;
+    for (int i = 0; i < count; i++) rows += n[i];
+    int tw = tw_env == 1 || tw_env == 2 ? tw_env : (rows >= 4096 ? 2 : 1);
     for (int i = 0; i + 1 < count; i++)
         if (n[i] % (16 * tw)) tw = 1;  // a tile must not straddle two matrices
     const int ks = ks_env == 2 || ks_env == 4 || ks_env == 8 || ks_env == 16 ? ks_env : 4;
