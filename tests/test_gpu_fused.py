@@ -492,12 +492,15 @@ def _q4_ref(orc, w, x, n, k):
 
 
 # (rows per matrix, k, activation rows, epilogue): q/k/v + bias, gate/up, down + residual
-# after the GLU, o + residual, ragged last matrix
+# after the GLU, o + residual, ragged last matrix, one 4-block group per row (k = 128:
+# per-group scale loads), a 4096+-row set whose first matrix is not a whole number of
+# 32-row tile pairs (one tile per wave)
 @pytest.mark.parametrize("ns,k,m,mode", [((3584, 512, 512), 3584, 8, "bias"), ((18944, 18944), 3584, 5, "none"),
                                          ((3584,), 18944, 8, "glu_add"), ((3584,), 3584, 16, "add"),
                                          ((96, 40), 256, 3, "bias"), ((1536,), 8960, 2, "glu"),
                                          ((3584, 512, 512), 3584, 8, "norm_bias"), ((18944, 18944), 3584, 8, "norm"),
-                                         ((256,), 4096, 3, "norm")])
+                                         ((256,), 4096, 3, "norm"), ((48, 40), 128, 4, "bias"),
+                                         ((4080, 48), 256, 6, "bias"), ((4096,), 128, 2, "add")])
 def test_q4_batch_set(gpu, orc, ns, k, m, mode):
     """Several activation rows through up to four Q4_0 matrices in one launch: bit-identical
     to one mi_mul_mat_q4_0_f32 launch per matrix followed by the ADD (the graph's node-by-node

@@ -155,7 +155,8 @@ def test_q8_0_gemv_shapes(gpu, orc, n, k, m):
 @pytest.mark.parametrize("n,k,m", [(1536, 8960, 1), (8960, 1536, 1), (7, 32, 1), (512, 3584, 8), (100, 18944, 1),
                                    (4608, 3584, 1), (2049, 256, 1), (300, 18944, 8), (3584, 4096, 5),
                                    (1030, 3584, 16), (77, 160, 2), (5, 16384, 1), (33, 8192, 1),
-                                   (9, 32000, 1), (9, 32768, 1), (50, 33792, 1), (3, 64, 1)])
+                                   (9, 32000, 1), (9, 32768, 1), (50, 33792, 1), (3, 64, 1), (64, 128, 4),
+                                   (4100, 128, 3)])
 def test_w4a16_gemv(gpu, orc, n, k, m):
     """one activation row: the register-resident kernel for k <= 32768 (every blocks-per-
     lane / waves-per-row shape; odd n leaves the last row pair half empty), beyond that the
