@@ -235,7 +235,8 @@ int mi_cast_f32_f16(void *stream, const float *x, uint16_t *y, int64_t n);
  * F16 GEMV (replaces cast + aclnnMatmul(FRACTAL_NZ) + cast, patch:1286-1309,
  * used for the tied output head).  w : fp16 rows, row stride ldw elements
  * (>= k, multiple of 8); x : fp32 [m][k], rounded to fp16 like ggml's
- * vec_dot_type conversion; y : fp32 [m][n]; fp32 accumulation.
+ * vec_dot_type conversion; y : fp32 [m][n]; fp32 accumulation (on the matrix cores
+ * for m = 2..8 when k % 32 == 0 and m * (k + 8) * 2 <= 64 KiB).
  * ---------------------------------------------------------------------- */
 int mi_gemv_f16(void *stream, const uint16_t *w, int64_t ldw, const float *x, float *y, int64_t n, int64_t k,
                 int64_t m);

@@ -9,9 +9,16 @@
 // tied-output NZ side copy of patch:1451-1464.
 #include "mi_common.h"
 
+#include <stdlib.h>
+
+#include <algorithm>
+
 namespace {
 
 using namespace mi;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
 
 template <int G, int U, int M>
 __global__ __launch_bounds__(256) void k_gemv_f16(const uint16_t *__restrict__ w, int64_t ldw,
@@ -79,6 +86,102 @@ __global__ __launch_bounds__(256) void k_gemv_f16(const uint16_t *__restrict__ w
     }
 }
 
+// Several activation rows (2..8) on the matrix cores: D[16 x rows][16 weight rows] +=
+// X[16 x 32 k] . W^T[32 k x 16 weight rows], one v_mfma_f32_16x16x32_f16 per 32-k step.
+// Lane (g, c) loads 16 bytes of weight row n0 + c at k 32s + 8g (a row's 4 lanes read 64
+// contiguous bytes) and the x fragment of row c at the same k from LDS; it receives x rows
+// 4g..4g+3 against weight row n0 + c.  The activation is staged once per workgroup as
+// fp16 (RNE, as ggml converts src1 to the F16 vec-dot type), rows padded by 16 bytes
+// (LDS banks); rows past m read row m - 1, whose products land in output rows that are
+// never stored.  Each wave owns whole 16-row tiles (all of k: no cross-wave reduction)
+// and walks them with a stride of the grid; two register stages of U steps each.
+template <int U>
+__global__ __launch_bounds__(256) void k_gemv_f16_mfma(const uint16_t *__restrict__ w, int64_t ldw,
+                                                       const float *__restrict__ x, float *__restrict__ y, int n,
+                                                       int k, int m, int n_tiles) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint16_t *s_x = (uint16_t *)smem;  // [m][k + 8] fp16
+    const int kp = k + 8;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int k4 = k / 4;
+    for (int i = tid; i < m * k4; i += 256) {
+        const int r = i / k4, f = i - r * k4;
+        const float4 v = ((const float4 *)x)[i];
+        *(uint2 *)(s_x + (size_t)r * kp + 4 * f) = make_uint2((uint32_t)f2h(v.x) | ((uint32_t)f2h(v.y) << 16),
+                                                              (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16));
+    }
+    __syncthreads();
+    const uint16_t *xs = s_x + (size_t)min(c, m - 1) * kp + 8 * g;
+    const int ns = k / 32;  // 32-k steps
+    for (int t = blockIdx.x * 4 + wave; t < n_tiles; t += gridDim.x * 4) {
+        const uint16_t *wr = w + (size_t)min(16 * t + c, n - 1) * ldw + 8 * g;
+        int4 wa[U], wb[U];
+        auto load = [&](int4 (&wv)[U], int s0) {
+#pragma unroll
+            for (int u = 0; u < U; u++) wv[u] = ld_stream16(wr + 32 * (size_t)min(s0 + u, ns - 1));
+        };
+        float4_t acc = {0.f, 0.f, 0.f, 0.f};
+        auto compute = [&](const int4 (&wv)[U], int s0) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                if (s0 + u < ns) {  // uniform
+                    const half8_t xf = __builtin_bit_cast(half8_t, *(const uint4 *)(xs + 32 * (s0 + u)));
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf, __builtin_bit_cast(half8_t, wv[u]), acc, 0, 0, 0);
+                }
+            }
+        };
+        // the prefetches are unconditional (clamped to the last step, a cache hit)
+        load(wa, 0);
+        for (int s0 = 0; s0 < ns; s0 += 2 * U) {
+            load(wb, s0 + U);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(wa, s0);
+            load(wa, s0 + 2 * U);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(wb, s0 + U);
+        }
+        const int col = 16 * t + c;
+        if (col < n) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (4 * g + i < m) y[(size_t)(4 * g + i) * n + col] = acc[i];
+        }
+    }
+}
+
+// workgroups of the matrix-core kernel resident at once for an LDS size
+int f16_mfma_resident(size_t smem) {
+    int per_cu = 0, cus = 0, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_gemv_f16_mfma<8>, 256, smem) !=
+            hipSuccess ||
+        per_cu < 1)
+        per_cu = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+    return per_cu * cus;
+}
+
+// the matrix-core kernel takes 2..8 rows when k is whole 32-k steps and the fp16 rows fit in LDS
+inline bool f16_mfma_ok(int64_t k, int64_t m) {
+    static const bool on = [] {
+        const char *e = getenv("MI_F16_MFMA");
+        return !(e && e[0] == '0');
+    }();
+    return on && m >= 2 && m <= 8 && k % 32 == 0 && (size_t)m * (k + 8) * 2 <= 64 * 1024;
+}
+
+int launch_f16_mfma(hipStream_t st, const uint16_t *w, int64_t ldw, const float *x, float *y, int64_t n, int64_t k,
+                    int64_t m) {
+    const size_t smem = (size_t)m * (k + 8) * 2;
+    const int n_tiles = (int)((n + 15) / 16);
+    const int grid = std::min((n_tiles + 3) / 4, f16_mfma_resident(smem));
+    hipLaunchKernelGGL((k_gemv_f16_mfma<8>), dim3((unsigned)grid), dim3(256), smem, st, w, ldw, x, y, (int)n, (int)k,
+                       (int)m, n_tiles);
+    MI_CHECK_LAUNCH("k_gemv_f16_mfma");
+    return MI_OK;
+}
+
 template <int G, int U, int M>
 int launch_gu(hipStream_t st, const uint16_t *w, int64_t ldw, const float *x, float *y, int64_t n, int64_t k,
               int64_t m) {
@@ -128,6 +231,7 @@ extern "C" int mi_gemv_f16(void *stream, const uint16_t *w, int64_t ldw, const f
     MI_CHECK_ARG(mi::aligned(w, 16) && mi::aligned(x, 16), "gemv_f16: w and x must be 16-byte aligned");
     MI_CHECK_ARG(n < (1ll << 31) && k < (1ll << 24), "gemv_f16: shape too large");
     hipStream_t st = (hipStream_t)stream;
+    if (f16_mfma_ok(k, m)) return launch_f16_mfma(st, w, ldw, x, y, n, k, m);
     if (m == 1) return launch_m<1>(st, w, ldw, x, y, n, k, m);
     if (m == 2) return launch_m<2>(st, w, ldw, x, y, n, k, m);
     if (m >= 3 && m <= 4) return launch_m<4>(st, w, ldw, x, y, n, k, m);

@@ -190,7 +190,11 @@ def test_w4a16_gemv(gpu, orc, n, k, m):
 
 # ---------------------------------------------------------------- F16
 
-@pytest.mark.parametrize("n,k,m,pad", [(151936, 1536, 1, 0), (1000, 1536, 2, 8), (33, 8960, 1, 0), (64, 72, 8, 0)])
+# m = 2..8 with k a multiple of 32 take the matrix-core kernel (ragged last 16-row tile,
+# padded rows, the 7B head's k); k = 72 and m = 1 the dot2 kernels
+@pytest.mark.parametrize("n,k,m,pad", [(151936, 1536, 1, 0), (1000, 1536, 2, 8), (33, 8960, 1, 0), (64, 72, 8, 0),
+                                       (20000, 3584, 8, 0), (4100, 256, 3, 0), (1031, 1536, 5, 8), (17, 4064, 2, 0),
+                                       (300, 2048, 8, 16)])
 def test_f16_gemv(gpu, orc, n, k, m, pad):
     mi = gpu
     rng = np.random.default_rng(n + k)
