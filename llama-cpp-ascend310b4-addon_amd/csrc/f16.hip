@@ -94,9 +94,13 @@ __global__ __launch_bounds__(256) void k_gemv_f16(const uint16_t *__restrict__ w
 // fp16 (RNE, as ggml converts src1 to the F16 vec-dot type), rows padded by 16 bytes
 // (LDS banks); rows past m read row m - 1, whose products land in output rows that are
 // never stored.  Each wave owns whole 16-row tiles (all of k: no cross-wave reduction)
-// and walks them with a stride of the grid; two register stages of U steps each.
-template <int U>
-__global__ __launch_bounds__(256) void k_gemv_f16_mfma(const uint16_t *__restrict__ w, int64_t ldw,
+// and walks them with a stride of the grid; two register stages of U steps each.  The
+// B-operand loads cover 16 rows x 64 bytes per instruction; the same bytes read as 4 rows
+// x 256 contiguous bytes measured 20% faster (a cross-lane exchange would be needed, and
+// its LDS does not fit beside the activation within 64 KB), while deeper stages, 8- or
+// 16-wave workgroups and fewer rows (less LDS, more residency) measured no faster.
+template <int U, int NW>
+__global__ __launch_bounds__(64 * NW) void k_gemv_f16_mfma(const uint16_t *__restrict__ w, int64_t ldw,
                                                        const float *__restrict__ x, float *__restrict__ y, int n,
                                                        int k, int m, int n_tiles) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -105,7 +109,7 @@ __global__ __launch_bounds__(256) void k_gemv_f16_mfma(const uint16_t *__restric
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int k4 = k / 4;
-    for (int i = tid; i < m * k4; i += 256) {
+    for (int i = tid; i < m * k4; i += 64 * NW) {
         const int r = i / k4, f = i - r * k4;
         const float4 v = ((const float4 *)x)[i];
         *(uint2 *)(s_x + (size_t)r * kp + 4 * f) = make_uint2((uint32_t)f2h(v.x) | ((uint32_t)f2h(v.y) << 16),
@@ -114,7 +118,7 @@ __global__ __launch_bounds__(256) void k_gemv_f16_mfma(const uint16_t *__restric
     __syncthreads();
     const uint16_t *xs = s_x + (size_t)min(c, m - 1) * kp + 8 * g;
     const int ns = k / 32;  // 32-k steps
-    for (int t = blockIdx.x * 4 + wave; t < n_tiles; t += gridDim.x * 4) {
+    for (int t = blockIdx.x * NW + wave; t < n_tiles; t += gridDim.x * NW) {
         const uint16_t *wr = w + (size_t)min(16 * t + c, n - 1) * ldw + 8 * g;
         int4 wa[U], wb[U];
         auto load = [&](int4 (&wv)[U], int s0) {
@@ -150,13 +154,11 @@ __global__ __launch_bounds__(256) void k_gemv_f16_mfma(const uint16_t *__restric
     }
 }
 
-// workgroups of the matrix-core kernel resident at once for an LDS size
-int f16_mfma_resident(size_t smem) {
+// workgroups of a kernel resident at once for a block size and LDS size
+int f16_resident(const void *fn, int threads, size_t smem) {
     int per_cu = 0, cus = 0, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_gemv_f16_mfma<8>, 256, smem) !=
-            hipSuccess ||
-        per_cu < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, smem) != hipSuccess || per_cu < 1)
         per_cu = 1;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
     return per_cu * cus;
@@ -175,9 +177,9 @@ int launch_f16_mfma(hipStream_t st, const uint16_t *w, int64_t ldw, const float 
                     int64_t m) {
     const size_t smem = (size_t)m * (k + 8) * 2;
     const int n_tiles = (int)((n + 15) / 16);
-    const int grid = std::min((n_tiles + 3) / 4, f16_mfma_resident(smem));
-    hipLaunchKernelGGL((k_gemv_f16_mfma<8>), dim3((unsigned)grid), dim3(256), smem, st, w, ldw, x, y, (int)n, (int)k,
-                       (int)m, n_tiles);
+    auto fn = k_gemv_f16_mfma<4, 4>;
+    const int grid = std::min((n_tiles + 3) / 4, f16_resident((const void *)fn, 256, smem));
+    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), smem, st, w, ldw, x, y, (int)n, (int)k, (int)m, n_tiles);
     MI_CHECK_LAUNCH("k_gemv_f16_mfma");
     return MI_OK;
 }
