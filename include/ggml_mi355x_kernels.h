@@ -157,6 +157,14 @@ int mi_mul_mat_q4_0_f32_batch(void *stream, int n_mats, const void *const *w_pac
                               float *const *y, const float *const *bias, const float *const *add, int64_t k,
                               int64_t m, const float *x, const float *up, const float *norm_w, float eps, void *ws,
                               size_t ws_bytes);
+/* The same projections from an activation already converted: xp holds the m rows as fp16,
+ * each 32-element block permuted as xp[row][block][g][8] = x[4g], x[4g+2], x[4g+1],
+ * x[4g+3], x[16+4g], x[18+4g], x[17+4g], x[19+4g] (g = 0..3), 16-byte aligned, as
+ * mi_fa_decode_batch_q4act writes the attention output.  No reference counterpart: the
+ * reference runs one row per projection (patch:1207). */
+int mi_mul_mat_q4_0_batch_xp(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
+                             float *const *y, const float *const *bias, const float *const *add, int64_t k,
+                             int64_t m, const void *xp);
 /* the attention-input chain of one token: [RMS_NORM -> MUL(norm_w)] -> q/k/v MUL_MATs
  * (w_packed[0..2], n[0..2] rows, k <= 4096) -> ADD bias[i] (or NULL) -> neox ROPE of q
  * and k (n_dims = head_dim, theta = pos[0] * freq_base^(-2i/head_dim), freq_scale,
@@ -274,6 +282,17 @@ int mi_fa_decode_batch(void *stream, const float *q, const void *k, const void *
                        size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out,
                        int64_t n_seq, size_t q_seq, size_t k_seq, size_t v_seq, size_t mask_seq, size_t out_seq,
                        void *ws, size_t ws_bytes);
+/* mi_fa_decode_batch whose output goes straight to the input of the next several-row
+ * W4A16 projection (mi_mul_mat_q4_0_batch_xp): sequence s's attention output row
+ * (n_q_heads * d values, head-major) is written to xp as fp16 (RNE, ggml's src1
+ * conversion) in that entry's permuted block layout; no fp32 output.  ws as for
+ * mi_fa_decode_batch (required here even for one split).  No reference counterpart
+ * (the reference decodes one sequence, patch:1957-1983). */
+int mi_fa_decode_batch_q4act(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
+                             const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                             size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, void *xp,
+                             int64_t n_seq, size_t q_seq, size_t k_seq, size_t v_seq, size_t mask_seq, void *ws,
+                             size_t ws_bytes);
 /* The split half of mi_fa_decode alone, for a consumer that merges the splits itself
  * (mi_mul_mat_q8_0_f32_lse): every split writes its record to ws and no combine runs.
  * Record of q head h, split s: floats ws[(h*S + s)*(d+4) + i], i < d: the unnormalised

@@ -698,12 +698,18 @@ __global__ __launch_bounds__(64 * NW) void k_fa_mfma(const float *__restrict__ q
 // of a 64-split chunk at once, so a chunk costs one round trip; the 8 groups then merge
 // through LDS.  w_s = 2^(m_s - M), 0 for a split with no position; out = sum w_s o_s /
 // sum w_s l_s, 0 when no split has a position.
-template <int D>
-__global__ __launch_bounds__(256) void k_fa_combine(const float *__restrict__ part, float *__restrict__ out,
+//
+// XP: the result goes out as the fp16 activation of a several-row W4A16 projection
+// (rounded RNE, as ggml converts src1), permuted within each 32-element block into the
+// nibble order of a weight dword: xp[seq][block][g][8] = x[4g], x[4g+2], x[4g+1], x[4g+3],
+// x[16+4g], x[18+4g], x[17+4g], x[19+4g] (out_seq is then the blocks per row).  The 32
+// dims of a workgroup are one whole block.
+template <int D, bool XP>
+__global__ __launch_bounds__(256) void k_fa_combine(const float *__restrict__ part, void *__restrict__ out_v,
                                                     int n_splits, size_t out_seq) {
     constexpr int PS = part_stride<D>();
     part += (size_t)blockIdx.z * gridDim.x * n_splits * PS;
-    out += (size_t)blockIdx.z * out_seq;
+    float *out = (float *)out_v + (XP ? 0 : (size_t)blockIdx.z * out_seq);
     __shared__ float s_m[8][32], s_l[8][32], s_a[8][32];
     const int h = blockIdx.x;
     const int d0 = blockIdx.y * 32;
@@ -753,7 +759,15 @@ __global__ __launch_bounds__(256) void k_fa_combine(const float *__restrict__ pa
                 aa = fmaf(s_a[g][tid], w, aa);
             }
         }
-        out[(size_t)h * D + d0 + tid] = ll == 0.0f ? 0.0f : aa / ll;
+        const float r = ll == 0.0f ? 0.0f : aa / ll;
+        if constexpr (XP) {
+            const int g = (tid & 15) >> 2, q = tid & 3;
+            const int j = (tid >> 4) * 4 + (q == 1 ? 2 : q == 2 ? 1 : q);
+            const size_t blk = ((size_t)h * D + d0) / 32;
+            ((uint16_t *)out_v)[(((size_t)blockIdx.z * out_seq + blk) * 4 + g) * 8 + j] = f2h(r);
+        } else {
+            out[(size_t)h * D + d0 + tid] = r;
+        }
     }
 }
 
@@ -792,16 +806,18 @@ struct FaArgs {
     unsigned *counters;
     FaSeq sq;
     bool partials_only;  // write every split's (o, m, l) record, no combine, out unused
+    uint16_t *xp;        // non-null: the combine writes the permuted fp16 activation here, out unused
+    int xp_nb;           // its 32-element blocks per sequence
 };
 
 template <int D, int GQ, bool MASK>
 int launch_split_m(hipStream_t st, const FaArgs &a, const FaPlan &p) {
     const dim3 grid((unsigned)p.n_splits, (unsigned)a.n_kv_heads, (unsigned)a.n_seq);
     const uint8_t *kb = (const uint8_t *)a.k, *vb = (const uint8_t *)a.v;
-    float *const out = a.partials_only ? nullptr : a.out;
+    float *const out = a.partials_only || a.xp ? nullptr : a.out;
     if (p.mfma) {
-        const bool merged =
-            !a.partials_only && p.n_splits <= kFusedMaxSplits && a.counters && mfma_merge_enabled();
+        const bool merged = !a.partials_only && !a.xp && p.n_splits <= kFusedMaxSplits && a.counters &&
+                            mfma_merge_enabled();
 #define MI_FA_NBW(NB)                                                                                          \
     hipLaunchKernelGGL((k_fa_mfma<D, GQ, MASK, NB>), grid, dim3(256), 0, st, a.q, kb, vb, a.mask, a.kv_len,      \
                        (int)a.n_kv, a.k_nb1, a.k_nb2, a.v_nb1, a.v_nb2, a.scale, p.chunk, p.n_splits, a.part, out,   \
@@ -818,7 +834,7 @@ int launch_split_m(hipStream_t st, const FaArgs &a, const FaPlan &p) {
         MI_CHECK_LAUNCH("k_fa_mfma");
         if (merged) return MI_OK;
     } else {
-        const bool fused = !a.partials_only && p.n_splits <= kFusedMaxSplits && fused_combine_enabled();
+        const bool fused = !a.partials_only && !a.xp && p.n_splits <= kFusedMaxSplits && fused_combine_enabled();
 #define MI_FA_KT(KT)                                                                                           \
     hipLaunchKernelGGL((k_fa_split<D, GQ, MASK, KT>), grid, dim3(256), 0, st, a.q, kb, vb, a.mask, a.kv_len,     \
                        (int)a.n_kv, a.k_nb1, a.k_nb2, a.v_nb1, a.v_nb2, a.scale, p.chunk, p.n_splits, a.part, out,   \
@@ -833,9 +849,14 @@ int launch_split_m(hipStream_t st, const FaArgs &a, const FaPlan &p) {
         MI_CHECK_LAUNCH("k_fa_split");
         if (fused) return MI_OK;
     }
-    if (p.n_splits > 1 && !a.partials_only) {
-        hipLaunchKernelGGL((k_fa_combine<D>), dim3((unsigned)(a.n_kv_heads * GQ), D / 32, (unsigned)a.n_seq),
-                           dim3(256), 0, st, a.part, a.out, p.n_splits, a.sq.out);
+    if ((p.n_splits > 1 || a.xp) && !a.partials_only) {
+        const dim3 cg((unsigned)(a.n_kv_heads * GQ), D / 32, (unsigned)a.n_seq);
+        if (a.xp)
+            hipLaunchKernelGGL((k_fa_combine<D, true>), cg, dim3(256), 0, st, a.part, (void *)a.xp, p.n_splits,
+                               (size_t)a.xp_nb);
+        else
+            hipLaunchKernelGGL((k_fa_combine<D, false>), cg, dim3(256), 0, st, a.part, (void *)a.out, p.n_splits,
+                               a.sq.out);
         MI_CHECK_LAUNCH("k_fa_combine");
     }
     return MI_OK;
@@ -907,8 +928,8 @@ static int fa_decode_run(void *stream, const float *q, const void *k, const void
                          const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
                          size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out,
                          int64_t n_seq, size_t q_seq, size_t k_seq, size_t v_seq, size_t mask_seq, size_t out_seq,
-                         void *ws, size_t ws_bytes, bool partials_only) {
-    MI_CHECK_ARG(q && k && v && (out || partials_only), "fa_decode: null pointer");
+                         void *ws, size_t ws_bytes, bool partials_only, uint16_t *xp = nullptr) {
+    MI_CHECK_ARG(q && k && v && (out || partials_only || xp), "fa_decode: null pointer");
     MI_CHECK_ARG(n_kv > 0 && n_kv < (1ll << 31) && n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0,
                  "fa_decode: bad heads/length n_kv=%lld nq=%lld nkv=%lld", (long long)n_kv, (long long)n_q_heads,
                  (long long)n_kv_heads);
@@ -920,7 +941,7 @@ static int fa_decode_run(void *stream, const float *q, const void *k, const void
                  "fa_decode: K/V base and strides must be 16-byte aligned");
     const FaPlan p = fa_plan(n_kv, n_kv_heads, d, n_q_heads / n_kv_heads, n_seq);
     const size_t need = mi_fa_decode_batch_workspace_size(n_kv, n_q_heads, n_kv_heads, d, n_seq);
-    if ((p.n_splits > 1 || partials_only) && (!ws || ws_bytes < need || !mi::aligned(ws, 256))) {
+    if ((p.n_splits > 1 || partials_only || xp) && (!ws || ws_bytes < need || !mi::aligned(ws, 256))) {
         mi::set_error("fa_decode: workspace %zu < %zu bytes (or not 256-byte aligned)", ws_bytes, need);
         return MI_ERR_WORKSPACE;
     }
@@ -947,6 +968,8 @@ static int fa_decode_run(void *stream, const float *q, const void *k, const void
     a.sq.mask = mask_seq;
     a.sq.out = out_seq;
     a.partials_only = partials_only;
+    a.xp = xp;
+    a.xp_nb = (int)(n_q_heads * d / 32);
     const int gq = (int)(n_q_heads / n_kv_heads);
     hipStream_t st = (hipStream_t)stream;
     if (d == 128) return launch_d<128>(st, gq, a, p);
@@ -960,6 +983,17 @@ int mi_fa_decode_batch(void *stream, const float *q, const void *k, const void *
                        void *ws, size_t ws_bytes) {
     return fa_decode_run(stream, q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1, k_nb2, v_nb1, v_nb2,
                          scale, out, n_seq, q_seq, k_seq, v_seq, mask_seq, out_seq, ws, ws_bytes, false);
+}
+
+int mi_fa_decode_batch_q4act(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
+                             const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                             size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, void *xp,
+                             int64_t n_seq, size_t q_seq, size_t k_seq, size_t v_seq, size_t mask_seq, void *ws,
+                             size_t ws_bytes) {
+    MI_CHECK_ARG(xp && mi::aligned(xp, 16), "fa_decode_batch_q4act: xp must be a 16-byte aligned pointer");
+    return fa_decode_run(stream, q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1, k_nb2, v_nb1, v_nb2,
+                         scale, nullptr, n_seq, q_seq, k_seq, v_seq, mask_seq, 0, ws, ws_bytes, false,
+                         (uint16_t *)xp);
 }
 
 int64_t mi_fa_decode_num_splits(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d) {

@@ -551,6 +551,8 @@ void run_fa(BackendCtx *ctx, ggml_tensor *node) {
 //                                                          mi_mul_mat_q8_0_f32_lse
 //   ubatch (Q4_0)   : [RMS_NORM, MUL(w)] MUL_MAT x1..4 [ADD bias each] or MUL_MAT
 //                     ADD(residual), and GLU swiglu, MUL_MAT, [ADD] -> mi_mul_mat_q4_0_f32_batch
+//   ubatch attn + o : FLASH_ATTN_EXT (n_seq rows), MUL_MAT (Q4_0), [ADD] -> mi_fa_decode_batch_q4act +
+//                                                          mi_mul_mat_q4_0_batch_xp
 //   rope + kv write : ROPE q, ROPE k, SET_ROWS k, SET_ROWS v -> mi_rope_kv_rows
 
 using Consumers = std::unordered_map<const ggml_tensor *, std::vector<const ggml_tensor *>>;
@@ -1084,6 +1086,42 @@ int try_fuse_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C
     return fuse_q4_batch_at(ctx, g, i, i, C, BatchNorm{});
 }
 
+// FLASH_ATTN_EXT (several sequences, one token each) whose output only feeds a Q4_0
+// projection of those rows [-> ADD bias or residual]: the attention's combine writes the
+// projection's permuted fp16 activation straight into the scratch (no attention-output
+// tensor, no conversion launch), then the matrix-core projection reads it.
+int try_fuse_fa_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    const ggml_tensor *fa = ggml_graph_node(g, i);
+    const ggml_tensor *q = fa->src[0], *k = fa->src[1], *v = fa->src[2], *mask = fa->src[3];
+    const ggml_tensor *kvl = fa->src[5];
+    const int64_t n_seq = q->ne[3], d = q->ne[0], n_head = q->ne[2];
+    if (n_seq < 2 || q->ne[1] != 1 || !ggml_is_contiguous(fa)) return 0;
+    const int j = next_real(g, i + 1);
+    if (j >= ggml_graph_n_nodes(g)) return 0;
+    const ggml_tensor *mm = ggml_graph_node(g, j);
+    if (!q4_batch_node(mm) || alias_root(mm->src[1]) != fa || !only_consumed_by(C, fa, {mm})) return 0;
+    const int64_t kk = mm->src[0]->ne[0], m = ggml_nrows(mm->src[1]);
+    if (kk != d * n_head || m != n_seq || (size_t)(m * kk * 2) > ctx->scratch_size) return 0;
+    const ggml_tensor *other = nullptr;
+    bool is_bias = false;
+    const ggml_tensor *ad = batch_add_tail(g, j, mm, C, other, is_bias);
+    float scale;
+    memcpy(&scale, fa->op_params, sizeof(float));
+    const size_t mask_seq = mask && mask->ne[3] > 1 ? mask->nb[3] / 2 : 0;
+    MI_K_CHECK(mi_fa_decode_batch_q4act(ctx->stream, (const float *)q->data, k->data, v->data,
+                                        mask ? (const uint16_t *)mask->data : nullptr,
+                                        kvl ? (const int32_t *)kvl->data : nullptr, k->ne[1], n_head, k->ne[2], d,
+                                        k->nb[1], k->nb[2], v->nb[1], v->nb[2], scale, ctx->scratch, n_seq,
+                                        q->nb[3] / 4, k->nb[3], v->nb[3], mask_seq, ctx->fa_ws, ctx->fa_ws_size));
+    const void *w = ((const TensorExtra *)mm->src[0]->extra)->packed;
+    const int64_t n = mm->src[0]->ne[1];
+    float *y = (float *)(ad ? ad->data : mm->data);
+    const float *bv = ad && is_bias ? (const float *)other->data : nullptr;
+    const float *av = ad && !is_bias ? (const float *)other->data : nullptr;
+    MI_K_CHECK(mi_mul_mat_q4_0_batch_xp(ctx->stream, 1, &w, &n, &y, &bv, &av, kk, m, ctx->scratch));
+    return (ad ? next_real(g, j + 1) : j) + 1 - i;
+}
+
 // RMS_NORM (2..16 rows, k <= 4096) -> MUL(norm_w row) -> the Q4_0 group of try_fuse_q4_batch
 int try_fuse_norm_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
     const int nn = ggml_graph_n_nodes(g);
@@ -1219,6 +1257,7 @@ int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
         }
         case GGML_OP_FLASH_ATTN_EXT:
             if (fuse) {
+                if (int used = try_fuse_fa_q4_batch(ctx, g, i, C)) return used;
                 if (int used = try_fuse_fa_o(ctx, g, i, C)) return used;
             }
             run_fa(ctx, node);

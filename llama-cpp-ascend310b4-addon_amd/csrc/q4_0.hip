@@ -397,6 +397,7 @@ __device__ __forceinline__ uint2 ldg_u2(uint64_t a) {
 constexpr int PERM_F16 = 0;   // fp16 rows
 constexpr int PERM_F32 = 1;   // fp32 rows, rounded to fp16 (RNE) as ggml converts src1
 constexpr int PERM_GLU = 2;   // fp32 gate and up rows: fp16(silu(g) * u), ggml swiglu then the conversion
+constexpr int PERM_READY = 3; // the activation arrives converted and permuted (no conversion launch)
 
 template <int MODE>
 __global__ __launch_bounds__(256) void k_perm_f16(const void *__restrict__ x, const float *__restrict__ up,
@@ -1364,7 +1365,9 @@ int launch_mfma_set(hipStream_t st, int count, const uint8_t *const *base, const
     const int nb = (int)(k / QK);
     const int64_t units = m * nb * 4;
     const dim3 pg((unsigned)((units + 255) / 256));
-    if (norm_w)
+    if (mode == PERM_READY)
+        ws = const_cast<void *>(x);
+    else if (norm_w)
         hipLaunchKernelGGL(k_perm_norm_f16, dim3((unsigned)m), dim3(256), 0, st, (const float *)x, norm_w, eps,
                            (uint4 *)ws, nb);
     else if (mode == PERM_F32)
@@ -1373,7 +1376,7 @@ int launch_mfma_set(hipStream_t st, int count, const uint8_t *const *base, const
         hipLaunchKernelGGL((k_perm_f16<PERM_GLU>), pg, dim3(256), 0, st, x, up, (uint4 *)ws, (int)m, nb);
     else
         hipLaunchKernelGGL((k_perm_f16<PERM_F16>), pg, dim3(256), 0, st, x, up, (uint4 *)ws, (int)m, nb);
-    MI_CHECK_LAUNCH("k_perm_f16");
+    if (mode != PERM_READY) MI_CHECK_LAUNCH("k_perm_f16");
     static const int tw_env = [] {
         const char *e = getenv("MI_Q4_MFMA_TW");
         return e ? atoi(e) : 0;
@@ -1604,6 +1607,28 @@ int mi_mul_mat_q4_0_f32_batch(void *stream, int n_mats, const void *const *w_pac
     }
     return launch_mfma_set((hipStream_t)stream, n_mats, base, n, y, bias, add, k, m, x, up ? PERM_GLU : PERM_F32, up,
                            ws, norm_w, eps);
+}
+
+int mi_mul_mat_q4_0_batch_xp(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
+                             float *const *y, const float *const *bias, const float *const *add, int64_t k,
+                             int64_t m, const void *xp) {
+    MI_CHECK_ARG(n_mats >= 1 && n_mats <= 4, "mul_mat_q4_0_batch_xp: %d matrices (1..4)", n_mats);
+    MI_CHECK_ARG(w_packed && n && y && xp, "mul_mat_q4_0_batch_xp: null pointer");
+    MI_CHECK_ARG(m >= 1 && m <= 16, "mul_mat_q4_0_batch_xp: m=%lld not in 1..16", (long long)m);
+    MI_CHECK_ARG(k % (4 * QK) == 0, "mul_mat_q4_0_batch_xp: k=%lld not a multiple of 128", (long long)k);
+    MI_CHECK_ARG(mi::aligned(xp, 16), "mul_mat_q4_0_batch_xp: xp not 16-byte aligned");
+    int64_t rows = 0;
+    const uint8_t *base[4];
+    for (int i = 0; i < n_mats; i++) {
+        if (int r = check_shape("mul_mat_q4_0_batch_xp", n[i], k)) return r;
+        MI_CHECK_ARG(w_packed[i] && y[i], "mul_mat_q4_0_batch_xp: matrix %d: null pointer", i);
+        MI_CHECK_ARG(mi::aligned(w_packed[i], 256), "mul_mat_q4_0_batch_xp: packed weight %d not 256-byte aligned", i);
+        base[i] = (const uint8_t *)w_packed[i];
+        rows += n[i];
+    }
+    MI_CHECK_ARG(rows < (1ll << 31), "mul_mat_q4_0_batch_xp: too many rows");
+    return launch_mfma_set((hipStream_t)stream, n_mats, base, n, y, bias, add, k, m, xp, PERM_READY, nullptr,
+                           nullptr);
 }
 
 int mi_mul_mat_q4_0_f32_fused(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,

@@ -704,3 +704,61 @@ def test_q4_qkv_rope_kv_skips_out_of_range_row(gpu):
              mi._P(vc.ptr), 256, mi._P(didx.ptr), 0, 8, None)
     mi.device_sync()
     assert not kc.download(np.uint16).any() and not vc.download(np.uint16).any()
+
+
+# (sequences, KV length, q heads, kv heads, head dim): the 7B shape with several splits and
+# with one, and the 1.5B head group
+@pytest.mark.parametrize("n_seq,L,nq,nkv,d", [(8, 3000, 28, 4, 128), (3, 40, 28, 4, 128), (2, 700, 12, 2, 128),
+                                              (4, 300, 8, 2, 64)])
+def test_fa_q4act_into_batch_projection(gpu, n_seq, L, nq, nkv, d):
+    """Attention of several sequences written straight into the o projection's permuted fp16
+    activation, then the matrix-core projection with its residual, is bit-identical to the
+    fp32 attention output followed by the projection that converts it (the node-by-node
+    ubatch path); the attention itself is pinned against the oracle by the flash-decoding
+    tests."""
+    mi = gpu
+    P = mi._P
+    rng = np.random.default_rng(n_seq * L + nq)
+    q = rng.standard_normal((n_seq, nq, d)).astype(F32)
+    kc = f16_bits(rng.standard_normal((n_seq, L, nkv, d)))
+    vc = f16_bits(rng.standard_normal((n_seq, L, nkv, d)))
+    lens = rng.integers(1, L + 1, n_seq).astype(np.int32)
+    dq, dk, dv, dl = mi.to_device(q), mi.to_device(kc), mi.to_device(vc), mi.to_device(lens)
+    k_in, n_out = nq * d, 3584
+    w = q4_0_weights(rng, n_out, k_in)
+    pw = _packed_q4(mi, w, n_out, k_in)
+    res = rng.standard_normal((n_seq, n_out)).astype(F32)
+    dres = mi.to_device(res)
+    wsb = mi.fa_decode_batch_workspace_size(L, nq, nkv, d, n_seq)
+    ws = mi.DeviceBuffer(wsb).zero()
+    nb1 = nkv * d * 2
+    seq_bytes = L * nb1
+    scale = F32(1 / np.sqrt(d))
+    # node by node: fp32 attention output, then the projection converting it
+    out = mi.DeviceBuffer(n_seq * k_in * 4)
+    mi.fa_decode_batch(dq.ptr, dk.ptr, dv.ptr, None, dl.ptr, L, nq, nkv, d, nb1, d * 2, nb1, d * 2, scale, out.ptr,
+                       n_seq, nq * d, seq_bytes, seq_bytes, 0, nq * d, ws.ptr, wsb)
+    y1 = mi.DeviceBuffer(4 * n_seq * n_out)
+    pws = mi.DeviceBuffer(n_seq * k_in * 2)
+    mi._call("mi_mul_mat_q4_0_f32_batch", None, 1, _ptrs(pw), _i64s(n_out), _ptrs(y1), None, _ptrs(dres), k_in,
+             n_seq, P(out.ptr), None, None, F32(1e-6), P(pws.ptr), n_seq * k_in * 2)
+    # fused: the combine writes the permuted activation
+    xp = mi.DeviceBuffer(n_seq * k_in * 2)
+    mi._call("mi_fa_decode_batch_q4act", None, P(dq.ptr), P(dk.ptr), P(dv.ptr), None, P(dl.ptr), L, nq, nkv, d, nb1,
+             d * 2, nb1, d * 2, scale, P(xp.ptr), n_seq, nq * d, seq_bytes, seq_bytes, 0, P(ws.ptr), wsb)
+    y2 = mi.DeviceBuffer(4 * n_seq * n_out)
+    mi._call("mi_mul_mat_q4_0_batch_xp", None, 1, _ptrs(pw), _i64s(n_out), _ptrs(y2), None, _ptrs(dres), k_in, n_seq,
+             P(xp.ptr))
+    mi.device_sync()
+    assert np.array_equal(xp.download(np.uint16), pws.download(np.uint16))
+    assert np.array_equal(y1.download(F32), y2.download(F32))
+
+
+def test_q4act_entry_points_reject_bad_arguments(gpu):
+    mi = gpu
+    P = mi._P
+    with pytest.raises(RuntimeError):
+        mi._call("mi_mul_mat_q4_0_batch_xp", None, 1, None, None, None, None, None, 128, 2, None)
+    with pytest.raises(RuntimeError):
+        mi._call("mi_fa_decode_batch_q4act", None, None, None, None, None, None, 64, 2, 1, 64, 128, 128, 128, 128,
+                 F32(0.1), None, 2, 128, 0, 0, 0, None, 0)
