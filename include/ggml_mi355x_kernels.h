@@ -165,6 +165,16 @@ int mi_mul_mat_q4_0_f32_batch(void *stream, int n_mats, const void *const *w_pac
 int mi_mul_mat_q4_0_batch_xp(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
                              float *const *y, const float *const *bias, const float *const *add, int64_t k,
                              int64_t m, const void *xp);
+/* [RMS_NORM -> MUL(norm_w)] -> gate and up MUL_MATs (Q4_0, n x k each) -> GLU swiglu for
+ * m activation rows (1..16) in two launches: hxp gets fp16(silu(gate) * up) as the down
+ * projection's activation in mi_mul_mat_q4_0_batch_xp's permuted layout (m * n * 2 bytes,
+ * 16-byte aligned), bit-identical to mi_mul_mat_q4_0_f32_batch of the gate/up pair followed
+ * by that call's GLU conversion.  k % 128 == 0, n % 128 == 0; ws: m * k * 2 bytes, not
+ * overlapping hxp.  No reference counterpart: the reference runs one row per matmul and
+ * the SwiGLU node apart (patch:1207). */
+int mi_mul_mat_q4_0_gate_up_glu_batch(void *stream, const void *w_gate, const void *w_up, int64_t n, int64_t k,
+                                      int64_t m, const float *x, const float *norm_w, float eps, void *ws,
+                                      size_t ws_bytes, void *hxp);
 /* the attention-input chain of one token: [RMS_NORM -> MUL(norm_w)] -> q/k/v MUL_MATs
  * (w_packed[0..2], n[0..2] rows, k <= 4096) -> ADD bias[i] (or NULL) -> neox ROPE of q
  * and k (n_dims = head_dim, theta = pos[0] * freq_base^(-2i/head_dim), freq_scale,

@@ -553,6 +553,8 @@ void run_fa(BackendCtx *ctx, ggml_tensor *node) {
 //                     ADD(residual), and GLU swiglu, MUL_MAT, [ADD] -> mi_mul_mat_q4_0_f32_batch
 //   ubatch attn + o : FLASH_ATTN_EXT (n_seq rows), MUL_MAT (Q4_0), [ADD] -> mi_fa_decode_batch_q4act +
 //                                                          mi_mul_mat_q4_0_batch_xp
+//   ubatch FFN      : [RMS_NORM, MUL(w)] MUL_MAT gate, MUL_MAT up, GLU swiglu, MUL_MAT down,
+//                     [ADD] -> mi_mul_mat_q4_0_gate_up_glu_batch + mi_mul_mat_q4_0_batch_xp
 //   rope + kv write : ROPE q, ROPE k, SET_ROWS k, SET_ROWS v -> mi_rope_kv_rows
 
 using Consumers = std::unordered_map<const ggml_tensor *, std::vector<const ggml_tensor *>>;
@@ -1029,6 +1031,45 @@ struct BatchNorm {
     float eps = 0.0f;
 };
 
+// gate, up (the group just matched) -> GLU swiglu -> down MUL_MAT [-> ADD]: gate and up
+// form the swiglu in their epilogue, written as the down projection's permuted fp16
+// activation (no gate/up outputs, no GLU tensor, no conversion launch)
+int fuse_q4_glu_pair(BackendCtx *ctx, ggml_cgraph *g, int i, int last, const Consumers &C,
+                     const ggml_tensor *const *mm, const float *x, const BatchNorm &norm, int64_t k, int64_t m) {
+    const int nn = ggml_graph_n_nodes(g);
+    const int64_t n = mm[0]->src[0]->ne[1];
+    if (mm[1]->src[0]->ne[1] != n || n % 128) return 0;
+    const int jg = next_real(g, last + 1);
+    if (jg >= nn) return 0;
+    const ggml_tensor *glu = ggml_graph_node(g, jg);
+    if (glu->op != GGML_OP_GLU || !supports_op_impl(glu) || glu->src[0] != mm[0] || glu->src[1] != mm[1] ||
+        !only_consumed_by(C, mm[0], {glu}) || !only_consumed_by(C, mm[1], {glu}))
+        return 0;
+    const int jd = next_real(g, jg + 1);
+    if (jd >= nn) return 0;
+    const ggml_tensor *down = ggml_graph_node(g, jd);
+    if (!q4_batch_node(down) || down->src[1] != glu || !only_consumed_by(C, glu, {down}) ||
+        down->src[0]->ne[0] != n)
+        return 0;
+    const size_t need_in = ((size_t)(m * k * 2) + 255) / 256 * 256, need_h = (size_t)(m * n * 2);
+    if (need_in + need_h > ctx->scratch_size) return 0;
+    const ggml_tensor *other = nullptr;
+    bool is_bias = false;
+    const ggml_tensor *ad = batch_add_tail(g, jd, down, C, other, is_bias);
+    uint8_t *hxp = (uint8_t *)ctx->scratch + need_in;
+    MI_K_CHECK(mi_mul_mat_q4_0_gate_up_glu_batch(ctx->stream, ((const TensorExtra *)mm[0]->src[0]->extra)->packed,
+                                                 ((const TensorExtra *)mm[1]->src[0]->extra)->packed, n, k, m, x,
+                                                 norm.w ? (const float *)norm.w->data : nullptr, norm.eps,
+                                                 ctx->scratch, need_in, hxp));
+    const void *w = ((const TensorExtra *)down->src[0]->extra)->packed;
+    const int64_t nd = down->src[0]->ne[1];
+    float *y = (float *)(ad ? ad->data : down->data);
+    const float *bv = ad && is_bias ? (const float *)other->data : nullptr;
+    const float *av = ad && !is_bias ? (const float *)other->data : nullptr;
+    MI_K_CHECK(mi_mul_mat_q4_0_batch_xp(ctx->stream, 1, &w, &nd, &y, &bv, &av, n, m, hxp));
+    return (ad ? next_real(g, jd + 1) : jd) + 1 - i;
+}
+
 int fuse_q4_batch_at(BackendCtx *ctx, ggml_cgraph *g, int i, int i0, const Consumers &C, const BatchNorm &norm) {
     const int nn = ggml_graph_n_nodes(g);
     ggml_tensor *mm0 = ggml_graph_node(g, i0);
@@ -1076,6 +1117,9 @@ int fuse_q4_batch_at(BackendCtx *ctx, ggml_cgraph *g, int i, int i0, const Consu
     }
     const int64_t k = mm0->src[0]->ne[0], m = ggml_nrows(mm0->src[1]);
     const float *x = (const float *)(norm.w ? norm.x->data : mm0->src[1]->data);
+    if (cnt == 2 && !all_add) {
+        if (int used = fuse_q4_glu_pair(ctx, g, i, last, C, mm, x, norm, k, m)) return used;
+    }
     MI_K_CHECK(mi_mul_mat_q4_0_f32_batch(ctx->stream, cnt, w, n, y, bv, av, k, m, x, nullptr,
                                          norm.w ? (const float *)norm.w->data : nullptr, norm.eps, ctx->scratch,
                                          ctx->scratch_size));

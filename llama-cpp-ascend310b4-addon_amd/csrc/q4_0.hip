@@ -493,6 +493,7 @@ struct Q4BSet {
     const float *add[4];
     int n[4];
     int wg_end[4];  // cumulative workgroup counts; unused slots INT_MAX
+    uint16_t *hxp;  // GLU pairs: the swiglu rows as the next projection's permuted fp16 activation
 };
 
 // selected once per workgroup: a register select (see opaque_s), not a kernel-argument
@@ -517,8 +518,11 @@ struct Q4XStage {
 // matrix's tiles never straddle into the next matrix (n[i] % (16*TW) == 0 but for the
 // last).  SP (two groups per stage, at least two groups per row) loads the scales of a
 // stage's groups j0, j0+1 together from group jp = min(j0, ng - 2), which stays inside
-// the row.
-template <int KS, int UG, int TW, bool SP>
+// the row.  GLU (TW = 2, matrices 0 and 1 of n rows each: gate and up): a workgroup's
+// tile 0 is gate rows 16b.., tile 1 the same up rows, and the epilogue writes
+// fp16(silu(gate) * up), ggml's swiglu then the src1 conversion, into S.hxp in the
+// permuted block layout of the activation (the next projection's input, k = n).
+template <int KS, int UG, int TW, bool SP, bool GLU = false>
 __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, const uint4 *__restrict__ xp, int nb,
                                                               int m) {
     __shared__ float s_acc[KS][TW][64][4];
@@ -527,18 +531,23 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, co
     const int lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int b = blockIdx.x;
-    const int mi = (b >= S.wg_end[0]) + (b >= S.wg_end[1]) + (b >= S.wg_end[2]);
-    const int wg0 = pick4(mi, 0, opaque_s(S.wg_end[0]), opaque_s(S.wg_end[1]), opaque_s(S.wg_end[2]));
+    static_assert(!GLU || TW == 2, "a GLU pair is one gate tile and one up tile");
+    const int mi = GLU ? 0 : (b >= S.wg_end[0]) + (b >= S.wg_end[1]) + (b >= S.wg_end[2]);
+    const int wg0 = GLU ? 0 : pick4(mi, 0, opaque_s(S.wg_end[0]), opaque_s(S.wg_end[1]), opaque_s(S.wg_end[2]));
     const int n = Q4B_PICK(S, n, mi);
-    const uint64_t qs = (uint64_t)Q4B_PICK(S, qs, mi);
-    const uint64_t wd = (uint64_t)Q4B_PICK(S, wd, mi);
-    const int row0 = (b - wg0) * 16 * TW;
+    uint64_t qsb[TW], wdb[TW];  // each tile's matrix (the same one but for GLU pairs)
+#pragma unroll
+    for (int t = 0; t < TW; t++) {
+        qsb[t] = (uint64_t)(GLU ? S.qs[t] : Q4B_PICK(S, qs, mi));
+        wdb[t] = (uint64_t)(GLU ? S.wd[t] : Q4B_PICK(S, wd, mi));
+    }
+    const int row0 = GLU ? b * 16 : (b - wg0) * 16 * TW;
     const int ng = nb / 4;               // whole groups (nb % 4 == 0)
     const int per = (ng + KS - 1) / KS;  // groups of this wave
     const int j_lo = wave * per, j_hi = min(ng, j_lo + per);
     uint64_t wrow[TW];
 #pragma unroll
-    for (int t = 0; t < TW; t++) wrow[t] = (uint64_t)min(row0 + 16 * t + c, n - 1) * nb;
+    for (int t = 0; t < TW; t++) wrow[t] = (uint64_t)min(row0 + (GLU ? 0 : 16 * t) + c, n - 1) * nb;
     // activation rows past m (lanes c >= m) re-read row m - 1: their products land only in
     // output rows >= m, which are never stored
     const uint4 *xrow = xp + (size_t)min(c, m - 1) * nb * 4 + g;
@@ -555,15 +564,15 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, co
         if constexpr (SP) {
             const int jp = min(j0, ng - 2);
 #pragma unroll
-            for (int t = 0; t < TW; t++) st.dp[t] = ldg_u4(wd + (wrow[t] + 4 * jp) * 2);
+            for (int t = 0; t < TW; t++) st.dp[t] = ldg_u4(wdb[t] + (wrow[t] + 4 * jp) * 2);
         }
 #pragma unroll
         for (int u = 0; u < UG; u++) {
             const int j = min(j0 + u, j_hi - 1);
 #pragma unroll
             for (int t = 0; t < TW; t++) {
-                st.w[u][t] = ldg_u4(qs + (wrow[t] + 4 * j + g) * 16);
-                if constexpr (!SP) st.d[u][t] = ldg_u2(wd + (wrow[t] + 4 * j) * 2);
+                st.w[u][t] = ldg_u4(qsb[t] + (wrow[t] + 4 * j + g) * 16);
+                if constexpr (!SP) st.d[u][t] = ldg_u2(wdb[t] + (wrow[t] + 4 * j) * 2);
             }
 #pragma unroll
             for (int jj = 0; jj < 4; jj++) st.x[u][jj] = xrow[(size_t)(4 * j + jj) * 4];
@@ -646,6 +655,27 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, co
         for (int i = 0; i < 4; i++) s_acc[wave][t][lane][i] = acc[t][i];
     __syncthreads();
     if (wave != 0) return;
+    if constexpr (GLU) {
+        const int row = row0 + c;  // h index
+        if (row >= n) return;
+        const int p = row & 31, q = p & 3;
+        const int gp = (p & 15) >> 2, jp = (p >> 4) * 4 + (q == 1 ? 2 : q == 2 ? 1 : q);
+        const size_t nbd = (size_t)n / QK;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = 4 * g + i;
+            if (r < m) {
+                float gv = 0.0f, uv = 0.0f;
+#pragma unroll
+                for (int w = 0; w < KS; w++) {
+                    gv += s_acc[w][0][lane][i];
+                    uv += s_acc[w][1][lane][i];
+                }
+                S.hxp[(((size_t)r * nbd + row / QK) * 4 + gp) * 8 + jp] = f2h((gv / (1.0f + expf(-gv))) * uv);
+            }
+        }
+        return;
+    }
     const uint64_t y = (uint64_t)Q4B_PICK(S, y, mi);
     const uint64_t bias = (uint64_t)Q4B_PICK(S, bias, mi);
     const uint64_t add = (uint64_t)Q4B_PICK(S, add, mi);
@@ -1395,6 +1425,7 @@ int launch_mfma_set(hipStream_t st, int count, const uint8_t *const *base, const
     const int ks = ks_env == 2 || ks_env == 4 || ks_env == 8 || ks_env == 16 ? ks_env : 4;
     const bool sp = nb / 4 >= 2;  // scale pairs need two groups per row
     Q4BSet S;
+    S.hxp = nullptr;
     int wgs = 0;
     for (int i = 0; i < 4; i++) {
         if (i < count) {
@@ -1433,6 +1464,43 @@ int launch_mfma_set(hipStream_t st, int count, const uint8_t *const *base, const
 #undef MI_MX_KS
 #undef MI_MX_TW
 #undef MI_MX
+    MI_CHECK_LAUNCH("k_gemv_q4_0_mfma_x");
+    return MI_OK;
+}
+
+// Gate and up (n rows each) of m activation rows, optionally after RMSNorm * norm_w, with
+// the swiglu in the epilogue: hxp gets the down projection's permuted fp16 activation
+// (k = n).  The activation's own conversion goes to ws (m * k * 2 bytes).
+int launch_mfma_glu(hipStream_t st, const uint8_t *gate, const uint8_t *up, int64_t n, int64_t k, int64_t m,
+                    const float *x, const float *norm_w, float eps, void *ws, uint16_t *hxp) {
+    const int nb = (int)(k / QK);
+    if (norm_w)
+        hipLaunchKernelGGL(k_perm_norm_f16, dim3((unsigned)m), dim3(256), 0, st, x, norm_w, eps, (uint4 *)ws, nb);
+    else
+        hipLaunchKernelGGL((k_perm_f16<PERM_F32>), dim3((unsigned)((m * nb * 4 + 255) / 256)), dim3(256), 0, st,
+                           (const void *)x, nullptr, (uint4 *)ws, (int)m, nb);
+    MI_CHECK_LAUNCH("k_perm_f16");
+    Q4BSet S;
+    const Q4Planes p = q4_planes(n, k);
+    const uint8_t *base[2] = {gate, up};
+    for (int i = 0; i < 4; i++) {
+        const uint8_t *b = base[i < 2 ? i : 0];
+        S.qs[i] = b;
+        S.wd[i] = (const uint16_t *)(b + p.plane);
+        S.y[i] = nullptr;
+        S.bias[i] = nullptr;
+        S.add[i] = nullptr;
+        S.n[i] = (int)n;
+        S.wg_end[i] = INT_MAX;
+    }
+    S.hxp = hxp;
+    const dim3 grid((unsigned)((n + 15) / 16));
+    if (nb / 4 >= 2)
+        hipLaunchKernelGGL((k_gemv_q4_0_mfma_x<4, 2, 2, true, true>), grid, dim3(256), 0, st, S, (const uint4 *)ws, nb,
+                           (int)m);
+    else
+        hipLaunchKernelGGL((k_gemv_q4_0_mfma_x<4, 2, 2, false, true>), grid, dim3(256), 0, st, S, (const uint4 *)ws,
+                           nb, (int)m);
     MI_CHECK_LAUNCH("k_gemv_q4_0_mfma_x");
     return MI_OK;
 }
@@ -1629,6 +1697,31 @@ int mi_mul_mat_q4_0_batch_xp(void *stream, int n_mats, const void *const *w_pack
     MI_CHECK_ARG(rows < (1ll << 31), "mul_mat_q4_0_batch_xp: too many rows");
     return launch_mfma_set((hipStream_t)stream, n_mats, base, n, y, bias, add, k, m, xp, PERM_READY, nullptr,
                            nullptr);
+}
+
+int mi_mul_mat_q4_0_gate_up_glu_batch(void *stream, const void *w_gate, const void *w_up, int64_t n, int64_t k,
+                                      int64_t m, const float *x, const float *norm_w, float eps, void *ws,
+                                      size_t ws_bytes, void *hxp) {
+    MI_CHECK_ARG(w_gate && w_up && x && hxp, "mul_mat_q4_0_gate_up_glu_batch: null pointer");
+    if (int r = check_shape("mul_mat_q4_0_gate_up_glu_batch", n, k)) return r;
+    MI_CHECK_ARG(m >= 1 && m <= 16, "mul_mat_q4_0_gate_up_glu_batch: m=%lld not in 1..16", (long long)m);
+    MI_CHECK_ARG(k % (4 * QK) == 0 && n % (4 * QK) == 0,
+                 "mul_mat_q4_0_gate_up_glu_batch: k=%lld and n=%lld must be multiples of 128", (long long)k,
+                 (long long)n);
+    MI_CHECK_ARG(mi::aligned(w_gate, 256) && mi::aligned(w_up, 256),
+                 "mul_mat_q4_0_gate_up_glu_batch: packed weights not 256-byte aligned");
+    MI_CHECK_ARG(mi::aligned(x, 16) && mi::aligned(hxp, 16) && (!norm_w || (k <= 4096 && mi::aligned(norm_w, 16))),
+                 "mul_mat_q4_0_gate_up_glu_batch: x, hxp (and norm_w, k <= 4096) must be 16-byte aligned");
+    const size_t need = (size_t)m * k * 2;
+    if (!ws || ws_bytes < need || !mi::aligned(ws, 16)) {
+        mi::set_error("mul_mat_q4_0_gate_up_glu_batch: workspace %zu < %zu bytes (or misaligned)", ws_bytes, need);
+        return MI_ERR_WORKSPACE;
+    }
+    const uint8_t *wsb = (const uint8_t *)ws, *hb = (const uint8_t *)hxp;
+    MI_CHECK_ARG(hb + (size_t)m * n * 2 <= wsb || wsb + need <= hb,
+                 "mul_mat_q4_0_gate_up_glu_batch: hxp overlaps the workspace");
+    return launch_mfma_glu((hipStream_t)stream, (const uint8_t *)w_gate, (const uint8_t *)w_up, n, k, m, x, norm_w,
+                           eps, ws, (uint16_t *)hxp);
 }
 
 int mi_mul_mat_q4_0_f32_fused(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,

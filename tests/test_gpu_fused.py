@@ -762,3 +762,42 @@ def test_q4act_entry_points_reject_bad_arguments(gpu):
     with pytest.raises(RuntimeError):
         mi._call("mi_fa_decode_batch_q4act", None, None, None, None, None, None, 64, 2, 1, 64, 128, 128, 128, 128,
                  F32(0.1), None, 2, 128, 0, 0, 0, None, 0)
+
+
+@pytest.mark.parametrize("n,k,m,norm", [(18944, 3584, 8, True), (512, 256, 3, False), (1024, 4096, 16, True),
+                                         (256, 128, 2, False)])
+def test_q4_gate_up_glu_batch(gpu, n, k, m, norm):
+    """Gate and up of several rows with the swiglu in their epilogue, written as the down
+    projection's permuted fp16 activation: bit-identical to the gate/up batch launch
+    followed by the down projection's GLU conversion (both checked on the activation and
+    on the down projection's output with the residual)."""
+    mi = gpu
+    P = mi._P
+    rng = np.random.default_rng(n + k + m)
+    wg, wu = q4_0_weights(rng, n, k), q4_0_weights(rng, n, k)
+    pg, pu = _packed_q4(mi, wg, n, k), _packed_q4(mi, wu, n, k)
+    nd = 384
+    wd = q4_0_weights(rng, nd, n)
+    pd = _packed_q4(mi, wd, nd, n)
+    x = rng.standard_normal((m, k)).astype(F32)
+    nw = rng.uniform(0.8, 1.2, k).astype(F32)
+    res = rng.standard_normal((m, nd)).astype(F32)
+    dx, dnw, dres = mi.to_device(x), mi.to_device(nw), mi.to_device(res)
+    ws = mi.DeviceBuffer(m * k * 2)
+    hxp = mi.DeviceBuffer(m * n * 2)
+    mi._call("mi_mul_mat_q4_0_gate_up_glu_batch", None, P(pg.ptr), P(pu.ptr), n, k, m, P(dx.ptr),
+             P(dnw.ptr if norm else None), F32(1e-6), P(ws.ptr), m * k * 2, P(hxp.ptr))
+    y1 = mi.DeviceBuffer(4 * m * nd)
+    mi._call("mi_mul_mat_q4_0_batch_xp", None, 1, _ptrs(pd), _i64s(nd), _ptrs(y1), None, _ptrs(dres), n, m,
+             P(hxp.ptr))
+    # node by node: gate/up batch (fp32 outputs), then the down projection converting the GLU
+    yg, yu = mi.DeviceBuffer(4 * m * n), mi.DeviceBuffer(4 * m * n)
+    ws2 = mi.DeviceBuffer(m * max(k, n) * 2)
+    mi._call("mi_mul_mat_q4_0_f32_batch", None, 2, _ptrs(pg, pu), _i64s(n, n), _ptrs(yg, yu), None, None, k, m,
+             P(dx.ptr), None, P(dnw.ptr if norm else None), F32(1e-6), P(ws2.ptr), m * max(k, n) * 2)
+    y2 = mi.DeviceBuffer(4 * m * nd)
+    mi._call("mi_mul_mat_q4_0_f32_batch", None, 1, _ptrs(pd), _i64s(nd), _ptrs(y2), None, _ptrs(dres), n, m,
+             P(yg.ptr), P(yu.ptr), None, F32(0.0), P(ws2.ptr), m * max(k, n) * 2)
+    mi.device_sync()
+    assert np.array_equal(hxp.download(np.uint16), ws2.download(np.uint16, m * n))
+    assert np.array_equal(y1.download(F32), y2.download(F32))
