@@ -175,6 +175,20 @@ int mi_mul_mat_q4_0_batch_xp(void *stream, int n_mats, const void *const *w_pack
 int mi_mul_mat_q4_0_gate_up_glu_batch(void *stream, const void *w_gate, const void *w_up, int64_t n, int64_t k,
                                       int64_t m, const float *x, const float *norm_w, float eps, void *ws,
                                       size_t ws_bytes, void *hxp);
+/* [RMS_NORM -> MUL(norm_w)] -> q/k/v MUL_MATs (Q4_0, w_packed[0..2], n[0..2] rows) ->
+ * ADD bias[i] (or NULL) -> neox ROPE of q and k (position pos[r] for activation row r,
+ * head_dim rows per head) -> SET_ROWS of k and v (fp16) into cache row kv_idx[r], for m
+ * activation rows (1..16) in two launches; q_out gets the rotated q ([m][n[0]] fp32).
+ * Bit-identical to mi_mul_mat_q4_0_f32_batch of the set (with the biases) followed by
+ * mi_rope_kv_rows.  head_dim a multiple of 32 up to 256, n[0] and n[1] multiples of it,
+ * n[2] of 32, k % 128 == 0; ws: m * k * 2 bytes.  No reference counterpart: the
+ * reference runs these nodes one row and one node at a time. */
+int mi_qkv_rope_kv_q4_0_batch(void *stream, const void *const *w_packed, const int64_t *n, const float *const *bias,
+                              int64_t k, int64_t m, const float *x, const float *norm_w, float eps, void *ws,
+                              size_t ws_bytes, int64_t head_dim, const int32_t *pos, float freq_base,
+                              float freq_scale, float attn_factor, float *q_out, void *k_cache, size_t k_row_bytes,
+                              void *v_cache, size_t v_row_bytes, const void *kv_idx, int kv_idx_is_i64,
+                              int64_t n_cache_rows);
 /* the attention-input chain of one token: [RMS_NORM -> MUL(norm_w)] -> q/k/v MUL_MATs
  * (w_packed[0..2], n[0..2] rows, k <= 4096) -> ADD bias[i] (or NULL) -> neox ROPE of q
  * and k (n_dims = head_dim, theta = pos[0] * freq_base^(-2i/head_dim), freq_scale,

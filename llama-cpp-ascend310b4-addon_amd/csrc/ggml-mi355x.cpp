@@ -555,6 +555,8 @@ void run_fa(BackendCtx *ctx, ggml_tensor *node) {
 //                                                          mi_mul_mat_q4_0_batch_xp
 //   ubatch FFN      : [RMS_NORM, MUL(w)] MUL_MAT gate, MUL_MAT up, GLU swiglu, MUL_MAT down,
 //                     [ADD] -> mi_mul_mat_q4_0_gate_up_glu_batch + mi_mul_mat_q4_0_batch_xp
+//   ubatch attn in  : [RMS_NORM, MUL(w)] MUL_MAT q/k/v, ADD bias x3, ROPE q, ROPE k, SET_ROWS k,
+//                     SET_ROWS v -> mi_qkv_rope_kv_q4_0_batch
 //   rope + kv write : ROPE q, ROPE k, SET_ROWS k, SET_ROWS v -> mi_rope_kv_rows
 
 using Consumers = std::unordered_map<const ggml_tensor *, std::vector<const ggml_tensor *>>;
@@ -1070,6 +1072,12 @@ int fuse_q4_glu_pair(BackendCtx *ctx, ggml_cgraph *g, int i, int last, const Con
     return (ad ? next_real(g, jd + 1) : jd) + 1 - i;
 }
 
+struct RopeKvMatch;
+bool match_rope_kv(ggml_cgraph *g, int i, const Consumers &C, RopeKvMatch &R);
+int fuse_q4_qkv_rope(BackendCtx *ctx, ggml_cgraph *g, int i, int tail, const Consumers &C,
+                     const ggml_tensor *const *mm, const ggml_tensor *const *ad, const ggml_tensor *const *bias,
+                     const float *x, const BatchNorm &norm, int64_t k, int64_t m);
+
 int fuse_q4_batch_at(BackendCtx *ctx, ggml_cgraph *g, int i, int i0, const Consumers &C, const BatchNorm &norm) {
     const int nn = ggml_graph_n_nodes(g);
     ggml_tensor *mm0 = ggml_graph_node(g, i0);
@@ -1119,6 +1127,9 @@ int fuse_q4_batch_at(BackendCtx *ctx, ggml_cgraph *g, int i, int i0, const Consu
     const float *x = (const float *)(norm.w ? norm.x->data : mm0->src[1]->data);
     if (cnt == 2 && !all_add) {
         if (int used = fuse_q4_glu_pair(ctx, g, i, last, C, mm, x, norm, k, m)) return used;
+    }
+    if (cnt == 3 && all_add && bias[0] && bias[1] && bias[2]) {
+        if (int used = fuse_q4_qkv_rope(ctx, g, i, tail, C, mm, ad, other, x, norm, k, m)) return used;
     }
     MI_K_CHECK(mi_mul_mat_q4_0_f32_batch(ctx->stream, cnt, w, n, y, bv, av, k, m, x, nullptr,
                                          norm.w ? (const float *)norm.w->data : nullptr, norm.eps, ctx->scratch,
@@ -1217,51 +1228,100 @@ int try_fuse_glu_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumer
 
 // ROPE q, ROPE k (same positions and parameters, all head dims rotated), SET_ROWS of the
 // rotated k, SET_ROWS of v (same row indices): one launch over the ubatch's rows
-int try_fuse_rope_kv(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+// ROPE q, ROPE k, SET_ROWS k, SET_ROWS v starting at node i (views between them skipped)
+struct RopeKvMatch {
+    const ggml_tensor *rope[2], *sr[2], *v, *pos, *idx;
+    int64_t hd, m;
+    float freq_base, freq_scale, attn_factor;
+    int last;  // the last node of the run
+};
+
+bool match_rope_kv(ggml_cgraph *g, int i, const Consumers &C, RopeKvMatch &R) {
     const int nn = ggml_graph_n_nodes(g);
-    const ggml_tensor *rope[2], *sr[2];
     int j = i;
     for (int t = 0; t < 2; t++) {
         if (t) j = next_real(g, j + 1);
-        if (j >= nn) return 0;
-        rope[t] = ggml_graph_node(g, j);
-        const ggml_tensor *x = rope[t]->src[0];
-        if (rope[t]->op != GGML_OP_ROPE || !supports_op_impl(rope[t]) || !is_f32_contig(x) || !is_f32_contig(rope[t]) ||
-            rope[t]->op_params[1] != x->ne[0] || x->ne[3] != 1)
-            return 0;
+        if (j >= nn) return false;
+        R.rope[t] = ggml_graph_node(g, j);
+        const ggml_tensor *x = R.rope[t]->src[0];
+        if (R.rope[t]->op != GGML_OP_ROPE || !supports_op_impl(R.rope[t]) || !is_f32_contig(x) ||
+            !is_f32_contig(R.rope[t]) || R.rope[t]->op_params[1] != x->ne[0] || x->ne[3] != 1)
+            return false;
     }
-    const int64_t hd = rope[0]->src[0]->ne[0], m = rope[0]->src[0]->ne[2];
-    const ggml_tensor *pos = rope[0]->src[1];
-    if (rope[1]->src[0]->ne[0] != hd || rope[1]->src[0]->ne[2] != m || rope[1]->src[1] != pos ||
-        ggml_nelements(pos) != m || hd > 256 ||
-        memcmp(rope[0]->op_params + 5, rope[1]->op_params + 5, 4 * sizeof(int32_t)) != 0)
-        return 0;
+    R.hd = R.rope[0]->src[0]->ne[0];
+    R.m = R.rope[0]->src[0]->ne[2];
+    R.pos = R.rope[0]->src[1];
+    if (R.rope[1]->src[0]->ne[0] != R.hd || R.rope[1]->src[0]->ne[2] != R.m || R.rope[1]->src[1] != R.pos ||
+        ggml_nelements(R.pos) != R.m || R.hd > 256 ||
+        memcmp(R.rope[0]->op_params + 5, R.rope[1]->op_params + 5, 4 * sizeof(int32_t)) != 0)
+        return false;
     for (int t = 0; t < 2; t++) {
         j = next_real(g, j + 1);
-        if (j >= nn) return 0;
-        sr[t] = ggml_graph_node(g, j);
-        const ggml_tensor *src = sr[t]->src[0];
-        if (sr[t]->op != GGML_OP_SET_ROWS || !supports_op_impl(sr[t]) || !is_f32_contig(src) || ggml_nrows(src) != m ||
-            ggml_nelements(sr[t]->src[1]) != m || (t == 1 && sr[1]->src[1] != sr[0]->src[1]))
-            return 0;
+        if (j >= nn) return false;
+        R.sr[t] = ggml_graph_node(g, j);
+        const ggml_tensor *src = R.sr[t]->src[0];
+        if (R.sr[t]->op != GGML_OP_SET_ROWS || !supports_op_impl(R.sr[t]) || !is_f32_contig(src) ||
+            ggml_nrows(src) != R.m || ggml_nelements(R.sr[t]->src[1]) != R.m ||
+            (t == 1 && R.sr[1]->src[1] != R.sr[0]->src[1]))
+            return false;
     }
-    if (alias_root(sr[0]->src[0]) != rope[1] || sr[0]->src[0]->ne[0] != rope[1]->src[0]->ne[1] * hd ||
-        !only_consumed_by(C, rope[1], {sr[0]}))
-        return 0;
-    const ggml_tensor *v = sr[1]->src[0];
+    if (alias_root(R.sr[0]->src[0]) != R.rope[1] || R.sr[0]->src[0]->ne[0] != R.rope[1]->src[0]->ne[1] * R.hd ||
+        !only_consumed_by(C, R.rope[1], {R.sr[0]}))
+        return false;
+    R.v = R.sr[1]->src[0];
+    R.idx = R.sr[0]->src[1];
+    memcpy(&R.freq_base, (const float *)R.rope[0]->op_params + 5, sizeof(float));
+    memcpy(&R.freq_scale, (const float *)R.rope[0]->op_params + 6, sizeof(float));
+    memcpy(&R.attn_factor, (const float *)R.rope[0]->op_params + 8, sizeof(float));
+    R.last = j;
+    return true;
+}
+
+int try_fuse_rope_kv(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    RopeKvMatch R;
+    if (!match_rope_kv(g, i, C, R)) return 0;
     // q_out is written while other workgroups read k and v
-    if (overlaps(rope[0], alias_root(rope[1]->src[0])) || overlaps(rope[0], v)) return 0;
-    float freq_base, freq_scale, attn_factor;
-    memcpy(&freq_base, (const float *)rope[0]->op_params + 5, sizeof(float));
-    memcpy(&freq_scale, (const float *)rope[0]->op_params + 6, sizeof(float));
-    memcpy(&attn_factor, (const float *)rope[0]->op_params + 8, sizeof(float));
-    const ggml_tensor *idx = sr[0]->src[1];
-    MI_K_CHECK(mi_rope_kv_rows(ctx->stream, (const float *)rope[0]->src[0]->data, (const float *)rope[1]->src[0]->data,
-                               (const float *)v->data, (float *)rope[0]->data, sr[0]->data, sr[0]->nb[1], sr[1]->data,
-                               sr[1]->nb[1], (const int32_t *)pos->data, idx->data, idx->type == GGML_TYPE_I64,
-                               std::min(sr[0]->ne[1], sr[1]->ne[1]), m, hd, rope[0]->src[0]->ne[1],
-                               rope[1]->src[0]->ne[1], v->ne[0], freq_base, freq_scale, attn_factor));
-    return j + 1 - i;
+    if (overlaps(R.rope[0], alias_root(R.rope[1]->src[0])) || overlaps(R.rope[0], R.v)) return 0;
+    MI_K_CHECK(mi_rope_kv_rows(ctx->stream, (const float *)R.rope[0]->src[0]->data,
+                               (const float *)R.rope[1]->src[0]->data, (const float *)R.v->data,
+                               (float *)R.rope[0]->data, R.sr[0]->data, R.sr[0]->nb[1], R.sr[1]->data, R.sr[1]->nb[1],
+                               (const int32_t *)R.pos->data, R.idx->data, R.idx->type == GGML_TYPE_I64,
+                               std::min(R.sr[0]->ne[1], R.sr[1]->ne[1]), R.m, R.hd, R.rope[0]->src[0]->ne[1],
+                               R.rope[1]->src[0]->ne[1], R.v->ne[0], R.freq_base, R.freq_scale, R.attn_factor));
+    return R.last + 1 - i;
+}
+
+// q, k, v (+ bias each: the group just matched) -> ROPE q, ROPE k, SET_ROWS k, SET_ROWS v:
+// the rotation and the cache writes run in the projection's epilogue (PAIR_ROPE), so
+// neither the projected rows nor the rotated k are written to memory
+int fuse_q4_qkv_rope(BackendCtx *ctx, ggml_cgraph *g, int i, int tail, const Consumers &C,
+                     const ggml_tensor *const *mm, const ggml_tensor *const *ad, const ggml_tensor *const *bias,
+                     const float *x, const BatchNorm &norm, int64_t k, int64_t m) {
+    const int ir = next_real(g, tail + 1);
+    if (ir >= ggml_graph_n_nodes(g)) return 0;
+    RopeKvMatch R;
+    if (!match_rope_kv(g, ir, C, R)) return 0;
+    if (R.m != m || alias_root(R.rope[0]->src[0]) != ad[0] || alias_root(R.rope[1]->src[0]) != ad[1] ||
+        alias_root(R.v) != ad[2] || !only_consumed_by(C, ad[0], {R.rope[0]}) ||
+        !only_consumed_by(C, ad[1], {R.rope[1]}) || !only_consumed_by(C, ad[2], {R.sr[1]}))
+        return 0;
+    const int64_t n[3] = {mm[0]->src[0]->ne[1], mm[1]->src[0]->ne[1], mm[2]->src[0]->ne[1]};
+    if (R.hd % 32 || n[0] % R.hd || n[1] % R.hd || n[2] % 32 || R.rope[0]->src[0]->ne[1] * R.hd != n[0] ||
+        R.rope[1]->src[0]->ne[1] * R.hd != n[1] || R.v->ne[0] != n[2] || ctx->scratch_size < (size_t)(m * k * 2))
+        return 0;
+    const void *w[3];
+    const float *bv[3];
+    for (int t = 0; t < 3; t++) {
+        w[t] = ((const TensorExtra *)mm[t]->src[0]->extra)->packed;
+        bv[t] = (const float *)bias[t]->data;
+    }
+    MI_K_CHECK(mi_qkv_rope_kv_q4_0_batch(ctx->stream, w, n, bv, k, m, x,
+                                         norm.w ? (const float *)norm.w->data : nullptr, norm.eps, ctx->scratch,
+                                         ctx->scratch_size, R.hd, (const int32_t *)R.pos->data, R.freq_base,
+                                         R.freq_scale, R.attn_factor, (float *)R.rope[0]->data, R.sr[0]->data,
+                                         R.sr[0]->nb[1], R.sr[1]->data, R.sr[1]->nb[1], R.idx->data,
+                                         R.idx->type == GGML_TYPE_I64, std::min(R.sr[0]->ne[1], R.sr[1]->ne[1])));
+    return R.last + 1 - i;
 }
 
 // Runs node i (and, when fused, the nodes it absorbs); returns the number of nodes consumed.

@@ -496,6 +496,22 @@ struct Q4BSet {
     uint16_t *hxp;  // GLU pairs: the swiglu rows as the next projection's permuted fp16 activation
 };
 
+// RoPE pairs: the attention-input tail of a q/k/v set (matrices 0, 1, 2), per activation
+// row r: neox rotation of q and k by pos[r], q to q_out, the rotated k and v as fp16 into
+// cache row kv_idx[r]
+struct Q4BRope {
+    float *q_out;
+    uint8_t *kc, *vc;
+    const int32_t *pos;
+    const void *kv_idx;
+    int kv_i64;
+    int hd;
+    size_t k_row_bytes, v_row_bytes;
+    int64_t n_cache_rows;
+    float theta_scale, freq_scale, attn_factor;
+};
+constexpr int PAIR_NONE = 0, PAIR_GLU = 1, PAIR_ROPE = 2;
+
 // selected once per workgroup: a register select (see opaque_s), not a kernel-argument
 // load whose latency would sit in front of the first weight loads
 #define Q4B_PICK(S, f, i) \
@@ -518,20 +534,26 @@ struct Q4XStage {
 // matrix's tiles never straddle into the next matrix (n[i] % (16*TW) == 0 but for the
 // last).  SP (two groups per stage, at least two groups per row) loads the scales of a
 // stage's groups j0, j0+1 together from group jp = min(j0, ng - 2), which stays inside
-// the row.  GLU (TW = 2, matrices 0 and 1 of n rows each: gate and up): a workgroup's
-// tile 0 is gate rows 16b.., tile 1 the same up rows, and the epilogue writes
-// fp16(silu(gate) * up), ggml's swiglu then the src1 conversion, into S.hxp in the
-// permuted block layout of the activation (the next projection's input, k = n).
-template <int KS, int UG, int TW, bool SP, bool GLU = false>
+// the row.  Pairs (TW = 2) put two related row tiles in one workgroup:
+// - PAIR_GLU (matrices 0 and 1 of n rows each: gate and up): tile 0 is gate rows 16b..,
+//   tile 1 the same up rows, and the epilogue writes fp16(silu(gate) * up), ggml's swiglu
+//   then the src1 conversion, into S.hxp in the permuted block layout of the activation
+//   (the next projection's input, k = n);
+// - PAIR_ROPE (q, k, v of a q/k/v set, heads of hd rows): for q and k, tile 0 is dims
+//   16t.. of a head and tile 1 dims hd/2 + 16t.., so a lane holds both members of its
+//   rotation pairs; v takes 32 consecutive rows.  The epilogue adds the bias, rotates as
+//   the rope + cache-write kernel does and writes q_out and the k / v cache rows.
+template <int KS, int UG, int TW, bool SP, int PAIR = PAIR_NONE>
 __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, const uint4 *__restrict__ xp, int nb,
-                                                              int m) {
+                                                              int m, const Q4BRope RP) {
+    constexpr bool GLU = PAIR == PAIR_GLU, ROPE = PAIR == PAIR_ROPE;
     __shared__ float s_acc[KS][TW][64][4];
     __shared__ uint32_t s_t[KS][16][4][4];  // per wave: [row c][dword][block in group]
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int b = blockIdx.x;
-    static_assert(!GLU || TW == 2, "a GLU pair is one gate tile and one up tile");
+    static_assert(PAIR == PAIR_NONE || TW == 2, "a pair is two tiles");
     const int mi = GLU ? 0 : (b >= S.wg_end[0]) + (b >= S.wg_end[1]) + (b >= S.wg_end[2]);
     const int wg0 = GLU ? 0 : pick4(mi, 0, opaque_s(S.wg_end[0]), opaque_s(S.wg_end[1]), opaque_s(S.wg_end[2]));
     const int n = Q4B_PICK(S, n, mi);
@@ -541,13 +563,26 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, co
         qsb[t] = (uint64_t)(GLU ? S.qs[t] : Q4B_PICK(S, qs, mi));
         wdb[t] = (uint64_t)(GLU ? S.wd[t] : Q4B_PICK(S, wd, mi));
     }
-    const int row0 = GLU ? b * 16 : (b - wg0) * 16 * TW;
+    // first row of each tile
+    int trow[TW];
+    const int wi = b - wg0;
+#pragma unroll
+    for (int t = 0; t < TW; t++) {
+        if constexpr (GLU) {
+            trow[t] = b * 16;
+        } else if constexpr (ROPE) {
+            const int tph = RP.hd / 32;  // workgroups per head
+            trow[t] = mi < 2 ? (wi / tph) * RP.hd + 16 * (wi % tph) + t * (RP.hd / 2) : wi * 32 + 16 * t;
+        } else {
+            trow[t] = wi * 16 * TW + 16 * t;
+        }
+    }
     const int ng = nb / 4;               // whole groups (nb % 4 == 0)
     const int per = (ng + KS - 1) / KS;  // groups of this wave
     const int j_lo = wave * per, j_hi = min(ng, j_lo + per);
     uint64_t wrow[TW];
 #pragma unroll
-    for (int t = 0; t < TW; t++) wrow[t] = (uint64_t)min(row0 + (GLU ? 0 : 16 * t) + c, n - 1) * nb;
+    for (int t = 0; t < TW; t++) wrow[t] = (uint64_t)min(trow[t] + c, n - 1) * nb;
     // activation rows past m (lanes c >= m) re-read row m - 1: their products land only in
     // output rows >= m, which are never stored
     const uint4 *xrow = xp + (size_t)min(c, m - 1) * nb * 4 + g;
@@ -654,15 +689,66 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, co
 #pragma unroll
         for (int i = 0; i < 4; i++) s_acc[wave][t][lane][i] = acc[t][i];
     __syncthreads();
-    if (wave != 0) return;
+    if constexpr (ROPE) {
+        // every wave takes one of the lane's 4 activation rows (the rotation's angle loop
+        // and sin / cos are the long part)
+        static_assert(KS == 4, "one epilogue row per wave");
+        const uint64_t bias = (uint64_t)Q4B_PICK(S, bias, mi);
+        float bv[TW];
+#pragma unroll
+        for (int t = 0; t < TW; t++) bv[t] = bias ? ldg_f32(bias + 4 * (uint64_t)(trow[t] + c)) : 0.0f;
+        const int half = RP.hd / 2;
+        const int p = trow[0] % RP.hd + c;  // rotation pair (q, k): dims p and p + half of its head
+        const int head = trow[0] / RP.hd;
+        {
+            const int i = wave;
+            const int r = 4 * g + i;
+            if (r >= m) return;
+            float v[TW];
+#pragma unroll
+            for (int t = 0; t < TW; t++) {
+                float a = 0.0f;
+#pragma unroll
+                for (int w = 0; w < KS; w++) a += s_acc[w][t][lane][i];
+                v[t] = bias ? a + bv[t] : a;
+            }
+            const int64_t ci = RP.kv_i64 ? ((const int64_t *)RP.kv_idx)[r] : (int64_t)((const int32_t *)RP.kv_idx)[r];
+            const bool ci_ok = ci >= 0 && ci < RP.n_cache_rows;
+            if (mi < 2) {
+                float theta = (float)RP.pos[r];
+                for (int tt = 0; tt < p; tt++) theta *= RP.theta_scale;  // the rope kernel's product order
+                const float th = RP.freq_scale * theta;
+                const float cs = cosf(th) * RP.attn_factor;
+                const float sn = sinf(th) * RP.attn_factor;
+                const float y0 = mul_sub_mul_rn(v[0], cs, v[1], sn);
+                const float y1 = mul_add_mul_rn(v[0], sn, v[1], cs);
+                if (mi == 0) {
+                    float *yr = RP.q_out + ((size_t)r * (n / RP.hd) + head) * RP.hd;
+                    yr[p] = y0;
+                    yr[p + half] = y1;
+                } else if (ci_ok) {
+                    uint16_t *kr = (uint16_t *)(RP.kc + (size_t)ci * RP.k_row_bytes) + (size_t)head * RP.hd;
+                    kr[p] = f2h(y0);
+                    kr[p + half] = f2h(y1);
+                }
+            } else if (ci_ok) {
+                uint16_t *vr = (uint16_t *)(RP.vc + (size_t)ci * RP.v_row_bytes);
+#pragma unroll
+                for (int t = 0; t < TW; t++)
+                    if (trow[t] + c < n) vr[trow[t] + c] = f2h(v[t]);
+            }
+        }
+        return;
+    }
+    // the waves share the epilogue: wave w takes the lane's activation rows 4g + i, i = w (mod KS)
+    if (wave >= 4) return;
     if constexpr (GLU) {
-        const int row = row0 + c;  // h index
+        const int row = trow[0] + c;  // h index
         if (row >= n) return;
         const int p = row & 31, q = p & 3;
         const int gp = (p & 15) >> 2, jp = (p >> 4) * 4 + (q == 1 ? 2 : q == 2 ? 1 : q);
         const size_t nbd = (size_t)n / QK;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = wave; i < 4; i += KS) {
             const int r = 4 * g + i;
             if (r < m) {
                 float gv = 0.0f, uv = 0.0f;
@@ -681,11 +767,10 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4_0_mfma_x(const Q4BSet S, co
     const uint64_t add = (uint64_t)Q4B_PICK(S, add, mi);
 #pragma unroll
     for (int t = 0; t < TW; t++) {
-        const int row = row0 + 16 * t + c;
+        const int row = trow[t] + c;
         if (row >= n) continue;
         const float bv = bias ? ldg_f32(bias + 4 * (uint64_t)row) : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = wave; i < 4; i += KS) {
             const int r = 4 * g + i;  // activation row
             if (r < m) {
                 float v = 0.0f;
@@ -1450,7 +1535,7 @@ int launch_mfma_set(hipStream_t st, int count, const uint8_t *const *base, const
     }
 #define MI_MX(KS, TW, SPV)                                                                                      \
     hipLaunchKernelGGL((k_gemv_q4_0_mfma_x<KS, 2, TW, SPV>), dim3((unsigned)wgs), dim3(64 * KS), 0, st, S,        \
-                       (const uint4 *)ws, nb, (int)m)
+                       (const uint4 *)ws, nb, (int)m, Q4BRope{})
 #define MI_MX_TW(KS, TW)              \
     {                                 \
         if (sp) MI_MX(KS, TW, true);  \
@@ -1496,11 +1581,49 @@ int launch_mfma_glu(hipStream_t st, const uint8_t *gate, const uint8_t *up, int6
     S.hxp = hxp;
     const dim3 grid((unsigned)((n + 15) / 16));
     if (nb / 4 >= 2)
-        hipLaunchKernelGGL((k_gemv_q4_0_mfma_x<4, 2, 2, true, true>), grid, dim3(256), 0, st, S, (const uint4 *)ws, nb,
-                           (int)m);
+        hipLaunchKernelGGL((k_gemv_q4_0_mfma_x<4, 2, 2, true, PAIR_GLU>), grid, dim3(256), 0, st, S,
+                           (const uint4 *)ws, nb, (int)m, Q4BRope{});
     else
-        hipLaunchKernelGGL((k_gemv_q4_0_mfma_x<4, 2, 2, false, true>), grid, dim3(256), 0, st, S, (const uint4 *)ws,
-                           nb, (int)m);
+        hipLaunchKernelGGL((k_gemv_q4_0_mfma_x<4, 2, 2, false, PAIR_GLU>), grid, dim3(256), 0, st, S,
+                           (const uint4 *)ws, nb, (int)m, Q4BRope{});
+    MI_CHECK_LAUNCH("k_gemv_q4_0_mfma_x");
+    return MI_OK;
+}
+
+// q/k/v (+ bias) of m activation rows after RMSNorm * norm_w (or not), then RoPE of q and
+// k and the k / v cache writes in the epilogue (PAIR_ROPE).  n[0], n[1] multiples of
+// the head size hd (a multiple of 32, <= 256), n[2] of 32.
+int launch_mfma_rope(hipStream_t st, const uint8_t *const *base, const int64_t *n, const float *const *bias,
+                     int64_t k, int64_t m, const float *x, const float *norm_w, float eps, void *ws,
+                     const Q4BRope &RP) {
+    const int nb = (int)(k / QK);
+    if (norm_w)
+        hipLaunchKernelGGL(k_perm_norm_f16, dim3((unsigned)m), dim3(256), 0, st, x, norm_w, eps, (uint4 *)ws, nb);
+    else
+        hipLaunchKernelGGL((k_perm_f16<PERM_F32>), dim3((unsigned)((m * nb * 4 + 255) / 256)), dim3(256), 0, st,
+                           (const void *)x, nullptr, (uint4 *)ws, (int)m, nb);
+    MI_CHECK_LAUNCH("k_perm_f16");
+    Q4BSet S;
+    int wgs = 0;
+    for (int i = 0; i < 4; i++) {
+        const int j = i < 3 ? i : 0;
+        const Q4Planes p = q4_planes(n[j], k);
+        S.qs[i] = base[j];
+        S.wd[i] = (const uint16_t *)(base[j] + p.plane);
+        S.y[i] = nullptr;
+        S.bias[i] = i < 3 && bias ? bias[i] : nullptr;
+        S.add[i] = nullptr;
+        S.n[i] = (int)n[j];
+        if (i < 3) wgs += (int)(n[i] / 32);
+        S.wg_end[i] = i < 3 ? wgs : INT_MAX;
+    }
+    S.hxp = nullptr;
+    if (nb / 4 >= 2)
+        hipLaunchKernelGGL((k_gemv_q4_0_mfma_x<4, 2, 2, true, PAIR_ROPE>), dim3((unsigned)wgs), dim3(256), 0, st, S,
+                           (const uint4 *)ws, nb, (int)m, RP);
+    else
+        hipLaunchKernelGGL((k_gemv_q4_0_mfma_x<4, 2, 2, false, PAIR_ROPE>), dim3((unsigned)wgs), dim3(256), 0, st, S,
+                           (const uint4 *)ws, nb, (int)m, RP);
     MI_CHECK_LAUNCH("k_gemv_q4_0_mfma_x");
     return MI_OK;
 }
@@ -1722,6 +1845,53 @@ int mi_mul_mat_q4_0_gate_up_glu_batch(void *stream, const void *w_gate, const vo
                  "mul_mat_q4_0_gate_up_glu_batch: hxp overlaps the workspace");
     return launch_mfma_glu((hipStream_t)stream, (const uint8_t *)w_gate, (const uint8_t *)w_up, n, k, m, x, norm_w,
                            eps, ws, (uint16_t *)hxp);
+}
+
+int mi_qkv_rope_kv_q4_0_batch(void *stream, const void *const *w_packed, const int64_t *n, const float *const *bias,
+                              int64_t k, int64_t m, const float *x, const float *norm_w, float eps, void *ws,
+                              size_t ws_bytes, int64_t head_dim, const int32_t *pos, float freq_base,
+                              float freq_scale, float attn_factor, float *q_out, void *k_cache, size_t k_row_bytes,
+                              void *v_cache, size_t v_row_bytes, const void *kv_idx, int kv_idx_is_i64,
+                              int64_t n_cache_rows) {
+    MI_CHECK_ARG(w_packed && n && x && pos && q_out && k_cache && v_cache && kv_idx,
+                 "qkv_rope_kv_q4_0_batch: null pointer");
+    MI_CHECK_ARG(m >= 1 && m <= 16, "qkv_rope_kv_q4_0_batch: m=%lld not in 1..16", (long long)m);
+    MI_CHECK_ARG(k % (4 * QK) == 0, "qkv_rope_kv_q4_0_batch: k=%lld not a multiple of 128", (long long)k);
+    MI_CHECK_ARG(head_dim >= 32 && head_dim <= 256 && head_dim % 32 == 0 && n[0] % head_dim == 0 &&
+                     n[1] % head_dim == 0 && n[2] % 32 == 0,
+                 "qkv_rope_kv_q4_0_batch: head_dim %lld / rows %lld %lld %lld not supported", (long long)head_dim,
+                 (long long)n[0], (long long)n[1], (long long)n[2]);
+    const uint8_t *base[3];
+    for (int i = 0; i < 3; i++) {
+        if (int r = check_shape("qkv_rope_kv_q4_0_batch", n[i], k)) return r;
+        MI_CHECK_ARG(w_packed[i] && mi::aligned(w_packed[i], 256),
+                     "qkv_rope_kv_q4_0_batch: packed weight %d null or not 256-byte aligned", i);
+        base[i] = (const uint8_t *)w_packed[i];
+    }
+    MI_CHECK_ARG(k_row_bytes >= (size_t)n[1] * 2 && v_row_bytes >= (size_t)n[2] * 2,
+                 "qkv_rope_kv_q4_0_batch: cache rows too short");
+    MI_CHECK_ARG(mi::aligned(x, 16) && (!norm_w || (k <= 4096 && mi::aligned(norm_w, 16))),
+                 "qkv_rope_kv_q4_0_batch: x (and norm_w, k <= 4096) must be 16-byte aligned");
+    const size_t need = (size_t)m * k * 2;
+    if (!ws || ws_bytes < need || !mi::aligned(ws, 16)) {
+        mi::set_error("qkv_rope_kv_q4_0_batch: workspace %zu < %zu bytes (or misaligned)", ws_bytes, need);
+        return MI_ERR_WORKSPACE;
+    }
+    Q4BRope RP;
+    RP.q_out = q_out;
+    RP.kc = (uint8_t *)k_cache;
+    RP.vc = (uint8_t *)v_cache;
+    RP.pos = pos;
+    RP.kv_idx = kv_idx;
+    RP.kv_i64 = kv_idx_is_i64;
+    RP.hd = (int)head_dim;
+    RP.k_row_bytes = k_row_bytes;
+    RP.v_row_bytes = v_row_bytes;
+    RP.n_cache_rows = n_cache_rows;
+    RP.theta_scale = powf(freq_base, -2.0f / (float)head_dim);
+    RP.freq_scale = freq_scale;
+    RP.attn_factor = attn_factor;
+    return launch_mfma_rope((hipStream_t)stream, base, n, bias, k, m, x, norm_w, eps, ws, RP);
 }
 
 int mi_mul_mat_q4_0_f32_fused(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,

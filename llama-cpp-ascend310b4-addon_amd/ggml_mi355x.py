@@ -107,6 +107,8 @@ _SIGS = {
     "mi_mul_mat_q4_0_f32_batch": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _F, _P, _SZ]),
     "mi_mul_mat_q4_0_batch_xp": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I64, _P]),
     "mi_mul_mat_q4_0_gate_up_glu_batch": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _F, _P, _SZ, _P]),
+    "mi_qkv_rope_kv_q4_0_batch": (_I, [_P, _P, _P, _P, _I64, _I64, _P, _P, _F, _P, _SZ, _I64, _P, _F, _F, _F, _P, _P, _SZ,
+                                       _P, _SZ, _P, _I, _I64]),
     "mi_fa_decode_batch_q4act": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _SZ, _SZ, _SZ, _SZ, _F, _P, _I64,
                                       _SZ, _SZ, _SZ, _SZ, _P, _SZ]),
     "mi_rope_kv_rows": (_I, [_P, _P, _P, _P, _P, _P, _SZ, _P, _SZ, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _F,

@@ -801,3 +801,55 @@ def test_q4_gate_up_glu_batch(gpu, n, k, m, norm):
     mi.device_sync()
     assert np.array_equal(hxp.download(np.uint16), ws2.download(np.uint16, m * n))
     assert np.array_equal(y1.download(F32), y2.download(F32))
+
+
+# (activation rows, k, head dim, q heads, kv heads, index type, norm): the 7B ubatch shape,
+# a 64-wide head, one sequence, two with 64-bit cache indices
+@pytest.mark.parametrize("m,k,hd,nhq,nhk,idx_i64,norm", [(8, 3584, 128, 28, 4, False, True),
+                                                         (3, 512, 64, 8, 2, True, False),
+                                                         (1, 1024, 128, 4, 2, False, True),
+                                                         (2, 256, 32, 4, 1, True, True)])
+def test_q4_qkv_rope_kv_batch(gpu, m, k, hd, nhq, nhk, idx_i64, norm):
+    """q/k/v of several rows with their biases, the rotation of q and k and the k / v cache
+    writes in the projection's epilogue: bit-identical to the q/k/v batch launch followed
+    by the rope + cache-write launch (the node-by-node ubatch path); a cache index outside
+    the cache is skipped."""
+    mi = gpu
+    P = mi._P
+    rng = np.random.default_rng(m * 100 + k + hd)
+    ns = (nhq * hd, nhk * hd, nhk * hd)
+    ws_ = [q4_0_weights(rng, n, k) for n in ns]
+    pw = [_packed_q4(mi, w, n, k) for w, n in zip(ws_, ns)]
+    bias = [rng.standard_normal(n).astype(F32) for n in ns]
+    db = [mi.to_device(b) for b in bias]
+    x = rng.standard_normal((m, k)).astype(F32)
+    nw = rng.uniform(0.8, 1.2, k).astype(F32)
+    dx, dnw = mi.to_device(x), mi.to_device(nw)
+    n_cache = 48
+    pos = rng.integers(0, 40000, m).astype(np.int32)
+    idx = rng.permutation(n_cache)[:m].astype(np.int64 if idx_i64 else np.int32)
+    if m > 2:
+        idx[1] = n_cache + 3  # outside the cache: not written
+    kc0 = f16_bits(rng.standard_normal((n_cache, ns[1])))
+    vc0 = f16_bits(rng.standard_normal((n_cache, ns[2])))
+    dp, di = mi.to_device(pos), mi.to_device(idx)
+    wsb = m * k * 2
+    # fused
+    kc1, vc1, qo1 = mi.to_device(kc0), mi.to_device(vc0), mi.DeviceBuffer(4 * m * ns[0])
+    ws1 = mi.DeviceBuffer(wsb)
+    mi._call("mi_qkv_rope_kv_q4_0_batch", None, _ptrs(*pw), _i64s(*ns), _ptrs(*db), k, m, P(dx.ptr),
+             P(dnw.ptr if norm else None), F32(1e-6), P(ws1.ptr), wsb, hd, P(dp.ptr), F32(1e6), F32(1.0), F32(1.0),
+             P(qo1.ptr), P(kc1.ptr), ns[1] * 2, P(vc1.ptr), ns[2] * 2, P(di.ptr), int(idx_i64), n_cache)
+    # node by node: the set with biases, then rope + cache writes
+    ys = [mi.DeviceBuffer(4 * m * n) for n in ns]
+    ws2 = mi.DeviceBuffer(wsb)
+    mi._call("mi_mul_mat_q4_0_f32_batch", None, 3, _ptrs(*pw), _i64s(*ns), _ptrs(*ys), _ptrs(*db), None, k, m,
+             P(dx.ptr), None, P(dnw.ptr if norm else None), F32(1e-6), P(ws2.ptr), wsb)
+    kc2, vc2, qo2 = mi.to_device(kc0), mi.to_device(vc0), mi.DeviceBuffer(4 * m * ns[0])
+    mi._call("mi_rope_kv_rows", None, P(ys[0].ptr), P(ys[1].ptr), P(ys[2].ptr), P(qo2.ptr), P(kc2.ptr), ns[1] * 2,
+             P(vc2.ptr), ns[2] * 2, P(dp.ptr), P(di.ptr), int(idx_i64), n_cache, m, hd, nhq, nhk, ns[2], F32(1e6),
+             F32(1.0), F32(1.0))
+    mi.device_sync()
+    assert np.array_equal(qo1.download(F32), qo2.download(F32))
+    assert np.array_equal(kc1.download(np.uint16), kc2.download(np.uint16))
+    assert np.array_equal(vc1.download(np.uint16), vc2.download(np.uint16))
