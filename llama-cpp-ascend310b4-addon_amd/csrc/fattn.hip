@@ -628,7 +628,8 @@ __global__ __launch_bounds__(64 * NW) void k_fa_mfma(const float *__restrict__ q
         // two register stages; the next pair's loads are unconditional (past the run they
         // re-read its last row: cache hits, masked), so no wait gathers every load
         issue(1, 1);
-#pragma unroll(NBW <= 8 ? NBW / 2 : 1)
+        constexpr int kUnroll = NBW <= 8 ? NBW / 2 : 1;
+#pragma unroll kUnroll
         for (int blk = 0; blk < NBW; blk += 2) {
             step(blk, B0{});
             issue(blk + 2, 0);

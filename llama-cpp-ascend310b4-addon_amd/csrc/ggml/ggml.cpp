@@ -285,7 +285,7 @@ static ggml_tensor *dup_tensor(ggml_context *ctx, const ggml_tensor *a) {
 static ggml_tensor *view_tensor(ggml_context *ctx, ggml_tensor *a) {
     ggml_tensor *r = new_tensor_impl(ctx, a->type, GGML_MAX_DIMS, a->ne, a, 0);
     for (int i = 0; i < GGML_MAX_DIMS; i++) r->nb[i] = a->nb[i];
-    snprintf(r->name, sizeof(r->name), "%.57s (view)", a->name);
+    snprintf(r->name, sizeof(r->name), "%.56s (view)", a->name);
     return r;
 }
 
@@ -310,7 +310,7 @@ struct ggml_tensor *ggml_reshape_2d(struct ggml_context *ctx, struct ggml_tensor
     GGML_ASSERT(ggml_is_contiguous(a) && ggml_nelements(a) == ne0 * ne1);
     const int64_t ne[2] = {ne0, ne1};
     ggml_tensor *r = new_tensor_impl(ctx, a->type, 2, ne, a, 0);
-    snprintf(r->name, sizeof(r->name), "%.53s (reshaped)", a->name);
+    snprintf(r->name, sizeof(r->name), "%.52s (reshaped)", a->name);
     r->op = GGML_OP_RESHAPE;
     r->src[0] = a;
     return r;
@@ -321,7 +321,7 @@ struct ggml_tensor *ggml_reshape_3d(struct ggml_context *ctx, struct ggml_tensor
     GGML_ASSERT(ggml_is_contiguous(a) && ggml_nelements(a) == ne0 * ne1 * ne2);
     const int64_t ne[3] = {ne0, ne1, ne2};
     ggml_tensor *r = new_tensor_impl(ctx, a->type, 3, ne, a, 0);
-    snprintf(r->name, sizeof(r->name), "%.53s (reshaped)", a->name);
+    snprintf(r->name, sizeof(r->name), "%.52s (reshaped)", a->name);
     r->op = GGML_OP_RESHAPE;
     r->src[0] = a;
     return r;
@@ -332,7 +332,7 @@ struct ggml_tensor *ggml_reshape_4d(struct ggml_context *ctx, struct ggml_tensor
     GGML_ASSERT(ggml_is_contiguous(a) && ggml_nelements(a) == ne0 * ne1 * ne2 * ne3);
     const int64_t ne[4] = {ne0, ne1, ne2, ne3};
     ggml_tensor *r = new_tensor_impl(ctx, a->type, 4, ne, a, 0);
-    snprintf(r->name, sizeof(r->name), "%.53s (reshaped)", a->name);
+    snprintf(r->name, sizeof(r->name), "%.52s (reshaped)", a->name);
     r->op = GGML_OP_RESHAPE;
     r->src[0] = a;
     return r;
@@ -340,7 +340,7 @@ struct ggml_tensor *ggml_reshape_4d(struct ggml_context *ctx, struct ggml_tensor
 
 static ggml_tensor *view_impl(ggml_context *ctx, ggml_tensor *a, int n_dims, const int64_t *ne, size_t offset) {
     ggml_tensor *r = new_tensor_impl(ctx, a->type, n_dims, ne, a, offset);
-    snprintf(r->name, sizeof(r->name), "%.57s (view)", a->name);
+    snprintf(r->name, sizeof(r->name), "%.56s (view)", a->name);
     set_op_params(r, &offset, sizeof(offset));
     r->op = GGML_OP_VIEW;
     r->src[0] = a;
@@ -394,7 +394,7 @@ struct ggml_tensor *ggml_permute(struct ggml_context *ctx, struct ggml_tensor *a
         r->ne[i] = ne[i];
         r->nb[i] = nb[i];
     }
-    snprintf(r->name, sizeof(r->name), "%.53s (permuted)", a->name);
+    snprintf(r->name, sizeof(r->name), "%.52s (permuted)", a->name);
     r->op = GGML_OP_PERMUTE;
     r->src[0] = a;
     const int32_t params[4] = {axis0, axis1, axis2, axis3};

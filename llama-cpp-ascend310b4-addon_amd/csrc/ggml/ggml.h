@@ -255,7 +255,7 @@ GGML_API ggml_fp16_t ggml_fp32_to_fp16(float f);
         if (!(x)) ggml_abort(__FILE__, __LINE__, "GGML_ASSERT(%s) failed", #x);   \
     } while (0)
 #define GGML_ABORT(...) ggml_abort(__FILE__, __LINE__, __VA_ARGS__)
-GGML_API void ggml_abort(const char *file, int line, const char *fmt, ...);
+GGML_API [[noreturn]] void ggml_abort(const char *file, int line, const char *fmt, ...);
 
 #ifdef __cplusplus
 }
