@@ -172,6 +172,32 @@ def test_fused_graph_matches_unfused_batch(gpu, monkeypatch, wtype):
     plain.free()
 
 
+def test_fused_graph_matches_unfused_batch_7b_width(gpu, monkeypatch):
+    """A ubatch of 4 sequences at the Qwen2.5-7B width (W4A16, 28/4 heads of 128, FFN
+    18944, two layers): the fused launches at their real shapes (q/k/v with RoPE pairs and
+    the cache writes, the combine writing the o projection's activation, gate/up GLU
+    pairs, the matrix-core head) against the node-by-node path, logits bit-identical."""
+    mi = gpu
+    n_seq = 4
+    hp = qs.qwen2_7b(n_layer=2, n_ctx=48, n_seq=n_seq)
+    tensors, smooth = qs.synth(hp, seed=31)
+    fused = mi.Qwen2Model(hp)
+    fused.load(tensors, smooth)
+    monkeypatch.setenv("GGML_MI355X_FUSION", "0")
+    plain = mi.Qwen2Model(hp)
+    plain.load(tensors, smooth)
+    rng = np.random.default_rng(32)
+    toks = rng.integers(0, hp["n_vocab"], n_seq)
+    for pos in range(6):
+        tf, lf = fused.decode_batch(toks, [pos] * n_seq, want_logits=True)
+        tp, lp = plain.decode_batch(toks, [pos] * n_seq, want_logits=True)
+        assert np.array_equal(lf, lp), f"position {pos}: max rel {np.abs(lf - lp).max() / np.abs(lp).max():.3e}"
+        assert np.array_equal(tf, tp)
+        toks = tf
+    fused.free()
+    plain.free()
+
+
 @pytest.mark.parametrize("wtype", [qs.GGML_TYPE_Q4_0, qs.GGML_TYPE_Q8_0])
 def test_qwen2_batch_of_sequences(gpu, orc, wtype):
     """Three sequences decoded together (one ubatch of 3 tokens per step, per-sequence KV
