@@ -696,7 +696,9 @@ __global__ __launch_bounds__(64 * NW) void k_fa_mfma(const float *__restrict__ q
 // Parallel log-sum-exp combine: grid (q head, D/32 dim slices, sequence), 256 threads =
 // 32 dims x 8 split groups.  A thread merges splits g, g+8, ... of its group itself
 // (online: running maximum, rescaled sums), loading every split's m, l and output value
-// of a 64-split chunk at once, so a chunk costs one round trip; the 8 groups then merge
+// of an 8U-split chunk at once, so a chunk costs one round trip (U = 16 above 64 splits:
+// 128 splits, 256 positions each at 32K, then take one round trip, not two in a
+// dependent loop; at most 64 splits keep U = 8 and its merge order); the 8 groups then merge
 // through LDS.  w_s = 2^(m_s - M), 0 for a split with no position; out = sum w_s o_s /
 // sum w_s l_s, 0 when no split has a position.
 //
@@ -705,7 +707,7 @@ __global__ __launch_bounds__(64 * NW) void k_fa_mfma(const float *__restrict__ q
 // nibble order of a weight dword: xp[seq][block][g][8] = x[4g], x[4g+2], x[4g+1], x[4g+3],
 // x[16+4g], x[18+4g], x[17+4g], x[19+4g] (out_seq is then the blocks per row).  The 32
 // dims of a workgroup are one whole block.
-template <int D, bool XP>
+template <int D, bool XP, int U>
 __global__ __launch_bounds__(256) void k_fa_combine(const float *__restrict__ part, void *__restrict__ out_v,
                                                     int n_splits, size_t out_seq) {
     constexpr int PS = part_stride<D>();
@@ -718,10 +720,10 @@ __global__ __launch_bounds__(256) void k_fa_combine(const float *__restrict__ pa
     const int dd = tid % 32, sg = tid / 32;
     const float *ph = part + (size_t)h * n_splits * PS;
     float M = -INFINITY, L = 0.0f, A = 0.0f;
-    for (int base = 0; base < n_splits; base += 64) {
-        float mv[8], lv[8], ov[8];
+    for (int base = 0; base < n_splits; base += 8 * U) {
+        float mv[U], lv[U], ov[U];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {  // clamped, branch-free: all loads of the chunk in flight
+        for (int u = 0; u < U; u++) {  // clamped, branch-free: all loads of the chunk in flight
             const int sp = base + sg + 8 * u;
             const float *rec = ph + (size_t)min(sp, n_splits - 1) * PS;
             mv[u] = sp < n_splits ? rec[D] : -INFINITY;
@@ -730,13 +732,13 @@ __global__ __launch_bounds__(256) void k_fa_combine(const float *__restrict__ pa
         }
         float cm = M;
 #pragma unroll
-        for (int u = 0; u < 8; u++) cm = fmaxf(cm, mv[u]);
+        for (int u = 0; u < U; u++) cm = fmaxf(cm, mv[u]);
         if (cm == -INFINITY) continue;
         const float r = M == -INFINITY ? 0.0f : fexp2(M - cm);
         L *= r;
         A *= r;
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+        for (int u = 0; u < U; u++) {
             const float w = mv[u] == -INFINITY ? 0.0f : fexp2(mv[u] - cm);
             L = fmaf(lv[u], w, L);
             A = fmaf(ov[u], w, A);
@@ -852,11 +854,18 @@ int launch_split_m(hipStream_t st, const FaArgs &a, const FaPlan &p) {
     }
     if ((p.n_splits > 1 || a.xp) && !a.partials_only) {
         const dim3 cg((unsigned)(a.n_kv_heads * GQ), D / 32, (unsigned)a.n_seq);
-        if (a.xp)
-            hipLaunchKernelGGL((k_fa_combine<D, true>), cg, dim3(256), 0, st, a.part, (void *)a.xp, p.n_splits,
+        const bool wide = p.n_splits > 64;
+        if (a.xp && wide)
+            hipLaunchKernelGGL((k_fa_combine<D, true, 16>), cg, dim3(256), 0, st, a.part, (void *)a.xp, p.n_splits,
                                (size_t)a.xp_nb);
+        else if (a.xp)
+            hipLaunchKernelGGL((k_fa_combine<D, true, 8>), cg, dim3(256), 0, st, a.part, (void *)a.xp, p.n_splits,
+                               (size_t)a.xp_nb);
+        else if (wide)
+            hipLaunchKernelGGL((k_fa_combine<D, false, 16>), cg, dim3(256), 0, st, a.part, (void *)a.out,
+                               p.n_splits, a.sq.out);
         else
-            hipLaunchKernelGGL((k_fa_combine<D, false>), cg, dim3(256), 0, st, a.part, (void *)a.out, p.n_splits,
+            hipLaunchKernelGGL((k_fa_combine<D, false, 8>), cg, dim3(256), 0, st, a.part, (void *)a.out, p.n_splits,
                                a.sq.out);
         MI_CHECK_LAUNCH("k_fa_combine");
     }

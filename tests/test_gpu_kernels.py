@@ -255,8 +255,11 @@ def test_fa_decode_config2(gpu, orc, L):
     _check_fa(orc, o, q, kc, vc, 2, 1 / np.sqrt(128), label=f"L={L}")
 
 
-@pytest.mark.parametrize("L", [1, 2, 15, 127, 128, 129, 239, 240, 241, 255, 256, 257, 511, 513, 1024, 8192])
+@pytest.mark.parametrize("L", [1, 2, 15, 127, 128, 129, 239, 240, 241, 255, 256, 257, 511, 513, 1024, 5000, 8192,
+                               12345])
 def test_fa_decode_boundaries(gpu, orc, L):
+    """Split and block edges; 5000 (79 splits) and 12345 (193) end the combine's 128-split
+    chunks part way, past 64 splits where each thread loads 16 splits at once."""
     mi = gpu
     rng = np.random.default_rng(1000 + L)
     q = rng.standard_normal((12, 128)).astype(np.float32)
