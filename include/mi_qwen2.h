@@ -50,6 +50,24 @@ const char *mi_qwen2_last_error(void);
 int mi_qwen2_set_tensor(mi_qwen2 *m, const char *name, const void *data, size_t size);
 /* SmoothQuant factors s (length = the weight's input dim) of one projection weight */
 int mi_qwen2_set_smooth(mi_qwen2 *m, const char *weight_name, const float *s, int64_t n);
+/* Read a SmoothQuant scale file: little-endian fp32 [n_layer][n_embd], every factor
+ * positive and finite, the file's size exactly n_layer*n_embd*4 bytes.  The format is
+ * the one tools/smoothquant/smoothquant-make-scales.py:14-17 writes (sq-scales-aXX.bin:
+ * per layer the FFN input channels' s = a^alpha / w^(1-alpha), clipped to [1e-3, 1e3]).
+ * Host-only; needs no device. */
+int mi_smooth_scales_read(const char *path, int64_t n_layer, int64_t n_embd, float *out);
+/* Load such a file into the model: row il is the SmoothQuant factor of blk.il.ffn_gate and
+ * blk.il.ffn_up (mi_qwen2_set_smooth on each; Q8_0 weights only). */
+int mi_qwen2_load_smooth_file(mi_qwen2 *m, const char *path);
+/* Write the latest decode step's layer outputs as LLDUMP1 records, the layer-dump format of
+ * the reference's llama-eval-callback (patch:825-892, enabled there by LLAMA_LAYER_DUMP,
+ * patch:928): the 8-byte magic "LLDUMP1\0" once, then per tensor a u16 name length, the
+ * name, a u64 value count and the values as fp32, all little-endian.  Records are named
+ * l_out-<layer> ([n_embd, n_seq] fp32, the residual stream after the layer).  The
+ * reference also dumps ffn_out-<layer>; here the down projection adds the residual in
+ * its own epilogue, so that tensor is never materialized.  append != 0 appends to an
+ * existing dump (the header is written when the file is empty). */
+int mi_qwen2_dump_layers(mi_qwen2 *m, const char *path, int append);
 /* byte size and dims of a named tensor (dims[0] = ne0, dims[1] = ne1); -1 if unknown */
 int64_t mi_qwen2_tensor_nbytes(mi_qwen2 *m, const char *name, int64_t *dims);
 

@@ -47,6 +47,7 @@ struct Graph {
     ggml_gallocr_t galloc = nullptr;
     ggml_tensor *logits = nullptr;
     ggml_tensor *argmax = nullptr;
+    std::vector<ggml_tensor *> l_out;  // each layer's output (the residual stream), F32 [n_embd, n_seq]
 };
 
 }  // namespace
@@ -62,6 +63,7 @@ struct mi_qwen2 {
     ggml_tensor *inp = nullptr;  // I32 [4 * n_seq]: tokens, positions, kv lengths, cache rows
     std::vector<int32_t> inp_host;
     std::map<int, Graph> graphs;  // by KV view length
+    Graph *last = nullptr;        // the graph of the latest decode step
 };
 
 namespace {
@@ -149,6 +151,8 @@ Graph build_graph(mi_qwen2 *m, int n_kv) {
         cur = ggml_swiglu_split(ctx, g, u);
         cur = ggml_mul_mat(ctx, W(m, p + "ffn_down.weight"), cur);
         inpL = ggml_add(ctx, cur, ffn_inp);
+        ggml_set_name(inpL, ("l_out-" + std::to_string(il)).c_str());  // the eval-callback name
+        G.l_out.push_back(inpL);
     }
     ggml_tensor *cur = ggml_rms_norm(ctx, inpL, hp.rms_eps);
     cur = ggml_mul(ctx, cur, W(m, "output_norm.weight"));
@@ -298,6 +302,65 @@ int mi_qwen2_set_smooth(mi_qwen2 *m, const char *weight_name, const float *s, in
     return 0;
 }
 
+int mi_smooth_scales_read(const char *path, int64_t n_layer, int64_t n_embd, float *out) {
+    if (!path || !out || n_layer <= 0 || n_embd <= 0) return fail("smooth scales: bad arguments");
+    FILE *f = fopen(path, "rb");
+    if (!f) return fail("smooth scales: cannot open %s", path);
+    const size_t want = (size_t)n_layer * (size_t)n_embd;
+    long size = -1;
+    if (fseek(f, 0, SEEK_END) == 0) size = ftell(f);
+    if (size != (long)(want * sizeof(float))) {
+        fclose(f);
+        return fail("smooth scales: %s holds %ld bytes, expected %zu (fp32 [%lld layers][%lld])", path, size,
+                    want * sizeof(float), (long long)n_layer, (long long)n_embd);
+    }
+    rewind(f);
+    const size_t got = fread(out, sizeof(float), want, f);  // little-endian fp32, as the file is written
+    fclose(f);
+    if (got != want) return fail("smooth scales: short read of %s", path);
+    for (size_t i = 0; i < want; i++)
+        if (!(out[i] > 0.0f) || !isfinite(out[i]))
+            return fail("smooth scales: entry %zu (layer %zu, channel %zu) is %g, not a positive finite factor", i,
+                        i / (size_t)n_embd, i % (size_t)n_embd, (double)out[i]);
+    return 0;
+}
+
+int mi_qwen2_load_smooth_file(mi_qwen2 *m, const char *path) {
+    const int64_t L = m->hp.n_layer, E = m->hp.n_embd;
+    std::vector<float> s((size_t)(L * E));
+    if (int r = mi_smooth_scales_read(path, L, E, s.data())) return r;
+    for (int64_t il = 0; il < L; il++)
+        for (const char *w : {"ffn_gate", "ffn_up"}) {
+            const std::string name = "blk." + std::to_string(il) + "." + w + ".weight";
+            if (int r = mi_qwen2_set_smooth(m, name.c_str(), s.data() + il * E, E)) return r;
+        }
+    return 0;
+}
+
+int mi_qwen2_dump_layers(mi_qwen2 *m, const char *path, int append) {
+    if (!path) return fail("qwen2: layer dump path is NULL");
+    if (!m->last) return fail("qwen2: no decode step to dump");
+    FILE *f = fopen(path, append ? "ab" : "wb");
+    if (!f) return fail("qwen2: cannot open layer dump %s", path);
+    bool ok = fseek(f, 0, SEEK_END) == 0;
+    const long at = ok ? ftell(f) : -1;
+    static const char magic[8] = {'L', 'L', 'D', 'U', 'M', 'P', '1', '\0'};
+    if (at == 0) ok = fwrite(magic, 1, 8, f) == 8;
+    else ok = ok && at >= 8;  // appending to a file that must already hold the header
+    std::vector<float> v;
+    for (size_t i = 0; ok && i < m->last->l_out.size(); i++) {
+        ggml_tensor *t = m->last->l_out[i];
+        const uint64_t n = (uint64_t)ggml_nelements(t);
+        const uint16_t nl = (uint16_t)strlen(t->name);
+        v.resize(n);
+        ggml_backend_tensor_get(t, v.data(), 0, n * sizeof(float));
+        ok = fwrite(&nl, sizeof nl, 1, f) == 1 && fwrite(t->name, 1, nl, f) == nl && fwrite(&n, sizeof n, 1, f) == 1 &&
+             fwrite(v.data(), sizeof(float), n, f) == n;
+    }
+    ok = (fclose(f) == 0) && ok;
+    return ok ? 0 : fail("qwen2: writing layer dump %s failed", path);
+}
+
 int mi_qwen2_decode_batch(mi_qwen2 *m, const int32_t *tokens, const int32_t *pos, int32_t *next_tokens,
                           float *logits) {
     const int S = m->n_seq;
@@ -319,6 +382,7 @@ int mi_qwen2_decode_batch(mi_qwen2 *m, const int32_t *tokens, const int32_t *pos
     }
     ggml_backend_tensor_set(m->inp, m->inp_host.data(), 0, m->inp_host.size() * sizeof(int32_t));
     if (ggml_backend_graph_compute(m->backend, G.gf) != GGML_STATUS_SUCCESS) return fail("qwen2: graph failed");
+    m->last = &G;
     if (next_tokens) ggml_backend_tensor_get(G.argmax, next_tokens, 0, (size_t)S * sizeof(int32_t));
     if (logits) ggml_backend_tensor_get(G.logits, logits, 0, ggml_nbytes(G.logits));
     return 0;

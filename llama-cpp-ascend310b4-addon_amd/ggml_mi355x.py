@@ -440,8 +440,20 @@ _QWEN_SIGS = {
     "mi_qwen2_fill_cache": (_I, [_P, ctypes.c_int32, ctypes.c_uint64, ctypes.c_float]),
     "mi_qwen2_get_cache": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, _SZ]),
     "mi_qwen2_reset": (_I, [_P]),
+    "mi_smooth_scales_read": (_I, [ctypes.c_char_p, _I64, _I64, _P]),
+    "mi_qwen2_load_smooth_file": (_I, [_P, ctypes.c_char_p]),
+    "mi_qwen2_dump_layers": (_I, [_P, ctypes.c_char_p, _I]),
 }
 EXPORTED = EXPORTED + tuple(_QWEN_SIGS)
+
+
+def read_smooth_scales(path, n_layer, n_embd):
+    """Host-side read of a SmoothQuant scale file through the library's own parser."""
+    out = np.empty((n_layer, n_embd), np.float32)
+    r = _qlib().mi_smooth_scales_read(str(path).encode(), n_layer, n_embd, out.ctypes.data)
+    if r != 0:
+        raise MiError("mi_smooth_scales_read", r, _qlib().mi_qwen2_last_error().decode())
+    return out
 
 
 def _qlib():
@@ -483,6 +495,16 @@ class Qwen2Model:
         s = np.ascontiguousarray(s, np.float32)
         self._chk("mi_qwen2_set_smooth", _qlib().mi_qwen2_set_smooth(self.ptr, weight_name.encode(), s.ctypes.data,
                                                                     s.size))
+
+    def load_smooth_file(self, path):
+        """SmoothQuant factors of every layer's ffn_gate / ffn_up from a scale file
+        (little-endian fp32 [n_layer][n_embd])."""
+        self._chk("mi_qwen2_load_smooth_file", _qlib().mi_qwen2_load_smooth_file(self.ptr, str(path).encode()))
+
+    def dump_layers(self, path, append=False):
+        """The latest step's l_out-<layer> tensors as LLDUMP1 records (see lldump.py)."""
+        self._chk("mi_qwen2_dump_layers", _qlib().mi_qwen2_dump_layers(self.ptr, str(path).encode(),
+                                                                      1 if append else 0))
 
     def load(self, tensors, smooth=None):
         for name, arr in tensors.items():

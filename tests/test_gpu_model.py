@@ -14,6 +14,7 @@ measured in the test by running the CPU model both ways.
 import numpy as np
 import pytest
 
+import lldump
 import qwen2_synth as qs
 
 pytestmark = pytest.mark.gpu
@@ -235,3 +236,49 @@ def test_qwen2_batch_of_sequences(gpu, orc, wtype):
           f"{worst:.3e} (ggml SIMD/generic spread {spread:.3e}), greedy mismatches {mism}/{n_seq * (n_gen + 1)}")
     assert worst < _bar(spread)
     assert mism == 0
+
+
+def test_smooth_scale_file_and_layer_dump(gpu, tmp_path):
+    """A SmoothQuant scale file (fp32 [layers, hidden], the scale tool's format) gives the
+    same logits as the per-weight factors; the LLDUMP1 dump holds every layer's output per
+    step, and the last layer's output through the output norm and the tied head gives the
+    logits the step returned."""
+    mi = gpu
+    hp = qs.qwen2_1p5b(n_layer=2, n_ctx=64, wtype=qs.GGML_TYPE_Q8_0)
+    tensors, smooth = qs.synth(hp, seed=41)
+    L, E = hp["n_layer"], hp["n_embd"]
+    sq = np.stack([smooth[f"blk.{i}.ffn_gate.weight"] for i in range(L)]).astype("<f4")
+    assert all(np.array_equal(smooth[f"blk.{i}.ffn_up.weight"], sq[i]) for i in range(L))
+    sq_path = tmp_path / "sq-scales-a05.bin"
+    sq.tofile(sq_path)
+    a = mi.Qwen2Model(hp)
+    a.load(tensors, smooth)
+    b = mi.Qwen2Model(hp)
+    b.load(tensors, {k: v for k, v in smooth.items() if ".ffn_gate." not in k and ".ffn_up." not in k})
+    b.load_smooth_file(sq_path)
+    with pytest.raises(mi.MiError, match="no decode step"):
+        a.dump_layers(tmp_path / "early.bin")
+    dump = tmp_path / "layers.bin"
+    rng = np.random.default_rng(42)
+    for pos in range(6):
+        t = int(rng.integers(0, hp["n_vocab"]))
+        ta, la = a.decode(t, pos, want_logits=True)
+        tb, lb = b.decode(t, pos, want_logits=True)
+        assert ta == tb and np.array_equal(la, lb), f"position {pos}"
+        b.dump_layers(dump, append=pos > 0)
+    d = lldump.read_dump(dump)
+    assert sorted(d) == [f"l_out-{i}" for i in range(L)]
+    assert all(len(v) == 6 and all(r.size == E and np.isfinite(r).all() for r in v) for v in d.values())
+    x = d[f"l_out-{L - 1}"][-1].astype(np.float64)
+    xn = x / np.sqrt(np.mean(x * x) + hp["rms_eps"]) * tensors["output_norm.weight"]
+    head = tensors["token_embd.weight"].view(np.float16).astype(np.float64).reshape(hp["n_vocab"], E)
+    ref = head @ xn
+    err = float(np.abs(lb - ref).max() / np.abs(ref).max())
+    print(f"logits from the dumped l_out-{L - 1}: max rel {err:.2e}")
+    assert err < 2e-3
+    a.dump_layers(tmp_path / "a.bin")
+    rows = lldump.compare(lldump.read_dump(tmp_path / "a.bin"), {k: v[-1:] for k, v in d.items()})
+    assert [r[1] for r in rows] == [f"l_out-{i}" for i in range(L)]
+    assert all(r[3] == pytest.approx(1.0) and r[4] == 0.0 for r in rows)
+    a.free()
+    b.free()
