@@ -87,6 +87,17 @@ int mi_prepack_q8_0_host(const void *src_blocks, void *dst_packed, int64_t n, in
 int mi_prepack_q4_0_host(const void *src_blocks, void *dst_packed, int64_t n, int64_t k);
 int mi_unpack_q8_0_host(const void *packed, void *dst_blocks, int64_t n, int64_t k);
 int mi_unpack_q4_0_host(const void *packed, void *dst_blocks, int64_t n, int64_t k);
+/* A8W8 weight quantization at upload (replaces ggml_backend_cann_transform_f16_a8w8,
+ * patch:1674-1695, run by set_tensor at patch:1716-1751 for the weights
+ * ggml_cann_310b_is_a8w8_weight selects, patch:1520-1533).  An F16 weight [n][k] (ggml
+ * rows, k contiguous) times the SmoothQuant factors s[k] (fp32, NULL = none) is quantized
+ * per 32-block to Q8_0 with quantize_row_q8_0_ref's rounding (d = amax/127 stored fp16,
+ * q = round-half-away(v/d)) and written in the Q8_0 packed layout above.  The reference
+ * quantizes per output channel into FRACTAL_NZ int8; here the A8W8 weight format is ggml
+ * Q8_0, so the same GEMVs serve quantized GGUFs and F16 GGUFs quantized at load.
+ * w_f16 8-byte aligned, s 16-byte aligned, dst 256-byte aligned. */
+int mi_quantize_f16_q8_0(void *stream, const uint16_t *w_f16, const float *s, void *dst_packed, int64_t n,
+                         int64_t k);
 
 /* ------------------------------------------------------------------------
  * Activation quantization (replaces aclnnW8a8QuantizeCustom,

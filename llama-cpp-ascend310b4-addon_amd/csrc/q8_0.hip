@@ -57,6 +57,43 @@ __global__ void k_prepack_q8_0(const uint8_t *__restrict__ src, uint8_t *__restr
     dpl[i] = w[0];
 }
 
+// ------------------------------------------------------------------ A8W8 weight quantization
+
+// An F16 weight [n][k] (the ggml rows the loader wrote) times the SmoothQuant factors
+// s[k] (NULL = none), quantized per 32-block to Q8_0 with ggml's quantize_row_q8_0_ref
+// rounding (what llama-quantize writes for Q8_0 weights), straight into the planar side
+// copy.  8 lanes per block, 4 values per lane: lanes 0..3 fill the qlo plane's 16 bytes,
+// lanes 4..7 the qhi plane's.  grid: ceil(n*nb / 32) x 256.
+__device__ __forceinline__ uint32_t quant4(float v0, float v1, float v2, float v3, int rounding, float &d);
+
+__global__ __launch_bounds__(256) void k_quantize_f16_q8_0(const uint16_t *__restrict__ w, const float *__restrict__ s,
+                                                           uint8_t *__restrict__ qlo, uint8_t *__restrict__ qhi,
+                                                           uint16_t *__restrict__ dpl, int64_t k,
+                                                           int64_t total_blocks) {
+    const int64_t blk = (int64_t)blockIdx.x * 32 + threadIdx.x / 8;
+    const int sub = threadIdx.x % 8;
+    const bool valid = blk < total_blocks;
+    const int64_t nb = k / QK;
+    const int64_t b = valid ? blk % nb : 0;
+    float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
+    if (valid) {
+        // block blk starts at element blk*32 of the row-major [n][k] weight
+        const uint2 h = *(const uint2 *)(w + blk * QK + sub * 4);
+        v0 = h2f((uint16_t)(h.x & 0xffff)); v1 = h2f((uint16_t)(h.x >> 16));
+        v2 = h2f((uint16_t)(h.y & 0xffff)); v3 = h2f((uint16_t)(h.y >> 16));
+        if (s) {
+            const float4 sv = *(const float4 *)(s + b * QK + sub * 4);
+            v0 *= sv.x; v1 *= sv.y; v2 *= sv.z; v3 *= sv.w;
+        }
+    }
+    float d;
+    const uint32_t q = quant4(v0, v1, v2, v3, MI_Q8_ROUND_REF, d);
+    if (valid) {
+        *(uint32_t *)((sub < 4 ? qlo : qhi) + blk * 16 + (sub & 3) * 4) = q;
+        if (sub == 0) dpl[blk] = f2h(d);
+    }
+}
+
 // ------------------------------------------------------------------ activation quant
 
 // 8 lanes per 32-block, 4 consecutive values per lane.  Returns the 4 int8 values
@@ -561,7 +598,8 @@ __global__ __launch_bounds__(256) void k_swiglu_quant_q8_0(const float *__restri
     }
 }
 
-// exact per-block int32 dots (debug / bit-exactness check), activation row 0
+// exact per-block int32 dots (bit-exactness check), activation row 0: the same dot_block
+// every GEMV kernel above uses on the same two 16-byte weight chunks and activation halves
 __global__ void k_q8_0_block_dots(const uint8_t *__restrict__ qlo, const uint8_t *__restrict__ qhi,
                                   const int8_t *__restrict__ xq_qs, int32_t *__restrict__ out, int64_t n, int nb) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -571,16 +609,7 @@ __global__ void k_q8_0_block_dots(const uint8_t *__restrict__ qlo, const uint8_t
     const int4 hi = *(const int4 *)(qhi + i * 16);
     const int4 x0 = *(const int4 *)(xq_qs + (size_t)b * QK);
     const int4 x1 = *(const int4 *)(xq_qs + (size_t)b * QK + 16);
-    int s = 0;
-    s = __builtin_amdgcn_sdot4(lo.x, x0.x, s, false);
-    s = __builtin_amdgcn_sdot4(lo.y, x0.y, s, false);
-    s = __builtin_amdgcn_sdot4(lo.z, x0.z, s, false);
-    s = __builtin_amdgcn_sdot4(lo.w, x0.w, s, false);
-    s = __builtin_amdgcn_sdot4(hi.x, x1.x, s, false);
-    s = __builtin_amdgcn_sdot4(hi.y, x1.y, s, false);
-    s = __builtin_amdgcn_sdot4(hi.z, x1.z, s, false);
-    s = __builtin_amdgcn_sdot4(hi.w, x1.w, s, false);
-    out[i] = s;
+    out[i] = dot_block(lo, hi, x0, x1);
 }
 
 // ------------------------------------------------------------------ launch helpers
@@ -836,6 +865,21 @@ int mi_prepack_q8_0(void *stream, const void *src_blocks, void *dst_packed, int6
     hipLaunchKernelGGL(k_prepack_q8_0, dim3((unsigned)((nblocks + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                        (const uint8_t *)src_blocks, base, base + p.plane, (uint16_t *)(base + 2 * p.plane), nblocks);
     MI_CHECK_LAUNCH("k_prepack_q8_0");
+    return MI_OK;
+}
+
+int mi_quantize_f16_q8_0(void *stream, const uint16_t *w_f16, const float *s, void *dst_packed, int64_t n,
+                         int64_t k) {
+    if (int r = check_shape("quantize_f16_q8_0", n, k)) return r;
+    MI_CHECK_ARG(w_f16 && dst_packed, "quantize_f16_q8_0: null pointer");
+    MI_CHECK_ARG(mi::aligned(w_f16, 8) && mi::aligned(dst_packed, 256) && (!s || mi::aligned(s, 16)),
+                 "quantize_f16_q8_0: w must be 8-byte, s 16-byte, dst 256-byte aligned");
+    const Q8Planes p = q8_planes(n, k);
+    const int64_t nblocks = n * (k / QK);
+    uint8_t *base = (uint8_t *)dst_packed;
+    hipLaunchKernelGGL(k_quantize_f16_q8_0, dim3((unsigned)((nblocks + 31) / 32)), dim3(256), 0, (hipStream_t)stream,
+                       w_f16, s, base, base + p.plane, (uint16_t *)(base + 2 * p.plane), k, nblocks);
+    MI_CHECK_LAUNCH("k_quantize_f16_q8_0");
     return MI_OK;
 }
 

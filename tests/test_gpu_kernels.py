@@ -239,8 +239,13 @@ def _check_fa(orc, o, q, kc, vc, nkv, scale, mask=None, kv_len=None, label=""):
     e_ggml = float(np.abs(o - ggml).max())
     dev_ggml = float(np.abs(ggml - exact).max())
     print(f"fa {label}: max|gpu-exact|={e_exact:.2e} max|gpu-ggml|={e_ggml:.2e} (ggml own {dev_ggml:.2e})")
+    # The gate is the exact fp64 attention (pinned by closed forms and brute force).  The
+    # ggml-CPU restatement keeps V.softmax in an fp16 accumulator (pinned by its own KATs);
+    # its distance from the exact answer grows with L and passes 2e-3 at some lengths, so
+    # an exact kernel cannot meet a 2e-3 bar against it there.  That distance is printed,
+    # not gated: it follows from the exact gate by the triangle inequality.
     assert e_exact < 5e-5
-    assert e_ggml <= max(2e-3, dev_ggml + 2e-4)
+    assert e_ggml <= dev_ggml + 5e-5
 
 
 @pytest.mark.parametrize("L", [512, 4096, 32768])

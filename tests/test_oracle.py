@@ -310,6 +310,49 @@ def test_attention_mask_and_kv_len(orc):
     assert not orc.flash_attn_ext_1tok(q, k, v, 2, 0.1, mask=allm, mode=0).any()
 
 
+@pytest.mark.parametrize("L,expect", [(1, 1.0), (2047, 1.0), (2048, 1.0), (2049, 2048 / 2049), (4096, 0.5),
+                                      (6144, 1 / 3)])
+def test_attention_ggml_mode_fp16_accumulator_kat(orc, L, expect):
+    """Closed form of ggml-CPU's fp16 V accumulator.  q = 0 scores every position 0, so every
+    softmax weight is exactly 1 and the fp32 sum S counts the positions; with V = 1 the fp16
+    accumulator counts too, but fp16 spacing is 2 above 2048, so 2048 + 1 rounds (to even)
+    back to 2048 and the count stops there: output = min(L, 2048) / L.  An fp32 or fp64
+    accumulator would give 1.0 for every L; the exact mode must."""
+    d = 128
+    q = np.zeros((2, d), np.float32)
+    k = f16_bits(RNG(L).standard_normal((L, 1, d)))
+    v = f16_bits(np.ones((L, 1, d)))
+    o = orc.flash_attn_ext_1tok(q, k, v, 1, 1 / np.sqrt(d), mode=0)
+    assert np.all(o == np.float32(expect)), (o[0, 0], expect)
+    assert np.all(orc.flash_attn_ext_1tok(q, k, v, 1, 1 / np.sqrt(d), mode=1) == 1.0)
+
+
+def test_attention_ggml_mode_mask_rescale_kat(orc):
+    """Three positions worked by hand, scale 1, one query head, D = 2.
+    q = (1, 0); K rows (0, 0), (2, 0), (5, 0); mask (0, -1, -inf); V rows (1, 0), (0, 1), (7, 7).
+      p0: s = 0           -> M = 0, acc = V0 = (1, 0), S = 1
+      p1: s = 2 - 1 = 1   -> new max: ms = e^-1, acc = fp16(acc * ms) + V1, S = ms + 1
+      p2: masked (-inf)   -> skipped, V2 never read into the sum
+    so out = (fp16(e^-1), 1) / (1 + e^-1): the first component carries the rescaled fp16
+    accumulator (0.367919921875 = 1507 * 2^-12), the second a clean 1.  The exact answer has
+    e^-1 there instead."""
+    import math
+    q = np.array([[1.0, 0.0]], np.float32)
+    k = f16_bits([[[0.0, 0.0]], [[2.0, 0.0]], [[5.0, 0.0]]])
+    v = f16_bits([[[1.0, 0.0]], [[0.0, 1.0]], [[7.0, 7.0]]])
+    mask = f16_bits([0.0, -1.0, -np.inf])
+    ms = np.float32(math.exp(-1.0))
+    S = np.float32(ms + np.float32(1.0))
+    acc0 = np.float32(np.float16(ms))
+    assert acc0 == np.float32(1507 * 2.0 ** -12)
+    o = orc.flash_attn_ext_1tok(q, k, v, 1, 1.0, mask=mask, mode=0)
+    inv = np.float32(1.0) / S
+    assert o[0, 0] == acc0 * inv and o[0, 1] == np.float32(1.0) * inv, o
+    ex = orc.flash_attn_ext_1tok(q, k, v, 1, 1.0, mask=mask, mode=1)
+    e1 = math.exp(-1.0)
+    assert abs(ex[0, 0] - e1 / (1 + e1)) < 1e-7 and abs(ex[0, 1] - 1 / (1 + e1)) < 1e-7
+
+
 def test_attention_ggml_mode_error_and_simd(orc):
     """The ggml-CPU restatement keeps the V accumulator in fp16 (ggml_vec_mad_f16); its distance
     to the exact answer is what bounds the achievable GPU-vs-ggml agreement."""
