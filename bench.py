@@ -20,6 +20,17 @@ Prints ONE JSON line.  Phases:
      steps and decodes from the same token and position, timed for ~15 s or K steps;
      its greedy tokens are compared with the GPU's timed tokens.
 
+  4. configs: every other workload measured in the same run, each HBM-cold (rotating
+     through copies of its weights or KV cache, more than 2x the 256 MB MALL) with live
+     HIP-event timing, next to the same operation of the ggml-CPU restatement on the
+     host's cores (median of 20 runs after warm-up):
+       C1 the A8W8 Q8_0 GEMV 8960 x 1536 (activation quantization fused),
+       C2 the W4A16 Q4_0 GEMV 1536 x 8960 on an fp16 row,
+       C3 the GQA flash-decoding 12q/2kv D=128 at L = 512, 4096, 32768 (split + combine),
+       C5 the Qwen2.5-7B-shaped W4A16 decode at a 32768-position context, 128 timed
+          tokens at batch 1 and at batch 8, with the attention's KV-read rate.
+     --quick skips this leg.
+
 Synthetic data: random weights of the Qwen2.5-1.5B shape (28 layers, hidden 1536,
 12 q / 2 kv heads of dim 128, FFN 8960, vocab 151936, fp16 tied head), SmoothQuant
 factors uniform in [0.5, 2] (no checkpoints exist offline).
@@ -40,6 +51,157 @@ HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 << 20
 PREFILL = 512
 SEED = 1234
+
+
+T_START = time.perf_counter()
+
+
+def log(msg):
+    """progress on stderr (stdout carries only the JSON line)"""
+    print(f"[bench {time.perf_counter() - T_START:6.1f} s] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_threads():
+    return min(16, os.cpu_count() or 1)
+
+
+def host_info(orc, threads):
+    model = "?"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"threads": threads, "nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+            "cpu_model": model, "isa": orc.simd_isa(),
+            "pinning": "none: OpenMP default placement (OMP_NUM_THREADS=%s)" % os.environ.get("OMP_NUM_THREADS", "unset")}
+
+
+def cold_launch_us(mi, st, launch, n_launches, plug):
+    """average us per launch of launch(i), i = 0..n_launches-1, issued back to back behind a
+    4 GiB device copy (the GPU is busy while they queue up, so they run back to back
+    whatever the host's launch rate); HIP events on the launch stream; median of 3"""
+    e0, e1 = mi.Event(), mi.Event()
+    samples = []
+    for _ in range(3):
+        for _ in range(2):
+            mi._call("mi_memcpy_d2d", mi._P(plug[1].ptr), mi._P(plug[0].ptr), 2 << 30, mi._P(st.ptr))
+        e0.record(st.ptr)
+        for i in range(n_launches):
+            launch(i)
+        e1.record(st.ptr)
+        st.sync()
+        samples.append(e0.elapsed_ms(e1) * 1e3 / n_launches)
+    return float(np.median(samples))
+
+
+def cpu_median_us(fn, reps=20, warm=3):
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)) * 1e6
+
+
+def _rate(algo, us):
+    return {"us": round(us, 3), "algorithmic_bytes": algo, "GBps": round(algo / us / 1e3, 1),
+            "frac": round(algo / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def measure_c1(mi, qs, orc, rng, st, plug, threads):
+    """A8W8 Q8_0 GEMV N=8960 x K=1536, one fp32 row quantized in the kernel's prologue"""
+    n, k = 8960, 1536
+    blocks = qs.q8_0_rows(rng, n, k)
+    psz = mi.q8_0_packed_size(n, k)
+    copies = int(np.ceil(2 * MALL_BYTES / psz)) + 1
+    src = mi.to_device(blocks)
+    big = mi.DeviceBuffer(copies * psz)
+    for c in range(copies):
+        mi.prepack_q8_0(src.ptr, big.ptr + c * psz, n, k, stream=st.ptr)
+    x = rng.standard_normal(k).astype(np.float32)
+    dx, dy = mi.to_device(x), mi.DeviceBuffer(n * 4)
+    fn = mi.lib().mi_mul_mat_q8_0_f32
+    args = [(mi._P(st.ptr), mi._P(big.ptr + c * psz), mi._P(dx.ptr), None, mi._P(dy.ptr), n, k, 1, mi.Q8_ROUND_X86,
+             None, 0) for c in range(copies)]
+    us = cold_launch_us(mi, st, lambda i: fn(*args[i % copies]), 4 * copies, plug)
+    cpu_us = cpu_median_us(lambda: orc.mul_mat_q8_0_mt(blocks, x, n, k, n_threads=threads))
+    for b in (src, big, dx, dy):
+        b.free()
+    return dict(_rate(n * k // 32 * 34 + k * 4 + n * 4, us), kernel="k_gemv_q8_0_fused1 (act-quant fused, 1 launch)",
+                shape=f"Q8_0 {n}x{k}, fp32 row", cpu_us=round(cpu_us, 1), weight_copies=copies)
+
+
+def measure_c2(mi, qs, orc, rng, st, plug, threads):
+    """W4A16 Q4_0 GEMV N=1536 x K=8960 on an fp16 activation row"""
+    n, k = 1536, 8960
+    blocks = qs.q4_0_rows(rng, n, k)
+    psz = mi.q4_0_packed_size(n, k)
+    copies = int(np.ceil(2 * MALL_BYTES / psz)) + 1
+    src = mi.to_device(blocks)
+    big = mi.DeviceBuffer(copies * psz)
+    for c in range(copies):
+        mi.prepack_q4_0(src.ptr, big.ptr + c * psz, n, k, stream=st.ptr)
+    x16 = rng.standard_normal(k).astype(np.float32).astype(np.float16).view(np.uint16)
+    dx, dy = mi.to_device(x16), mi.DeviceBuffer(n * 4)
+    fn = mi.lib().mi_gemv_q4_0_f16
+    args = [(mi._P(st.ptr), mi._P(big.ptr + c * psz), mi._P(dx.ptr), mi._P(dy.ptr), n, k, 1) for c in range(copies)]
+    us = cold_launch_us(mi, st, lambda i: fn(*args[i % copies]), 4 * copies, plug)
+    cpu_us = cpu_median_us(lambda: orc.mul_mat_q4_0_f16_mt(blocks, x16, n, k, n_threads=threads))
+    for b in (src, big, dx, dy):
+        b.free()
+    return dict(_rate(n * k // 32 * 18 + k * 2 + n * 4, us), kernel="k_gemv_q4_0_gx", shape=f"Q4_0 {n}x{k}, fp16 row",
+                cpu_us=round(cpu_us, 1), weight_copies=copies)
+
+
+def measure_c3(mi, orc, rng, st, plug, threads, L):
+    """GQA decode attention 12q/2kv D=128 over an fp16 KV cache of L positions (split + combine)"""
+    nq, nkv, d = 12, 2, 128
+    row = nkv * d * 2
+    kvb = L * row
+    copies = max(2, int(np.ceil(2 * MALL_BYTES / (2 * kvb))) + 1)
+    kbig, vbig = mi.DeviceBuffer(copies * kvb), mi.DeviceBuffer(copies * kvb)
+    for b, sd in ((kbig, 11), (vbig, 12)):
+        mi._call("mi_fill_f16_uniform", mi._P(st.ptr), mi._P(b.ptr), copies * L, nkv * d, row, ctypes.c_uint64(sd),
+                 ctypes.c_float(1.0))
+    q = rng.standard_normal((nq, d)).astype(np.float32)
+    dq, out = mi.to_device(q), mi.DeviceBuffer(nq * d * 4)
+    wsb = mi.fa_decode_workspace_size(L, nq, nkv, d)
+    ws = mi.DeviceBuffer(wsb).zero(stream=st.ptr)
+    fn = mi.lib().mi_fa_decode
+    scale = ctypes.c_float(1.0 / np.sqrt(d))
+    args = [(mi._P(st.ptr), mi._P(dq.ptr), mi._P(kbig.ptr + c * kvb), mi._P(vbig.ptr + c * kvb), None, None, L, nq, nkv,
+             d, row, d * 2, row, d * 2, scale, mi._P(out.ptr), mi._P(ws.ptr), wsb) for c in range(copies)]
+    us = cold_launch_us(mi, st, lambda i: fn(*args[i % copies]), 4 * copies, plug)
+    kc = rng.standard_normal((L, nkv, d)).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((L, nkv, d)).astype(np.float16).view(np.uint16)
+    cpu_us = cpu_median_us(lambda: orc.flash_attn_ext_1tok(q, kc, vc, nkv, 1.0 / np.sqrt(d), n_threads=threads))
+    for b in (kbig, vbig, dq, out, ws):
+        b.free()
+    return dict(_rate(2 * kvb + 2 * nq * d * 4, us), kernel="k_fa_mfma + k_fa_combine",
+                shape=f"12q/2kv D=128, L={L}", cpu_us=round(cpu_us, 1), kv_copies=copies)
+
+
+def measure_configs(mi, qs, orc, threads):
+    rng = np.random.default_rng(SEED + 7)
+    st = mi.Stream()
+    plug = (mi.DeviceBuffer(2 << 30), mi.DeviceBuffer(2 << 30))
+    out = {"C1": measure_c1(mi, qs, orc, rng, st, plug, threads)}
+    log("C1 done")
+    out["C2"] = measure_c2(mi, qs, orc, rng, st, plug, threads)
+    log("C2 done")
+    for L in (512, 4096, 32768):
+        out[f"C3_L{L}"] = measure_c3(mi, orc, rng, st, plug, threads, L)
+        log(f"C3 L={L} done")
+    for b in plug:
+        b.free()
+    st.destroy()
+    return out
 
 
 def measure_roofline(mi, qs, hp, rng):
@@ -92,41 +254,58 @@ def measure_roofline(mi, qs, hp, rng):
         b.free()
     st.destroy()
     achieved = algo / avg_us / 1e3
-    traffic = None
+    # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes over
+    # `bench.py --roofline-only` (counters cannot be read from inside this process); used
+    # only while the counted kernel is the one timed here
+    kernel = "k_gemv_q8_0_fused1<16,3,2,true>"
+    traffic, source = None, None
     tpath = os.path.join(ROOT, "profiles", "traffic_gate_up_q8_0.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
-    return {"kernel": "k_gemv_q8_0_fused1<16,3,2,true>: the gate+up launch of every layer (RMSNorm*w, SmoothQuant "
+            t = json.load(f)
+        if t.get("kernel", "").replace(" ", "") == kernel:
+            traffic = t.get("hbm_bytes_per_launch")
+            source = "profiles/traffic_gate_up_q8_0.md (rocprofv3 --pmc of this kernel, " + t.get("measured", "?") + ")"
+    return {"kernel": kernel + ": the gate+up launch of every layer (RMSNorm*w, SmoothQuant "
                       "and Q8_0 act-quant fused; 2 x Q8_0 8960x1536), HBM-cold", "bound": "hbm",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "avg_us": round(avg_us, 3),
-            "algorithmic_bytes": algo, "launches": launches, "weight_copies": copies}
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": source,
+            "avg_us": round(avg_us, 3), "algorithmic_bytes": algo, "launches": launches, "weight_copies": copies}
 
 
 def cpu_baseline(qs, hp, tensors, smooth, model, token, pos, gpu_tokens, budget_s=15.0):
+    """the ggml-CPU restatement decoding from the GPU's KV cache at `pos`, timed; then the
+    GPU re-decodes the CPU's steps (same input tokens, same positions) for the logit error"""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
-    threads = min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     cpu = orc.Qwen2(hp, tensors, smooth, fa_mode=0, n_threads=threads)
     for il in range(hp["n_layer"]):
         cpu.k_cache[il, :pos] = model.get_cache(il, 0, pos)
         cpu.v_cache[il, :pos] = model.get_cache(il, 1, pos)
-    toks = []
+    toks, inputs, logits = [], [], []
     t0 = time.perf_counter()
     nxt = token
     for i in range(len(gpu_tokens)):
-        nxt, _ = cpu.decode(nxt, pos + i)
+        inputs.append(nxt)
+        nxt, lg = cpu.decode(nxt, pos + i)
         toks.append(nxt)
+        logits.append(lg)
         if time.perf_counter() - t0 >= budget_s:
             break
     el = time.perf_counter() - t0
+    err = rel = 0.0
+    for i, (t, lc) in enumerate(zip(inputs, logits)):
+        _, lg = model.decode(t, pos + i, want_logits=True)
+        err = max(err, float(np.abs(lg - lc).max()))
+        rel = max(rel, float(np.abs(lg - lc).max() / np.abs(lc).max()))
     agree = int(np.sum(np.asarray(toks) == np.asarray(gpu_tokens[:len(toks)])))
     first_diff = next((i for i, (a, b) in enumerate(zip(toks, gpu_tokens)) if a != b), None)
     return {"value": round(len(toks) / el, 3), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{len(toks)} greedy decode steps of the same model from the GPU's KV cache at position {pos} "
                       f"(ggml-CPU restatement in oracle/, {orc.simd_isa()}, {threads} threads, {el:.1f} s)",
-            "greedy_agreement": f"{agree}/{len(toks)}", "first_divergence": first_diff}
+            "greedy_agreement": f"{agree}/{len(toks)}", "first_divergence": first_diff,
+            "logit_max_abs": round(err, 6), "logit_max_rel": round(rel, 6), "host": host_info(orc, threads)}
 
 
 def measure_fa(mi, hp, n_seq, n_kv, rng):
@@ -174,18 +353,14 @@ def measure_fa(mi, hp, n_seq, n_kv, rng):
             "frac": round(algo / us / 1e3 / HBM_PEAK_GBS, 4), "bound": "hbm"}
 
 
-def run_7b(args, mi, qs):
-    """Qwen2.5-7B-shaped W4A16 decode at a 32768-position context, bs = --batch sequences"""
-    S = args.batch
-    n_ctx = 32768
-    warm = max(args.warmup, 1)
-    hp = qs.qwen2_7b(n_ctx=n_ctx, n_seq=S)
-    tensors, _ = qs.synth(hp, seed=SEED)
+def decode_7b(mi, qs, hp, tensors, steps, warm):
+    """one Qwen2.5-7B-shaped W4A16 model of hp["n_seq"] sequences: every sequence's KV cache
+    filled on the device to n_ctx - steps - warm positions, warm untimed then `steps`
+    timed greedy steps -> (seconds, first position, model)"""
+    S = hp["n_seq"]
     model = mi.Qwen2Model(hp)
     model.load(tensors)
-    weight_bytes = qs.weight_bytes(hp)
-    del tensors
-    n_fill = n_ctx - args.steps - warm
+    n_fill = hp["n_ctx"] - steps - warm
     model.fill_cache(n_fill, seed=SEED, scale=1.0)
     rng = np.random.default_rng(SEED + 2)
     toks = rng.integers(0, hp["n_vocab"], S).astype(np.int32)
@@ -194,26 +369,77 @@ def run_7b(args, mi, qs):
     toks, pos = wt[-1], pos + warm
     mi.device_sync()
     t0 = time.perf_counter()
-    out, _ = model.decode_steps_batch(toks, pos, args.steps)
+    model.decode_steps_batch(toks, pos, steps)
     mi.device_sync()
-    el = time.perf_counter() - t0
-    model.free()
-    kv_step = qs.kv_bytes_per_position(hp) * S * (int(pos[0]) + args.steps // 2)
+    return time.perf_counter() - t0, int(pos[0]), model
+
+
+def c5_line(mi, qs, hp, el, pos0, steps, warm, weight_bytes, fa):
+    S = hp["n_seq"]
+    kv_step = qs.kv_bytes_per_position(hp) * S * (pos0 + steps // 2)
     step_bytes = weight_bytes + kv_step
-    fa = None if args.no_roofline else measure_fa(mi, hp, S, n_ctx, rng)
+    return {"tok_s": round(S * steps / el, 2), "ms_per_step": round(el * 1e3 / steps, 4), "batch": S,
+            "steps": steps, "warmup": warm, "context": hp["n_ctx"], "bytes_per_step": step_bytes,
+            "kv_bytes_per_step": kv_step, "step_GBps": round(step_bytes * steps / el / 1e9, 1),
+            "kv_GBps_in_step": round(kv_step * steps / el / 1e9, 1),
+            "step_roofline_frac": round(step_bytes * steps / el / 1e9 / HBM_PEAK_GBS, 4), "attention": fa}
+
+
+def measure_c5(mi, qs, orc, threads, batches=(1, 8), steps=128, warm=8, cpu_steps=2):
+    """Qwen2.5-7B-shaped W4A16 decode at context 32768 for each batch size, one weight
+    synthesis shared by the models; a bounded CPU sample (cpu_steps tokens of sequence 0
+    from the same filled cache) beside batch 1"""
+    n_ctx = 32768
+    hp1 = qs.qwen2_7b(n_ctx=n_ctx, n_seq=1)
+    tensors, _ = qs.synth(hp1, seed=SEED)
+    log("7B weights synthesized")
+    wbytes = qs.weight_bytes(hp1)
+    out = {}
+    for S in batches:
+        hp = qs.qwen2_7b(n_ctx=n_ctx, n_seq=S)
+        el, pos0, model = decode_7b(mi, qs, hp, tensors, steps, warm)
+        fa = measure_fa(mi, hp, S, n_ctx, np.random.default_rng(SEED + 3))
+        line = c5_line(mi, qs, hp, el, pos0, steps, warm, wbytes, fa)
+        if S == 1 and cpu_steps > 0:
+            cpu = orc.Qwen2(hp1, tensors, None, fa_mode=0, n_threads=threads)
+            n_pos = pos0 + steps
+            for il in range(hp["n_layer"]):
+                cpu.k_cache[il, :n_pos] = model.get_cache_seq(il, 0, 0, n_pos)
+                cpu.v_cache[il, :n_pos] = model.get_cache_seq(il, 1, 0, n_pos)
+            t0 = time.perf_counter()
+            tok = 0
+            for i in range(cpu_steps):
+                tok, _ = cpu.decode(tok, n_pos + i if n_pos + i < n_ctx else n_ctx - 1)
+            el_cpu = time.perf_counter() - t0
+            line["cpu_baseline"] = {"value": round(cpu_steps / el_cpu, 3), "unit": "tok/s", "cores": threads,
+                                    "kind": "port", "sample": f"{cpu_steps} decode steps of sequence 0 at position "
+                                    f"{n_pos} (ggml-CPU restatement, {orc.simd_isa()}, {threads} threads)"}
+            del cpu
+        model.free()
+        out[f"C5_bs{S}"] = line
+        log(f"C5 bs={S}: {line['tok_s']} tok/s")
+    return out
+
+
+def run_7b(args, mi, qs):
+    """--workload qwen2-7b-w4a16: the C5 decode as the headline line, bs = --batch sequences"""
+    S = args.batch
+    warm = max(args.warmup, 1)
+    hp = qs.qwen2_7b(n_ctx=32768, n_seq=S)
+    tensors, _ = qs.synth(dict(hp, n_seq=1), seed=SEED)
+    el, pos0, model = decode_7b(mi, qs, hp, tensors, args.steps, warm)
+    model.free()
+    fa = None if args.no_roofline else measure_fa(mi, hp, S, hp["n_ctx"], np.random.default_rng(SEED + 3))
+    line = c5_line(mi, qs, hp, el, pos0, args.steps, warm, qs.weight_bytes(hp), fa)
     return {
         "metric": f"decode tok/s, Qwen2.5-7B-shape W4A16 bs={S} at context 32768",
-        "value": round(S * args.steps / el, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": warm,
-        "ms_per_step": round(el * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "value": line["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": warm,
+        "ms_per_step": line["ms_per_step"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "W4A16 (int4 g32 weights x fp16 activations, fp32 accumulate), fp16 KV and head",
         "data": "synthetic (random weights of the named shape, random KV-cache contents of the named length)",
         "config": {"workload": f"Qwen2.5-7B-shaped Q4_0 W4A16 whole-model greedy decode, {S} independent sequence(s), "
                                "28 layers, hidden 3584, 28q/4kv heads x 128, FFN 18944, vocab 152064 tied fp16 head; "
-                               f"KV cache of {int(pos[0])} positions per sequence, then the timed tokens",
-                   "batch": S, "context": n_ctx, "bytes_per_step": step_bytes, "kv_bytes_per_step": kv_step,
-                   "step_GBps": round(step_bytes * args.steps / el / 1e9, 1),
-                   "kv_GBps_in_step": round(kv_step * args.steps / el / 1e9, 1),
-                   "step_roofline_frac": round(step_bytes * args.steps / el / 1e9 / HBM_PEAK_GBS, 4)},
+                               f"KV cache of {pos0} positions per sequence, then the timed tokens", **line},
         "roofline": fa, "cpu_baseline": None,
     }
 
@@ -231,6 +457,7 @@ def main():
     ap.add_argument("--workload", default="qwen2-1.5b-a8w8", choices=["qwen2-1.5b-a8w8", "qwen2-7b-w4a16"],
                     help="qwen2-7b-w4a16: the 7B-shaped W4A16 decode at a 32K context (see --batch)")
     ap.add_argument("--batch", type=int, default=1, help="independent sequences for qwen2-7b-w4a16 (1..8)")
+    ap.add_argument("--quick", action="store_true", help="skip the configs leg (C1, C2, C3, C5)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); how the decode path "
@@ -260,6 +487,7 @@ def main():
     rng = np.random.default_rng(SEED + 1)
     prompt = rng.integers(0, hp["n_vocab"], PREFILL)
 
+    log("1.5B model loaded")
     # context: 512 tokens, one per step (untimed), then the warm-up decode steps
     nxt = 0
     for i, t in enumerate(prompt):
@@ -276,9 +504,18 @@ def main():
     tok_s = args.steps / el
     step_bytes = qs.weight_bytes(hp) + qs.kv_bytes_per_position(hp) * (pos0 + args.steps // 2)
 
+    log(f"C4 decode: {tok_s:.1f} tok/s")
     roof = None if args.no_roofline else measure_roofline(mi, qs, hp, rng)
+    log("roofline leg done")
     cpu = None if args.no_cpu else cpu_baseline(qs, hp, tensors, smooth, model, nxt, pos0, list(toks))
     model.free()
+    del tensors, smooth
+    configs = None
+    if not args.quick:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as orc
+        configs = measure_configs(mi, qs, orc, cpu_threads())
+        configs.update(measure_c5(mi, qs, orc, cpu_threads()))
 
     out = {
         "metric": "decode tok/s, Qwen2.5-1.5B-shape bs=1; GEMV HBM GB/s as % of peak",
@@ -304,6 +541,7 @@ def main():
         },
         "roofline": roof,
         "cpu_baseline": cpu,
+        "configs": configs,
     }
     print(json.dumps(out))
 

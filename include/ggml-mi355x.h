@@ -10,8 +10,11 @@
  * hot path (the 310B branch of ggml-cann, patch:1037-1986):
  *   - buffer get_alloc_size / set_tensor: Q8_0 and Q4_0 matmul weights get a
  *     planar side copy after the ggml bytes (replaces the FRACTAL_NZ / INT8-NZ side
- *     copies of patch:1535-1562, 1700-1847); F16 weights, including the tied output
- *     head, stream from their ND rows (no dual layout, patch:1451-1464);
+ *     copies of patch:1535-1562, 1700-1847); with GGML_MI355X_A8W8=1, F16 projection
+ *     weights get a Q8_0 side copy quantized on the device (patch:1472-1533,
+ *     1674-1751; GGML_MI355X_A8W8_DISABLE_LAYERS keeps listed layers F16); other F16
+ *     weights, including the tied output head, stream from their ND rows (no dual
+ *     layout, patch:1451-1464);
  *   - MUL_MAT (M <= 8) runs the A8W8 / W4A16 / F16 GEMV kernels (patch:1188-1355);
  *   - FLASH_ATTN_EXT with one query row runs split-KV GQA flash-decoding for
  *     head dims 64 and 128 and honours the I32 kv_lengths src[5]
@@ -44,13 +47,28 @@ GGML_BACKEND_API void ggml_backend_mi355x_get_device_description(int device, cha
 GGML_BACKEND_API void ggml_backend_mi355x_get_device_memory(int device, size_t *free, size_t *total);
 GGML_BACKEND_API ggml_backend_reg_t ggml_backend_mi355x_reg(void);
 
-/* SmoothQuant: the Q8_0 weight holds W*diag(s); MUL_MAT with this weight quantizes x/s
- * (x times the fp32 reciprocal of s).  Tensors sharing one s pointer of equal content
- * share the device copy.  The reference reads no scale file at run time (its interface
- * is described in tools/smoothquant/README.md); this is the runtime side of that
- * contract.  Returns false if the tensor is not a prepacked Q8_0 weight of this backend
- * or n != ne[0]. */
+/* SmoothQuant factors s[n] (n = ne[0], every s > 0 and finite) of one projection weight:
+ * MUL_MAT with this weight quantizes x/s (x times the fp32 reciprocal of s) against a
+ * Q8_0 weight that holds W*diag(s).
+ *   - F16 weight on the A8W8 path (GGML_MI355X_A8W8=1, quantized at upload, the
+ *     reference's GGML_CANN_A8W8 of patch:1472-1533): the backend folds s in itself,
+ *     re-quantizing W*diag(s) to Q8_0 on the device from the F16 bytes it keeps.
+ *   - Q8_0 weight: only the activation divisor is set; the blocks must already hold
+ *     W*diag(s) (quantized offline from the smoothed weight).
+ *   - F16 weight without a Q8_0 copy (a layer GGML_MI355X_A8W8_DISABLE_LAYERS keeps F16,
+ *     or A8W8 off): accepted, nothing changes, since (x/s) . W*diag(s) = W.x exactly.
+ * Tensors given equal factors share one device copy.  Returns false, changing nothing,
+ * for a weight of another backend's buffer, a W4A16 (Q4_0) weight, n != ne[0], or a
+ * factor that is not a positive finite number.  The reference reads the
+ * scale file of tools/smoothquant/smoothquant-make-scales.py:14-17 offline; this is the
+ * runtime side of that contract. */
 GGML_BACKEND_API bool ggml_backend_mi355x_set_smooth_factors(struct ggml_tensor *weight, const float *s, int64_t n);
+
+/* No counterpart in the reference (an integration check for dynamic loading): returns 1
+ * when the op and type ids this backend was compiled with carry the same names in the
+ * loaded ggml (ggml_op_name / ggml_type_name), else 0; msg receives a description.
+ * ggml_backend_init (GGML_BACKEND_DL builds) refuses to register on a mismatch. */
+GGML_BACKEND_API int ggml_backend_mi355x_abi_check(char *msg, size_t msg_size);
 
 #ifdef __cplusplus
 }

@@ -33,7 +33,8 @@ typedef struct mi_qwen2_hparams {
     int32_t n_ctx;      /* KV cache capacity (positions) */
     float rms_eps;
     float rope_theta;
-    int32_t wtype;      /* ggml type id of the projection weights: 8 = Q8_0, 2 = Q4_0 */
+    int32_t wtype;      /* ggml type id of the projection weights: 8 = Q8_0, 2 = Q4_0, 1 = F16 (A8W8 when the
+                         * backend runs with GGML_MI355X_A8W8=1: quantized to Q8_0 at upload, else F16 GEMVs) */
     int32_t use_bias;   /* q/k/v biases (Qwen2 has them) */
     int32_t n_seq;      /* independent sequences decoded together, 1..8 (0 = 1) */
 } mi_qwen2_hparams;
@@ -57,16 +58,23 @@ int mi_qwen2_set_smooth(mi_qwen2 *m, const char *weight_name, const float *s, in
  * Host-only; needs no device. */
 int mi_smooth_scales_read(const char *path, int64_t n_layer, int64_t n_embd, float *out);
 /* Load such a file into the model: row il is the SmoothQuant factor of blk.il.ffn_gate and
- * blk.il.ffn_up (mi_qwen2_set_smooth on each; Q8_0 weights only). */
-int mi_qwen2_load_smooth_file(mi_qwen2 *m, const char *path);
-/* Write the latest decode step's layer outputs as LLDUMP1 records, the layer-dump format of
+ * blk.il.ffn_up (mi_qwen2_set_smooth on each).  F16 weights on the A8W8 path get s folded
+ * in by the backend (W*diag(s) quantized on the device).  Q8_0 weights must already hold
+ * W*diag(s); the call refuses them unless weights_presmoothed != 0 asserts that. */
+int mi_qwen2_load_smooth_file(mi_qwen2 *m, const char *path, int weights_presmoothed);
+/* on != 0: later decode steps keep each layer's normed FFN input (ffn_norm-<layer>, the
+ * input smoothquant-collect.py:15 reads) and FFN output (ffn_out-<layer>) as graph outputs,
+ * so mi_qwen2_dump_layers can write them; the fused launches that would skip writing them
+ * give way to unfused ones for those tensors. */
+int mi_qwen2_set_layer_dump(mi_qwen2 *m, int on);
+/* Write the latest decode step's layer tensors as LLDUMP1 records, the layer-dump format of
  * the reference's llama-eval-callback (patch:825-892, enabled there by LLAMA_LAYER_DUMP,
  * patch:928): the 8-byte magic "LLDUMP1\0" once, then per tensor a u16 name length, the
- * name, a u64 value count and the values as fp32, all little-endian.  Records are named
- * l_out-<layer> ([n_embd, n_seq] fp32, the residual stream after the layer).  The
- * reference also dumps ffn_out-<layer>; here the down projection adds the residual in
- * its own epilogue, so that tensor is never materialized.  append != 0 appends to an
- * existing dump (the header is written when the file is empty). */
+ * name, a u64 value count and the values as fp32, all little-endian.  Per layer, in graph
+ * order: ffn_norm-<layer> and ffn_out-<layer> when the layer dump is on
+ * (mi_qwen2_set_layer_dump), then l_out-<layer> (the residual stream after the layer);
+ * each [n_embd, n_seq] fp32.  append != 0 appends to an existing dump (the header is
+ * written when the file is empty). */
 int mi_qwen2_dump_layers(mi_qwen2 *m, const char *path, int append);
 /* byte size and dims of a named tensor (dims[0] = ne0, dims[1] = ne1); -1 if unknown */
 int64_t mi_qwen2_tensor_nbytes(mi_qwen2 *m, const char *name, int64_t *dims);

@@ -98,22 +98,79 @@ bool is_matmul_weight(const ggml_tensor *t) {
     return false;
 }
 
-bool prepack_eligible(const ggml_tensor *t) {
-    return prepack_enabled() && (t->type == GGML_TYPE_Q8_0 || t->type == GGML_TYPE_Q4_0) && t->ne[2] == 1 &&
-           t->ne[3] == 1 && t->view_src == nullptr && t->ne[0] % 32 == 0 && is_matmul_weight(t);
+// A8W8 from F16 weights (the reference's GGML_CANN_A8W8, patch:1472-1479): F16 projection
+// weights get a Q8_0 side copy quantized at upload.  Read on every call (not cached) so a
+// process can load one model with it and one without; get_alloc_size, init_tensor and
+// set_tensor of one model load see the same environment.
+bool a8w8_enabled() { return env_flag("GGML_MI355X_A8W8", false); }
+
+// GGML_MI355X_A8W8_DISABLE_LAYERS="0-2,27": layers whose weights stay F16 (the reference's
+// GGML_CANN_A8W8_DISABLE_LAYERS, patch:1481-1518: comma-separated layers or lo-hi ranges)
+bool a8w8_layer_disabled(const char *name) {
+    const char *p = strstr(name, "blk.");
+    if (!p || !isdigit((unsigned char)p[4])) return false;
+    const long layer = strtol(p + 4, nullptr, 10);
+    const char *v = getenv("GGML_MI355X_A8W8_DISABLE_LAYERS");
+    if (!v) return false;
+    std::string s(v);
+    size_t pos = 0;
+    while (pos < s.size()) {
+        size_t end = s.find(',', pos);
+        if (end == std::string::npos) end = s.size();
+        std::string item = s.substr(pos, end - pos);
+        item.erase(std::remove(item.begin(), item.end(), ' '), item.end());
+        if (!item.empty()) {
+            char *dash = nullptr;
+            const long lo = strtol(item.c_str(), &dash, 10);
+            const long hi = (dash && *dash == '-') ? strtol(dash + 1, nullptr, 10) : lo;
+            if (layer >= lo && layer <= hi) return true;
+        }
+        pos = end + 1;
+    }
+    return false;
 }
+
+// the projection classes quantized from F16: the reference's A8W8 takes the FFN matrices
+// (patch:1520-1533); here every per-layer projection (q/k/v/o/gate/up/down), since the
+// decode's A8W8 GEMVs serve all of them.  The tied output head stays F16.
+bool is_a8w8_weight(const ggml_tensor *t) {
+    return t->type == GGML_TYPE_F16 && strncmp(t->name, "blk.", 4) == 0 && is_matmul_weight(t) && a8w8_enabled() &&
+           !a8w8_layer_disabled(t->name);
+}
+
+// The packed side-copy format of a weight (GGML_TYPE_COUNT: no side copy): Q8_0 and Q4_0
+// matmul weights are re-laid out; F16 projection weights on the A8W8 path get Q8_0.
+ggml_type side_fmt(const ggml_tensor *t) {
+    if (!prepack_enabled() || t->ne[2] != 1 || t->ne[3] != 1 || t->view_src != nullptr || t->ne[0] % 32 != 0)
+        return GGML_TYPE_COUNT;
+    if ((t->type == GGML_TYPE_Q8_0 || t->type == GGML_TYPE_Q4_0) && is_matmul_weight(t)) return t->type;
+    if (is_a8w8_weight(t)) return GGML_TYPE_Q8_0;
+    return GGML_TYPE_COUNT;
+}
+
+bool prepack_eligible(const ggml_tensor *t) { return side_fmt(t) != GGML_TYPE_COUNT; }
 
 size_t side_offset(const ggml_tensor *t) { return GGML_PAD(ggml_nbytes(t), 256); }
 
 size_t packed_size(const ggml_tensor *t) {
-    return t->type == GGML_TYPE_Q8_0 ? mi_q8_0_packed_size(t->ne[1], t->ne[0]) : mi_q4_0_packed_size(t->ne[1], t->ne[0]);
+    return side_fmt(t) == GGML_TYPE_Q8_0 ? mi_q8_0_packed_size(t->ne[1], t->ne[0])
+                                         : mi_q4_0_packed_size(t->ne[1], t->ne[0]);
 }
 
 struct TensorExtra {
     void *packed = nullptr;  // planar side copy (device)
+    ggml_type fmt = GGML_TYPE_COUNT;  // its format (Q8_0 for an F16 weight quantized at upload)
     bool ready = false;      // side copy built
     const float *inv_s = nullptr;  // SmoothQuant reciprocal factors (device), owned by the buffer
+    const float *s = nullptr;      // SmoothQuant factors folded into an F16 weight's Q8_0 copy (device)
+    std::mutex mtx;                // orders a side-copy build against a change of s
 };
+
+// the weight format the kernels see: the side copy's when there is one
+ggml_type packed_fmt(const ggml_tensor *w) {
+    const TensorExtra *ex = (const TensorExtra *)w->extra;
+    return ex ? ex->fmt : w->type;
+}
 
 struct SetTracker {
     std::mutex mtx;
@@ -140,7 +197,7 @@ struct BufferCtx {
     std::unordered_map<const ggml_tensor *, std::unique_ptr<SetTracker>> trackers;
     std::vector<std::unique_ptr<TensorExtra>> extras;
     std::vector<void *> owned;  // SmoothQuant factor copies
-    std::unordered_map<std::string, void *> inv_s_by_content;
+    std::unordered_map<std::string, void *> factors_by_content;
 };
 
 struct BackendCtx {
@@ -186,24 +243,60 @@ void *buffer_get_base(ggml_backend_buffer_t buffer) { return ((BufferCtx *)buffe
 enum ggml_status buffer_init_tensor(ggml_backend_buffer_t buffer, ggml_tensor *tensor) {
     BufferCtx *ctx = (BufferCtx *)buffer->context;
     if (tensor->view_src != nullptr) return GGML_STATUS_SUCCESS;
-    if (prepack_eligible(tensor)) {
+    const ggml_type fmt = side_fmt(tensor);
+    if (fmt != GGML_TYPE_COUNT) {
         std::lock_guard<std::mutex> lk(ctx->mtx);
         auto ex = std::make_unique<TensorExtra>();
         ex->packed = (char *)tensor->data + side_offset(tensor);
+        ex->fmt = fmt;
         tensor->extra = ex.get();
         ctx->extras.push_back(std::move(ex));
     }
     return GGML_STATUS_SUCCESS;
 }
 
-void build_side_copy(BufferCtx *ctx, ggml_tensor *tensor) {
+// Builds the side copy from the bytes at tensor->data: a re-layout of Q8_0 / Q4_0 blocks,
+// or, for an F16 weight on the A8W8 path, W*diag(s) quantized to Q8_0 on the device
+// (the reference quantizes on the host, patch:1674-1695).
+void build_side_copy_locked(BufferCtx *ctx, ggml_tensor *tensor) {
     TensorExtra *ex = (TensorExtra *)tensor->extra;
-    if (tensor->type == GGML_TYPE_Q8_0)
-        MI_K_CHECK(mi_prepack_q8_0(ctx->stream, tensor->data, ex->packed, tensor->ne[1], tensor->ne[0]));
-    else
-        MI_K_CHECK(mi_prepack_q4_0(ctx->stream, tensor->data, ex->packed, tensor->ne[1], tensor->ne[0]));
+    switch (tensor->type) {
+        case GGML_TYPE_Q8_0:
+            MI_K_CHECK(mi_prepack_q8_0(ctx->stream, tensor->data, ex->packed, tensor->ne[1], tensor->ne[0]));
+            break;
+        case GGML_TYPE_Q4_0:
+            MI_K_CHECK(mi_prepack_q4_0(ctx->stream, tensor->data, ex->packed, tensor->ne[1], tensor->ne[0]));
+            break;
+        case GGML_TYPE_F16:
+            MI_K_CHECK(mi_quantize_f16_q8_0(ctx->stream, (const uint16_t *)tensor->data, ex->s, ex->packed,
+                                            tensor->ne[1], tensor->ne[0]));
+            break;
+        default:
+            GGML_ABORT("MI355X: no side copy for %s weights", ggml_type_name(tensor->type));
+    }
     MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
     ex->ready = true;
+}
+
+void build_side_copy(BufferCtx *ctx, ggml_tensor *tensor) {
+    std::lock_guard<std::mutex> lk(((TensorExtra *)tensor->extra)->mtx);
+    build_side_copy_locked(ctx, tensor);
+}
+
+// a device copy of n fp32 factors, shared by every weight of the buffer with the same
+// contents (the q/k/v projections share one SmoothQuant vector, gate/up another)
+const float *upload_factors(BufferCtx *ctx, const float *v, int64_t n) {
+    const std::string key((const char *)v, (size_t)n * sizeof(float));
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    auto it = ctx->factors_by_content.find(key);
+    if (it != ctx->factors_by_content.end()) return (const float *)it->second;
+    set_device(ctx->device);
+    void *dev = nullptr;
+    MI_HIP_CHECK(hipMalloc(&dev, (size_t)n * sizeof(float)));
+    MI_HIP_CHECK(hipMemcpy(dev, v, (size_t)n * sizeof(float), hipMemcpyHostToDevice));
+    ctx->owned.push_back(dev);
+    ctx->factors_by_content.emplace(key, dev);
+    return (const float *)dev;
 }
 
 void buffer_set_tensor(ggml_backend_buffer_t buffer, ggml_tensor *tensor, const void *data, size_t offset,
@@ -339,12 +432,15 @@ bool supports_mul_mat(const ggml_tensor *op) {
     if (!is_f32_contig(b) || !is_f32_contig(op)) return false;
     if (b->ne[1] < 1 || b->ne[1] > 8 || b->ne[2] != 1 || b->ne[3] != 1) return false;
     if (a->ne[2] != 1 || a->ne[3] != 1) return false;
+    // the planar side copy exists only for weights of this backend's buffers (a CPU
+    // extra buffer type may hang its own data on tensor->extra)
+    const bool owned = a->extra != nullptr && a->buffer && a->buffer->buft->iface.get_alloc_size == buft_get_alloc_size;
     switch (a->type) {
         case GGML_TYPE_Q8_0:
         case GGML_TYPE_Q4_0:
-            // the planar side copy exists only for weights of this backend's buffers
-            return a->extra != nullptr && a->buffer && a->buffer->buft->iface.get_alloc_size == buft_get_alloc_size;
+            return owned;
         case GGML_TYPE_F16:
+            if (a->extra) return owned;  // quantized at upload (A8W8): the Q8_0 path
             return a->nb[0] == 2 && a->nb[1] % 16 == 0 && a->ne[0] % 8 == 0 && b->ne[0] * b->ne[1] * 2 <= 64 * 1024;
         default:
             return false;
@@ -441,10 +537,10 @@ size_t fa_ws_need(const ggml_tensor *node) {
 }
 
 size_t scratch_need(const ggml_tensor *node) {
-    if (node->op == GGML_OP_MUL_MAT && node->src[0]->type == GGML_TYPE_Q8_0)
+    if (node->op == GGML_OP_MUL_MAT && packed_fmt(node->src[0]) == GGML_TYPE_Q8_0)
         return std::max(mi_mul_mat_q8_0_workspace_size(node->src[1]->ne[1], node->src[1]->ne[0]),
                         node->src[1]->ne[1] == 1 ? mi_xq_size(1, node->src[1]->ne[0]) : (size_t)0);
-    if (node->op == GGML_OP_MUL_MAT && node->src[0]->type == GGML_TYPE_Q4_0)
+    if (node->op == GGML_OP_MUL_MAT && packed_fmt(node->src[0]) == GGML_TYPE_Q4_0)
         return mi_mul_mat_q4_0_workspace_size(node->src[1]->ne[1], node->src[1]->ne[0]);
     if (node->op == GGML_OP_ARGMAX) return mi_argmax_workspace_size(node->src[0]->ne[0], ggml_nrows(node->src[0]));
     if (node->op == GGML_OP_GLU && ggml_nrows(node) == 1) return (size_t)ggml_nelements(node) * 2;  // fp16 row
@@ -495,10 +591,10 @@ void run_mul_mat_q8_group(BackendCtx *ctx, ggml_tensor **nodes, int count) {
 void run_mul_mat(BackendCtx *ctx, ggml_tensor *node) {
     const ggml_tensor *a = node->src[0], *b = node->src[1];
     const int64_t n = a->ne[1], k = a->ne[0], m = b->ne[1];
-    switch (a->type) {
+    switch (packed_fmt(a)) {
         case GGML_TYPE_Q8_0: {
             const TensorExtra *ex = (const TensorExtra *)a->extra;
-            GGML_ASSERT(ex && ex->ready && "Q8_0 weight used before its upload completed");
+            GGML_ASSERT(ex && ex->ready && "Q8_0 / A8W8 weight used before its upload completed");
             MI_K_CHECK(mi_mul_mat_q8_0_f32(ctx->stream, ex->packed, (const float *)b->data, ex->inv_s,
                                            (float *)node->data, n, k, m, q8_rounding(), ctx->scratch,
                                            ctx->scratch_size));
@@ -575,8 +671,14 @@ bool is_view_op(const ggml_tensor *t) {
     return t->op == GGML_OP_RESHAPE || t->op == GGML_OP_VIEW || t->op == GGML_OP_PERMUTE || t->op == GGML_OP_TRANSPOSE;
 }
 
-// non-view consumers of t, looking through view nodes
+// Stands for a reader outside the graph: a tensor flagged GGML_TENSOR_FLAG_OUTPUT (such as
+// llama.cpp's result_norm, which it reads back as the embeddings) is consumed by the host
+// after the graph ran, so a fusion must still write it.
+const ggml_tensor kHostReader{};
+
+// non-view consumers of t, looking through view nodes; kHostReader for an output tensor
 void real_consumers(const Consumers &C, const ggml_tensor *t, std::vector<const ggml_tensor *> &out) {
+    if (t->flags & GGML_TENSOR_FLAG_OUTPUT) out.push_back(&kHostReader);
     auto it = C.find(t);
     if (it == C.end()) return;
     for (const ggml_tensor *c : it->second) {
@@ -629,7 +731,7 @@ bool gemv_node(const ggml_tensor *n, ggml_type t) {
     if (n->op != GGML_OP_MUL_MAT) return false;
     const ggml_tensor *a = n->src[0], *b = n->src[1];
     const TensorExtra *ex = (const TensorExtra *)a->extra;
-    return a->type == t && ex && ex->ready && b->type == GGML_TYPE_F32 && ggml_nrows(b) == 1 &&
+    return ex && ex->fmt == t && ex->ready && b->type == GGML_TYPE_F32 && ggml_nrows(b) == 1 &&
            ggml_is_contiguous(b) && aligned16(b->data) && is_f32_contig(n);
 }
 bool q8_gemv_node(const ggml_tensor *n) { return gemv_node(n, GGML_TYPE_Q8_0); }
@@ -1337,14 +1439,14 @@ int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
                 if (int used = try_fuse_q4_batch(ctx, g, i, C)) return used;
             }
             // consecutive Q8_0 GEMVs reading the same activation (q/k/v, gate/up): one grouped launch
-            if (fuse && node->src[0]->type == GGML_TYPE_Q8_0 && node->src[1]->ne[1] == 1 &&
+            if (fuse && packed_fmt(node->src[0]) == GGML_TYPE_Q8_0 && node->src[1]->ne[1] == 1 &&
                 node->src[1]->ne[0] <= 4096) {
                 ggml_tensor *grp[4] = {node};
                 int cnt = 1;
                 while (cnt < 4 && i + cnt < nn) {
                     ggml_tensor *nx = ggml_graph_node(g, i + cnt);
                     if (nx->op != GGML_OP_MUL_MAT || nx->src[1] != node->src[1] ||
-                        nx->src[0]->type != GGML_TYPE_Q8_0 || !nx->src[0]->extra ||
+                        !nx->src[0]->extra || packed_fmt(nx->src[0]) != GGML_TYPE_Q8_0 ||
                         inv_s_of(nx->src[0]) != inv_s_of(node->src[0]))
                         break;
                     grp[cnt++] = nx;
@@ -1758,29 +1860,92 @@ bool ggml_backend_is_mi355x(ggml_backend_t backend) {
 }
 
 bool ggml_backend_mi355x_set_smooth_factors(struct ggml_tensor *weight, const float *s, int64_t n) {
-    if (!weight || !weight->extra || weight->type != GGML_TYPE_Q8_0 || n != weight->ne[0] || !s) return false;
+    // only weights of this backend's buffers carry a TensorExtra (CPU extra buffer types
+    // hang their own data on tensor->extra)
+    if (!weight || !s || n != weight->ne[0] || !weight->buffer ||
+        weight->buffer->buft->iface.get_alloc_size != buft_get_alloc_size)
+        return false;
+    for (int64_t i = 0; i < n; i++)
+        if (!(s[i] > 0.0f) || !isfinite(s[i])) return false;
+    // an unquantized F16 weight (a layer kept F16, or A8W8 off): (x/s) . W*diag(s) is W.x,
+    // so there is nothing to fold in or divide by
+    if (!weight->extra) return weight->type == GGML_TYPE_F16;
+    TensorExtra *ex = (TensorExtra *)weight->extra;
+    if (ex->fmt != GGML_TYPE_Q8_0) return false;  // W4A16 quantizes no activation
     BufferCtx *bctx = (BufferCtx *)weight->buffer->context;
     std::vector<float> inv((size_t)n);
     for (int64_t i = 0; i < n; i++) inv[i] = 1.0f / s[i];
-    const std::string key((const char *)inv.data(), inv.size() * sizeof(float));
-    std::lock_guard<std::mutex> lk(bctx->mtx);
-    void *dev = nullptr;
-    auto it = bctx->inv_s_by_content.find(key);
-    if (it != bctx->inv_s_by_content.end()) {
-        dev = it->second;
-    } else {
-        set_device(bctx->device);
-        MI_HIP_CHECK(hipMalloc(&dev, inv.size() * sizeof(float)));
-        MI_HIP_CHECK(hipMemcpy(dev, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice));
-        bctx->owned.push_back(dev);
-        bctx->inv_s_by_content.emplace(key, dev);
+    const float *dev_inv = upload_factors(bctx, inv.data(), n);
+    const float *dev_s = weight->type == GGML_TYPE_F16 ? upload_factors(bctx, s, n) : nullptr;
+    std::lock_guard<std::mutex> lk(ex->mtx);
+    ex->inv_s = dev_inv;
+    if (weight->type == GGML_TYPE_F16) {
+        ex->s = dev_s;
+        if (ex->ready) build_side_copy_locked(bctx, weight);  // re-quantize W*diag(s)
     }
-    ((TensorExtra *)weight->extra)->inv_s = (const float *)dev;
     return true;
 }
 
+// The backend dispatches on enum ggml_op / ggml_type values compiled in from the ggml
+// headers it was built against.  Loaded dynamically it runs inside the host process's
+// libggml-base, whose op and type tables must give those values the same names;
+// otherwise the two were built from different ggml revisions and every id could mean
+// another op (an upstream DIV read as MUL_MAT).
+int ggml_backend_mi355x_abi_check(char *msg, size_t msg_size) {
+    struct Id {
+        bool is_op;
+        int value;
+        const char *name;
+    };
+    static const Id ids[] = {
+        {true, GGML_OP_NONE, "NONE"},         {true, GGML_OP_ADD, "ADD"},
+        {true, GGML_OP_MUL, "MUL"},           {true, GGML_OP_RMS_NORM, "RMS_NORM"},
+        {true, GGML_OP_MUL_MAT, "MUL_MAT"},   {true, GGML_OP_RESHAPE, "RESHAPE"},
+        {true, GGML_OP_VIEW, "VIEW"},         {true, GGML_OP_PERMUTE, "PERMUTE"},
+        {true, GGML_OP_TRANSPOSE, "TRANSPOSE"}, {true, GGML_OP_GET_ROWS, "GET_ROWS"},
+        {true, GGML_OP_SET_ROWS, "SET_ROWS"}, {true, GGML_OP_ROPE, "ROPE"},
+        {true, GGML_OP_FLASH_ATTN_EXT, "FLASH_ATTN_EXT"}, {true, GGML_OP_GLU, "GLU"},
+        {true, GGML_OP_ARGMAX, "ARGMAX"},
+        {false, GGML_TYPE_F32, "f32"},        {false, GGML_TYPE_F16, "f16"},
+        {false, GGML_TYPE_Q4_0, "q4_0"},      {false, GGML_TYPE_Q8_0, "q8_0"},
+        {false, GGML_TYPE_I32, "i32"},        {false, GGML_TYPE_I64, "i64"},
+    };
+    for (const Id &id : ids) {
+        const char *got = id.is_op ? ggml_op_name((enum ggml_op)id.value) : ggml_type_name((enum ggml_type)id.value);
+        if (!got || strcmp(got, id.name) != 0) {
+            if (msg && msg_size)
+                snprintf(msg, msg_size, "ggml %s id %d is %s in the loaded ggml, %s in this backend's build",
+                         id.is_op ? "op" : "type", id.value, got ? got : "(null)", id.name);
+            return 0;
+        }
+    }
+    if (msg && msg_size) snprintf(msg, msg_size, "ok: %zu op and type ids agree", sizeof(ids) / sizeof(ids[0]));
+    return 1;
+}
+
 #ifdef GGML_BACKEND_DL
-ggml_backend_reg_t ggml_backend_init(void) { return ggml_backend_mi355x_reg(); }
+// the entry points ggml's dynamic backend loader resolves (GGML_BACKEND_DL_IMPL /
+// GGML_BACKEND_DL_SCORE_IMPL of ggml-backend-impl.h)
+ggml_backend_reg_t ggml_backend_init(void) {
+    char msg[256];
+    if (!ggml_backend_mi355x_abi_check(msg, sizeof(msg))) {
+        fprintf(stderr, "MI355X: not registering: %s\n", msg);
+        return nullptr;
+    }
+    return ggml_backend_mi355x_reg();
+}
+
+// 0 (not usable) without a gfx950 device or with mismatched ggml ids
+int ggml_backend_score(void) {
+    if (!ggml_backend_mi355x_abi_check(nullptr, 0)) return 0;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    for (int i = 0; i < n; i++) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, i) == hipSuccess && strncmp(p.gcnArchName, "gfx950", 6) == 0) return 100;
+    }
+    return 0;
+}
 #endif
 
 }  // extern "C"

@@ -3,6 +3,7 @@
 // allocators a model loader and a graph runner need.
 #include "ggml-backend-impl.h"
 
+#include <stdlib.h>
 #include <string.h>
 
 #include <vector>
@@ -142,6 +143,44 @@ ggml_backend_dev_t ggml_backend_reg_dev_get(ggml_backend_reg_t reg, size_t index
 }
 void *ggml_backend_reg_get_proc_address(ggml_backend_reg_t reg, const char *name) {
     return reg->iface.get_proc_address ? reg->iface.get_proc_address(reg, name) : nullptr;
+}
+
+// ---------------------------------------------------------------- host-memory buffer type
+// (upstream's ggml_backend_cpu_buffer_type lives in ggml-base too: plain aligned host
+// memory, set/get are copies; its device is NULL)
+
+namespace {
+constexpr size_t kHostAlign = 64;
+
+void host_free_buffer(ggml_backend_buffer_t b) { free(b->context); }
+void *host_get_base(ggml_backend_buffer_t b) { return b->context; }
+void host_memset_tensor(ggml_backend_buffer_t, struct ggml_tensor *t, uint8_t v, size_t off, size_t size) {
+    memset((char *)t->data + off, v, size);
+}
+void host_set_tensor(ggml_backend_buffer_t, struct ggml_tensor *t, const void *data, size_t off, size_t size) {
+    memcpy((char *)t->data + off, data, size);
+}
+void host_get_tensor(ggml_backend_buffer_t, const struct ggml_tensor *t, void *data, size_t off, size_t size) {
+    memcpy(data, (const char *)t->data + off, size);
+}
+void host_clear(ggml_backend_buffer_t b, uint8_t v) { memset(b->context, v, b->size); }
+
+const ggml_backend_buffer_i kHostBufferIface = {host_free_buffer, host_get_base, nullptr, host_memset_tensor,
+                                                host_set_tensor, host_get_tensor, nullptr, host_clear, nullptr};
+
+const char *host_buft_name(ggml_backend_buffer_type_t) { return "CPU"; }
+ggml_backend_buffer_t host_alloc_buffer(ggml_backend_buffer_type_t buft, size_t size) {
+    void *p = aligned_alloc(kHostAlign, GGML_PAD(size ? size : 1, kHostAlign));
+    return p ? ggml_backend_buffer_init(buft, kHostBufferIface, p, size) : nullptr;
+}
+size_t host_alignment(ggml_backend_buffer_type_t) { return kHostAlign; }
+bool host_is_host(ggml_backend_buffer_type_t) { return true; }
+}  // namespace
+
+ggml_backend_buffer_type_t ggml_backend_cpu_buffer_type(void) {
+    static ggml_backend_buffer_type buft = {
+        {host_buft_name, host_alloc_buffer, host_alignment, nullptr, nullptr, host_is_host}, nullptr, nullptr};
+    return &buft;
 }
 
 // ---------------------------------------------------------------- allocation

@@ -57,6 +57,8 @@ GGML_API ggml_backend_buffer_t ggml_backend_buft_alloc_buffer(ggml_backend_buffe
 GGML_API size_t ggml_backend_buft_get_alignment(ggml_backend_buffer_type_t buft);
 GGML_API size_t ggml_backend_buft_get_alloc_size(ggml_backend_buffer_type_t buft, const struct ggml_tensor *tensor);
 GGML_API bool ggml_backend_buft_is_host(ggml_backend_buffer_type_t buft);
+/* plain host memory (the CPU backend's buffer type, part of ggml-base upstream) */
+GGML_API ggml_backend_buffer_type_t ggml_backend_cpu_buffer_type(void);
 
 /* buffers */
 GGML_API void ggml_backend_buffer_free(ggml_backend_buffer_t buffer);

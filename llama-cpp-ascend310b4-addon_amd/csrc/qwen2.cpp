@@ -48,6 +48,8 @@ struct Graph {
     ggml_tensor *logits = nullptr;
     ggml_tensor *argmax = nullptr;
     std::vector<ggml_tensor *> l_out;  // each layer's output (the residual stream), F32 [n_embd, n_seq]
+    // with the layer dump on: each layer's normed FFN input and FFN output, F32 [n_embd, n_seq]
+    std::vector<ggml_tensor *> ffn_norm, ffn_out;
 };
 
 }  // namespace
@@ -64,6 +66,7 @@ struct mi_qwen2 {
     std::vector<int32_t> inp_host;
     std::map<int, Graph> graphs;  // by KV view length
     Graph *last = nullptr;        // the graph of the latest decode step
+    bool dump = false;            // graphs keep ffn_norm-N / ffn_out-N as outputs
 };
 
 namespace {
@@ -144,12 +147,22 @@ Graph build_graph(mi_qwen2 *m, int n_kv) {
         ggml_tensor *ffn_inp = ggml_add(ctx, cur, inpL);
         cur = ggml_rms_norm(ctx, ffn_inp, hp.rms_eps);
         cur = ggml_mul(ctx, cur, W(m, p + "ffn_norm.weight"));
+        if (m->dump) {  // named as llama.cpp's graph callback names them; outputs, so no fusion skips them
+            ggml_set_name(cur, ("ffn_norm-" + std::to_string(il)).c_str());
+            ggml_set_output(cur);
+            G.ffn_norm.push_back(cur);
+        }
         ggml_tensor *g = ggml_mul_mat(ctx, W(m, p + "ffn_gate.weight"), cur);
         ggml_tensor *u = ggml_mul_mat(ctx, W(m, p + "ffn_up.weight"), cur);
         ggml_build_forward_expand(gf, g);  // gate/up adjacent
         ggml_build_forward_expand(gf, u);
         cur = ggml_swiglu_split(ctx, g, u);
         cur = ggml_mul_mat(ctx, W(m, p + "ffn_down.weight"), cur);
+        if (m->dump) {
+            ggml_set_name(cur, ("ffn_out-" + std::to_string(il)).c_str());
+            ggml_set_output(cur);
+            G.ffn_out.push_back(cur);
+        }
         inpL = ggml_add(ctx, cur, ffn_inp);
         ggml_set_name(inpL, ("l_out-" + std::to_string(il)).c_str());  // the eval-callback name
         G.l_out.push_back(inpL);
@@ -195,7 +208,8 @@ const char *mi_qwen2_last_error(void) { return g_err; }
 mi_qwen2 *mi_qwen2_create(const mi_qwen2_hparams *hp, int device) {
     if (!hp || hp->n_layer <= 0 || hp->n_embd <= 0 || hp->n_head <= 0 || hp->n_head_kv <= 0 ||
         hp->n_head % hp->n_head_kv != 0 || hp->head_dim * hp->n_head != hp->n_embd || hp->n_ctx <= 0 ||
-        hp->n_seq < 0 || hp->n_seq > 8 || (hp->wtype != GGML_TYPE_Q8_0 && hp->wtype != GGML_TYPE_Q4_0)) {
+        hp->n_seq < 0 || hp->n_seq > 8 ||
+        (hp->wtype != GGML_TYPE_Q8_0 && hp->wtype != GGML_TYPE_Q4_0 && hp->wtype != GGML_TYPE_F16)) {
         fail("qwen2: invalid hyper-parameters");
         return nullptr;
     }
@@ -325,8 +339,12 @@ int mi_smooth_scales_read(const char *path, int64_t n_layer, int64_t n_embd, flo
     return 0;
 }
 
-int mi_qwen2_load_smooth_file(mi_qwen2 *m, const char *path) {
+int mi_qwen2_load_smooth_file(mi_qwen2 *m, const char *path, int weights_presmoothed) {
     const int64_t L = m->hp.n_layer, E = m->hp.n_embd;
+    if (m->hp.wtype == GGML_TYPE_Q8_0 && !weights_presmoothed)
+        return fail("smooth scales: the Q8_0 FFN weights must already hold W*diag(s) (quantized from the smoothed "
+                    "weights); pass weights_presmoothed = 1 to assert that, or load F16 weights with "
+                    "GGML_MI355X_A8W8=1 so the backend folds s in at upload");
     std::vector<float> s((size_t)(L * E));
     if (int r = mi_smooth_scales_read(path, L, E, s.data())) return r;
     for (int64_t il = 0; il < L; il++)
@@ -334,6 +352,18 @@ int mi_qwen2_load_smooth_file(mi_qwen2 *m, const char *path) {
             const std::string name = "blk." + std::to_string(il) + "." + w + ".weight";
             if (int r = mi_qwen2_set_smooth(m, name.c_str(), s.data() + il * E, E)) return r;
         }
+    return 0;
+}
+
+int mi_qwen2_set_layer_dump(mi_qwen2 *m, int on) {
+    if (m->dump == (on != 0)) return 0;
+    m->dump = on != 0;
+    for (auto &kv : m->graphs) {  // rebuilt on demand with the new outputs
+        ggml_gallocr_free(kv.second.galloc);
+        ggml_free(kv.second.ctx);
+    }
+    m->graphs.clear();
+    m->last = nullptr;
     return 0;
 }
 
@@ -347,9 +377,15 @@ int mi_qwen2_dump_layers(mi_qwen2 *m, const char *path, int append) {
     static const char magic[8] = {'L', 'L', 'D', 'U', 'M', 'P', '1', '\0'};
     if (at == 0) ok = fwrite(magic, 1, 8, f) == 8;
     else ok = ok && at >= 8;  // appending to a file that must already hold the header
+    std::vector<ggml_tensor *> recs;  // graph order: per layer ffn_norm, ffn_out (dump mode), l_out
+    for (size_t i = 0; i < m->last->l_out.size(); i++) {
+        if (i < m->last->ffn_norm.size()) recs.push_back(m->last->ffn_norm[i]);
+        if (i < m->last->ffn_out.size()) recs.push_back(m->last->ffn_out[i]);
+        recs.push_back(m->last->l_out[i]);
+    }
     std::vector<float> v;
-    for (size_t i = 0; ok && i < m->last->l_out.size(); i++) {
-        ggml_tensor *t = m->last->l_out[i];
+    for (size_t i = 0; ok && i < recs.size(); i++) {
+        ggml_tensor *t = recs[i];
         const uint64_t n = (uint64_t)ggml_nelements(t);
         const uint16_t nl = (uint16_t)strlen(t->name);
         v.resize(n);

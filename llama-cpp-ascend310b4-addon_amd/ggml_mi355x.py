@@ -70,6 +70,7 @@ _SIGS = {
     "mi_prepack_q4_0_host": (_I, [_P, _P, _I64, _I64]),
     "mi_unpack_q8_0_host": (_I, [_P, _P, _I64, _I64]),
     "mi_unpack_q4_0_host": (_I, [_P, _P, _I64, _I64]),
+    "mi_quantize_f16_q8_0": (_I, [_P, _P, _P, _P, _I64, _I64]),
     "mi_xq_size": (_SZ, [_I64, _I64]),
     "mi_xq_d_offset": (_SZ, [_I64, _I64]),
     "mi_act_quant_q8_0": (_I, [_P, _P, _P, _I64, _I64, _P, _I]),
@@ -320,6 +321,11 @@ def unpack_q4_0_host(packed, n, k):
     return out.reshape(n, -1)
 
 
+def quantize_f16_q8_0(w_f16_dev, s_dev, dst_dev, n, k, stream=None):
+    """A8W8 weight quantization: F16 [n][k] times s[k] (None = 1) to the Q8_0 packed layout"""
+    _call("mi_quantize_f16_q8_0", _P(stream), _P(w_f16_dev), _P(s_dev), _P(dst_dev), n, k)
+
+
 def prepack_q8_0(src_dev, dst_dev, n, k, stream=None):
     _call("mi_prepack_q8_0", _P(stream), _P(src_dev), _P(dst_dev), n, k)
 
@@ -441,7 +447,8 @@ _QWEN_SIGS = {
     "mi_qwen2_get_cache": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, _SZ]),
     "mi_qwen2_reset": (_I, [_P]),
     "mi_smooth_scales_read": (_I, [ctypes.c_char_p, _I64, _I64, _P]),
-    "mi_qwen2_load_smooth_file": (_I, [_P, ctypes.c_char_p]),
+    "mi_qwen2_load_smooth_file": (_I, [_P, ctypes.c_char_p, _I]),
+    "mi_qwen2_set_layer_dump": (_I, [_P, _I]),
     "mi_qwen2_dump_layers": (_I, [_P, ctypes.c_char_p, _I]),
 }
 EXPORTED = EXPORTED + tuple(_QWEN_SIGS)
@@ -496,13 +503,21 @@ class Qwen2Model:
         self._chk("mi_qwen2_set_smooth", _qlib().mi_qwen2_set_smooth(self.ptr, weight_name.encode(), s.ctypes.data,
                                                                     s.size))
 
-    def load_smooth_file(self, path):
+    def load_smooth_file(self, path, weights_presmoothed=False):
         """SmoothQuant factors of every layer's ffn_gate / ffn_up from a scale file
-        (little-endian fp32 [n_layer][n_embd])."""
-        self._chk("mi_qwen2_load_smooth_file", _qlib().mi_qwen2_load_smooth_file(self.ptr, str(path).encode()))
+        (little-endian fp32 [n_layer][n_embd]).  F16 weights on the A8W8 path get s
+        folded in by the backend; Q8_0 weights are refused unless weights_presmoothed
+        asserts that their blocks already hold W*diag(s)."""
+        self._chk("mi_qwen2_load_smooth_file", _qlib().mi_qwen2_load_smooth_file(self.ptr, str(path).encode(),
+                                                                                1 if weights_presmoothed else 0))
+
+    def set_layer_dump(self, on=True):
+        """keep ffn_norm-<layer> / ffn_out-<layer> as graph outputs in later steps"""
+        self._chk("mi_qwen2_set_layer_dump", _qlib().mi_qwen2_set_layer_dump(self.ptr, 1 if on else 0))
 
     def dump_layers(self, path, append=False):
-        """The latest step's l_out-<layer> tensors as LLDUMP1 records (see lldump.py)."""
+        """The latest step's layer tensors as LLDUMP1 records (see lldump.py): per layer
+        ffn_norm-<layer> and ffn_out-<layer> with the layer dump on, then l_out-<layer>."""
         self._chk("mi_qwen2_dump_layers", _qlib().mi_qwen2_dump_layers(self.ptr, str(path).encode(),
                                                                       1 if append else 0))
 

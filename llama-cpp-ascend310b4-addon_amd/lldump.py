@@ -1,110 +1,165 @@
-"""LLDUMP1 layer dumps: read, write and compare.
+"""LLDUMP1 layer dumps: index, read, write and compare.
 
-The format is the layer-dump file of the reference's llama-eval-callback
-(patches/ascend310b4-llama-cpp.patch:825-892 writes it; its reader and comparison
-script are patch:2800-2890, scripts/compare-layer-dumps.py): the 8-byte magic
-b"LLDUMP1\\0", then records of a little-endian u16 name length, the UTF-8 name, a u64
-value count and that many little-endian fp32 values.  A name may repeat (one record per
-decode step); records keep their file order.
+The byte format is the layer dump of the reference's llama-eval-callback (written at
+patches/ascend310b4-llama-cpp.patch:825-892; its comparison tool is
+scripts/compare-layer-dumps.py, patch:2800-2890): the 8-byte magic b"LLDUMP1\\0", then
+records of a little-endian u16 name length, the UTF-8 name, a little-endian u64 value
+count and that many little-endian fp32 values.  A name repeats once per decode step.
 
-`compare` gives, per tensor name present in both dumps, the value count, the cosine and
-the relative L2 error of the candidate against the reference over all of that name's
-records, and for l_out-<layer> rows the growth of (1 - cosine) since the previous
-l_out row: the columns of the reference's comparison
-(layer,tensor,values,cosine,relative_l2,cumulative_error_delta).
+Design here: `LayerDump` maps the file and indexes it in one pass (per name, the byte
+offset and value count of each record); values are read as views of the mapping and
+stacked per name into one [records, values] matrix, so `agreement` takes each of its
+float64 sums (dot, both squared norms, squared difference) as a single reduction over
+the stacked pair.  `compare` emits one row per name both dumps hold, in the order the
+reference dump first wrote them (graph order: ffn_norm-N, ffn_out-N, l_out-N, ...), with
+the columns of the reference's tool: layer, tensor, values, cosine, relative_l2, and for
+l_out-<layer> rows cumulative_error_delta, the change of (1 - cosine) from the previous
+l_out row, which shows the layer where the error grows.
+
+Command line: python lldump.py REFERENCE CANDIDATE [--output FILE] prints the CSV.
 """
 
-import math
-import re
+import argparse
+import os
 import struct
 
 import numpy as np
 
 MAGIC = b"LLDUMP1\0"
+CSV_HEADER = "layer,tensor,values,cosine,relative_l2,cumulative_error_delta"
+
+
+class DumpMismatch(ValueError):
+    """The two dumps disagree on the shape of a tensor's records."""
+
+
+def _layer(name):
+    """trailing -<digits> of a callback name (l_out-12 -> 12), -1 when there is none"""
+    head, sep, tail = name.rpartition("-")
+    return int(tail) if sep and tail.isdigit() else -1
+
+
+class LayerDump:
+    """An LLDUMP1 file indexed by tensor name (records in file order)."""
+
+    def __init__(self, path):
+        self.path = str(path)
+        size = os.path.getsize(self.path)
+        self._mem = np.memmap(self.path, dtype=np.uint8, mode="r") if size else np.zeros(0, np.uint8)
+        if size < len(MAGIC) or self._mem[:len(MAGIC)].tobytes() != MAGIC:
+            raise ValueError(f"{self.path}: not an LLDUMP1 file")
+        self.index = {}     # name -> [(value byte offset, value count), ...]
+        at = len(MAGIC)
+        while at < size:
+            at = self._index_record(at, size)
+
+    def _index_record(self, at, size):
+        def need(n, what):
+            if at + n > size:
+                raise EOFError(f"{self.path}: truncated {what} at byte {at}")
+        need(2, "name length")
+        (name_len,) = struct.unpack_from("<H", self._mem, at)
+        at += 2
+        need(name_len + 8, "record header")
+        name = self._mem[at:at + name_len].tobytes().decode("utf-8")
+        (count,) = struct.unpack_from("<Q", self._mem, at + name_len)
+        at += name_len + 8
+        need(4 * count, f"values of {name}")
+        self.index.setdefault(name, []).append((at, count))
+        return at + 4 * count
+
+    @property
+    def names(self):
+        return list(self.index)
+
+    def records(self, name):
+        """the records of one name, each a float32 array (copied out of the mapping)"""
+        return [np.frombuffer(self._mem, dtype="<f4", count=n, offset=o).astype(np.float32)
+                for o, n in self.index[name]]
+
+    def matrix(self, name):
+        """[records, values] float64 stack of one name's records"""
+        return _stack(self.records(name), name)
+
+    def as_dict(self):
+        return {n: self.records(n) for n in self.index}
+
+
+def read_dump(path):
+    """-> dict name -> list of fp32 arrays (one per record, in file order)"""
+    return LayerDump(path).as_dict()
 
 
 def write_dump(path, records, append=False):
-    """records: iterable of (name, array); values are written as fp32."""
+    """records: iterable of (name, array); values are written as little-endian fp32"""
     with open(path, "ab" if append else "wb") as f:
         if f.tell() == 0:
             f.write(MAGIC)
         for name, values in records:
             raw = name.encode("utf-8")
-            v = np.ascontiguousarray(values, dtype="<f4").reshape(-1)
-            f.write(struct.pack("<H", len(raw)))
-            f.write(raw)
-            f.write(struct.pack("<Q", v.size))
-            f.write(v.tobytes())
+            v = np.ascontiguousarray(values, dtype="<f4").ravel()
+            f.write(struct.pack("<H", len(raw)) + raw + struct.pack("<Q", v.size) + v.tobytes())
 
 
-def read_dump(path):
-    """-> dict name -> list of fp32 arrays (one per record, in file order)."""
-    out = {}
-    with open(path, "rb") as f:
-        if f.read(8) != MAGIC:
-            raise ValueError(f"{path}: not an LLDUMP1 file")
-        while True:
-            head = f.read(2)
-            if not head:
-                break
-            if len(head) != 2:
-                raise EOFError(f"{path}: truncated record header")
-            (nl,) = struct.unpack("<H", head)
-            name = f.read(nl)
-            cnt = f.read(8)
-            if len(name) != nl or len(cnt) != 8:
-                raise EOFError(f"{path}: truncated record header")
-            (n,) = struct.unpack("<Q", cnt)
-            raw = f.read(4 * n)
-            if len(raw) != 4 * n:
-                raise EOFError(f"{path}: truncated values of {name.decode('utf-8', 'replace')}")
-            out.setdefault(name.decode("utf-8"), []).append(np.frombuffer(raw, dtype="<f4").astype(np.float32))
-    return out
+def _stack(recs, name="tensor"):
+    sizes = {r.size for r in recs}
+    if len(sizes) > 1:
+        raise DumpMismatch(f"{name}: records of different lengths {sorted(sizes)}")
+    return np.stack([np.asarray(r, np.float64).ravel() for r in recs]) if recs else np.zeros((0, 0))
 
 
-def layer_of(name):
-    m = re.search(r"-(\d+)$", name)
-    return int(m.group(1)) if m else -1
-
-
-def metric(ref, cand):
-    """(values, cosine, relative L2) of cand against ref over lists of records, in float64."""
-    if len(ref) != len(cand):
-        raise ValueError("record count mismatch")
-    dot = r2 = c2 = d2 = 0.0
-    count = 0
-    for a, b in zip(ref, cand):
-        if a.size != b.size:
-            raise ValueError("tensor size mismatch")
-        a = a.astype(np.float64)
-        b = b.astype(np.float64)
-        dot += float(a @ b)
-        r2 += float(a @ a)
-        c2 += float(b @ b)
-        d2 += float((b - a) @ (b - a))
-        count += a.size
-    cos = dot / math.sqrt(r2 * c2) if r2 and c2 else float("nan")
-    rel = math.sqrt(d2 / r2) if r2 else float("nan")
-    return count, cos, rel
+def agreement(ref_records, cand_records, name="tensor"):
+    """(values, cosine, relative L2 error) of the candidate against the reference, pooled
+    over every record of one tensor name; nan where a norm is zero"""
+    R, C = _stack(ref_records, name), _stack(cand_records, name)
+    if R.shape != C.shape:
+        raise DumpMismatch(f"{name}: reference holds {R.shape[0]} x {R.shape[1] if R.ndim > 1 else 0} values, "
+                           f"candidate {C.shape[0]} x {C.shape[1] if C.ndim > 1 else 0}")
+    r, c = R.ravel(), C.ravel()
+    rr, cc, rc = float(r @ r), float(c @ c), float(r @ c)
+    d = c - r
+    dd = float(d @ d)
+    cos = rc / np.sqrt(rr * cc) if rr > 0 and cc > 0 else float("nan")
+    rel = np.sqrt(dd / rr) if rr > 0 else float("nan")
+    return r.size, float(cos), float(rel)
 
 
 def compare(reference, candidate):
     """Rows (layer, name, values, cosine, relative_l2, cumulative_error_delta or None) for
-    the names both dumps hold, by layer then name."""
-    names = sorted(set(reference) & set(candidate), key=lambda n: (layer_of(n), n))
-    rows, prev = [], 0.0
-    for name in names:
-        count, cos, rel = metric(reference[name], candidate[name])
-        delta = None
-        if name.startswith("l_out-"):
-            delta = (1.0 - cos) - prev
-            prev = 1.0 - cos
-        rows.append((layer_of(name), name, count, cos, rel, delta))
-    return rows
+    the names both dumps hold, in the reference's first-write order.  reference and
+    candidate are LayerDump objects or dicts name -> list of records."""
+    ref = reference.as_dict() if isinstance(reference, LayerDump) else reference
+    cand = candidate.as_dict() if isinstance(candidate, LayerDump) else candidate
+    names = [n for n in ref if n in cand]
+    stats = [agreement(ref[n], cand[n], n) for n in names]
+    is_lout = np.array([n.startswith("l_out-") for n in names], bool)
+    err = np.array([1.0 - s[1] for s in stats], np.float64)
+    delta = np.full(len(names), np.nan)
+    delta[is_lout] = np.diff(err[is_lout], prepend=0.0)
+    return [(_layer(n), n, s[0], s[1], s[2], float(dl) if lo else None)
+            for n, s, dl, lo in zip(names, stats, delta, is_lout)]
 
 
 def format_rows(rows):
-    lines = ["layer,tensor,values,cosine,relative_l2,cumulative_error_delta"]
+    out = [CSV_HEADER]
     for layer, name, count, cos, rel, delta in rows:
-        lines.append(f"{layer},{name},{count},{cos:.9g},{rel:.9g}," + ("" if delta is None else f"{delta:.9g}"))
-    return "\n".join(lines) + "\n"
+        tail = "" if delta is None else format(delta, ".9g")
+        out.append(",".join([str(layer), name, str(count), format(cos, ".9g"), format(rel, ".9g"), tail]))
+    return "\n".join(out) + "\n"
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description="Compare two LLDUMP1 layer dumps tensor by tensor.")
+    ap.add_argument("reference")
+    ap.add_argument("candidate")
+    ap.add_argument("--output")
+    a = ap.parse_args(argv)
+    text = format_rows(compare(LayerDump(a.reference), LayerDump(a.candidate)))
+    if a.output:
+        with open(a.output, "w", encoding="utf-8") as f:
+            f.write(text)
+    print(text, end="")
+
+
+if __name__ == "__main__":
+    main()

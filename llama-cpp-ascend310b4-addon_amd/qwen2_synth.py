@@ -6,15 +6,18 @@ and laid out as ggml stores them: Q8_0 / Q4_0 block rows for the projections,
 an fp16 token embedding that doubles as the tied output head, fp32 norms and
 q/k/v biases.  Q8_0 blocks have qs uniform in [-127, 127] and
 d = fp16(|N(0, 0.02)| / 127); Q4_0 nibbles are uniform in [0, 15] with
-d = fp16(|N(0, 0.02)| / 8).  A8W8 models carry SmoothQuant factors uniform in
-[0.5, 2], one vector per projection input (q/k/v share one, gate/up share one);
-the Q8_0 blocks are taken to be the already smoothed weights W*diag(s).
+d = fp16(|N(0, 0.02)| / 8); F16 projections are N(0, 0.02).  A8W8 models carry
+SmoothQuant factors uniform in [0.5, 2], one vector per projection input (q/k/v share
+one, gate/up share one).  With Q8_0 projections the blocks are taken to be the already
+smoothed weights W*diag(s); with F16 projections the weights are the unsmoothed W and
+the backend folds s in when it quantizes them at upload (GGML_MI355X_A8W8=1).
 With random weights, attention scores are small and the softmax is nearly uniform;
 qk_gain > 1 scales the q and k projection scales so that attention is peaked and the
 logits depend on which positions it selects (RoPE angles, the GQA head map).
 """
 import numpy as np
 
+GGML_TYPE_F16 = 1
 GGML_TYPE_Q4_0 = 2
 GGML_TYPE_Q8_0 = 8
 
@@ -55,6 +58,10 @@ def q4_0_rows(rng, n, k):
     return blk.reshape(n, nb * 18)
 
 
+def f16_rows(rng, n, k):
+    return _f16(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+
+
 def projections(hp):
     """(name suffix, n_out, n_in, smoothing group) of one layer's matmul weights"""
     E, F, nkv = hp["n_embd"], hp["n_ff"], hp["n_head_kv"] * hp["head_dim"]
@@ -76,10 +83,10 @@ def synth(hp, seed=0, smooth=None, qk_gain=1.0):
     rng = np.random.default_rng(seed)
     E = hp["n_embd"]
     nkv = hp["n_head_kv"] * hp["head_dim"]
-    q8 = hp["wtype"] == GGML_TYPE_Q8_0
+    wt = hp["wtype"]
     if smooth is None:
-        smooth = q8
-    rows = q8_0_rows if q8 else q4_0_rows
+        smooth = wt in (GGML_TYPE_Q8_0, GGML_TYPE_F16)
+    rows = {GGML_TYPE_Q8_0: q8_0_rows, GGML_TYPE_Q4_0: q4_0_rows, GGML_TYPE_F16: f16_rows}[wt]
     t = {"token_embd.weight": _f16(rng.standard_normal((hp["n_vocab"], E), dtype=np.float32) * np.float32(0.02)),
          "output_norm.weight": rng.uniform(0.8, 1.2, E).astype(np.float32)}
     sm = {}
@@ -91,7 +98,12 @@ def synth(hp, seed=0, smooth=None, qk_gain=1.0):
         for name, n, k, grp in projections(hp):
             t[p + name + ".weight"] = rows(rng, n, k)
             if qk_gain != 1.0 and name in ("attn_q", "attn_k"):
-                t[p + name + ".weight"] = _scale_blocks(t[p + name + ".weight"], qk_gain, 34 if q8 else 18)
+                if wt == GGML_TYPE_F16:
+                    t[p + name + ".weight"] = _f16(t[p + name + ".weight"].view(np.float16).astype(np.float32) *
+                                                   np.float32(qk_gain))
+                else:
+                    t[p + name + ".weight"] = _scale_blocks(t[p + name + ".weight"], qk_gain,
+                                                            34 if wt == GGML_TYPE_Q8_0 else 18)
             if smooth:
                 if grp not in groups:
                     groups[grp] = rng.uniform(0.5, 2.0, k).astype(np.float32)

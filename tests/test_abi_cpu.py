@@ -88,3 +88,21 @@ def test_q4_0_prepack_roundtrip(mi, n, k):
     packed = mi.prepack_q4_0_host(w, n, k)
     assert packed.size == mi.q4_0_packed_size(n, k)
     assert np.array_equal(mi.unpack_q4_0_host(packed, n, k), w)
+
+
+def test_smooth_factors_refuse_a_foreign_weight(mi):
+    """A Q8_0 weight in another backend's buffer whose extra holds that backend's data (as
+    the CPU repack buffer types do) is not this backend's: no factors, nothing written."""
+    import ctypes
+
+    import ggml_api as ga
+    ctx = ga.Context(mi.lib())
+    L = ctx.L
+    w = ctx.tensor(ga.GGML_TYPE_Q8_0, 64, 16, name="blk.0.ffn_up.weight")
+    ctx.alloc(L.ggml_backend_cpu_buffer_type())
+    foreign = ctypes.create_string_buffer(b"\x5a" * 64)
+    w.contents.extra = ctypes.addressof(foreign)
+    s = np.full(64, 2.0, np.float32)
+    assert not L.ggml_backend_mi355x_set_smooth_factors(w, s.ctypes.data, 64)
+    assert foreign.raw[:64] == b"\x5a" * 64
+    ctx.free()

@@ -15,20 +15,35 @@ import numpy as np
 import pytest
 
 import lldump
+from synth import rel_err
 import qwen2_synth as qs
 
 pytestmark = pytest.mark.gpu
 
 
-def _run(gpu, orc, hp, n_prompt, n_gen, seed):
+def a8w8_reference(orc, hp, tensors, smooth):
+    """The CPU model of an F16 model run on the A8W8 path: every projection W (F16) with
+    its SmoothQuant factors s becomes the Q8_0 blocks of W*diag(s) by the oracle's weight
+    quantizer (quantize_row_q8_0_ref, what the backend does on the device at upload)."""
+    q = dict(tensors)
+    for il in range(hp["n_layer"]):
+        for name, n, k, _ in qs.projections(hp):
+            key = f"blk.{il}.{name}.weight"
+            w = tensors[key].view(np.float16).astype(np.float32).reshape(n, k)
+            q[key] = orc.quantize_weight_q8_0(w, smooth.get(key))
+    return dict(hp, wtype=qs.GGML_TYPE_Q8_0), q
+
+
+def _run(gpu, orc, hp, n_prompt, n_gen, seed, threads=8):
     mi = gpu
     tensors, smooth = qs.synth(hp, seed=seed, qk_gain=6.0)   # peaked attention
     model = mi.Qwen2Model(hp)
     model.load(tensors, smooth)
-    cpu = orc.Qwen2(hp, tensors, smooth, fa_mode=0, n_threads=8)
-    cpu_exact = orc.Qwen2(hp, tensors, smooth, fa_mode=1, n_threads=8)
-    q8 = hp["wtype"] == qs.GGML_TYPE_Q8_0
-    cpu_generic = orc.Qwen2(hp, tensors, smooth, fa_mode=1, n_threads=8, q8_generic=True) if q8 else None
+    chp, ct = (hp, tensors) if hp["wtype"] != qs.GGML_TYPE_F16 else a8w8_reference(orc, hp, tensors, smooth)
+    cpu = orc.Qwen2(chp, ct, smooth, fa_mode=0, n_threads=threads)
+    cpu_exact = orc.Qwen2(chp, ct, smooth, fa_mode=1, n_threads=threads)
+    q8 = chp["wtype"] == qs.GGML_TYPE_Q8_0
+    cpu_generic = orc.Qwen2(chp, ct, smooth, fa_mode=1, n_threads=threads, q8_generic=True) if q8 else None
     rng = np.random.default_rng(seed + 1)
     tokens = list(rng.integers(0, hp["n_vocab"], n_prompt))
     max_err_ggml = max_rel_exact = spread = 0.0
@@ -89,6 +104,41 @@ def test_qwen2_7b_width_two_layers_q4_0(gpu, orc):
     err, rel, spread, mism = _run(gpu, orc, hp, n_prompt=8, n_gen=8, seed=6)
     assert rel < 2e-3
     assert mism == 0
+
+
+def test_qwen2_a8w8_from_f16_weights(gpu, orc, monkeypatch):
+    """An F16 model on the A8W8 path (GGML_MI355X_A8W8=1, the reference's GGML_CANN_A8W8) at
+    the full Qwen2.5-1.5B width: every projection is quantized at upload to Q8_0 of
+    W*diag(s).  Its logits must be bit-identical to the same backend running the Q8_0 model
+    the oracle's weight quantizer makes of the same F16 weights (so the upload path adds
+    nothing), and its greedy tokens identical to the CPU model of that Q8_0 model."""
+    mi = gpu
+    monkeypatch.setenv("GGML_MI355X_A8W8", "1")
+    monkeypatch.delenv("GGML_MI355X_A8W8_DISABLE_LAYERS", raising=False)
+    hp = qs.qwen2_1p5b(n_layer=2, n_ctx=64, wtype=qs.GGML_TYPE_F16)
+    tensors, smooth = qs.synth(hp, seed=15)
+    f16 = mi.Qwen2Model(hp)
+    f16.load(tensors, smooth)
+    qhp, qt = a8w8_reference(orc, hp, tensors, smooth)
+    q8 = mi.Qwen2Model(qhp)
+    q8.load(qt, smooth)
+    cpu = orc.Qwen2(qhp, qt, smooth, fa_mode=0, n_threads=8)
+    rng = np.random.default_rng(16)
+    tok, worst, mism = None, 0.0, 0
+    for pos in range(32):
+        t = int(rng.integers(0, hp["n_vocab"])) if pos < 16 else tok
+        ta, la = f16.decode(t, pos, want_logits=True)
+        tb, lb = q8.decode(t, pos, want_logits=True)
+        tc, lc = cpu.decode(t, pos)
+        assert ta == tb and np.array_equal(la, lb), f"position {pos}"
+        worst = max(worst, float(np.abs(la - lc).max() / np.abs(lc).max()))
+        mism += int(pos >= 15 and ta != tc)
+        tok = ta
+    print(f"A8W8 from F16, 2L x 1536: logits bit-identical to the oracle-quantized Q8_0 model; rel vs ggml-CPU "
+          f"{worst:.3e}, greedy mismatches {mism}/17")
+    assert mism == 0
+    f16.free()
+    q8.free()
 
 
 @pytest.mark.parametrize("wtype", [qs.GGML_TYPE_Q8_0, qs.GGML_TYPE_Q4_0])
@@ -255,7 +305,9 @@ def test_smooth_scale_file_and_layer_dump(gpu, tmp_path):
     a.load(tensors, smooth)
     b = mi.Qwen2Model(hp)
     b.load(tensors, {k: v for k, v in smooth.items() if ".ffn_gate." not in k and ".ffn_up." not in k})
-    b.load_smooth_file(sq_path)
+    with pytest.raises(mi.MiError, match=r"must already hold W\*diag\(s\)"):
+        b.load_smooth_file(sq_path)            # Q8_0 weights: only when asserted pre-smoothed
+    b.load_smooth_file(sq_path, weights_presmoothed=True)
     with pytest.raises(mi.MiError, match="no decode step"):
         a.dump_layers(tmp_path / "early.bin")
     dump = tmp_path / "layers.bin"
@@ -280,5 +332,55 @@ def test_smooth_scale_file_and_layer_dump(gpu, tmp_path):
     rows = lldump.compare(lldump.read_dump(tmp_path / "a.bin"), {k: v[-1:] for k, v in d.items()})
     assert [r[1] for r in rows] == [f"l_out-{i}" for i in range(L)]
     assert all(r[3] == pytest.approx(1.0) and r[4] == 0.0 for r in rows)
+    a.free()
+    b.free()
+
+
+def test_layer_dump_ffn_records(gpu, orc, tmp_path):
+    """With the layer dump on, each step writes ffn_norm-N, ffn_out-N, l_out-N per layer (the
+    records the reference's SmoothQuant collector and layer comparison read); the fusions that
+    would skip writing ffn_norm / ffn_out give way, and the logits stay bit-identical to the
+    fused model's.  Closed forms tie the records together: ffn_norm = RMSNorm(l_out - ffn_out)
+    * w, and ffn_out is the FFN (oracle matmuls) of ffn_norm."""
+    mi = gpu
+    hp = qs.qwen2_1p5b(n_layer=2, n_ctx=64, wtype=qs.GGML_TYPE_Q8_0)
+    tensors, smooth = qs.synth(hp, seed=43)
+    L, E, F = hp["n_layer"], hp["n_embd"], hp["n_ff"]
+    a = mi.Qwen2Model(hp)
+    a.load(tensors, smooth)
+    b = mi.Qwen2Model(hp)
+    b.load(tensors, smooth)
+    b.set_layer_dump(True)
+    dump = tmp_path / "d.bin"
+    rng = np.random.default_rng(44)
+    for pos in range(4):
+        t = int(rng.integers(0, hp["n_vocab"]))
+        ta, la = a.decode(t, pos, want_logits=True)
+        tb, lb = b.decode(t, pos, want_logits=True)
+        assert ta == tb and np.array_equal(la, lb), f"position {pos}"
+        b.dump_layers(dump, append=pos > 0)
+    d = lldump.LayerDump(dump)
+    assert d.names == [f"{kind}-{i}" for i in range(L) for kind in ("ffn_norm", "ffn_out", "l_out")]
+    for i in range(L):
+        fn, fo, lo = d.matrix(f"ffn_norm-{i}"), d.matrix(f"ffn_out-{i}"), d.matrix(f"l_out-{i}")
+        assert fn.shape == fo.shape == lo.shape == (4, E)
+        inp = (lo - fo)[-1]
+        w = tensors[f"blk.{i}.ffn_norm.weight"].astype(np.float64)
+        ref_norm = inp / np.sqrt(np.mean(inp * inp) + hp["rms_eps"]) * w
+        assert rel_err(fn[-1], ref_norm) < 1e-4, i
+        x = fn[-1].astype(np.float32)
+        p = f"blk.{i}."
+        g = orc.mul_mat_q8_0(tensors[p + "ffn_gate.weight"], x, F, E, inv_s=1 / smooth[p + "ffn_gate.weight"])
+        u = orc.mul_mat_q8_0(tensors[p + "ffn_up.weight"], x, F, E, inv_s=1 / smooth[p + "ffn_up.weight"])
+        h = (g / (1 + np.exp(-g)) * u).astype(np.float32)
+        down = orc.mul_mat_q8_0(tensors[p + "ffn_down.weight"], h, E, F, inv_s=1 / smooth[p + "ffn_down.weight"])
+        assert rel_err(fo[-1], down) < 2e-2, i
+    # what smoothquant-collect.py takes from such a dump: per layer the max |ffn_norm| channel
+    amax = np.stack([np.abs(d.matrix(f"ffn_norm-{i}")).max(axis=0) for i in range(L)])
+    assert amax.shape == (L, E) and np.all(amax > 0)
+    b.set_layer_dump(False)
+    tb2, lb2 = b.decode(5, 4, want_logits=True)
+    ta2, la2 = a.decode(5, 4, want_logits=True)
+    assert tb2 == ta2 and np.array_equal(lb2, la2)
     a.free()
     b.free()

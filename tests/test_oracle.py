@@ -193,6 +193,22 @@ def test_weight_quantizer_smoothquant(orc):
     assert np.all(np.abs(deq - ws).reshape(n, -1, 32) <= (amax / 127 * 0.51 + amax * 2.0 ** -10)[:, :, None])
 
 
+def test_weight_quantizer_is_ref_rounding_of_w_times_s(orc):
+    """Exact pin: with power-of-two factors w*s is exact in fp32, so each weight row must
+    quantize to the bytes quantize_row_q8_0_ref gives for w*s (the row quantizer is pinned
+    by its own known answers); a divide by s, or the SIMD rounding, fails this."""
+    rng = RNG(8)
+    n, k = 16, 128
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    s = (2.0 ** rng.integers(-3, 4, k)).astype(np.float32)
+    q = orc.quantize_weight_q8_0(w, s)
+    ws = w * s
+    for r in range(n):
+        assert np.array_equal(q[r], orc.quantize_row_q8_0(ws[r], variant=orc.Q8_ROUND_REF).reshape(-1)), r
+    assert not np.array_equal(q, orc.quantize_weight_q8_0(w / s))
+    assert np.array_equal(orc.quantize_weight_q8_0(w), orc.quantize_weight_q8_0(w, np.ones(k, np.float32)))
+
+
 # ---------------------------------------------------------------- Q4_0
 
 def test_q4_0_dequant_closed_form(orc):
