@@ -402,14 +402,14 @@ def measure_c5(mi, qs, orc, threads, batches=(1, 8), steps=128, warm=8, cpu_step
         line = c5_line(mi, qs, hp, el, pos0, steps, warm, wbytes, fa)
         if S == 1 and cpu_steps > 0:
             cpu = orc.Qwen2(hp1, tensors, None, fa_mode=0, n_threads=threads)
-            n_pos = pos0 + steps
+            n_pos = pos0 + steps - cpu_steps   # the positions the last timed GPU steps decoded
             for il in range(hp["n_layer"]):
                 cpu.k_cache[il, :n_pos] = model.get_cache_seq(il, 0, 0, n_pos)
                 cpu.v_cache[il, :n_pos] = model.get_cache_seq(il, 1, 0, n_pos)
             t0 = time.perf_counter()
             tok = 0
             for i in range(cpu_steps):
-                tok, _ = cpu.decode(tok, n_pos + i if n_pos + i < n_ctx else n_ctx - 1)
+                tok, _ = cpu.decode(tok, n_pos + i)
             el_cpu = time.perf_counter() - t0
             line["cpu_baseline"] = {"value": round(cpu_steps / el_cpu, 3), "unit": "tok/s", "cores": threads,
                                     "kind": "port", "sample": f"{cpu_steps} decode steps of sequence 0 at position "
