@@ -5,9 +5,10 @@
 // instead of one core per q head streaming the whole KV length, the KV length is
 // split across workgroups (one per (split, kv head)); every K/V row is read once
 // and shared by all q heads of its GQA group; each workgroup keeps an online
-// softmax state (m, l, o) per q head and a log-sum-exp combine kernel merges
-// the splits (inside the last workgroup of a kv head when there are few splits,
-// else in a parallel combine kernel).  Score order follows the reference and ggml: q rounded to fp16,
+// softmax state (m, l, o) per q head and a parallel log-sum-exp combine kernel
+// merges the splits.  (An in-kernel merge by the last workgroup of a kv head exists
+// behind MI_FA_MERGE=1 / MI_FA_FUSED_COMBINE=1; it measured slower, so it is off by
+// default.)  Score order follows the reference and ggml: q rounded to fp16,
 // s = (q.k) * scale, s += mask, online softmax, one final divide.
 #include "mi_common.h"
 
