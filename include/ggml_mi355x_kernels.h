@@ -6,7 +6,8 @@
  * backend calls on the decode hot path.  Every entry point takes plain device
  * pointers, sizes and a hipStream_t passed as void*, returns 0 on success or a
  * negative MI_ERR_* / positive hipError_t code, never aborts, and keeps no
- * global state other than per-device lazily created function handles.
+ * global state other than per-device lazily created function handles and the
+ * fixed per-device scratch array of mi_fa_decode_noalloc.
  * The last error message of the calling thread is available from
  * mi_last_error().
  *
@@ -340,6 +341,19 @@ int mi_fa_decode_partials(void *stream, const float *q, const void *k, const voi
                           const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
                           size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, void *ws,
                           size_t ws_bytes);
+/* mi_fa_decode without a workspace argument, allocating nothing: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The split partials go
+ * to a fixed per-device scratch array inside the library (mi_fa_decode_noalloc_max_workspace()
+ * = 4 MiB, held until the process ends); a call whose mi_fa_decode_workspace_size exceeds
+ * it fails with MI_ERR_WORKSPACE (12 q / 2 kv heads at D=128 fit up to ~400K positions,
+ * 28 q / 4 kv up to 131K).  Every call on one device shares that array: calls that overlap
+ * on one GPU (concurrent streams, or threads) race and must be serialised by the caller.
+ * The stream must belong to the current device.  Results are bit-identical to mi_fa_decode. */
+size_t mi_fa_decode_noalloc_max_workspace(void);
+int mi_fa_decode_noalloc(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
+                         const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                         size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out);
 
 /* ------------------------------------------------------------------------
  * Decode-graph glue ops (one launch each; ggml-CPU semantics of

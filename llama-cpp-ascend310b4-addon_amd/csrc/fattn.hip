@@ -15,6 +15,8 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 #include <type_traits>
 
 namespace {
@@ -921,7 +923,46 @@ __global__ __launch_bounds__(256) void k_kv_lengths(const void *__restrict__ mas
 
 }  // namespace
 
+// Split partials of mi_fa_decode_noalloc: the workspace of callers that cannot allocate,
+// one copy per device (held until the process ends).  In host code this name is only a
+// stand-in for the symbol: kernels get the device address hipGetSymbolAddress returns.
+constexpr size_t kFaNoAllocScratchBytes = 4u << 20;
+static __device__ __align__(256) unsigned char scratch[kFaNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mtx;
+void *g_scratch_ptr[kScratchDevices] = {};
+
+// the device address of the current device's scratch array, looked up once per device
+int fa_scratch_current_device(void **ptr) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        mi::set_error("fa_decode_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+        return (int)e;
+    }
+    MI_CHECK_ARG(dev >= 0 && dev < kScratchDevices, "fa_decode_noalloc: device %d beyond %d", dev, kScratchDevices);
+    std::lock_guard<std::mutex> lk(g_scratch_mtx);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            mi::set_error("fa_decode_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                          hipGetErrorString(e));
+            return e != hipSuccess ? (int)e : MI_ERR_NODEVICE;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return MI_OK;
+}
+
+}  // namespace
+
 extern "C" {
+
 
 size_t mi_fa_decode_batch_workspace_size(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
                                          int64_t n_seq) {
@@ -939,7 +980,8 @@ static int fa_decode_run(void *stream, const float *q, const void *k, const void
                          const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
                          size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out,
                          int64_t n_seq, size_t q_seq, size_t k_seq, size_t v_seq, size_t mask_seq, size_t out_seq,
-                         void *ws, size_t ws_bytes, bool partials_only, uint16_t *xp = nullptr) {
+                         void *ws, size_t ws_bytes, bool partials_only, uint16_t *xp = nullptr,
+                         bool use_counters = true) {
     MI_CHECK_ARG(q && k && v && (out || partials_only || xp), "fa_decode: null pointer");
     MI_CHECK_ARG(n_kv > 0 && n_kv < (1ll << 31) && n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0,
                  "fa_decode: bad heads/length n_kv=%lld nq=%lld nkv=%lld", (long long)n_kv, (long long)n_q_heads,
@@ -972,7 +1014,8 @@ static int fa_decode_run(void *stream, const float *q, const void *k, const void
     a.scale = scale;
     a.out = out;
     a.part = (float *)ws;
-    a.counters = ws ? (unsigned *)((uint8_t *)ws + fa_part_bytes(n_q_heads * n_seq, p.n_splits, d)) : nullptr;
+    a.counters = ws && use_counters ? (unsigned *)((uint8_t *)ws + fa_part_bytes(n_q_heads * n_seq, p.n_splits, d))
+                                    : nullptr;
     a.sq.q = q_seq;
     a.sq.k = k_seq;
     a.sq.v = v_seq;
@@ -1034,6 +1077,29 @@ int mi_kv_lengths(void *stream, const void *mask, int mask_is_f16, int64_t n_kv,
                        n_kv, out);
     MI_CHECK_LAUNCH("k_kv_lengths");
     return MI_OK;
+}
+
+size_t mi_fa_decode_noalloc_max_workspace(void) { return kFaNoAllocScratchBytes; }
+
+int mi_fa_decode_noalloc(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
+                         const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                         size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out) {
+    MI_CHECK_ARG(n_kv > 0 && n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0,
+                 "fa_decode_noalloc: bad heads/length n_kv=%lld nq=%lld nkv=%lld", (long long)n_kv,
+                 (long long)n_q_heads, (long long)n_kv_heads);
+    const size_t need = mi_fa_decode_workspace_size(n_kv, n_q_heads, n_kv_heads, d);
+    if (need > kFaNoAllocScratchBytes) {
+        mi::set_error("fa_decode_noalloc: %lld positions x %lld heads need %zu bytes of split partials, more than "
+                      "the %zu-byte scratch (use mi_fa_decode with a workspace)",
+                      (long long)n_kv, (long long)n_q_heads, need, kFaNoAllocScratchBytes);
+        return MI_ERR_WORKSPACE;
+    }
+    void *ws = nullptr;
+    if (int r = fa_scratch_current_device(&ws)) return r;
+    // no arrival counters (they would have to start at zero): the split kernel writes every
+    // record the combine reads in this call
+    return fa_decode_run(stream, q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1, k_nb2, v_nb1, v_nb2,
+                         scale, out, 1, 0, 0, 0, 0, 0, ws, kFaNoAllocScratchBytes, false, nullptr, false);
 }
 
 }  // extern "C"

@@ -92,6 +92,8 @@ _SIGS = {
                                 _SZ, _SZ, _SZ, _SZ, _P, _SZ]),
     "mi_fa_decode_num_splits": (_I64, [_I64, _I64, _I64, _I64]),
     "mi_fa_decode_partials": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _SZ, _SZ, _SZ, _SZ, _F, _P, _SZ]),
+    "mi_fa_decode_noalloc_max_workspace": (_SZ, []),
+    "mi_fa_decode_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _SZ, _SZ, _SZ, _SZ, _F, _P]),
     "mi_mul_mat_q8_0_f32_multi": (_I, [_P, _I, _P, _P, _P, _I64, _P, _P, _I, _P, _SZ]),
     "mi_rms_norm": (_I, [_P, _P, _P, _P, _I64, _I64, _F]),
     "mi_add_bcast": (_I, [_P, _P, _P, _P, _I64, _I64]),
@@ -411,6 +413,13 @@ def fa_decode_batch(q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1
     _call("mi_fa_decode_batch", _P(stream), _P(q), _P(k), _P(v), _P(mask), _P(kv_len), n_kv, n_q_heads, n_kv_heads,
           d, k_nb1, k_nb2, v_nb1, v_nb2, scale, _P(out), n_seq, q_seq, k_seq, v_seq, mask_seq, out_seq, _P(ws),
           ws_bytes)
+
+
+def fa_decode_noalloc(q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1, k_nb2, v_nb1, v_nb2, scale,
+                      out, stream=None):
+    """mi_fa_decode on the library's fixed per-device scratch (allocates nothing)"""
+    _call("mi_fa_decode_noalloc", _P(stream), _P(q), _P(k), _P(v), _P(mask), _P(kv_len), n_kv, n_q_heads, n_kv_heads,
+          d, k_nb1, k_nb2, v_nb1, v_nb2, scale, _P(out))
 
 
 def kv_lengths(mask, is_f16, n_kv, n_rows, out, stream=None):
