@@ -64,6 +64,12 @@ GGML_BACKEND_API ggml_backend_reg_t ggml_backend_mi355x_reg(void);
  * runtime side of that contract. */
 GGML_BACKEND_API bool ggml_backend_mi355x_set_smooth_factors(struct ggml_tensor *weight, const float *s, int64_t n);
 
+/* No counterpart in the reference (the persistent layer-stack decode, GGML_MI355X_PERSIST=1,
+ * has in-kernel dependency waits that give up after a bounded number of polls): waits for
+ * the backend's stream, then returns 0, or -1 when a launch since the last call gave up
+ * (its results are invalid; the next graph_compute also reports GGML_STATUS_FAILED once). */
+GGML_BACKEND_API int ggml_backend_mi355x_status(ggml_backend_t backend);
+
 /* No counterpart in the reference (an integration check for dynamic loading): returns 1
  * when the op and type ids this backend was compiled with carry the same names in the
  * loaded ggml (ggml_op_name / ggml_type_name), else 0; msg receives a description.

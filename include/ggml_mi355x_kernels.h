@@ -134,6 +134,71 @@ int mi_mul_mat_q8_0_f32(void *stream, const void *w_packed, const float *x, cons
 int mi_mul_mat_q8_0_f32_multi(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
                               float *const *y, int64_t k, const float *x, const float *inv_s, int rounding, void *ws,
                               size_t ws_bytes);
+/* ------------------------------------------------------------------------
+ * The decoder layers of one A8W8 decode token as ONE persistent launch (the
+ * backend's whole-layer-stack fusion).  Replaces, for a run of consecutive layers,
+ * the reference's node-by-node evaluation (evaluate_and_capture_cann_graph,
+ * patch:1897-1930) of RMS_NORM, MUL, MUL_MAT (q/k/v/o/gate/up/down, Q8_0 A8W8 with
+ * SmoothQuant), ADD, ROPE, SET_ROWS, FLASH_ATTN_EXT (patch:1370-1432), GLU.
+ * A grid of one resident workgroup per CU walks every layer through five phases
+ * (q/k/v + RoPE + KV write; attention splits; split merge + o + residual; RMSNorm +
+ * gate/up; swiglu + quantization + down + residual) separated by in-kernel dependency
+ * hops; results are bit-identical to the per-node launches.  Shapes: Qwen2.5-1.5B-like
+ * (n_embd 1536, head_dim 128, 6 q heads per kv head, n_ff 8960), one sequence, an
+ * attention view of at most 1024 positions (16 splits), 256 CUs.
+ * ---------------------------------------------------------------------- */
+typedef struct mi_persist_layer {
+    const void *wq, *wk, *wv, *wo, *w_gate, *w_up, *w_down; /* Q8_0 packed (mi_prepack_q8_0 layout) */
+    const float *bq, *bk, *bv;                              /* q/k/v biases, or NULL */
+    const float *attn_norm, *ffn_norm;                      /* RMSNorm weights [n_embd] */
+    const float *inv_s_attn, *inv_s_o, *inv_s_ffn, *inv_s_down; /* SmoothQuant 1/s of each input, or NULL */
+    void *k_cache, *v_cache;  /* fp16 [n_cache_rows][n_head_kv*head_dim]; row kv_idx is written */
+} mi_persist_layer;
+
+typedef struct mi_persist_args {
+    const float *x_in;         /* the first layer's input (residual stream) fp32 [n_embd] */
+    float *x_out;              /* the last layer's output fp32 [n_embd]; the layers in between
+                                  keep theirs in the context's scratch */
+    const int32_t *pos;        /* RoPE position (device, 1 value) */
+    const void *kv_idx;        /* cache row to write (device, 1 value, int32 or int64) */
+    int kv_idx_is_i64;
+    int64_t n_cache_rows;
+    size_t kv_row_bytes;       /* K and V cache row stride */
+    int n_kv;                  /* attention view length (positions) */
+    const int32_t *kv_len;     /* effective length (the FLASH_ATTN_EXT src[5]), or NULL */
+    float kq_scale, rms_eps;
+    float freq_base, freq_scale, attn_factor;  /* neox RoPE over the head dim */
+    int rounding;              /* MI_Q8_ROUND_* of the activation quantizations */
+    long spin_limit;           /* polls before a dependency wait gives up (<= 0: default, seconds) */
+    int debug_stall_hop;       /* -1; h in 0..4: the waits on hop h of the first layer expect one
+                                  arrival more than its producers make, so they give up after
+                                  spin_limit polls (tests of the error path) */
+} mi_persist_args;
+
+/* context: scratch (per-layer intermediates), counters, pinned error word; allocates */
+int mi_persist_create(void **ctx, int device, int n_layer, int n_embd, int n_head, int n_head_kv, int head_dim,
+                      int n_ff);
+void mi_persist_destroy(void *ctx);
+/* the layers' tensors (host array).  When it differs from the last call's it is copied
+ * to the device after the stream synchronised (a launch in flight may still read the
+ * old one): call outside stream capture; an unchanged array does nothing. */
+int mi_persist_set_layers(void *stream, void *ctx, const mi_persist_layer *layers, int n_layer);
+/* 1 when the pipeline is instantiated for this shape and an attention view of n_kv
+ * positions fits its split records (at most 16 splits), else 0 */
+int mi_persist_supported(int64_t n_kv, int n_embd, int n_head, int n_head_kv, int head_dim, int n_ff);
+/* one launch over all layers (no allocation, capturable) */
+int mi_persist_decode_q8_0(void *stream, void *ctx, const mi_persist_args *args);
+/* phase timestamps (profiling): after enable_trace (allocates), every launch records the
+ * device wall clock at its phase boundaries per layer and workgroup; read_trace copies the
+ * last launch's [n_layer][n_wg][n_events] words (dst NULL: only the sizes and the clock
+ * rate in ticks per microsecond) */
+int mi_persist_enable_trace(void *ctx);
+int mi_persist_read_trace(void *ctx, uint64_t *dst, size_t n_words, int *n_layer, int *n_wg, int *n_events,
+                          double *ticks_per_us);
+/* after the stream synchronised: MI_OK, or an error when a dependency wait gave up in a
+ * launch since the last call (that launch's results are invalid) */
+int mi_persist_status(void *ctx);
+
 /* ---- fused decode chains (the backend's graph fusions).  Each replaces a run of
  * adjacent ggml nodes of llama.cpp's decode graph with one launch; the reference's
  * evaluate_and_capture_cann_graph runs every node through ggml_cann_compute_forward

@@ -10,7 +10,7 @@
 // behind MI_FA_MERGE=1 / MI_FA_FUSED_COMBINE=1; it measured slower, so it is off by
 // default.)  Score order follows the reference and ggml: q rounded to fp16,
 // s = (q.k) * scale, s += mask, online softmax, one final divide.
-#include "mi_common.h"
+#include "fattn_dev.h"
 
 #include <math.h>
 #include <stdlib.h>
@@ -22,89 +22,6 @@
 namespace {
 
 using namespace mi;
-
-constexpr int kNW = 4;  // waves per workgroup
-constexpr float kLog2e = 1.4426950408889634f;
-
-// 2^x with the hardware v_exp_f32 (arguments here are <= 0; -inf gives 0)
-__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-template <int D>
-constexpr int part_stride() { return D + 4; }  // o[D], m, l, pad -> 16-byte aligned records
-
-struct FaPlan {
-    int chunk;     // positions per workgroup
-    int n_splits;
-    int kt;        // VALU kernel: positions per lane group per tile (all loads of a tile in flight together)
-    int nbw;       // MFMA kernel: 16-position blocks per wave
-    bool mfma;
-};
-
-
-// One workgroup per (split, kv head), each with 4 waves of lane groups (one KV row
-// per lane group: 16 groups per workgroup at D = 128, 32 at D = 64).  A workgroup's
-// time is a chain of dependent steps per tile, so short contexts get one short tile
-// per workgroup and many workgroups; long contexts aim at ~512 workgroups with 8-deep
-// tiles.  With at most kFusedMaxSplits splits the last workgroup of a kv head can
-// merge the partials itself (opt-in).  MI_FA_CHUNK=<positions> overrides the chunk.
-constexpr int kFusedMaxSplits = 16;
-constexpr int kMaxSplits = 1024;
-
-inline int fa_chunk_override() {
-    static const int v = [] {
-        const char *e = getenv("MI_FA_CHUNK");
-        return e ? atoi(e) : 0;
-    }();
-    return v;
-}
-
-inline bool fa_valu_forced() {
-    static const bool v = [] {
-        const char *e = getenv("MI_FA_VALU");
-        return e && e[0] == '1';
-    }();
-    return v;
-}
-
-inline FaPlan fa_plan(int64_t n_kv, int64_t n_kv_heads, int64_t d, int64_t gq, int64_t n_seq = 1) {
-    const int64_t ng = 4 * 64 / (d / 8);  // lane groups per workgroup
-    const int64_t target_wg = 512;        // over all sequences of the launch
-    int64_t per = (n_kv * n_kv_heads * n_seq + target_wg - 1) / target_wg;
-    if (fa_chunk_override() > 0) per = fa_chunk_override();
-    FaPlan p;
-    p.mfma = !fa_valu_forced() && gq <= 16;
-    if (p.mfma) {
-        // 4 waves x nbw blocks of 16 positions per workgroup
-        p.kt = 1;
-        // at most 8 blocks per wave (fully unrolled, 3 waves per SIMD); longer runs (a
-        // runtime loop at 2 waves per SIMD, measured slower) only when the split count
-        // would exceed kMaxSplits (over 512K positions)
-        p.nbw = per <= 64 ? 1 : per <= 128 ? 2 : per <= 256 ? 4 : 8;
-        int64_t chunk = 64 * p.nbw;
-        while ((n_kv + chunk - 1) / chunk > kMaxSplits) chunk *= 2;
-        if (chunk <= 64 * 32) {  // a run of at most 32 blocks per wave (the kernel's instances)
-            p.chunk = (int)chunk;
-            p.nbw = (int)(chunk / 64);
-            p.n_splits = (int)((n_kv + chunk - 1) / chunk);
-            return p;
-        }
-        p.mfma = false;  // over 2M positions: the VALU kernel, whose chunk is a runtime loop
-    }
-    p.nbw = 0;
-    if (per <= ng) p.kt = 1;
-    else if (per <= 2 * ng) p.kt = 2;
-    else if (per <= 4 * ng) p.kt = 4;
-    else p.kt = 8;
-    int64_t chunk = (per + ng * p.kt - 1) / (ng * p.kt) * (ng * p.kt);
-    while ((n_kv + chunk - 1) / chunk > kMaxSplits) chunk *= 2;
-    p.chunk = (int)chunk;
-    p.n_splits = (int)((n_kv + chunk - 1) / chunk);
-    return p;
-}
-
-inline size_t fa_part_bytes(int64_t n_q_heads, int64_t n_splits, int64_t d) {
-    return align_up((size_t)n_q_heads * n_splits * (d + 4) * sizeof(float), 256);
-}
 
 template <int LPR>
 __device__ __forceinline__ void merge_state(float &m, float &l, float *o, int xor_mask) {
@@ -122,13 +39,6 @@ __device__ __forceinline__ void merge_state(float &m, float &l, float *o, int xo
     for (int i = 0; i < 8; i++) o[i] = o[i] * a + oo[i] * b;
     m = mn;
 }
-
-// Sequences (grid z) are independent problems: per-sequence strides of q / out
-// (floats), K / V (bytes) and mask (elements); kv_len and the partials are indexed by
-// sequence.
-struct FaSeq {
-    size_t q, k, v, mask, out;
-};
 
 template <int D, int GQ, bool MASK, int kT>
 __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, const uint8_t *__restrict__ kc,
@@ -370,13 +280,6 @@ __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, c
 // device coherence point), waits for them, then counts its arrival; the workgroup that
 // arrives last reads all records with agent-scope atomic loads and merges them.  The
 // counter goes back to zero for the next launch.
-__device__ __forceinline__ void st_coherent(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_coherent(const float *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 template <int D, int GQ>
 __device__ __forceinline__ void fa_merge_last(const float *part, float *out, unsigned *counter, int kvh, int n_splits,
                                               int tid) {
@@ -445,46 +348,6 @@ __device__ __forceinline__ void fa_merge_last(const float *part, float *out, uns
 // 4g..4g+3 at dims [D/16*c, D/16*(c+1)); output tile t column c is dim D/16*c + t.
 // P is split into fp16 hi + lo parts (two MFMAs) so the PV product keeps fp32-level
 // accuracy.  Online softmax per head in log2 units; the waves merge through LDS.
-typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-typedef float float4_t __attribute__((ext_vector_type(4)));
-
-template <int N>
-struct U32s {
-    uint32_t w[N];
-};
-
-template <int NB>  // bytes per load group: 64 / 32 (K) or 16 / 8 (V)
-__device__ __forceinline__ void ld_bytes(uint32_t *dst, const uint8_t *src) {
-    if constexpr (NB % 16 == 0) {
-#pragma unroll
-        for (int i = 0; i < NB / 16; i++) {
-            const int4 v = *(const int4 *)(src + 16 * i);
-            dst[4 * i] = (uint32_t)v.x; dst[4 * i + 1] = (uint32_t)v.y;
-            dst[4 * i + 2] = (uint32_t)v.z; dst[4 * i + 3] = (uint32_t)v.w;
-        }
-    } else {
-        const int2 v = *(const int2 *)src;
-        dst[0] = (uint32_t)v.x; dst[1] = (uint32_t)v.y;
-    }
-}
-
-// K row slice of lane group g: NC 16-byte chunks at byte offsets 64i + 16g, so that one
-// load instruction covers a contiguous 64-byte piece of each of its 16 rows
-template <int NC>
-__device__ __forceinline__ void ld_k_chunks(uint32_t *dst, const uint8_t *src) {
-#pragma unroll
-    for (int i = 0; i < NC; i++) {
-        const int4 v = *(const int4 *)(src + 64 * i);
-        dst[4 * i] = (uint32_t)v.x; dst[4 * i + 1] = (uint32_t)v.y;
-        dst[4 * i + 2] = (uint32_t)v.z; dst[4 * i + 3] = (uint32_t)v.w;
-    }
-}
-
-__device__ __forceinline__ half4_t h4(uint32_t a, uint32_t b) {
-    uint32_t t[2] = {a, b};
-    return __builtin_bit_cast(half4_t, t);
-}
-
 template <int D, int GQ, bool MASK, int NBW, int NW = 4>
 __global__ __launch_bounds__(64 * NW) void k_fa_mfma(const float *__restrict__ q, const uint8_t *__restrict__ kc,
                                                  const uint8_t *__restrict__ vc, const uint16_t *__restrict__ mask,
@@ -492,207 +355,15 @@ __global__ __launch_bounds__(64 * NW) void k_fa_mfma(const float *__restrict__ q
                                                  size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, int chunk,
                                                  int n_splits, float *__restrict__ part, float *__restrict__ out,
                                                  unsigned *__restrict__ counters, const FaSeq sq) {
-    {
-        const int seq = blockIdx.z;
-        q += (size_t)seq * sq.q;
-        kc += (size_t)seq * sq.k;
-        vc += (size_t)seq * sq.v;
-        if (MASK) mask += (size_t)seq * sq.mask;
-        if (kv_len_p) kv_len_p += seq;
-        out += (size_t)seq * sq.out;
-        part += (size_t)seq * gridDim.y * GQ * n_splits * part_stride<D>();
-        if (counters) counters += (size_t)seq * gridDim.y;
-    }
-    constexpr int KS = D / 16;    // k-steps of the score product
-    constexpr int KW = D / 8;     // K dwords per lane per block (D/4 halves)
-    constexpr int VT = D / 16;    // output tiles = V halves per lane per row
-    constexpr int VW = D / 32;    // V dwords per lane per row
-    constexpr int PS = part_stride<D>();
-    __shared__ float s_m[NW][16];
-    __shared__ float s_l[NW][16];
-    __shared__ __align__(16) float s_o[NW][GQ][D];
-
-    const int split = blockIdx.x;
-    const int kvh = blockIdx.y;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int g = lane >> 4;
-    const int c = lane & 15;
-
-    const int kl = kv_len_p ? *kv_len_p : n_kv;
-    const int eff = (kl > 0 && kl < n_kv) ? kl : n_kv;
-    const int start = split * chunk;
-    const int end_phys = min(start + chunk, n_kv);
-    const int end_eff = min(end_phys, eff);
-    const int wstart = start + wave * NBW * 16;
-
-    // q fragment (B operand): lane (g, c) holds head c, dims 32*(s/2) + 8g + 4*(s%2) .. +3
-    // for step s, the dims its K chunks hold
-    half4_t qf[KS];
-    {
-        const float *qh = q + (size_t)(kvh * GQ + min(c, GQ - 1)) * D + 8 * g;
-#pragma unroll
-        for (int s2 = 0; s2 < KS; s2++) {
-            const float4 v = *(const float4 *)(qh + 32 * (s2 / 2) + 4 * (s2 % 2));
-            const uint32_t a = (uint32_t)f2h(v.x) | ((uint32_t)f2h(v.y) << 16);
-            const uint32_t b = (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16);
-            qf[s2] = c < GQ ? h4(a, b) : h4(0u, 0u);
-        }
-    }
-
-    const uint8_t *kb = kc + (size_t)kvh * k_nb2 + (size_t)16 * g;
-    const uint8_t *vb = vc + (size_t)kvh * v_nb2 + (size_t)(D / 8) * c;
-    const int last = end_phys - 1;
-
-    float m = -INFINITY, l = 0.0f;
-    float4_t o[VT];
-#pragma unroll
-    for (int t = 0; t < VT; t++) o[t] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-    U32s<KW> kr[2];
-    U32s<VW> vr[2][4];
-    auto issue = [&](int blk, int buf) {
-        const int p0 = wstart + blk * 16;
-        ld_k_chunks<D / 32>(kr[buf].w, kb + (size_t)min(p0 + c, last) * k_nb1);
-#pragma unroll
-        for (int r = 0; r < 4; r++) ld_bytes<D / 8>(vr[buf][r].w, vb + (size_t)min(p0 + 4 * g + r, last) * v_nb1);
-    };
-    // one 16-position block: scores, online softmax, P.V (buffer buf holds its K / V)
-    auto step = [&](int blk, auto bufc) {
-        constexpr int buf = decltype(bufc)::value;
-        const int p0 = wstart + blk * 16;
-        float mk[4] = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (MASK) {
-#pragma unroll
-            for (int r = 0; r < 4; r++) mk[r] = h2f(mask[min(p0 + 4 * g + r, last)]);
-        }
-        float4_t sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s2 = 0; s2 < KS; s2++)
-            sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(h4(kr[buf].w[2 * s2], kr[buf].w[2 * s2 + 1]), qf[s2], sacc,
-                                                         0, 0, 0);
-        float sc[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const bool ok = c < GQ && p0 + 4 * g + r < end_eff;
-            // ggml order: s = (q.k)*scale; s += mask; kept in log2 units for v_exp_f32
-            const float v = mul_add_rn(sacc[r], scale, mk[r]) * kLog2e;
-            sc[r] = ok ? v : -INFINITY;
-        }
-        float bm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-        bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-        const float mn = fmaxf(m, bm);
-        const float alpha = mn == -INFINITY ? 1.0f : fexp2(m - mn);
-        float p[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) p[r] = mn == -INFINITY ? 0.0f : fexp2(sc[r] - mn);
-        l = l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-        m = mn;
-        // rescale the output rows: row 4g+r belongs to head 4g+r, whose alpha sits in lane 4g+r
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float a = __shfl(alpha, 4 * g + r, 64);
-#pragma unroll
-            for (int t = 0; t < VT; t++) o[t][r] *= a;
-        }
-        half_t ph[4], pl[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            ph[r] = (half_t)p[r];
-            pl[r] = (half_t)(p[r] - (float)ph[r]);
-        }
-        const half4_t ahi = {ph[0], ph[1], ph[2], ph[3]};
-        const half4_t alo = {pl[0], pl[1], pl[2], pl[3]};
-#pragma unroll
-        for (int t = 0; t < VT; t++) {
-            // column c of tile t is dim D/16*c + t: half t of each of the lane's 4 V rows
-            const int wd = t >> 1;
-            uint32_t a0, a1;
-            if (t & 1) {
-                a0 = (vr[buf][0].w[wd] >> 16) | (vr[buf][1].w[wd] & 0xffff0000u);
-                a1 = (vr[buf][2].w[wd] >> 16) | (vr[buf][3].w[wd] & 0xffff0000u);
-            } else {
-                a0 = (vr[buf][0].w[wd] & 0xffffu) | (vr[buf][1].w[wd] << 16);
-                a1 = (vr[buf][2].w[wd] & 0xffffu) | (vr[buf][3].w[wd] << 16);
-            }
-            const half4_t bv = h4(a0, a1);
-            o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(ahi, bv, o[t], 0, 0, 0);
-            o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(alo, bv, o[t], 0, 0, 0);
-        }
-    };
-    using B0 = std::integral_constant<int, 0>;
-    using B1 = std::integral_constant<int, 1>;
-    issue(0, 0);
-    if constexpr (NBW == 1) {
-        step(0, B0{});
-    } else {
-        // two register stages; the next pair's loads are unconditional (past the run they
-        // re-read its last row: cache hits, masked), so no wait gathers every load
-        issue(1, 1);
-        constexpr int kUnroll = NBW <= 8 ? NBW / 2 : 1;
-#pragma unroll kUnroll
-        for (int blk = 0; blk < NBW; blk += 2) {
-            step(blk, B0{});
-            issue(blk + 2, 0);
-            step(blk + 1, B1{});
-            issue(blk + 3, 1);
-        }
-    }
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-
-    if (g == 0) {
-        s_m[wave][c] = m;
-        s_l[wave][c] = l;
-    }
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int h = 4 * g + r;
-        if (h < GQ) {
-#pragma unroll
-            for (int t = 0; t < VT; t++) s_o[wave][h][(D / 16) * c + t] = o[t][r];
-        }
-    }
-    __syncthreads();
-
-    for (int idx = tid; idx < GQ * D; idx += 64 * NW) {
-        const int h = idx / D;
-        const int dd = idx % D;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < NW; w++) M = fmaxf(M, s_m[w][h]);
-        float L = 0.0f, acc = 0.0f;
-        if (M != -INFINITY) {
-#pragma unroll
-            for (int w = 0; w < NW; w++) {
-                const float e = fexp2(s_m[w][h] - M);
-                L += s_l[w][h] * e;
-                acc += s_o[w][h][dd] * e;
-            }
-        }
-        const int qh_idx = kvh * GQ + h;
-        if (n_splits == 1 && out) {
-            out[(size_t)qh_idx * D + dd] = L == 0.0f ? 0.0f : acc / L;
-        } else if (counters) {
-            float *rec = part + ((size_t)qh_idx * n_splits + split) * PS;
-            st_coherent(rec + dd, acc);
-            if (dd == 0) {
-                st_coherent(rec + D, M);
-                st_coherent(rec + D + 1, L);
-            }
-        } else {
-            float *rec = part + ((size_t)qh_idx * n_splits + split) * PS;
-            rec[dd] = acc;
-            if (dd == 0) {
-                rec[D] = M;
-                rec[D + 1] = L;
-            }
-        }
-    }
+    const int seq = blockIdx.z;
+    fa_mfma_tile<D, GQ, MASK, NBW, NW>(q, kc, vc, mask, kv_len_p, n_kv, k_nb1, k_nb2, v_nb1, v_nb2, scale, chunk,
+                                       n_splits, part, out, counters != nullptr, sq, blockIdx.x, blockIdx.y, seq,
+                                       gridDim.y);
     if constexpr (NW == 4) {
-        if (n_splits > 1 && counters) fa_merge_last<D, GQ>(part, out, counters + kvh, kvh, n_splits, tid);
+        if (n_splits > 1 && counters)
+            fa_merge_last<D, GQ>(part + (size_t)seq * gridDim.y * GQ * n_splits * part_stride<D>(),
+                                 out + (size_t)seq * sq.out, counters + (size_t)seq * gridDim.y + blockIdx.y,
+                                 blockIdx.y, n_splits, threadIdx.x);
     }
 }
 

@@ -218,9 +218,16 @@ struct BackendCtx {
         float freq_base = 0, freq_scale = 0, attn_factor = 0;
         bool valid = false;
     } rope_key;
+    // the persistent layer-stack decode (created for the first run of layers it fuses)
+    bool persist_on = false;      // GGML_MI355X_PERSIST, read when the backend is created
+    std::string persist_trace;    // GGML_MI355X_PERSIST_TRACE: file for the last launch's phase timestamps
+    void *persist = nullptr;
+    int persist_layers = 0;
+    bool persist_failed = false;  // the context could not be created: per-node path from then on
+    bool persist_error = false;   // a launch gave up waiting (reported once)
     // captured replay of the last graph
     hipGraphExec_t gexec = nullptr;
-    std::vector<uint64_t> signature;
+    std::vector<uint64_t> signature, sig_scratch;
     int same_calls = 0;
 };
 
@@ -779,97 +786,121 @@ const float *rope_table_for(BackendCtx *ctx, const void *pos, int64_t hd, float 
     return ctx->rope_tab;
 }
 
-int try_fuse_attn_in(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+// The attention-input chain of one token: RMS_NORM, MUL(w), MUL_MAT q/k/v (one activation
+// row, Q8_0 or Q4_0), [ADD bias x3], ROPE q, ROPE k, SET_ROWS k, SET_ROWS v.
+struct AttnInMatch {
+    int end = -1;  // index of the last node (SET_ROWS v)
+    const ggml_tensor *x = nullptr, *nw = nullptr, *mul = nullptr;
+    float eps = 0.0f;
+    const ggml_tensor *mm[3] = {}, *out[3] = {}, *bias[3] = {}, *rope[2] = {}, *sr[2] = {};
+    ggml_type wt = GGML_TYPE_COUNT;
+    int64_t hd = 0;
+};
+
+bool match_attn_in(ggml_cgraph *g, int i, const Consumers &C, AttnInMatch &M) {
     const int nn = ggml_graph_n_nodes(g);
     int j;
-    const ggml_tensor *x, *nw, *mul;
-    float eps;
-    if (!rms_mul_head(g, i, C, j, x, nw, mul, eps)) return 0;
-    const ggml_tensor *mm[3], *out[3], *bias[3] = {nullptr, nullptr, nullptr};
-    ggml_type wt = GGML_TYPE_COUNT;
+    if (!rms_mul_head(g, i, C, j, M.x, M.nw, M.mul, M.eps)) return false;
+    const ggml_tensor *const *mm = M.mm;
     for (int t = 0; t < 3; t++) {
         j = next_real(g, j + 1);
-        if (j >= nn) return 0;
-        mm[t] = ggml_graph_node(g, j);
-        if (t == 0) wt = gemv_type(mm[0]);
-        if (wt == GGML_TYPE_COUNT || !gemv_node(mm[t], wt) || mm[t]->src[1] != mul ||
+        if (j >= nn) return false;
+        M.mm[t] = ggml_graph_node(g, j);
+        if (t == 0) M.wt = gemv_type(M.mm[0]);
+        if (M.wt == GGML_TYPE_COUNT || !gemv_node(mm[t], M.wt) || mm[t]->src[1] != M.mul ||
             inv_s_of(mm[t]->src[0]) != inv_s_of(mm[0]->src[0]))
-            return 0;
-        out[t] = mm[t];
+            return false;
+        M.out[t] = mm[t];
     }
-    if (!only_consumed_by(C, mul, {mm[0], mm[1], mm[2]})) return 0;
+    if (!only_consumed_by(C, M.mul, {mm[0], mm[1], mm[2]})) return false;
     int jb = next_real(g, j + 1);
     if (jb < nn && ggml_graph_node(g, jb)->op == GGML_OP_ADD) {
         for (int t = 0; t < 3; t++) {
-            if (jb >= nn) return 0;
+            if (jb >= nn) return false;
             const ggml_tensor *ad = ggml_graph_node(g, jb);
             if (ad->op != GGML_OP_ADD || ad->src[0] != mm[t] || !is_row_vector(ad->src[1], mm[t]->ne[0]) ||
                 !is_f32_contig(ad) || !only_consumed_by(C, mm[t], {ad}))
-                return 0;
-            bias[t] = ad->src[1];
-            out[t] = ad;
+                return false;
+            M.bias[t] = ad->src[1];
+            M.out[t] = ad;
             j = jb;
             jb = next_real(g, jb + 1);
         }
     }
-    const ggml_tensor *rope[2], *sr[2];
+    const ggml_tensor *const *rope = M.rope;
     for (int t = 0; t < 2; t++) {
         j = next_real(g, j + 1);
-        if (j >= nn) return 0;
-        rope[t] = ggml_graph_node(g, j);
-        if (rope[t]->op != GGML_OP_ROPE || !supports_op_impl(rope[t]) || alias_root(rope[t]->src[0]) != out[t] ||
-            !only_consumed_by(C, out[t], {rope[t]}))
-            return 0;
+        if (j >= nn) return false;
+        M.rope[t] = ggml_graph_node(g, j);
+        if (rope[t]->op != GGML_OP_ROPE || !supports_op_impl(rope[t]) || alias_root(rope[t]->src[0]) != M.out[t] ||
+            !only_consumed_by(C, M.out[t], {rope[t]}))
+            return false;
     }
     const ggml_tensor *r = rope[0];
     const int64_t hd = r->src[0]->ne[0];
+    M.hd = hd;
     if (r->op_params[1] != hd || rope[1]->op_params[1] != hd || rope[1]->src[0]->ne[0] != hd || hd % 16 ||
         rope[1]->src[1] != r->src[1] || ggml_nelements(r->src[1]) != 1 ||
         memcmp(r->op_params + 5, rope[1]->op_params + 5, 4 * sizeof(int32_t)) != 0 ||
         mm[0]->ne[0] % hd || mm[1]->ne[0] % hd || !is_f32_contig(rope[0]))
-        return 0;
-    if (wt == GGML_TYPE_Q4_0 && (hd > 128 || mm[2]->ne[0] % 2)) return 0;
+        return false;
+    if (M.wt == GGML_TYPE_Q4_0 && (hd > 128 || mm[2]->ne[0] % 2)) return false;
+    const ggml_tensor *const *sr = M.sr;
     for (int t = 0; t < 2; t++) {
         j = next_real(g, j + 1);
-        if (j >= nn) return 0;
-        sr[t] = ggml_graph_node(g, j);
-        const ggml_tensor *src = t == 0 ? rope[1] : out[2];
+        if (j >= nn) return false;
+        M.sr[t] = ggml_graph_node(g, j);
+        const ggml_tensor *src = t == 0 ? rope[1] : M.out[2];
         if (sr[t]->op != GGML_OP_SET_ROWS || !supports_op_impl(sr[t]) || alias_root(sr[t]->src[0]) != src ||
             ggml_nrows(sr[t]->src[0]) != 1 || sr[t]->src[0]->ne[0] != mm[t + 1]->ne[0] ||
             ggml_nelements(sr[t]->src[1]) != 1 || (t == 1 && sr[1]->src[1] != sr[0]->src[1]))
-            return 0;
+            return false;
     }
-    if (!only_consumed_by(C, rope[1], {sr[0]}) || !only_consumed_by(C, out[2], {sr[1]})) return 0;
-    if (overlaps(rope[0], x) || overlaps(rope[0], nw)) return 0;
+    if (!only_consumed_by(C, rope[1], {sr[0]}) || !only_consumed_by(C, M.out[2], {sr[1]})) return false;
+    if (overlaps(rope[0], M.x) || overlaps(rope[0], M.nw)) return false;
+    M.end = j;
+    return true;
+}
 
+void rope_params(const ggml_tensor *r, float &freq_base, float &freq_scale, float &attn_factor) {
+    memcpy(&freq_base, (const float *)r->op_params + 5, sizeof(float));
+    memcpy(&freq_scale, (const float *)r->op_params + 6, sizeof(float));
+    memcpy(&attn_factor, (const float *)r->op_params + 8, sizeof(float));
+}
+
+int try_fuse_attn_in(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    AttnInMatch M;
+    if (!match_attn_in(g, i, C, M)) return 0;
+    const ggml_tensor *const *mm = M.mm, *const *sr = M.sr;
+    const ggml_tensor *r = M.rope[0];
+    const int64_t hd = M.hd;
     const void *w[3];
     int64_t n[3];
     const float *bp[3];
     for (int t = 0; t < 3; t++) {
         w[t] = ((const TensorExtra *)mm[t]->src[0]->extra)->packed;
         n[t] = mm[t]->src[0]->ne[1];
-        bp[t] = bias[t] ? (const float *)bias[t]->data : nullptr;
+        bp[t] = M.bias[t] ? (const float *)M.bias[t]->data : nullptr;
     }
     float freq_base, freq_scale, attn_factor;
-    memcpy(&freq_base, (const float *)r->op_params + 5, sizeof(float));
-    memcpy(&freq_scale, (const float *)r->op_params + 6, sizeof(float));
-    memcpy(&attn_factor, (const float *)r->op_params + 8, sizeof(float));
+    rope_params(r, freq_base, freq_scale, attn_factor);
     const ggml_tensor *idx = sr[0]->src[1];
     const float *tab = rope_table_for(ctx, r->src[1]->data, hd, freq_base, freq_scale, attn_factor);
-    if (wt == GGML_TYPE_Q4_0) {
-        MI_K_CHECK(mi_qkv_rope_kv_q4_0(ctx->stream, w, n, bp, x->ne[0], (const float *)x->data, (const float *)nw->data,
-                                       eps, hd, (const int32_t *)r->src[1]->data, freq_base, freq_scale, attn_factor,
-                                       (float *)rope[0]->data, sr[0]->data, sr[0]->nb[1], sr[1]->data, sr[1]->nb[1],
-                                       idx->data, idx->type == GGML_TYPE_I64, std::min(sr[0]->ne[1], sr[1]->ne[1]),
-                                       tab));
-        return j + 1 - i;
+    if (M.wt == GGML_TYPE_Q4_0) {
+        MI_K_CHECK(mi_qkv_rope_kv_q4_0(ctx->stream, w, n, bp, M.x->ne[0], (const float *)M.x->data,
+                                       (const float *)M.nw->data, M.eps, hd, (const int32_t *)r->src[1]->data,
+                                       freq_base, freq_scale, attn_factor, (float *)M.rope[0]->data, sr[0]->data,
+                                       sr[0]->nb[1], sr[1]->data, sr[1]->nb[1], idx->data,
+                                       idx->type == GGML_TYPE_I64, std::min(sr[0]->ne[1], sr[1]->ne[1]), tab));
+        return M.end + 1 - i;
     }
-    MI_K_CHECK(mi_qkv_rope_kv_q8_0(ctx->stream, w, n, bp, x->ne[0], (const float *)x->data, (const float *)nw->data, eps,
-                                   inv_s_of(mm[0]->src[0]), q8_rounding(), hd, (const int32_t *)r->src[1]->data,
-                                   freq_base, freq_scale, attn_factor, (float *)rope[0]->data, sr[0]->data,
-                                   sr[0]->nb[1], sr[1]->data, sr[1]->nb[1], idx->data, idx->type == GGML_TYPE_I64,
-                                   std::min(sr[0]->ne[1], sr[1]->ne[1]), tab));
-    return j + 1 - i;
+    MI_K_CHECK(mi_qkv_rope_kv_q8_0(ctx->stream, w, n, bp, M.x->ne[0], (const float *)M.x->data,
+                                   (const float *)M.nw->data, M.eps, inv_s_of(mm[0]->src[0]), q8_rounding(), hd,
+                                   (const int32_t *)r->src[1]->data, freq_base, freq_scale, attn_factor,
+                                   (float *)M.rope[0]->data, sr[0]->data, sr[0]->nb[1], sr[1]->data, sr[1]->nb[1],
+                                   idx->data, idx->type == GGML_TYPE_I64, std::min(sr[0]->ne[1], sr[1]->ne[1]),
+                                   tab));
+    return M.end + 1 - i;
 }
 
 const ggml_tensor *matmul_add_tail(ggml_cgraph *g, int j, const ggml_tensor *mm, const Consumers &C,
@@ -1095,6 +1126,208 @@ int try_fuse_fa_o(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
                                        ad ? (const float *)vec->data : nullptr, (const float *)ctx->fa_ws, S, n_head,
                                        d, ex->inv_s, q8_rounding()));
     return (ad ? next_real(g, j + 1) : j) + 1 - i;
+}
+
+// ---- the whole layer stack of one A8W8 token as one persistent launch
+//
+// A decoder layer of the one-token graph:
+//   attention input (match_attn_in, Q8_0), FLASH_ATTN_EXT (q = the rotated q, K / V = the
+//   views of the caches the SET_ROWS wrote, no mask), MUL_MAT o (Q8_0), ADD(o, x),
+//   RMS_NORM, MUL(w), MUL_MAT gate, MUL_MAT up, GLU swiglu, MUL_MAT down, ADD(down, x1)
+// with every intermediate read by nothing outside the layer.  A run of such layers, each
+// reading the previous one's output, with one position / cache row / attention view,
+// runs as mi_persist_decode_q8_0 (GGML_MI355X_PERSIST=1).
+struct PersistLayerMatch {
+    int end = -1;  // the layer's last node (the FFN residual ADD)
+    const ggml_tensor *x = nullptr, *out = nullptr, *rms = nullptr, *x1 = nullptr;
+    const ggml_tensor *rope = nullptr, *idx = nullptr, *kvl = nullptr, *fa = nullptr;
+    mi_persist_layer L{};
+    float eps = 0.0f, eps_ffn = 0.0f, kq_scale = 0.0f;
+    int64_t n_embd = 0, n_head = 0, n_head_kv = 0, hd = 0, n_ff = 0, n_kv = 0, n_cache_rows = 0;
+    size_t kv_row_bytes = 0;
+};
+
+
+// ADD(a, b) in either operand order, one row of n floats
+bool is_add_of(const ggml_tensor *ad, const ggml_tensor *a, const ggml_tensor *b, int64_t n) {
+    return ad->op == GGML_OP_ADD && is_f32_contig(ad) && ggml_nelements(ad) == n && aligned16(ad->data) &&
+           ((ad->src[0] == a && ad->src[1] == b) || (ad->src[0] == b && ad->src[1] == a));
+}
+
+bool match_persist_layer(ggml_cgraph *g, int i, const Consumers &C, PersistLayerMatch &P) {
+    const int nn = ggml_graph_n_nodes(g);
+    AttnInMatch M;
+    if (!match_attn_in(g, i, C, M) || M.wt != GGML_TYPE_Q8_0) return false;
+    const ggml_tensor *const *mm = M.mm;
+    P.x = M.x;
+    P.rms = ggml_graph_node(g, i);
+    P.hd = M.hd;
+    P.n_embd = M.x->ne[0];
+    P.n_head = mm[0]->ne[0] / M.hd;
+    P.n_head_kv = mm[1]->ne[0] / M.hd;
+    P.eps = M.eps;
+    P.rope = M.rope[0];
+    P.idx = M.sr[0]->src[1];
+    if (mm[1]->ne[0] != mm[2]->ne[0] || !aligned16(M.nw->data)) return false;
+    // attention: one sequence, one query row, no mask, over the caches just written
+    int j = next_real(g, M.end + 1);
+    if (j >= nn) return false;
+    const ggml_tensor *fa = ggml_graph_node(g, j);
+    if (fa->op != GGML_OP_FLASH_ATTN_EXT || !supports_fa(fa)) return false;
+    const ggml_tensor *q = fa->src[0], *k = fa->src[1], *v = fa->src[2];
+    if (fa->src[3] || q->data != M.rope[0]->data || q->ne[0] != P.hd || q->ne[1] != 1 || q->ne[2] != P.n_head ||
+        q->ne[3] != 1 || k->ne[2] != P.n_head_kv || k->ne[3] != 1 || k->data != M.sr[0]->data ||
+        v->data != M.sr[1]->data || k->nb[1] != M.sr[0]->nb[1] || v->nb[1] != M.sr[1]->nb[1] || v->nb[1] != k->nb[1] ||
+        k->nb[2] != (size_t)P.hd * 2 || v->nb[2] != (size_t)P.hd * 2 || !only_consumed_by(C, M.rope[0], {fa}) ||
+        !aligned16(k->data) || !aligned16(v->data))
+        return false;
+    P.fa = fa;
+    P.kvl = fa->src[5];
+    P.n_kv = k->ne[1];
+    P.kv_row_bytes = k->nb[1];
+    P.n_cache_rows = std::min(M.sr[0]->ne[1], M.sr[1]->ne[1]);
+    memcpy(&P.kq_scale, fa->op_params, sizeof(float));
+    // o projection + residual
+    j = next_real(g, j + 1);
+    if (j >= nn) return false;
+    const ggml_tensor *mo = ggml_graph_node(g, j);
+    if (!q8_gemv_node(mo) || alias_root(mo->src[1]) != fa || !only_consumed_by(C, fa, {mo}) ||
+        mo->src[0]->ne[0] != P.n_head * P.hd || mo->src[0]->ne[1] != P.n_embd)
+        return false;
+    j = next_real(g, j + 1);
+    if (j >= nn) return false;
+    const ggml_tensor *x1 = ggml_graph_node(g, j);
+    if (!is_add_of(x1, mo, M.x, P.n_embd) || !only_consumed_by(C, mo, {x1})) return false;
+    // FFN
+    j = next_real(g, j + 1);
+    if (j >= nn) return false;
+    const ggml_tensor *x2, *nw2, *mul2;
+    const int j_rms = j;
+    if (!rms_mul_head(g, j_rms, C, j, x2, nw2, mul2, P.eps_ffn) || x2 != x1 || !aligned16(nw2->data)) return false;
+    const ggml_tensor *gu[2];
+    for (int t = 0; t < 2; t++) {
+        j = next_real(g, j + 1);
+        if (j >= nn) return false;
+        gu[t] = ggml_graph_node(g, j);
+        if (!q8_gemv_node(gu[t]) || gu[t]->src[1] != mul2 || gu[t]->src[0]->ne[0] != P.n_embd ||
+            inv_s_of(gu[t]->src[0]) != inv_s_of(gu[0]->src[0]))
+            return false;
+    }
+    P.n_ff = gu[0]->ne[0];
+    if (gu[1]->ne[0] != P.n_ff || !only_consumed_by(C, mul2, {gu[0], gu[1]})) return false;
+    j = next_real(g, j + 1);
+    if (j >= nn) return false;
+    const ggml_tensor *glu = ggml_graph_node(g, j);
+    if (glu->op != GGML_OP_GLU || !supports_op_impl(glu) || glu->src[0] != gu[0] || glu->src[1] != gu[1] ||
+        !only_consumed_by(C, gu[0], {glu}) || !only_consumed_by(C, gu[1], {glu}))
+        return false;
+    j = next_real(g, j + 1);
+    if (j >= nn) return false;
+    const ggml_tensor *down = ggml_graph_node(g, j);
+    if (!q8_gemv_node(down) || down->src[1] != glu || !only_consumed_by(C, glu, {down}) ||
+        down->src[0]->ne[0] != P.n_ff || down->src[0]->ne[1] != P.n_embd)
+        return false;
+    j = next_real(g, j + 1);
+    if (j >= nn) return false;
+    const ggml_tensor *out = ggml_graph_node(g, j);
+    if (!is_add_of(out, down, x1, P.n_embd) || !only_consumed_by(C, down, {out}) ||
+        !only_consumed_by(C, x1, {ggml_graph_node(g, j_rms), out}))
+        return false;
+    P.out = out;
+    P.x1 = x1;
+    P.end = j;
+    mi_persist_layer &L = P.L;
+    auto packed = [](const ggml_tensor *mmn) { return ((const TensorExtra *)mmn->src[0]->extra)->packed; };
+    L.wq = packed(mm[0]);
+    L.wk = packed(mm[1]);
+    L.wv = packed(mm[2]);
+    L.wo = packed(mo);
+    L.w_gate = packed(gu[0]);
+    L.w_up = packed(gu[1]);
+    L.w_down = packed(down);
+    L.bq = M.bias[0] ? (const float *)M.bias[0]->data : nullptr;
+    L.bk = M.bias[1] ? (const float *)M.bias[1]->data : nullptr;
+    L.bv = M.bias[2] ? (const float *)M.bias[2]->data : nullptr;
+    L.attn_norm = (const float *)M.nw->data;
+    L.ffn_norm = (const float *)nw2->data;
+    L.inv_s_attn = inv_s_of(mm[0]->src[0]);
+    L.inv_s_o = inv_s_of(mo->src[0]);
+    L.inv_s_ffn = inv_s_of(gu[0]->src[0]);
+    L.inv_s_down = inv_s_of(down->src[0]);
+    L.k_cache = M.sr[0]->data;
+    L.v_cache = M.sr[1]->data;
+    return true;
+}
+
+// the values one launch shares over its layers
+bool persist_same_step(const PersistLayerMatch &a, const PersistLayerMatch &b) {
+    float fa0[3], fb0[3];
+    rope_params(a.rope, fa0[0], fa0[1], fa0[2]);
+    rope_params(b.rope, fb0[0], fb0[1], fb0[2]);
+    return a.rope->src[1] == b.rope->src[1] && a.idx == b.idx && a.kvl == b.kvl && a.eps == b.eps &&
+           a.eps_ffn == b.eps && b.eps_ffn == b.eps && a.kq_scale == b.kq_scale && a.n_embd == b.n_embd &&
+           a.n_head == b.n_head && a.n_head_kv == b.n_head_kv && a.hd == b.hd && a.n_ff == b.n_ff &&
+           a.n_kv == b.n_kv && a.n_cache_rows == b.n_cache_rows && a.kv_row_bytes == b.kv_row_bytes &&
+           memcmp(fa0, fb0, sizeof(fa0)) == 0 && a.idx->type == b.idx->type;
+}
+
+int try_fuse_persist(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    if (!ctx->persist_on || ctx->persist_failed) return 0;
+    std::vector<PersistLayerMatch> run;
+    PersistLayerMatch P;
+    for (int at = i; match_persist_layer(g, at, C, P); at = next_real(g, P.end + 1)) {
+        // the layer outputs inside the run are never written: only the next layer may read them
+        if (!run.empty() && (P.x != run.back().out || !persist_same_step(run.front(), P) ||
+                             !only_consumed_by(C, P.x, {P.rms, P.x1})))
+            break;
+        if (run.empty() && P.eps_ffn != P.eps) return 0;
+        run.push_back(P);
+        if (next_real(g, P.end + 1) >= ggml_graph_n_nodes(g)) break;
+    }
+    if (run.empty()) return 0;
+    const PersistLayerMatch &F = run.front();
+    if (!mi_persist_supported(F.n_kv, (int)F.n_embd, (int)F.n_head, (int)F.n_head_kv, (int)F.hd, (int)F.n_ff))
+        return 0;
+    const int n_layer = (int)run.size();
+    if (!ctx->persist || ctx->persist_layers != n_layer) {
+        if (ctx->persist) {
+            MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+            mi_persist_destroy(ctx->persist);
+            ctx->persist = nullptr;
+        }
+        if (mi_persist_create(&ctx->persist, ctx->device, n_layer, (int)F.n_embd, (int)F.n_head, (int)F.n_head_kv,
+                              (int)F.hd, (int)F.n_ff) != MI_OK) {
+            fprintf(stderr, "MI355X: persistent decode unavailable (%s); per-node path\n", mi_last_error());
+            ctx->persist = nullptr;
+            ctx->persist_failed = true;
+            return 0;
+        }
+        ctx->persist_layers = n_layer;
+        if (!ctx->persist_trace.empty()) MI_K_CHECK(mi_persist_enable_trace(ctx->persist));
+    }
+    std::vector<mi_persist_layer> layers(n_layer);
+    for (int l = 0; l < n_layer; l++) layers[l] = run[l].L;
+    MI_K_CHECK(mi_persist_set_layers(ctx->stream, ctx->persist, layers.data(), n_layer));
+    mi_persist_args a{};
+    a.x_in = (const float *)F.x->data;
+    a.x_out = (float *)run.back().out->data;
+    a.pos = (const int32_t *)F.rope->src[1]->data;
+    a.kv_idx = F.idx->data;
+    a.kv_idx_is_i64 = F.idx->type == GGML_TYPE_I64;
+    a.n_cache_rows = F.n_cache_rows;
+    a.kv_row_bytes = F.kv_row_bytes;
+    a.n_kv = (int)F.n_kv;
+    a.kv_len = F.kvl ? (const int32_t *)F.kvl->data : nullptr;
+    a.kq_scale = F.kq_scale;
+    a.rms_eps = F.eps;
+    rope_params(F.rope, a.freq_base, a.freq_scale, a.attn_factor);
+    a.rounding = q8_rounding();
+    // test hooks, read per call: a short bounded wait and a hop that never completes
+    const char *spin = getenv("GGML_MI355X_PERSIST_SPIN"), *stall = getenv("GGML_MI355X_PERSIST_STALL_HOP");
+    a.spin_limit = spin && *spin ? atol(spin) : 0;
+    a.debug_stall_hop = stall && *stall ? atoi(stall) : -1;
+    MI_K_CHECK(mi_persist_decode_q8_0(ctx->stream, ctx->persist, &a));
+    return run.back().end + 1 - i;
 }
 
 // ---- several activation rows (a ubatch of tokens) through Q4_0 weights
@@ -1470,6 +1703,7 @@ int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
             return 1;
         case GGML_OP_RMS_NORM: {
             if (fuse) {
+                if (int used = try_fuse_persist(ctx, g, i, C)) return used;
                 if (int used = try_fuse_attn_in(ctx, g, i, C)) return used;
                 if (int used = try_fuse_norm_matmuls(ctx, g, i, C)) return used;
                 if (int used = try_fuse_norm_q4_batch(ctx, g, i, C)) return used;
@@ -1570,33 +1804,65 @@ void run_graph_nodes(BackendCtx *ctx, ggml_cgraph *g) {
     }
 }
 
-// everything the captured launches depend on: ops, data pointers, shapes, strides, params
-std::vector<uint64_t> graph_signature(ggml_cgraph *g) {
-    std::vector<uint64_t> sig;
-    for (int i = 0; i < ggml_graph_n_nodes(g); i++) {
+// everything the captured launches depend on: per node its op, data pointer, shape,
+// strides and op params, per source its data pointer, type, shape and strides (weights
+// also their prepacked copy and SmoothQuant divisor) -- written into sig, whose capacity
+// is kept from call to call (no allocation once warm)
+void graph_signature(ggml_cgraph *g, std::vector<uint64_t> &sig) {
+    sig.clear();
+    const int nn = ggml_graph_n_nodes(g);
+    sig.reserve((size_t)nn * 64);
+    for (int i = 0; i < nn; i++) {
         const ggml_tensor *t = ggml_graph_node(g, i);
-        sig.push_back((uint64_t)t->op);
+        sig.push_back((uint64_t)t->op | ((uint64_t)t->type << 32));
         sig.push_back((uint64_t)(uintptr_t)t->data);
-        for (int d = 0; d < 4; d++) {
-            sig.push_back((uint64_t)t->ne[d]);
-            sig.push_back((uint64_t)t->nb[d]);
+        for (int d = 0; d < 4; d++) sig.push_back((uint64_t)t->ne[d]);
+        for (int d = 0; d < 4; d++) sig.push_back((uint64_t)t->nb[d]);
+        for (int p = 0; p < GGML_MAX_OP_PARAMS / 8; p++) {
+            uint64_t w;
+            memcpy(&w, (const char *)t->op_params + 8 * p, 8);
+            sig.push_back(w);
         }
-        for (int p = 0; p < GGML_MAX_OP_PARAMS / 4; p++) sig.push_back((uint64_t)(uint32_t)t->op_params[p]);
         for (int s = 0; s < GGML_MAX_SRC; s++) {
             const ggml_tensor *src = t->src[s];
-            sig.push_back(src ? (uint64_t)(uintptr_t)src->data : 0);
-            if (src) {
-                sig.push_back((uint64_t)src->type);
-                for (int d = 0; d < 4; d++) sig.push_back((uint64_t)src->nb[d] ^ ((uint64_t)src->ne[d] << 32));
-                sig.push_back((uint64_t)(uintptr_t)src->extra);
-                if (src->extra) sig.push_back((uint64_t)(uintptr_t)((TensorExtra *)src->extra)->inv_s);
+            if (!src) continue;
+            sig.push_back(((uint64_t)s << 56) ^ (uint64_t)(uintptr_t)src->data);
+            sig.push_back((uint64_t)src->type);
+            for (int d = 0; d < 4; d++) sig.push_back((uint64_t)src->ne[d]);
+            for (int d = 1; d < 4; d++) sig.push_back((uint64_t)src->nb[d]);
+            if (src->extra) {
+                const TensorExtra *ex = (const TensorExtra *)src->extra;
+                sig.push_back((uint64_t)(uintptr_t)ex);
+                sig.push_back((uint64_t)(uintptr_t)ex->inv_s);
             }
         }
     }
-    return sig;
 }
 
 // ---- backend iface
+
+// the last persistent launch's phase timestamps: int32 n_layer, n_wg, n_events, float64
+// clock ticks per microsecond, then uint64 [n_layer][n_wg][n_events]
+void write_persist_trace(BackendCtx *ctx) {
+    int nl = 0, nw = 0, ne = 0;
+    double tpu = 0.0;
+    if (mi_persist_read_trace(ctx->persist, nullptr, 0, &nl, &nw, &ne, &tpu) != MI_OK) return;
+    std::vector<uint64_t> buf((size_t)nl * nw * ne);
+    if (mi_persist_read_trace(ctx->persist, buf.data(), buf.size(), nullptr, nullptr, nullptr, nullptr) != MI_OK) {
+        fprintf(stderr, "MI355X: persist trace: %s\n", mi_last_error());
+        return;
+    }
+    FILE *f = fopen(ctx->persist_trace.c_str(), "wb");
+    if (!f) {
+        fprintf(stderr, "MI355X: persist trace: cannot write %s\n", ctx->persist_trace.c_str());
+        return;
+    }
+    const int32_t hdr[3] = {nl, nw, ne};
+    fwrite(hdr, sizeof(hdr), 1, f);
+    fwrite(&tpu, sizeof(tpu), 1, f);
+    fwrite(buf.data(), sizeof(uint64_t), buf.size(), f);
+    fclose(f);
+}
 
 const char *backend_get_name(ggml_backend_t backend) { return ((BackendCtx *)backend->context)->name.c_str(); }
 
@@ -1605,6 +1871,8 @@ void backend_free(ggml_backend_t backend) {
     set_device(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->gexec) (void)hipGraphExecDestroy(ctx->gexec);
+    if (ctx->persist && !ctx->persist_trace.empty()) write_persist_trace(ctx);
+    if (ctx->persist) mi_persist_destroy(ctx->persist);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->fa_ws) (void)hipFree(ctx->fa_ws);
     if (ctx->rope_tab) (void)hipFree(ctx->rope_tab);
@@ -1633,24 +1901,38 @@ void backend_synchronize(ggml_backend_t backend) {
     BackendCtx *ctx = (BackendCtx *)backend->context;
     set_device(ctx->device);
     MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    // a persistent launch whose dependency wait gave up has produced invalid results
+    if (ctx->persist && mi_persist_status(ctx->persist) != MI_OK) {
+        fprintf(stderr, "MI355X: %s\n", mi_last_error());
+        ctx->persist_error = true;
+    }
 }
 
 enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgraph) {
     BackendCtx *ctx = (BackendCtx *)backend->context;
     set_device(ctx->device);
+    if (ctx->persist && mi_persist_status(ctx->persist) != MI_OK) {
+        fprintf(stderr, "MI355X: %s\n", mi_last_error());
+        ctx->persist_error = true;
+    }
+    if (ctx->persist_error) {  // an earlier launch's results were invalid
+        ctx->persist_error = false;
+        return GGML_STATUS_FAILED;
+    }
     ensure_buffers(ctx, cgraph);
     if (!graphs_enabled()) {
         run_graph_nodes(ctx, cgraph);
         return GGML_STATUS_SUCCESS;
     }
-    std::vector<uint64_t> sig = graph_signature(cgraph);
+    std::vector<uint64_t> &sig = ctx->sig_scratch;
+    graph_signature(cgraph, sig);
     if (ctx->gexec && sig == ctx->signature) {
         MI_HIP_CHECK(hipGraphLaunch(ctx->gexec, ctx->stream));
         return GGML_STATUS_SUCCESS;
     }
     // a changed graph runs eagerly once; when the same graph comes back it is captured
     if (sig != ctx->signature) {
-        ctx->signature = std::move(sig);
+        std::swap(ctx->signature, sig);
         ctx->same_calls = 0;
         if (ctx->gexec) {
             MI_HIP_CHECK(hipGraphExecDestroy(ctx->gexec));
@@ -1850,6 +2132,8 @@ ggml_backend_t ggml_backend_mi355x_init(int device) {
     BackendCtx *ctx = new BackendCtx();
     ctx->device = device;
     ctx->fuse = fusion_env();
+    ctx->persist_on = env_flag("GGML_MI355X_PERSIST", false);
+    if (const char *tp = getenv("GGML_MI355X_PERSIST_TRACE")) ctx->persist_trace = tp;
     ctx->name = std::string(GGML_MI355X_NAME) + std::to_string(device);
     MI_HIP_CHECK(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
     return new ggml_backend{backend_guid(), kBackendIface, c->devs[device].get(), ctx};
@@ -1857,6 +2141,17 @@ ggml_backend_t ggml_backend_mi355x_init(int device) {
 
 bool ggml_backend_is_mi355x(ggml_backend_t backend) {
     return backend != nullptr && backend->guid == backend_guid();
+}
+
+int ggml_backend_mi355x_status(ggml_backend_t backend) {
+    if (!ggml_backend_is_mi355x(backend)) return -1;
+    BackendCtx *ctx = (BackendCtx *)backend->context;
+    set_device(ctx->device);
+    MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    if (ctx->persist && mi_persist_status(ctx->persist) != MI_OK) ctx->persist_error = true;
+    if (!ctx->persist_error) return 0;
+    ctx->persist_error = false;
+    return -1;
 }
 
 bool ggml_backend_mi355x_set_smooth_factors(struct ggml_tensor *weight, const float *s, int64_t n) {

@@ -75,6 +75,27 @@ void ggml_backend_tensor_set(struct ggml_tensor *tensor, const void *data, size_
     buf->iface.set_tensor(buf, tensor, data, offset, size);
 }
 
+// ggml-backend.h: the backend's asynchronous copy when it has one (ordered with its
+// graph_compute calls; data must stay valid until ggml_backend_synchronize), else the
+// buffer's synchronous copy
+void ggml_backend_tensor_set_async(ggml_backend_t backend, struct ggml_tensor *tensor, const void *data, size_t offset,
+                                   size_t size) {
+    GGML_ASSERT(tensor->data != nullptr && "tensor not allocated");
+    GGML_ASSERT(offset + size <= ggml_nbytes(tensor) && "tensor write out of bounds");
+    if (size == 0) return;
+    if (backend->iface.set_tensor_async == nullptr) ggml_backend_tensor_set(tensor, data, offset, size);
+    else backend->iface.set_tensor_async(backend, tensor, data, offset, size);
+}
+
+void ggml_backend_tensor_get_async(ggml_backend_t backend, const struct ggml_tensor *tensor, void *data,
+                                   size_t offset, size_t size) {
+    GGML_ASSERT(tensor->data != nullptr && "tensor not allocated");
+    GGML_ASSERT(offset + size <= ggml_nbytes(tensor) && "tensor read out of bounds");
+    if (size == 0) return;
+    if (backend->iface.get_tensor_async == nullptr) ggml_backend_tensor_get(tensor, data, offset, size);
+    else backend->iface.get_tensor_async(backend, tensor, data, offset, size);
+}
+
 void ggml_backend_tensor_get(const struct ggml_tensor *tensor, void *data, size_t offset, size_t size) {
     ggml_backend_buffer_t buf = tensor->view_src ? tensor->view_src->buffer : tensor->buffer;
     GGML_ASSERT(buf != nullptr && "tensor buffer not set");

@@ -75,6 +75,10 @@ GGML_API size_t ggml_backend_buffer_get_alloc_size(ggml_backend_buffer_t buffer,
 GGML_API void ggml_backend_tensor_set(struct ggml_tensor *tensor, const void *data, size_t offset, size_t size);
 GGML_API void ggml_backend_tensor_get(const struct ggml_tensor *tensor, void *data, size_t offset, size_t size);
 GGML_API void ggml_backend_tensor_memset(struct ggml_tensor *tensor, uint8_t value, size_t offset, size_t size);
+GGML_API void ggml_backend_tensor_set_async(ggml_backend_t backend, struct ggml_tensor *tensor, const void *data,
+                                            size_t offset, size_t size);
+GGML_API void ggml_backend_tensor_get_async(ggml_backend_t backend, const struct ggml_tensor *tensor, void *data,
+                                            size_t offset, size_t size);
 
 /* backends */
 GGML_API const char *ggml_backend_name(ggml_backend_t backend);

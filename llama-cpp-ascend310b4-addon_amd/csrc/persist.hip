@@ -1,0 +1,791 @@
+// persist.hip -- the decoder layers of one A8W8 (Q8_0) decode token as one persistent
+// launch.
+//
+// The per-node path runs 7 launches per layer; each kernel boundary costs ~2.4 us on
+// gfx950 (dispatch, drain, cache write-back) plus the tail of its last workgroups.  Here
+// one grid of resident workgroups (one per CU) walks every layer through five phases
+// separated by dependency hops instead of kernel boundaries:
+//
+//   1. q/k/v:  RMSNorm, SmoothQuant, Q8_0 quantization of x, the q/k/v rows, bias, neox
+//              RoPE, q written, k and v written into the cache row
+//   2. attn:   the MFMA flash-decoding split tiles (one per (split, kv head))
+//   3. o:      the splits' log-sum-exp merge (in the combine kernel's exact order), the
+//              o rows, + residual x -> x1
+//   4. gate/up: RMSNorm(x1), SmoothQuant, quantization, the gate and up rows
+//   5. down:   swiglu(gate, up), SmoothQuant, quantization (every workgroup, into LDS),
+//              the down rows, + residual x1 -> the layer output
+//
+// Every phase computes what the per-node kernels compute, with the same lane layout,
+// block order and reductions, so a token's logits are bit-identical to the per-node
+// path's.  A workgroup issues the first weight loads of its next phase before it waits
+// on that phase's hop, so the weight stream overlaps the synchronisation.
+//
+// Hops: only the workgroups that produce a phase's outputs arrive (an agent-scope add
+// to one of 8 counters, by workgroup id mod 8, after their outputs are written through
+// with agent-scope stores); only the consumers wait (lanes 0..7 of wave 0 poll the 8
+// counters).  Every produced buffer is distinct per layer and written once per launch,
+// so a consumer's plain loads after the hop can only miss to memory or hit lines filled
+// after the producers finished.  Every wait is bounded (spin_limit polls): on a timeout
+// the workgroup raises the error word, every later wait returns at once, and all
+// workgroups still reach the exit, where the last one to arrive puts the counters back
+// to zero for the next launch.  The host reads the error from pinned memory.
+#include "q8_0_dev.h"
+#include "fattn_dev.h"
+#include "persist_plan.h"
+
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+namespace {
+
+using persist_plan::kCtrStride;
+using persist_plan::kHops;
+using persist_plan::Layout;
+constexpr int kPersistMaxSplits = persist_plan::kMaxSplits;
+constexpr int kTraceEvents = 16;  // timestamps per (layer, workgroup); see trace_mark below
+
+struct PArgs {
+    const mi_persist_layer *layers;
+    int n_layer, n_embd, n_head_kv, hd, n_ff;
+    const int32_t *pos;
+    const void *kv_idx;
+    int kv_idx_i64;
+    int64_t n_cache_rows;
+    size_t kv_row_bytes;
+    int n_kv;
+    const int32_t *kv_len;
+    float kq_scale, eps, theta_scale, freq_scale, attn_factor;
+    int rounding;
+    long spin_limit;
+    int stall_hop;
+    int fa_chunk, fa_splits;
+    Layout lo;
+    const float *x_in;    // the first layer's input
+    float *x_out;         // the last layer's output
+    uint64_t *trace;      // phase timestamps [layer][workgroup][kTraceEvents], or null
+    float *scratch;
+    unsigned *sync;       // hop counters, exit counter, error word (device)
+    unsigned *err_host;   // pinned host word, written on error
+};
+
+__device__ __forceinline__ unsigned ld_u(const unsigned *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_u(unsigned *p, unsigned v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_f(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_h(uint16_t *p, uint16_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// All of this workgroup's writes done, then one arrival (thread 0).
+__device__ __forceinline__ void hop_arrive(const PArgs &a, int layer, int hop) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(a.sync + persist_plan::hop_ctr_word(layer, hop, blockIdx.x & 7), 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait until every producer of the hop arrived (bounded; see the file comment).
+__device__ __forceinline__ void hop_wait(const PArgs &a, int layer, int hop) {
+    if (threadIdx.x < 64) {
+        const int j = threadIdx.x & 7;
+        const unsigned want = persist_plan::hop_want(a.lo, hop, j) + (layer == 0 && hop == a.stall_hop && j == 0);
+        const unsigned *ctr = a.sync + persist_plan::hop_ctr_word(layer, hop, j);
+        unsigned *err = a.sync + persist_plan::err_word(a.n_layer);
+        long spins = 0;
+        for (;;) {
+            if (__all(ld_u(ctr) >= want)) break;
+            bool stop = false;
+            if (threadIdx.x == 0) {
+                stop = ld_u(err) != 0u;
+                if (!stop && ++spins > a.spin_limit) {
+                    st_u(err, 1u);
+                    if (a.err_host) __hip_atomic_store(a.err_host, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    stop = true;
+                }
+            }
+            if (__any(stop)) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __syncthreads();
+}
+
+// Exit: the last workgroup to arrive zeroes every hop counter, the exit counter and the
+// device error word (nobody reads them again in this launch).
+__device__ __forceinline__ void persist_exit(const PArgs &a) {
+    __shared__ int s_last;
+    unsigned *exit_ctr = a.sync + persist_plan::exit_word(a.n_layer);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(exit_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    const int n = a.n_layer * kHops * 8;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) st_u(a.sync + (size_t)i * kCtrStride, 0u);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        st_u(a.sync + persist_plan::err_word(a.n_layer), 0u);
+        st_u(exit_ctr, 0u);
+    }
+}
+
+__device__ __forceinline__ int opaque_int(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// the matrix / row of a tile row of a set of matrices stacked along the rows
+struct Mat {
+    const uint8_t *qlo, *qhi;
+    const uint16_t *d;
+};
+__device__ __forceinline__ Mat mat_of(const void *packed, int n, int nb) {
+    const size_t plane = ((size_t)n * nb * 16 + 255) / 256 * 256;
+    Mat m;
+    m.qlo = (const uint8_t *)packed;
+    m.qhi = m.qlo + plane;
+    m.d = (const uint16_t *)(m.qlo + 2 * plane);
+    return m;
+}
+
+// LDS of one workgroup: the k = n_embd activation stage of the fused GEMVs, the down
+// projection's activation (n_ff int8 + n_ff/32 scales), the RoPE tile's 16 results.
+template <int NB_E, int NF, int NH>
+struct PLds {
+    int8_t qs[NB_E * 32];
+    float d[NB_E];
+    double red[4];
+    float y[16];
+    int8_t fqs[NF];
+    float fd[NF / 32];
+    // the attention merge's per-(head, split group) weights
+    float mw[NH][8][kPersistMaxSplits / 8];  // split weights within a group
+    float mg[NH][8], ml[NH][8];              // group maximum and sum
+    float mwg[NH][8];                        // group weights
+    float mll[NH];                           // the head's total sum
+};
+
+template <int XN, int GE, int UE, int GF, int UF, int D, int GQ, int NBW, int NB_E, int NF, int NGU, int NDN>
+__global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
+    constexpr int RPB = 256 / GE;     // rows per k = n_embd tile (16)
+    constexpr int HALF = RPB / 2;     // RoPE pairs per rotated tile
+    constexpr int RPBF = 256 / GF;    // rows per down tile (4)
+    constexpr int NBF = NF / 32;      // down blocks
+    // NGU / NDN: gate/up and down tiles per workgroup (all prefetched before the hop)
+    constexpr int NH = NB_E * 32 / D;  // query heads (o projection input = NH x D)
+    __shared__ __align__(16) PLds<NB_E, NF, NH> L;
+    const int tid = threadIdx.x;
+    const int wg = blockIdx.x;
+    const int nwg = gridDim.x;
+    const Layout &lo = a.lo;
+    const int E = a.n_embd;
+    const int k4 = E / 4;
+    const int j = tid % GE;
+    const int slot = tid / GE;
+
+    // ---- this workgroup's q/k/v tile (at most one): its rows and RoPE angles, per token
+    RopeKV R;
+    R.hd = a.hd;
+    R.n_q = lo.n_q;
+    R.n_k = lo.n_k;
+    R.n_v = lo.n_v;
+    RopeKVPlace pl;
+    const bool has_qkv = persist_plan::is_qkv(lo, wg);
+    const int qkv_b = has_qkv ? wg : 0;
+    const int qkv_n = lo.n_q + lo.n_k + lo.n_v;
+    const int qkv_rc = min(rope_kv_row<RPB>(R, qkv_b, slot, pl), qkv_n - 1);
+    const int qkv_mi = qkv_rc < lo.n_q ? 0 : qkv_rc < lo.n_q + lo.n_k ? 1 : 2;
+    const int qkv_row = qkv_rc - (qkv_mi == 0 ? 0 : qkv_mi == 1 ? lo.n_q : lo.n_q + lo.n_k);
+    float tab_cs = 0.0f, tab_sn = 0.0f;
+    if (has_qkv && pl.rope && tid < HALF) {  // the angles of rope_kv_epilogue / k_rope_table
+        const int p = pl.chunk * HALF + tid;
+        float theta = (float)a.pos[0];
+        for (int i = 0; i < p; i++) theta *= a.theta_scale;
+        const float th = a.freq_scale * theta;
+        tab_cs = cosf(th) * a.attn_factor;
+        tab_sn = sinf(th) * a.attn_factor;
+    }
+    const int64_t ci = a.kv_idx_i64 ? ((const int64_t *)a.kv_idx)[0] : (int64_t)((const int32_t *)a.kv_idx)[0];
+    const bool ci_ok = ci >= 0 && ci < a.n_cache_rows;
+
+    const int fa_t = persist_plan::fa_tile(lo, wg);  // attention tile of this workgroup (if < n_fa)
+    const int o_t = persist_plan::o_tile(lo, wg);    // o tile (if < n_o_tiles)
+
+    // wall-clock timestamps of one workgroup's phase boundaries (thread 0, when tracing):
+    // 0 layer start, 1 q/k/v waited, 2 q/k/v done, 3 attention waited, 4 attention done,
+    // 5 o waited, 6 o done, 7 gate/up start, 8 gate/up waited, 9 gate/up done,
+    // 10 down start, 11 down waited, 12 down done
+    auto trace_mark = [&](int layer, int ev) {
+        if (a.trace && tid == 0) a.trace[((size_t)layer * nwg + wg) * kTraceEvents + ev] = wall_clock64();
+    };
+
+    for (int layer = 0; layer < a.n_layer; layer++) {
+        // the thread index, opaque to the optimizer in every iteration: the phases' address
+        // arithmetic is then recomputed per layer instead of being hoisted out of the loop,
+        // where it would stay live (in registers) through every other phase
+        const int tid = opaque_int((int)threadIdx.x);
+        const int j = tid % GE;
+        const int slot = tid / GE;
+        const mi_persist_layer &P = a.layers[layer];
+        trace_mark(layer, 0);
+        float *scr = a.scratch + (size_t)layer * lo.layer_floats;
+        float *q_buf = scr + lo.q_off;
+        float *part = scr + lo.part_off;
+        float *x1 = scr + lo.x1_off;
+        float *gbuf = scr + lo.g_off;
+        float *ubuf = scr + lo.u_off;
+        // the residual stream: the caller's input and output at the ends of the stack, the
+        // per-layer scratch copies in between (each written once per launch)
+        const float *x = layer == 0 ? a.x_in : a.scratch + (size_t)(layer - 1) * lo.layer_floats + lo.xr_off;
+        float *x_out = layer == a.n_layer - 1 ? a.x_out : scr + lo.xr_off;
+        const int nbE = NB_E;
+
+        // ================= phase 1: q/k/v + RoPE + KV write
+        if (has_qkv) {
+            const Mat m = mat_of(qkv_mi == 0 ? P.wq : qkv_mi == 1 ? P.wk : P.wv,
+                                 qkv_mi == 0 ? lo.n_q : qkv_mi == 1 ? lo.n_k : lo.n_v, nbE);
+            const size_t rbase = (size_t)qkv_row * nbE;
+            int4 wlo[UE], whi[UE];
+            uint32_t wdw[UE];
+            q8_first_pass<GE, UE>(m.qlo, m.qhi, m.d, rbase, nbE, j, wlo, whi, wdw);
+            if (layer > 0) hop_wait(a, layer - 1, 4);
+            trace_mark(layer, 1);
+            XStage<XN, true> st;
+            xstage_load(st, x, P.attn_norm, P.inv_s_attn, k4, tid);
+            const float scale = xstage_scale(st, k4, a.eps, L.red, tid);
+            xstage_quant(st, P.inv_s_attn, k4, scale, a.rounding, L.qs, L.d, tid);
+            __syncthreads();
+            const float s = q8_row_dot<GE, UE>(m.qlo, m.qhi, m.d, rbase, nbE, j, wlo, whi, wdw, L.qs, L.d);
+            if (j == 0) {
+                const float *bias = qkv_mi == 0 ? P.bq : qkv_mi == 1 ? P.bk : P.bv;
+                L.y[slot] = bias ? s + bias[qkv_row] : s;
+            }
+            __syncthreads();
+            // rope_kv_epilogue with coherent stores
+            if (pl.rope) {
+                if (tid < HALF) {
+                    const int p = pl.chunk * HALF + tid;
+                    const float x0 = L.y[tid], x1v = L.y[tid + HALF];
+                    const float y0 = mul_sub_mul_rn(x0, tab_cs, x1v, tab_sn);
+                    const float y1 = mul_add_mul_rn(x0, tab_sn, x1v, tab_cs);
+                    const int r0 = pl.head * a.hd + p;
+                    if (r0 < lo.n_q) {
+                        st_f(q_buf + r0, y0);
+                        st_f(q_buf + r0 + a.hd / 2, y1);
+                    } else if (ci_ok) {
+                        uint16_t *kr = (uint16_t *)((uint8_t *)P.k_cache + (size_t)ci * a.kv_row_bytes);
+                        st_h(kr + (r0 - lo.n_q), f2h(y0));
+                        st_h(kr + (r0 - lo.n_q + a.hd / 2), f2h(y1));
+                    }
+                }
+            } else if (tid < RPB) {
+                const int vr = qkv_b * RPB + tid - (lo.n_q + lo.n_k);
+                if (vr < lo.n_v && ci_ok)
+                    st_h((uint16_t *)((uint8_t *)P.v_cache + (size_t)ci * a.kv_row_bytes) + vr, f2h(L.y[tid]));
+            }
+            hop_arrive(a, layer, 0);
+            trace_mark(layer, 2);
+        }
+
+        // ================= phase 2: attention split tiles
+        if (persist_plan::is_fa(lo, wg)) {
+            hop_wait(a, layer, 0);
+            trace_mark(layer, 3);
+            const FaSeq sq = {0, 0, 0, 0, 0};
+            fa_mfma_tile<D, GQ, false, NBW, 4>(q_buf, (const uint8_t *)P.k_cache, (const uint8_t *)P.v_cache, nullptr,
+                                               a.kv_len, a.n_kv, a.kv_row_bytes, (size_t)a.hd * 2, a.kv_row_bytes,
+                                               (size_t)a.hd * 2, a.kq_scale, a.fa_chunk, a.fa_splits, part, nullptr,
+                                               true, sq, fa_t % a.fa_splits, fa_t / a.fa_splits, 0, a.n_head_kv);
+            hop_arrive(a, layer, 1);
+            trace_mark(layer, 4);
+        }
+
+        // ================= phase 3: merge + o + residual
+        if (persist_plan::is_o(lo, wg)) {
+            const Mat m = mat_of(P.wo, E, nbE);
+            const int row = o_t * RPB + slot;
+            const size_t rbase = (size_t)row * nbE;
+            int4 wlo[UE], whi[UE];
+            uint32_t wdw[UE];
+            q8_first_pass<GE, UE>(m.qlo, m.qhi, m.d, rbase, nbE, j, wlo, whi, wdw);
+            hop_wait(a, layer, 1);
+            trace_mark(layer, 5);
+            // The attention output (the splits' merge), SmoothQuant and Q8_0 quantization of
+            // the o projection's input.  The merge is fa_merge_exact4's arithmetic (that of
+            // k_fa_combine<D, *, 8> for at most 16 splits) with the per-(head, split group)
+            // weights computed once into LDS instead of in every element's thread: each
+            // element still gets the same fmaf chain over the same operands.
+            constexpr int UL = kPersistMaxSplits / 8;
+            constexpr int PS = part_stride<D>();
+            constexpr int NI = (NB_E * 8 + 255) / 256;  // float4 elements per thread
+            const int S = a.fa_splits;
+            float4 ov[NI][8][UL];  // this thread's split records, loaded first
+#pragma unroll
+            for (int it = 0; it < NI; it++) {
+                const int fc = min(tid + it * 256, k4 - 1);
+                const float *ph = part + (size_t)(fc * 4 / D) * S * PS + (fc * 4) % D;
+#pragma unroll
+                for (int g = 0; g < 8; g++)
+#pragma unroll
+                    for (int u = 0; u < UL; u++)
+                        ov[it][g][u] = *(const float4 *)(ph + (size_t)min(g + 8 * u, S - 1) * PS);
+            }
+            if (tid < NH * 8) {  // group g of head h: splits g, g + 8, ...
+                const int h = tid / 8, g = tid % 8;
+                const float *ph = part + (size_t)h * S * PS;
+                float mv[UL], lv[UL];
+#pragma unroll
+                for (int u = 0; u < UL; u++) {
+                    const int sp = g + 8 * u;
+                    const float *rec = ph + (size_t)min(sp, S - 1) * PS;
+                    mv[u] = sp < S ? rec[D] : -INFINITY;
+                    lv[u] = rec[D + 1];
+                }
+                float cm = -INFINITY, sum = 0.0f;
+#pragma unroll
+                for (int u = 0; u < UL; u++) cm = fmaxf(cm, mv[u]);
+#pragma unroll
+                for (int u = 0; u < UL; u++) {
+                    // an empty group keeps the weights 0: its element sums stay +0
+                    const float w = cm == -INFINITY || mv[u] == -INFINITY ? 0.0f : fexp2(mv[u] - cm);
+                    if (cm != -INFINITY) sum = fmaf(lv[u], w, sum);
+                    L.mw[h][g][u] = w;
+                }
+                L.mg[h][g] = cm;
+                L.ml[h][g] = sum;
+            }
+            __syncthreads();
+            if (tid < NH) {
+                float mm = -INFINITY, ll = 0.0f;
+#pragma unroll
+                for (int g = 0; g < 8; g++) mm = fmaxf(mm, L.mg[tid][g]);
+#pragma unroll
+                for (int g = 0; g < 8; g++) {
+                    const float gm = L.mg[tid][g];
+                    const float w = mm == -INFINITY || gm == -INFINITY ? 0.0f : fexp2(gm - mm);
+                    if (mm != -INFINITY) ll = fmaf(L.ml[tid][g], w, ll);
+                    L.mwg[tid][g] = w;
+                }
+                L.mll[tid] = ll;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int it = 0; it < NI; it++) {
+                const int f = tid + it * 256;  // float4 index; 8 consecutive threads form one 32-block
+                if (f < k4) {  // whole waves drop out together, so the 8-lane groups stay whole
+                    const int h = f * 4 / D;
+                    float4 aa = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+                    for (int g = 0; g < 8; g++) {
+                        float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+                        for (int u = 0; u < UL; u++) {
+                            const float w = L.mw[h][g][u];
+                            A.x = fmaf(ov[it][g][u].x, w, A.x);
+                            A.y = fmaf(ov[it][g][u].y, w, A.y);
+                            A.z = fmaf(ov[it][g][u].z, w, A.z);
+                            A.w = fmaf(ov[it][g][u].w, w, A.w);
+                        }
+                        const float wg = L.mwg[h][g];
+                        aa.x = fmaf(A.x, wg, aa.x);
+                        aa.y = fmaf(A.y, wg, aa.y);
+                        aa.z = fmaf(A.z, wg, aa.z);
+                        aa.w = fmaf(A.w, wg, aa.w);
+                    }
+                    const float ll = L.mll[h];
+                    float4 v = ll == 0.0f ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
+                                          : make_float4(aa.x / ll, aa.y / ll, aa.z / ll, aa.w / ll);
+                    if (P.inv_s_o) {
+                        const float4 sv = ((const float4 *)P.inv_s_o)[f];
+                        v.x *= sv.x;
+                        v.y *= sv.y;
+                        v.z *= sv.z;
+                        v.w *= sv.w;
+                    }
+                    float d;
+                    *(uint32_t *)(L.qs + (size_t)f * 4) = quant4(v.x, v.y, v.z, v.w, a.rounding, d);
+                    if ((f & 7) == 0) L.d[f >> 3] = h2f(f2h(d));
+                }
+            }
+            __syncthreads();
+            const float s = q8_row_dot<GE, UE>(m.qlo, m.qhi, m.d, rbase, nbE, j, wlo, whi, wdw, L.qs, L.d);
+            if (j == 0 && row < E) st_f(x1 + row, s + x[row]);
+            hop_arrive(a, layer, 2);
+            trace_mark(layer, 6);
+        }
+
+        // ================= phase 4: FFN norm + gate/up
+        {
+            trace_mark(layer, 7);
+            const Mat mg = mat_of(P.w_gate, a.n_ff, nbE), mu = mat_of(P.w_up, a.n_ff, nbE);
+            const int n_tot = 2 * a.n_ff;
+            // the workgroup's tiles wg, wg + nwg, ... (rows of [gate; up]) stream through a
+            // ring of NPRE register sets: the first NPRE are loaded before the hop, tile
+            // i + NPRE as soon as tile i's dot has consumed its set
+            constexpr int NPRE = NGU < 3 ? NGU : 3;
+            int4 wlo[NPRE][UE], whi[NPRE][UE];
+            uint32_t wdw[NPRE][UE];
+            auto gu_load = [&](int i, int set) {
+                const int t = wg + i * nwg;
+                if (t < lo.n_gu_tiles) {
+                    const int grow = min(t * RPB + slot, n_tot - 1);
+                    const bool up = grow >= a.n_ff;
+                    const size_t rbase = (size_t)(up ? grow - a.n_ff : grow) * nbE;
+                    q8_first_pass<GE, UE>(up ? mu.qlo : mg.qlo, up ? mu.qhi : mg.qhi, up ? mu.d : mg.d, rbase, nbE,
+                                          j, wlo[set], whi[set], wdw[set]);
+                }
+            };
+#pragma unroll
+            for (int i = 0; i < NPRE; i++) gu_load(i, i);
+            hop_wait(a, layer, 2);
+            trace_mark(layer, 8);
+            XStage<XN, true> st;
+            xstage_load(st, x1, P.ffn_norm, P.inv_s_ffn, k4, tid);
+            const float scale = xstage_scale(st, k4, a.eps, L.red, tid);
+            xstage_quant(st, P.inv_s_ffn, k4, scale, a.rounding, L.qs, L.d, tid);
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < NGU; i++) {
+                const int t = wg + i * nwg;
+                const int set = i % NPRE;
+                if (t < lo.n_gu_tiles) {
+                    const int grow = t * RPB + slot;
+                    const int gr = min(grow, n_tot - 1);
+                    const bool up = gr >= a.n_ff;
+                    const size_t rbase = (size_t)(up ? gr - a.n_ff : gr) * nbE;
+                    const float s = q8_row_dot<GE, UE>(up ? mu.qlo : mg.qlo, up ? mu.qhi : mg.qhi, up ? mu.d : mg.d,
+                                                       rbase, nbE, j, wlo[set], whi[set], wdw[set], L.qs, L.d);
+                    if (j == 0 && grow < n_tot) st_f((up ? ubuf : gbuf) + (up ? grow - a.n_ff : grow), s);
+                }
+                if (i + NPRE < NGU) gu_load(i + NPRE, set);
+            }
+            if (persist_plan::is_gu(lo, wg)) hop_arrive(a, layer, 3);
+            trace_mark(layer, 9);
+        }
+
+        // ================= phase 5: swiglu + quant (every workgroup) + down + residual
+        {
+            trace_mark(layer, 10);
+            const Mat md = mat_of(P.w_down, E, NBF);
+            const int jf = tid % GF;
+            int4 wlo[NDN][UF], whi[NDN][UF];
+            uint32_t wdw[NDN][UF];
+#pragma unroll
+            for (int i = 0; i < NDN; i++) {
+                const int t = wg + i * nwg;
+                if (t < lo.n_down_tiles) {
+                    const int row = min(t * RPBF + tid / GF, E - 1);
+                    const size_t rbase = (size_t)row * NBF;
+#pragma unroll
+                    for (int u = 0; u < UF; u++) {
+                        const int b = min(jf + u * GF, NBF - 1);
+                        wlo[i][u] = ld_stream16(md.qlo + (rbase + b) * 16);
+                        whi[i][u] = ld_stream16(md.qhi + (rbase + b) * 16);
+                        wdw[i][u] = md.d[rbase + b];
+                    }
+                }
+            }
+            hop_wait(a, layer, 3);
+            trace_mark(layer, 11);
+            // k_swiglu_quant_q8_0's arithmetic for every 32-block of the row, into LDS, in
+            // batches of SWB passes of 32 blocks: a batch's loads first, then its math
+            constexpr int NSW = (NBF + 31) / 32;
+            constexpr int SWB = 3;
+            const int sub = tid % 8;
+#pragma unroll
+            for (int p0 = 0; p0 < NSW; p0 += SWB) {
+                float4 gv[SWB], uv[SWB], sv[SWB];
+#pragma unroll
+                for (int q = 0; q < SWB; q++) {
+                    const int e = min((p0 + q) * 32 + tid / 8, NBF - 1) * 32 + sub * 4;
+                    gv[q] = *(const float4 *)(gbuf + e);
+                    uv[q] = *(const float4 *)(ubuf + e);
+                    sv[q] = P.inv_s_down ? *(const float4 *)(P.inv_s_down + e) : make_float4(1.f, 1.f, 1.f, 1.f);
+                }
+#pragma unroll
+                for (int q = 0; q < SWB; q++) {
+                    const int blk = (p0 + q) * 32 + tid / 8;
+                    float4 v;
+                    v.x = (gv[q].x / (1.0f + expf(-gv[q].x))) * uv[q].x;
+                    v.y = (gv[q].y / (1.0f + expf(-gv[q].y))) * uv[q].y;
+                    v.z = (gv[q].z / (1.0f + expf(-gv[q].z))) * uv[q].z;
+                    v.w = (gv[q].w / (1.0f + expf(-gv[q].w))) * uv[q].w;
+                    if (P.inv_s_down) {
+                        v.x *= sv[q].x;
+                        v.y *= sv[q].y;
+                        v.z *= sv[q].z;
+                        v.w *= sv[q].w;
+                    }
+                    float d;
+                    const uint32_t qv = quant4(v.x, v.y, v.z, v.w, a.rounding, d);  // every lane: whole 8-lane groups
+                    if (blk < NBF) {
+                        *(uint32_t *)(L.fqs + blk * 32 + sub * 4) = qv;
+                        if (sub == 0) L.fd[blk] = h2f(f2h(d));
+                    }
+                }
+            }
+            __syncthreads();
+            // k_gemv_q8_0_xq<GF, UF, 1>'s row dot (one pass covers the row: UF * GF >= NBF)
+#pragma unroll
+            for (int i = 0; i < NDN; i++) {
+                const int t = wg + i * nwg;
+                if (t < lo.n_down_tiles) {
+                    const int row = t * RPBF + tid / GF;
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int u = 0; u < UF; u++) {
+                        const int b = jf + u * GF;
+                        if (b < NBF) {
+                            const int4 *xs = (const int4 *)(L.fqs + (size_t)b * 32);
+                            const int s = dot_block(wlo[i][u], whi[i][u], xs[0], xs[1]);
+                            acc = fmaf((float)s, h2f((uint16_t)wdw[i][u]) * L.fd[b], acc);
+                        }
+                    }
+                    const float s = group_sum<GF>(acc);
+                    if (jf == 0 && row < E) st_f(x_out + row, s + x1[row]);
+                }
+            }
+            if (persist_plan::is_down(lo, wg)) hop_arrive(a, layer, 4);
+            trace_mark(layer, 12);
+        }
+    }
+    persist_exit(a);
+}
+
+// ---------------------------------------------------------------- host side
+
+struct PersistCtx {
+    int device = 0;
+    int n_wg = 0;
+    int n_layer = 0, n_embd = 0, n_head = 0, n_head_kv = 0, hd = 0, n_ff = 0;
+    mi_persist_layer *layers_dev = nullptr;
+    std::vector<mi_persist_layer> layers_host;
+    float *scratch = nullptr;
+    size_t scratch_floats = 0;
+    unsigned *sync = nullptr;
+    size_t sync_words = 0;
+    unsigned *err_host = nullptr;  // pinned, device-visible
+    uint64_t *trace = nullptr;     // phase timestamps of the last launch (when enabled)
+};
+
+Layout layout_of(const PersistCtx &c, int fa_splits) {
+    return persist_plan::make_layout(c.n_wg, c.n_embd, c.n_head, c.n_head_kv, c.hd, c.n_ff, fa_splits,
+                                     part_stride<128>());
+}
+
+// the one instantiated shape: Qwen2.5-1.5B-like (n_embd 1536, head_dim 128, GQA 6, n_ff 8960)
+// on 256 workgroups (gate/up: 1120 tiles = 5 per workgroup; down: 384 tiles = 2)
+constexpr int kNbE = 48, kNF = 8960, kWG = 256;
+
+bool shape_supported(int n_embd, int n_head, int n_head_kv, int hd, int n_ff) {
+    return n_embd == kNbE * 32 && hd == 128 && n_head_kv > 0 && n_head % n_head_kv == 0 && n_head / n_head_kv == 6 &&
+           n_head * hd == n_embd && n_ff == kNF;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi_persist_create(void **out, int device, int n_layer, int n_embd, int n_head, int n_head_kv, int head_dim,
+                      int n_ff) {
+    MI_CHECK_ARG(out && n_layer > 0, "persist_create: bad arguments");
+    MI_CHECK_ARG(shape_supported(n_embd, n_head, n_head_kv, head_dim, n_ff),
+                 "persist_create: shape n_embd=%d heads=%d/%d hd=%d n_ff=%d not instantiated", n_embd, n_head,
+                 n_head_kv, head_dim, n_ff);
+    *out = nullptr;
+    hipError_t e = hipSetDevice(device);
+    if (e != hipSuccess) return mi::hip_fail(e, "persist_create: hipSetDevice");
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return mi::hip_fail(e, "persist_create: hipGetDeviceProperties");
+    PersistCtx *c = new PersistCtx();
+    c->device = device;
+    c->n_wg = prop.multiProcessorCount;  // one resident workgroup per CU
+    if (c->n_wg != kWG) {
+        delete c;
+        mi::set_error("persist_create: %d CUs; the pipeline is instantiated for %d", prop.multiProcessorCount, kWG);
+        return MI_ERR_UNSUPPORTED;
+    }
+    c->n_layer = n_layer;
+    c->n_embd = n_embd;
+    c->n_head = n_head;
+    c->n_head_kv = n_head_kv;
+    c->hd = head_dim;
+    c->n_ff = n_ff;
+    const Layout lo = layout_of(*c, kPersistMaxSplits);
+    c->scratch_floats = lo.layer_floats * n_layer;
+    c->sync_words = persist_plan::sync_words(n_layer);
+    if ((e = hipMalloc(&c->scratch, c->scratch_floats * sizeof(float))) != hipSuccess ||
+        (e = hipMalloc(&c->sync, c->sync_words * sizeof(unsigned))) != hipSuccess ||
+        (e = hipMalloc(&c->layers_dev, (size_t)n_layer * sizeof(mi_persist_layer))) != hipSuccess ||
+        (e = hipHostMalloc(&c->err_host, 64, hipHostMallocMapped)) != hipSuccess ||
+        (e = hipMemset(c->sync, 0, c->sync_words * sizeof(unsigned))) != hipSuccess ||
+        (e = hipDeviceSynchronize()) != hipSuccess) {
+        mi_persist_destroy(c);
+        return mi::hip_fail(e, "persist_create: allocation");
+    }
+    *c->err_host = 0;
+    *out = c;
+    return MI_OK;
+}
+
+void mi_persist_destroy(void *ctx) {
+    PersistCtx *c = (PersistCtx *)ctx;
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->scratch) (void)hipFree(c->scratch);
+    if (c->sync) (void)hipFree(c->sync);
+    if (c->layers_dev) (void)hipFree(c->layers_dev);
+    if (c->err_host) (void)hipHostFree(c->err_host);
+    if (c->trace) (void)hipFree(c->trace);
+    delete c;
+}
+
+int mi_persist_set_layers(void *stream, void *ctx, const mi_persist_layer *layers, int n_layer) {
+    PersistCtx *c = (PersistCtx *)ctx;
+    MI_CHECK_ARG(c && layers && n_layer == c->n_layer, "persist_set_layers: %d layers, context has %d", n_layer,
+                 c ? c->n_layer : 0);
+    for (int l = 0; l < n_layer; l++) {
+        const mi_persist_layer &L = layers[l];
+        MI_CHECK_ARG(L.wq && L.wk && L.wv && L.wo && L.w_gate && L.w_up && L.w_down && L.attn_norm && L.ffn_norm &&
+                         L.k_cache && L.v_cache,
+                     "persist_set_layers: layer %d has a null tensor", l);
+        MI_CHECK_ARG(mi::aligned(L.attn_norm, 16) &&
+                         mi::aligned(L.ffn_norm, 16) && (!L.inv_s_attn || mi::aligned(L.inv_s_attn, 16)) &&
+                         (!L.inv_s_o || mi::aligned(L.inv_s_o, 16)) && (!L.inv_s_ffn || mi::aligned(L.inv_s_ffn, 16)) &&
+                         (!L.inv_s_down || mi::aligned(L.inv_s_down, 16)) && mi::aligned(L.k_cache, 16) &&
+                         mi::aligned(L.v_cache, 16),
+                     "persist_set_layers: layer %d: vectors must be 16-byte aligned", l);
+    }
+    if (c->layers_host.size() == (size_t)n_layer &&
+        memcmp(c->layers_host.data(), layers, (size_t)n_layer * sizeof(mi_persist_layer)) == 0)
+        return MI_OK;  // unchanged: nothing to upload (and nothing to record under stream capture)
+    hipError_t e = hipSetDevice(c->device);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+    if (e == hipSuccess)
+        e = hipMemcpy(c->layers_dev, layers, (size_t)n_layer * sizeof(mi_persist_layer), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return mi::hip_fail(e, "persist_set_layers: upload");
+    c->layers_host.assign(layers, layers + n_layer);
+    return MI_OK;
+}
+
+int mi_persist_decode_q8_0(void *stream, void *ctx, const mi_persist_args *args) {
+    PersistCtx *c = (PersistCtx *)ctx;
+    MI_CHECK_ARG(c && args && !c->layers_host.empty(), "persist_decode: no context or no layers set");
+    MI_CHECK_ARG(args->x_in && args->x_out && mi::aligned(args->x_in, 16) && mi::aligned(args->x_out, 16),
+                 "persist_decode: x_in / x_out must be 16-byte aligned device vectors");
+    MI_CHECK_ARG(args->pos && args->kv_idx && args->kv_row_bytes >= (size_t)c->n_head_kv * c->hd * 2 &&
+                     args->kv_row_bytes % 16 == 0 && args->n_kv > 0 && args->n_cache_rows > 0,
+                 "persist_decode: bad position / cache arguments");
+    const FaPlan p = fa_plan(args->n_kv, c->n_head_kv, c->hd, c->n_head / c->n_head_kv);
+    MI_CHECK_ARG(p.mfma && p.nbw == 1 && p.n_splits <= kPersistMaxSplits,
+                 "persist_decode: a %d-position view needs %d attention splits (at most %d fit the o prologue)",
+                 args->n_kv, p.n_splits, kPersistMaxSplits);
+    PArgs a;
+    memset(&a, 0, sizeof(a));
+    a.layers = c->layers_dev;
+    a.n_layer = c->n_layer;
+    a.n_embd = c->n_embd;
+    a.n_head_kv = c->n_head_kv;
+    a.hd = c->hd;
+    a.n_ff = c->n_ff;
+    a.pos = args->pos;
+    a.kv_idx = args->kv_idx;
+    a.kv_idx_i64 = args->kv_idx_is_i64;
+    a.n_cache_rows = args->n_cache_rows;
+    a.kv_row_bytes = args->kv_row_bytes;
+    a.n_kv = args->n_kv;
+    a.kv_len = args->kv_len;
+    a.kq_scale = args->kq_scale;
+    a.eps = args->rms_eps;
+    // theta_scale on the host with the C library powf, as the CPU rope cache does
+    a.theta_scale = powf(args->freq_base, -2.0f / (float)c->hd);
+    a.freq_scale = args->freq_scale;
+    a.attn_factor = args->attn_factor;
+    a.rounding = args->rounding;
+    a.spin_limit = args->spin_limit > 0 ? args->spin_limit : (1l << 22);
+    a.stall_hop = args->debug_stall_hop >= 0 && args->debug_stall_hop < kHops ? args->debug_stall_hop : -1;
+    a.fa_chunk = p.chunk;
+    a.fa_splits = p.n_splits;
+    a.lo = layout_of(*c, p.n_splits);
+    constexpr int NGU = 5, NDN = 2;
+    MI_CHECK_ARG(persist_plan::layout_fits(a.lo, NGU, NDN), "persist_decode: %d workgroups do not fit the tiles",
+                 c->n_wg);
+    a.x_in = args->x_in;
+    a.x_out = args->x_out;
+    a.trace = c->trace;
+    a.scratch = c->scratch;
+    a.sync = c->sync;
+    a.err_host = c->err_host;
+    hipLaunchKernelGGL((k_persist_q8_0<2, 16, 3, 64, 5, 128, 6, 1, kNbE, kNF, NGU, NDN>), dim3((unsigned)c->n_wg),
+                       dim3(256), 0, (hipStream_t)stream, a);
+    MI_CHECK_LAUNCH("k_persist_q8_0");
+    return MI_OK;
+}
+
+int mi_persist_enable_trace(void *ctx) {
+    PersistCtx *c = (PersistCtx *)ctx;
+    MI_CHECK_ARG(c, "persist_enable_trace: no context");
+    if (c->trace) return MI_OK;
+    hipError_t e = hipSetDevice(c->device);
+    const size_t n = (size_t)c->n_layer * c->n_wg * kTraceEvents;
+    if (e == hipSuccess) e = hipMalloc(&c->trace, n * sizeof(uint64_t));
+    if (e == hipSuccess) e = hipMemset(c->trace, 0, n * sizeof(uint64_t));
+    if (e != hipSuccess) return mi::hip_fail(e, "persist_enable_trace");
+    return MI_OK;
+}
+
+int mi_persist_read_trace(void *ctx, uint64_t *dst, size_t n_words, int *n_layer, int *n_wg, int *n_events,
+                          double *ticks_per_us) {
+    PersistCtx *c = (PersistCtx *)ctx;
+    MI_CHECK_ARG(c && c->trace, "persist_read_trace: tracing is not enabled");
+    const size_t n = (size_t)c->n_layer * c->n_wg * kTraceEvents;
+    if (n_layer) *n_layer = c->n_layer;
+    if (n_wg) *n_wg = c->n_wg;
+    if (n_events) *n_events = kTraceEvents;
+    if (ticks_per_us) {
+        int khz = 0;
+        (void)hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, c->device);
+        *ticks_per_us = khz / 1000.0;
+    }
+    if (!dst) return MI_OK;
+    MI_CHECK_ARG(n_words >= n, "persist_read_trace: %zu words, %zu needed", n_words, n);
+    hipError_t e = hipSetDevice(c->device);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(dst, c->trace, n * sizeof(uint64_t), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return mi::hip_fail(e, "persist_read_trace");
+    return MI_OK;
+}
+
+int mi_persist_supported(int64_t n_kv, int n_embd, int n_head, int n_head_kv, int head_dim, int n_ff) {
+    if (!shape_supported(n_embd, n_head, n_head_kv, head_dim, n_ff) || n_kv < 1) return 0;
+    const FaPlan p = fa_plan(n_kv, n_head_kv, head_dim, n_head / n_head_kv);
+    return p.mfma && p.nbw == 1 && p.n_splits <= kPersistMaxSplits ? 1 : 0;
+}
+
+int mi_persist_status(void *ctx) {
+    PersistCtx *c = (PersistCtx *)ctx;
+    if (!c || !c->err_host) return MI_ERR_ARG;
+    const unsigned v = __atomic_load_n(c->err_host, __ATOMIC_ACQUIRE);
+    if (v == 0) return MI_OK;
+    __atomic_store_n(c->err_host, 0u, __ATOMIC_RELEASE);
+    mi::set_error("persist_decode: a workgroup gave up waiting for a dependency (spin limit); that token's "
+                  "results are invalid");
+    return MI_ERR_UNSUPPORTED;
+}
+
+}  // extern "C"

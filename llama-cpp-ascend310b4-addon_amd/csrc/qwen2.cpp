@@ -24,6 +24,8 @@
 #include <string>
 #include <vector>
 
+#include <hip/hip_runtime.h>
+
 #include "ggml-backend.h"
 #include "ggml-mi355x.h"
 #include "ggml.h"
@@ -63,7 +65,9 @@ struct mi_qwen2 {
     std::map<std::string, ggml_tensor *> tensors;
     std::vector<ggml_tensor *> k_cache, v_cache;  // F16 [n_embd_kv, n_ctx * n_seq]
     ggml_tensor *inp = nullptr;  // I32 [4 * n_seq]: tokens, positions, kv lengths, cache rows
-    std::vector<int32_t> inp_host;
+    // pinned host words: the 4 * n_seq inputs, then the n_seq greedy tokens read back
+    // (asynchronous copies on the backend's stream)
+    int32_t *io_pinned = nullptr;
     std::map<int, Graph> graphs;  // by KV view length
     Graph *last = nullptr;        // the graph of the latest decode step
     bool dump = false;            // graphs keep ffn_norm-N / ffn_out-N as outputs
@@ -217,11 +221,17 @@ mi_qwen2 *mi_qwen2_create(const mi_qwen2_hparams *hp, int device) {
     m->hp = *hp;
     m->n_seq = hp->n_seq > 0 ? hp->n_seq : 1;
     m->hp.n_seq = m->n_seq;
-    m->inp_host.assign(4 * (size_t)m->n_seq, 0);
     m->backend = ggml_backend_mi355x_init(device);
     if (!m->backend) {
         delete m;
         fail("qwen2: no MI355X device %d", device);
+        return nullptr;
+    }
+    if (hipHostMalloc((void **)&m->io_pinned, 5 * (size_t)m->n_seq * sizeof(int32_t), hipHostMallocDefault) !=
+        hipSuccess) {
+        ggml_backend_free(m->backend);
+        delete m;
+        fail("qwen2: pinned host allocation failed");
         return nullptr;
     }
     ggml_init_params ip = {0, nullptr, true};
@@ -276,6 +286,7 @@ void mi_qwen2_free(mi_qwen2 *m) {
     ggml_backend_buffer_free(m->wbuf);
     ggml_free(m->wctx);
     ggml_backend_free(m->backend);
+    if (m->io_pinned) (void)hipHostFree(m->io_pinned);
     delete m;
 }
 
@@ -410,16 +421,20 @@ int mi_qwen2_decode_batch(mi_qwen2 *m, const int32_t *tokens, const int32_t *pos
         max_len = std::max(max_len, pos[s] + 1);
     }
     Graph &G = graph_for(m, max_len);
+    int32_t *in = m->io_pinned, *out = m->io_pinned + 4 * S;
     for (int s = 0; s < S; s++) {
-        m->inp_host[s] = tokens[s];
-        m->inp_host[S + s] = pos[s];
-        m->inp_host[2 * S + s] = pos[s] + 1;
-        m->inp_host[3 * S + s] = s * m->hp.n_ctx + pos[s];
+        in[s] = tokens[s];
+        in[S + s] = pos[s];
+        in[2 * S + s] = pos[s] + 1;
+        in[3 * S + s] = s * m->hp.n_ctx + pos[s];
     }
-    ggml_backend_tensor_set(m->inp, m->inp_host.data(), 0, m->inp_host.size() * sizeof(int32_t));
+    // inputs in, graph, greedy tokens out: one stream, one synchronisation
+    ggml_backend_tensor_set_async(m->backend, m->inp, in, 0, 4 * (size_t)S * sizeof(int32_t));
     if (ggml_backend_graph_compute(m->backend, G.gf) != GGML_STATUS_SUCCESS) return fail("qwen2: graph failed");
+    if (next_tokens) ggml_backend_tensor_get_async(m->backend, G.argmax, out, 0, (size_t)S * sizeof(int32_t));
+    if (ggml_backend_mi355x_status(m->backend) != 0) return fail("qwen2: decode failed: %s", mi_last_error());
     m->last = &G;
-    if (next_tokens) ggml_backend_tensor_get(G.argmax, next_tokens, 0, (size_t)S * sizeof(int32_t));
+    if (next_tokens) memcpy(next_tokens, out, (size_t)S * sizeof(int32_t));
     if (logits) ggml_backend_tensor_get(G.logits, logits, 0, ggml_nbytes(G.logits));
     return 0;
 }

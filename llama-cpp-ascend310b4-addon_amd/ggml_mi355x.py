@@ -127,6 +127,14 @@ _SIGS = {
     "mi_gemv_q8_0_add": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64]),
     "mi_fill_mask_f16": (_I, [_P, _P, _P, _I64]),
     "mi_fill_f16_uniform": (_I, [_P, _P, _I64, _I64, _SZ, ctypes.c_uint64, _F]),
+    "mi_persist_create": (_I, [_P, _I, _I, _I, _I, _I, _I, _I]),
+    "mi_persist_destroy": (None, [_P]),
+    "mi_persist_set_layers": (_I, [_P, _P, _P, _I]),
+    "mi_persist_supported": (_I, [_I64, _I, _I, _I, _I, _I]),
+    "mi_persist_decode_q8_0": (_I, [_P, _P, _P]),
+    "mi_persist_status": (_I, [_P]),
+    "mi_persist_enable_trace": (_I, [_P]),
+    "mi_persist_read_trace": (_I, [_P, _P, _SZ, _P, _P, _P, _P]),
 }
 
 # every symbol the C ABI header declares (checked by the CPU tests)
