@@ -227,7 +227,7 @@ struct BackendCtx {
     bool persist_error = false;   // a launch gave up waiting (reported once)
     // captured replay of the last graph
     hipGraphExec_t gexec = nullptr;
-    std::vector<uint64_t> signature, sig_scratch;
+    std::vector<uint64_t> signature;
     int same_calls = 0;
 };
 
@@ -1804,42 +1804,58 @@ void run_graph_nodes(BackendCtx *ctx, ggml_cgraph *g) {
     }
 }
 
-// everything the captured launches depend on: per node its op, data pointer, shape,
-// strides and op params, per source its data pointer, type, shape and strides (weights
-// also their prepacked copy and SmoothQuant divisor) -- written into sig, whose capacity
-// is kept from call to call (no allocation once warm)
-void graph_signature(ggml_cgraph *g, std::vector<uint64_t> &sig) {
-    sig.clear();
+// Everything the captured launches depend on, as a word sequence: per computed node its
+// op, type and flags, data pointer, shape, strides and op params; per source its data
+// pointer, type, shape and strides (weights also their prepacked copy and SmoothQuant
+// divisor).  View nodes launch nothing: what they change reaches the launches through
+// their consumers' source entries.  emit(word) returns false to stop the walk.
+template <class Emit>
+bool walk_signature(ggml_cgraph *g, Emit &&emit) {
     const int nn = ggml_graph_n_nodes(g);
-    sig.reserve((size_t)nn * 64);
     for (int i = 0; i < nn; i++) {
         const ggml_tensor *t = ggml_graph_node(g, i);
-        sig.push_back((uint64_t)t->op | ((uint64_t)t->type << 32));
-        sig.push_back((uint64_t)(uintptr_t)t->data);
-        for (int d = 0; d < 4; d++) sig.push_back((uint64_t)t->ne[d]);
-        for (int d = 0; d < 4; d++) sig.push_back((uint64_t)t->nb[d]);
+        if (is_noop(t)) continue;
+        if (!emit((uint64_t)t->op | ((uint64_t)t->type << 16) | ((uint64_t)(uint32_t)t->flags << 32)) ||
+            !emit((uint64_t)(uintptr_t)t->data))
+            return false;
+        for (int d = 0; d < 4; d++)
+            if (!emit((uint64_t)t->ne[d]) || !emit((uint64_t)t->nb[d])) return false;
         for (int p = 0; p < GGML_MAX_OP_PARAMS / 8; p++) {
             uint64_t w;
             memcpy(&w, (const char *)t->op_params + 8 * p, 8);
-            sig.push_back(w);
+            if (!emit(w)) return false;
         }
         for (int s = 0; s < GGML_MAX_SRC; s++) {
             const ggml_tensor *src = t->src[s];
             if (!src) continue;
-            sig.push_back(((uint64_t)s << 56) ^ (uint64_t)(uintptr_t)src->data);
-            sig.push_back((uint64_t)src->type);
-            for (int d = 0; d < 4; d++) sig.push_back((uint64_t)src->ne[d]);
-            for (int d = 1; d < 4; d++) sig.push_back((uint64_t)src->nb[d]);
+            if (!emit(((uint64_t)s << 56) ^ (uint64_t)(uintptr_t)src->data) || !emit((uint64_t)src->type)) return false;
+            for (int d = 0; d < 4; d++)
+                if (!emit((uint64_t)src->ne[d])) return false;
+            for (int d = 1; d < 4; d++)
+                if (!emit((uint64_t)src->nb[d])) return false;
             if (src->extra) {
                 const TensorExtra *ex = (const TensorExtra *)src->extra;
-                sig.push_back((uint64_t)(uintptr_t)ex);
-                sig.push_back((uint64_t)(uintptr_t)ex->inv_s);
+                if (!emit((uint64_t)(uintptr_t)ex) || !emit((uint64_t)(uintptr_t)ex->inv_s)) return false;
             }
         }
     }
+    return true;
 }
 
-// ---- backend iface
+// g against the stored signature, reading both and writing nothing (the per-token case)
+bool signature_matches(ggml_cgraph *g, const std::vector<uint64_t> &sig) {
+    size_t pos = 0;
+    const bool walked = walk_signature(g, [&](uint64_t w) { return pos < sig.size() && sig[pos++] == w; });
+    return walked && pos == sig.size();
+}
+
+void graph_signature(ggml_cgraph *g, std::vector<uint64_t> &sig) {
+    sig.clear();
+    walk_signature(g, [&](uint64_t w) {
+        sig.push_back(w);
+        return true;
+    });
+}
 
 // the last persistent launch's phase timestamps: int32 n_layer, n_wg, n_events, float64
 // clock ticks per microsecond, then uint64 [n_layer][n_wg][n_events]
@@ -1924,15 +1940,14 @@ enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgra
         run_graph_nodes(ctx, cgraph);
         return GGML_STATUS_SUCCESS;
     }
-    std::vector<uint64_t> &sig = ctx->sig_scratch;
-    graph_signature(cgraph, sig);
-    if (ctx->gexec && sig == ctx->signature) {
+    const bool same = signature_matches(cgraph, ctx->signature);
+    if (ctx->gexec && same) {
         MI_HIP_CHECK(hipGraphLaunch(ctx->gexec, ctx->stream));
         return GGML_STATUS_SUCCESS;
     }
     // a changed graph runs eagerly once; when the same graph comes back it is captured
-    if (sig != ctx->signature) {
-        std::swap(ctx->signature, sig);
+    if (!same) {
+        graph_signature(cgraph, ctx->signature);
         ctx->same_calls = 0;
         if (ctx->gexec) {
             MI_HIP_CHECK(hipGraphExecDestroy(ctx->gexec));

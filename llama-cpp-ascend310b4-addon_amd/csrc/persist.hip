@@ -11,9 +11,11 @@
 //   2. attn:   the MFMA flash-decoding split tiles (one per (split, kv head))
 //   3. o:      the splits' log-sum-exp merge (in the combine kernel's exact order), the
 //              o rows, + residual x -> x1
-//   4. gate/up: RMSNorm(x1), SmoothQuant, quantization, the gate and up rows
-//   5. down:   swiglu(gate, up), SmoothQuant, quantization (every workgroup, into LDS),
-//              the down rows, + residual x1 -> the layer output
+//   4. gate/up: RMSNorm(x1), SmoothQuant, quantization, the gate and up rows (each
+//              tile pairs 8 gate rows with the same 8 up rows), swiglu(gate, up) and the
+//              down projection's SmoothQuant divisor
+//   5. down:   Q8_0 quantization of that product (every workgroup, into LDS), the down
+//              rows, + residual x1 -> the layer output
 //
 // Every phase computes what the per-node kernels compute, with the same lane layout,
 // block order and reductions, so a token's logits are bit-identical to the per-node
@@ -45,7 +47,7 @@ using persist_plan::kCtrStride;
 using persist_plan::kHops;
 using persist_plan::Layout;
 constexpr int kPersistMaxSplits = persist_plan::kMaxSplits;
-constexpr int kTraceEvents = 16;  // timestamps per (layer, workgroup); see trace_mark below
+constexpr int kTraceEvents = 24;  // timestamps per (layer, workgroup); see trace_mark below
 
 struct PArgs {
     const mi_persist_layer *layers;
@@ -114,7 +116,7 @@ __device__ __forceinline__ void hop_wait(const PArgs &a, int layer, int hop) {
                 }
             }
             if (__any(stop)) break;
-            __builtin_amdgcn_s_sleep(1);
+            __builtin_amdgcn_s_sleep(20);  // ~0.5 us between polls: 2048 pollers on 8 lines otherwise queue the arrivals
         }
     }
     __syncthreads();
@@ -164,7 +166,7 @@ __device__ __forceinline__ Mat mat_of(const void *packed, int n, int nb) {
 
 // LDS of one workgroup: the k = n_embd activation stage of the fused GEMVs, the down
 // projection's activation (n_ff int8 + n_ff/32 scales), the RoPE tile's 16 results.
-template <int NB_E, int NF, int NH>
+template <int NB_E, int NF, int NH, int NGU>
 struct PLds {
     int8_t qs[NB_E * 32];
     float d[NB_E];
@@ -177,6 +179,7 @@ struct PLds {
     float mg[NH][8], ml[NH][8];              // group maximum and sum
     float mwg[NH][8];                        // group weights
     float mll[NH];                           // the head's total sum
+    float gu[NGU][16];                       // gate (slots 0..7) and up (8..15) rows per tile
 };
 
 template <int XN, int GE, int UE, int GF, int UF, int D, int GQ, int NBW, int NB_E, int NF, int NGU, int NDN>
@@ -187,7 +190,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
     constexpr int NBF = NF / 32;      // down blocks
     // NGU / NDN: gate/up and down tiles per workgroup (all prefetched before the hop)
     constexpr int NH = NB_E * 32 / D;  // query heads (o projection input = NH x D)
-    __shared__ __align__(16) PLds<NB_E, NF, NH> L;
+    __shared__ __align__(16) PLds<NB_E, NF, NH, NGU> L;
     const int tid = threadIdx.x;
     const int wg = blockIdx.x;
     const int nwg = gridDim.x;
@@ -228,7 +231,9 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
     // wall-clock timestamps of one workgroup's phase boundaries (thread 0, when tracing):
     // 0 layer start, 1 q/k/v waited, 2 q/k/v done, 3 attention waited, 4 attention done,
     // 5 o waited, 6 o done, 7 gate/up start, 8 gate/up waited, 9 gate/up done,
-    // 10 down start, 11 down waited, 12 down done
+    // 10 down start, 11 down waited, 12 down done, 13 down activation staged,
+    // 14 o input staged, 15 gate/up input staged, 16 o records requested, 17 o group
+    // weights, 18 o head weights
     auto trace_mark = [&](int layer, int ev) {
         if (a.trace && tid == 0) a.trace[((size_t)layer * nwg + wg) * kTraceEvents + ev] = wall_clock64();
     };
@@ -246,8 +251,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
         float *q_buf = scr + lo.q_off;
         float *part = scr + lo.part_off;
         float *x1 = scr + lo.x1_off;
-        float *gbuf = scr + lo.g_off;
-        float *ubuf = scr + lo.u_off;
+        float *hbuf = scr + lo.h_off;
         // the residual stream: the caller's input and output at the ends of the stack, the
         // per-layer scratch copies in between (each written once per launch)
         const float *x = layer == 0 ? a.x_in : a.scratch + (size_t)(layer - 1) * lo.layer_floats + lo.xr_off;
@@ -262,6 +266,8 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
             int4 wlo[UE], whi[UE];
             uint32_t wdw[UE];
             q8_first_pass<GE, UE>(m.qlo, m.qhi, m.d, rbase, nbE, j, wlo, whi, wdw);
+            const float *bias = qkv_mi == 0 ? P.bq : qkv_mi == 1 ? P.bk : P.bv;
+            const float bvalue = bias ? bias[qkv_row] : 0.0f;
             if (layer > 0) hop_wait(a, layer - 1, 4);
             trace_mark(layer, 1);
             XStage<XN, true> st;
@@ -270,10 +276,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
             xstage_quant(st, P.inv_s_attn, k4, scale, a.rounding, L.qs, L.d, tid);
             __syncthreads();
             const float s = q8_row_dot<GE, UE>(m.qlo, m.qhi, m.d, rbase, nbE, j, wlo, whi, wdw, L.qs, L.d);
-            if (j == 0) {
-                const float *bias = qkv_mi == 0 ? P.bq : qkv_mi == 1 ? P.bk : P.bv;
-                L.y[slot] = bias ? s + bias[qkv_row] : s;
-            }
+            if (j == 0) L.y[slot] = bias ? s + bvalue : s;
             __syncthreads();
             // rope_kv_epilogue with coherent stores
             if (pl.rope) {
@@ -324,6 +327,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
             q8_first_pass<GE, UE>(m.qlo, m.qhi, m.d, rbase, nbE, j, wlo, whi, wdw);
             hop_wait(a, layer, 1);
             trace_mark(layer, 5);
+            const float xres = x[min(row, E - 1)];  // the residual (the layer input)
             // The attention output (the splits' merge), SmoothQuant and Q8_0 quantization of
             // the o projection's input.  The merge is fa_merge_exact4's arithmetic (that of
             // k_fa_combine<D, *, 8> for at most 16 splits) with the per-(head, split group)
@@ -333,17 +337,22 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
             constexpr int PS = part_stride<D>();
             constexpr int NI = (NB_E * 8 + 255) / 256;  // float4 elements per thread
             const int S = a.fa_splits;
-            float4 ov[NI][8][UL];  // this thread's split records, loaded first
+            // this thread's split records, loaded first; slots past the last split (weight
+            // 0 in the merge) and elements past the row (whole waves) are not loaded
+            float4 ov[NI][8][UL];
 #pragma unroll
             for (int it = 0; it < NI; it++) {
                 const int fc = min(tid + it * 256, k4 - 1);
                 const float *ph = part + (size_t)(fc * 4 / D) * S * PS + (fc * 4) % D;
+                const bool in_row = tid + it * 256 < k4;
 #pragma unroll
                 for (int g = 0; g < 8; g++)
 #pragma unroll
                     for (int u = 0; u < UL; u++)
-                        ov[it][g][u] = *(const float4 *)(ph + (size_t)min(g + 8 * u, S - 1) * PS);
+                        ov[it][g][u] = in_row && g + 8 * u < S ? *(const float4 *)(ph + (size_t)(g + 8 * u) * PS)
+                                                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
+            trace_mark(layer, 16);
             if (tid < NH * 8) {  // group g of head h: splits g, g + 8, ...
                 const int h = tid / 8, g = tid % 8;
                 const float *ph = part + (size_t)h * S * PS;
@@ -369,6 +378,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
                 L.ml[h][g] = sum;
             }
             __syncthreads();
+            trace_mark(layer, 17);
             if (tid < NH) {
                 float mm = -INFINITY, ll = 0.0f;
 #pragma unroll
@@ -383,6 +393,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
                 L.mll[tid] = ll;
             }
             __syncthreads();
+            trace_mark(layer, 18);
 #pragma unroll
             for (int it = 0; it < NI; it++) {
                 const int f = tid + it * 256;  // float4 index; 8 consecutive threads form one 32-block
@@ -422,35 +433,40 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
                 }
             }
             __syncthreads();
+            trace_mark(layer, 14);
             const float s = q8_row_dot<GE, UE>(m.qlo, m.qhi, m.d, rbase, nbE, j, wlo, whi, wdw, L.qs, L.d);
-            if (j == 0 && row < E) st_f(x1 + row, s + x[row]);
+            if (j == 0 && row < E) st_f(x1 + row, s + xres);
             hop_arrive(a, layer, 2);
             trace_mark(layer, 6);
         }
 
-        // ================= phase 4: FFN norm + gate/up
+        // ================= phase 4: FFN norm + gate/up + swiglu
         {
             trace_mark(layer, 7);
             const Mat mg = mat_of(P.w_gate, a.n_ff, nbE), mu = mat_of(P.w_up, a.n_ff, nbE);
-            const int n_tot = 2 * a.n_ff;
-            // the workgroup's tiles wg, wg + nwg, ... (rows of [gate; up]) stream through a
-            // ring of NPRE register sets: the first NPRE are loaded before the hop, tile
-            // i + NPRE as soon as tile i's dot has consumed its set
-            constexpr int NPRE = NGU < 3 ? NGU : 3;
-            int4 wlo[NPRE][UE], whi[NPRE][UE];
-            uint32_t wdw[NPRE][UE];
-            auto gu_load = [&](int i, int set) {
+            // tile t holds gate rows 8t .. 8t+7 (slots 0..7) and the same up rows (slots
+            // 8..15), so the workgroup forms k_swiglu_quant_q8_0's product for its rows
+            // itself; its tiles are wg, wg + nwg, ...
+            constexpr int HR = RPB / 2;  // rows of each matrix per tile
+            const Mat &mm = slot < HR ? mg : mu;
+            int4 wlo[NGU][UE], whi[NGU][UE];
+            uint32_t wdw[NGU][UE];
+            auto gu_load = [&](int i) {
                 const int t = wg + i * nwg;
                 if (t < lo.n_gu_tiles) {
-                    const int grow = min(t * RPB + slot, n_tot - 1);
-                    const bool up = grow >= a.n_ff;
-                    const size_t rbase = (size_t)(up ? grow - a.n_ff : grow) * nbE;
-                    q8_first_pass<GE, UE>(up ? mu.qlo : mg.qlo, up ? mu.qhi : mg.qhi, up ? mu.d : mg.d, rbase, nbE,
-                                          j, wlo[set], whi[set], wdw[set]);
+                    const size_t rbase = (size_t)(t * HR + slot % HR) * nbE;
+                    q8_first_pass<GE, UE>(mm.qlo, mm.qhi, mm.d, rbase, nbE, j, wlo[i], whi[i], wdw[i]);
                 }
             };
+            // all of them load ahead of the hop: most workgroups reach this phase long
+            // before it, while the attention and o phases leave HBM idle
 #pragma unroll
-            for (int i = 0; i < NPRE; i++) gu_load(i, i);
+            for (int i = 0; i < NGU; i++) gu_load(i);
+            // the down projection's SmoothQuant divisor of this thread's swiglu row
+            const int sw_i = tid / HR, sw_r = tid % HR;
+            const int sw_t = wg + sw_i * nwg;
+            const bool sw_row = tid < NGU * HR && sw_t < lo.n_gu_tiles;
+            const float sw_s = sw_row && P.inv_s_down ? P.inv_s_down[sw_t * HR + sw_r] : 1.0f;
             hop_wait(a, layer, 2);
             trace_mark(layer, 8);
             XStage<XN, true> st;
@@ -458,87 +474,78 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
             const float scale = xstage_scale(st, k4, a.eps, L.red, tid);
             xstage_quant(st, P.inv_s_ffn, k4, scale, a.rounding, L.qs, L.d, tid);
             __syncthreads();
+            trace_mark(layer, 15);
 #pragma unroll
             for (int i = 0; i < NGU; i++) {
                 const int t = wg + i * nwg;
-                const int set = i % NPRE;
                 if (t < lo.n_gu_tiles) {
-                    const int grow = t * RPB + slot;
-                    const int gr = min(grow, n_tot - 1);
-                    const bool up = gr >= a.n_ff;
-                    const size_t rbase = (size_t)(up ? gr - a.n_ff : gr) * nbE;
-                    const float s = q8_row_dot<GE, UE>(up ? mu.qlo : mg.qlo, up ? mu.qhi : mg.qhi, up ? mu.d : mg.d,
-                                                       rbase, nbE, j, wlo[set], whi[set], wdw[set], L.qs, L.d);
-                    if (j == 0 && grow < n_tot) st_f((up ? ubuf : gbuf) + (up ? grow - a.n_ff : grow), s);
+                    const size_t rbase = (size_t)(t * HR + slot % HR) * nbE;
+                    const float sd = q8_row_dot<GE, UE>(mm.qlo, mm.qhi, mm.d, rbase, nbE, j, wlo[i], whi[i], wdw[i],
+                                                        L.qs, L.d);
+                    if (j == 0) L.gu[i][slot] = sd;
                 }
-                if (i + NPRE < NGU) gu_load(i + NPRE, set);
+            }
+            __syncthreads();
+            if (sw_row) {  // k_swiglu_quant_q8_0's product (before its quantization)
+                const float g = L.gu[sw_i][sw_r], u = L.gu[sw_i][sw_r + HR];
+                float v = (g / (1.0f + expf(-g))) * u;
+                if (P.inv_s_down) v *= sw_s;
+                st_f(hbuf + sw_t * HR + sw_r, v);
             }
             if (persist_plan::is_gu(lo, wg)) hop_arrive(a, layer, 3);
             trace_mark(layer, 9);
         }
 
-        // ================= phase 5: swiglu + quant (every workgroup) + down + residual
+        // ================= phase 5: quantization (every workgroup) + down + residual
         {
             trace_mark(layer, 10);
             const Mat md = mat_of(P.w_down, E, NBF);
             const int jf = tid % GF;
+            // the weights load ahead of the hop, the product after it
             int4 wlo[NDN][UF], whi[NDN][UF];
             uint32_t wdw[NDN][UF];
+            auto dn_load = [&]() {
 #pragma unroll
-            for (int i = 0; i < NDN; i++) {
-                const int t = wg + i * nwg;
-                if (t < lo.n_down_tiles) {
-                    const int row = min(t * RPBF + tid / GF, E - 1);
-                    const size_t rbase = (size_t)row * NBF;
+                for (int i = 0; i < NDN; i++) {
+                    const int t = wg + i * nwg;
+                    if (t < lo.n_down_tiles) {
+                        const int row = min(t * RPBF + tid / GF, E - 1);
+                        const size_t rbase = (size_t)row * NBF;
 #pragma unroll
-                    for (int u = 0; u < UF; u++) {
-                        const int b = min(jf + u * GF, NBF - 1);
-                        wlo[i][u] = ld_stream16(md.qlo + (rbase + b) * 16);
-                        whi[i][u] = ld_stream16(md.qhi + (rbase + b) * 16);
-                        wdw[i][u] = md.d[rbase + b];
+                        for (int u = 0; u < UF; u++) {
+                            const int b = min(jf + u * GF, NBF - 1);
+                            wlo[i][u] = ld_stream16(md.qlo + (rbase + b) * 16);
+                            whi[i][u] = ld_stream16(md.qhi + (rbase + b) * 16);
+                            wdw[i][u] = md.d[rbase + b];
+                        }
                     }
                 }
-            }
+            };
+            dn_load();
+            float xres[NDN];  // the residual x1 (complete since hop 2)
+#pragma unroll
+            for (int i = 0; i < NDN; i++) xres[i] = x1[min((wg + i * nwg) * RPBF + tid / GF, E - 1)];
             hop_wait(a, layer, 3);
             trace_mark(layer, 11);
-            // k_swiglu_quant_q8_0's arithmetic for every 32-block of the row, into LDS, in
-            // batches of SWB passes of 32 blocks: a batch's loads first, then its math
-            constexpr int NSW = (NBF + 31) / 32;
-            constexpr int SWB = 3;
+            constexpr int NSW = (NBF + 31) / 32;  // passes of 32 blocks
             const int sub = tid % 8;
+            float4 hv[NSW];
 #pragma unroll
-            for (int p0 = 0; p0 < NSW; p0 += SWB) {
-                float4 gv[SWB], uv[SWB], sv[SWB];
+            for (int p = 0; p < NSW; p++)
+                hv[p] = *(const float4 *)(hbuf + min(p * 32 + tid / 8, NBF - 1) * 32 + sub * 4);
+            // k_swiglu_quant_q8_0's quantization of every 32-block of the product, into LDS
 #pragma unroll
-                for (int q = 0; q < SWB; q++) {
-                    const int e = min((p0 + q) * 32 + tid / 8, NBF - 1) * 32 + sub * 4;
-                    gv[q] = *(const float4 *)(gbuf + e);
-                    uv[q] = *(const float4 *)(ubuf + e);
-                    sv[q] = P.inv_s_down ? *(const float4 *)(P.inv_s_down + e) : make_float4(1.f, 1.f, 1.f, 1.f);
-                }
-#pragma unroll
-                for (int q = 0; q < SWB; q++) {
-                    const int blk = (p0 + q) * 32 + tid / 8;
-                    float4 v;
-                    v.x = (gv[q].x / (1.0f + expf(-gv[q].x))) * uv[q].x;
-                    v.y = (gv[q].y / (1.0f + expf(-gv[q].y))) * uv[q].y;
-                    v.z = (gv[q].z / (1.0f + expf(-gv[q].z))) * uv[q].z;
-                    v.w = (gv[q].w / (1.0f + expf(-gv[q].w))) * uv[q].w;
-                    if (P.inv_s_down) {
-                        v.x *= sv[q].x;
-                        v.y *= sv[q].y;
-                        v.z *= sv[q].z;
-                        v.w *= sv[q].w;
-                    }
-                    float d;
-                    const uint32_t qv = quant4(v.x, v.y, v.z, v.w, a.rounding, d);  // every lane: whole 8-lane groups
-                    if (blk < NBF) {
-                        *(uint32_t *)(L.fqs + blk * 32 + sub * 4) = qv;
-                        if (sub == 0) L.fd[blk] = h2f(f2h(d));
-                    }
+            for (int p = 0; p < NSW; p++) {
+                const int blk = p * 32 + tid / 8;
+                float d;
+                const uint32_t qv = quant4(hv[p].x, hv[p].y, hv[p].z, hv[p].w, a.rounding, d);  // whole 8-lane groups
+                if (blk < NBF) {
+                    *(uint32_t *)(L.fqs + blk * 32 + sub * 4) = qv;
+                    if (sub == 0) L.fd[blk] = h2f(f2h(d));
                 }
             }
             __syncthreads();
+            trace_mark(layer, 13);
             // k_gemv_q8_0_xq<GF, UF, 1>'s row dot (one pass covers the row: UF * GF >= NBF)
 #pragma unroll
             for (int i = 0; i < NDN; i++) {
@@ -556,7 +563,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
                         }
                     }
                     const float s = group_sum<GF>(acc);
-                    if (jf == 0 && row < E) st_f(x_out + row, s + x1[row]);
+                    if (jf == 0 && row < E) st_f(x_out + row, s + xres[i]);
                 }
             }
             if (persist_plan::is_down(lo, wg)) hop_arrive(a, layer, 4);

@@ -12,6 +12,7 @@
 //   1 attention   workgroups fa0 .. fa0+n_fa-1           o tiles                (hop 1)
 //   2 o           workgroups o0 .. o0+n_o_tiles-1        every workgroup        (hop 2)
 //   3 gate/up     every workgroup with a tile            every workgroup        (hop 3)
+//     (+ swiglu)
 //   4 down        every workgroup with a tile            next layer's q/k/v     (hop 4)
 //
 // The three first phases run on disjoint workgroups, so the attention of layer l can
@@ -41,8 +42,9 @@ struct Layout {
     int n_qkv_tiles, n_fa, n_o_tiles, n_gu_tiles, n_down_tiles;
     int fa0, o0;        // first workgroup of the attention and o tiles
     int hop_first[kHops], hop_count[kHops];  // producers: workgroups first .. first+count-1 (mod n_wg)
-    // per-layer scratch (floats): q, attention split records, x1 = o + x, gate, up, layer output
-    size_t q_off, part_off, x1_off, g_off, u_off, xr_off, layer_floats;
+    // per-layer scratch (floats): q, attention split records, x1 = o + x, the swiglu
+    // product (SmoothQuant-divided), layer output
+    size_t q_off, part_off, x1_off, h_off, xr_off, layer_floats;
 };
 
 MI_PLAN_HD inline size_t round_up64(size_t v) { return (v + 63) / 64 * 64; }
@@ -58,7 +60,7 @@ MI_PLAN_HD inline Layout make_layout(int n_wg, int n_embd, int n_head, int n_hea
     lo.n_qkv_tiles = (lo.n_q + lo.n_k + lo.n_v) / kRowsE;
     lo.n_fa = fa_splits * n_head_kv;
     lo.n_o_tiles = n_embd / kRowsE;
-    lo.n_gu_tiles = 2 * n_ff / kRowsE;
+    lo.n_gu_tiles = 2 * n_ff / kRowsE;  // 8 gate rows + the same 8 up rows each
     lo.n_down_tiles = n_embd / kRowsF;
     lo.fa0 = lo.n_qkv_tiles % n_wg;
     lo.o0 = (lo.fa0 + lo.n_fa) % n_wg;
@@ -71,9 +73,8 @@ MI_PLAN_HD inline Layout make_layout(int n_wg, int n_embd, int n_head, int n_hea
     lo.q_off = 0;
     lo.part_off = round_up64((size_t)lo.n_q);
     lo.x1_off = lo.part_off + round_up64((size_t)n_head * kMaxSplits * part_rec);
-    lo.g_off = lo.x1_off + round_up64((size_t)n_embd);
-    lo.u_off = lo.g_off + round_up64((size_t)n_ff);
-    lo.xr_off = lo.u_off + round_up64((size_t)n_ff);
+    lo.h_off = lo.x1_off + round_up64((size_t)n_embd);
+    lo.xr_off = lo.h_off + round_up64((size_t)n_ff);
     lo.layer_floats = lo.xr_off + round_up64((size_t)n_embd);
     return lo;
 }
