@@ -153,18 +153,30 @@ __device__ __forceinline__ half4_t h4(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(half4_t, t);
 }
 
+struct FaNoWait {
+    __device__ void operator()() const {}
+};
+
 // One (split, kv head, sequence) tile of the MFMA flash-decoding kernel: a workgroup of
 // NW waves (64*NW threads).  Partials go to part (coherent: written through with
 // agent-scope stores, for readers on other XCDs within the same launch), or straight to
 // out when there is one split.
-template <int D, int GQ, bool MASK, int NBW, int NW = 4>
+//
+// The first K / V loads are issued before q is read.  A caller whose q and newest cache
+// row are produced in the same launch passes wait (called by every thread between the
+// first K / V loads and the q loads) and late_row, the row written behind that wait:
+// lanes whose first-block row is late_row load it after wait, so no line of it is cached
+// before it was written.  (NBW == 1 only; the plain kernel passes FaNoWait and -1.)
+template <int D, int GQ, bool MASK, int NBW, int NW = 4, class Wait = FaNoWait>
 __device__ __forceinline__ void fa_mfma_tile(const float *__restrict__ q, const uint8_t *__restrict__ kc,
                                              const uint8_t *__restrict__ vc, const uint16_t *__restrict__ mask,
                                              const int32_t *__restrict__ kv_len_p, int n_kv, size_t k_nb1,
                                              size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, int chunk,
                                              int n_splits, float *__restrict__ part, float *__restrict__ out,
                                              bool coherent, const FaSeq &sq, int split, int kvh, int seq,
-                                             int n_kvh) {
+                                             int n_kvh, int late_row = -1, Wait wait = Wait{}) {
+    constexpr bool kLate = !std::is_same<Wait, FaNoWait>::value;
+    static_assert(!kLate || NBW == 1, "a wait inside the tile needs NBW == 1");
     {
         q += (size_t)seq * sq.q;
         kc += (size_t)seq * sq.k;
@@ -199,7 +211,7 @@ __device__ __forceinline__ void fa_mfma_tile(const float *__restrict__ q, const 
     // q fragment (B operand): lane (g, c) holds head c, dims 32*(s/2) + 8g + 4*(s%2) .. +3
     // for step s, the dims its K chunks hold
     half4_t qf[KS];
-    {
+    auto load_q = [&]() {
         const float *qh = q + (size_t)(kvh * GQ + min(c, GQ - 1)) * D + 8 * g;
 #pragma unroll
         for (int s2 = 0; s2 < KS; s2++) {
@@ -208,7 +220,8 @@ __device__ __forceinline__ void fa_mfma_tile(const float *__restrict__ q, const 
             const uint32_t b = (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16);
             qf[s2] = c < GQ ? h4(a, b) : h4(0u, 0u);
         }
-    }
+    };
+    if constexpr (!kLate) load_q();
 
     const uint8_t *kb = kc + (size_t)kvh * k_nb2 + (size_t)16 * g;
     const uint8_t *vb = vc + (size_t)kvh * v_nb2 + (size_t)(D / 8) * c;
@@ -223,9 +236,13 @@ __device__ __forceinline__ void fa_mfma_tile(const float *__restrict__ q, const 
     U32s<VW> vr[2][4];
     auto issue = [&](int blk, int buf) {
         const int p0 = wstart + blk * 16;
-        ld_k_chunks<D / 32>(kr[buf].w, kb + (size_t)min(p0 + c, last) * k_nb1);
+        const int kro = min(p0 + c, last);
+        if (!kLate || kro != late_row) ld_k_chunks<D / 32>(kr[buf].w, kb + (size_t)kro * k_nb1);
 #pragma unroll
-        for (int r = 0; r < 4; r++) ld_bytes<D / 8>(vr[buf][r].w, vb + (size_t)min(p0 + 4 * g + r, last) * v_nb1);
+        for (int r = 0; r < 4; r++) {
+            const int vro = min(p0 + 4 * g + r, last);
+            if (!kLate || vro != late_row) ld_bytes<D / 8>(vr[buf][r].w, vb + (size_t)vro * v_nb1);
+        }
     };
     // one 16-position block: scores, online softmax, P.V (buffer buf holds its K / V)
     auto step = [&](int blk, auto bufc) {
@@ -294,6 +311,17 @@ __device__ __forceinline__ void fa_mfma_tile(const float *__restrict__ q, const 
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
     issue(0, 0);
+    if constexpr (kLate) {
+        wait();
+        load_q();
+        const int kro = min(wstart + c, last);
+        if (kro == late_row) ld_k_chunks<D / 32>(kr[0].w, kb + (size_t)kro * k_nb1);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int vro = min(wstart + 4 * g + r, last);
+            if (vro == late_row) ld_bytes<D / 8>(vr[0][r].w, vb + (size_t)vro * v_nb1);
+        }
+    }
     if constexpr (NBW == 1) {
         step(0, B0{});
     } else {

@@ -258,6 +258,28 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
         float *x_out = layer == a.n_layer - 1 ? a.x_out : scr + lo.xr_off;
         const int nbE = NB_E;
 
+        // the gate/up weights of this workgroup's phase-4 tiles (tile t: gate rows 8t .. 8t+7
+        // in slots 0..7, the same up rows in slots 8..15; tiles wg, wg + nwg, ...), loaded
+        // ahead of phase 4's hop: by the o workgroups before their phase 3 (they reach
+        // phase 4 just before its hop, and a poll behind in-flight loads would come back
+        // late), by the others at the start of phase 4
+        constexpr int HR = RPB / 2;  // rows of each matrix per gate/up tile
+        const Mat mg = mat_of(P.w_gate, a.n_ff, nbE), mu = mat_of(P.w_up, a.n_ff, nbE);
+        const Mat &mm = slot < HR ? mg : mu;
+        int4 gwlo[NGU][UE], gwhi[NGU][UE];
+        uint32_t gwdw[NGU][UE];
+        auto gu_prefetch = [&]() {
+#pragma unroll
+            for (int i = 0; i < NGU; i++) {
+                const int t = wg + i * nwg;
+                if (t < lo.n_gu_tiles) {
+                    const size_t rbase = (size_t)(t * HR + slot % HR) * nbE;
+                    q8_first_pass<GE, UE>(mm.qlo, mm.qhi, mm.d, rbase, nbE, j, gwlo[i], gwhi[i], gwdw[i]);
+                }
+            }
+        };
+        const bool o_role = persist_plan::is_o(lo, wg);
+
         // ================= phase 1: q/k/v + RoPE + KV write
         if (has_qkv) {
             const Mat m = mat_of(qkv_mi == 0 ? P.wq : qkv_mi == 1 ? P.wk : P.wv,
@@ -306,19 +328,24 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
 
         // ================= phase 2: attention split tiles
         if (persist_plan::is_fa(lo, wg)) {
-            hop_wait(a, layer, 0);
-            trace_mark(layer, 3);
+            // the K / V rows of the tile load ahead of the hop, except the row this token
+            // writes in phase 1 (loaded after it, so no stale copy of it is cached)
             const FaSeq sq = {0, 0, 0, 0, 0};
             fa_mfma_tile<D, GQ, false, NBW, 4>(q_buf, (const uint8_t *)P.k_cache, (const uint8_t *)P.v_cache, nullptr,
                                                a.kv_len, a.n_kv, a.kv_row_bytes, (size_t)a.hd * 2, a.kv_row_bytes,
                                                (size_t)a.hd * 2, a.kq_scale, a.fa_chunk, a.fa_splits, part, nullptr,
-                                               true, sq, fa_t % a.fa_splits, fa_t / a.fa_splits, 0, a.n_head_kv);
+                                               true, sq, fa_t % a.fa_splits, fa_t / a.fa_splits, 0, a.n_head_kv,
+                                               ci_ok ? (int)ci : -1, [&]() {
+                                                   hop_wait(a, layer, 0);
+                                                   trace_mark(layer, 3);
+                                               });
             hop_arrive(a, layer, 1);
             trace_mark(layer, 4);
         }
 
         // ================= phase 3: merge + o + residual
-        if (persist_plan::is_o(lo, wg)) {
+        if (o_role) {
+            gu_prefetch();
             const Mat m = mat_of(P.wo, E, nbE);
             const int row = o_t * RPB + slot;
             const size_t rbase = (size_t)row * nbE;
@@ -443,25 +470,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
         // ================= phase 4: FFN norm + gate/up + swiglu
         {
             trace_mark(layer, 7);
-            const Mat mg = mat_of(P.w_gate, a.n_ff, nbE), mu = mat_of(P.w_up, a.n_ff, nbE);
-            // tile t holds gate rows 8t .. 8t+7 (slots 0..7) and the same up rows (slots
-            // 8..15), so the workgroup forms k_swiglu_quant_q8_0's product for its rows
-            // itself; its tiles are wg, wg + nwg, ...
-            constexpr int HR = RPB / 2;  // rows of each matrix per tile
-            const Mat &mm = slot < HR ? mg : mu;
-            int4 wlo[NGU][UE], whi[NGU][UE];
-            uint32_t wdw[NGU][UE];
-            auto gu_load = [&](int i) {
-                const int t = wg + i * nwg;
-                if (t < lo.n_gu_tiles) {
-                    const size_t rbase = (size_t)(t * HR + slot % HR) * nbE;
-                    q8_first_pass<GE, UE>(mm.qlo, mm.qhi, mm.d, rbase, nbE, j, wlo[i], whi[i], wdw[i]);
-                }
-            };
-            // all of them load ahead of the hop: most workgroups reach this phase long
-            // before it, while the attention and o phases leave HBM idle
-#pragma unroll
-            for (int i = 0; i < NGU; i++) gu_load(i);
+            if (!o_role) gu_prefetch();
             // the down projection's SmoothQuant divisor of this thread's swiglu row
             const int sw_i = tid / HR, sw_r = tid % HR;
             const int sw_t = wg + sw_i * nwg;
@@ -480,8 +489,8 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
                 const int t = wg + i * nwg;
                 if (t < lo.n_gu_tiles) {
                     const size_t rbase = (size_t)(t * HR + slot % HR) * nbE;
-                    const float sd = q8_row_dot<GE, UE>(mm.qlo, mm.qhi, mm.d, rbase, nbE, j, wlo[i], whi[i], wdw[i],
-                                                        L.qs, L.d);
+                    const float sd = q8_row_dot<GE, UE>(mm.qlo, mm.qhi, mm.d, rbase, nbE, j, gwlo[i], gwhi[i],
+                                                        gwdw[i], L.qs, L.d);
                     if (j == 0) L.gu[i][slot] = sd;
                 }
             }
@@ -507,8 +516,8 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
             auto dn_load = [&]() {
 #pragma unroll
                 for (int i = 0; i < NDN; i++) {
-                    const int t = wg + i * nwg;
-                    if (t < lo.n_down_tiles) {
+                    const int t = persist_plan::down_tile(lo, wg, i);
+                    if (t >= 0) {
                         const int row = min(t * RPBF + tid / GF, E - 1);
                         const size_t rbase = (size_t)row * NBF;
 #pragma unroll
@@ -524,7 +533,8 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
             dn_load();
             float xres[NDN];  // the residual x1 (complete since hop 2)
 #pragma unroll
-            for (int i = 0; i < NDN; i++) xres[i] = x1[min((wg + i * nwg) * RPBF + tid / GF, E - 1)];
+            for (int i = 0; i < NDN; i++)
+                xres[i] = x1[min(max(persist_plan::down_tile(lo, wg, i), 0) * RPBF + tid / GF, E - 1)];
             hop_wait(a, layer, 3);
             trace_mark(layer, 11);
             constexpr int NSW = (NBF + 31) / 32;  // passes of 32 blocks
@@ -549,8 +559,8 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
             // k_gemv_q8_0_xq<GF, UF, 1>'s row dot (one pass covers the row: UF * GF >= NBF)
 #pragma unroll
             for (int i = 0; i < NDN; i++) {
-                const int t = wg + i * nwg;
-                if (t < lo.n_down_tiles) {
+                const int t = persist_plan::down_tile(lo, wg, i);
+                if (t >= 0) {
                     const int row = t * RPBF + tid / GF;
                     float acc = 0.0f;
 #pragma unroll

@@ -95,6 +95,15 @@ MI_PLAN_HD inline bool is_o(const Layout &lo, int wg) { return o_tile(lo, wg) < 
 MI_PLAN_HD inline bool is_gu(const Layout &lo, int wg) { return wg < lo.n_gu_tiles; }
 MI_PLAN_HD inline bool is_down(const Layout &lo, int wg) { return wg < lo.n_down_tiles; }
 
+// down tile i (0 or 1) of workgroup wg, or -1: every workgroup has tile wg; the tiles
+// past n_wg go to the last workgroups (wg >= 2 n_wg - n_down_tiles), whose q/k/v and
+// gate/up shares are the lighter ones
+MI_PLAN_HD inline int down_tile(const Layout &lo, int wg, int i) {
+    if (i == 0) return wg < lo.n_down_tiles ? wg : -1;
+    const int extra = lo.n_down_tiles - lo.n_wg;
+    return extra > 0 && wg >= lo.n_wg - extra ? wg + extra : -1;
+}
+
 // arrivals expected on counter j (0..7) of hop h: the producers (first + t) mod n_wg,
 // t < count, whose id mod 8 is j (n_wg is a multiple of 8, so (first + t) mod 8 == j)
 MI_PLAN_HD inline unsigned hop_want(const Layout &lo, int h, int j) {

@@ -153,6 +153,23 @@ int main(int argc, char **argv) {
         printf("unfit\n");
         return 3;
     }
+    {  // every down tile has exactly one workgroup
+        std::vector<int> cover(lo.n_down_tiles, 0);
+        for (int w = 0; w < n_wg; w++)
+            for (int i = 0; i < 2; i++) {
+                const int t = down_tile(lo, w, i);
+                if (t >= lo.n_down_tiles) {
+                    printf("down tile %d of workgroup %d out of range\n", t, w);
+                    return 5;
+                }
+                if (t >= 0) cover[t]++;
+            }
+        for (int t = 0; t < lo.n_down_tiles; t++)
+            if (cover[t] != 1) {
+                printf("down tile %d covered %d times\n", t, cover[t]);
+                return 5;
+            }
+    }
     long expected = 0;
     for (int h = 0; h < kHops; h++) {
         long sum = 0;
