@@ -9,7 +9,10 @@ Prints ONE JSON line.  Phases:
      SmoothQuant, RoPE, fp16 KV cache write, GQA flash-decoding, SwiGLU, residuals,
      tied fp16 head, argmax) run by ggml_backend_graph_compute, replayed as a HIP graph;
      the argmax is read back to the host each step, as llama.cpp's sampler does.
-     tokens/s = K / elapsed, bracketed by device synchronisation.
+     tokens/s = K / elapsed, bracketed by device synchronisation.  Both decode paths of
+     the backend are timed: the persistent one (all 28 layers in one launch,
+     GGML_MI355X_PERSIST=1; the headline by default) and the per-node one (one launch
+     per fused node group); their greedy tokens are compared.
   2. roofline: the dominant kernel, the grouped gate+up Q8_0 GEMV of one layer (two
      8960 x 1536 matrices on one activation row, one launch), timed live with HIP events
      over back-to-back launches on the stream they are issued to, rotating through enough
@@ -458,6 +461,8 @@ def main():
                     help="qwen2-7b-w4a16: the 7B-shaped W4A16 decode at a 32K context (see --batch)")
     ap.add_argument("--batch", type=int, default=1, help="independent sequences for qwen2-7b-w4a16 (1..8)")
     ap.add_argument("--quick", action="store_true", help="skip the configs leg (C1, C2, C3, C5)")
+    ap.add_argument("--decode-path", default="persistent", choices=["persistent", "per-node"],
+                    help="the C4 headline's decode path (the other one is timed too and reported beside it)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); how the decode path "
@@ -482,27 +487,41 @@ def main():
         print(json.dumps({"roofline": measure_roofline(mi, qs, hp, np.random.default_rng(SEED + 1))}))
         return
     tensors, smooth = qs.synth(hp, seed=SEED)
-    model = mi.Qwen2Model(hp)
-    model.load(tensors, smooth)
-    rng = np.random.default_rng(SEED + 1)
-    prompt = rng.integers(0, hp["n_vocab"], PREFILL)
 
-    log("1.5B model loaded")
-    # context: 512 tokens, one per step (untimed), then the warm-up decode steps
-    nxt = 0
-    for i, t in enumerate(prompt):
-        nxt = model.decode(int(t), i)
-    if warm:
-        wt, _ = model.decode_steps(nxt, PREFILL, warm)
-        nxt = int(wt[-1])
-    pos0 = PREFILL + warm
-    mi.device_sync()
-    t0 = time.perf_counter()
-    toks, _ = model.decode_steps(nxt, pos0, args.steps)
-    mi.device_sync()
-    el = time.perf_counter() - t0
+    def c4_run(persistent):
+        """the C4 decode through one of the backend's two decode paths; returns the model
+        (still loaded), the last token, the first timed position, the timed tokens and
+        the elapsed seconds"""
+        os.environ["GGML_MI355X_PERSIST"] = "1" if persistent else "0"
+        model = mi.Qwen2Model(hp)
+        model.load(tensors, smooth)
+        rng = np.random.default_rng(SEED + 1)
+        prompt = rng.integers(0, hp["n_vocab"], PREFILL)
+        log(f"1.5B model loaded ({'persistent' if persistent else 'per-node'} decode)")
+        # context: 512 tokens, one per step (untimed), then the warm-up decode steps
+        nxt = 0
+        for i, t in enumerate(prompt):
+            nxt = model.decode(int(t), i)
+        if warm:
+            wt, _ = model.decode_steps(nxt, PREFILL, warm)
+            nxt = int(wt[-1])
+        pos0 = PREFILL + warm
+        mi.device_sync()
+        t0 = time.perf_counter()
+        toks, _ = model.decode_steps(nxt, pos0, args.steps)
+        mi.device_sync()
+        return model, nxt, pos0, toks, time.perf_counter() - t0
+
+    persistent = args.decode_path == "persistent"
+    # the other path first (its model freed), then the headline path
+    other, _, _, other_toks, other_el = c4_run(not persistent)
+    other.free()
+    other_tok_s = args.steps / other_el
+    log(f"C4 decode, {'per-node' if persistent else 'persistent'} path: {other_tok_s:.1f} tok/s")
+    model, nxt, pos0, toks, el = c4_run(persistent)
     tok_s = args.steps / el
     step_bytes = qs.weight_bytes(hp) + qs.kv_bytes_per_position(hp) * (pos0 + args.steps // 2)
+    rng = np.random.default_rng(SEED + 2)
 
     log(f"C4 decode: {tok_s:.1f} tok/s")
     roof = None if args.no_roofline else measure_roofline(mi, qs, hp, rng)
@@ -535,6 +554,10 @@ def main():
                         "hidden 1536, 12q/2kv heads x 128, FFN 8960, vocab 151936 tied fp16 head; 512-token "
                         "context then the timed decode tokens, through ggml_backend_graph_compute",
             "context": PREFILL, "graph": not args.no_graph,
+            "decode_path": args.decode_path + (" (one persistent launch for the 28 layers, GGML_MI355X_PERSIST=1)"
+                                               if persistent else " (one launch per fused node group)"),
+            "other_path_tok_s": round(other_tok_s, 2),
+            "other_path_same_tokens": [int(t) for t in other_toks] == [int(t) for t in toks],
             "bytes_per_step": step_bytes,
             "step_GBps": round(step_bytes * args.steps / el / 1e9, 1),
             "step_roofline_frac": round(step_bytes * args.steps / el / 1e9 / HBM_PEAK_GBS, 4),

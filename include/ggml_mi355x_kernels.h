@@ -142,7 +142,7 @@ int mi_mul_mat_q8_0_f32_multi(void *stream, int n_mats, const void *const *w_pac
  * SmoothQuant), ADD, ROPE, SET_ROWS, FLASH_ATTN_EXT (patch:1370-1432), GLU.
  * A grid of one resident workgroup per CU walks every layer through five phases
  * (q/k/v + RoPE + KV write; attention splits; split merge + o + residual; RMSNorm +
- * gate/up; swiglu + quantization + down + residual) separated by in-kernel dependency
+ * gate/up + swiglu; quantization + down + residual) separated by in-kernel dependency
  * hops; results are bit-identical to the per-node launches.  Shapes: Qwen2.5-1.5B-like
  * (n_embd 1536, head_dim 128, 6 q heads per kv head, n_ff 8960), one sequence, an
  * attention view of at most 1024 positions (16 splits), 256 CUs.
