@@ -10,9 +10,9 @@ Prints ONE JSON line.  Phases:
      tied fp16 head, argmax) run by ggml_backend_graph_compute, replayed as a HIP graph;
      the argmax is read back to the host each step, as llama.cpp's sampler does.
      tokens/s = K / elapsed, bracketed by device synchronisation.  Both decode paths of
-     the backend are timed: the persistent one (all 28 layers in one launch,
-     GGML_MI355X_PERSIST=1; the headline by default) and the per-node one (one launch
-     per fused node group); their greedy tokens are compared.
+     the backend are timed: the per-node one (one launch per fused node group, the
+     backend's default and the headline) and the persistent one (all 28 layers in one
+     launch, GGML_MI355X_PERSIST=1, reported beside it); their greedy tokens are compared.
   2. roofline: the dominant kernel, the grouped gate+up Q8_0 GEMV of one layer (two
      8960 x 1536 matrices on one activation row, one launch), timed live with HIP events
      over back-to-back launches on the stream they are issued to, rotating through enough
@@ -461,8 +461,9 @@ def main():
                     help="qwen2-7b-w4a16: the 7B-shaped W4A16 decode at a 32K context (see --batch)")
     ap.add_argument("--batch", type=int, default=1, help="independent sequences for qwen2-7b-w4a16 (1..8)")
     ap.add_argument("--quick", action="store_true", help="skip the configs leg (C1, C2, C3, C5)")
-    ap.add_argument("--decode-path", default="persistent", choices=["persistent", "per-node"],
-                    help="the C4 headline's decode path (the other one is timed too and reported beside it)")
+    ap.add_argument("--decode-path", default="per-node", choices=["per-node", "persistent"],
+                    help="the C4 headline's decode path (the other one is timed too and reported beside it); "
+                         "per-node is the backend's default, and the roofline leg times its dominant launch")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); how the decode path "
