@@ -370,9 +370,9 @@ __global__ __launch_bounds__(64 * NW) void k_fa_mfma(const float *__restrict__ q
 // Parallel log-sum-exp combine: grid (q head, D/32 dim slices, sequence), 256 threads =
 // 32 dims x 8 split groups.  A thread merges splits g, g+8, ... of its group itself
 // (online: running maximum, rescaled sums), loading every split's m, l and output value
-// of an 8U-split chunk at once, so a chunk costs one round trip (U = 16 above 64 splits:
-// 128 splits, 256 positions each at 32K, then take one round trip, not two in a
-// dependent loop; at most 64 splits keep U = 8 and its merge order); the 8 groups then merge
+// of an 8U-split chunk at once, so a chunk costs one round trip (U = 16 above 64 splits,
+// U = 32 above 128: up to 256 splits, 128 positions each at 32K, take one round trip,
+// not two in a dependent loop; at most 64 splits keep U = 8 and its merge order); the 8 groups then merge
 // through LDS.  w_s = 2^(m_s - M), 0 for a split with no position; out = sum w_s o_s /
 // sum w_s l_s, 0 when no split has a position.
 //
@@ -529,7 +529,10 @@ int launch_split_m(hipStream_t st, const FaArgs &a, const FaPlan &p) {
     if ((p.n_splits > 1 || a.xp) && !a.partials_only) {
         const dim3 cg((unsigned)(a.n_kv_heads * GQ), D / 32, (unsigned)a.n_seq);
         const bool wide = p.n_splits > 64;
-        if (a.xp && wide)
+        if (!a.xp && p.n_splits > 128)  // one round trip for up to 256 splits
+            hipLaunchKernelGGL((k_fa_combine<D, false, 32>), cg, dim3(256), 0, st, a.part, (void *)a.out,
+                               p.n_splits, a.sq.out);
+        else if (a.xp && wide)
             hipLaunchKernelGGL((k_fa_combine<D, true, 16>), cg, dim3(256), 0, st, a.part, (void *)a.xp, p.n_splits,
                                (size_t)a.xp_nb);
         else if (a.xp)

@@ -325,16 +325,26 @@ __device__ __forceinline__ void fa_mfma_tile(const float *__restrict__ q, const 
     if constexpr (NBW == 1) {
         step(0, B0{});
     } else {
-        // two register stages; the next pair's loads are unconditional (past the run they
-        // re-read its last row: cache hits, masked), so no wait gathers every load
+        // two register stages.  Fully unrolled (NBW <= 8) the last pair issues nothing
+        // past the run; in the runtime loop (NBW > 8) the next pair's loads stay
+        // unconditional (past the run they re-read its last row: cache hits, masked), so
+        // no wait gathers every load
         issue(1, 1);
-        constexpr int kUnroll = NBW <= 8 ? NBW / 2 : 1;
-#pragma unroll kUnroll
-        for (int blk = 0; blk < NBW; blk += 2) {
-            step(blk, B0{});
-            issue(blk + 2, 0);
-            step(blk + 1, B1{});
-            issue(blk + 3, 1);
+        if constexpr (NBW <= 8) {
+#pragma unroll
+            for (int blk = 0; blk < NBW; blk += 2) {
+                step(blk, B0{});
+                if (blk + 2 < NBW) issue(blk + 2, 0);
+                step(blk + 1, B1{});
+                if (blk + 3 < NBW) issue(blk + 3, 1);
+            }
+        } else {
+            for (int blk = 0; blk < NBW; blk += 2) {
+                step(blk, B0{});
+                issue(blk + 2, 0);
+                step(blk + 1, B1{});
+                issue(blk + 3, 1);
+            }
         }
     }
     l += __shfl_xor(l, 16, 64);
