@@ -166,6 +166,8 @@ typedef struct mi_persist_args {
     size_t kv_row_bytes;       /* K and V cache row stride */
     int n_kv;                  /* attention view length (positions) */
     const int32_t *kv_len;     /* effective length (the FLASH_ATTN_EXT src[5]), or NULL */
+    const uint16_t *mask;      /* F16 KQ mask over the view (the FLASH_ATTN_EXT src[3], one row of
+                                  >= n_kv elements, added to the scaled scores), or NULL */
     float kq_scale, rms_eps;
     float freq_base, freq_scale, attn_factor;  /* neox RoPE over the head dim */
     int rounding;              /* MI_Q8_ROUND_* of the activation quantizations */

@@ -473,7 +473,8 @@ bool supports_fa(const ggml_tensor *op) {
     if (k->nb[0] != 2 || v->nb[0] != 2 || k->nb[1] % 16 || k->nb[2] % 16 || v->nb[1] % 16 || v->nb[2] % 16 ||
         (n_seq > 1 && (k->nb[3] % 16 || v->nb[3] % 16)))
         return false;
-    if (mask && (mask->type != GGML_TYPE_F16 || mask->ne[0] < k->ne[1] || mask->nb[0] != 2 ||
+    // one mask row per sequence, shared by the heads
+    if (mask && (mask->type != GGML_TYPE_F16 || mask->ne[0] < k->ne[1] || mask->nb[0] != 2 || mask->ne[2] != 1 ||
                  (mask->ne[3] != 1 && mask->ne[3] != n_seq)))
         return false;
     if (kvl && (kvl->type != GGML_TYPE_I32 || !ggml_is_contiguous(kvl) || ggml_nelements(kvl) < n_seq)) return false;
@@ -1132,15 +1133,16 @@ int try_fuse_fa_o(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
 //
 // A decoder layer of the one-token graph:
 //   attention input (match_attn_in, Q8_0), FLASH_ATTN_EXT (q = the rotated q, K / V = the
-//   views of the caches the SET_ROWS wrote, no mask), MUL_MAT o (Q8_0), ADD(o, x),
+//   views of the caches the SET_ROWS wrote, an optional F16 mask row), MUL_MAT o (Q8_0), ADD(o, x),
 //   RMS_NORM, MUL(w), MUL_MAT gate, MUL_MAT up, GLU swiglu, MUL_MAT down, ADD(down, x1)
 // with every intermediate read by nothing outside the layer.  A run of such layers, each
-// reading the previous one's output, with one position / cache row / attention view,
-// runs as mi_persist_decode_q8_0 (GGML_MI355X_PERSIST=1).
+// reading the previous one's output, with one position / cache row / attention view /
+// mask, runs as mi_persist_decode_q8_0 (GGML_MI355X_PERSIST=1).
 struct PersistLayerMatch {
     int end = -1;  // the layer's last node (the FFN residual ADD)
     const ggml_tensor *x = nullptr, *out = nullptr, *rms = nullptr, *x1 = nullptr;
     const ggml_tensor *rope = nullptr, *idx = nullptr, *kvl = nullptr, *fa = nullptr;
+    const void *mask = nullptr;  // the F16 mask row's data, or null
     mi_persist_layer L{};
     float eps = 0.0f, eps_ffn = 0.0f, kq_scale = 0.0f;
     int64_t n_embd = 0, n_head = 0, n_head_kv = 0, hd = 0, n_ff = 0, n_kv = 0, n_cache_rows = 0;
@@ -1169,19 +1171,21 @@ bool match_persist_layer(ggml_cgraph *g, int i, const Consumers &C, PersistLayer
     P.rope = M.rope[0];
     P.idx = M.sr[0]->src[1];
     if (mm[1]->ne[0] != mm[2]->ne[0] || !aligned16(M.nw->data)) return false;
-    // attention: one sequence, one query row, no mask, over the caches just written
+    // attention: one sequence, one query row, over the caches just written; the mask, if
+    // any, is one F16 row (supports_fa: >= n_kv elements, shared by the heads)
     int j = next_real(g, M.end + 1);
     if (j >= nn) return false;
     const ggml_tensor *fa = ggml_graph_node(g, j);
     if (fa->op != GGML_OP_FLASH_ATTN_EXT || !supports_fa(fa)) return false;
-    const ggml_tensor *q = fa->src[0], *k = fa->src[1], *v = fa->src[2];
-    if (fa->src[3] || q->data != M.rope[0]->data || q->ne[0] != P.hd || q->ne[1] != 1 || q->ne[2] != P.n_head ||
+    const ggml_tensor *q = fa->src[0], *k = fa->src[1], *v = fa->src[2], *mask = fa->src[3];
+    if ((mask && mask->ne[3] != 1) || q->data != M.rope[0]->data || q->ne[0] != P.hd || q->ne[1] != 1 || q->ne[2] != P.n_head ||
         q->ne[3] != 1 || k->ne[2] != P.n_head_kv || k->ne[3] != 1 || k->data != M.sr[0]->data ||
         v->data != M.sr[1]->data || k->nb[1] != M.sr[0]->nb[1] || v->nb[1] != M.sr[1]->nb[1] || v->nb[1] != k->nb[1] ||
         k->nb[2] != (size_t)P.hd * 2 || v->nb[2] != (size_t)P.hd * 2 || !only_consumed_by(C, M.rope[0], {fa}) ||
         !aligned16(k->data) || !aligned16(v->data))
         return false;
     P.fa = fa;
+    P.mask = mask ? mask->data : nullptr;
     P.kvl = fa->src[5];
     P.n_kv = k->ne[1];
     P.kv_row_bytes = k->nb[1];
@@ -1264,7 +1268,8 @@ bool persist_same_step(const PersistLayerMatch &a, const PersistLayerMatch &b) {
     float fa0[3], fb0[3];
     rope_params(a.rope, fa0[0], fa0[1], fa0[2]);
     rope_params(b.rope, fb0[0], fb0[1], fb0[2]);
-    return a.rope->src[1] == b.rope->src[1] && a.idx == b.idx && a.kvl == b.kvl && a.eps == b.eps &&
+    return a.rope->src[1] == b.rope->src[1] && a.idx == b.idx && a.kvl == b.kvl && a.mask == b.mask &&
+           a.eps == b.eps &&
            a.eps_ffn == b.eps && b.eps_ffn == b.eps && a.kq_scale == b.kq_scale && a.n_embd == b.n_embd &&
            a.n_head == b.n_head && a.n_head_kv == b.n_head_kv && a.hd == b.hd && a.n_ff == b.n_ff &&
            a.n_kv == b.n_kv && a.n_cache_rows == b.n_cache_rows && a.kv_row_bytes == b.kv_row_bytes &&
@@ -1318,6 +1323,7 @@ int try_fuse_persist(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C)
     a.kv_row_bytes = F.kv_row_bytes;
     a.n_kv = (int)F.n_kv;
     a.kv_len = F.kvl ? (const int32_t *)F.kvl->data : nullptr;
+    a.mask = (const uint16_t *)F.mask;
     a.kq_scale = F.kq_scale;
     a.rms_eps = F.eps;
     rope_params(F.rope, a.freq_base, a.freq_scale, a.attn_factor);

@@ -59,6 +59,7 @@ struct PArgs {
     size_t kv_row_bytes;
     int n_kv;
     const int32_t *kv_len;
+    const uint16_t *mask;  // F16 [n_kv] KQ mask, or null
     float kq_scale, eps, theta_scale, freq_scale, attn_factor;
     int rounding;
     long spin_limit;
@@ -182,7 +183,8 @@ struct PLds {
     float gu[NGU][16];                       // gate (slots 0..7) and up (8..15) rows per tile
 };
 
-template <int XN, int GE, int UE, int GF, int UF, int D, int GQ, int NBW, int NB_E, int NF, int NGU, int NDN>
+template <int XN, int GE, int UE, int GF, int UF, int D, int GQ, int NBW, int NB_E, int NF, int NGU, int NDN,
+          bool MASK>
 __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
     constexpr int RPB = 256 / GE;     // rows per k = n_embd tile (16)
     constexpr int HALF = RPB / 2;     // RoPE pairs per rotated tile
@@ -331,7 +333,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
             // the K / V rows of the tile load ahead of the hop, except the row this token
             // writes in phase 1 (loaded after it, so no stale copy of it is cached)
             const FaSeq sq = {0, 0, 0, 0, 0};
-            fa_mfma_tile<D, GQ, false, NBW, 4>(q_buf, (const uint8_t *)P.k_cache, (const uint8_t *)P.v_cache, nullptr,
+            fa_mfma_tile<D, GQ, MASK, NBW, 4>(q_buf, (const uint8_t *)P.k_cache, (const uint8_t *)P.v_cache, a.mask,
                                                a.kv_len, a.n_kv, a.kv_row_bytes, (size_t)a.hd * 2, a.kv_row_bytes,
                                                (size_t)a.hd * 2, a.kq_scale, a.fa_chunk, a.fa_splits, part, nullptr,
                                                true, sq, fa_t % a.fa_splits, fa_t / a.fa_splits, 0, a.n_head_kv,
@@ -727,6 +729,7 @@ int mi_persist_decode_q8_0(void *stream, void *ctx, const mi_persist_args *args)
     a.kv_row_bytes = args->kv_row_bytes;
     a.n_kv = args->n_kv;
     a.kv_len = args->kv_len;
+    a.mask = args->mask;
     a.kq_scale = args->kq_scale;
     a.eps = args->rms_eps;
     // theta_scale on the host with the C library powf, as the CPU rope cache does
@@ -748,8 +751,12 @@ int mi_persist_decode_q8_0(void *stream, void *ctx, const mi_persist_args *args)
     a.scratch = c->scratch;
     a.sync = c->sync;
     a.err_host = c->err_host;
-    hipLaunchKernelGGL((k_persist_q8_0<2, 16, 3, 64, 5, 128, 6, 1, kNbE, kNF, NGU, NDN>), dim3((unsigned)c->n_wg),
-                       dim3(256), 0, (hipStream_t)stream, a);
+    if (a.mask)
+        hipLaunchKernelGGL((k_persist_q8_0<2, 16, 3, 64, 5, 128, 6, 1, kNbE, kNF, NGU, NDN, true>),
+                           dim3((unsigned)c->n_wg), dim3(256), 0, (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL((k_persist_q8_0<2, 16, 3, 64, 5, 128, 6, 1, kNbE, kNF, NGU, NDN, false>),
+                           dim3((unsigned)c->n_wg), dim3(256), 0, (hipStream_t)stream, a);
     MI_CHECK_LAUNCH("k_persist_q8_0");
     return MI_OK;
 }

@@ -16,6 +16,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -68,6 +69,14 @@ struct mi_qwen2 {
     // pinned host words: the 4 * n_seq inputs, then the n_seq greedy tokens read back
     // (asynchronous copies on the backend's stream)
     int32_t *io_pinned = nullptr;
+    // MI_QWEN2_KQ_MASK=1 (one sequence): the attention also takes llama.cpp's KQ mask, F16
+    // [n_ctx] (0 up to the token's position, -inf after it), beside the kv lengths, as the
+    // reference's patched llama.cpp graph passes both.  MI_QWEN2_KQ_MASK=swa:N keeps only
+    // the last N positions (a sliding-window mask, as llama.cpp builds for SWA layers).
+    bool use_mask = false;
+    int32_t mask_window = 0;  // 0: causal only
+    ggml_tensor *mask = nullptr;
+    uint16_t *mask_pinned = nullptr;
     std::map<int, Graph> graphs;  // by KV view length
     Graph *last = nullptr;        // the graph of the latest decode step
     bool dump = false;            // graphs keep ffn_norm-N / ffn_out-N as outputs
@@ -143,7 +152,8 @@ Graph build_graph(mi_qwen2 *m, int n_kv) {
         ggml_tensor *v = ggml_view_4d(ctx, vc, hd, n_kv, hp.n_head_kv, S, vc->nb[1], ggml_row_size(GGML_TYPE_F16, hd),
                                       seq_bytes, 0);
         ggml_tensor *q = ggml_permute(ctx, ggml_reshape_4d(ctx, Q, hd, hp.n_head, 1, S), 0, 2, 1, 3);
-        ggml_tensor *att = ggml_flash_attn_ext(ctx, q, k, v, nullptr, kq_scale, 0.0f, 0.0f);
+        ggml_tensor *kq_mask = m->mask ? ggml_view_1d(ctx, m->mask, n_kv, 0) : nullptr;
+        ggml_tensor *att = ggml_flash_attn_ext(ctx, q, k, v, kq_mask, kq_scale, 0.0f, 0.0f);
         ggml_flash_attn_ext_add_kv_lengths(att, kvl);
         ggml_flash_attn_ext_set_prec(att, GGML_PREC_F32);
         cur = ggml_reshape_2d(ctx, att, hd * hp.n_head, S);
@@ -266,6 +276,16 @@ mi_qwen2 *mi_qwen2_create(const mi_qwen2_hparams *hp, int device) {
     m->inp = ggml_new_tensor_1d(m->wctx, GGML_TYPE_I32, 4 * (int64_t)m->n_seq);
     ggml_set_name(m->inp, "inp_decode");
     ggml_set_input(m->inp);
+    {
+        const char *e = getenv("MI_QWEN2_KQ_MASK");
+        if (e && !strncmp(e, "swa:", 4)) m->mask_window = std::max(1, atoi(e + 4));
+        m->use_mask = e && (e[0] == '1' || m->mask_window > 0) && m->n_seq == 1;
+    }
+    if (m->use_mask) {
+        m->mask = ggml_new_tensor_1d(m->wctx, GGML_TYPE_F16, hp->n_ctx);
+        ggml_set_name(m->mask, "inp_kq_mask");
+        ggml_set_input(m->mask);
+    }
     m->wbuf = ggml_backend_alloc_ctx_tensors_from_buft(m->wctx, ggml_backend_mi355x_buffer_type(device));
     if (!m->wbuf) {
         mi_qwen2_free(m);
@@ -273,6 +293,11 @@ mi_qwen2 *mi_qwen2_create(const mi_qwen2_hparams *hp, int device) {
         return nullptr;
     }
     ggml_backend_buffer_set_usage(m->wbuf, GGML_BACKEND_BUFFER_USAGE_WEIGHTS);
+    if (m->mask && hipHostMalloc((void **)&m->mask_pinned, (size_t)hp->n_ctx * 2, hipHostMallocDefault) != hipSuccess) {
+        mi_qwen2_free(m);
+        fail("qwen2: pinned host allocation failed");
+        return nullptr;
+    }
     mi_qwen2_reset(m);
     return m;
 }
@@ -287,6 +312,7 @@ void mi_qwen2_free(mi_qwen2 *m) {
     ggml_free(m->wctx);
     ggml_backend_free(m->backend);
     if (m->io_pinned) (void)hipHostFree(m->io_pinned);
+    if (m->mask_pinned) (void)hipHostFree(m->mask_pinned);
     delete m;
 }
 
@@ -430,6 +456,11 @@ int mi_qwen2_decode_batch(mi_qwen2 *m, const int32_t *tokens, const int32_t *pos
     }
     // inputs in, graph, greedy tokens out: one stream, one synchronisation
     ggml_backend_tensor_set_async(m->backend, m->inp, in, 0, 4 * (size_t)S * sizeof(int32_t));
+    if (m->mask) {  // fp16 0 over the kept positions, -inf elsewhere
+        const int32_t lo = m->mask_window > 0 ? pos[0] - m->mask_window + 1 : 0;
+        for (int32_t j = 0; j < m->hp.n_ctx; j++) m->mask_pinned[j] = j <= pos[0] && j >= lo ? 0x0000 : 0xFC00;
+        ggml_backend_tensor_set_async(m->backend, m->mask, m->mask_pinned, 0, (size_t)m->hp.n_ctx * 2);
+    }
     if (ggml_backend_graph_compute(m->backend, G.gf) != GGML_STATUS_SUCCESS) return fail("qwen2: graph failed");
     if (next_tokens) ggml_backend_tensor_get_async(m->backend, G.argmax, out, 0, (size_t)S * sizeof(int32_t));
     if (ggml_backend_mi355x_status(m->backend) != 0) return fail("qwen2: decode failed: %s", mi_last_error());

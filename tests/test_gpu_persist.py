@@ -17,7 +17,10 @@ import qwen2_synth as qs
 pytestmark = pytest.mark.gpu
 
 
-def _pair(mi, monkeypatch, hp, seed):
+def _pair(mi, monkeypatch, hp, seed, mask=None):
+    # mask: MI_QWEN2_KQ_MASK for both models ("1" causal, "swa:N" a sliding window)
+    if mask is not None:
+        monkeypatch.setenv("MI_QWEN2_KQ_MASK", mask)
     tensors, smooth = qs.synth(hp, seed=seed, qk_gain=6.0)
     monkeypatch.setenv("GGML_MI355X_PERSIST", "0")
     node = mi.Qwen2Model(hp)
@@ -26,7 +29,24 @@ def _pair(mi, monkeypatch, hp, seed):
     pers = mi.Qwen2Model(hp)
     pers.load(tensors, smooth)
     monkeypatch.delenv("GGML_MI355X_PERSIST")
+    monkeypatch.delenv("MI_QWEN2_KQ_MASK", raising=False)
     return node, pers
+
+
+def _assert_persistent_runs(mi, monkeypatch, hp, seed, mask):
+    # a fresh model of this configuration whose first launch stalls a hop: the decode
+    # fails only when the persistent launch runs (a silent per-node fallback would pass)
+    monkeypatch.setenv("MI_QWEN2_KQ_MASK", mask)
+    monkeypatch.setenv("GGML_MI355X_PERSIST", "1")
+    m = mi.Qwen2Model(hp)
+    m.load(*qs.synth(hp, seed=seed, qk_gain=6.0))
+    monkeypatch.setenv("GGML_MI355X_PERSIST_SPIN", "20000")
+    monkeypatch.setenv("GGML_MI355X_PERSIST_STALL_HOP", "1")
+    with pytest.raises(mi.MiError, match="gave up waiting"):
+        m.decode(3, 0)
+    for k in ("MI_QWEN2_KQ_MASK", "GGML_MI355X_PERSIST", "GGML_MI355X_PERSIST_SPIN", "GGML_MI355X_PERSIST_STALL_HOP"):
+        monkeypatch.delenv(k)
+    m.free()
 
 
 def _same_steps(node, pers, start, n, tok, label):
@@ -74,6 +94,56 @@ def test_persistent_beyond_its_views_falls_back(gpu, monkeypatch):
     _same_steps(node, pers, 1100, 4, 9, "context 1100")
     node.free()
     pers.free()
+
+
+@pytest.mark.parametrize("start", [0, 600])
+def test_persistent_with_kq_mask(gpu, monkeypatch, start):
+    # the graph with llama.cpp's KQ mask beside the kv lengths: the persistent launch
+    # adds the mask row like the per-node attention, and a causal mask (0 up to the
+    # position, -inf after it, all beyond the kv length) changes no bit
+    hp = qs.qwen2_1p5b(n_layer=3, n_ctx=1024, wtype=qs.GGML_TYPE_Q8_0)
+    _assert_persistent_runs(gpu, monkeypatch, hp, 81, "1")
+    node, pers = _pair(gpu, monkeypatch, hp, seed=81, mask="1")
+    plain, spare = _pair(gpu, monkeypatch, hp, seed=81)
+    spare.free()
+    for m in (node, pers, plain):
+        if start:
+            m.fill_cache(start, seed=8, scale=1.0)
+    tok = 17
+    for pos in range(start, start + 12):
+        tn, ln = node.decode(tok, pos, want_logits=True)
+        tp, lp = pers.decode(tok, pos, want_logits=True)
+        tu, lu = plain.decode(tok, pos, want_logits=True)
+        assert np.array_equal(ln, lp), f"position {pos}: persistent {np.abs(ln - lp).max():.3e} from per-node"
+        assert np.array_equal(ln, lu), f"position {pos}: masked {np.abs(ln - lu).max():.3e} from unmasked"
+        assert tn == tp == tu
+        tok = tn
+    for m in (node, pers, plain):
+        m.free()
+
+
+def test_persistent_with_sliding_window_mask(gpu, monkeypatch):
+    # a mask that drops positions inside the kv length (the last 200 kept): persistent ==
+    # per-node bit for bit, and the logits move away from the causal-only ones
+    hp = qs.qwen2_1p5b(n_layer=3, n_ctx=1024, wtype=qs.GGML_TYPE_Q8_0)
+    _assert_persistent_runs(gpu, monkeypatch, hp, 91, "swa:200")
+    node, pers = _pair(gpu, monkeypatch, hp, seed=91, mask="swa:200")
+    causal, spare = _pair(gpu, monkeypatch, hp, seed=91, mask="1")
+    spare.free()
+    for m in (node, pers, causal):
+        m.fill_cache(700, seed=9, scale=1.0)
+    tok, moved = 29, 0
+    for pos in range(700, 710):
+        tn, ln = node.decode(tok, pos, want_logits=True)
+        tp, lp = pers.decode(tok, pos, want_logits=True)
+        _, lc = causal.decode(tok, pos, want_logits=True)
+        assert np.array_equal(ln, lp), f"position {pos}: persistent {np.abs(ln - lp).max():.3e} from per-node"
+        assert tn == tp
+        moved += not np.array_equal(ln, lc)
+        tok = tn
+    assert moved == 10
+    for m in (node, pers, causal):
+        m.free()
 
 
 def test_persistent_greedy_matches_oracle(gpu, orc, monkeypatch):
