@@ -155,6 +155,7 @@ __device__ __forceinline__ half4_t h4(uint32_t a, uint32_t b) {
 
 struct FaNoWait {
     __device__ void operator()() const {}
+    __device__ void mark(int) const {}
 };
 
 // One (split, kv head, sequence) tile of the MFMA flash-decoding kernel: a workgroup of
@@ -167,6 +168,8 @@ struct FaNoWait {
 // first K / V loads and the q loads) and late_row, the row written behind that wait:
 // lanes whose first-block row is late_row load it after wait, so no line of it is cached
 // before it was written.  (NBW == 1 only; the plain kernel passes FaNoWait and -1.)
+// wait.mark(k) is called at the tile's stage boundaries (k = 0: first block's scores
+// formed, 1: output merged across waves, 2: partials stored), for phase timestamps.
 template <int D, int GQ, bool MASK, int NBW, int NW = 4, class Wait = FaNoWait>
 __device__ __forceinline__ void fa_mfma_tile(const float *__restrict__ q, const uint8_t *__restrict__ kc,
                                              const uint8_t *__restrict__ vc, const uint16_t *__restrict__ mask,
@@ -324,6 +327,7 @@ __device__ __forceinline__ void fa_mfma_tile(const float *__restrict__ q, const 
     }
     if constexpr (NBW == 1) {
         step(0, B0{});
+        if constexpr (kLate) wait.mark(0);
     } else {
         // two register stages.  Fully unrolled (NBW <= 8) the last pair issues nothing
         // past the run; in the runtime loop (NBW > 8) the next pair's loads stay
@@ -363,6 +367,7 @@ __device__ __forceinline__ void fa_mfma_tile(const float *__restrict__ q, const 
         }
     }
     __syncthreads();
+    if constexpr (kLate) wait.mark(1);
 
     for (int idx = tid; idx < GQ * D; idx += 64 * NW) {
         const int h = idx / D;
@@ -398,6 +403,7 @@ __device__ __forceinline__ void fa_mfma_tile(const float *__restrict__ q, const 
             }
         }
     }
+    if constexpr (kLate) wait.mark(2);
 }
 
 // The log-sum-exp merge of one output element over the splits' records, in exactly the

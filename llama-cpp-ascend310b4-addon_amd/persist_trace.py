@@ -10,7 +10,8 @@ Events per (layer, workgroup), as k_persist_q8_0 records them:
   5 o waited, 6 o done, 7 gate/up start, 8 gate/up waited, 9 gate/up done,
   10 down start, 11 down waited, 12 down done, 13 down activation staged,
   14 o input staged, 15 gate/up input staged, 16 o records requested,
-  17 o group weights, 18 o head weights.
+  17 o group weights, 18 o head weights, 19 attention scores formed,
+  20 attention waves merged, 21 attention partials stored.
 
 usage: python persist_trace.py DUMP [--layers FIRST LAST]
 Prints per phase the span (first workgroup past the hop -> last one done), the median
@@ -24,7 +25,8 @@ import sys
 import numpy as np
 
 PHASES = [("q/k/v", 1, 2), ("attention", 3, 4), ("merge + o", 5, 6), ("gate/up", 8, 9), ("down", 11, 12)]
-STAGES = [("o: merge input staged", 5, 14), ("o: dot + arrive", 14, 6), ("gate/up: input staged", 8, 15),
+STAGES = [("attention: q read + first scores", 3, 19), ("attention: partials stored", 19, 21),
+          ("o: merge input staged", 5, 14), ("o: dot + arrive", 14, 6), ("gate/up: input staged", 8, 15),
           ("gate/up: dots + swiglu + arrive", 15, 9), ("down: product quantized", 11, 13),
           ("down: dot + arrive", 13, 12)]
 
