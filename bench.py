@@ -158,7 +158,7 @@ def measure_c2(mi, qs, orc, rng, st, plug, threads):
     cpu_us = cpu_median_us(lambda: orc.mul_mat_q4_0_f16_mt(blocks, x16, n, k, n_threads=threads))
     for b in (src, big, dx, dy):
         b.free()
-    return dict(_rate(n * k // 32 * 18 + k * 2 + n * 4, us), kernel="k_gemv_q4_0_gx", shape=f"Q4_0 {n}x{k}, fp16 row",
+    return dict(_rate(n * k // 32 * 18 + k * 2 + n * 4, us), kernel="k_gemv_q4_0_kb", shape=f"Q4_0 {n}x{k}, fp16 row",
                 cpu_us=round(cpu_us, 1), weight_copies=copies)
 
 

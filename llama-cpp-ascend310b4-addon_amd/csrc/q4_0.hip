@@ -1645,6 +1645,113 @@ inline bool mfma_x_enabled() {
 // the grouped kernel needs whole groups of 4 blocks per row
 inline bool mfma_x_ok(int64_t k) { return mfma_x_enabled() && (k / QK) % 4 == 0; }
 
+// One fp16 row, few rows (n <= 2048) and short rows (at most 512 blocks): a workgroup
+// of NW waves owns RW consecutive rows, and lane t owns block t of every one of them.
+// The lane loads its 32 activation values once and uses them for all RW rows, so the
+// activation crosses L2 -> L1 once per workgroup (the row-per-wave kernel reads it once
+// per row: 17.5 KB per row at k = 8960, 3.5x the row's weights).  The activation loads
+// go first and the rows' weights after them in row order (a wave's loads return in
+// order), so row r's dot starts as soon as row r has arrived.  The dot is the register
+// kernel's (q4_dot_xr: nibbles made fp16 16 + q with one shift and one AND-OR per pair,
+// the activation pairs permuted to match once per lane).  Each row's lane partials
+// reduce within the wave, then over the NW waves through LDS.
+template <int RW, int NW>
+__global__ __launch_bounds__(NW * 64) void k_gemv_q4_0_kb(const uint8_t *__restrict__ qs,
+                                                          const uint16_t *__restrict__ wd,
+                                                          const uint16_t *__restrict__ x16, float *__restrict__ y,
+                                                          int n, int nb) {
+    __shared__ float s_part[NW][RW];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int row0 = blockIdx.x * RW;
+    float acc[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) acc[r] = 0.0f;
+    if (tid < nb) {
+        const int b = tid;
+        const int4 *xp = (const int4 *)(x16 + (size_t)b * QK);
+        int4 xv[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) xv[c] = xp[c];
+        int4 wq[RW];
+        uint16_t dw[RW];
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const size_t rb = (size_t)min(row0 + r, n - 1) * nb + b;
+            wq[r] = ld_stream16(qs + rb * 16);
+            dw[r] = wd[rb];
+        }
+        // xs[i] = (x[2i], x[2i+1]) -> the pair order of q4_dot_xr
+        uint32_t xs[16], xq[16];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            xs[4 * c + 0] = (uint32_t)xv[c].x; xs[4 * c + 1] = (uint32_t)xv[c].y;
+            xs[4 * c + 2] = (uint32_t)xv[c].z; xs[4 * c + 3] = (uint32_t)xv[c].w;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t a = xs[2 * t], bb = xs[2 * t + 1], c = xs[8 + 2 * t], d = xs[9 + 2 * t];
+            xq[4 * t + 0] = (a & 0xffffu) | (bb << 16);
+            xq[4 * t + 1] = (a >> 16) | (bb & 0xffff0000u);
+            xq[4 * t + 2] = (c & 0xffffu) | (d << 16);
+            xq[4 * t + 3] = (c >> 16) | (d & 0xffff0000u);
+        }
+        uint32_t magic = 0x4C004C00u;
+        asm volatile("" : "+v"(magic));
+        float xsum = 0.0f;  // the block's activation sum: one dot2 with (1, 1) per pair
+#pragma unroll
+        for (int i = 0; i < 16; i++) xsum = fdot2(xq[i], 0x3C003C00u, xsum);
+#pragma unroll
+        for (int r = 0; r < RW; r++) acc[r] = fmaf(h2f(dw[r]), q4_dot_xr(wq[r], xq, magic, xsum), acc[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const float v = group_sum<64>(acc[r]);
+        if (lane == 0) s_part[wave][r] = v;
+    }
+    __syncthreads();
+    if (tid < RW && row0 + tid < n) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) v += s_part[w][tid];
+        y[row0 + tid] = v;
+    }
+}
+
+template <int NW>
+int launch_kb_nw(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, const uint16_t *x16, float *y) {
+    const Q4Planes p = q4_planes(n, k);
+    // rows per workgroup: about two workgroups per CU (at 1536 x 8960: 3 rows, 512
+    // workgroups measured 4.24 us against 4.31 for 2 rows, 4.46 for 6 and 4.86 for 1)
+    const int rw = (int)((n + 511) / 512);
+    const unsigned grid = (unsigned)((n + rw - 1) / rw);
+    const uint16_t *wd = (const uint16_t *)(base + p.plane);
+#define MI_RW_CASE(R)                                                                                          \
+    case R:                                                                                                    \
+        hipLaunchKernelGGL((k_gemv_q4_0_kb<R, NW>), dim3(grid), dim3(NW * 64), 0, st, base, wd, x16, y, (int)n, \
+                           (int)(k / QK));                                                                     \
+        break;
+    switch (rw) {
+        MI_RW_CASE(1) MI_RW_CASE(2) MI_RW_CASE(3) MI_RW_CASE(4) MI_RW_CASE(5) MI_RW_CASE(6) MI_RW_CASE(7)
+        MI_RW_CASE(8)
+        default: set_error("gemv_q4_0_kb: %lld rows", (long long)n); return MI_ERR_ARG;
+    }
+#undef MI_RW_CASE
+    MI_CHECK_LAUNCH("k_gemv_q4_0_kb");
+    return MI_OK;
+}
+
+// one fp16 row, n <= 2048 rows of at most 512 blocks (3584 x 3584 measured 4.83 us here
+// against 4.73 for the row-per-wave kernel): 4 waves up to 256 blocks, 5 up to
+// 320, else 8
+inline bool kb_fits(int64_t n, int64_t k) { return n <= 2048 && k / QK <= 512; }
+int launch_kb(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, const uint16_t *x16, float *y) {
+    const int64_t nb = k / QK;
+    if (nb <= 256) return launch_kb_nw<4>(st, base, n, k, x16, y);
+    if (nb <= 320) return launch_kb_nw<5>(st, base, n, k, x16, y);
+    return launch_kb_nw<8>(st, base, n, k, x16, y);
+}
+
 int launch_gx(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t m, const uint16_t *x16, float *y,
               const float *add = nullptr) {
     if (m >= 2 && m <= 16) return launch_mfma<false>(st, base, n, k, m, x16, y, add);
@@ -1654,6 +1761,7 @@ int launch_gx(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t
     // per row, where it measured faster.
     if (m == 1 && xr_enabled() && k / QK <= 1024 && (add || k / QK >= 512))
         return launch_xr_gemv(st, base, n, k, x16, false, y, add);
+    if (m == 1 && !add && kb_fits(n, k)) return launch_kb(st, base, n, k, x16, y);
     const bool tall = n >= 2048;
     if (m == 1) return tall ? launch_gx_mr<1, 2>(st, base, n, k, m, x16, y, add)
                             : launch_gx_mr<1, 1>(st, base, n, k, m, x16, y, add);
