@@ -206,7 +206,8 @@ int mi_persist_status(void *ctx);
  * evaluate_and_capture_cann_graph runs every node through ggml_cann_compute_forward
  * one by one (patch:1897-1930). ---- */
 
-/* [RMS_NORM -> MUL(norm_w)] -> MUL_MAT x n_mats (Q8_0, one activation row, k <= 4096)
+/* [RMS_NORM -> MUL(norm_w)] -> MUL_MAT x n_mats (Q8_0, one activation row, k <= 4096;
+ * without a norm k <= 12288, e.g. the down projection of a gate/up pair)
  * -> optional ADD of add[i] (bias or residual, length n[i]) per matrix.  norm_w == NULL
  * skips the RMSNorm (x is the activation itself). */
 int mi_mul_mat_q8_0_f32_fused(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
@@ -290,6 +291,28 @@ int mi_qkv_rope_kv_q8_0(void *stream, const void *const *w_packed, const int64_t
 int mi_gate_up_swiglu_q8_0(void *stream, const void *w_gate, const void *w_up, int64_t n_ff, int64_t k,
                            const float *x, const float *norm_w, float eps, const float *inv_s,
                            const float *inv_s_down, int rounding, void *xq);
+/* [RMS_NORM -> MUL(norm_w)] -> gate and up MUL_MATs (Q8_0, n_ff x k each, one activation
+ * row, k <= 2048, SmoothQuant inv_s of both) -> GLU swiglu times inv_s_down (length n_ff,
+ * or NULL): h fp32 [n_ff], the down projection's input before its Q8_0 quantization, which
+ * mi_mul_mat_q8_0_f32_fused (norm_w and inv_s NULL, n_ff <= 12288) does in its prologue.
+ * A workgroup pairs 8 gate rows with the same 8 up rows: n_ff % 8 == 0.  h and its
+ * quantization are bit-identical to mi_mul_mat_q8_0_f32_fused then mi_swiglu_quant_q8_0.
+ * Replaces the CANN gate/up matmuls and the SwiGLU node before the down projection
+ * (patch:1188-1355 per matmul). */
+int mi_gate_up_swiglu_f32_q8_0(void *stream, const void *w_gate, const void *w_up, int64_t n_ff, int64_t k,
+                               const float *x, const float *norm_w, float eps, const float *inv_s,
+                               const float *inv_s_down, int rounding, float *h);
+/* mi_gate_up_swiglu_q8_0's result (xq of the swiglu times inv_s_down, ready for
+ * mi_gemv_q8_0_add) from the grid of mi_gate_up_swiglu_f32_q8_0: a workgroup pairs 8 gate
+ * rows with the same 8 up rows, and the last of the four workgroups of each 32-block
+ * (counted on counters[block]) quantizes the block.  h_tmp: n_ff floats (16-byte
+ * aligned) for the swiglu values; counters: n_ff / 32 words, zero before the first call,
+ * left zero by every call.  n_ff % 32 == 0, k <= 2048.  Calls that overlap on the same
+ * counters race.  Bit-identical to mi_mul_mat_q8_0_f32_fused then mi_swiglu_quant_q8_0.
+ * Replaces the CANN gate/up matmuls and the SwiGLU node (patch:1188-1355 per matmul). */
+int mi_gate_up_pair_q8_0(void *stream, const void *w_gate, const void *w_up, int64_t n_ff, int64_t k, const float *x,
+                         const float *norm_w, float eps, const float *inv_s, const float *inv_s_down, int rounding,
+                         void *xq, float *h_tmp, unsigned *counters);
 /* GLU swiglu(g, u) of one row (k floats) times inv_s, quantized to Q8_0 into xq (the
  * planar layout of mi_act_quant_q8_0 with m = 1): the input side of the down projection */
 int mi_swiglu_quant_q8_0(void *stream, const float *g, const float *u, const float *inv_s, int64_t k, void *xq,

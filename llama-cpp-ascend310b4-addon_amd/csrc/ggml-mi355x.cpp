@@ -209,6 +209,9 @@ struct BackendCtx {
     size_t scratch_size = 0;
     void *fa_ws = nullptr;
     size_t fa_ws_size = 0;
+    // per-32-block arrival counters of the A8W8 gate/up pair launch (zeroed once, left zero)
+    unsigned *ffn_counters = nullptr;
+    int64_t ffn_counters_words = 0;
     // the rotation table of the current graph's position (built by its first fused q/k/v
     // chain, read by every layer's)
     float *rope_tab = nullptr;  // [2][512]
@@ -551,16 +554,29 @@ size_t scratch_need(const ggml_tensor *node) {
     if (node->op == GGML_OP_MUL_MAT && packed_fmt(node->src[0]) == GGML_TYPE_Q4_0)
         return mi_mul_mat_q4_0_workspace_size(node->src[1]->ne[1], node->src[1]->ne[0]);
     if (node->op == GGML_OP_ARGMAX) return mi_argmax_workspace_size(node->src[0]->ne[0], ggml_nrows(node->src[0]));
-    if (node->op == GGML_OP_GLU && ggml_nrows(node) == 1) return (size_t)ggml_nelements(node) * 2;  // fp16 row
+    // one GLU row: fp16 (W4A16 down), or the A8W8 gate/up pair's quantized row and its
+    // fp32 swiglu values
+    if (node->op == GGML_OP_GLU && ggml_nrows(node) == 1)
+        return mi_xq_size(1, ggml_nelements(node)) + GGML_PAD((size_t)ggml_nelements(node) * 4, 256);
     return 0;
 }
 
 void ensure_buffers(BackendCtx *ctx, ggml_cgraph *g) {
     size_t need_s = 0, need_fa = 0;
+    int64_t need_c = 0;
     for (int i = 0; i < ggml_graph_n_nodes(g); i++) {
         ggml_tensor *n = ggml_graph_node(g, i);
         if (n->op == GGML_OP_FLASH_ATTN_EXT) need_fa = std::max(need_fa, fa_ws_need(n));
+        if (n->op == GGML_OP_GLU && ggml_nrows(n) == 1) need_c = std::max(need_c, ggml_nelements(n) / 32);
         need_s = std::max(need_s, scratch_need(n));
+    }
+    if (need_c > ctx->ffn_counters_words) {
+        if (ctx->ffn_counters) MI_HIP_CHECK(hipFree(ctx->ffn_counters));
+        ctx->ffn_counters_words = GGML_PAD(need_c, 1024);
+        MI_HIP_CHECK(hipMalloc(&ctx->ffn_counters, ctx->ffn_counters_words * 4));
+        MI_HIP_CHECK(hipMemsetAsync(ctx->ffn_counters, 0, ctx->ffn_counters_words * 4, ctx->stream));
+        MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+        ctx->signature.clear();
     }
     if (need_s > ctx->scratch_size) {
         if (ctx->scratch) MI_HIP_CHECK(hipFree(ctx->scratch));
@@ -938,15 +954,27 @@ int try_fuse_gate_up_down_q4(BackendCtx *ctx, ggml_cgraph *g, int i, const Consu
     return (ad ? next_real(g, jd + 1) : jd) + 1 - i;
 }
 
-// A8W8 FFN: [norm] -> gate, up -> GLU swiglu -> down MUL_MAT [-> ADD residual]: gate/up
-// write the down projection's quantized activation directly (two launches).  Opt-in
-// (MI_FUSE_GU_SWIGLU=1): a workgroup must own whole 32-row blocks of both matrices, so
-// the 1.5B shape gets 280 workgroups on 256 CUs, and the launch measured 10.9 us against
-// 8.2 + 2.6 us for the gate/up GEMV and the separate swiglu-quantize launch.
+// A8W8 FFN: [norm] -> gate, up -> GLU swiglu -> down MUL_MAT [-> ADD residual] in two
+// launches (MI_FFN_PAIR; 0 keeps the three of fused gate/up, swiglu-quantize, down):
+//   default: the gate/up launch pairs 8 gate rows with the same 8 up rows per workgroup
+//     (its 1120-workgroup grid at the 1.5B shape), and the last of the four workgroups of
+//     each 32-block quantizes it (per-block arrival counters), so the down launch is
+//     unchanged and the swiglu-quantize launch is gone;
+//   f32: the pair writes the swiglu values in fp32 and the down launch quantizes them in
+//     its prologue (mi_mul_mat_q8_0_f32_fused without norm): measured 1,028 against 1,044
+//     tok/s for the three launches (every down workgroup reads and quantizes 35 KB).
+// MI_FUSE_GU_SWIGLU=1 instead quantizes in the gate/up epilogue with whole 32-row blocks
+// per workgroup: 280 workgroups on 256 CUs at the 1.5B shape, 10.9 us against 8.2 + 2.6 us.
 int try_fuse_gate_up_down_q8(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C, int last,
                              const ggml_tensor *const *mm, const ggml_tensor *x, const ggml_tensor *nw, float eps) {
-    static const bool on = env_flag("MI_FUSE_GU_SWIGLU", false);
-    if (!on) return 0;
+    static const bool blocks = env_flag("MI_FUSE_GU_SWIGLU", false);
+    static const int pair = [] {  // 0 off, 1 fp32 + down prologue, 2 last-arrival quantization
+        const char *e = getenv("MI_FFN_PAIR");
+        if (!e || !*e) return 2;
+        if (e[0] == '0') return 0;
+        return strcmp(e, "f32") == 0 ? 1 : 2;
+    }();
+    if (!blocks && !pair) return 0;
     const int nn = ggml_graph_n_nodes(g);
     const int jg = next_real(g, last + 1);
     if (jg >= nn) return 0;
@@ -959,17 +987,39 @@ int try_fuse_gate_up_down_q8(BackendCtx *ctx, ggml_cgraph *g, int i, const Consu
     const ggml_tensor *down = ggml_graph_node(g, jd);
     const int64_t nf = mm[0]->ne[0], k = x->ne[0];
     if (!q8_gemv_node(down) || down->src[1] != glu || !only_consumed_by(C, glu, {down}) || down->src[0]->ne[0] != nf ||
-        nf % 32 || k > 2048 || ctx->scratch_size < mi_xq_size(1, nf))
+        k > 2048)
         return 0;
     const ggml_tensor *vec = nullptr;
     const ggml_tensor *ad = matmul_add_tail(g, jd, down, C, vec);
     const TensorExtra *exd = (const TensorExtra *)down->src[0]->extra;
-    MI_K_CHECK(mi_gate_up_swiglu_q8_0(ctx->stream, ((const TensorExtra *)mm[0]->src[0]->extra)->packed,
-                                      ((const TensorExtra *)mm[1]->src[0]->extra)->packed, nf, k,
-                                      (const float *)x->data, nw ? (const float *)nw->data : nullptr, eps,
-                                      inv_s_of(mm[0]->src[0]), exd->inv_s, q8_rounding(), ctx->scratch));
-    MI_K_CHECK(mi_gemv_q8_0_add(ctx->stream, exd->packed, ctx->scratch, ad ? (const float *)vec->data : nullptr,
-                                (float *)(ad ? ad->data : down->data), down->src[0]->ne[1], nf, 1));
+    const void *wg = ((const TensorExtra *)mm[0]->src[0]->extra)->packed;
+    const void *wu = ((const TensorExtra *)mm[1]->src[0]->extra)->packed;
+    const float *xf = (const float *)x->data, *nwf = nw ? (const float *)nw->data : nullptr;
+    float *yd = (float *)(ad ? ad->data : down->data);
+    const float *addv = ad ? (const float *)vec->data : nullptr;
+    if (blocks) {
+        if (nf % 32 || ctx->scratch_size < mi_xq_size(1, nf)) return 0;
+        MI_K_CHECK(mi_gate_up_swiglu_q8_0(ctx->stream, wg, wu, nf, k, xf, nwf, eps, inv_s_of(mm[0]->src[0]),
+                                          exd->inv_s, q8_rounding(), ctx->scratch));
+        MI_K_CHECK(mi_gemv_q8_0_add(ctx->stream, exd->packed, ctx->scratch, addv, yd, down->src[0]->ne[1], nf, 1));
+    } else if (pair == 2) {
+        const size_t hoff = mi_xq_size(1, nf);
+        if (nf % 32 || ctx->scratch_size < hoff + (size_t)nf * 4 || ctx->ffn_counters_words < nf / 32) return 0;
+        MI_K_CHECK(mi_gate_up_pair_q8_0(ctx->stream, wg, wu, nf, k, xf, nwf, eps, inv_s_of(mm[0]->src[0]), exd->inv_s,
+                                        q8_rounding(), ctx->scratch, (float *)((uint8_t *)ctx->scratch + hoff),
+                                        ctx->ffn_counters));
+        MI_K_CHECK(mi_gemv_q8_0_add(ctx->stream, exd->packed, ctx->scratch, addv, yd, down->src[0]->ne[1], nf, 1));
+    } else {
+        // the down launch quantizes h in its prologue: n_ff <= 12288
+        if (nf % 32 || nf > 12288 || ctx->scratch_size < (size_t)nf * 4) return 0;
+        float *h = (float *)ctx->scratch;
+        MI_K_CHECK(mi_gate_up_swiglu_f32_q8_0(ctx->stream, wg, wu, nf, k, xf, nwf, eps, inv_s_of(mm[0]->src[0]),
+                                              exd->inv_s, q8_rounding(), h));
+        const void *wdn = exd->packed;
+        const int64_t nd = down->src[0]->ne[1];
+        MI_K_CHECK(mi_mul_mat_q8_0_f32_fused(ctx->stream, 1, &wdn, &nd, &yd, &addv, nf, h, nullptr, 0.0f, nullptr,
+                                             q8_rounding()));
+    }
     return (ad ? next_real(g, jd + 1) : jd) + 1 - i;
 }
 
@@ -1897,6 +1947,7 @@ void backend_free(ggml_backend_t backend) {
     if (ctx->persist) mi_persist_destroy(ctx->persist);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->fa_ws) (void)hipFree(ctx->fa_ws);
+    if (ctx->ffn_counters) (void)hipFree(ctx->ffn_counters);
     if (ctx->rope_tab) (void)hipFree(ctx->rope_tab);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;

@@ -267,6 +267,93 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0_gu_swiglu(const Q8Set S, cons
     }
 }
 
+// Gate and up projections of one activation row with the swiglu in the epilogue: a
+// workgroup pairs gate rows 8t..8t+7 (row slots 0..7) with the same up rows (slots
+// 8..15) and forms h[8t + i] = silu(g) * u times the down projection's SmoothQuant
+// reciprocal.  Each row's dot is fused1's (G = 16 lanes, same block order and reduction)
+// and the swiglu is k_swiglu_quant_q8_0's expression, so h and its quantization equal
+// the unfused chain's bit for bit; the 1120 workgroups of the Qwen2.5-1.5B shape keep the
+// gate+up launch's grid.
+//   QUANT = false: h is written in fp32 (the down launch quantizes it in its prologue).
+//   QUANT = true: h is quantized to Q8_0 in this launch.  The four workgroups of a
+//   32-block publish their 8 values (agent-scope stores, completed before the count) and
+//   count themselves on the block's counter; the one that brings it to 4 reads the block
+//   back, quantizes it (quant4 over 8 lanes, as k_swiglu_quant_q8_0) and zeroes the
+//   counter for the next launch.  Nothing waits: the last arrival does the work.
+template <int U, int XN, bool NORM, bool QUANT>
+__global__ __launch_bounds__(256) void k_gemv_q8_0_gu_pair(const Q8Set S, const float *__restrict__ x,
+                                                           const float *__restrict__ norm_w, float eps,
+                                                           const float *__restrict__ inv_s,
+                                                           const float *__restrict__ inv_s_down, float *h,
+                                                           unsigned *counters, int8_t *__restrict__ xq_qs,
+                                                           uint16_t *__restrict__ xq_d, int nb, int rounding) {
+    constexpr int G = 16;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const FusedLds L = fused_lds(smem, nb);
+    __shared__ float s_gu[16];  // gate rows 0..7, then up rows 0..7
+    __shared__ int s_last;
+    const int tid = threadIdx.x;
+    const int j = tid % G, slot = tid / G;
+    const int t = blockIdx.x;  // h indices 8t .. 8t+7
+    const int k4 = nb * (QK / 4);
+    const bool up = slot >= 8;
+    const uint8_t *qlo = up ? S.qlo[1] : S.qlo[0];
+    const uint8_t *qhi = up ? S.qhi[1] : S.qhi[0];
+    const uint16_t *wd = up ? S.d[1] : S.d[0];
+    const size_t rbase = (size_t)(8 * t + (slot & 7)) * nb;
+
+    XStage<XN, NORM> st;
+    xstage_load(st, x, norm_w, inv_s, k4, tid);
+    int4 lo[U], hi[U];
+    uint32_t dw[U];
+    q8_first_pass<G, U>(qlo, qhi, wd, rbase, nb, j, lo, hi, dw);
+    float sd = 1.0f;  // the down divisor of this thread's h index, loaded with the weights
+    if (tid < 8 && inv_s_down) sd = inv_s_down[8 * t + tid];
+    const float scale = xstage_scale(st, k4, eps, L.red, tid);  // 1 without NORM
+    xstage_quant(st, inv_s, k4, scale, rounding, L.qs, L.d, tid);
+    __syncthreads();
+    const float s = q8_row_dot<G, U>(qlo, qhi, wd, rbase, nb, j, lo, hi, dw, L.qs, L.d);
+    if (j == 0) s_gu[slot] = s;
+    __syncthreads();
+    if constexpr (!QUANT) {
+        if (tid < 8) {
+            const float gv = s_gu[tid], uv = s_gu[8 + tid];
+            float v = (gv / (1.0f + expf(-gv))) * uv;
+            if (inv_s_down) v *= sd;
+            h[8 * t + tid] = v;
+        }
+    } else {
+        if (tid < 8) {
+            const float gv = s_gu[tid], uv = s_gu[8 + tid];
+            float v = (gv / (1.0f + expf(-gv))) * uv;
+            if (inv_s_down) v *= sd;
+            __hip_atomic_store(h + 8 * t + tid, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this workgroup's values are written through
+        __syncthreads();
+        const int blk = t / 4;
+        if (tid == 0) {
+            const unsigned prev =
+                __hip_atomic_fetch_add(counters + blk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = prev == 3u;
+        }
+        __syncthreads();
+        if (s_last && tid < 8) {  // 4 consecutive h values per lane, 8 lanes per block
+            const float *hb = h + 32 * blk + 4 * tid;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] = __hip_atomic_load(hb + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            float d;
+            const uint32_t q = quant4(v[0], v[1], v[2], v[3], rounding, d);
+            *(uint32_t *)(xq_qs + (size_t)32 * blk + 4 * tid) = q;
+            if (tid == 0) {
+                xq_d[blk] = f2h(d);
+                __hip_atomic_store(counters + blk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+}
+
 // The projection of an attention output still in flash-decoding split form: every
 // workgroup merges the splits' records (log-sum-exp combine) for the whole row in its
 // prologue, then scales by the SmoothQuant reciprocal and quantizes as fused1 does.
@@ -550,7 +637,17 @@ int launch_fused_n(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const
     const int64_t xn = (k / 4 + 255) / 256;
     if (xn <= 1) return launch_fused_x<1, NORM>(st, S, n_total, k, x, norm_w, eps, inv_s, rounding);
     if (xn <= 2) return launch_fused_x<2, NORM>(st, S, n_total, k, x, norm_w, eps, inv_s, rounding);
-    return launch_fused_x<4, NORM>(st, S, n_total, k, x, norm_w, eps, inv_s, rounding);
+    if (xn <= 4) return launch_fused_x<4, NORM>(st, S, n_total, k, x, norm_w, eps, inv_s, rounding);
+    // up to 12288 floats (the down projection's row): 32 or 64 lanes per row, no norm
+    if constexpr (!NORM) {
+        if (xn <= 12) {
+            const int g = pick_g_rows(k / QK, n_total);
+            if (g == 32) return launch_fused_gx<32, 12, false>(st, S, n_total, k, x, nullptr, eps, inv_s, rounding);
+            if (g == 64) return launch_fused_gx<64, 12, false>(st, S, n_total, k, x, nullptr, eps, inv_s, rounding);
+        }
+    }
+    set_error("mul_mat_q8_0_f32_fused: k=%lld not supported%s", (long long)k, NORM ? " with a norm" : "");
+    return MI_ERR_ARG;
 }
 
 // one activation row with k <= 4096 (16 floats per thread): single fused launch
@@ -813,7 +910,8 @@ int mi_mul_mat_q8_0_f32_fused(void *stream, int n_mats, const void *const *w_pac
                               const float *norm_w, float eps, const float *inv_s, int rounding) {
     MI_CHECK_ARG(w_packed && n && y && x, "mul_mat_q8_0_f32_fused: null pointer");
     if (int r = check_shape("mul_mat_q8_0_f32_fused", 1, k)) return r;
-    MI_CHECK_ARG(k <= 4096, "mul_mat_q8_0_f32_fused: k=%lld > 4096", (long long)k);
+    MI_CHECK_ARG(k <= 4096 || (!norm_w && k <= 12288), "mul_mat_q8_0_f32_fused: k=%lld > %s", (long long)k,
+                 norm_w ? "4096 with a norm" : "12288");
     MI_CHECK_ARG(mi::aligned(x, 16) && (!inv_s || mi::aligned(inv_s, 16)) && (!norm_w || mi::aligned(norm_w, 16)),
                  "mul_mat_q8_0_f32_fused: x/norm_w/inv_s must be 16-byte aligned");
     Q8Set S;
@@ -870,6 +968,84 @@ int mi_gate_up_swiglu_q8_0(void *stream, const void *w_gate, const void *w_up, i
 #undef MI_GUS
     MI_CHECK_LAUNCH("k_gemv_q8_0_gu_swiglu");
     return MI_OK;
+}
+
+namespace {
+// the gate/up pair launch of both forms (QUANT: counters and xq given)
+int launch_gu_pair(hipStream_t st, const void *w_gate, const void *w_up, int64_t n_ff, int64_t k, const float *x,
+                   const float *norm_w, float eps, const float *inv_s, const float *inv_s_down, int rounding,
+                   float *h, unsigned *counters, void *xq) {
+    const Q8Planes p = q8_planes(n_ff, k);
+    Q8Set S;
+    const uint8_t *wb[2] = {(const uint8_t *)w_gate, (const uint8_t *)w_up};
+    for (int i = 0; i < 4; i++) {
+        const uint8_t *b = wb[i < 2 ? i : 0];
+        S.qlo[i] = b;
+        S.qhi[i] = b + p.plane;
+        S.d[i] = (const uint16_t *)(b + 2 * p.plane);
+        S.y[i] = nullptr;
+        S.add[i] = nullptr;
+        S.row_end[i] = INT_MAX;
+    }
+    const int nb = (int)(k / QK);
+    const int xn = (int)((k / 4 + 255) / 256);
+    int8_t *qs = xq ? (int8_t *)xq : nullptr;
+    uint16_t *dq = xq ? (uint16_t *)((uint8_t *)xq + mi_xq_d_offset(1, n_ff)) : nullptr;
+    const dim3 grid((unsigned)(n_ff / 8));
+#define MI_GUP(UU, XX, NN, QQ)                                                                                     \
+    hipLaunchKernelGGL((k_gemv_q8_0_gu_pair<UU, XX, NN, QQ>), grid, dim3(256), fused_smem(nb), st, S, x, norm_w,  \
+                       eps, inv_s, inv_s_down, h, counters, qs, dq, nb, rounding)
+#define MI_GUP_U(XX, NN, QQ)                        \
+    switch (pick_u(nb, 16)) {                       \
+        case 1: MI_GUP(1, XX, NN, QQ); break;       \
+        case 2: MI_GUP(2, XX, NN, QQ); break;       \
+        case 3: MI_GUP(3, XX, NN, QQ); break;       \
+        default: MI_GUP(4, XX, NN, QQ); break;      \
+    }
+#define MI_GUP_X(NN, QQ)                                  \
+    if (xn <= 1) { MI_GUP_U(1, NN, QQ) } else { MI_GUP_U(2, NN, QQ) }
+    if (xq) {
+        if (norm_w) { MI_GUP_X(true, true) } else { MI_GUP_X(false, true) }
+    } else {
+        if (norm_w) { MI_GUP_X(true, false) } else { MI_GUP_X(false, false) }
+    }
+#undef MI_GUP_X
+#undef MI_GUP_U
+#undef MI_GUP
+    MI_CHECK_LAUNCH("k_gemv_q8_0_gu_pair");
+    return MI_OK;
+}
+
+int check_gu_pair(const char *fn, const void *w_gate, const void *w_up, int64_t n_ff, int64_t k, const float *x,
+                  const float *norm_w, const float *inv_s, int n_ff_multiple) {
+    MI_CHECK_ARG(w_gate && w_up && x, "%s: null pointer", fn);
+    if (int r = check_shape(fn, n_ff, k)) return r;
+    MI_CHECK_ARG(n_ff % n_ff_multiple == 0, "%s: n_ff=%lld not a multiple of %d", fn, (long long)n_ff, n_ff_multiple);
+    MI_CHECK_ARG(k <= 2048, "%s: k=%lld > 2048", fn, (long long)k);
+    MI_CHECK_ARG(mi::aligned(w_gate, 256) && mi::aligned(w_up, 256), "%s: packed weights not 256-byte aligned", fn);
+    MI_CHECK_ARG(mi::aligned(x, 16) && (!norm_w || mi::aligned(norm_w, 16)) && (!inv_s || mi::aligned(inv_s, 16)),
+                 "%s: misaligned vectors", fn);
+    return MI_OK;
+}
+}  // namespace
+
+int mi_gate_up_swiglu_f32_q8_0(void *stream, const void *w_gate, const void *w_up, int64_t n_ff, int64_t k,
+                               const float *x, const float *norm_w, float eps, const float *inv_s,
+                               const float *inv_s_down, int rounding, float *h) {
+    if (int r = check_gu_pair("gate_up_swiglu_f32_q8_0", w_gate, w_up, n_ff, k, x, norm_w, inv_s, 8)) return r;
+    MI_CHECK_ARG(h && mi::aligned(h, 4), "gate_up_swiglu_f32_q8_0: bad h");
+    return launch_gu_pair((hipStream_t)stream, w_gate, w_up, n_ff, k, x, norm_w, eps, inv_s, inv_s_down, rounding, h,
+                          nullptr, nullptr);
+}
+
+int mi_gate_up_pair_q8_0(void *stream, const void *w_gate, const void *w_up, int64_t n_ff, int64_t k, const float *x,
+                         const float *norm_w, float eps, const float *inv_s, const float *inv_s_down, int rounding,
+                         void *xq, float *h_tmp, unsigned *counters) {
+    if (int r = check_gu_pair("gate_up_pair_q8_0", w_gate, w_up, n_ff, k, x, norm_w, inv_s, 32)) return r;
+    MI_CHECK_ARG(xq && mi::aligned(xq, 4) && h_tmp && mi::aligned(h_tmp, 16) && counters,
+                 "gate_up_pair_q8_0: bad xq / h_tmp / counters");
+    return launch_gu_pair((hipStream_t)stream, w_gate, w_up, n_ff, k, x, norm_w, eps, inv_s, inv_s_down, rounding,
+                          h_tmp, counters, xq);
 }
 
 int mi_mul_mat_q8_0_f32_lse(void *stream, const void *w_packed, int64_t n, float *y, const float *add,

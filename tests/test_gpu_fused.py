@@ -385,6 +385,66 @@ def test_gate_up_swiglu_q8_0(gpu, orc, nff, k, norm):
     assert d_same >= 0.99 and dq_.max() <= 1 and np.mean(dq_ > 0) < 1e-2
 
 
+@pytest.mark.parametrize("norm", [True, False])
+@pytest.mark.parametrize("nff,k", [(8960, 1536), (4864, 896), (11008, 2048), (512, 256)])
+def test_gate_up_pair_then_down_q8_0(gpu, orc, nff, k, norm):
+    """The two-launch FFN forms: gate/up rows paired per workgroup with the swiglu (times
+    the down divisor) kept in fp32, then the down projection quantizing it in its prologue
+    (+ residual); and the pair launch quantizing each 32-block in the last of its four
+    workgroups.  Bit-identical to the three launches they replace (fused gate/up GEMV,
+    swiglu-quantize, down GEMV + residual), and within the GEMV bar of the oracle's
+    gate/up -> swiglu -> quantized down."""
+    mi = gpu
+    P = mi._P
+    rng = np.random.default_rng(nff + 3 * k + norm)
+    n = k  # the down projection maps back to the embedding width
+    x = (rng.standard_normal(k) * 0.5).astype(F32)
+    nw = rng.uniform(0.8, 1.2, k).astype(F32)
+    inv = (1.0 / rng.uniform(0.5, 2.0, k)).astype(F32)
+    inv_d = (1.0 / rng.uniform(0.5, 2.0, nff)).astype(F32)
+    wg, wu, wd = q8_0_weights(rng, nff, k), q8_0_weights(rng, nff, k), q8_0_weights(rng, n, nff)
+    pg, pu, pd = _packed_q8(mi, wg, nff, k), _packed_q8(mi, wu, nff, k), _packed_q8(mi, wd, n, nff)
+    res = rng.standard_normal(n).astype(F32)
+    dx, dnw, dinv, dinvd, dres = (mi.to_device(a) for a in (x, nw, inv, inv_d, res))
+    h = mi.DeviceBuffer(4 * nff)
+    y = mi.DeviceBuffer(4 * n)
+    mi._call("mi_gate_up_swiglu_f32_q8_0", None, P(pg.ptr), P(pu.ptr), nff, k, P(dx.ptr),
+             P(dnw.ptr if norm else None), F32(1e-6), P(dinv.ptr), P(dinvd.ptr), mi.Q8_ROUND_X86, P(h.ptr))
+    mi._call("mi_mul_mat_q8_0_f32_fused", None, 1, _ptrs(pd), _i64s(n), _ptrs(y), _ptrs(dres), nff, P(h.ptr), None,
+             F32(0.0), None, mi.Q8_ROUND_X86)
+    # the three launches
+    yg, yu = mi.DeviceBuffer(4 * nff), mi.DeviceBuffer(4 * nff)
+    mi._call("mi_mul_mat_q8_0_f32_fused", None, 2, _ptrs(pg, pu), _i64s(nff, nff), _ptrs(yg, yu), None, k,
+             P(dx.ptr), P(dnw.ptr if norm else None), F32(1e-6), P(dinv.ptr), mi.Q8_ROUND_X86)
+    xq = mi.DeviceBuffer(mi.xq_size(1, nff))
+    mi._call("mi_swiglu_quant_q8_0", None, P(yg.ptr), P(yu.ptr), P(dinvd.ptr), nff, P(xq.ptr), mi.Q8_ROUND_X86)
+    y3 = mi.DeviceBuffer(4 * n)
+    mi._call("mi_gemv_q8_0_add", None, P(pd.ptr), P(xq.ptr), P(dres.ptr), P(y3.ptr), n, nff, 1)
+    # the last-arrival form: quantized row written by the pair launch itself, twice on the
+    # same counters (each call leaves them zero)
+    xqp = mi.DeviceBuffer(mi.xq_size(1, nff))
+    ht = mi.DeviceBuffer(4 * nff)
+    ctr = mi.DeviceBuffer(4 * (nff // 32)).zero()
+    for _ in range(2):
+        mi._call("mi_gate_up_pair_q8_0", None, P(pg.ptr), P(pu.ptr), nff, k, P(dx.ptr), P(dnw.ptr if norm else None),
+                 F32(1e-6), P(dinv.ptr), P(dinvd.ptr), mi.Q8_ROUND_X86, P(xqp.ptr), P(ht.ptr), P(ctr.ptr))
+    mi.device_sync()
+    got, three = y.download(F32), y3.download(F32)
+    assert np.array_equal(got, three), f"max |diff| {np.abs(got - three).max():.3e}"
+    doff = mi.xq_d_offset(1, nff)
+    assert np.array_equal(xqp.download(np.int8, nff), xq.download(np.int8, nff))
+    assert np.array_equal(xqp.download(np.uint16, nff // 32, offset=doff), xq.download(np.uint16, nff // 32, offset=doff))
+    assert not ctr.download(np.uint32, nff // 32).any()
+    xin = rms_norm_ref(x, nw, 1e-6) if norm else x
+    g = _q8_ref(orc, wg, xin, nff, k, inv)
+    u = _q8_ref(orc, wu, xin, nff, k, inv)
+    v = ((g.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64)))).astype(F32) * u).astype(F32)
+    ref = (_q8_ref(orc, wd, v, n, nff, inv_d) + res).astype(F32)
+    err = rel_err(got, ref)
+    print(f"gate/up pair + down {nff}x{k}: rel vs oracle {err:.2e}")
+    assert err < GEMV_TOL
+
+
 def test_gemv_q8_0_add_equals_gemv_plus_vector(gpu):
     mi = gpu
     rng = np.random.default_rng(11)
