@@ -18,6 +18,8 @@ using namespace mi;
 
 constexpr int kNW = 4;  // waves per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
+// lazy softmax rescaling threshold (log2 units): probabilities stay below 2^8 = 256
+constexpr float kLazyLog2 = 8.0f;
 
 // 2^x with the hardware v_exp_f32 (arguments here are <= 0; -inf gives 0)
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -272,20 +274,29 @@ __device__ __forceinline__ void fa_mfma_tile(const float *__restrict__ q, const 
         float bm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
         bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
         bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-        const float mn = fmaxf(m, bm);
-        const float alpha = mn == -INFINITY ? 1.0f : fexp2(m - mn);
+        // Lazy rescaling: the reference maximum m moves only when a score exceeds it by more
+        // than kLazyLog2 (log2 units), so most blocks skip the output rescale (a read,
+        // multiply and write-back of each MFMA accumulator).  p = 2^(s - m) then stays below
+        // 2^kLazyLog2; l and o share the reference m, so o / l and the records' (m, l, o)
+        // mean what they meant with an exact running maximum.
+        const bool grow = bm > m + kLazyLog2;  // m = -inf: the first finite score
+        if (__any(grow)) {
+            const float mn = grow ? bm : m;
+            const float alpha = mn == -INFINITY ? 1.0f : fexp2(m - mn);
+            l *= alpha;
+            m = mn;
+            // rescale the output rows: row 4g+r belongs to head 4g+r, whose alpha sits in lane 4g+r
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float a = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+                for (int t = 0; t < VT; t++) o[t][r] *= a;
+            }
+        }
         float p[4];
 #pragma unroll
-        for (int r = 0; r < 4; r++) p[r] = mn == -INFINITY ? 0.0f : fexp2(sc[r] - mn);
-        l = l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-        m = mn;
-        // rescale the output rows: row 4g+r belongs to head 4g+r, whose alpha sits in lane 4g+r
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float a = __shfl(alpha, 4 * g + r, 64);
-#pragma unroll
-            for (int t = 0; t < VT; t++) o[t][r] *= a;
-        }
+        for (int r = 0; r < 4; r++) p[r] = m == -INFINITY ? 0.0f : fexp2(sc[r] - m);
+        l += (p[0] + p[1]) + (p[2] + p[3]);
         half_t ph[4], pl[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
