@@ -23,9 +23,10 @@
 // on that phase's hop, so the weight stream overlaps the synchronisation.
 //
 // Hops: only the workgroups that produce a phase's outputs arrive (an agent-scope add
-// to one of 8 counters, by workgroup id mod 8, after their outputs are written through
-// with agent-scope stores); only the consumers wait (lanes 0..7 of wave 0 poll the 8
-// counters).  Every produced buffer is distinct per layer and written once per launch,
+// to one of 8 counters, by workgroup id mod 8, in each of the kReps replicas of the hop's
+// counter set, after their outputs are written through with agent-scope stores); only
+// the consumers wait (lanes 0..7 of wave 0 poll the 8 counters of the replica of their
+// workgroup id mod kReps, so few workgroups poll any one line).  Every produced buffer is distinct per layer and written once per launch,
 // so a consumer's plain loads after the hop can only miss to memory or hit lines filled
 // after the producers finished.  Every wait is bounded (spin_limit polls): on a timeout
 // the workgroup raises the error word, every later wait returns at once, and all
@@ -87,22 +88,24 @@ __device__ __forceinline__ void st_h(uint16_t *p, uint16_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// All of this workgroup's writes done, then one arrival (thread 0).
+// All of this workgroup's writes done, then one arrival in each counter replica (threads
+// 0 .. kReps-1 of wave 0).
 __device__ __forceinline__ void hop_arrive(const PArgs &a, int layer, int hop) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(a.sync + persist_plan::hop_ctr_word(layer, hop, blockIdx.x & 7), 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x < persist_plan::kReps)  // one arrival in every replica of the counter set
+        __hip_atomic_fetch_add(a.sync + persist_plan::hop_ctr_word(layer, hop, blockIdx.x & 7, threadIdx.x), 1u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Wait until every producer of the hop arrived (bounded; see the file comment).
+// Wait until every producer of the hop arrived, polling the 8 counters of this
+// workgroup's replica (bounded; see the file comment).
 __device__ __forceinline__ void hop_wait(const PArgs &a, int layer, int hop) {
     if (threadIdx.x < 64) {
         const int j = threadIdx.x & 7;
         const unsigned want = persist_plan::hop_want(a.lo, hop, j) + (layer == 0 && hop == a.stall_hop && j == 0);
-        const unsigned *ctr = a.sync + persist_plan::hop_ctr_word(layer, hop, j);
+        const unsigned *ctr = a.sync + persist_plan::hop_ctr_word(layer, hop, j, blockIdx.x % persist_plan::kReps);
         unsigned *err = a.sync + persist_plan::err_word(a.n_layer);
         long spins = 0;
         for (;;) {
@@ -137,7 +140,7 @@ __device__ __forceinline__ void persist_exit(const PArgs &a) {
     }
     __syncthreads();
     if (!s_last) return;
-    const int n = a.n_layer * kHops * 8;
+    const int n = (int)persist_plan::hop_counters(a.n_layer);
     for (int i = threadIdx.x; i < n; i += blockDim.x) st_u(a.sync + (size_t)i * kCtrStride, 0u);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);

@@ -4,8 +4,9 @@
 //
 // A grid of n_wg workgroups (a multiple of 8) walks every layer through five phases; hop
 // h of layer l is the event "every producer of phase h of layer l has written its
-// outputs".  Producers arrive on one of 8 counters (workgroup id mod 8); a consumer
-// waits until every counter holds the arrivals expected on it.
+// outputs".  Producers arrive on one of 8 counters (workgroup id mod 8), in each of
+// kReps replicas of the counter set; a consumer polls the replica of its workgroup id mod
+// kReps until every counter holds the arrivals expected on it (fewer pollers per line).
 //
 //   phase (hop)   producers                              consumers (wait before use)
 //   0 q/k/v       tiles 0 .. n_qkv_tiles-1 (wg = tile)   attention tiles        (hop 0)
@@ -32,6 +33,7 @@ namespace persist_plan {
 
 constexpr int kHops = 5;         // hops per layer
 constexpr int kCtrStride = 64;   // unsigned words between counters (256 bytes)
+constexpr int kReps = 16;        // replicas of each hop's 8 counters (16 pollers per line at 256 workgroups)
 constexpr int kMaxSplits = 16;   // attention splits the o prologue merges
 constexpr int kRowsE = 16;       // rows per k = n_embd tile (q/k/v, o, gate/up)
 constexpr int kRowsF = 4;        // rows per k = n_ff tile (down)
@@ -111,12 +113,13 @@ MI_PLAN_HD inline unsigned hop_want(const Layout &lo, int h, int j) {
     return (unsigned)(count / 8 + (((j - first) & 7) < (count & 7) ? 1 : 0));
 }
 
-// word offsets in the sync area: 8 counters per (layer, hop), then the exit counter and
-// the device error word, each on its own 256-byte line
-MI_PLAN_HD inline size_t hop_ctr_word(int layer, int hop, int j) {
-    return ((size_t)(layer * kHops + hop) * 8 + j) * kCtrStride;
+// word offsets in the sync area: kReps x 8 counters per (layer, hop), then the exit
+// counter and the device error word, each on its own 256-byte line
+MI_PLAN_HD inline size_t hop_ctr_word(int layer, int hop, int j, int rep) {
+    return (((size_t)(layer * kHops + hop) * kReps + rep) * 8 + j) * kCtrStride;
 }
-MI_PLAN_HD inline size_t exit_word(int n_layer) { return (size_t)n_layer * kHops * 8 * kCtrStride; }
+MI_PLAN_HD inline size_t hop_counters(int n_layer) { return (size_t)n_layer * kHops * kReps * 8; }
+MI_PLAN_HD inline size_t exit_word(int n_layer) { return hop_counters(n_layer) * kCtrStride; }
 MI_PLAN_HD inline size_t err_word(int n_layer) { return exit_word(n_layer) + kCtrStride; }
 MI_PLAN_HD inline size_t sync_words(int n_layer) { return exit_word(n_layer) + 2 * kCtrStride; }
 

@@ -3,7 +3,8 @@
 //
 // One std::thread per workgroup walks the kernel's sequence of phases with the roles,
 // expected-arrival counts and sync-area layout of persist_plan.h (the header the kernel
-// and its launcher use), on std::atomic counters.  A producer marks its output of
+// and its launcher use), on std::atomic counters: arrivals go to every replica of a hop's
+// counter set, a workgroup polls its own replica.  A producer marks its output of
 // (layer, hop) before it arrives; after every wait the consumer checks that every
 // producer of that hop has marked, so a wait that returns early is a violation.  Waits
 // are bounded like the kernel's (spin_limit polls, then the error word), threads sleep
@@ -66,7 +67,8 @@ struct Walker {
     }
     void arrive(int layer, int hop) {
         S.mk(layer, hop, wg).store(1, std::memory_order_release);
-        S.sync[hop_ctr_word(layer, hop, wg & 7)].fetch_add(1, std::memory_order_acq_rel);
+        for (int r = 0; r < kReps; r++)  // every replica of the counter set
+            S.sync[hop_ctr_word(layer, hop, wg & 7, r)].fetch_add(1, std::memory_order_acq_rel);
         S.arrivals.fetch_add(1);
     }
     // the kernel's hop_wait: poll the 8 counters; give up after spin_limit polls or when
@@ -76,9 +78,9 @@ struct Walker {
         long spins = 0;
         for (;;) {
             bool all = true;
-            for (int j = 0; j < 8; j++) {
+            for (int j = 0; j < 8; j++) {  // the replica of this workgroup
                 const unsigned want = hop_want(S.lo, hop, j) + (layer == 0 && hop == S.stall_hop && j == 0);
-                all = all && S.sync[hop_ctr_word(layer, hop, j)].load(std::memory_order_acquire) >= want;
+                all = all && S.sync[hop_ctr_word(layer, hop, j, wg % kReps)].load(std::memory_order_acquire) >= want;
             }
             if (all) break;
             if (err.load(std::memory_order_acquire)) return;
@@ -98,7 +100,7 @@ struct Walker {
         std::atomic<unsigned> &ex = S.sync[exit_word(S.n_layer)];
         const unsigned prev = ex.fetch_add(1, std::memory_order_acq_rel);
         if (prev != (unsigned)S.lo.n_wg - 1) return;
-        for (int i = 0; i < S.n_layer * kHops * 8; i++) S.sync[(size_t)i * kCtrStride].store(0);
+        for (size_t i = 0; i < hop_counters(S.n_layer); i++) S.sync[i * kCtrStride].store(0);
         S.sync[err_word(S.n_layer)].store(0);
         ex.store(0);
     }
