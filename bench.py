@@ -10,18 +10,24 @@ Prints ONE JSON line.  Phases:
      tied fp16 head, argmax) run by ggml_backend_graph_compute, replayed as a HIP graph;
      the argmax is read back to the host each step, as llama.cpp's sampler does.
      tokens/s = K / elapsed, bracketed by device synchronisation.  Both decode paths of
-     the backend are timed: the per-node one (one launch per fused node group, the
-     backend's default and the headline) and the persistent one (all 28 layers in one
-     launch, GGML_MI355X_PERSIST=1, reported beside it); their greedy tokens are compared.
-  2. roofline: the dominant kernel, the grouped gate+up Q8_0 GEMV of one layer (two
-     8960 x 1536 matrices on one activation row, one launch), timed live with HIP events
-     over back-to-back launches on the stream they are issued to, rotating through enough
-     weight copies (> 2x the 256 MB MALL) to be HBM-cold; achieved = algorithmic bytes /
-     average launch time.
+     the backend are timed: the persistent one (all 28 layers in one launch,
+     GGML_MI355X_PERSIST=1; the headline) and the per-node one (one launch per fused node
+     group, the backend's default, reported beside it); their greedy tokens are compared.
+  2. roofline: the dominant kernel of the headline path, the persistent layer-stack
+     launch, timed live with HIP events the backend records on its stream around each
+     launch (GGML_MI355X_PERSIST_TIMING=1, launches run eagerly) over K decode steps of a
+     second model at the same positions; its 1.39 GB of weights are over 5x the 256 MB
+     MALL, so every launch streams them from HBM; achieved = algorithmic bytes (weights,
+     vectors, K/V rows read and written) / average launch time.  Beside it, the per-node
+     path's dominant kernel, the grouped gate+up Q8_0 GEMV of one layer (two 8960 x 1536
+     matrices on one activation row, one launch), timed with HIP events over back-to-back
+     launches on the stream they are issued to, rotating through enough weight copies
+     (> 2x the MALL) to be HBM-cold.
   3. cpu_baseline: the ggml-CPU restatement in oracle/ (AVX2/AVX-512 VNNI, OpenMP) on a
      bounded sample of the same decode: it takes the GPU's KV cache after the warm-up
-     steps and decodes from the same token and position, timed for ~15 s or K steps;
-     its greedy tokens are compared with the GPU's timed tokens.
+     steps and decodes K steps from the same token and position (at most ~15 s), then
+     the same K steps again until at least 10 s are timed; its greedy tokens are compared
+     with the GPU's timed tokens.
 
   4. configs: every other workload measured in the same run, each HBM-cold (rotating
      through copies of its weights or KV cache, more than 2x the 256 MB MALL) with live
@@ -276,9 +282,77 @@ def measure_roofline(mi, qs, hp, rng):
             "avg_us": round(avg_us, 3), "algorithmic_bytes": algo, "launches": launches, "weight_copies": copies}
 
 
-def cpu_baseline(qs, hp, tensors, smooth, model, token, pos, gpu_tokens, budget_s=15.0):
-    """the ggml-CPU restatement decoding from the GPU's KV cache at `pos`, timed; then the
-    GPU re-decodes the CPU's steps (same input tokens, same positions) for the logit error"""
+def persist_launch_bytes(qs, hp, kv_len):
+    """algorithmic HBM bytes of one persistent launch (every layer of one decode token) when
+    the attention reads kv_len positions: Q8_0 weights, q/k/v biases, the two RMSNorm
+    weights, the four SmoothQuant 1/s rows, the K and V rows read and the new position's
+    written, and the residual row in and out"""
+    E, F, nkv = hp["n_embd"], hp["n_ff"], hp["n_head_kv"] * hp["head_dim"]
+    per = sum(n * k // 32 * 34 for _, n, k, _ in qs.projections(hp))
+    per += (E + 2 * nkv) * 4 + 2 * E * 4 + (3 * E + F) * 4
+    per += kv_len * nkv * 2 * 2 + nkv * 2 * 2
+    return hp["n_layer"] * per + 2 * E * 4
+
+
+PERSIST_KERNEL = "k_persist_q8_0"
+
+
+def measure_persist_roofline(mi, qs, hp, tensors, smooth, steps, warm):
+    """the persistent layer-stack launch (all 28 layers of one decode token in one launch),
+    timed live with HIP events that the backend records on its stream around each launch
+    (GGML_MI355X_PERSIST_TIMING=1; launches run eagerly so every one is timed); the weights
+    (1.39 GB) are over 5x the 256 MB MALL, so every launch streams them from HBM"""
+    env = {"GGML_MI355X_PERSIST": "1", "GGML_MI355X_PERSIST_TIMING": "1", "GGML_MI355X_GRAPHS": "0"}
+    saved = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        model = mi.Qwen2Model(hp)
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    model.load(tensors, smooth)
+    model.fill_cache(PREFILL, seed=SEED + 3, scale=1.0)
+    nxt = 0
+    if warm:
+        wt, _ = model.decode_steps(0, PREFILL, warm)
+        nxt = int(wt[-1])
+    pos0 = PREFILL + warm
+    n0, ms0 = model.persist_timing()
+    model.decode_steps(nxt, pos0, steps)
+    n1, ms1 = model.persist_timing()
+    model.free()
+    launches = n1 - n0
+    if launches != steps:
+        raise RuntimeError(f"persistent roofline: {launches} launches timed for {steps} decode steps "
+                           "(the persistent path did not take every step)")
+    avg_us = (ms1 - ms0) * 1e3 / launches
+    algo = sum(persist_launch_bytes(qs, hp, pos0 + j + 1) for j in range(steps)) // steps
+    achieved = algo / avg_us / 1e3
+    traffic, source = None, None
+    tpath = os.path.join(ROOT, "profiles", "traffic_persist_q8_0.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            t = json.load(f)
+        if t.get("kernel") == PERSIST_KERNEL and t.get("first_position") == pos0 and t.get("steps") == steps:
+            traffic = t.get("hbm_bytes_per_launch")
+            source = "profiles/traffic_persist_q8_0.md (rocprofv3 --pmc of this kernel, " + t.get("measured", "?") + ")"
+    return {"kernel": PERSIST_KERNEL + ": the persistent layer stack, all 28 layers of a decode token in one "
+                      "launch of 256 workgroups (norms, A8W8 q/k/v + RoPE + KV write, flash-decoding, o, "
+                      "gate/up + SwiGLU, down, residuals), weights HBM-cold", "bound": "hbm",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": source,
+            "avg_us": round(avg_us, 3), "algorithmic_bytes": algo, "launches": launches,
+            "positions": [pos0 + 1, pos0 + steps]}
+
+
+def cpu_baseline(qs, hp, tensors, smooth, model, token, pos, gpu_tokens, budget_s=15.0, min_s=10.0):
+    """the ggml-CPU restatement decoding from the GPU's KV cache at `pos`, timed; the same
+    steps are decoded again (same input tokens, rewriting the same cache rows) until at
+    least min_s of CPU decode is timed; then the GPU re-decodes the CPU's steps (same input
+    tokens, same positions) for the logit error"""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
     threads = cpu_threads()
@@ -296,6 +370,12 @@ def cpu_baseline(qs, hp, tensors, smooth, model, token, pos, gpu_tokens, budget_
         logits.append(lg)
         if time.perf_counter() - t0 >= budget_s:
             break
+    n_steps, passes = len(toks), 1
+    while time.perf_counter() - t0 < min_s:
+        for i, t in enumerate(inputs):
+            cpu.decode(t, pos + i)
+        n_steps += len(inputs)
+        passes += 1
     el = time.perf_counter() - t0
     err = rel = 0.0
     for i, (t, lc) in enumerate(zip(inputs, logits)):
@@ -304,9 +384,10 @@ def cpu_baseline(qs, hp, tensors, smooth, model, token, pos, gpu_tokens, budget_
         rel = max(rel, float(np.abs(lg - lc).max() / np.abs(lc).max()))
     agree = int(np.sum(np.asarray(toks) == np.asarray(gpu_tokens[:len(toks)])))
     first_diff = next((i for i, (a, b) in enumerate(zip(toks, gpu_tokens)) if a != b), None)
-    return {"value": round(len(toks) / el, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{len(toks)} greedy decode steps of the same model from the GPU's KV cache at position {pos} "
-                      f"(ggml-CPU restatement in oracle/, {orc.simd_isa()}, {threads} threads, {el:.1f} s)",
+    return {"value": round(n_steps / el, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{len(toks)} greedy decode steps of the same model from the GPU's KV cache at position {pos}, "
+                      f"{passes} pass(es), {n_steps} steps (ggml-CPU restatement in oracle/, {orc.simd_isa()}, "
+                      f"{threads} threads, {el:.1f} s)",
             "greedy_agreement": f"{agree}/{len(toks)}", "first_divergence": first_diff,
             "logit_max_abs": round(err, 6), "logit_max_rel": round(rel, 6), "host": host_info(orc, threads)}
 
@@ -455,15 +536,15 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying HIP graphs")
     ap.add_argument("--no-roofline", action="store_true", help="skip the standalone roofline leg")
-    ap.add_argument("--roofline-only", action="store_true",
-                    help="run only the roofline leg (short program for rocprofv3 counter passes)")
+    ap.add_argument("--roofline-only", nargs="?", const="persistent", choices=["persistent", "gate-up"],
+                    help="run only one roofline leg (a short program for rocprofv3 counter passes)")
     ap.add_argument("--workload", default="qwen2-1.5b-a8w8", choices=["qwen2-1.5b-a8w8", "qwen2-7b-w4a16"],
                     help="qwen2-7b-w4a16: the 7B-shaped W4A16 decode at a 32K context (see --batch)")
     ap.add_argument("--batch", type=int, default=1, help="independent sequences for qwen2-7b-w4a16 (1..8)")
     ap.add_argument("--quick", action="store_true", help="skip the configs leg (C1, C2, C3, C5)")
-    ap.add_argument("--decode-path", default="per-node", choices=["per-node", "persistent"],
+    ap.add_argument("--decode-path", default="persistent", choices=["per-node", "persistent"],
                     help="the C4 headline's decode path (the other one is timed too and reported beside it); "
-                         "per-node is the backend's default, and the roofline leg times its dominant launch")
+                         "the roofline is that path's dominant launch, the other path's is reported beside it")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); how the decode path "
@@ -484,10 +565,13 @@ def main():
 
     warm = max(args.warmup, 0)
     hp = qs.qwen2_1p5b(n_ctx=PREFILL + warm + args.steps)
-    if args.roofline_only:
+    if args.roofline_only == "gate-up":
         print(json.dumps({"roofline": measure_roofline(mi, qs, hp, np.random.default_rng(SEED + 1))}))
         return
     tensors, smooth = qs.synth(hp, seed=SEED)
+    if args.roofline_only == "persistent":
+        print(json.dumps({"roofline": measure_persist_roofline(mi, qs, hp, tensors, smooth, args.steps, warm)}))
+        return
 
     def c4_run(persistent):
         """the C4 decode through one of the backend's two decode paths; returns the model
@@ -525,8 +609,13 @@ def main():
     rng = np.random.default_rng(SEED + 2)
 
     log(f"C4 decode: {tok_s:.1f} tok/s")
-    roof = None if args.no_roofline else measure_roofline(mi, qs, hp, rng)
-    log("roofline leg done")
+    roof = roof_other = None
+    if not args.no_roofline:
+        roof_p = measure_persist_roofline(mi, qs, hp, tensors, smooth, args.steps, warm)
+        log("persistent roofline leg done")
+        roof_g = measure_roofline(mi, qs, hp, rng)
+        log("gate+up roofline leg done")
+        roof, roof_other = (roof_p, roof_g) if persistent else (roof_g, roof_p)
     cpu = None if args.no_cpu else cpu_baseline(qs, hp, tensors, smooth, model, nxt, pos0, list(toks))
     model.free()
     del tensors, smooth
@@ -564,6 +653,7 @@ def main():
             "step_roofline_frac": round(step_bytes * args.steps / el / 1e9 / HBM_PEAK_GBS, 4),
         },
         "roofline": roof,
+        ("roofline_gate_up" if persistent else "roofline_persistent"): roof_other,
         "cpu_baseline": cpu,
         "configs": configs,
     }

@@ -69,6 +69,12 @@ GGML_BACKEND_API bool ggml_backend_mi355x_set_smooth_factors(struct ggml_tensor 
  * the backend's stream, then returns 0, or -1 when a launch since the last call gave up
  * (its results are invalid; the next graph_compute also reports GGML_STATUS_FAILED once). */
 GGML_BACKEND_API int ggml_backend_mi355x_status(ggml_backend_t backend);
+/* With GGML_MI355X_PERSIST_TIMING=1 set when the backend was created: the number of
+ * persistent layer-stack launches timed so far and their summed duration in ms (HIP
+ * events on the backend's stream around each launch run eagerly, i.e. not inside a
+ * captured graph; read at each ggml_backend_mi355x_status).  Returns 0, or -1 when the
+ * timing is off.  No reference counterpart (a measurement hook). */
+GGML_BACKEND_API int ggml_backend_mi355x_persist_timing(ggml_backend_t backend, int64_t *launches, double *total_ms);
 
 /* No counterpart in the reference (an integration check for dynamic loading): returns 1
  * when the op and type ids this backend was compiled with carry the same names in the

@@ -109,6 +109,10 @@ int mi_qwen2_get_cache_seq(mi_qwen2 *m, int32_t layer, int32_t is_v, int32_t seq
                            size_t size);
 int mi_qwen2_set_cache_seq(mi_qwen2 *m, int32_t layer, int32_t is_v, int32_t seq, int32_t n_pos, const void *src,
                            size_t size);
+/* the backend's persistent-launch timing (ggml_backend_mi355x_persist_timing): launches
+ * timed so far and their summed ms; -1 unless GGML_MI355X_PERSIST_TIMING=1 was set when the
+ * model was created */
+int mi_qwen2_persist_timing(mi_qwen2 *m, int64_t *launches, double *total_ms);
 /* synthetic context: positions < n_pos of every layer's K and V cache of every sequence set to
  * fp16 values uniform in [-scale, scale) on the device (decode timing at long contexts) */
 int mi_qwen2_fill_cache(mi_qwen2 *m, int32_t n_pos, uint64_t seed, float scale);

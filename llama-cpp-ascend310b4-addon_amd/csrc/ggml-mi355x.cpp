@@ -65,10 +65,8 @@ bool prepack_enabled() {
     static const bool on = env_flag("GGML_MI355X_PREPACK", true);
     return on;
 }
-bool graphs_enabled() {
-    static const bool on = env_flag("GGML_MI355X_GRAPHS", true) && !env_flag("GGML_MI355X_TRACE_NODE_SYNC", false);
-    return on;
-}
+// read when a backend is created (one process may hold backends with and without replay)
+bool graphs_env() { return env_flag("GGML_MI355X_GRAPHS", true) && !env_flag("GGML_MI355X_TRACE_NODE_SYNC", false); }
 bool trace_node_sync() {
     static const bool on = env_flag("GGML_MI355X_TRACE_NODE_SYNC", false);
     return on;
@@ -228,6 +226,14 @@ struct BackendCtx {
     int persist_layers = 0;
     bool persist_failed = false;  // the context could not be created: per-node path from then on
     bool persist_error = false;   // a launch gave up waiting (reported once)
+    // GGML_MI355X_PERSIST_TIMING: HIP events around every eager persistent launch (not
+    // under capture), summed at each status check
+    bool persist_timing = false;
+    hipEvent_t pt_ev[2] = {nullptr, nullptr};
+    bool pt_pending = false;
+    int64_t pt_launches = 0;
+    double pt_ms = 0.0;
+    bool graphs_on = true;  // GGML_MI355X_GRAPHS (replay of unchanged graphs)
     // captured replay of the last graph
     hipGraphExec_t gexec = nullptr;
     std::vector<uint64_t> signature;
@@ -1326,6 +1332,17 @@ bool persist_same_step(const PersistLayerMatch &a, const PersistLayerMatch &b) {
            memcmp(fa0, fb0, sizeof(fa0)) == 0 && a.idx->type == b.idx->type;
 }
 
+// folds the last timed persistent launch into the totals (waits for its end event)
+void collect_persist_timing(BackendCtx *ctx) {
+    if (!ctx->pt_pending) return;
+    float ms = 0.0f;
+    MI_HIP_CHECK(hipEventSynchronize(ctx->pt_ev[1]));
+    MI_HIP_CHECK(hipEventElapsedTime(&ms, ctx->pt_ev[0], ctx->pt_ev[1]));
+    ctx->pt_ms += ms;
+    ctx->pt_launches++;
+    ctx->pt_pending = false;
+}
+
 int try_fuse_persist(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
     if (!ctx->persist_on || ctx->persist_failed) return 0;
     std::vector<PersistLayerMatch> run;
@@ -1382,7 +1399,18 @@ int try_fuse_persist(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C)
     const char *spin = getenv("GGML_MI355X_PERSIST_SPIN"), *stall = getenv("GGML_MI355X_PERSIST_STALL_HOP");
     a.spin_limit = spin && *spin ? atol(spin) : 0;
     a.debug_stall_hop = stall && *stall ? atoi(stall) : -1;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    MI_HIP_CHECK(hipStreamIsCapturing(ctx->stream, &cap));
+    const bool timed = ctx->persist_timing && cap == hipStreamCaptureStatusNone;
+    if (timed) {
+        collect_persist_timing(ctx);  // one event pair: a launch not yet read is read first
+        MI_HIP_CHECK(hipEventRecord(ctx->pt_ev[0], ctx->stream));
+    }
     MI_K_CHECK(mi_persist_decode_q8_0(ctx->stream, ctx->persist, &a));
+    if (timed) {
+        MI_HIP_CHECK(hipEventRecord(ctx->pt_ev[1], ctx->stream));
+        ctx->pt_pending = true;
+    }
     return run.back().end + 1 - i;
 }
 
@@ -1948,6 +1976,8 @@ void backend_free(ggml_backend_t backend) {
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->fa_ws) (void)hipFree(ctx->fa_ws);
     if (ctx->ffn_counters) (void)hipFree(ctx->ffn_counters);
+    for (hipEvent_t e : ctx->pt_ev)
+        if (e) (void)hipEventDestroy(e);
     if (ctx->rope_tab) (void)hipFree(ctx->rope_tab);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -1993,7 +2023,7 @@ enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgra
         return GGML_STATUS_FAILED;
     }
     ensure_buffers(ctx, cgraph);
-    if (!graphs_enabled()) {
+    if (!ctx->graphs_on) {
         run_graph_nodes(ctx, cgraph);
         return GGML_STATUS_SUCCESS;
     }
@@ -2206,6 +2236,10 @@ ggml_backend_t ggml_backend_mi355x_init(int device) {
     ctx->fuse = fusion_env();
     ctx->persist_on = env_flag("GGML_MI355X_PERSIST", false);
     if (const char *tp = getenv("GGML_MI355X_PERSIST_TRACE")) ctx->persist_trace = tp;
+    ctx->persist_timing = env_flag("GGML_MI355X_PERSIST_TIMING", false);
+    ctx->graphs_on = graphs_env();
+    if (ctx->persist_timing)
+        for (hipEvent_t &e : ctx->pt_ev) MI_HIP_CHECK(hipEventCreate(&e));
     ctx->name = std::string(GGML_MI355X_NAME) + std::to_string(device);
     MI_HIP_CHECK(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
     return new ggml_backend{backend_guid(), kBackendIface, c->devs[device].get(), ctx};
@@ -2220,10 +2254,19 @@ int ggml_backend_mi355x_status(ggml_backend_t backend) {
     BackendCtx *ctx = (BackendCtx *)backend->context;
     set_device(ctx->device);
     MI_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    collect_persist_timing(ctx);
     if (ctx->persist && mi_persist_status(ctx->persist) != MI_OK) ctx->persist_error = true;
     if (!ctx->persist_error) return 0;
     ctx->persist_error = false;
     return -1;
+}
+
+int ggml_backend_mi355x_persist_timing(ggml_backend_t backend, int64_t *launches, double *total_ms) {
+    if (!ggml_backend_is_mi355x(backend) || !launches || !total_ms) return -1;
+    const BackendCtx *ctx = (const BackendCtx *)backend->context;
+    *launches = ctx->pt_launches;
+    *total_ms = ctx->pt_ms;
+    return ctx->persist_timing ? 0 : -1;
 }
 
 bool ggml_backend_mi355x_set_smooth_factors(struct ggml_tensor *weight, const float *s, int64_t n) {

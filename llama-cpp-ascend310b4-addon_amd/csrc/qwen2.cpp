@@ -539,6 +539,13 @@ int mi_qwen2_get_cache(mi_qwen2 *m, int32_t layer, int32_t is_v, int32_t n_pos, 
     return mi_qwen2_get_cache_seq(m, layer, is_v, 0, n_pos, dst, size);
 }
 
+int mi_qwen2_persist_timing(mi_qwen2 *m, int64_t *launches, double *total_ms) {
+    if (!m || !launches || !total_ms) return fail("qwen2: persist_timing: null argument");
+    if (ggml_backend_mi355x_persist_timing(m->backend, launches, total_ms) != 0)
+        return fail("qwen2: persistent-launch timing is off (GGML_MI355X_PERSIST_TIMING=1 at model creation)");
+    return 0;
+}
+
 int mi_qwen2_fill_cache(mi_qwen2 *m, int32_t n_pos, uint64_t seed, float scale) {
     if (n_pos < 0 || n_pos > m->hp.n_ctx) return fail("qwen2: n_pos %d outside the cache", n_pos);
     for (int il = 0; il < m->hp.n_layer; il++) {

@@ -461,6 +461,7 @@ _QWEN_SIGS = {
     "mi_qwen2_decode_batch": (_I, [_P, _P, _P, _P, _P]),
     "mi_qwen2_decode_steps_batch": (_I, [_P, _P, _P, ctypes.c_int32, _P, ctypes.POINTER(ctypes.c_double)]),
     "mi_qwen2_get_cache_seq": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, _SZ]),
+    "mi_qwen2_persist_timing": (_I, [_P, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_double)]),
     "mi_qwen2_set_cache_seq": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, _SZ]),
     "mi_qwen2_fill_cache": (_I, [_P, ctypes.c_int32, ctypes.c_uint64, ctypes.c_float]),
     "mi_qwen2_get_cache": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, _SZ]),
@@ -600,6 +601,13 @@ class Qwen2Model:
         data = np.ascontiguousarray(data, np.uint16)
         self._chk("mi_qwen2_set_cache_seq", _qlib().mi_qwen2_set_cache_seq(
             self.ptr, int(layer), int(is_v), int(seq), int(data.shape[0]), data.ctypes.data, data.nbytes))
+
+    def persist_timing(self):
+        """(launches, total ms) of the persistent layer-stack launches timed so far
+        (GGML_MI355X_PERSIST_TIMING=1 at creation)"""
+        n, ms = _I64(0), ctypes.c_double(0.0)
+        self._chk("mi_qwen2_persist_timing", _qlib().mi_qwen2_persist_timing(self.ptr, ctypes.byref(n), ctypes.byref(ms)))
+        return int(n.value), float(ms.value)
 
     def fill_cache(self, n_pos, seed=0, scale=1.0):
         self._chk("mi_qwen2_fill_cache", _qlib().mi_qwen2_fill_cache(self.ptr, int(n_pos), int(seed), float(scale)))

@@ -181,3 +181,37 @@ def test_persistent_stalled_hop_reports_and_recovers(gpu, monkeypatch, hop):
     _same_steps(ref, stalled, 0, 6, 11, f"after a stall on hop {hop}")
     for m in (node, pers, stalled, ref):
         m.free()
+
+
+def test_persistent_launch_timing(gpu, monkeypatch):
+    # GGML_MI355X_PERSIST_TIMING: every eager persistent launch is timed with events on the
+    # backend's stream and counted; graph replays are not; results are unchanged
+    hp = qs.qwen2_1p5b(n_layer=3, n_ctx=64, wtype=qs.GGML_TYPE_Q8_0)
+    tensors, smooth = qs.synth(hp, seed=61, qk_gain=6.0)
+    monkeypatch.setenv("GGML_MI355X_PERSIST", "0")
+    ref = gpu.Qwen2Model(hp)
+    ref.load(tensors, smooth)
+    monkeypatch.setenv("GGML_MI355X_PERSIST", "1")
+    with pytest.raises(gpu.MiError, match="timing is off"):
+        ref.persist_timing()
+    monkeypatch.setenv("GGML_MI355X_PERSIST_TIMING", "1")
+    monkeypatch.setenv("GGML_MI355X_GRAPHS", "0")
+    eager = gpu.Qwen2Model(hp)
+    eager.load(tensors, smooth)
+    monkeypatch.delenv("GGML_MI355X_GRAPHS")
+    replay = gpu.Qwen2Model(hp)
+    replay.load(tensors, smooth)
+    for k in ("GGML_MI355X_PERSIST", "GGML_MI355X_PERSIST_TIMING"):
+        monkeypatch.delenv(k)
+    assert eager.persist_timing() == (0, 0.0)
+    want, _ = ref.decode_steps(7, 0, 8)
+    got, _ = eager.decode_steps(7, 0, 8)
+    assert np.array_equal(want, got)
+    n, ms = eager.persist_timing()
+    assert n == 8 and 0.0 < ms < 8 * 50.0, (n, ms)
+    got, _ = replay.decode_steps(7, 0, 8)
+    assert np.array_equal(want, got)
+    n, _ = replay.persist_timing()
+    assert 1 <= n < 8, n  # the first graph runs eagerly; the captured replays are not timed
+    for m in (ref, eager, replay):
+        m.free()
