@@ -408,6 +408,18 @@ int mi_fa_decode_batch(void *stream, const float *q, const void *k, const void *
                        size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out,
                        int64_t n_seq, size_t q_seq, size_t k_seq, size_t v_seq, size_t mask_seq, size_t out_seq,
                        void *ws, size_t ws_bytes);
+/* n_rows (1..8) query rows of ONE sequence in one launch: ggml FLASH_ATTN_EXT with
+ * q ne[1] = n_rows (a prompt ubatch of llama.cpp, q permuted to [d, n_rows, n_q_heads]).
+ * Every row reads the same K/V view and the same kv_len[0]; row r uses q + r*q_row and
+ * out + r*out_row (floats, heads contiguous within a row) and mask + r*mask_row
+ * (elements: llama.cpp's causal mask, one F16 row per query row).  Workspace:
+ * mi_fa_decode_batch_workspace_size(..., n_rows).  No reference counterpart: the
+ * reference's attention operator takes one query row (patch:1957-1983); this keeps a
+ * one-sequence ubatch of up to 8 tokens on the device. */
+int mi_fa_decode_rows(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
+                      const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                      size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out, int64_t n_rows,
+                      size_t q_row, size_t mask_row, size_t out_row, void *ws, size_t ws_bytes);
 /* mi_fa_decode_batch whose output goes straight to the input of the next several-row
  * W4A16 projection (mi_mul_mat_q4_0_batch_xp): sequence s's attention output row
  * (n_q_heads * d values, head-major) is written to xp as fp16 (RNE, ggml's src1

@@ -90,6 +90,15 @@ int mi_qwen2_decode_batch(mi_qwen2 *m, const int32_t *tokens, const int32_t *pos
 /* n_steps greedy steps of all sequences from tokens[s] at pos[s]; out_tokens [n_steps][n_seq] */
 int mi_qwen2_decode_steps_batch(mi_qwen2 *m, const int32_t *tokens, const int32_t *pos, int32_t n_steps,
                                 int32_t *out_tokens, double *seconds);
+/* prompt tokens of sequence seq at positions pos0.. in ubatches of up to n_ubatch (1..8)
+ * tokens, one graph per ubatch as llama.cpp builds it for a prompt batch: MUL_MATs of
+ * n_ubatch rows, FLASH_ATTN_EXT with n_ubatch query rows under the causal KQ mask (one F16
+ * row per token) beside the kv length, logits of the ubatch's last token only.  Writes the
+ * greedy token after the last prompt token (next_token) and its logits [n_vocab] when not
+ * NULL, and the seconds taken.  Cf. the reference's prompt path, which feeds its ubatches
+ * through the same graph (patch:940-1019 chunks the prompt; patch:1286-1309 routes any M). */
+int mi_qwen2_prefill(mi_qwen2 *m, int32_t seq, const int32_t *tokens, int32_t n_tokens, int32_t pos0,
+                     int32_t n_ubatch, int32_t *next_token, float *logits, double *seconds);
 /* the prompt (one token per step), then n_gen timed greedy decode steps: the first
  * consumes the prompt's greedy continuation, out_tokens[i] is the token step i produces;
  * the seconds of the n_gen steps are written to *gen_seconds when not NULL */

@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256) void k_fa_split(const float *__restrict__ q, c
         kc += (size_t)seq * sq.k;
         vc += (size_t)seq * sq.v;
         if (MASK) mask += (size_t)seq * sq.mask;
-        if (kv_len_p) kv_len_p += seq;
+        if (kv_len_p) kv_len_p += (size_t)seq * sq.kvl;
         out += (size_t)seq * sq.out;
         part += (size_t)seq * gridDim.y * GQ * n_splits * part_stride<D>();
         if (counters) counters += (size_t)seq * gridDim.y;
@@ -655,7 +655,7 @@ static int fa_decode_run(void *stream, const float *q, const void *k, const void
                          size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out,
                          int64_t n_seq, size_t q_seq, size_t k_seq, size_t v_seq, size_t mask_seq, size_t out_seq,
                          void *ws, size_t ws_bytes, bool partials_only, uint16_t *xp = nullptr,
-                         bool use_counters = true) {
+                         bool use_counters = true, size_t kvl_seq = 1) {
     MI_CHECK_ARG(q && k && v && (out || partials_only || xp), "fa_decode: null pointer");
     MI_CHECK_ARG(n_kv > 0 && n_kv < (1ll << 31) && n_q_heads > 0 && n_kv_heads > 0 && n_q_heads % n_kv_heads == 0,
                  "fa_decode: bad heads/length n_kv=%lld nq=%lld nkv=%lld", (long long)n_kv, (long long)n_q_heads,
@@ -695,6 +695,7 @@ static int fa_decode_run(void *stream, const float *q, const void *k, const void
     a.sq.v = v_seq;
     a.sq.mask = mask_seq;
     a.sq.out = out_seq;
+    a.sq.kvl = kvl_seq;
     a.partials_only = partials_only;
     a.xp = xp;
     a.xp_nb = (int)(n_q_heads * d / 32);
@@ -722,6 +723,18 @@ int mi_fa_decode_batch_q4act(void *stream, const float *q, const void *k, const 
     return fa_decode_run(stream, q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1, k_nb2, v_nb1, v_nb2,
                          scale, nullptr, n_seq, q_seq, k_seq, v_seq, mask_seq, 0, ws, ws_bytes, false,
                          (uint16_t *)xp);
+}
+
+int mi_fa_decode_rows(void *stream, const float *q, const void *k, const void *v, const uint16_t *mask,
+                      const int32_t *kv_len, int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d,
+                      size_t k_nb1, size_t k_nb2, size_t v_nb1, size_t v_nb2, float scale, float *out, int64_t n_rows,
+                      size_t q_row, size_t mask_row, size_t out_row, void *ws, size_t ws_bytes) {
+    MI_CHECK_ARG(n_rows >= 1 && n_rows <= kFaMaxRows, "fa_decode_rows: %lld query rows (1..%d)", (long long)n_rows,
+                 kFaMaxRows);
+    // every row reads the same cache and length; row r takes mask row r
+    return fa_decode_run(stream, q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1, k_nb2, v_nb1, v_nb2,
+                         scale, out, n_rows, q_row, 0, 0, mask ? mask_row : 0, out_row, ws, ws_bytes, false, nullptr,
+                         true, 0);
 }
 
 int64_t mi_fa_decode_num_splits(int64_t n_kv, int64_t n_q_heads, int64_t n_kv_heads, int64_t d) {

@@ -43,6 +43,8 @@ struct FaPlan {
 // tiles.  With at most kFusedMaxSplits splits the last workgroup of a kv head can
 // merge the partials itself (opt-in).  MI_FA_CHUNK=<positions> overrides the chunk.
 constexpr int kFusedMaxSplits = 16;
+// query rows of one sequence in one launch (a prompt ubatch): the MUL_MAT row limit
+constexpr int kFaMaxRows = 8;
 constexpr int kMaxSplits = 1024;
 
 inline int fa_chunk_override() {
@@ -104,8 +106,12 @@ inline size_t fa_part_bytes(int64_t n_q_heads, int64_t n_splits, int64_t d) {
 // Sequences (grid z) are independent problems: per-sequence strides of q / out
 // (floats), K / V (bytes) and mask (elements); kv_len and the partials are indexed by
 // sequence.
+// per-launch-row element strides (blockIdx.z): a row is a sequence of a batch, or one of
+// the query rows of a single sequence's ubatch (then k = v = kvl = 0: one cache, one
+// length, and its own mask row)
 struct FaSeq {
     size_t q, k, v, mask, out;
+    size_t kvl = 1;
 };
 
 __device__ __forceinline__ void st_coherent(float *p, float v) {
@@ -187,7 +193,7 @@ __device__ __forceinline__ void fa_mfma_tile(const float *__restrict__ q, const 
         kc += (size_t)seq * sq.k;
         vc += (size_t)seq * sq.v;
         if (MASK) mask += (size_t)seq * sq.mask;
-        if (kv_len_p) kv_len_p += seq;
+        if (kv_len_p) kv_len_p += (size_t)seq * sq.kvl;
         out += (size_t)seq * sq.out;
         part += (size_t)seq * n_kvh * GQ * n_splits * part_stride<D>();
     }

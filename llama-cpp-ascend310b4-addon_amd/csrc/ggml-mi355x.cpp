@@ -8,7 +8,8 @@
 //   set_tensor       ND bytes at tensor->data, side copy built when the tensor is
 //                    complete; chunked and concurrent uploads through a per-tensor
 //                    tracker under a mutex (patch:1647-1653, 1700-1809)
-//   supports_op      MUL_MAT with M <= 8, FLASH_ATTN_EXT with one query row
+//   supports_op      MUL_MAT with M <= 8, FLASH_ATTN_EXT with one query row per sequence
+//                    or up to 8 rows of one sequence
 //                    (cf. patch:1925-1983), everything else false -> CPU fallback
 //   graph_compute    per-node dispatch on one stream (patch:1884-1922); runtime
 //                    errors abort like ACL_CHECK; GGML_MI355X_TRACE_NODE_SYNC=1
@@ -471,9 +472,11 @@ bool supports_fa(const ggml_tensor *op) {
     memcpy(&softcap, (const float *)op->op_params + 2, sizeof(float));
     if (max_bias != 0.0f || softcap != 0.0f || sinks) return false;
     if (!q || q->type != GGML_TYPE_F32 || op->type != GGML_TYPE_F32 || !ggml_is_contiguous(op)) return false;
-    // one query row per head and stream; streams (ne[3]) are independent sequences
-    const int64_t n_seq = q->ne[3];
-    if (q->ne[1] != 1 || q->nb[0] != 4 || (q->ne[2] > 1 && q->nb[2] != (size_t)q->ne[0] * 4) || q->nb[3] % 4) return false;
+    // streams (ne[3]) are independent sequences with one query row each, or one stream
+    // carries up to 8 query rows (ne[1]: a prompt ubatch, each row with its own mask row)
+    const int64_t n_seq = q->ne[3], n_rows = q->ne[1];
+    if (n_rows < 1 || n_rows > 8 || (n_rows > 1 && n_seq != 1)) return false;
+    if (q->nb[0] != 4 || (q->ne[2] > 1 && q->nb[2] != (size_t)q->ne[0] * 4) || q->nb[3] % 4 || q->nb[1] % 4) return false;
     if (k->type != GGML_TYPE_F16 || v->type != GGML_TYPE_F16) return false;
     const int64_t d = q->ne[0];
     if ((d != 64 && d != 128) || k->ne[0] != d || v->ne[0] != d) return false;
@@ -482,9 +485,9 @@ bool supports_fa(const ggml_tensor *op) {
     if (k->nb[0] != 2 || v->nb[0] != 2 || k->nb[1] % 16 || k->nb[2] % 16 || v->nb[1] % 16 || v->nb[2] % 16 ||
         (n_seq > 1 && (k->nb[3] % 16 || v->nb[3] % 16)))
         return false;
-    // one mask row per sequence, shared by the heads
+    // one mask row per sequence (or per query row), shared by the heads
     if (mask && (mask->type != GGML_TYPE_F16 || mask->ne[0] < k->ne[1] || mask->nb[0] != 2 || mask->ne[2] != 1 ||
-                 (mask->ne[3] != 1 && mask->ne[3] != n_seq)))
+                 mask->ne[1] < n_rows || (mask->ne[3] != 1 && mask->ne[3] != n_seq)))
         return false;
     if (kvl && (kvl->type != GGML_TYPE_I32 || !ggml_is_contiguous(kvl) || ggml_nelements(kvl) < n_seq)) return false;
     return true;
@@ -550,7 +553,7 @@ const float *inv_s_of(const ggml_tensor *w) {
 
 size_t fa_ws_need(const ggml_tensor *node) {
     const ggml_tensor *q = node->src[0], *k = node->src[1];
-    return mi_fa_decode_batch_workspace_size(k->ne[1], q->ne[2], k->ne[2], q->ne[0], q->ne[3]);
+    return mi_fa_decode_batch_workspace_size(k->ne[1], q->ne[2], k->ne[2], q->ne[0], q->ne[3] * q->ne[1]);
 }
 
 size_t scratch_need(const ggml_tensor *node) {
@@ -651,6 +654,15 @@ void run_fa(BackendCtx *ctx, ggml_tensor *node) {
     const ggml_tensor *kvl = node->src[5];
     float scale;
     memcpy(&scale, node->op_params, sizeof(float));
+    if (q->ne[1] > 1) {  // one sequence's query rows: output [d, n_head, n_rows] contiguous
+        MI_K_CHECK(mi_fa_decode_rows(ctx->stream, (const float *)q->data, k->data, v->data,
+                                     mask ? (const uint16_t *)mask->data : nullptr,
+                                     kvl ? (const int32_t *)kvl->data : nullptr, k->ne[1], q->ne[2], k->ne[2],
+                                     q->ne[0], k->nb[1], k->nb[2], v->nb[1], v->nb[2], scale, (float *)node->data,
+                                     q->ne[1], q->nb[1] / 4, mask ? mask->nb[1] / 2 : 0,
+                                     (size_t)(q->ne[0] * q->ne[2]), ctx->fa_ws, ctx->fa_ws_size));
+        return;
+    }
     // output [d, n_head, 1, n_seq] contiguous; per-sequence strides of the inputs
     const size_t mask_seq = mask && mask->ne[3] > 1 ? mask->nb[3] / 2 : 0;
     MI_K_CHECK(mi_fa_decode_batch(ctx->stream, (const float *)q->data, k->data, v->data,

@@ -23,6 +23,7 @@
 #include <chrono>
 #include <map>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include <hip/hip_runtime.h>
@@ -44,7 +45,11 @@ int fail(const char *fmt, ...) {
     return -1;
 }
 
+constexpr int kMaxUbatch = 8;                      // prompt tokens per ubatch (the MUL_MAT row limit)
+constexpr int kPromptWords = 3 * kMaxUbatch + 2;  // pinned prompt inputs + the greedy token read back
+
 struct Graph {
+    int n_kv = 0;  // KV view length
     ggml_context *ctx = nullptr;
     ggml_cgraph *gf = nullptr;
     ggml_gallocr_t galloc = nullptr;
@@ -77,7 +82,12 @@ struct mi_qwen2 {
     int32_t mask_window = 0;  // 0: causal only
     ggml_tensor *mask = nullptr;
     uint16_t *mask_pinned = nullptr;
+    // prompt ubatches (mi_qwen2_prefill): I32 [3 * 8 + 1] tokens, positions, the kv length,
+    // cache rows; the causal mask F16 [n_kv, T] of the ubatch (up to n_ctx x 8)
+    ggml_tensor *inp_pf = nullptr, *mask_pf = nullptr;
+    uint16_t *mask_pf_pinned = nullptr;
     std::map<int, Graph> graphs;  // by KV view length
+    std::map<std::tuple<int, int, int>, Graph> pgraphs;  // prompt ubatches: (KV view, rows, sequence)
     Graph *last = nullptr;        // the graph of the latest decode step
     bool dump = false;            // graphs keep ffn_norm-N / ffn_out-N as outputs
 };
@@ -97,21 +107,30 @@ ggml_tensor *add_tensor(mi_qwen2 *m, const std::string &name, ggml_type type, in
     return t;
 }
 
-Graph build_graph(mi_qwen2 *m, int n_kv) {
+// One decode step of every sequence (T = 0: S = n_seq streams of one token each), or a
+// prompt ubatch of T tokens of sequence `seq` (one stream; FLASH_ATTN_EXT with T query
+// rows and llama.cpp's causal mask, one mask row per token; logits of the last token).
+Graph build_graph(mi_qwen2 *m, int n_kv, int T = 0, int seq = 0) {
     const mi_qwen2_hparams &hp = m->hp;
-    const int S = m->n_seq;
+    const bool prompt = T > 0;
+    const int S = prompt ? 1 : m->n_seq;  // KV streams
+    if (!prompt) T = 1;
+    const int R = S * T;                  // activation rows
     const int hd = hp.head_dim, n_embd_kv = hp.n_head_kv * hd;
     Graph G;
+    G.n_kv = n_kv;
     ggml_init_params ip = {0, nullptr, true};
     G.ctx = ggml_init(ip);
     ggml_context *ctx = G.ctx;
     ggml_cgraph *gf = ggml_new_graph_custom(ctx, 16384, false);
     G.gf = gf;
 
-    ggml_tensor *tok = ggml_view_1d(ctx, m->inp, S, 0);
-    ggml_tensor *pos = ggml_view_1d(ctx, m->inp, S, 4 * (size_t)S);
-    ggml_tensor *kvl = ggml_view_1d(ctx, m->inp, S, 8 * (size_t)S);
-    ggml_tensor *kidx = ggml_view_1d(ctx, m->inp, S, 12 * (size_t)S);
+    // inputs: R tokens, R positions, S kv lengths, R cache rows
+    ggml_tensor *in = prompt ? m->inp_pf : m->inp;
+    ggml_tensor *tok = ggml_view_1d(ctx, in, R, 0);
+    ggml_tensor *pos = ggml_view_1d(ctx, in, R, 4 * (size_t)R);
+    ggml_tensor *kvl = ggml_view_1d(ctx, in, S, 8 * (size_t)R);
+    ggml_tensor *kidx = ggml_view_1d(ctx, in, R, 8 * (size_t)R + 4 * (size_t)S);
     ggml_tensor *tok_embd = W(m, "token_embd.weight");
 
     ggml_tensor *inpL = ggml_get_rows(ctx, tok_embd, tok);
@@ -134,8 +153,8 @@ Graph build_graph(mi_qwen2 *m, int n_kv) {
             ggml_build_forward_expand(gf, K);
             ggml_build_forward_expand(gf, V);
         }
-        Q = ggml_reshape_3d(ctx, Q, hd, hp.n_head, S);
-        K = ggml_reshape_3d(ctx, K, hd, hp.n_head_kv, S);
+        Q = ggml_reshape_3d(ctx, Q, hd, hp.n_head, R);
+        K = ggml_reshape_3d(ctx, K, hd, hp.n_head_kv, R);
         Q = ggml_rope_ext(ctx, Q, pos, nullptr, hd, GGML_ROPE_TYPE_NEOX, 0, hp.rope_theta, 1.0f, 0.0f, 1.0f, 0.0f,
                           0.0f);
         K = ggml_rope_ext(ctx, K, pos, nullptr, hd, GGML_ROPE_TYPE_NEOX, 0, hp.rope_theta, 1.0f, 0.0f, 1.0f, 0.0f,
@@ -143,20 +162,24 @@ Graph build_graph(mi_qwen2 *m, int n_kv) {
         ggml_build_forward_expand(gf, Q);  // rope q, rope k, then the two cache writes: the
         ggml_build_forward_expand(gf, K);  // attention-input chain the backend fuses
         ggml_tensor *kc = m->k_cache[il], *vc = m->v_cache[il];
-        ggml_build_forward_expand(gf, ggml_set_rows(ctx, kc, ggml_reshape_2d(ctx, K, n_embd_kv, S), kidx));
+        ggml_build_forward_expand(gf, ggml_set_rows(ctx, kc, ggml_reshape_2d(ctx, K, n_embd_kv, R), kidx));
         ggml_build_forward_expand(gf, ggml_set_rows(ctx, vc, V, kidx));
         // sequence s's cache is rows [s*n_ctx, (s+1)*n_ctx): stream s of the 4-D view
         const size_t seq_bytes = (size_t)hp.n_ctx * kc->nb[1];
+        const size_t seq_off = prompt ? (size_t)seq * seq_bytes : 0;
         ggml_tensor *k = ggml_view_4d(ctx, kc, hd, n_kv, hp.n_head_kv, S, kc->nb[1], ggml_row_size(GGML_TYPE_F16, hd),
-                                      seq_bytes, 0);
+                                      seq_bytes, seq_off);
         ggml_tensor *v = ggml_view_4d(ctx, vc, hd, n_kv, hp.n_head_kv, S, vc->nb[1], ggml_row_size(GGML_TYPE_F16, hd),
-                                      seq_bytes, 0);
-        ggml_tensor *q = ggml_permute(ctx, ggml_reshape_4d(ctx, Q, hd, hp.n_head, 1, S), 0, 2, 1, 3);
-        ggml_tensor *kq_mask = m->mask ? ggml_view_1d(ctx, m->mask, n_kv, 0) : nullptr;
+                                      seq_bytes, seq_off);
+        // q [hd, T, n_head, S], as llama.cpp permutes it for FLASH_ATTN_EXT
+        ggml_tensor *q = ggml_permute(ctx, ggml_reshape_4d(ctx, Q, hd, hp.n_head, T, S), 0, 2, 1, 3);
+        ggml_tensor *kq_mask = prompt   ? ggml_view_2d(ctx, m->mask_pf, n_kv, T, (size_t)n_kv * 2, 0)
+                               : m->mask ? ggml_view_1d(ctx, m->mask, n_kv, 0)
+                                         : nullptr;
         ggml_tensor *att = ggml_flash_attn_ext(ctx, q, k, v, kq_mask, kq_scale, 0.0f, 0.0f);
         ggml_flash_attn_ext_add_kv_lengths(att, kvl);
         ggml_flash_attn_ext_set_prec(att, GGML_PREC_F32);
-        cur = ggml_reshape_2d(ctx, att, hd * hp.n_head, S);
+        cur = ggml_reshape_2d(ctx, att, hd * hp.n_head, R);
         cur = ggml_mul_mat(ctx, W(m, p + "attn_output.weight"), cur);
         ggml_tensor *ffn_inp = ggml_add(ctx, cur, inpL);
         cur = ggml_rms_norm(ctx, ffn_inp, hp.rms_eps);
@@ -181,6 +204,8 @@ Graph build_graph(mi_qwen2 *m, int n_kv) {
         ggml_set_name(inpL, ("l_out-" + std::to_string(il)).c_str());  // the eval-callback name
         G.l_out.push_back(inpL);
     }
+    // a prompt ubatch's logits: its last token only (llama.cpp's output ids)
+    if (prompt && T > 1) inpL = ggml_view_2d(ctx, inpL, hp.n_embd, 1, inpL->nb[1], (size_t)(T - 1) * inpL->nb[1]);
     ggml_tensor *cur = ggml_rms_norm(ctx, inpL, hp.rms_eps);
     cur = ggml_mul(ctx, cur, W(m, "output_norm.weight"));
     G.logits = ggml_mul_mat(ctx, tok_embd, cur);  // tied output head
@@ -204,6 +229,15 @@ Graph &graph_for(mi_qwen2 *m, int32_t kv_len) {
     auto it = m->graphs.find(n_kv);
     if (it != m->graphs.end()) return it->second;
     return m->graphs.emplace(n_kv, build_graph(m, n_kv)).first->second;
+}
+
+Graph &prompt_graph_for(mi_qwen2 *m, int32_t kv_len, int T, int seq) {
+    int n_kv = (kv_len + 255) / 256 * 256;
+    if (n_kv > m->hp.n_ctx) n_kv = m->hp.n_ctx;
+    const auto key = std::make_tuple(n_kv, T, seq);
+    auto it = m->pgraphs.find(key);
+    if (it != m->pgraphs.end()) return it->second;
+    return m->pgraphs.emplace(key, build_graph(m, n_kv, T, seq)).first->second;
 }
 
 int check_cache_args(mi_qwen2 *m, int32_t layer, int32_t seq, int32_t n_pos) {
@@ -237,7 +271,8 @@ mi_qwen2 *mi_qwen2_create(const mi_qwen2_hparams *hp, int device) {
         fail("qwen2: no MI355X device %d", device);
         return nullptr;
     }
-    if (hipHostMalloc((void **)&m->io_pinned, 5 * (size_t)m->n_seq * sizeof(int32_t), hipHostMallocDefault) !=
+    if (hipHostMalloc((void **)&m->io_pinned, (5 * (size_t)m->n_seq + kPromptWords) * sizeof(int32_t),
+                      hipHostMallocDefault) !=
         hipSuccess) {
         ggml_backend_free(m->backend);
         delete m;
@@ -276,6 +311,12 @@ mi_qwen2 *mi_qwen2_create(const mi_qwen2_hparams *hp, int device) {
     m->inp = ggml_new_tensor_1d(m->wctx, GGML_TYPE_I32, 4 * (int64_t)m->n_seq);
     ggml_set_name(m->inp, "inp_decode");
     ggml_set_input(m->inp);
+    m->inp_pf = ggml_new_tensor_1d(m->wctx, GGML_TYPE_I32, 3 * kMaxUbatch + 1);
+    ggml_set_name(m->inp_pf, "inp_prompt");
+    ggml_set_input(m->inp_pf);
+    m->mask_pf = ggml_new_tensor_1d(m->wctx, GGML_TYPE_F16, (int64_t)hp->n_ctx * kMaxUbatch);
+    ggml_set_name(m->mask_pf, "inp_kq_mask_prompt");
+    ggml_set_input(m->mask_pf);
     {
         const char *e = getenv("MI_QWEN2_KQ_MASK");
         if (e && !strncmp(e, "swa:", 4)) m->mask_window = std::max(1, atoi(e + 4));
@@ -293,7 +334,9 @@ mi_qwen2 *mi_qwen2_create(const mi_qwen2_hparams *hp, int device) {
         return nullptr;
     }
     ggml_backend_buffer_set_usage(m->wbuf, GGML_BACKEND_BUFFER_USAGE_WEIGHTS);
-    if (m->mask && hipHostMalloc((void **)&m->mask_pinned, (size_t)hp->n_ctx * 2, hipHostMallocDefault) != hipSuccess) {
+    if ((m->mask && hipHostMalloc((void **)&m->mask_pinned, (size_t)hp->n_ctx * 2, hipHostMallocDefault) != hipSuccess) ||
+        hipHostMalloc((void **)&m->mask_pf_pinned, (size_t)hp->n_ctx * kMaxUbatch * 2, hipHostMallocDefault) !=
+            hipSuccess) {
         mi_qwen2_free(m);
         fail("qwen2: pinned host allocation failed");
         return nullptr;
@@ -308,11 +351,16 @@ void mi_qwen2_free(mi_qwen2 *m) {
         ggml_gallocr_free(kv.second.galloc);
         ggml_free(kv.second.ctx);
     }
+    for (auto &kv : m->pgraphs) {
+        ggml_gallocr_free(kv.second.galloc);
+        ggml_free(kv.second.ctx);
+    }
     ggml_backend_buffer_free(m->wbuf);
     ggml_free(m->wctx);
     ggml_backend_free(m->backend);
     if (m->io_pinned) (void)hipHostFree(m->io_pinned);
     if (m->mask_pinned) (void)hipHostFree(m->mask_pinned);
+    if (m->mask_pf_pinned) (void)hipHostFree(m->mask_pf_pinned);
     delete m;
 }
 
@@ -501,6 +549,51 @@ int mi_qwen2_decode_steps(mi_qwen2 *m, int32_t token, int32_t pos, int32_t n_ste
                           double *seconds) {
     if (m->n_seq != 1) return fail("qwen2: mi_qwen2_decode_steps needs n_seq == 1");
     return mi_qwen2_decode_steps_batch(m, &token, &pos, n_steps, out_tokens, seconds);
+}
+
+int mi_qwen2_prefill(mi_qwen2 *m, int32_t seq, const int32_t *tokens, int32_t n_tokens, int32_t pos0,
+                     int32_t n_ubatch, int32_t *next_token, float *logits, double *seconds) {
+    if (!m || !tokens) return fail("qwen2: prefill: null argument");
+    if (seq < 0 || seq >= m->n_seq) return fail("qwen2: prefill: sequence %d of %d", seq, m->n_seq);
+    if (n_ubatch < 1 || n_ubatch > kMaxUbatch) return fail("qwen2: prefill: ubatch of %d tokens (1..%d)", n_ubatch,
+                                                           kMaxUbatch);
+    if (n_tokens < 1 || pos0 < 0 || pos0 + n_tokens > m->hp.n_ctx)
+        return fail("qwen2: prefill: positions %d..%d outside the cache (%d)", pos0, pos0 + n_tokens - 1, m->hp.n_ctx);
+    for (int32_t i = 0; i < n_tokens; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->hp.n_vocab) return fail("qwen2: prefill: token %d outside the vocabulary",
+                                                                     tokens[i]);
+    int32_t *in = m->io_pinned + 5 * (size_t)m->n_seq, *out = in + 3 * kMaxUbatch + 1;
+    const auto t0 = std::chrono::steady_clock::now();
+    Graph *G = nullptr;
+    for (int32_t done = 0; done < n_tokens;) {
+        const int T = std::min(n_ubatch, n_tokens - done);
+        const int32_t p0 = pos0 + done, kv_len = p0 + T;
+        G = &prompt_graph_for(m, kv_len, T, seq);
+        const int64_t n_kv = G->n_kv;
+        for (int t = 0; t < T; t++) {
+            in[t] = tokens[done + t];
+            in[T + t] = p0 + t;
+            in[2 * T + 1 + t] = seq * m->hp.n_ctx + p0 + t;
+        }
+        in[2 * T] = kv_len;
+        // causal: token t sees positions <= p0 + t (fp16 0), not the later ones (-inf)
+        for (int t = 0; t < T; t++)
+            for (int64_t j = 0; j < n_kv; j++) m->mask_pf_pinned[t * n_kv + j] = j <= p0 + t ? 0x0000 : 0xFC00;
+        ggml_backend_tensor_set_async(m->backend, m->inp_pf, in, 0, (3 * (size_t)T + 1) * sizeof(int32_t));
+        ggml_backend_tensor_set_async(m->backend, m->mask_pf, m->mask_pf_pinned, 0, (size_t)T * n_kv * 2);
+        if (ggml_backend_graph_compute(m->backend, G->gf) != GGML_STATUS_SUCCESS) return fail("qwen2: graph failed");
+        done += T;
+        if (done == n_tokens && next_token)
+            ggml_backend_tensor_get_async(m->backend, G->argmax, out, 0, sizeof(int32_t));
+        // one synchronisation per ubatch: the pinned inputs are rewritten for the next one
+        if (ggml_backend_mi355x_status(m->backend) != 0) return fail("qwen2: prefill failed: %s", mi_last_error());
+    }
+    const auto t1 = std::chrono::steady_clock::now();
+    if (seconds) *seconds = std::chrono::duration<double>(t1 - t0).count();
+    m->last = G;
+    if (next_token) *next_token = out[0];
+    if (logits) ggml_backend_tensor_get(G->logits, logits, 0, ggml_nbytes(G->logits));
+    return 0;
 }
 
 int mi_qwen2_generate(mi_qwen2 *m, const int32_t *prompt, int32_t n_prompt, int32_t n_gen, int32_t *out_tokens,

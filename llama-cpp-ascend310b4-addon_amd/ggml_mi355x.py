@@ -90,6 +90,8 @@ _SIGS = {
     "mi_fa_decode_batch_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "mi_fa_decode_batch": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _SZ, _SZ, _SZ, _SZ, _F, _P, _I64, _SZ,
                                 _SZ, _SZ, _SZ, _SZ, _P, _SZ]),
+    "mi_fa_decode_rows": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _SZ, _SZ, _SZ, _SZ, _F, _P, _I64, _SZ,
+                               _SZ, _SZ, _P, _SZ]),
     "mi_fa_decode_num_splits": (_I64, [_I64, _I64, _I64, _I64]),
     "mi_fa_decode_partials": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _SZ, _SZ, _SZ, _SZ, _F, _P, _SZ]),
     "mi_fa_decode_noalloc_max_workspace": (_SZ, []),
@@ -425,6 +427,12 @@ def fa_decode_batch(q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1
           ws_bytes)
 
 
+def fa_decode_rows(q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1, k_nb2, v_nb1, v_nb2, scale, out,
+                   n_rows, q_row, mask_row, out_row, ws, ws_bytes, stream=None):
+    _call("mi_fa_decode_rows", _P(stream), _P(q), _P(k), _P(v), _P(mask), _P(kv_len), n_kv, n_q_heads, n_kv_heads,
+          d, k_nb1, k_nb2, v_nb1, v_nb2, scale, _P(out), n_rows, q_row, mask_row, out_row, _P(ws), ws_bytes)
+
+
 def fa_decode_noalloc(q, k, v, mask, kv_len, n_kv, n_q_heads, n_kv_heads, d, k_nb1, k_nb2, v_nb1, v_nb2, scale,
                       out, stream=None):
     """mi_fa_decode on the library's fixed per-device scratch (allocates nothing)"""
@@ -462,6 +470,8 @@ _QWEN_SIGS = {
     "mi_qwen2_decode_steps_batch": (_I, [_P, _P, _P, ctypes.c_int32, _P, ctypes.POINTER(ctypes.c_double)]),
     "mi_qwen2_get_cache_seq": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, _SZ]),
     "mi_qwen2_persist_timing": (_I, [_P, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_double)]),
+    "mi_qwen2_prefill": (_I, [_P, ctypes.c_int32, _P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, _P,
+                              ctypes.POINTER(ctypes.c_double)]),
     "mi_qwen2_set_cache_seq": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, _SZ]),
     "mi_qwen2_fill_cache": (_I, [_P, ctypes.c_int32, ctypes.c_uint64, ctypes.c_float]),
     "mi_qwen2_get_cache": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, _SZ]),
@@ -601,6 +611,17 @@ class Qwen2Model:
         data = np.ascontiguousarray(data, np.uint16)
         self._chk("mi_qwen2_set_cache_seq", _qlib().mi_qwen2_set_cache_seq(
             self.ptr, int(layer), int(is_v), int(seq), int(data.shape[0]), data.ctypes.data, data.nbytes))
+
+    def prefill(self, tokens, pos0=0, n_ubatch=8, seq=0, want_logits=False):
+        """prompt tokens in ubatches of n_ubatch -> (next token, logits or None, seconds)"""
+        t = np.ascontiguousarray(tokens, np.int32)
+        nxt = ctypes.c_int32(0)
+        lg = np.empty(self.hp["n_vocab"], np.float32) if want_logits else None
+        secs = ctypes.c_double(0.0)
+        self._chk("mi_qwen2_prefill", _qlib().mi_qwen2_prefill(
+            self.ptr, int(seq), t.ctypes.data, int(t.size), int(pos0), int(n_ubatch), ctypes.byref(nxt),
+            lg.ctypes.data if want_logits else None, ctypes.byref(secs)))
+        return int(nxt.value), lg, secs.value
 
     def persist_timing(self):
         """(launches, total ms) of the persistent layer-stack launches timed so far

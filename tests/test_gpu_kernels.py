@@ -356,6 +356,40 @@ def test_fa_decode_batch_eight_sequences(gpu, orc):
         _check_fa(orc, o[s], q[s], kc[s], vc[s], nkv, 1 / np.sqrt(d), kv_len=lens[s], label=f"seq {s}")
 
 
+@pytest.mark.parametrize("T,L,p0,use_kvl", [(8, 4096, 1000, True), (3, 256, 100, False), (8, 512, 0, True),
+                                             (5, 32768, 30000, True), (2, 768, 700, False)])
+def test_fa_decode_rows_prompt_ubatch(gpu, orc, T, L, p0, use_kvl):
+    """A prompt ubatch of one sequence: T query rows per head (q [d, T, n_head] as llama.cpp
+    permutes it), one K/V view and kv length for all rows, llama.cpp's causal mask (row t
+    keeps positions <= p0 + t) with a hole and a finite bias; every row against the oracle
+    run with its own mask row."""
+    mi = gpu
+    nq, nkv, d = 12, 2, 128
+    rng = np.random.default_rng(T * 7 + L)
+    q = rng.standard_normal((T, nq, d)).astype(np.float32)
+    kc = f16_bits(rng.standard_normal((L, nkv, d)))
+    vc = f16_bits(rng.standard_normal((L, nkv, d)))
+    mask = np.zeros((T, L), np.float32)
+    for t in range(T):
+        mask[t, p0 + t + 1:] = -np.inf
+    mask[:, p0 // 2: p0 // 2 + 3] = -np.inf
+    mask[:, p0 // 3] = -2.5
+    m16 = f16_bits(mask)
+    kvl = p0 + T if use_kvl else None
+    dq, dk, dv, dm = mi.to_device(q), mi.to_device(kc), mi.to_device(vc), mi.to_device(m16)
+    dl = mi.to_device(np.array([kvl], np.int32)) if use_kvl else None
+    out = mi.DeviceBuffer(T * nq * d * 4)
+    wsb = mi.fa_decode_batch_workspace_size(L, nq, nkv, d, T)
+    ws = mi.DeviceBuffer(wsb).zero()
+    nb1 = nkv * d * 2
+    mi.fa_decode_rows(dq.ptr, dk.ptr, dv.ptr, dm.ptr, dl.ptr if dl else None, L, nq, nkv, d, nb1, d * 2, nb1, d * 2,
+                      1 / np.sqrt(d), out.ptr, T, nq * d, L, nq * d, ws.ptr, wsb)
+    mi.device_sync()
+    o = out.download(np.float32).reshape(T, nq, d)
+    for t in range(T):
+        _check_fa(orc, o[t], q[t], kc, vc, nkv, 1 / np.sqrt(d), mask=m16[t], kv_len=kvl, label=f"row {t}")
+
+
 @pytest.mark.parametrize("L", [600_000, 1_100_000])
 def test_fa_decode_longest_views(gpu, orc, L):
     """Views past 512K positions, where the split count cap lengthens each wave's run to

@@ -288,6 +288,71 @@ def test_qwen2_batch_of_sequences(gpu, orc, wtype):
     assert mism == 0
 
 
+@pytest.mark.parametrize("wtype,n_ubatch", [(qs.GGML_TYPE_Q8_0, 8), (qs.GGML_TYPE_Q4_0, 8), (qs.GGML_TYPE_Q8_0, 3)])
+def test_qwen2_prompt_ubatches(gpu, orc, wtype, n_ubatch):
+    """The prompt fed in ubatches of n_ubatch tokens (mi_qwen2_prefill: MUL_MATs of several
+    rows, FLASH_ATTN_EXT with several query rows under llama.cpp's causal mask, the last
+    token's logits) against the same model fed one token per step on the GPU and against
+    the CPU models fed one token per step.
+
+    Bar: with Q8_0 weights the ubatch path is bit-identical to the one-token path (logits,
+    every K/V cache row, and the greedy steps decoded afterwards: the several-row GEMV keeps
+    each row's block order); with Q4_0 weights (matrix-core several-row GEMVs) within a
+    relative 2e-3.  Against the CPU at the prompt's end: logits within the whole-model bar
+    of this file and the same greedy token."""
+    mi = gpu
+    n_prompt, n_gen = 261, 8   # a ragged last ubatch; KV views of 256 and 320 positions
+    hp = qs.qwen2_1p5b(n_layer=2, n_ctx=320, n_vocab=32000, wtype=wtype)
+    tensors, smooth = qs.synth(hp, seed=27, qk_gain=6.0)
+    model, ref = mi.Qwen2Model(hp), mi.Qwen2Model(hp)
+    model.load(tensors, smooth)
+    ref.load(tensors, smooth)
+    cpu = orc.Qwen2(hp, tensors, smooth, fa_mode=0, n_threads=8)
+    exact = orc.Qwen2(hp, tensors, smooth, fa_mode=1, n_threads=8)
+    q8 = wtype == qs.GGML_TYPE_Q8_0
+    gen = orc.Qwen2(hp, tensors, smooth, fa_mode=1, n_threads=8, q8_generic=True) if q8 else None
+    rng = np.random.default_rng(28)
+    prompt = [int(t) for t in rng.integers(0, hp["n_vocab"], n_prompt)]
+    g_tok, g_log, _ = model.prefill(prompt, 0, n_ubatch, want_logits=True)
+    spread = 0.0
+    for pos, tok in enumerate(prompt):
+        r_tok, r_log = ref.decode(tok, pos, want_logits=True)
+        c_tok, c_log = cpu.decode(tok, pos)
+        e_tok, e_log = exact.decode(tok, pos)
+        if gen is not None:
+            spread = max(spread, float(np.abs(gen.decode(tok, pos)[1] - e_log).max()) / float(np.abs(e_log).max()))
+    scale = float(np.abs(e_log).max())
+    rel_tbt = float(np.abs(g_log - r_log).max()) / scale
+    cache_diff = 0.0
+    for il in range(hp["n_layer"]):
+        for is_v in (0, 1):
+            a = model.get_cache(il, is_v, n_prompt).view(np.float16).astype(np.float32)
+            b = ref.get_cache(il, is_v, n_prompt).view(np.float16).astype(np.float32)
+            cache_diff = max(cache_diff, float(np.abs(a - b).max()))
+    err_ggml = float(np.abs(g_log - c_log).max())
+    rel = float(np.abs(g_log - e_log).max()) / scale
+    print(f"prompt in ubatches of {n_ubatch} ({'Q8_0' if q8 else 'Q4_0'}): vs one token per step on the GPU: "
+          f"logits rel {rel_tbt:.3e}, cache max-abs {cache_diff:.3e}; vs CPU: logit max-abs {err_ggml:.3e}, "
+          f"rel vs exact-attention {rel:.3e} (ggml SIMD/generic spread {spread:.3e}); greedy {g_tok} / {r_tok} / {c_tok}")
+    if q8:
+        assert rel_tbt == 0.0 and cache_diff == 0.0
+    else:
+        assert rel_tbt < 2e-3
+    assert g_tok == r_tok == c_tok
+    assert rel < _bar(spread)
+    tok = g_tok
+    for pos in range(n_prompt, n_prompt + n_gen):
+        g_tok, g_log = model.decode(tok, pos, want_logits=True)
+        r_tok, r_log = ref.decode(tok, pos, want_logits=True)
+        if q8:
+            assert np.array_equal(g_log, r_log), f"position {pos}"
+        else:
+            assert float(np.abs(g_log - r_log).max()) / float(np.abs(r_log).max()) < 2e-3, f"position {pos}"
+        tok = g_tok
+    model.free()
+    ref.free()
+
+
 def test_smooth_scale_file_and_layer_dump(gpu, tmp_path):
     """A SmoothQuant scale file (fp32 [layers, hidden], the scale tool's format) gives the
     same logits as the per-weight factors; the LLDUMP1 dump holds every layer's output per
