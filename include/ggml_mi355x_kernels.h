@@ -213,6 +213,20 @@ int mi_persist_status(void *ctx);
 int mi_mul_mat_q8_0_f32_fused(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
                               float *const *y, const float *const *add, int64_t k, const float *x,
                               const float *norm_w, float eps, const float *inv_s, int rounding);
+/* A ubatch (m = 2..8 activation rows) through up to four Q8_0 matrices of equal k that
+ * read the same activation, in two launches: the activation rows' Q8_0 blocks with
+ * their producer folded in (RMSNorm(x) * norm_w when norm_w is set, k <= 4096; else
+ * silu(x) * x_up when x_up is set, ggml's swiglu; else x), times inv_s; then one GEMV
+ * launch over the stacked matrices with the blocks staged in LDS.  Matrix i writes
+ * y[i] [m, n[i]] (row-major, ggml's MUL_MAT layout) plus bias[i] (a row of n[i],
+ * broadcast) or add[i] ([m, n[i]], a residual), either may be NULL.  Bit-identical to
+ * RMS_NORM + MUL (or GLU) then mi_mul_mat_q8_0_f32 per matrix then ADD.  ws:
+ * mi_xq_size(m, k) bytes, 16-byte aligned.  Cf. the reference's M <= 8 matmul
+ * routing (patch:1207, 1286-1309): one kernel per projection there. */
+int mi_mul_mat_q8_0_f32_batch(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
+                              float *const *y, const float *const *bias, const float *const *add, int64_t k, int64_t m,
+                              const float *x, const float *x_up, const float *norm_w, float eps, const float *inv_s,
+                              int rounding, void *ws, size_t ws_bytes);
 /* FLASH_ATTN_EXT (one token, one sequence) -> MUL_MAT(Q8_0) [-> ADD(add)]: the projection
  * of an attention output left in split form by mi_fa_decode_partials.  Every workgroup
  * merges the n_splits records (the log-sum-exp combine of mi_fa_decode) for its whole

@@ -1438,6 +1438,16 @@ bool q4_batch_node(const ggml_tensor *n) {
            b->ne[1] == m && m >= 2 && m <= 16 && a->ne[0] % 128 == 0 && is_f32_contig(n);
 }
 
+// a Q8_0 MUL_MAT on 2..8 contiguous fp32 activation rows with the prepacked copy ready
+bool q8_batch_node(const ggml_tensor *n) {
+    if (n->op != GGML_OP_MUL_MAT) return false;
+    const ggml_tensor *a = n->src[0], *b = n->src[1];
+    const TensorExtra *ex = (const TensorExtra *)a->extra;
+    const int64_t m = ggml_nrows(b);
+    return packed_fmt(a) == GGML_TYPE_Q8_0 && ex && ex->ready && b->type == GGML_TYPE_F32 && ggml_is_contiguous(b) &&
+           b->ne[1] == m && m >= 2 && m <= 8 && a->ne[0] % 32 == 0 && aligned16(b->data) && is_f32_contig(n);
+}
+
 // ADD(mm, other) as mm's only consumer: other is a bias row of mm's width (broadcast over
 // the rows) or a tensor of mm's shape (the residual)
 const ggml_tensor *batch_add_tail(ggml_cgraph *g, int j, const ggml_tensor *mm, const Consumers &C,
@@ -1572,6 +1582,69 @@ int try_fuse_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C
     return fuse_q4_batch_at(ctx, g, i, i, C, BatchNorm{});
 }
 
+// MUL_MAT x 1..4 (Q8_0, the same 2..8 activation rows and SmoothQuant divisors)
+// [-> ADD bias per matrix, in order] or MUL_MAT -> ADD(residual), starting at node i0,
+// optionally after RMS_NORM -> MUL(norm_w) at node i: one quantization of the activation
+// rows (norm folded in) and one launch over the stacked matrices.
+int fuse_q8_batch_at(BackendCtx *ctx, ggml_cgraph *g, int i, int i0, const Consumers &C, const BatchNorm &norm) {
+    const int nn = ggml_graph_n_nodes(g);
+    ggml_tensor *mm0 = ggml_graph_node(g, i0);
+    if (!q8_batch_node(mm0)) return 0;
+    const ggml_tensor *mm[4] = {mm0};
+    int cnt = 1, last = i0;
+    while (cnt < 4) {
+        const int j = next_real(g, last + 1);
+        if (j >= nn) break;
+        const ggml_tensor *nx = ggml_graph_node(g, j);
+        if (!q8_batch_node(nx) || nx->src[1] != mm0->src[1] || nx->src[0]->ne[0] != mm0->src[0]->ne[0] ||
+            inv_s_of(nx->src[0]) != inv_s_of(mm0->src[0]))
+            break;
+        mm[cnt++] = nx;
+        last = j;
+    }
+    const ggml_tensor *ad[4] = {}, *other[4] = {};
+    bool bias[4] = {};
+    int tail = last;
+    bool all_add = true;
+    for (int t = 0; t < cnt && all_add; t++) {
+        const ggml_tensor *a = batch_add_tail(g, tail, mm[t], C, other[t], bias[t]);
+        if (!a || (cnt > 1 && !bias[t])) all_add = false;
+        ad[t] = a;
+        if (a) tail = next_real(g, tail + 1);
+    }
+    if (!all_add) tail = last;
+    if (norm.w) {
+        std::vector<const ggml_tensor *> cs;
+        real_consumers(C, mm0->src[1], cs);
+        if (cs.size() != (size_t)cnt) return 0;  // the normed activation is read only by the group
+        for (const ggml_tensor *c : cs)
+            if (std::find(mm, mm + cnt, c) == mm + cnt) return 0;
+    }
+    const int64_t k = mm0->src[0]->ne[0], m = ggml_nrows(mm0->src[1]);
+    if (norm.w && k > 4096) return 0;
+    if (ctx->scratch_size < mi_xq_size(m, k)) return 0;
+    const void *w[4];
+    int64_t n[4];
+    float *y[4];
+    const float *bv[4], *av[4];
+    for (int t = 0; t < cnt; t++) {
+        w[t] = ((const TensorExtra *)mm[t]->src[0]->extra)->packed;
+        n[t] = mm[t]->src[0]->ne[1];
+        y[t] = (float *)(all_add ? ad[t]->data : mm[t]->data);
+        bv[t] = all_add && bias[t] ? (const float *)other[t]->data : nullptr;
+        av[t] = all_add && !bias[t] ? (const float *)other[t]->data : nullptr;
+    }
+    const float *x = (const float *)(norm.w ? norm.x->data : mm0->src[1]->data);
+    MI_K_CHECK(mi_mul_mat_q8_0_f32_batch(ctx->stream, cnt, w, n, y, bv, av, k, m, x, nullptr,
+                                         norm.w ? (const float *)norm.w->data : nullptr, norm.eps,
+                                         inv_s_of(mm0->src[0]), q8_rounding(), ctx->scratch, ctx->scratch_size));
+    return tail + 1 - i;
+}
+
+int try_fuse_q8_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    return fuse_q8_batch_at(ctx, g, i, i, C, BatchNorm{});
+}
+
 // FLASH_ATTN_EXT (several sequences, one token each) whose output only feeds a Q4_0
 // projection of those rows [-> ADD bias or residual]: the attention's combine writes the
 // projection's permuted fp16 activation straight into the scratch (no attention-output
@@ -1614,7 +1687,7 @@ int try_fuse_norm_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consume
     const ggml_tensor *rms = ggml_graph_node(g, i);
     const ggml_tensor *x = rms->src[0];
     const int64_t m = ggml_nrows(x);
-    if (!is_f32_contig(x) || m < 2 || m > 16 || x->ne[1] != m || x->ne[0] > 4096 || x->ne[0] % 128 ||
+    if (!is_f32_contig(x) || m < 2 || m > 16 || x->ne[1] != m || x->ne[0] > 4096 || x->ne[0] % 32 ||
         !aligned16(x->data))
         return 0;
     const int j = next_real(g, i + 1);
@@ -1629,6 +1702,9 @@ int try_fuse_norm_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consume
     norm.x = x;
     norm.w = mul->src[1];
     memcpy(&norm.eps, rms->op_params, sizeof(float));
+    if (!aligned16(norm.w->data)) return 0;
+    if (q8_batch_node(ggml_graph_node(g, i0))) return fuse_q8_batch_at(ctx, g, i, i0, C, norm);
+    if (x->ne[0] % 128) return 0;
     return fuse_q4_batch_at(ctx, g, i, i0, C, norm);
 }
 
@@ -1642,7 +1718,8 @@ int try_fuse_glu_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumer
     const int j = next_real(g, i + 1);
     if (j >= ggml_graph_n_nodes(g)) return 0;
     const ggml_tensor *mm = ggml_graph_node(g, j);
-    if (!q4_batch_node(mm) || mm->src[1] != glu || !only_consumed_by(C, glu, {mm})) return 0;
+    const bool q8 = q8_batch_node(mm);
+    if ((!q8 && !q4_batch_node(mm)) || mm->src[1] != glu || !only_consumed_by(C, glu, {mm})) return 0;
     const ggml_tensor *other = nullptr;
     bool is_bias = false;
     const ggml_tensor *ad = batch_add_tail(g, j, mm, C, other, is_bias);
@@ -1651,6 +1728,15 @@ int try_fuse_glu_q4_batch(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumer
     float *y = (float *)(ad ? ad->data : mm->data);
     const float *bv = ad && is_bias ? (const float *)other->data : nullptr;
     const float *av = ad && !is_bias ? (const float *)other->data : nullptr;
+    if (q8) {  // the swiglu formed while the down projection's activation rows are quantized
+        if (!aligned16(glu->src[0]->data) || !aligned16(glu->src[1]->data) || ctx->scratch_size < mi_xq_size(m, k))
+            return 0;
+        MI_K_CHECK(mi_mul_mat_q8_0_f32_batch(ctx->stream, 1, &w, &n, &y, &bv, &av, k, m,
+                                             (const float *)glu->src[0]->data, (const float *)glu->src[1]->data,
+                                             nullptr, 0.0f, inv_s_of(mm->src[0]), q8_rounding(), ctx->scratch,
+                                             ctx->scratch_size));
+        return (ad ? next_real(g, j + 1) : j) + 1 - i;
+    }
     MI_K_CHECK(mi_mul_mat_q4_0_f32_batch(ctx->stream, 1, &w, &n, &y, &bv, &av, k, m, (const float *)glu->src[0]->data,
                                          (const float *)glu->src[1]->data, nullptr, 0.0f, ctx->scratch,
                                          ctx->scratch_size));
@@ -1766,6 +1852,7 @@ int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
             if (fuse) {
                 if (int used = try_fuse_matmul_add(ctx, g, i, C)) return used;
                 if (int used = try_fuse_q4_batch(ctx, g, i, C)) return used;
+                if (int used = try_fuse_q8_batch(ctx, g, i, C)) return used;
             }
             // consecutive Q8_0 GEMVs reading the same activation (q/k/v, gate/up): one grouped launch
             if (fuse && packed_fmt(node->src[0]) == GGML_TYPE_Q8_0 && node->src[1]->ne[1] == 1 &&

@@ -598,6 +598,186 @@ int launch_xq(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t
     return MI_ERR_ARG;
 }
 
+// ---- several activation rows (2..8: a ubatch) through up to four matrices
+
+// The Q8_0 blocks of m activation rows with the activation's producer folded in, one
+// workgroup per row: RMSNorm(x) * norm_w when norm_w is set (k <= 1024*XN), else
+// silu(x) * up when up is set, else x; then * inv_s and the quantization.  The float
+// operations are those of k_rms_norm + MUL (XStage), or k_swiglu, then
+// k_act_quant_q8_0, so the bytes equal what those launches write in sequence.
+template <int XN>
+__global__ __launch_bounds__(256) void k_act_quant_rows_q8_0(const float *__restrict__ x, const float *__restrict__ up,
+                                                             const float *__restrict__ norm_w, float eps,
+                                                             const float *__restrict__ inv_s, int8_t *__restrict__ qs,
+                                                             uint16_t *__restrict__ dout, int k, int rounding) {
+    __shared__ double s_red[4];
+    const int row = blockIdx.x, tid = threadIdx.x, k4 = k / 4, nb = k / QK;
+    const float *xr = x + (size_t)row * k;
+    int8_t *qr = qs + (size_t)row * k;
+    uint16_t *dr = dout + (size_t)row * nb;
+    auto put = [&](int f, float4 v) {  // whole 8-lane groups (k4 % 8 == 0): all lanes call it
+        if (inv_s) {
+            const float4 sv = ((const float4 *)inv_s)[min(f, k4 - 1)];
+            v.x *= sv.x; v.y *= sv.y; v.z *= sv.z; v.w *= sv.w;
+        }
+        float d;
+        const uint32_t q = quant4(v.x, v.y, v.z, v.w, rounding, d);
+        if (f < k4) {
+            *(uint32_t *)(qr + (size_t)f * 4) = q;
+            if ((f & 7) == 0) dr[f >> 3] = f2h(d);
+        }
+    };
+    if (norm_w) {
+        XStage<XN, true> st;
+        xstage_load(st, xr, norm_w, nullptr, k4, tid);
+        const float scale = xstage_scale(st, k4, eps, s_red, tid);
+#pragma unroll
+        for (int t = 0; t < XN; t++) put(tid + t * 256, xstage_value(st, scale, t));
+        return;
+    }
+    const float *ur = up ? up + (size_t)row * k : nullptr;
+    for (int f0 = 0; f0 < k4; f0 += 256) {
+        const int f = f0 + tid, fc = min(f, k4 - 1);
+        float4 v = ((const float4 *)xr)[fc];
+        if (ur) {  // ggml's silu(g) * u
+            const float4 u = ((const float4 *)ur)[fc];
+            v.x = (v.x / (1.0f + expf(-v.x))) * u.x;
+            v.y = (v.y / (1.0f + expf(-v.y))) * u.y;
+            v.z = (v.z / (1.0f + expf(-v.z))) * u.z;
+            v.w = (v.w / (1.0f + expf(-v.w))) * u.w;
+        }
+        put(f, v);
+    }
+}
+
+// The several-row GEMV over a stacked set of up to four matrices (Q8Set).  The m rows'
+// activation blocks are staged in LDS once per workgroup, so only the weights sit in
+// registers; each row's lanes walk their blocks in k_gemv_q8_0_xq's order with the same
+// products, so the results are bit-identical to it (and to the one-row kernels).
+// Epilogue per matrix: + add[row] (a bias row) or, with bit t of add_rows set,
+// + add[i*n + row] (a residual of the output's shape).
+template <int G, int U, int M>
+__global__ __launch_bounds__(256) void k_gemv_q8_0_xs(const Q8Set S, unsigned add_rows, const int8_t *__restrict__ xq_qs,
+                                                      const uint16_t *__restrict__ xq_d, int n_total, int nb, int m) {
+    constexpr int RPB = 256 / G;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int k = nb * QK;
+    int8_t *s_qs = (int8_t *)smem;
+    uint16_t *s_d = (uint16_t *)(smem + (size_t)m * k);
+    const int tid = threadIdx.x;
+    const int j = tid % G;
+    const int grow = blockIdx.x * RPB + tid / G;
+    const bool row_ok = grow < n_total;
+    const int rc = min(grow, n_total - 1);
+    const int mi = q8set_index(S, rc);
+    const int r = rc - q8set_row_start(S, mi);
+    const uint8_t *qlo = S.qlo[mi], *qhi = S.qhi[mi];
+    const uint16_t *wd = S.d[mi];
+    const size_t rbase = (size_t)r * nb;
+    int4 lo[U], hi[U];
+    uint32_t dw[U];
+    q8_first_pass<G, U>(qlo, qhi, wd, rbase, nb, j, lo, hi, dw);  // in flight during the staging
+    {
+        const int qn = m * k / 16, dn = (m * nb + 1) / 2;  // int4 / uint32 words (xs_lds_bytes rounds up)
+        for (int o = tid; o < qn; o += 256) ((int4 *)s_qs)[o] = ((const int4 *)xq_qs)[o];
+        for (int o = tid; o < dn; o += 256) ((uint32_t *)s_d)[o] = ((const uint32_t *)xq_d)[o];
+    }
+    __syncthreads();
+    float acc[M];
+#pragma unroll
+    for (int i = 0; i < M; i++) acc[i] = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += U * G) {
+        if (b0) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int b = min(b0 + j + u * G, nb - 1);
+                lo[u] = ld_stream16(qlo + (rbase + b) * 16);
+                hi[u] = ld_stream16(qhi + (rbase + b) * 16);
+                dw[u] = wd[rbase + b];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int b = b0 + j + u * G;
+            if (b < nb) {
+                const float dwf = h2f((uint16_t)dw[u]);
+#pragma unroll
+                for (int i = 0; i < M; i++) {
+                    const int ii = min(i, m - 1);
+                    const int4 *xs = (const int4 *)(s_qs + (size_t)ii * k + (size_t)b * QK);
+                    const int s = dot_block(lo[u], hi[u], xs[0], xs[1]);
+                    acc[i] = fmaf((float)s, dwf * h2f(s_d[ii * nb + b]), acc[i]);
+                }
+            }
+        }
+    }
+    const int n_mi = S.row_end[mi] - q8set_row_start(S, mi);
+    const float *add = S.add[mi];
+    const bool full = (add_rows >> mi) & 1u;
+#pragma unroll
+    for (int i = 0; i < M; i++) {
+        const float v = group_sum<G>(acc[i]);
+        if (row_ok && j == 0 && i < m) {
+            const size_t o = (size_t)i * n_mi + r;
+            S.y[mi][o] = add ? v + add[full ? o : (size_t)r] : v;
+        }
+    }
+}
+
+size_t xs_lds_bytes(int64_t m, int64_t k) { return (size_t)(m * k + (m * (k / QK) + 1) / 2 * 4); }
+
+template <int G, int U, int M>
+int launch_xs_gum(hipStream_t st, const Q8Set &S, unsigned add_rows, int n_total, int64_t k, int64_t m,
+                  const int8_t *xq_qs, const uint16_t *xq_d) {
+    constexpr int RPB = 256 / G;
+    const size_t lds = xs_lds_bytes(m, k);
+    auto kern = k_gemv_q8_0_xs<G, U, M>;
+    static size_t raised = 65536;  // per instantiation: dynamic LDS allowed so far (64 KB by default)
+    if (lds > raised) {
+        if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+            hipSuccess) {
+            (void)hipGetLastError();
+            set_error("gemv_q8_0_xs: %zu bytes of LDS per workgroup not available", lds);
+            return MI_ERR_UNSUPPORTED;
+        }
+        raised = lds;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)((n_total + RPB - 1) / RPB)), dim3(256), lds, st, S, add_rows, xq_qs, xq_d,
+                       n_total, (int)(k / QK), (int)m);
+    MI_CHECK_LAUNCH("k_gemv_q8_0_xs");
+    return MI_OK;
+}
+
+template <int G, int M>
+int launch_xs_gm(hipStream_t st, const Q8Set &S, unsigned add_rows, int n_total, int64_t k, int64_t m,
+                 const int8_t *xq_qs, const uint16_t *xq_d) {
+#define MI_U_CASE(UU) case UU: return launch_xs_gum<G, UU, M>(st, S, add_rows, n_total, k, m, xq_qs, xq_d);
+    switch (pick_u(k / QK, G)) {
+        MI_U_CASE(1) MI_U_CASE(2) MI_U_CASE(3) MI_U_CASE(4) MI_U_CASE(5) MI_U_CASE(6) MI_U_CASE(7) MI_U_CASE(8)
+    }
+#undef MI_U_CASE
+    return MI_ERR_ARG;
+}
+
+template <int M>
+int launch_xs_m(hipStream_t st, const Q8Set &S, unsigned add_rows, int n_total, int64_t k, int64_t m,
+                const int8_t *xq_qs, const uint16_t *xq_d) {
+    switch (pick_g(k / QK)) {  // the lane layout of k_gemv_q8_0_xq at this k
+        case 16: return launch_xs_gm<16, M>(st, S, add_rows, n_total, k, m, xq_qs, xq_d);
+        case 32: return launch_xs_gm<32, M>(st, S, add_rows, n_total, k, m, xq_qs, xq_d);
+        default: return launch_xs_gm<64, M>(st, S, add_rows, n_total, k, m, xq_qs, xq_d);
+    }
+}
+
+int launch_xs(hipStream_t st, const Q8Set &S, unsigned add_rows, int n_total, int64_t k, int64_t m,
+              const int8_t *xq_qs, const uint16_t *xq_d) {
+    if (m == 2) return launch_xs_m<2>(st, S, add_rows, n_total, k, m, xq_qs, xq_d);
+    if (m >= 3 && m <= 4) return launch_xs_m<4>(st, S, add_rows, n_total, k, m, xq_qs, xq_d);
+    if (m >= 5 && m <= 8) return launch_xs_m<8>(st, S, add_rows, n_total, k, m, xq_qs, xq_d);
+    set_error("gemv_q8_0_xs: m=%lld not in 2..8", (long long)m);
+    return MI_ERR_ARG;
+}
+
 template <int G, int U, int XN, bool NORM>
 int launch_fused_gux(hipStream_t st, const Q8Set &S, int n_total, int64_t k, const float *x, const float *norm_w,
                      float eps, const float *inv_s, int rounding) {
@@ -903,6 +1083,43 @@ int mi_mul_mat_q8_0_f32(void *stream, const void *w_packed, const float *x, cons
     }
     if (int r = mi_act_quant_q8_0(stream, x, inv_s, m, k, ws, rounding)) return r;
     return mi_gemv_q8_0(stream, w_packed, ws, y, n, k, m);
+}
+
+int mi_mul_mat_q8_0_f32_batch(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,
+                              float *const *y, const float *const *bias, const float *const *add, int64_t k, int64_t m,
+                              const float *x, const float *x_up, const float *norm_w, float eps, const float *inv_s,
+                              int rounding, void *ws, size_t ws_bytes) {
+    if (int r = check_shape("mul_mat_q8_0_f32_batch", m, k)) return r;
+    MI_CHECK_ARG(w_packed && n && y && x, "mul_mat_q8_0_f32_batch: null pointer");
+    MI_CHECK_ARG(m >= 2 && m <= 8, "mul_mat_q8_0_f32_batch: m=%lld not in 2..8", (long long)m);
+    MI_CHECK_ARG(!(norm_w && x_up), "mul_mat_q8_0_f32_batch: a norm and a swiglu partner together");
+    MI_CHECK_ARG(!norm_w || k <= 4096, "mul_mat_q8_0_f32_batch: k=%lld > 4096 with a norm", (long long)k);
+    MI_CHECK_ARG(mi::aligned(x, 16) && (!x_up || mi::aligned(x_up, 16)) && (!norm_w || mi::aligned(norm_w, 16)) &&
+                     (!inv_s || mi::aligned(inv_s, 16)),
+                 "mul_mat_q8_0_f32_batch: x/x_up/norm_w/inv_s must be 16-byte aligned");
+    const size_t need = mi_xq_size(m, k);
+    if (!ws || ws_bytes < need || !mi::aligned(ws, 16)) {
+        mi::set_error("mul_mat_q8_0_f32_batch: workspace %zu < %zu bytes (or misaligned)", ws_bytes, need);
+        return MI_ERR_WORKSPACE;
+    }
+    Q8Set S;
+    int n_total = 0;
+    const float *adds[4] = {};
+    unsigned add_rows = 0;
+    for (int i = 0; i < n_mats && i < 4; i++) {
+        MI_CHECK_ARG(!(bias && bias[i] && add && add[i]), "mul_mat_q8_0_f32_batch: matrix %d has a bias and a residual", i);
+        adds[i] = bias && bias[i] ? bias[i] : add ? add[i] : nullptr;
+        if (add && add[i]) add_rows |= 1u << i;
+    }
+    if (int r = make_set(S, n_mats, w_packed, n, y, k, n_total, adds)) return r;
+    hipStream_t st = (hipStream_t)stream;
+    uint8_t *xb = (uint8_t *)ws;
+    int8_t *qs = (int8_t *)xb;
+    uint16_t *qd = (uint16_t *)(xb + mi_xq_d_offset(m, k));
+    hipLaunchKernelGGL(k_act_quant_rows_q8_0<4>, dim3((unsigned)m), dim3(256), 0, st, x, x_up, norm_w, eps, inv_s, qs,
+                       qd, (int)k, rounding);
+    MI_CHECK_LAUNCH("k_act_quant_rows_q8_0");
+    return launch_xs(st, S, add_rows, n_total, k, m, qs, qd);
 }
 
 int mi_mul_mat_q8_0_f32_fused(void *stream, int n_mats, const void *const *w_packed, const int64_t *n,

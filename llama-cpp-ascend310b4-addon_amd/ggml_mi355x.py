@@ -107,6 +107,7 @@ _SIGS = {
     "mi_argmax_workspace_size": (_SZ, [_I64, _I64]),
     "mi_argmax": (_I, [_P, _P, _P, _I64, _I64, _P, _SZ]),
     "mi_mul_mat_q8_0_f32_fused": (_I, [_P, _I, _P, _P, _P, _P, _I64, _P, _P, _F, _P, _I]),
+    "mi_mul_mat_q8_0_f32_batch": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _F, _P, _I, _P, _SZ]),
     "mi_mul_mat_q8_0_f32_lse": (_I, [_P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _I]),
     "mi_gate_up_swiglu_q8_0": (_I, [_P, _P, _P, _I64, _I64, _P, _P, _F, _P, _P, _I, _P]),
     "mi_gate_up_swiglu_f32_q8_0": (_I, [_P, _P, _P, _I64, _I64, _P, _P, _F, _P, _P, _I, _P]),

@@ -628,6 +628,69 @@ def test_q4_batch_set(gpu, orc, ns, k, m, mode):
             assert rel_err(got[r], ref) < GEMV_TOL, f"matrix {t} row {r}"
 
 
+@pytest.mark.parametrize("ns,k,m,mode", [((1536, 256, 256), 1536, 8, "norm_bias"), ((8960, 8960), 1536, 8, "norm"),
+                                         ((1536,), 8960, 8, "glu_add"), ((1536,), 1536, 3, "add"),
+                                         ((96, 40), 256, 2, "bias"), ((256,), 4096, 5, "norm"),
+                                         ((512,), 8960, 5, "glu"), ((300, 33, 64, 7), 96, 4, "plain")])
+def test_q8_batch_set(gpu, orc, ns, k, m, mode):
+    """Several activation rows through up to four Q8_0 matrices (mi_mul_mat_q8_0_f32_batch:
+    the activation's quantization with RMSNorm or swiglu folded in, then one launch over the
+    stacked matrices with the blocks in LDS): bit-identical to the node-by-node path
+    (RMS_NORM+MUL or GLU, one mi_mul_mat_q8_0_f32 per matrix, then the ADD), and within the
+    GEMV bar of the oracle's Q8_0 MUL_MAT.  k = 8960 at 8 rows stages 76 KB of LDS."""
+    mi = gpu
+    P = mi._P
+    rng = np.random.default_rng(sum(ns) + k + m + len(mode))
+    ws = [q8_0_weights(rng, n, k) for n in ns]
+    pw = [_packed_q8(mi, w, n, k) for w, n in zip(ws, ns)]
+    x = rng.standard_normal((m, k)).astype(F32)
+    up = rng.standard_normal((m, k)).astype(F32) if mode.startswith("glu") else None
+    bias = [rng.standard_normal(n).astype(F32) for n in ns] if mode.endswith("bias") else None
+    add = [rng.standard_normal((m, n)).astype(F32) for n in ns] if mode.endswith("add") else None
+    nw = rng.uniform(0.8, 1.2, k).astype(F32) if mode.startswith("norm") else None
+    inv = (1.0 / rng.uniform(0.5, 2.0, k)).astype(F32)
+    dx, dinv = mi.to_device(x), mi.to_device(inv)
+    dup = mi.to_device(up) if up is not None else None
+    dnw = mi.to_device(nw) if nw is not None else None
+    db = [mi.to_device(b) for b in bias] if bias else None
+    da = [mi.to_device(a) for a in add] if add else None
+    ys = [mi.DeviceBuffer(4 * m * n) for n in ns]
+    wsb = mi.mul_mat_q8_0_workspace_size(m, k)
+    wbuf = mi.DeviceBuffer(wsb)
+    mi._call("mi_mul_mat_q8_0_f32_batch", None, len(ns), _ptrs(*pw), _i64s(*ns), _ptrs(*ys),
+             _ptrs(*db) if db else None, _ptrs(*da) if da else None, k, m, P(dx.ptr), P(dup.ptr if dup else None),
+             P(dnw.ptr if dnw else None), F32(1e-6), P(dinv.ptr), mi.Q8_ROUND_X86, P(wbuf.ptr), wsb)
+    mi.device_sync()
+    # node-by-node: the GLU or the norm, then one launch per matrix, then the ADD
+    act_dev = dx
+    if up is not None or nw is not None:
+        act_dev = mi.DeviceBuffer(4 * m * k)
+        if up is not None:
+            mi._call("mi_swiglu", None, P(dx.ptr), P(dup.ptr), P(act_dev.ptr), m * k)
+        else:
+            mi._call("mi_rms_norm", None, P(dx.ptr), P(dnw.ptr), P(act_dev.ptr), k, m, F32(1e-6))
+        mi.device_sync()
+    act = act_dev.download(F32).reshape(m, k)
+    for t, n in enumerate(ns):
+        yb = mi.DeviceBuffer(4 * m * n)
+        mi.mul_mat_q8_0_f32(pw[t].ptr, act_dev.ptr, dinv.ptr, yb.ptr, n, k, m, ws=wbuf.ptr, ws_bytes=wsb)
+        mi.device_sync()
+        plain = yb.download(F32).reshape(m, n)
+        if bias:
+            plain = (plain + bias[t]).astype(F32)
+        if add:
+            plain = (plain + add[t]).astype(F32)
+        got = ys[t].download(F32).reshape(m, n)
+        assert np.array_equal(got, plain), f"matrix {t}: batch launch differs from node-by-node"
+        for r in range(m):
+            ref = _q8_ref(orc, ws[t], act[r], n, k, inv)
+            if bias:
+                ref = (ref + bias[t]).astype(F32)
+            if add:
+                ref = (ref + add[t][r]).astype(F32)
+            assert rel_err(got[r], ref) < GEMV_TOL, f"matrix {t} row {r}"
+
+
 def test_q4_batch_set_rejects_bad_shapes(gpu):
     mi = gpu
     P = mi._P
