@@ -81,7 +81,8 @@ __global__ __launch_bounds__(256) void k_quantize_f16_q8_0(const uint16_t *__res
 // grid: ceil(m*nb / 32) x 256 threads
 __global__ __launch_bounds__(256) void k_act_quant_q8_0(const float *__restrict__ x, const float *__restrict__ inv_s,
                                                         int8_t *__restrict__ qs, uint16_t *__restrict__ dout,
-                                                        int64_t k, int64_t total_blocks, int rounding) {
+                                                        int64_t k, int64_t total_blocks, int rounding,
+                                                        const float *__restrict__ up = nullptr) {
     const int64_t blk = (int64_t)blockIdx.x * 32 + threadIdx.x / 8;
     const int sub = threadIdx.x % 8;
     const bool valid = blk < total_blocks;
@@ -91,6 +92,13 @@ __global__ __launch_bounds__(256) void k_act_quant_q8_0(const float *__restrict_
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (valid) {
         v = *(const float4 *)(x + row * k + b * QK + sub * 4);
+        if (up) {  // ggml's silu(g) * u (k_swiglu)
+            const float4 u = *(const float4 *)(up + row * k + b * QK + sub * 4);
+            v.x = (v.x / (1.0f + expf(-v.x))) * u.x;
+            v.y = (v.y / (1.0f + expf(-v.y))) * u.y;
+            v.z = (v.z / (1.0f + expf(-v.z))) * u.z;
+            v.w = (v.w / (1.0f + expf(-v.w))) * u.w;
+        }
         if (inv_s) {
             const float4 s = *(const float4 *)(inv_s + b * QK + sub * 4);
             v.x *= s.x; v.y *= s.y; v.z *= s.z; v.w *= s.w;
@@ -600,53 +608,37 @@ int launch_xq(hipStream_t st, const uint8_t *base, int64_t n, int64_t k, int64_t
 
 // ---- several activation rows (2..8: a ubatch) through up to four matrices
 
-// The Q8_0 blocks of m activation rows with the activation's producer folded in, one
-// workgroup per row: RMSNorm(x) * norm_w when norm_w is set (k <= 1024*XN), else
-// silu(x) * up when up is set, else x; then * inv_s and the quantization.  The float
-// operations are those of k_rms_norm + MUL (XStage), or k_swiglu, then
-// k_act_quant_q8_0, so the bytes equal what those launches write in sequence.
+// The Q8_0 blocks of m activation rows with their RMSNorm folded in, one workgroup per
+// row (k <= 1024*XN): RMSNorm(x) * norm_w, then * inv_s and the quantization.  The float
+// operations are those of k_rms_norm + MUL (XStage) then k_act_quant_q8_0, so the bytes
+// equal what those launches write in sequence.  (Without a norm, k_act_quant_q8_0 takes
+// the rows 32 blocks per workgroup, the swiglu folded in when given.)
 template <int XN>
-__global__ __launch_bounds__(256) void k_act_quant_rows_q8_0(const float *__restrict__ x, const float *__restrict__ up,
+__global__ __launch_bounds__(256) void k_act_quant_rows_q8_0(const float *__restrict__ x,
                                                              const float *__restrict__ norm_w, float eps,
                                                              const float *__restrict__ inv_s, int8_t *__restrict__ qs,
                                                              uint16_t *__restrict__ dout, int k, int rounding) {
     __shared__ double s_red[4];
     const int row = blockIdx.x, tid = threadIdx.x, k4 = k / 4, nb = k / QK;
-    const float *xr = x + (size_t)row * k;
     int8_t *qr = qs + (size_t)row * k;
     uint16_t *dr = dout + (size_t)row * nb;
-    auto put = [&](int f, float4 v) {  // whole 8-lane groups (k4 % 8 == 0): all lanes call it
+    XStage<XN, true> st;
+    xstage_load(st, x + (size_t)row * k, norm_w, nullptr, k4, tid);
+    const float scale = xstage_scale(st, k4, eps, s_red, tid);
+#pragma unroll
+    for (int t = 0; t < XN; t++) {
+        const int f = tid + t * 256;  // float4 index; 8 consecutive threads form one 32-block
+        float4 v = xstage_value(st, scale, t);
         if (inv_s) {
             const float4 sv = ((const float4 *)inv_s)[min(f, k4 - 1)];
             v.x *= sv.x; v.y *= sv.y; v.z *= sv.z; v.w *= sv.w;
         }
         float d;
-        const uint32_t q = quant4(v.x, v.y, v.z, v.w, rounding, d);
+        const uint32_t q = quant4(v.x, v.y, v.z, v.w, rounding, d);  // whole 8-lane groups (k4 % 8 == 0)
         if (f < k4) {
             *(uint32_t *)(qr + (size_t)f * 4) = q;
             if ((f & 7) == 0) dr[f >> 3] = f2h(d);
         }
-    };
-    if (norm_w) {
-        XStage<XN, true> st;
-        xstage_load(st, xr, norm_w, nullptr, k4, tid);
-        const float scale = xstage_scale(st, k4, eps, s_red, tid);
-#pragma unroll
-        for (int t = 0; t < XN; t++) put(tid + t * 256, xstage_value(st, scale, t));
-        return;
-    }
-    const float *ur = up ? up + (size_t)row * k : nullptr;
-    for (int f0 = 0; f0 < k4; f0 += 256) {
-        const int f = f0 + tid, fc = min(f, k4 - 1);
-        float4 v = ((const float4 *)xr)[fc];
-        if (ur) {  // ggml's silu(g) * u
-            const float4 u = ((const float4 *)ur)[fc];
-            v.x = (v.x / (1.0f + expf(-v.x))) * u.x;
-            v.y = (v.y / (1.0f + expf(-v.y))) * u.y;
-            v.z = (v.z / (1.0f + expf(-v.z))) * u.z;
-            v.w = (v.w / (1.0f + expf(-v.w))) * u.w;
-        }
-        put(f, v);
     }
 }
 
@@ -1026,7 +1018,8 @@ int mi_act_quant_q8_0(void *stream, const float *x, const float *inv_s, int64_t 
     const int64_t total = m * (k / QK);
     uint8_t *base = (uint8_t *)xq;
     hipLaunchKernelGGL(k_act_quant_q8_0, dim3((unsigned)((total + 31) / 32)), dim3(256), 0, (hipStream_t)stream, x,
-                       inv_s, (int8_t *)base, (uint16_t *)(base + mi_xq_d_offset(m, k)), k, total, rounding);
+                       inv_s, (int8_t *)base, (uint16_t *)(base + mi_xq_d_offset(m, k)), k, total, rounding,
+                       (const float *)nullptr);
     MI_CHECK_LAUNCH("k_act_quant_q8_0");
     return MI_OK;
 }
@@ -1116,9 +1109,16 @@ int mi_mul_mat_q8_0_f32_batch(void *stream, int n_mats, const void *const *w_pac
     uint8_t *xb = (uint8_t *)ws;
     int8_t *qs = (int8_t *)xb;
     uint16_t *qd = (uint16_t *)(xb + mi_xq_d_offset(m, k));
-    hipLaunchKernelGGL(k_act_quant_rows_q8_0<4>, dim3((unsigned)m), dim3(256), 0, st, x, x_up, norm_w, eps, inv_s, qs,
-                       qd, (int)k, rounding);
-    MI_CHECK_LAUNCH("k_act_quant_rows_q8_0");
+    if (norm_w) {
+        hipLaunchKernelGGL(k_act_quant_rows_q8_0<4>, dim3((unsigned)m), dim3(256), 0, st, x, norm_w, eps, inv_s, qs, qd,
+                           (int)k, rounding);
+        MI_CHECK_LAUNCH("k_act_quant_rows_q8_0");
+    } else {
+        const int64_t total = m * (k / QK);
+        hipLaunchKernelGGL(k_act_quant_q8_0, dim3((unsigned)((total + 31) / 32)), dim3(256), 0, st, x, inv_s, qs, qd, k,
+                           total, rounding, x_up);
+        MI_CHECK_LAUNCH("k_act_quant_q8_0");
+    }
     return launch_xs(st, S, add_rows, n_total, k, m, qs, qd);
 }
 
