@@ -30,8 +30,11 @@
 // so a consumer's plain loads after the hop can only miss to memory or hit lines filled
 // after the producers finished.  Every wait is bounded (spin_limit polls): on a timeout
 // the workgroup raises the error word, every later wait returns at once, and all
-// workgroups still reach the exit, where the last one to arrive puts the counters back
-// to zero for the next launch.  The host reads the error from pinned memory.
+// workgroups still reach the exit.  Launches alternate between two counter sets: each
+// workgroup clears its share of the previous launch's set when it starts, and the last
+// one to exit flips the parity word that names the next launch's set (one workgroup
+// zeroing 17,920 counter lines at the exit held the launch 23 us).  The host reads the
+// error from pinned memory.
 #include "q8_0_dev.h"
 #include "fattn_dev.h"
 #include "persist_plan.h"
@@ -90,22 +93,22 @@ __device__ __forceinline__ void st_h(uint16_t *p, uint16_t v) {
 
 // All of this workgroup's writes done, then one arrival in each counter replica (threads
 // 0 .. kReps-1 of wave 0).
-__device__ __forceinline__ void hop_arrive(const PArgs &a, int layer, int hop) {
+__device__ __forceinline__ void hop_arrive(const PArgs &a, unsigned *ctrs, int layer, int hop) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x < persist_plan::kReps)  // one arrival in every replica of the counter set
-        __hip_atomic_fetch_add(a.sync + persist_plan::hop_ctr_word(layer, hop, blockIdx.x & 7, threadIdx.x), 1u,
+        __hip_atomic_fetch_add(ctrs + persist_plan::hop_ctr_word(layer, hop, blockIdx.x & 7, threadIdx.x), 1u,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Wait until every producer of the hop arrived, polling the 8 counters of this
 // workgroup's replica (bounded; see the file comment).
-__device__ __forceinline__ void hop_wait(const PArgs &a, int layer, int hop) {
+__device__ __forceinline__ void hop_wait(const PArgs &a, const unsigned *ctrs, int layer, int hop) {
     if (threadIdx.x < 64) {
         const int j = threadIdx.x & 7;
         const unsigned want = persist_plan::hop_want(a.lo, hop, j) + (layer == 0 && hop == a.stall_hop && j == 0);
-        const unsigned *ctr = a.sync + persist_plan::hop_ctr_word(layer, hop, j, blockIdx.x % persist_plan::kReps);
+        const unsigned *ctr = ctrs + persist_plan::hop_ctr_word(layer, hop, j, blockIdx.x % persist_plan::kReps);
         unsigned *err = a.sync + persist_plan::err_word(a.n_layer);
         long spins = 0;
         for (;;) {
@@ -128,9 +131,9 @@ __device__ __forceinline__ void hop_wait(const PArgs &a, int layer, int hop) {
     __syncthreads();
 }
 
-// Exit: the last workgroup to arrive zeroes every hop counter, the exit counter and the
-// device error word (nobody reads them again in this launch).
-__device__ __forceinline__ void persist_exit(const PArgs &a) {
+// Exit: the last workgroup to arrive flips the parity word (the next launch counts on the
+// set this launch cleared) and zeroes the exit counter and the device error word.
+__device__ __forceinline__ void persist_exit(const PArgs &a, unsigned par) {
     __shared__ int s_last;
     unsigned *exit_ctr = a.sync + persist_plan::exit_word(a.n_layer);
     __syncthreads();
@@ -139,16 +142,10 @@ __device__ __forceinline__ void persist_exit(const PArgs &a) {
         s_last = prev == gridDim.x - 1;
     }
     __syncthreads();
-    if (!s_last) return;
-    const int n = (int)persist_plan::hop_counters(a.n_layer);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) st_u(a.sync + (size_t)i * kCtrStride, 0u);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        st_u(a.sync + persist_plan::err_word(a.n_layer), 0u);
-        st_u(exit_ctr, 0u);
-    }
+    if (!s_last || threadIdx.x != 0) return;
+    st_u(a.sync + persist_plan::err_word(a.n_layer), 0u);
+    st_u(a.sync + persist_plan::parity_word(a.n_layer), par ^ 1u);
+    st_u(exit_ctr, 0u);
 }
 
 // the attention tile's wait on hop 0 (q and the new cache row written), and its stage
@@ -156,10 +153,11 @@ __device__ __forceinline__ void persist_exit(const PArgs &a) {
 template <class Mark>
 struct FaHop {
     const PArgs &a;
+    const unsigned *ctrs;
     int layer;
     Mark &mark_fn;
     __device__ void operator()() const {
-        hop_wait(a, layer, 0);
+        hop_wait(a, ctrs, layer, 0);
         mark_fn(layer, 3);
     }
     __device__ void mark(int k) const { mark_fn(layer, 19 + k); }
@@ -255,10 +253,22 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
     // 10 down start, 11 down waited, 12 down done, 13 down activation staged,
     // 14 o input staged, 15 gate/up input staged, 16 o records requested, 17 o group
     // weights, 18 o head weights, 19 attention scores formed, 20 attention waves merged,
-    // 21 attention partials stored
+    // 21 attention partials stored; layer 0 only: 22 kernel entry, 23 exit (after the
+    // last workgroup's counter reset)
     auto trace_mark = [&](int layer, int ev) {
         if (a.trace && tid == 0) a.trace[((size_t)layer * nwg + wg) * kTraceEvents + ev] = wall_clock64();
     };
+    trace_mark(0, 22);
+    // the counter set of this launch (the parity word, flipped by the previous launch's
+    // exit); the other set, the previous launch's, is cleared here for the next launch
+    const unsigned par = ld_u(a.sync + persist_plan::parity_word(a.n_layer)) & 1u;
+    unsigned *const ctrs = a.sync + persist_plan::set_base(a.n_layer, (int)par);
+    {
+        unsigned *other = a.sync + persist_plan::set_base(a.n_layer, (int)(par ^ 1u));
+        const size_t n = persist_plan::hop_counters(a.n_layer);
+        for (size_t i = (size_t)wg * 256 + tid; i < n; i += (size_t)nwg * 256)
+            st_u(other + i * persist_plan::kCtrStride, 0u);
+    }
 
     for (int layer = 0; layer < a.n_layer; layer++) {
         // the thread index, opaque to the optimizer in every iteration: the phases' address
@@ -312,7 +322,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
             q8_first_pass<GE, UE>(m.qlo, m.qhi, m.d, rbase, nbE, j, wlo, whi, wdw);
             const float *bias = qkv_mi == 0 ? P.bq : qkv_mi == 1 ? P.bk : P.bv;
             const float bvalue = bias ? bias[qkv_row] : 0.0f;
-            if (layer > 0) hop_wait(a, layer - 1, 4);
+            if (layer > 0) hop_wait(a, ctrs, layer - 1, 4);
             trace_mark(layer, 1);
             XStage<XN, true> st;
             xstage_load(st, x, P.attn_norm, P.inv_s_attn, k4, tid);
@@ -344,7 +354,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
                 if (vr < lo.n_v && ci_ok)
                     st_h((uint16_t *)((uint8_t *)P.v_cache + (size_t)ci * a.kv_row_bytes) + vr, f2h(L.y[tid]));
             }
-            hop_arrive(a, layer, 0);
+            hop_arrive(a, ctrs, layer, 0);
             trace_mark(layer, 2);
         }
 
@@ -357,8 +367,8 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
                                                a.kv_len, a.n_kv, a.kv_row_bytes, (size_t)a.hd * 2, a.kv_row_bytes,
                                                (size_t)a.hd * 2, a.kq_scale, a.fa_chunk, a.fa_splits, part, nullptr,
                                                true, sq, fa_t % a.fa_splits, fa_t / a.fa_splits, 0, a.n_head_kv,
-                                               ci_ok ? (int)ci : -1, FaHop<decltype(trace_mark)>{a, layer, trace_mark});
-            hop_arrive(a, layer, 1);
+                                               ci_ok ? (int)ci : -1, FaHop<decltype(trace_mark)>{a, ctrs, layer, trace_mark});
+            hop_arrive(a, ctrs, layer, 1);
             trace_mark(layer, 4);
         }
 
@@ -387,7 +397,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
             for (int it = 0; it < NI; it++)
                 osv[it] = P.inv_s_o ? ((const float4 *)P.inv_s_o)[min(tid + it * 256, k4 - 1)]
                                     : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
-            hop_wait(a, layer, 1);
+            hop_wait(a, ctrs, layer, 1);
             trace_mark(layer, 5);
             const float xres = x[min(row, E - 1)];  // the residual (the layer input)
             // the records' maxima and sums first (a wave's loads return in order: the merge
@@ -494,7 +504,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
             trace_mark(layer, 14);
             const float s = q8_row_dot<GE, UE>(m.qlo, m.qhi, m.d, rbase, nbE, j, wlo, whi, wdw, L.qs, L.d);
             if (j == 0 && row < E) st_f(x1 + row, s + xres);
-            hop_arrive(a, layer, 2);
+            hop_arrive(a, ctrs, layer, 2);
             trace_mark(layer, 6);
         }
 
@@ -507,7 +517,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
             const int sw_t = wg + sw_i * nwg;
             const bool sw_row = tid < NGU * HR && sw_t < lo.n_gu_tiles;
             const float sw_s = sw_row && P.inv_s_down ? P.inv_s_down[sw_t * HR + sw_r] : 1.0f;
-            hop_wait(a, layer, 2);
+            hop_wait(a, ctrs, layer, 2);
             trace_mark(layer, 8);
             XStage<XN, true> st;
             xstage_load(st, x1, P.ffn_norm, P.inv_s_ffn, k4, tid);
@@ -532,7 +542,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
                 if (P.inv_s_down) v *= sw_s;
                 st_f(hbuf + sw_t * HR + sw_r, v);
             }
-            if (persist_plan::is_gu(lo, wg)) hop_arrive(a, layer, 3);
+            if (persist_plan::is_gu(lo, wg)) hop_arrive(a, ctrs, layer, 3);
             trace_mark(layer, 9);
         }
 
@@ -566,7 +576,7 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
 #pragma unroll
             for (int i = 0; i < NDN; i++)
                 xres[i] = x1[min(max(persist_plan::down_tile(lo, wg, i), 0) * RPBF + tid / GF, E - 1)];
-            hop_wait(a, layer, 3);
+            hop_wait(a, ctrs, layer, 3);
             trace_mark(layer, 11);
             constexpr int NSW = (NBF + 31) / 32;  // passes of 32 blocks
             const int sub = tid % 8;
@@ -607,11 +617,12 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
                     if (jf == 0 && row < E) st_f(x_out + row, s + xres[i]);
                 }
             }
-            if (persist_plan::is_down(lo, wg)) hop_arrive(a, layer, 4);
+            if (persist_plan::is_down(lo, wg)) hop_arrive(a, ctrs, layer, 4);
             trace_mark(layer, 12);
         }
     }
-    persist_exit(a);
+    persist_exit(a, par);
+    trace_mark(0, 23);
 }
 
 // ---------------------------------------------------------------- host side

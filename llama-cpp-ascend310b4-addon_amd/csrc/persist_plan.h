@@ -113,14 +113,19 @@ MI_PLAN_HD inline unsigned hop_want(const Layout &lo, int h, int j) {
     return (unsigned)(count / 8 + (((j - first) & 7) < (count & 7) ? 1 : 0));
 }
 
-// word offsets in the sync area: kReps x 8 counters per (layer, hop), then the exit
-// counter and the device error word, each on its own 256-byte line
+// word offsets in the sync area: two sets of counters, kReps x 8 per (layer, hop) each;
+// a launch counts on the set the parity word names and clears the other one (the set
+// of the previous launch, which nobody reads any more) for the next launch, whose set
+// it becomes when the last workgroup to exit flips the parity.  Then the exit counter,
+// the device error word and the parity word.  Every word on its own 256-byte line.
 MI_PLAN_HD inline size_t hop_ctr_word(int layer, int hop, int j, int rep) {
     return (((size_t)(layer * kHops + hop) * kReps + rep) * 8 + j) * kCtrStride;
 }
 MI_PLAN_HD inline size_t hop_counters(int n_layer) { return (size_t)n_layer * kHops * kReps * 8; }
-MI_PLAN_HD inline size_t exit_word(int n_layer) { return hop_counters(n_layer) * kCtrStride; }
+MI_PLAN_HD inline size_t set_base(int n_layer, int set) { return (size_t)set * hop_counters(n_layer) * kCtrStride; }
+MI_PLAN_HD inline size_t exit_word(int n_layer) { return 2 * hop_counters(n_layer) * kCtrStride; }
 MI_PLAN_HD inline size_t err_word(int n_layer) { return exit_word(n_layer) + kCtrStride; }
-MI_PLAN_HD inline size_t sync_words(int n_layer) { return exit_word(n_layer) + 2 * kCtrStride; }
+MI_PLAN_HD inline size_t parity_word(int n_layer) { return exit_word(n_layer) + 2 * kCtrStride; }
+MI_PLAN_HD inline size_t sync_words(int n_layer) { return exit_word(n_layer) + 3 * kCtrStride; }
 
 }  // namespace persist_plan

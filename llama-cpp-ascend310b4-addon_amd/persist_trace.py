@@ -11,7 +11,8 @@ Events per (layer, workgroup), as k_persist_q8_0 records them:
   10 down start, 11 down waited, 12 down done, 13 down activation staged,
   14 o input staged, 15 gate/up input staged, 16 o records requested,
   17 o group weights, 18 o head weights, 19 attention scores formed,
-  20 attention waves merged, 21 attention partials stored.
+  20 attention waves merged, 21 attention partials stored; in layer 0 also 22 kernel
+  entry and 23 exit (after the last workgroup has reset the counters).
 
 usage: python persist_trace.py DUMP [--layers FIRST LAST]
 Prints per phase the span (first workgroup past the hop -> last one done), the median
@@ -36,7 +37,8 @@ def load(path):
     nl, nw, ne = struct.unpack("iii", raw[:12])
     (tpu,) = struct.unpack("d", raw[12:20])
     t = np.frombuffer(raw[20:], np.uint64).reshape(nl, nw, ne).astype(np.int64)
-    t0 = t[0, :, 0].min()  # the launch's start: every workgroup stamps event 0 of every layer
+    first = t[0, :, [0, 22]] if ne > 22 else t[0, :, [0]]
+    t0 = first[first > 0].min()  # the launch's start: the earliest entry or layer-0 stamp
     us = (t - t0) / tpu
     us[t < t0] = np.nan  # stamps left from an earlier launch (roles depend on the view length)
     us[t == 0] = np.nan
@@ -79,6 +81,13 @@ def main():
     us = load(args.dump)
     print(f"{us.shape[0]} layers x {us.shape[1]} workgroups, launch span {np.nanmax(us):.1f} us")
     print(summarise(us, *args.layers))
+    if us.shape[2] > 23 and np.isfinite(us[0, :, 22]).any():
+        nl = us.shape[0]
+        last_done = np.nanmax(us[nl - 1, :, 12])
+        print(f"entry: workgroups start over {np.nanmax(us[0, :, 22]) - np.nanmin(us[0, :, 22]):.2f} us; "
+              f"entry -> layer 0 start: median {np.nanmedian(us[0, :, 0] - us[0, :, 22]):.2f} us; "
+              f"last layer done -> last exit: {np.nanmax(us[0, :, 23]) - last_done:.2f} us "
+              f"(median workgroup exit {np.nanmedian(us[0, :, 23]) - last_done:.2f} us)")
 
 
 if __name__ == "__main__":

@@ -8,8 +8,10 @@
 // (layer, hop) before it arrives; after every wait the consumer checks that every
 // producer of that hop has marked, so a wait that returns early is a violation.  Waits
 // are bounded like the kernel's (spin_limit polls, then the error word), threads sleep
-// for random short times between steps to vary the interleaving, and the last thread to
-// exit resets the counters.  Each run does several launches on one sync area.
+// for random short times between steps to vary the interleaving.  Launches alternate
+// between the two counter sets as the kernel's do: each thread clears its share of the
+// other set when it starts, the last thread to exit flips the parity word.  Each run does
+// several launches on one sync area.
 //
 // usage: persist_sim n_wg n_embd n_head n_head_kv hd n_ff n_layer fa_splits launches
 //                    spin_limit stall_hop seed
@@ -65,10 +67,12 @@ struct Walker {
         if (r < 14) std::this_thread::yield();
         else std::this_thread::sleep_for(std::chrono::microseconds(rng() % 50));
     }
+    size_t base = 0;  // this launch's counter set
+    unsigned par = 0;
     void arrive(int layer, int hop) {
         S.mk(layer, hop, wg).store(1, std::memory_order_release);
         for (int r = 0; r < kReps; r++)  // every replica of the counter set
-            S.sync[hop_ctr_word(layer, hop, wg & 7, r)].fetch_add(1, std::memory_order_acq_rel);
+            S.sync[base + hop_ctr_word(layer, hop, wg & 7, r)].fetch_add(1, std::memory_order_acq_rel);
         S.arrivals.fetch_add(1);
     }
     // the kernel's hop_wait: poll the 8 counters; give up after spin_limit polls or when
@@ -80,7 +84,8 @@ struct Walker {
             bool all = true;
             for (int j = 0; j < 8; j++) {  // the replica of this workgroup
                 const unsigned want = hop_want(S.lo, hop, j) + (layer == 0 && hop == S.stall_hop && j == 0);
-                all = all && S.sync[hop_ctr_word(layer, hop, j, wg % kReps)].load(std::memory_order_acquire) >= want;
+                all = all &&
+                      S.sync[base + hop_ctr_word(layer, hop, j, wg % kReps)].load(std::memory_order_acquire) >= want;
             }
             if (all) break;
             if (err.load(std::memory_order_acquire)) return;
@@ -100,13 +105,20 @@ struct Walker {
         std::atomic<unsigned> &ex = S.sync[exit_word(S.n_layer)];
         const unsigned prev = ex.fetch_add(1, std::memory_order_acq_rel);
         if (prev != (unsigned)S.lo.n_wg - 1) return;
-        for (size_t i = 0; i < hop_counters(S.n_layer); i++) S.sync[i * kCtrStride].store(0);
         S.sync[err_word(S.n_layer)].store(0);
+        S.sync[parity_word(S.n_layer)].store(par ^ 1u);
         ex.store(0);
     }
     // the walk of k_persist_q8_0: phase order, roles, which hop each phase waits on
     void run() {
         const Layout &lo = S.lo;
+        par = S.sync[parity_word(S.n_layer)].load() & 1u;
+        base = set_base(S.n_layer, (int)par);
+        const size_t other = set_base(S.n_layer, (int)(par ^ 1u));
+        for (size_t i = (size_t)wg; i < hop_counters(S.n_layer); i += (size_t)lo.n_wg) {  // this thread's share
+            jitter();
+            S.sync[other + i * kCtrStride].store(0);
+        }
         for (int l = 0; l < S.n_layer; l++) {
             if (is_qkv(lo, wg)) {  // q/k/v: after the previous layer's output
                 jitter();
@@ -193,8 +205,10 @@ int main(int argc, char **argv) {
         for (int w = 0; w < n_wg; w++)
             th.emplace_back([&S, w, seed, it] { Walker(S, w, seed + 1000u * (unsigned)it).run(); });
         for (auto &t : th) t.join();
-        // the next launch must find a clean sync area
-        for (size_t i = 0; i < S.sync.size(); i++) residue += S.sync[i].load() != 0;
+        // the next launch must find its counter set, the exit counter and the error word clean
+        const size_t next = set_base(n_layer, (int)(S.sync[parity_word(n_layer)].load() & 1u));
+        for (size_t i = 0; i < hop_counters(n_layer); i++) residue += S.sync[next + i * kCtrStride].load() != 0;
+        residue += S.sync[exit_word(n_layer)].load() != 0;
         err_left += S.sync[err_word(n_layer)].load();
         S.seed++;
         if (stall >= 0) S.stall_hop = -1;  // only the first launch stalls
