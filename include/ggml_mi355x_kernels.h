@@ -379,6 +379,18 @@ int mi_mul_mat_q4_0_f32(void *stream, const void *w_packed, const float *x, floa
 /* fp32 -> fp16 round-to-nearest-even of n values (n % 4 == 0) */
 int mi_cast_f32_f16(void *stream, const float *x, uint16_t *y, int64_t n);
 
+/* The output head of a decode token with its graph neighbours folded in:
+ * RMS_NORM(x) -> MUL(norm_w) -> MUL_MAT(F16 weight w [n rows of k, row stride ldw
+ * elements]) -> ARGMAX.  Writes the logits y [n] (bit-identical to mi_rms_norm,
+ * mi_gemv_f16 and mi_argmax in sequence) and their first maximum *out, in two launches:
+ * the head with the norm in its prologue and ARGMAX's first pass in its epilogue, then
+ * the final pass.  k a multiple of 32, at most 4096.  ws:
+ * mi_head_f16_argmax_workspace_size(n, k) bytes.  Replaces the reference's separate
+ * RMS_NORM, MUL and F16 MUL_MAT (patch:1133-1170, 1286-1309) and the host's greedy pick
+ * over the logits. */
+size_t mi_head_f16_argmax_workspace_size(int64_t n, int64_t k);
+int mi_head_f16_argmax(void *stream, const uint16_t *w, int64_t ldw, const float *x, const float *norm_w, float eps,
+                       float *y, int32_t *out, int64_t n, int64_t k, void *ws, size_t ws_bytes);
 /* ------------------------------------------------------------------------
  * F16 GEMV (replaces cast + aclnnMatmul(FRACTAL_NZ) + cast, patch:1286-1309,
  * used for the tied output head).  w : fp16 rows, row stride ldw elements

@@ -7,8 +7,10 @@
 // lines per 8 lanes), so F16 weights need no side copy.  Replaces the
 // cast + aclnnMatmul(FRACTAL_NZ) + cast chain of patch:1286-1309 and the
 // tied-output NZ side copy of patch:1451-1464.
+#include "decode_common.h"
 #include "mi_common.h"
 
+#include <limits.h>
 #include <stdlib.h>
 
 #include <algorithm>
@@ -213,6 +215,159 @@ int launch_g(hipStream_t st, const uint16_t *w, int64_t ldw, const float *x, flo
     return MI_ERR_ARG;
 }
 
+// The tied output head of a decode token with its neighbours in the graph folded in:
+// the output RMSNorm ((x*scale)*norm_w, as k_rms_norm then MUL compute it; XStage)
+// converted to fp16 into LDS as k_gemv_f16 converts its activation, k_gemv_f16<G,U,1>'s
+// row dot (same lanes, same order: the logits are bit-identical), and per workgroup the
+// first maximum of its rows, ARGMAX's first pass (strict >, so NaN is never taken and
+// ties keep the lower row; -inf rows leave the workgroup's first row).
+template <int G, int U, int XN>
+__global__ __launch_bounds__(256) void k_head_f16(const uint16_t *__restrict__ w, int64_t ldw,
+                                                  const float *__restrict__ x, const float *__restrict__ norm_w,
+                                                  float eps, float *__restrict__ y, float2 *__restrict__ part, int n,
+                                                  int k) {
+    constexpr int RPB = 256 / G;
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint16_t *s_x = (uint16_t *)smem;  // [k] fp16
+    __shared__ double s_red[4];
+    __shared__ float s_v[RPB];
+    __shared__ int s_i[RPB];
+    const int tid = threadIdx.x;
+    const int j = tid % G;
+    const int row = blockIdx.x * RPB + tid / G;
+    const bool row_ok = row < n;
+    const int nc = k / 8, k4 = k / 4;
+    const uint16_t *wr = w + (size_t)min(row, n - 1) * ldw;
+
+    int4 wv[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) wv[u] = ld_stream16(wr + (size_t)min(j + u * G, nc - 1) * 8);
+
+    XStage<XN, true> st;
+    xstage_load(st, x, norm_w, nullptr, k4, tid);
+    const float scale = xstage_scale(st, k4, eps, s_red, tid);
+#pragma unroll
+    for (int t = 0; t < XN; t++) {
+        const int f = tid + t * 256;
+        if (f < k4) {
+            const float4 v = xstage_value(st, scale, t);
+            *(uint2 *)(s_x + (size_t)f * 4) = make_uint2((uint32_t)f2h(v.x) | ((uint32_t)f2h(v.y) << 16),
+                                                         (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16));
+        }
+    }
+    __syncthreads();
+
+    float acc = 0.0f;
+    auto consume = [&](int c, const int4 &wq) {
+        const int4 xv = *(const int4 *)(s_x + (size_t)c * 8);
+        float s = acc;
+        s = fdot2((uint32_t)wq.x, (uint32_t)xv.x, s);
+        s = fdot2((uint32_t)wq.y, (uint32_t)xv.y, s);
+        s = fdot2((uint32_t)wq.z, (uint32_t)xv.z, s);
+        s = fdot2((uint32_t)wq.w, (uint32_t)xv.w, s);
+        acc = s;
+    };
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int c = j + u * G;
+        if (c < nc) consume(c, wv[u]);
+    }
+    for (int c0 = U * G; c0 < nc; c0 += U * G) {
+#pragma unroll
+        for (int u = 0; u < U; u++) wv[u] = ld_stream16(wr + (size_t)min(c0 + j + u * G, nc - 1) * 8);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int c = c0 + j + u * G;
+            if (c < nc) consume(c, wv[u]);
+        }
+    }
+    const float v = group_sum<G>(acc);
+    if (j == 0) {
+        if (row_ok) y[row] = v;
+        s_v[tid / G] = row_ok ? v : -INFINITY;
+        s_i[tid / G] = row;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float best = -INFINITY;
+        int bi = blockIdx.x * RPB;
+#pragma unroll
+        for (int r = 0; r < RPB; r++)
+            if (s_v[r] > best) {
+                best = s_v[r];
+                bi = s_i[r];
+            }
+        part[blockIdx.x] = make_float2(best, __int_as_float(bi));
+    }
+}
+
+// ARGMAX's final pass over the head's per-workgroup partials: the first maximum (equal
+// values keep the lower index)
+__global__ __launch_bounds__(256) void k_head_argmax_final(const float2 *__restrict__ part, int n_parts,
+                                                           int32_t *__restrict__ out) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    auto merge = [](float &v, int &i, float v2, int i2) {
+        if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+    };
+    float best = -INFINITY;
+    int bi = INT_MAX;
+    for (int c = threadIdx.x; c < n_parts; c += 256) {
+        const float2 p = part[c];
+        merge(best, bi, p.x, __float_as_int(p.y));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) merge(best, bi, __shfl_xor(best, o, 64), __shfl_xor(bi, o, 64));
+    if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = best; si[threadIdx.x >> 6] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        best = sv[0];
+        bi = si[0];
+#pragma unroll
+        for (int w = 1; w < 4; w++) merge(best, bi, sv[w], si[w]);
+        out[0] = bi == INT_MAX ? 0 : bi;
+    }
+}
+
+// the lanes per row and the rows per pass of k_gemv_f16<G, U, 1> at this k
+int head_g(int64_t k) { return k / 8 <= 128 ? 16 : (k / 8 <= 256 ? 32 : 64); }
+int head_u(int64_t k, int g) {
+    int64_t u = (k / 8 + g - 1) / g;
+    if (u > 8) u = (u + 1) / 2 > 8 ? 8 : (u + 1) / 2;
+    return (int)u;
+}
+
+template <int G, int U, int XN>
+int launch_head_gux(hipStream_t st, const uint16_t *w, int64_t ldw, const float *x, const float *norm_w, float eps,
+                    float *y, float2 *part, int64_t n, int64_t k) {
+    constexpr int RPB = 256 / G;
+    hipLaunchKernelGGL((k_head_f16<G, U, XN>), dim3((unsigned)((n + RPB - 1) / RPB)), dim3(256), (size_t)k * 2, st, w,
+                       ldw, x, norm_w, eps, y, part, (int)n, (int)k);
+    MI_CHECK_LAUNCH("k_head_f16");
+    return MI_OK;
+}
+
+template <int G, int XN>
+int launch_head_gx(hipStream_t st, const uint16_t *w, int64_t ldw, const float *x, const float *norm_w, float eps,
+                   float *y, float2 *part, int64_t n, int64_t k) {
+#define MI_U_CASE(UU) case UU: return launch_head_gux<G, UU, XN>(st, w, ldw, x, norm_w, eps, y, part, n, k);
+    switch (head_u(k, G)) {
+        MI_U_CASE(1) MI_U_CASE(2) MI_U_CASE(3) MI_U_CASE(4) MI_U_CASE(5) MI_U_CASE(6) MI_U_CASE(7) MI_U_CASE(8)
+    }
+#undef MI_U_CASE
+    return MI_ERR_ARG;
+}
+
+template <int XN>
+int launch_head_x(hipStream_t st, const uint16_t *w, int64_t ldw, const float *x, const float *norm_w, float eps,
+                  float *y, float2 *part, int64_t n, int64_t k) {
+    switch (head_g(k)) {
+        case 16: return launch_head_gx<16, XN>(st, w, ldw, x, norm_w, eps, y, part, n, k);
+        case 32: return launch_head_gx<32, XN>(st, w, ldw, x, norm_w, eps, y, part, n, k);
+        default: return launch_head_gx<64, XN>(st, w, ldw, x, norm_w, eps, y, part, n, k);
+    }
+}
+
 template <int M>
 int launch_m(hipStream_t st, const uint16_t *w, int64_t ldw, const float *x, float *y, int64_t n, int64_t k,
              int64_t m) {
@@ -223,6 +378,38 @@ int launch_m(hipStream_t st, const uint16_t *w, int64_t ldw, const float *x, flo
 }
 
 }  // namespace
+
+extern "C" size_t mi_head_f16_argmax_workspace_size(int64_t n, int64_t k) {
+    if (n <= 0 || k <= 0) return 0;
+    const int64_t rpb = 256 / head_g(k);
+    return mi::align_up((size_t)((n + rpb - 1) / rpb) * sizeof(float2), 256);
+}
+
+extern "C" int mi_head_f16_argmax(void *stream, const uint16_t *w, int64_t ldw, const float *x, const float *norm_w,
+                                  float eps, float *y, int32_t *out, int64_t n, int64_t k, void *ws,
+                                  size_t ws_bytes) {
+    MI_CHECK_ARG(w && x && norm_w && y && out, "head_f16_argmax: null pointer");
+    MI_CHECK_ARG(n > 0 && k > 0 && k % 32 == 0 && k <= 4096 && ldw >= k && ldw % 8 == 0 && n < (1ll << 31),
+                 "head_f16_argmax: bad shape n=%lld k=%lld ldw=%lld (k a multiple of 32, <= 4096)", (long long)n,
+                 (long long)k, (long long)ldw);
+    MI_CHECK_ARG(mi::aligned(w, 16) && mi::aligned(x, 16) && mi::aligned(norm_w, 16),
+                 "head_f16_argmax: w, x and norm_w must be 16-byte aligned");
+    const size_t need = mi_head_f16_argmax_workspace_size(n, k);
+    if (!ws || ws_bytes < need || !mi::aligned(ws, 8)) {
+        mi::set_error("head_f16_argmax: workspace %zu < %zu bytes (or misaligned)", ws_bytes, need);
+        return MI_ERR_WORKSPACE;
+    }
+    hipStream_t st = (hipStream_t)stream;
+    float2 *part = (float2 *)ws;
+    const int r = k <= 2048 ? launch_head_x<2>(st, w, ldw, x, norm_w, eps, y, part, n, k)
+                            : launch_head_x<4>(st, w, ldw, x, norm_w, eps, y, part, n, k);
+    if (r) return r;
+    const int64_t rpb = 256 / head_g(k);
+    hipLaunchKernelGGL(k_head_argmax_final, dim3(1), dim3(256), 0, st, (const float2 *)part, (int)((n + rpb - 1) / rpb),
+                       out);
+    MI_CHECK_LAUNCH("k_head_argmax_final");
+    return MI_OK;
+}
 
 extern "C" int mi_gemv_f16(void *stream, const uint16_t *w, int64_t ldw, const float *x, float *y, int64_t n,
                            int64_t k, int64_t m) {

@@ -562,7 +562,9 @@ size_t scratch_need(const ggml_tensor *node) {
                         node->src[1]->ne[1] == 1 ? mi_xq_size(1, node->src[1]->ne[0]) : (size_t)0);
     if (node->op == GGML_OP_MUL_MAT && packed_fmt(node->src[0]) == GGML_TYPE_Q4_0)
         return mi_mul_mat_q4_0_workspace_size(node->src[1]->ne[1], node->src[1]->ne[0]);
-    if (node->op == GGML_OP_ARGMAX) return mi_argmax_workspace_size(node->src[0]->ne[0], ggml_nrows(node->src[0]));
+    if (node->op == GGML_OP_ARGMAX)  // also the partials of the fused output head (try_fuse_norm_head)
+        return std::max(mi_argmax_workspace_size(node->src[0]->ne[0], ggml_nrows(node->src[0])),
+                        mi_head_f16_argmax_workspace_size(node->src[0]->ne[0], 4096));
     // one GLU row: fp16 (W4A16 down), or the A8W8 gate/up pair's quantized row and its
     // fp32 swiglu values
     if (node->op == GGML_OP_GLU && ggml_nrows(node) == 1)
@@ -1105,6 +1107,37 @@ const ggml_tensor *matmul_add_tail(ggml_cgraph *g, int j, const ggml_tensor *mm,
     if (!other || other == mm || !is_row_vector(other, mm->ne[0]) || !only_consumed_by(C, mm, {ad})) return nullptr;
     vec = other;
     return ad;
+}
+
+// RMS_NORM -> MUL(norm_w) -> MUL_MAT(F16 weight, one row) -> ARGMAX: the output head of
+// a decode token in one launch with the norm in its prologue and the argmax's first pass
+// in its epilogue, then the argmax's final pass (the logits are written as the MUL_MAT
+// node's output)
+int try_fuse_norm_head(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    int j;
+    const ggml_tensor *x, *nw, *mul;
+    float eps;
+    if (!rms_mul_head(g, i, C, j, x, nw, mul, eps)) return 0;
+    const int nn = ggml_graph_n_nodes(g);
+    const int jm = next_real(g, j + 1);
+    if (jm >= nn) return 0;
+    ggml_tensor *mm = ggml_graph_node(g, jm);
+    if (mm->op != GGML_OP_MUL_MAT || mm->src[1] != mul || !is_f32_contig(mm) || !only_consumed_by(C, mul, {mm}))
+        return 0;
+    const ggml_tensor *a = mm->src[0];
+    if (a->type != GGML_TYPE_F16 || a->nb[0] != 2 || a->nb[1] % 16 || !aligned16(a->data) || a->ne[0] != x->ne[0] ||
+        a->ne[2] != 1 || a->ne[3] != 1 || !aligned16(nw->data))
+        return 0;
+    const int ja = next_real(g, jm + 1);
+    if (ja >= nn) return 0;
+    ggml_tensor *am = ggml_graph_node(g, ja);
+    if (am->op != GGML_OP_ARGMAX || am->src[0] != mm) return 0;
+    const int64_t n = a->ne[1], k = a->ne[0];
+    if (ctx->scratch_size < mi_head_f16_argmax_workspace_size(n, k)) return 0;
+    MI_K_CHECK(mi_head_f16_argmax(ctx->stream, (const uint16_t *)a->data, (int64_t)(a->nb[1] / 2),
+                                  (const float *)x->data, (const float *)nw->data, eps, (float *)mm->data,
+                                  (int32_t *)am->data, n, k, ctx->scratch, ctx->scratch_size));
+    return ja + 1 - i;
 }
 
 int try_fuse_matmul_add(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
@@ -1890,6 +1923,7 @@ int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
                 if (int used = try_fuse_attn_in(ctx, g, i, C)) return used;
                 if (int used = try_fuse_norm_matmuls(ctx, g, i, C)) return used;
                 if (int used = try_fuse_norm_q4_batch(ctx, g, i, C)) return used;
+                if (int used = try_fuse_norm_head(ctx, g, i, C)) return used;
             }
             float eps;
             memcpy(&eps, node->op_params, sizeof(float));

@@ -98,6 +98,8 @@ _SIGS = {
     "mi_fa_decode_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _SZ, _SZ, _SZ, _SZ, _F, _P]),
     "mi_mul_mat_q8_0_f32_multi": (_I, [_P, _I, _P, _P, _P, _I64, _P, _P, _I, _P, _SZ]),
     "mi_rms_norm": (_I, [_P, _P, _P, _P, _I64, _I64, _F]),
+    "mi_head_f16_argmax_workspace_size": (_SZ, [_I64, _I64]),
+    "mi_head_f16_argmax": (_I, [_P, _P, _I64, _P, _P, _F, _P, _P, _I64, _I64, _P, _SZ]),
     "mi_add_bcast": (_I, [_P, _P, _P, _P, _I64, _I64]),
     "mi_mul_bcast": (_I, [_P, _P, _P, _P, _I64, _I64]),
     "mi_rope_neox": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _F, _F, _SZ, _SZ, _SZ, _SZ]),

@@ -691,6 +691,52 @@ def test_q8_batch_set(gpu, orc, ns, k, m, mode):
             assert rel_err(got[r], ref) < GEMV_TOL, f"matrix {t} row {r}"
 
 
+@pytest.mark.parametrize("n,k,case", [(151936, 1536, "random"), (152064, 3584, "random"), (5000, 1536, "ties"),
+                                      (333, 256, "nan"), (77, 512, "all_neg_inf")])
+def test_head_f16_argmax(gpu, n, k, case):
+    """The output head with the norm and the argmax folded in (mi_head_f16_argmax):
+    logits bit-identical to mi_rms_norm + mi_gemv_f16, and the same index as mi_argmax
+    over them, including equal maxima in different workgroups (the lower row wins), NaN
+    rows (never taken) and all-(-inf) logits (index 0)."""
+    mi = gpu
+    P = mi._P
+    rng = np.random.default_rng(n + k)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * F32(0.05)).astype(np.float16)
+    x = rng.standard_normal(k).astype(F32)
+    if case == "ties":  # rows 4321 and 17 (workgroups apart) equal, and far above the others
+        w[17] = w[4321] = (np.sign(x) * 0.5).astype(np.float16)
+    if case == "nan":
+        w[5, :] = np.float16(np.nan)
+    if case == "all_neg_inf":
+        w[:, :] = np.float16(-np.inf)
+    if case == "all_neg_inf":
+        x = np.abs(x) + F32(0.5)
+    nw = rng.uniform(0.8, 1.2, k).astype(F32)
+    dw, dx, dnw = mi.to_device(w.view(np.uint16)), mi.to_device(x), mi.to_device(nw)
+    y1, y2 = mi.DeviceBuffer(4 * n), mi.DeviceBuffer(4 * n)
+    o1, o2 = mi.DeviceBuffer(4), mi.DeviceBuffer(4)
+    h = mi.DeviceBuffer(4 * k)
+    wsb = max(mi.lib().mi_head_f16_argmax_workspace_size(n, k), mi.lib().mi_argmax_workspace_size(n, 1))
+    ws = mi.DeviceBuffer(wsb)
+    mi._call("mi_head_f16_argmax", None, P(dw.ptr), k, P(dx.ptr), P(dnw.ptr), F32(1e-6), P(y1.ptr), P(o1.ptr), n, k,
+             P(ws.ptr), wsb)
+    mi.device_sync()
+    mi._call("mi_rms_norm", None, P(dx.ptr), P(dnw.ptr), P(h.ptr), k, 1, F32(1e-6))
+    mi._call("mi_gemv_f16", None, P(dw.ptr), k, P(h.ptr), P(y2.ptr), n, k, 1)
+    mi._call("mi_argmax", None, P(y2.ptr), P(o2.ptr), n, 1, P(ws.ptr), wsb)
+    mi.device_sync()
+    a, b = y1.download(F32), y2.download(F32)
+    assert np.array_equal(a.view(np.int32), b.view(np.int32)), f"logits differ at {np.flatnonzero(a != b)[:5]}"
+    i1, i2 = int(o1.download(np.int32)[0]), int(o2.download(np.int32)[0])
+    assert i1 == i2, (i1, i2)
+    if case == "ties":
+        assert i1 == 17
+    if case == "all_neg_inf":
+        assert i1 == 0 and np.all(np.isneginf(a))
+    if case == "nan":
+        assert np.isnan(a[5]) and i1 != 5
+
+
 def test_q4_batch_set_rejects_bad_shapes(gpu):
     mi = gpu
     P = mi._P
