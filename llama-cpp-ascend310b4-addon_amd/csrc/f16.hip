@@ -301,20 +301,29 @@ __global__ __launch_bounds__(256) void k_head_f16(const uint16_t *__restrict__ w
     }
 }
 
-// ARGMAX's final pass over the head's per-workgroup partials: the first maximum (equal
-// values keep the lower index)
-__global__ __launch_bounds__(256) void k_head_argmax_final(const float2 *__restrict__ part, int n_parts,
-                                                           int32_t *__restrict__ out) {
-    __shared__ float sv[4];
-    __shared__ int si[4];
+// ARGMAX's final pass over the head's per-workgroup partials (one per 4..16 rows: ~19K
+// for a 152K vocabulary): the first maximum (equal values keep the lower index).  1024
+// threads, each with 8 partials' loads in flight per step: one thread walking its share
+// with one load at a time took ~24 us.
+__global__ __launch_bounds__(1024) void k_head_argmax_final(const float2 *__restrict__ part, int n_parts,
+                                                            int32_t *__restrict__ out) {
+    constexpr int B = 8;
+    __shared__ float sv[16];
+    __shared__ int si[16];
     auto merge = [](float &v, int &i, float v2, int i2) {
         if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
     };
     float best = -INFINITY;
     int bi = INT_MAX;
-    for (int c = threadIdx.x; c < n_parts; c += 256) {
-        const float2 p = part[c];
-        merge(best, bi, p.x, __float_as_int(p.y));
+    for (int c0 = threadIdx.x; c0 < n_parts; c0 += 1024 * B) {
+        float2 p[B];
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const int c = c0 + b * 1024;
+            p[b] = c < n_parts ? part[c] : make_float2(-INFINITY, __int_as_float(INT_MAX));
+        }
+#pragma unroll
+        for (int b = 0; b < B; b++) merge(best, bi, p[b].x, __float_as_int(p[b].y));
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) merge(best, bi, __shfl_xor(best, o, 64), __shfl_xor(bi, o, 64));
@@ -324,7 +333,7 @@ __global__ __launch_bounds__(256) void k_head_argmax_final(const float2 *__restr
         best = sv[0];
         bi = si[0];
 #pragma unroll
-        for (int w = 1; w < 4; w++) merge(best, bi, sv[w], si[w]);
+        for (int w = 1; w < 16; w++) merge(best, bi, sv[w], si[w]);
         out[0] = bi == INT_MAX ? 0 : bi;
     }
 }
@@ -405,8 +414,8 @@ extern "C" int mi_head_f16_argmax(void *stream, const uint16_t *w, int64_t ldw, 
                             : launch_head_x<4>(st, w, ldw, x, norm_w, eps, y, part, n, k);
     if (r) return r;
     const int64_t rpb = 256 / head_g(k);
-    hipLaunchKernelGGL(k_head_argmax_final, dim3(1), dim3(256), 0, st, (const float2 *)part, (int)((n + rpb - 1) / rpb),
-                       out);
+    hipLaunchKernelGGL(k_head_argmax_final, dim3(1), dim3(1024), 0, st, (const float2 *)part,
+                       (int)((n + rpb - 1) / rpb), out);
     MI_CHECK_LAUNCH("k_head_argmax_final");
     return MI_OK;
 }
