@@ -13,6 +13,7 @@
 #include "q8_0_dev.h"
 
 #include <limits.h>
+#include <atomic>
 #include <math.h>
 #include <string.h>
 
@@ -716,6 +717,8 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0_xs(const Q8Set S, unsigned ad
     }
 }
 
+constexpr int kMaxDevices = 64;
+
 size_t xs_lds_bytes(int64_t m, int64_t k) { return (size_t)(m * k + (m * (k / QK) + 1) / 2 * 4); }
 
 template <int G, int U, int M>
@@ -724,15 +727,22 @@ int launch_xs_gum(hipStream_t st, const Q8Set &S, unsigned add_rows, int n_total
     constexpr int RPB = 256 / G;
     const size_t lds = xs_lds_bytes(m, k);
     auto kern = k_gemv_q8_0_xs<G, U, M>;
-    static size_t raised = 65536;  // per instantiation: dynamic LDS allowed so far (64 KB by default)
-    if (lds > raised) {
+    // dynamic LDS allowed so far per device for this instantiation (64 KB by default)
+    static std::atomic<size_t> raised[kMaxDevices];
+    int dev = 0;
+    if (lds > 65536 && (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices ||
+                        lds > raised[dev].load(std::memory_order_relaxed))) {
         if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
             hipSuccess) {
             (void)hipGetLastError();
             set_error("gemv_q8_0_xs: %zu bytes of LDS per workgroup not available", lds);
             return MI_ERR_UNSUPPORTED;
         }
-        raised = lds;
+        if (dev >= 0 && dev < kMaxDevices) {
+            size_t cur = raised[dev].load(std::memory_order_relaxed);
+            while (cur < lds && !raised[dev].compare_exchange_weak(cur, lds)) {
+            }
+        }
     }
     hipLaunchKernelGGL(kern, dim3((unsigned)((n_total + RPB - 1) / RPB)), dim3(256), lds, st, S, add_rows, xq_qs, xq_d,
                        n_total, (int)(k / QK), (int)m);
