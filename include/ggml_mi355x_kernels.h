@@ -175,6 +175,11 @@ typedef struct mi_persist_args {
     int debug_stall_hop;       /* -1; h in 0..4: the waits on hop h of the first layer expect one
                                   arrival more than its producers make, so they give up after
                                   spin_limit polls (tests of the error path) */
+    const uint16_t *embd;      /* or, with x_in NULL: the first layer's input is row tok[0] of this
+                                  F16 table (the token embedding; GET_ROWS folded in), rows embd_ld
+                                  elements apart, 8-byte aligned */
+    int64_t embd_ld;
+    const int32_t *tok;        /* the row index (device, 1 value) */
 } mi_persist_args;
 
 /* context: scratch (per-layer intermediates), counters, pinned error word; allocates */

@@ -1388,7 +1388,9 @@ void collect_persist_timing(BackendCtx *ctx) {
     ctx->pt_pending = false;
 }
 
-int try_fuse_persist(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+// embd_rows: the GET_ROWS node whose output is the run's input (try_fuse_persist_embd)
+int try_fuse_persist(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C,
+                     const ggml_tensor *embd_rows = nullptr) {
     if (!ctx->persist_on || ctx->persist_failed) return 0;
     std::vector<PersistLayerMatch> run;
     PersistLayerMatch P;
@@ -1403,6 +1405,7 @@ int try_fuse_persist(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C)
     }
     if (run.empty()) return 0;
     const PersistLayerMatch &F = run.front();
+    if (embd_rows && (F.x != embd_rows || !only_consumed_by(C, embd_rows, {F.rms, F.x1}))) return 0;
     if (!mi_persist_supported(F.n_kv, (int)F.n_embd, (int)F.n_head, (int)F.n_head_kv, (int)F.hd, (int)F.n_ff))
         return 0;
     const int n_layer = (int)run.size();
@@ -1426,7 +1429,14 @@ int try_fuse_persist(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C)
     for (int l = 0; l < n_layer; l++) layers[l] = run[l].L;
     MI_K_CHECK(mi_persist_set_layers(ctx->stream, ctx->persist, layers.data(), n_layer));
     mi_persist_args a{};
-    a.x_in = (const float *)F.x->data;
+    if (embd_rows) {  // the run reads the token's embedding row itself (GET_ROWS not launched)
+        a.x_in = nullptr;
+        a.embd = (const uint16_t *)embd_rows->src[0]->data;
+        a.embd_ld = (int64_t)(embd_rows->src[0]->nb[1] / 2);
+        a.tok = (const int32_t *)embd_rows->src[1]->data;
+    } else {
+        a.x_in = (const float *)F.x->data;
+    }
     a.x_out = (float *)run.back().out->data;
     a.pos = (const int32_t *)F.rope->src[1]->data;
     a.kv_idx = F.idx->data;
@@ -1457,6 +1467,23 @@ int try_fuse_persist(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C)
         ctx->pt_pending = true;
     }
     return run.back().end + 1 - i;
+}
+
+// GET_ROWS (one token's F16 embedding row) read only by the first layer of a persistent
+// run that follows it: the run reads the row itself, so the GET_ROWS launch and its fp32
+// row go
+int try_fuse_persist_embd(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
+    if (!ctx->persist_on || ctx->persist_failed) return 0;
+    const ggml_tensor *gr = ggml_graph_node(g, i);
+    const ggml_tensor *t = gr->src[0], *ids = gr->src[1];
+    if (t->type != GGML_TYPE_F16 || ids->type != GGML_TYPE_I32 || ggml_nelements(ids) != 1 ||
+        gr->type != GGML_TYPE_F32 || ggml_nrows(gr) != 1 || t->ne[0] != gr->ne[0] || t->nb[0] != 2 || t->nb[1] % 8 ||
+        ((uintptr_t)t->data & 7))
+        return 0;
+    const int j = next_real(g, i + 1);
+    if (j >= ggml_graph_n_nodes(g) || ggml_graph_node(g, j)->op != GGML_OP_RMS_NORM) return 0;
+    const int used = try_fuse_persist(ctx, g, j, C, gr);
+    return used ? j + used - i : 0;
 }
 
 // ---- several activation rows (a ubatch of tokens) through Q4_0 weights
@@ -1972,6 +1999,8 @@ int compute_node(BackendCtx *ctx, ggml_cgraph *g, int i, const Consumers &C) {
             return 1;
         }
         case GGML_OP_GET_ROWS: {
+            if (fuse)
+                if (int used = try_fuse_persist_embd(ctx, g, i, C)) return used;
             const ggml_tensor *src = node->src[0], *idx = node->src[1];
             MI_K_CHECK(mi_get_rows(st, src->data, src->type == GGML_TYPE_F16, (const int32_t *)idx->data,
                                    (float *)node->data, src->ne[0], idx->ne[0], src->nb[1], src->ne[1]));

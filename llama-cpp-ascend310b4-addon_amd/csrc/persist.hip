@@ -70,7 +70,10 @@ struct PArgs {
     int stall_hop;
     int fa_chunk, fa_splits;
     Layout lo;
-    const float *x_in;    // the first layer's input
+    const float *x_in;    // the first layer's input, or null: then row tok[0] of embd
+    const uint16_t *embd;  // F16 token-embedding table, rows embd_ld elements apart
+    size_t embd_ld;
+    const int32_t *tok;
     float *x_out;         // the last layer's output
     uint64_t *trace;      // phase timestamps [layer][workgroup][kTraceEvents], or null
     float *scratch;
@@ -146,6 +149,23 @@ __device__ __forceinline__ void persist_exit(const PArgs &a, unsigned par) {
     st_u(a.sync + persist_plan::err_word(a.n_layer), 0u);
     st_u(a.sync + persist_plan::parity_word(a.n_layer), par ^ 1u);
     st_u(exit_ctr, 0u);
+}
+
+// xstage_load of a row of fp16 values (the token's embedding row, GET_ROWS folded in: the
+// fp16 -> fp32 conversion is exact, so the staged values are GET_ROWS' output)
+template <int XN, bool NORM>
+__device__ __forceinline__ void xstage_load_h(XStage<XN, NORM> &st, const uint16_t *__restrict__ x,
+                                              const float *__restrict__ norm_w, const float *__restrict__ inv_s,
+                                              int k4, int tid) {
+#pragma unroll
+    for (int t = 0; t < XN; t++) {
+        const int f = min(tid + t * 256, k4 - 1);
+        const uint2 h = *(const uint2 *)(x + (size_t)f * 4);
+        st.xv[t] = make_float4(h2f((uint16_t)(h.x & 0xffffu)), h2f((uint16_t)(h.x >> 16)),
+                               h2f((uint16_t)(h.y & 0xffffu)), h2f((uint16_t)(h.y >> 16)));
+        if constexpr (NORM) st.nv[t] = ((const float4 *)norm_w)[f];
+        if (inv_s) st.sv[t] = ((const float4 *)inv_s)[f];
+    }
 }
 
 // the attention tile's wait on hop 0 (q and the new cache row written), and its stage
@@ -263,6 +283,8 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
     // exit); the other set, the previous launch's, is cleared here for the next launch
     const unsigned par = ld_u(a.sync + persist_plan::parity_word(a.n_layer)) & 1u;
     unsigned *const ctrs = a.sync + persist_plan::set_base(a.n_layer, (int)par);
+    // the first layer's input as the token's fp16 embedding row (or null: a.x_in)
+    const uint16_t *const erow = a.x_in ? nullptr : a.embd + (size_t)a.tok[0] * a.embd_ld;
     {
         unsigned *other = a.sync + persist_plan::set_base(a.n_layer, (int)(par ^ 1u));
         const size_t n = persist_plan::hop_counters(a.n_layer);
@@ -325,7 +347,10 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
             if (layer > 0) hop_wait(a, ctrs, layer - 1, 4);
             trace_mark(layer, 1);
             XStage<XN, true> st;
-            xstage_load(st, x, P.attn_norm, P.inv_s_attn, k4, tid);
+            if (layer == 0 && erow)
+                xstage_load_h(st, erow, P.attn_norm, P.inv_s_attn, k4, tid);
+            else
+                xstage_load(st, x, P.attn_norm, P.inv_s_attn, k4, tid);
             const float scale = xstage_scale(st, k4, a.eps, L.red, tid);
             xstage_quant(st, P.inv_s_attn, k4, scale, a.rounding, L.qs, L.d, tid);
             __syncthreads();
@@ -399,7 +424,8 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
                                     : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
             hop_wait(a, ctrs, layer, 1);
             trace_mark(layer, 5);
-            const float xres = x[min(row, E - 1)];  // the residual (the layer input)
+            const float xres = layer == 0 && erow ? h2f(erow[min(row, E - 1)])
+                                                  : x[min(row, E - 1)];  // the residual (the layer input)
             // the records' maxima and sums first (a wave's loads return in order: the merge
             // weights are formed while the partial outputs still arrive), then this thread's
             // partial outputs; slots past the last split (weight 0 in the merge) and elements
@@ -745,8 +771,12 @@ int mi_persist_set_layers(void *stream, void *ctx, const mi_persist_layer *layer
 int mi_persist_decode_q8_0(void *stream, void *ctx, const mi_persist_args *args) {
     PersistCtx *c = (PersistCtx *)ctx;
     MI_CHECK_ARG(c && args && !c->layers_host.empty(), "persist_decode: no context or no layers set");
-    MI_CHECK_ARG(args->x_in && args->x_out && mi::aligned(args->x_in, 16) && mi::aligned(args->x_out, 16),
-                 "persist_decode: x_in / x_out must be 16-byte aligned device vectors");
+    MI_CHECK_ARG(args->x_out && mi::aligned(args->x_out, 16) &&
+                     (args->x_in ? mi::aligned(args->x_in, 16)
+                                 : args->embd && args->tok && mi::aligned(args->embd, 8) && args->embd_ld >= c->n_embd &&
+                                       args->embd_ld % 4 == 0),
+                 "persist_decode: x_in / x_out must be 16-byte aligned device vectors (or x_in NULL and an "
+                 "8-byte aligned F16 embedding table with its row index)");
     MI_CHECK_ARG(args->pos && args->kv_idx && args->kv_row_bytes >= (size_t)c->n_head_kv * c->hd * 2 &&
                      args->kv_row_bytes % 16 == 0 && args->n_kv > 0 && args->n_cache_rows > 0,
                  "persist_decode: bad position / cache arguments");
@@ -786,6 +816,9 @@ int mi_persist_decode_q8_0(void *stream, void *ctx, const mi_persist_args *args)
     MI_CHECK_ARG(persist_plan::layout_fits(a.lo, NGU, NDN), "persist_decode: %d workgroups do not fit the tiles",
                  c->n_wg);
     a.x_in = args->x_in;
+    a.embd = args->x_in ? nullptr : args->embd;
+    a.embd_ld = (size_t)args->embd_ld;
+    a.tok = args->tok;
     a.x_out = args->x_out;
     a.trace = c->trace;
     a.scratch = c->scratch;
