@@ -31,8 +31,8 @@
 // after the producers finished.  Every wait is bounded (spin_limit polls): on a timeout
 // the workgroup raises the error word, every later wait returns at once, and all
 // workgroups still reach the exit.  Launches alternate between two counter sets: each
-// workgroup clears its share of the previous launch's set when it starts, and the last
-// one to exit flips the parity word that names the next launch's set (one workgroup
+// workgroup clears its share of the previous launch's set in the first layer, and the
+// last one to exit flips the parity word that names the next launch's set (one workgroup
 // zeroing 17,920 counter lines at the exit held the launch 23 us).  The host reads the
 // error from pinned memory.
 #include "q8_0_dev.h"
@@ -280,17 +280,12 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
     };
     trace_mark(0, 22);
     // the counter set of this launch (the parity word, flipped by the previous launch's
-    // exit); the other set, the previous launch's, is cleared here for the next launch
+    // exit); the other set, the previous launch's, is cleared in the first layer's phase 4
+    // for the next launch (there the parity load has long returned)
     const unsigned par = ld_u(a.sync + persist_plan::parity_word(a.n_layer)) & 1u;
     unsigned *const ctrs = a.sync + persist_plan::set_base(a.n_layer, (int)par);
     // the first layer's input as the token's fp16 embedding row (or null: a.x_in)
     const uint16_t *const erow = a.x_in ? nullptr : a.embd + (size_t)a.tok[0] * a.embd_ld;
-    {
-        unsigned *other = a.sync + persist_plan::set_base(a.n_layer, (int)(par ^ 1u));
-        const size_t n = persist_plan::hop_counters(a.n_layer);
-        for (size_t i = (size_t)wg * 256 + tid; i < n; i += (size_t)nwg * 256)
-            st_u(other + i * persist_plan::kCtrStride, 0u);
-    }
 
     for (int layer = 0; layer < a.n_layer; layer++) {
         // the thread index, opaque to the optimizer in every iteration: the phases' address
@@ -537,6 +532,12 @@ __global__ __launch_bounds__(256) void k_persist_q8_0(const PArgs a) {
         // ================= phase 4: FFN norm + gate/up + swiglu
         {
             trace_mark(layer, 7);
+            if (layer == 0) {  // this workgroup's share of the other counter set
+                unsigned *other = a.sync + persist_plan::set_base(a.n_layer, (int)(par ^ 1u));
+                const size_t n = persist_plan::hop_counters(a.n_layer);
+                for (size_t i = (size_t)wg * 256 + tid; i < n; i += (size_t)nwg * 256)
+                    st_u(other + i * persist_plan::kCtrStride, 0u);
+            }
             if (!o_role) gu_prefetch();
             // the down projection's SmoothQuant divisor of this thread's swiglu row
             const int sw_i = tid / HR, sw_r = tid % HR;

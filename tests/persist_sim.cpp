@@ -10,7 +10,8 @@
 // are bounded like the kernel's (spin_limit polls, then the error word), threads sleep
 // for random short times between steps to vary the interleaving.  Launches alternate
 // between the two counter sets as the kernel's do: each thread clears its share of the
-// other set when it starts, the last thread to exit flips the parity word.  Each run does
+// other set in the first layer's gate/up phase, the last thread to exit flips the parity
+// word.  Each run does
 // several launches on one sync area.
 //
 // usage: persist_sim n_wg n_embd n_head n_head_kv hd n_ff n_layer fa_splits launches
@@ -115,10 +116,6 @@ struct Walker {
         par = S.sync[parity_word(S.n_layer)].load() & 1u;
         base = set_base(S.n_layer, (int)par);
         const size_t other = set_base(S.n_layer, (int)(par ^ 1u));
-        for (size_t i = (size_t)wg; i < hop_counters(S.n_layer); i += (size_t)lo.n_wg) {  // this thread's share
-            jitter();
-            S.sync[other + i * kCtrStride].store(0);
-        }
         for (int l = 0; l < S.n_layer; l++) {
             if (is_qkv(lo, wg)) {  // q/k/v: after the previous layer's output
                 jitter();
@@ -137,6 +134,11 @@ struct Walker {
                 jitter();
                 arrive(l, 2);
             }
+            if (l == 0)  // this thread's share of the other counter set, where the kernel clears it
+                for (size_t i = (size_t)wg; i < hop_counters(S.n_layer); i += (size_t)lo.n_wg) {
+                    jitter();
+                    S.sync[other + i * kCtrStride].store(0);
+                }
             jitter();  // gate/up: after x1
             wait(l, 2);
             jitter();
