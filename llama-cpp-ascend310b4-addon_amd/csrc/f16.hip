@@ -215,6 +215,8 @@ int launch_g(hipStream_t st, const uint16_t *w, int64_t ldw, const float *x, flo
     return MI_ERR_ARG;
 }
 
+constexpr int kHeadRI = 2;  // row groups per head workgroup: half the partials, half the norm prologues
+
 // The tied output head of a decode token with its neighbours in the graph folded in:
 // the output RMSNorm ((x*scale)*norm_w, as k_rms_norm then MUL compute it; XStage)
 // converted to fp16 into LDS as k_gemv_f16 converts its activation, k_gemv_f16<G,U,1>'s
@@ -226,22 +228,25 @@ __global__ __launch_bounds__(256) void k_head_f16(const uint16_t *__restrict__ w
                                                   const float *__restrict__ x, const float *__restrict__ norm_w,
                                                   float eps, float *__restrict__ y, float2 *__restrict__ part, int n,
                                                   int k) {
-    constexpr int RPB = 256 / G;
+    constexpr int RPB = 256 / G;          // rows per pass of the workgroup
+    constexpr int RPW = RPB * kHeadRI;    // rows per workgroup (one norm prologue for all)
     extern __shared__ __align__(16) uint8_t smem[];
     uint16_t *s_x = (uint16_t *)smem;  // [k] fp16
     __shared__ double s_red[4];
-    __shared__ float s_v[RPB];
-    __shared__ int s_i[RPB];
+    __shared__ float s_v[RPW];
+    __shared__ int s_i[RPW];
     const int tid = threadIdx.x;
     const int j = tid % G;
-    const int row = blockIdx.x * RPB + tid / G;
-    const bool row_ok = row < n;
+    const int row0 = blockIdx.x * RPW + tid / G;  // this thread's rows: row0 + ri * RPB
     const int nc = k / 8, k4 = k / 4;
-    const uint16_t *wr = w + (size_t)min(row, n - 1) * ldw;
 
-    int4 wv[U];
+    int4 wv[kHeadRI][U];  // the first pass of every row group, in flight during the norm
 #pragma unroll
-    for (int u = 0; u < U; u++) wv[u] = ld_stream16(wr + (size_t)min(j + u * G, nc - 1) * 8);
+    for (int ri = 0; ri < kHeadRI; ri++) {
+        const uint16_t *wr = w + (size_t)min(row0 + ri * RPB, n - 1) * ldw;
+#pragma unroll
+        for (int u = 0; u < U; u++) wv[ri][u] = ld_stream16(wr + (size_t)min(j + u * G, nc - 1) * 8);
+    }
 
     XStage<XN, true> st;
     xstage_load(st, x, norm_w, nullptr, k4, tid);
@@ -257,42 +262,48 @@ __global__ __launch_bounds__(256) void k_head_f16(const uint16_t *__restrict__ w
     }
     __syncthreads();
 
-    float acc = 0.0f;
-    auto consume = [&](int c, const int4 &wq) {
-        const int4 xv = *(const int4 *)(s_x + (size_t)c * 8);
-        float s = acc;
-        s = fdot2((uint32_t)wq.x, (uint32_t)xv.x, s);
-        s = fdot2((uint32_t)wq.y, (uint32_t)xv.y, s);
-        s = fdot2((uint32_t)wq.z, (uint32_t)xv.z, s);
-        s = fdot2((uint32_t)wq.w, (uint32_t)xv.w, s);
-        acc = s;
-    };
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-        const int c = j + u * G;
-        if (c < nc) consume(c, wv[u]);
-    }
-    for (int c0 = U * G; c0 < nc; c0 += U * G) {
-#pragma unroll
-        for (int u = 0; u < U; u++) wv[u] = ld_stream16(wr + (size_t)min(c0 + j + u * G, nc - 1) * 8);
+    for (int ri = 0; ri < kHeadRI; ri++) {
+        const int row = row0 + ri * RPB;
+        const uint16_t *wr = w + (size_t)min(row, n - 1) * ldw;
+        float acc = 0.0f;
+        auto consume = [&](int c, const int4 &wq) {
+            const int4 xv = *(const int4 *)(s_x + (size_t)c * 8);
+            float s = acc;
+            s = fdot2((uint32_t)wq.x, (uint32_t)xv.x, s);
+            s = fdot2((uint32_t)wq.y, (uint32_t)xv.y, s);
+            s = fdot2((uint32_t)wq.z, (uint32_t)xv.z, s);
+            s = fdot2((uint32_t)wq.w, (uint32_t)xv.w, s);
+            acc = s;
+        };
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int c = c0 + j + u * G;
-            if (c < nc) consume(c, wv[u]);
+            const int c = j + u * G;
+            if (c < nc) consume(c, wv[ri][u]);
+        }
+        for (int c0 = U * G; c0 < nc; c0 += U * G) {
+            int4 wq[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) wq[u] = ld_stream16(wr + (size_t)min(c0 + j + u * G, nc - 1) * 8);
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int c = c0 + j + u * G;
+                if (c < nc) consume(c, wq[u]);
+            }
+        }
+        const float v = group_sum<G>(acc);
+        if (j == 0) {
+            if (row < n) y[row] = v;
+            s_v[ri * RPB + tid / G] = row < n ? v : -INFINITY;
+            s_i[ri * RPB + tid / G] = row;
         }
     }
-    const float v = group_sum<G>(acc);
-    if (j == 0) {
-        if (row_ok) y[row] = v;
-        s_v[tid / G] = row_ok ? v : -INFINITY;
-        s_i[tid / G] = row;
-    }
     __syncthreads();
-    if (tid == 0) {
+    if (tid == 0) {  // the rows in ascending order
         float best = -INFINITY;
-        int bi = blockIdx.x * RPB;
+        int bi = blockIdx.x * RPW;
 #pragma unroll
-        for (int r = 0; r < RPB; r++)
+        for (int r = 0; r < RPW; r++)
             if (s_v[r] > best) {
                 best = s_v[r];
                 bi = s_i[r];
@@ -301,7 +312,7 @@ __global__ __launch_bounds__(256) void k_head_f16(const uint16_t *__restrict__ w
     }
 }
 
-// ARGMAX's final pass over the head's per-workgroup partials (one per 4..16 rows: ~19K
+// ARGMAX's final pass over the head's per-workgroup partials (one per 8..32 rows: ~9.5K
 // for a 152K vocabulary): the first maximum (equal values keep the lower index).  1024
 // threads, each with 8 partials' loads in flight per step: one thread walking its share
 // with one load at a time took ~24 us.
@@ -349,8 +360,8 @@ int head_u(int64_t k, int g) {
 template <int G, int U, int XN>
 int launch_head_gux(hipStream_t st, const uint16_t *w, int64_t ldw, const float *x, const float *norm_w, float eps,
                     float *y, float2 *part, int64_t n, int64_t k) {
-    constexpr int RPB = 256 / G;
-    hipLaunchKernelGGL((k_head_f16<G, U, XN>), dim3((unsigned)((n + RPB - 1) / RPB)), dim3(256), (size_t)k * 2, st, w,
+    constexpr int RPW = 256 / G * kHeadRI;
+    hipLaunchKernelGGL((k_head_f16<G, U, XN>), dim3((unsigned)((n + RPW - 1) / RPW)), dim3(256), (size_t)k * 2, st, w,
                        ldw, x, norm_w, eps, y, part, (int)n, (int)k);
     MI_CHECK_LAUNCH("k_head_f16");
     return MI_OK;
@@ -390,8 +401,8 @@ int launch_m(hipStream_t st, const uint16_t *w, int64_t ldw, const float *x, flo
 
 extern "C" size_t mi_head_f16_argmax_workspace_size(int64_t n, int64_t k) {
     if (n <= 0 || k <= 0) return 0;
-    const int64_t rpb = 256 / head_g(k);
-    return mi::align_up((size_t)((n + rpb - 1) / rpb) * sizeof(float2), 256);
+    const int64_t rpw = 256 / head_g(k) * kHeadRI;
+    return mi::align_up((size_t)((n + rpw - 1) / rpw) * sizeof(float2), 256);
 }
 
 extern "C" int mi_head_f16_argmax(void *stream, const uint16_t *w, int64_t ldw, const float *x, const float *norm_w,
@@ -413,9 +424,9 @@ extern "C" int mi_head_f16_argmax(void *stream, const uint16_t *w, int64_t ldw, 
     const int r = k <= 2048 ? launch_head_x<2>(st, w, ldw, x, norm_w, eps, y, part, n, k)
                             : launch_head_x<4>(st, w, ldw, x, norm_w, eps, y, part, n, k);
     if (r) return r;
-    const int64_t rpb = 256 / head_g(k);
+    const int64_t rpw = 256 / head_g(k) * kHeadRI;
     hipLaunchKernelGGL(k_head_argmax_final, dim3(1), dim3(1024), 0, st, (const float2 *)part,
-                       (int)((n + rpb - 1) / rpb), out);
+                       (int)((n + rpw - 1) / rpw), out);
     MI_CHECK_LAUNCH("k_head_argmax_final");
     return MI_OK;
 }
