@@ -215,7 +215,7 @@ int launch_g(hipStream_t st, const uint16_t *w, int64_t ldw, const float *x, flo
     return MI_ERR_ARG;
 }
 
-constexpr int kHeadRI = 2;  // row groups per head workgroup: half the partials, half the norm prologues
+constexpr int kHeadRI = 2;  // row groups per head workgroup (4 measured slower: 69.9 / 156.6 us)
 
 // The tied output head of a decode token with its neighbours in the graph folded in:
 // the output RMSNorm ((x*scale)*norm_w, as k_rms_norm then MUL compute it; XStage)
@@ -240,13 +240,17 @@ __global__ __launch_bounds__(256) void k_head_f16(const uint16_t *__restrict__ w
     const int row0 = blockIdx.x * RPW + tid / G;  // this thread's rows: row0 + ri * RPB
     const int nc = k / 8, k4 = k / 4;
 
-    int4 wv[kHeadRI][U];  // the first pass of every row group, in flight during the norm
-#pragma unroll
-    for (int ri = 0; ri < kHeadRI; ri++) {
+    // the first pass of two row groups in flight (the first two during the norm prologue,
+    // each later one while the group two before it is consumed)
+    constexpr int NBUF = kHeadRI < 2 ? kHeadRI : 2;
+    int4 wv[NBUF][U];
+    auto first_pass = [&](int ri, int4 (&dst)[U]) {
         const uint16_t *wr = w + (size_t)min(row0 + ri * RPB, n - 1) * ldw;
 #pragma unroll
-        for (int u = 0; u < U; u++) wv[ri][u] = ld_stream16(wr + (size_t)min(j + u * G, nc - 1) * 8);
-    }
+        for (int u = 0; u < U; u++) dst[u] = ld_stream16(wr + (size_t)min(j + u * G, nc - 1) * 8);
+    };
+#pragma unroll
+    for (int ri = 0; ri < NBUF; ri++) first_pass(ri, wv[ri]);
 
     XStage<XN, true> st;
     xstage_load(st, x, norm_w, nullptr, k4, tid);
@@ -279,8 +283,9 @@ __global__ __launch_bounds__(256) void k_head_f16(const uint16_t *__restrict__ w
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int c = j + u * G;
-            if (c < nc) consume(c, wv[ri][u]);
+            if (c < nc) consume(c, wv[ri % NBUF][u]);
         }
+        if (ri + NBUF < kHeadRI) first_pass(ri + NBUF, wv[ri % NBUF]);
         for (int c0 = U * G; c0 < nc; c0 += U * G) {
             int4 wq[U];
 #pragma unroll
